@@ -1,0 +1,238 @@
+#!/usr/bin/env python3
+"""Triangle-attention block benchmark on one MI355X.
+
+Workload (default ``--config c4``): both triangle-attention blocks (starting
+and ending node) at N=1536, FP32, c_z=128, H=4, d=32, z ~ 2*N(0,1), the last
+184 residues (12%) masked on both axes, triangle-bias weights x8 (logits span
+about +/-40).  One step = one starting-node block followed by one ending-node
+block on the same z, each a single C-ABI call (``fpx_tri_attn_block``).
+Inputs, weights, outputs and workspace are resident in HBM before timing.
+
+Output: one JSON line.  ``value`` is the step's algorithmic TFLOP/s
+(2 x (512 N^3 + 164864 N^2) flop per step); ``ms_per_step`` covers both
+blocks.  ``roofline`` is the attention kernel alone (``fpx_tri_attn_attend``,
+512 N^3 flop per launch) timed with HIP events on the launch stream, against
+the 157.3 TFLOP/s FP32 matrix peak.  ``cpu_baseline`` times the CPU oracle
+(native PyTorch op order, FP32) on the host cores for a bounded sample of outer
+rows and extrapolates linearly in rows (rows are independent).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import platform
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "triangle-attn block ms + TFLOP/s (% MFMA peak) at N=1536 FP32, 1 GPU"
+FP32_MFMA_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBPS = 8000.0
+TRAFFIC_FILE = ROOT / "profiles" / "attention_traffic.json"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(cfg, z, mask, weights, row_counts=(8, 24)) -> dict:
+    """Time the CPU oracle on outer-row samples; extrapolate to all N rows."""
+    import torch
+
+    from oracle import triangle_attention as oracle
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    params = oracle.BlockParams(**weights)
+    total = 0.0
+    detail = {}
+    with torch.inference_mode():
+        for ending in (False, True):
+            times = []
+            for rows in row_counts:
+                sel = torch.linspace(0, cfg.n - 1, rows).round().long()
+                t0 = time.perf_counter()
+                oracle.block(z, mask, params, ending=ending, outer_rows=sel)
+                times.append(time.perf_counter() - t0)
+                log(f"cpu oracle ending={ending} rows={rows}: {times[-1]:.2f} s")
+            per_row = max((times[1] - times[0]) / (row_counts[1] - row_counts[0]), 0.0)
+            common = max(times[0] - per_row * row_counts[0], 0.0)
+            est = common + per_row * cfg.n
+            detail["end" if ending else "start"] = {"common_s": round(common, 3),
+                                                    "per_row_s": round(per_row, 5),
+                                                    "block_s": round(est, 2)}
+            total += est
+    from oracle.triangle_attention import block_flops
+
+    flop = 2 * block_flops(cfg.n)["block"]
+    return {
+        "value": round(flop / total / 1e12, 5),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"CPU oracle (native PyTorch op order, FP32, {threads} threads) on the same "
+                   f"{cfg.name} inputs: per direction, full LayerNorm + triangle bias and "
+                   f"attention/gate/out-projection for {row_counts[0]} and {row_counts[1]} "
+                   f"evenly spaced outer rows, fitted linearly in rows and extrapolated to "
+                   f"{cfg.n} rows; start+end step {total:.1f} s"),
+        "step_s": round(total, 2),
+        "detail": detail,
+        "cpu": platform.processor() or platform.machine(),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c4", choices=["c1", "c2", "c3", "c4"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py runs on exactly one GPU: the triangle-attention block is measured on "
+              "one MI355X (multi-GPU sharding is a design note, not a measured path); "
+              "use --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from fireprot_amd import _native, block, workloads
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        return 2
+    lib = _native.library()
+    cfg = workloads.CONFIGS[args.config]
+    n = cfg.n
+    log(f"inputs {cfg.name}")
+    z_cpu, mask_cpu, w = workloads.make_inputs(cfg)
+    dev = torch.device("cuda:0")
+    z = z_cpu.to(dev)
+    mask = None if mask_cpu is None else mask_cpu.to(dev)
+    weights = block.BlockWeights.from_tensors(**w).to(dev)
+    out_s = torch.empty_like(z)
+    out_e = torch.empty_like(z)
+    ws = torch.empty(block.workspace_bytes(n), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        block.triangle_attention_block(z, mask, weights, ending=False, out=out_s, workspace=ws)
+        block.triangle_attention_block(z, mask, weights, ending=True, out=out_e, workspace=ws)
+
+    with torch.inference_mode():
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        log(f"warmup {args.warmup} done")
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record(stream)
+        for _ in range(args.steps):
+            step()
+        t1.record(stream)
+        torch.cuda.synchronize()
+        ms_per_step = t0.elapsed_time(t1) / args.steps
+        log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step")
+
+        # Stage timing on the launch stream: prepare (mask bias + LN/projections),
+        # attend (attention kernel), finish (output projection), starting node.
+        ws_bytes = ws.numel()
+        sptr = stream.cuda_stream
+        mptr = mask.data_ptr() if mask is not None else None
+        mstr = (mask.stride(0), mask.stride(1)) if mask is not None else (0, 0)
+
+        def prepare():
+            _native.check(lib.fpx_tri_attn_prepare(
+                0, z.data_ptr(), z.stride(0), z.stride(1), mptr, mstr[0], mstr[1],
+                weights.ln_w.data_ptr(), weights.ln_b.data_ptr(), weights.eps,
+                weights.w_qkvg.data_ptr(), None, weights.w_bias.data_ptr(), weights.inf, n, 0,
+                ws.data_ptr(), ws_bytes, sptr), "prepare")
+
+        def attend():
+            _native.check(lib.fpx_tri_attn_attend(0, n, ws.data_ptr(), ws_bytes, sptr), "attend")
+
+        def finish():
+            _native.check(lib.fpx_tri_attn_finish(0, weights.w_o.data_ptr(), None, n, 0,
+                                                  out_s.data_ptr(), out_s.stride(0),
+                                                  out_s.stride(1), ws.data_ptr(), ws_bytes,
+                                                  sptr), "finish")
+
+        stages = {}
+        for name, fn in (("prepare", prepare), ("attend", attend), ("finish", finish)):
+            fn()
+            torch.cuda.synchronize()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            reps = max(args.steps, 5)
+            e0.record(stream)
+            for _ in range(reps):
+                fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            stages[name] = e0.elapsed_time(e1) / reps
+            log(f"stage {name}: {stages[name]:.3f} ms")
+
+    flops = block.block_flops(n)
+    step_flop = 2 * flops["block"]
+    value = step_flop / (ms_per_step * 1e-3) / 1e12
+    attend_tflops = flops["core"] / (stages["attend"] * 1e-3) / 1e12
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        try:
+            traffic = json.loads(TRAFFIC_FILE.read_text()).get(cfg.name, {}).get("bytes_per_launch")
+        except (ValueError, AttributeError):
+            traffic = None
+    result = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded torch.Generator inputs and N(0,0.02) random-init weights)",
+        "config": {
+            "workload": f"{cfg.name}: starting + ending triangle-attention block",
+            "n": n, "c_z": 128, "heads": 4, "head_dim": 32,
+            "valid_residues": cfg.valid if cfg.valid is not None else n,
+            "bias_scale": cfg.bias_scale,
+            "block_ms": round(ms_per_step / 2, 4),
+            "block_tflops": round(value, 3),
+            "block_mfma_peak_frac": round(value / FP32_MFMA_PEAK_TFLOPS, 4),
+            "step_flop": step_flop,
+            "stage_ms_start_node": {k: round(v, 4) for k, v in stages.items()},
+        },
+        "roofline": {
+            "kernel": "attention_kernel<kAttnBlock> (fpx_tri_attn_attend)",
+            "bound": "mfma",
+            "achieved": round(attend_tflops, 3),
+            "peak": FP32_MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(attend_tflops / FP32_MFMA_PEAK_TFLOPS, 4),
+            "traffic": traffic,
+            "flop_per_launch": flops["core"],
+            "avg_launch_ms": round(stages["attend"], 4),
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        del out_s, out_e, ws
+        torch.cuda.empty_cache()
+        result["cpu_baseline"] = cpu_baseline(cfg, z_cpu, mask_cpu, w)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,295 @@
+// C-ABI entry points (declared in include/fireprot_amd.h).
+//
+// Every entry validates sizes and pointers on the host first (status 2 / 3 /
+// 4, before any device pointer is touched), then enqueues on the caller's
+// stream and returns the launch status.  Nothing here allocates or
+// synchronises.
+#include "fireprot_amd.h"
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+#include <cmath>
+
+namespace {
+
+using fpx::round_up;
+
+bool aligned(const void* p, uintptr_t bytes) {
+  return p != nullptr && reinterpret_cast<uintptr_t>(p) % bytes == 0;
+}
+bool aligned_or_null(const void* p, uintptr_t bytes) {
+  return p == nullptr || reinterpret_cast<uintptr_t>(p) % bytes == 0;
+}
+
+constexpr int kMaxN = 4096;
+constexpr int kQueryTile = 128;  // attention query tile: every block extent pads to it
+
+// Workspace segments of the F32 block, all 256-byte aligned:
+//   qh, kh [n][4][np][32]; vt [n][4][32][np]; gs, og [n][n][128];
+//   tri_bias [4][np][np]; mbias [n][np]
+struct BlockWorkspace {
+  size_t qh, kh, vt, gs, og, bias, mbias, total;
+};
+
+BlockWorkspace block_workspace(int n) {
+  const size_t np = (size_t)round_up(n, kQueryTile);
+  auto seg = [](size_t bytes) { return (size_t)round_up((int64_t)bytes, 256); };
+  const size_t qkv = seg((size_t)n * fpx::kHeads * np * fpx::kHeadDim * sizeof(float));
+  const size_t g = seg((size_t)n * n * fpx::kHidden * sizeof(float));
+  const size_t bias = seg((size_t)fpx::kHeads * np * np * sizeof(float));
+  const size_t mb = seg((size_t)n * np * sizeof(float));
+  BlockWorkspace w{};
+  w.qh = 0;
+  w.kh = w.qh + qkv;
+  w.vt = w.kh + qkv;
+  w.gs = w.vt + qkv;
+  w.og = w.gs + g;
+  w.bias = w.og + g;
+  w.mbias = w.bias + bias;
+  w.total = w.mbias + mb;
+  return w;
+}
+
+bool block_dims_ok(int n, int c, int heads, int head_dim, int dtype) {
+  return dtype == FPX_F32 && c == fpx::kChannels && heads == fpx::kHeads &&
+         head_dim == fpx::kHeadDim && n >= 1 && n <= kMaxN;
+}
+
+int status(hipError_t e) { return e == hipSuccess ? FPX_OK : (int)e; }
+
+}  // namespace
+
+extern "C" {
+
+int fpx_abi_version(void) { return FPX_ABI_VERSION; }
+
+size_t fpx_tri_attn_workspace_bytes(int n, int c, int heads, int head_dim, int dtype) {
+  if (!block_dims_ok(n, c, heads, head_dim, dtype)) return 0;
+  return block_workspace(n).total;
+}
+
+namespace {
+
+struct BlockPointers {
+  float *qh, *kh, *vt, *gs, *og, *tri, *mbias;
+  int np;
+};
+
+BlockPointers block_pointers(void* workspace, int n) {
+  const BlockWorkspace ws = block_workspace(n);
+  char* base = static_cast<char*>(workspace);
+  BlockPointers p{};
+  p.qh = reinterpret_cast<float*>(base + ws.qh);
+  p.kh = reinterpret_cast<float*>(base + ws.kh);
+  p.vt = reinterpret_cast<float*>(base + ws.vt);
+  p.gs = reinterpret_cast<float*>(base + ws.gs);
+  p.og = reinterpret_cast<float*>(base + ws.og);
+  p.tri = reinterpret_cast<float*>(base + ws.bias);
+  p.mbias = reinterpret_cast<float*>(base + ws.mbias);
+  p.np = (int)round_up(n, kQueryTile);
+  return p;
+}
+
+int check_workspace(int n, const void* workspace, size_t workspace_bytes) {
+  if (!aligned(workspace, 256)) return FPX_ERR_POINTER;
+  if (workspace_bytes < block_workspace(n).total) return FPX_ERR_WORKSPACE;
+  return FPX_OK;
+}
+
+}  // namespace
+
+int fpx_tri_attn_prepare(int dtype, const void* z, int64_t z_stride0, int64_t z_stride1,
+                         const float* mask, int64_t m_stride0, int64_t m_stride1,
+                         const void* ln_w, const void* ln_b, float eps, const void* w_qkvg,
+                         const void* b_g, const void* w_bias, float mask_inf, int n, int ending,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  if (!block_dims_ok(n, fpx::kChannels, fpx::kHeads, fpx::kHeadDim, dtype)) return FPX_ERR_DIMS;
+  if (ending != 0 && ending != 1) return FPX_ERR_DIMS;
+  if (z_stride0 % 4 || z_stride1 % 4 || z_stride0 < 0 || z_stride1 < 0) return FPX_ERR_DIMS;
+  if (m_stride0 < 0 || m_stride1 < 0) return FPX_ERR_DIMS;
+  if (!(eps >= 0.0f) || !std::isfinite(mask_inf)) return FPX_ERR_DIMS;
+  if (!aligned(z, 16) || !aligned(w_qkvg, 16) || !aligned(w_bias, 16)) return FPX_ERR_POINTER;
+  if (!aligned_or_null(mask, 4) || !aligned_or_null(ln_w, 8) || !aligned_or_null(ln_b, 8) ||
+      !aligned_or_null(b_g, 4))
+    return FPX_ERR_POINTER;
+  if (int rc = check_workspace(n, workspace, workspace_bytes)) return rc;
+
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const BlockPointers w = block_pointers(workspace, n);
+  // x-frame strides: the ending node reads x[i][j] = z[j][i] (and the mask alike).
+  const int64_t xs_i = ending ? z_stride1 : z_stride0;
+  const int64_t xs_j = ending ? z_stride0 : z_stride1;
+  const int64_t ms_i = ending ? m_stride1 : m_stride0;
+  const int64_t ms_j = ending ? m_stride0 : m_stride1;
+
+  hipError_t e = fpx::launch_mask_bias(mask, ms_i, ms_j, n, w.np, mask_inf, w.mbias, w.tri, s);
+  if (e != hipSuccess) return status(e);
+
+  const float* wq = static_cast<const float*>(w_qkvg);
+  const int64_t wstride = (int64_t)fpx::kHidden * fpx::kChannels;
+  fpx::ProjArgs p{};
+  p.x = static_cast<const float*>(z);
+  p.xs_i = xs_i;
+  p.xs_j = xs_j;
+  p.rows_i = n;
+  p.rows_j = n;
+  p.span_j = w.np;
+  p.ln_w = static_cast<const float*>(ln_w);
+  p.ln_b = static_cast<const float*>(ln_b);
+  p.eps = eps;
+  for (int g = 0; g < 4; ++g) p.w[g] = wq + g * wstride;
+  p.b_g = static_cast<const float*>(b_g);
+  p.w_bias = static_cast<const float*>(w_bias);
+  p.q_scale = 1.0f / std::sqrt((float)fpx::kHeadDim);
+  p.qh = w.qh;
+  p.kh = w.kh;
+  p.vt = w.vt;
+  p.gs = w.gs;
+  p.tri_bias = w.tri;
+  p.np = w.np;
+  return status(fpx::launch_projection(fpx::kProjBlock, p, s));
+}
+
+int fpx_tri_attn_attend(int dtype, int n, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!block_dims_ok(n, fpx::kChannels, fpx::kHeads, fpx::kHeadDim, dtype)) return FPX_ERR_DIMS;
+  if (int rc = check_workspace(n, workspace, workspace_bytes)) return rc;
+  const BlockPointers w = block_pointers(workspace, n);
+  fpx::AttnArgs a{};
+  a.q = w.qh;
+  a.k = w.kh;
+  a.v = w.vt;
+  a.mbias = w.mbias;
+  a.mb_stride = w.np;
+  a.bias = w.tri;
+  a.bias_stride = w.np;
+  a.bias_rows = w.np;
+  a.gate = w.gs;
+  a.out = w.og;
+  a.batch = n;
+  a.n = n;
+  a.np = w.np;
+  return status(fpx::launch_attention(fpx::kAttnBlock, a, static_cast<hipStream_t>(stream)));
+}
+
+int fpx_tri_attn_finish(int dtype, const void* w_o, const void* b_o, int n, int ending, void* dz,
+                        int64_t dz_stride0, int64_t dz_stride1, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  if (!block_dims_ok(n, fpx::kChannels, fpx::kHeads, fpx::kHeadDim, dtype)) return FPX_ERR_DIMS;
+  if (ending != 0 && ending != 1) return FPX_ERR_DIMS;
+  if (dz_stride0 < 0 || dz_stride1 < 0) return FPX_ERR_DIMS;
+  if (!aligned(w_o, 16) || !aligned(dz, 16) || !aligned_or_null(b_o, 4)) return FPX_ERR_POINTER;
+  if (int rc = check_workspace(n, workspace, workspace_bytes)) return rc;
+  const BlockPointers w = block_pointers(workspace, n);
+  fpx::ProjArgs o{};
+  o.x = w.og;
+  o.xs_i = (int64_t)n * fpx::kHidden;
+  o.xs_j = fpx::kHidden;
+  o.rows_i = n;
+  o.rows_j = n;
+  o.span_j = n;
+  o.w[0] = static_cast<const float*>(w_o);
+  o.b_g = static_cast<const float*>(b_o);
+  o.out = static_cast<float*>(dz);
+  o.os_i = ending ? dz_stride1 : dz_stride0;
+  o.os_j = ending ? dz_stride0 : dz_stride1;
+  return status(fpx::launch_projection(fpx::kProjOut, o, static_cast<hipStream_t>(stream)));
+}
+
+int fpx_tri_attn_block(int dtype, const void* z, int64_t z_stride0, int64_t z_stride1,
+                       const float* mask, int64_t m_stride0, int64_t m_stride1,
+                       const void* ln_w, const void* ln_b, float eps, const void* w_qkvg,
+                       const void* b_g, const void* w_bias, const void* w_o, const void* b_o,
+                       float mask_inf, int n, int c, int heads, int head_dim, int ending,
+                       void* dz, int64_t dz_stride0, int64_t dz_stride1, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  if (!block_dims_ok(n, c, heads, head_dim, dtype)) return FPX_ERR_DIMS;
+  if (ending != 0 && ending != 1) return FPX_ERR_DIMS;
+  if (dz_stride0 < 0 || dz_stride1 < 0) return FPX_ERR_DIMS;
+  if (!aligned(w_o, 16) || !aligned(dz, 16) || !aligned_or_null(b_o, 4)) return FPX_ERR_POINTER;
+  int rc = fpx_tri_attn_prepare(dtype, z, z_stride0, z_stride1, mask, m_stride0, m_stride1, ln_w,
+                                ln_b, eps, w_qkvg, b_g, w_bias, mask_inf, n, ending, workspace,
+                                workspace_bytes, stream);
+  if (rc) return rc;
+  rc = fpx_tri_attn_attend(dtype, n, workspace, workspace_bytes, stream);
+  if (rc) return rc;
+  return fpx_tri_attn_finish(dtype, w_o, b_o, n, ending, dz, dz_stride0, dz_stride1, workspace,
+                             workspace_bytes, stream);
+}
+
+int fpx_attn_core_masked(const float* q, const float* k, const float* v, const float* mask_bias,
+                         int64_t mask_bias_stride, const float* bias, int64_t bias_row_stride,
+                         float* out, int batch, int n, void* stream) {
+  if (batch < 1 || n < 1 || n % 4 != 0 || n > 65536) return FPX_ERR_DIMS;
+  if (bias_row_stride < n || bias_row_stride % 4 != 0) return FPX_ERR_DIMS;
+  if (mask_bias != nullptr && mask_bias_stride < 0) return FPX_ERR_DIMS;
+  if ((int64_t)batch * fpx::kHeads * (round_up(n, kQueryTile) / kQueryTile) > 0x7fffffffll)
+    return FPX_ERR_DIMS;
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(bias, 16) ||
+      !aligned(out, 16))
+    return FPX_ERR_POINTER;
+  if (!aligned_or_null(mask_bias, 4)) return FPX_ERR_POINTER;
+  fpx::AttnArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.mbias = mask_bias;
+  a.mb_stride = mask_bias_stride;
+  a.bias = bias;
+  a.bias_stride = bias_row_stride;
+  a.bias_rows = n;
+  a.gate = nullptr;
+  a.out = out;
+  a.batch = batch;
+  a.n = n;
+  a.np = n;
+  return status(fpx::launch_attention(fpx::kAttnHeadLast, a, static_cast<hipStream_t>(stream)));
+}
+
+int fpx_attn_core(float* q, float* k, float* v, float* bias, float* out, int batch, int n,
+                  void* stream) {
+  return fpx_attn_core_masked(q, k, v, nullptr, 0, bias, n, out, batch, n, stream);
+}
+
+int fpx_layer_norm_c128(const float* x, int64_t rows_i, int64_t rows_j, int64_t stride_i,
+                        int64_t stride_j, const float* w, const float* b, float eps, float* y,
+                        void* stream) {
+  if (rows_i < 0 || rows_j < 0 || stride_i < 0 || stride_j < 0) return FPX_ERR_DIMS;
+  if (stride_i % 2 || stride_j % 2 || !(eps >= 0.0f)) return FPX_ERR_DIMS;
+  if (!aligned(x, 8) || !aligned(y, 8) || !aligned_or_null(w, 8) || !aligned_or_null(b, 8))
+    return FPX_ERR_POINTER;
+  return status(fpx::launch_layer_norm(x, rows_i, rows_j, stride_i, stride_j, w, b, eps, y,
+                                       static_cast<hipStream_t>(stream)));
+}
+
+int fpx_qkv_projection(const float* x, int64_t rows, const float* wq, const float* wk,
+                       const float* wv, float* out, void* stream) {
+  if (rows < 0 || rows > 0x7fffffffll) return FPX_ERR_DIMS;
+  if (!aligned(x, 16) || !aligned(wq, 16) || !aligned(wk, 16) || !aligned(wv, 16) ||
+      !aligned(out, 16))
+    return FPX_ERR_POINTER;
+  fpx::ProjArgs p{};
+  p.x = x;
+  p.xs_i = 0;
+  p.xs_j = fpx::kChannels;
+  p.rows_i = 1;
+  p.rows_j = (int)rows;
+  p.span_j = (int)rows;
+  p.w[0] = wq;
+  p.w[1] = wk;
+  p.w[2] = wv;
+  p.w[3] = wv;
+  p.q_scale = 1.0f / std::sqrt((float)fpx::kHeadDim);
+  p.out = out;
+  return status(fpx::launch_projection(fpx::kProjQkv, p, static_cast<hipStream_t>(stream)));
+}
+
+int fpx_sigmoid_mul_out(const float* gate, const float* value, float* out, int64_t count,
+                        void* stream) {
+  if (count < 0 || count % 4 != 0) return FPX_ERR_DIMS;
+  if (!aligned(gate, 16) || !aligned(value, 16) || !aligned(out, 16)) return FPX_ERR_POINTER;
+  return status(fpx::launch_sigmoid_mul(gate, value, out, count / 4,
+                                        static_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"

@@ -1,0 +1,91 @@
+// Shared device helpers for the gfx950 triangle-attention kernels.
+//
+// Everything here is CDNA4-specific: 64-lane wavefronts, the FP32 matrix-core
+// instruction v_mfma_f32_32x32x2_f32, and an XCD-aware work-group remap for the
+// 8 accelerator dies of an MI355X.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace fpx {
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kWave = 64;
+constexpr int kHeads = 4;
+constexpr int kHeadDim = 32;
+constexpr int kChannels = 128;
+constexpr int kHidden = kHeads * kHeadDim;  // 128
+constexpr int kXcds = 8;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// D = A x B + C for one 32x32x2 FP32 matrix-core step.
+// Operand/result lane layouts (CDNA3/CDNA4 ISA, "32x32x2 f32", single block):
+//   A[row][k]  : lane = row + 32*k                      (row 0..31, k 0..1)
+//   B[k][col]  : lane = col + 32*k
+//   D[row][col]: lane = col + 32*((row/4)%2), register = (row%4) + 4*(row/8)
+// i.e. lane l, register r holds D[8*(r/4) + 4*(l/32) + r%4][l%32].
+// tests/test_gpu_mfma_layout.py calibrates this on the device.
+__device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// Row index (0..31) of result register r in lane half `half` (= lane/32).
+__device__ __forceinline__ int mfma_row(int r, int half) {
+  return 8 * (r >> 2) + 4 * half + (r & 3);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// Two-pass LayerNorm statistics of a 128-channel row held as two values per
+// lane.  Values are shifted by lane 0's first value before summing, so rows
+// with |mean| >> std (e.g. 1000 + 0.001*c) keep their digits: the centred
+// values are formed from small differences instead of from a rounded mean of
+// large values.  Returns the centred values and 1/sqrt(biased var + eps).
+__device__ __forceinline__ void ln_stats_c128(float a, float b, float eps, float& da, float& db,
+                                              float& rstd) {
+  const float pivot =
+      __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, a)));
+  const float sa = a - pivot;
+  const float sb = b - pivot;
+  const float mean_s = wave_sum(sa + sb) * (1.0f / kChannels);
+  da = sa - mean_s;
+  db = sb - mean_s;
+  const float var = wave_sum(da * da + db * db) * (1.0f / kChannels);
+  rstd = 1.0f / sqrtf(var + eps);
+}
+
+__device__ __forceinline__ float exp2_fast(float x) {
+  return __builtin_amdgcn_exp2f(x);
+}
+
+__device__ __forceinline__ float sigmoidf_(float x) {
+  return 1.0f / (1.0f + __expf(-x));
+}
+
+// Work-groups are dispatched round-robin over the XCDs: hardware block b runs
+// on XCD b % 8.  Return a logical index such that each XCD receives one
+// contiguous range of logical indices, so neighbouring tiles (which share
+// K/V rows or bias rows) meet in the same 4 MB L2.  Bijective for any total.
+__device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t total) {
+  const uint32_t per = total / kXcds;
+  const uint32_t extra = total % kXcds;
+  const uint32_t xcd = b % kXcds;
+  const uint32_t slot = b / kXcds;
+  return xcd < extra ? xcd * (per + 1) + slot
+                     : extra * (per + 1) + (xcd - extra) * per + slot;
+}
+
+__host__ __device__ __forceinline__ int64_t round_up(int64_t x, int64_t m) {
+  return (x + m - 1) / m * m;
+}
+
+}  // namespace fpx

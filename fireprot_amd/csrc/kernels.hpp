@@ -1,0 +1,103 @@
+// Internal launch interface between the C-ABI layer (capi.hip) and the kernels.
+// Nothing here is exported; the public surface is include/fireprot_amd.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace fpx {
+
+// ---------------------------------------------------------------- attention
+// Row-wise triangle attention over B outer rows, H = 4 heads, d = 32.
+//
+// kAttnBlock:  the block's own workspace layout (all extents padded to np,
+//              a multiple of 128; padded keys carry -inf in mbias):
+//                q, k : [B][H][np][32]   (q pre-scaled by 1/sqrt(32))
+//                v    : [B][H][32][np]   (transposed per head)
+//                mbias: [B][np]          (required)
+//                bias : [H][np][np]
+//                gate : [B][n][128] sigmoid(g), multiplied in the epilogue
+//                out  : [B][n][128]      (o * gate, head-last)
+// kAttnHeadLast: the reference C-ABI layout (fireprot_ck_attention.cpp:34-43):
+//                q, k, v, out : [B][n][H][32] (strides n*128, 32, 128, 1)
+//                bias : [H][n][bias_stride]  (batch stride 0)
+//                mbias: nullable, [B] rows of n values, row stride mb_stride
+enum AttnLayout { kAttnBlock = 0, kAttnHeadLast = 1 };
+
+struct AttnArgs {
+  const float* q;
+  const float* k;
+  const float* v;
+  const float* mbias;
+  int64_t mb_stride;
+  const float* bias;
+  int64_t bias_stride;
+  int64_t bias_rows;
+  const float* gate;
+  float* out;
+  int batch;
+  int n;
+  int np;
+};
+
+hipError_t launch_attention(int layout, const AttnArgs& args, hipStream_t stream);
+
+// --------------------------------------------------------------- projection
+// Row tiles are 32 consecutive j of one outer row i; A rows are read at
+// x + i*xs_i + j*xs_j (channel stride 1), which covers the ending-node
+// transposed read without a copy.
+enum ProjMode {
+  kProjBlock = 0,  // LN -> q,k,v,g (+ triangle bias) into the block workspace
+  kProjQkv = 1,    // q,k,v of already-normalised rows -> out[3][rows][128]
+  kProjOut = 2,    // (o * gate) rows -> W_o (+ b_o) -> out + i*os_i + j*os_j
+};
+
+struct ProjArgs {
+  const float* x;
+  int64_t xs_i;
+  int64_t xs_j;
+  int rows_i;
+  int rows_j;    // valid j extent
+  int span_j;    // j extent covered by tiles (np for kProjBlock, else rows_j)
+  const float* ln_w;
+  const float* ln_b;
+  float eps;
+  const float* w[4];   // [128 out][128 in] torch layout, one per output group
+  const float* b_g;    // kProjBlock: gate bias (nullable); kProjOut: b_o (nullable)
+  const float* w_bias; // kProjBlock: [4][128] triangle-bias weights
+  float q_scale;
+  // kProjBlock outputs
+  float* qh;
+  float* kh;
+  float* vt;
+  float* gs;
+  float* tri_bias;
+  int np;
+  // kProjQkv / kProjOut outputs
+  float* out;
+  int64_t os_i;
+  int64_t os_j;
+};
+
+hipError_t launch_projection(int mode, const ProjArgs& args, hipStream_t stream);
+
+// -------------------------------------------------------------- elementwise
+// mbias[i][k] = k < n ? inf * (mask_x[i][k] - 1) : -inf  (0 for k < n when
+// mask is null), and zero rows [n, np) of every head of the triangle bias.
+hipError_t launch_mask_bias(const float* mask, int64_t ms_i, int64_t ms_j, int n, int np,
+                            float inf, float* mbias, float* tri_bias, hipStream_t stream);
+
+// LayerNorm over 128 channels of rows x[i][j] at x + i*xs_i + j*xs_j,
+// written contiguously to y[(i*rows_j + j)*128 + c].
+hipError_t launch_layer_norm(const float* x, int64_t rows_i, int64_t rows_j, int64_t xs_i,
+                             int64_t xs_j, const float* w, const float* b, float eps, float* y,
+                             hipStream_t stream);
+
+// out = value * sigmoid(gate), float4 vectors.
+hipError_t launch_sigmoid_mul(const float* gate, const float* value, float* out, int64_t count4,
+                              hipStream_t stream);
+
+int device_cu_count();
+
+}  // namespace fpx

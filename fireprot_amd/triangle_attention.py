@@ -1,0 +1,231 @@
+"""Capability-gated triangle-attention dispatch on gfx950.
+
+Two operations are registered in the shared ``fireprot_amd.registry``:
+
+``triangle_attention`` -- the attention core behind Protenix
+``Attention.forward``'s ``triangle_attention="fireprot"`` branch
+(patches/protenix/0002-*.patch:46-58).  ``dispatch_triangle_attention`` has the
+reference's signature and builds the same ``OperationSignature``
+(python/fireprot/backends/amd/triangle_attention.py:199-256); the HIP
+candidate ``amd-gfx950-hip-attention-f32`` takes q/k/v ``[B, H, N, 32]`` in
+the head-last projection layout (strides ``(N*128, 32, 128, 1)``), the
+triangle bias ``[1, 4, N, N]`` and optionally the mask bias ``[B, 1, 1, N]``,
+and returns ``[B, N, H, 32]`` like the native lambda
+``_attention(q, k, v, biases).transpose(-2, -3)``.
+
+``triangle_attention_block`` -- the whole module call ``(z, mask) -> dz``,
+as AtlasFold's per-instance hook dispatches it
+(python/fireprot/adapters/atlasfold/runtime.py:185-207).  The module's
+weights are read through ``BlockWeights.from_protenix`` or
+``from_atlasfold``.
+
+Unsupported calls go to the caller's ``native`` function, never to a CPU
+path of this package.
+"""
+from __future__ import annotations
+
+import functools
+from collections.abc import Callable, Sequence
+from typing import Any
+
+from . import _native
+from .block import BlockWeights, triangle_attention_block
+from .registry import OperationSignature, registry, signature_from_tensor
+
+OPERATION = "triangle_attention"
+BLOCK_OPERATION = "triangle_attention_block"
+IMPLEMENTATION = "amd-gfx950-hip-attention-f32"
+BLOCK_IMPLEMENTATION = "amd-gfx950-hip-block-f32"
+ARCHITECTURE = "gfx950"
+HEADS = 4
+HEAD_DIM = 32
+
+
+@functools.lru_cache(maxsize=None)
+def _device_architecture(index: int) -> str:
+    import torch
+
+    properties = torch.cuda.get_device_properties(index)
+    return str(getattr(properties, "gcnArchName", "")).split(":", 1)[0]
+
+
+def _architecture(tensor: Any) -> str:
+    try:
+        if tensor.device.type != "cuda":
+            return "cpu"
+        return _device_architecture(int(tensor.device.index or 0))
+    except Exception:
+        return "unknown"
+
+
+def _mode(module: Any, tensors: Sequence[Any]) -> str:
+    import torch
+
+    training = bool(getattr(module, "training", False))
+    if not training and not torch.is_grad_enabled() and not any(t.requires_grad for t in tensors):
+        return "inference"
+    return "training"
+
+
+# ------------------------------------------------------------------ core
+
+def _supports_core(signature: OperationSignature) -> bool | tuple[bool, str]:
+    attributes = dict(signature.attributes)
+    if signature.device_type != "cuda":
+        return False, "device is not CUDA/HIP"
+    if signature.architecture != ARCHITECTURE:
+        return False, f"architecture is not {ARCHITECTURE}"
+    if signature.dtype != "float32":
+        return False, "dtype is not float32"
+    if signature.mode != "inference":
+        return False, "training or autograd is enabled"
+    if len(signature.shape) != 4:
+        return False, "q must be [B, H, N, D]"
+    batch, heads, n, dim = signature.shape
+    if heads != HEADS or dim != HEAD_DIM:
+        return False, "requires 4 heads of dimension 32"
+    if n % 4:
+        return False, "sequence length must be a multiple of 4"
+    strides = (n * HEADS * HEAD_DIM, HEAD_DIM, HEADS * HEAD_DIM, 1)
+    if attributes.get("qkv_strides") != repr((strides,) * 3):
+        return False, "q/k/v must use the head-last projection layout"
+    shapes = attributes.get("bias_shapes")
+    allowed = {repr(((1, HEADS, n, n),)),
+               repr(((batch, 1, 1, n), (1, HEADS, n, n))),
+               repr(((1, 1, 1, n), (1, HEADS, n, n)))}
+    if shapes not in allowed:
+        return False, "biases must be [mask_bias [B|1,1,1,N],] triangle bias [1,4,N,N]"
+    if attributes.get("ck_tile_compatible") != "True":
+        return False, "q/k/v/bias dtype, device or 16-byte alignment mismatch"
+    if not _native.available():
+        return False, "HIP extension unavailable"
+    return True
+
+
+def attention(*, module: Any, q: Any, k: Any, v: Any, biases: Sequence[Any],
+              native: Callable[..., Any]) -> Any:
+    """HIP flash attention; returns ``[B, N, H, D]`` (contiguous)."""
+    import torch
+
+    del module, native
+    lib = _native.library()
+    batch, _, n, _ = q.shape
+    with torch.cuda.device(q.device):
+        bias = biases[-1].contiguous()
+        if bias.data_ptr() % 16:
+            bias = bias.clone()
+        mask_ptr, mask_stride = None, 0
+        if len(biases) == 2:
+            mask = biases[0].reshape(biases[0].shape[0], n)
+            if mask.stride(-1) != 1:
+                mask = mask.contiguous()
+            mask_ptr = mask.data_ptr()
+            mask_stride = mask.stride(0) if mask.shape[0] > 1 else 0
+        output = torch.empty((batch, n, HEADS, HEAD_DIM), device=q.device, dtype=q.dtype)
+        code = lib.fpx_attn_core_masked(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), mask_ptr, mask_stride, bias.data_ptr(),
+            n, output.data_ptr(), batch, n, torch.cuda.current_stream(q.device).cuda_stream)
+    _native.check(code, "fpx_attn_core_masked")
+    return output
+
+
+def dispatch_triangle_attention(*, module: Any, q: Any, k: Any, v: Any, biases: Sequence[Any],
+                                native: Callable[..., Any]) -> Any:
+    """Select the HIP core or the caller's native lambda (same contract as the
+    reference's ``dispatch_triangle_attention``)."""
+    bias_shapes = tuple(tuple(int(x) for x in b.shape) for b in biases)
+    signature = signature_from_tensor(
+        OPERATION, q, architecture=_architecture(q), mode=_mode(module, (q, k, v)),
+        mask=("triangle-bias" if len(biases) == 1
+              else "additive-mask-and-triangle-bias" if len(biases) == 2 else "unsupported"),
+        inplace=False,
+        attributes={
+            "bias_count": len(biases),
+            "bias_shapes": repr(bias_shapes),
+            "qkv_strides": repr(tuple(tuple(t.stride()) for t in (q, k, v))),
+            "ck_tile_compatible": (
+                all(t.shape == q.shape and t.dtype == q.dtype and t.device == q.device
+                    and t.data_ptr() % 16 == 0 for t in (q, k, v))
+                and all(b.dtype == q.dtype and b.device == q.device for b in biases)),
+            "heads": q.shape[-3] if q.ndim >= 3 else -1,
+            "head_dim": q.shape[-1] if q.ndim else -1,
+        })
+    return registry.dispatch(signature, native, module=module, q=q, k=k, v=v, biases=biases,
+                             native=native)
+
+
+# ----------------------------------------------------------------- block
+
+def _weights_of(module: Any) -> BlockWeights:
+    if hasattr(module, "mha"):
+        return BlockWeights.from_protenix(module)
+    if hasattr(module, "linear_qkv"):
+        return BlockWeights.from_atlasfold(module)
+    raise TypeError(f"unrecognised triangle-attention module {type(module).__name__}")
+
+
+def block_eligible(module: Any, z: Any, mask: Any) -> tuple[bool, str]:
+    """Check the tensor/module contract that the signature cannot carry."""
+    import torch
+
+    if not getattr(z, "is_cuda", False) or z.dtype != torch.float32:
+        return False, "z is not a float32 HIP tensor"
+    if z.dim() != 3 or z.shape[0] != z.shape[1] or z.shape[2] != 128 or z.stride(2) != 1:
+        return False, "z must be [N, N, 128] with unit channel stride"
+    if z.stride(0) % 4 or z.stride(1) % 4 or z.data_ptr() % 16:
+        return False, "z rows are not 16-byte aligned"
+    if mask is not None and (tuple(mask.shape) != tuple(z.shape[:2]) or mask.device != z.device):
+        return False, "mask must be [N, N] on z's device"
+    heads = getattr(getattr(module, "mha", module), "no_heads", getattr(module, "num_heads", None))
+    dim = getattr(getattr(module, "mha", module), "c_hidden",
+                  getattr(module, "channel_hidden", None))
+    if heads != HEADS or dim != HEAD_DIM:
+        return False, "module must have 4 heads of dimension 32"
+    try:
+        weights = _weights_of(module)
+    except (AttributeError, TypeError, ValueError) as error:
+        return False, f"module layout: {error}"
+    if any(t is not None and (t.device != z.device or t.dtype != torch.float32)
+           for t in weights.tensors()):
+        return False, "weights are not float32 on z's device"
+    return True, ""
+
+
+def _supports_block(signature: OperationSignature) -> bool | tuple[bool, str]:
+    attributes = dict(signature.attributes)
+    if signature.device_type != "cuda":
+        return False, "device is not CUDA/HIP"
+    if signature.architecture != ARCHITECTURE:
+        return False, f"architecture is not {ARCHITECTURE}"
+    if signature.dtype != "float32":
+        return False, "dtype is not float32"
+    if signature.mode != "inference":
+        return False, "training or autograd is enabled"
+    if attributes.get("eligible") != "True":
+        return False, attributes.get("reason", "tensor/module contract mismatch")
+    if not _native.available():
+        return False, "HIP extension unavailable"
+    return True
+
+
+def _block(*, module: Any, z: Any, mask: Any, ending: bool, native: Any) -> Any:
+    del native
+    return triangle_attention_block(z, mask, _weights_of(module).to(z.device), ending=ending)
+
+
+def dispatch_triangle_attention_block(*, module: Any, z: Any, mask: Any, ending: bool,
+                                      native: Callable[..., Any]) -> Any:
+    """Module-level drop-in ``(z, mask) -> dz`` with native fallback."""
+    eligible, reason = block_eligible(module, z, mask)
+    signature = signature_from_tensor(
+        BLOCK_OPERATION, z, architecture=_architecture(z),
+        mode=_mode(module, (z,)), mask="none" if mask is None else "pair-mask", inplace=False,
+        attributes={"eligible": eligible, "reason": reason, "ending": bool(ending)})
+    return registry.dispatch(signature, native, module=module, z=z, mask=mask, ending=ending,
+                             native=native)
+
+
+registry.register(operation=OPERATION, name=IMPLEMENTATION, function=attention,
+                  supports=_supports_core, priority=30, version="1")
+registry.register(operation=BLOCK_OPERATION, name=BLOCK_IMPLEMENTATION, function=_block,
+                  supports=_supports_block, priority=30, version="1")

@@ -1,0 +1,96 @@
+"""Seeded synthetic workloads for the triangle-attention block.
+
+Five pair-representation configurations, c_z = 128, H = 4, d = 32:
+
+  c1  N=124,  FP32, starting node, mask all ones (the CPU-runnable case)
+  c2  N=512,  FP32, starting + ending, last 51 residues masked on both axes
+  c3  N=1000, FP32, starting + ending, mask all ones
+  c4  N=1536, FP32, starting + ending, z ~ 2*N(0,1), 12% tail masked
+      (1352 valid), triangle-bias weights x8 so logits span about +/-40
+  c5  N=2048, BF16 storage / FP32 accumulate, starting + ending, mask all ones
+
+Everything is drawn on the CPU from ``torch.Generator`` seeds (z: 419 + N,
+following benchmarks/protenix/benchmark_attention.py:145; weights: 719,
+following benchmarks/protenix/benchmark_attention_surround.py:38) so the HIP
+path and the oracle see identical bits.  Weights are N(0, 0.02) in torch
+``[out, in]`` layout with no bias vectors; LN gamma = 1, beta = 0.  The
+triangle-bias weight is N(0, 1/128) so the bias has std ~1 on unit-variance
+LN output (scaled by 8 for c4).  A mask of all ones is omitted (``None``), as
+the reference omits an implicit all-ones mask (patches/protenix/0005-*.patch:
+18-19).
+"""
+from __future__ import annotations
+
+import dataclasses
+import math
+
+import torch
+
+Z_SEED_BASE = 419
+WEIGHT_SEED = 719
+
+
+@dataclasses.dataclass(frozen=True)
+class Workload:
+    key: str
+    name: str
+    n: int
+    dtype: str                      # "f32" or "bf16" (storage)
+    directions: tuple[str, ...]
+    valid: int | None = None        # residues kept by the mask (None: no mask)
+    z_scale: float = 1.0
+    bias_scale: float = 1.0
+
+
+CONFIGS: dict[str, Workload] = {
+    "c1": Workload("c1", "n124-start-f32", 124, "f32", ("start",)),
+    "c2": Workload("c2", "n512-tail51-f32", 512, "f32", ("start", "end"), valid=461),
+    "c3": Workload("c3", "n1000-f32", 1000, "f32", ("start", "end")),
+    "c4": Workload("c4", "n1536-tail184-bias8-f32", 1536, "f32", ("start", "end"),
+                   valid=1536 - round(0.12 * 1536), z_scale=2.0, bias_scale=8.0),
+    "c5": Workload("c5", "n2048-bf16", 2048, "bf16", ("start", "end")),
+}
+
+
+def make_weights(bias_scale: float = 1.0, channels: int = 128, heads: int = 4,
+                 head_dim: int = 32) -> dict[str, torch.Tensor | None]:
+    g = torch.Generator().manual_seed(WEIGHT_SEED)
+    hidden = heads * head_dim
+
+    def normal(*shape, std):
+        return torch.randn(*shape, generator=g, dtype=torch.float32) * std
+
+    weights: dict[str, torch.Tensor | None] = {
+        "ln_w": torch.ones(channels),
+        "ln_b": torch.zeros(channels),
+        "w_q": normal(hidden, channels, std=0.02),
+        "w_k": normal(hidden, channels, std=0.02),
+        "w_v": normal(hidden, channels, std=0.02),
+        "w_g": normal(hidden, channels, std=0.02),
+        "b_g": None,
+        "w_bias": normal(heads, channels, std=1.0 / math.sqrt(channels)) * bias_scale,
+        "w_o": normal(channels, hidden, std=0.02),
+        "b_o": None,
+    }
+    return weights
+
+
+def make_pair(n: int, z_scale: float = 1.0, channels: int = 128) -> torch.Tensor:
+    g = torch.Generator().manual_seed(Z_SEED_BASE + n)
+    z = torch.randn(n, n, channels, generator=g, dtype=torch.float32)
+    return z * z_scale if z_scale != 1.0 else z
+
+
+def make_mask(n: int, valid: int | None) -> torch.Tensor | None:
+    if valid is None:
+        return None
+    keep = torch.arange(n) < valid
+    return (keep[:, None] & keep[None, :]).to(torch.float32)
+
+
+def make_inputs(cfg: Workload | str):
+    """Return ``(z, mask, weights)`` on the CPU for a configuration."""
+    if isinstance(cfg, str):
+        cfg = CONFIGS[cfg]
+    return (make_pair(cfg.n, cfg.z_scale), make_mask(cfg.n, cfg.valid),
+            make_weights(cfg.bias_scale))

@@ -1,0 +1,157 @@
+/*
+ * fireprot_amd -- C ABI of the MI355X (gfx950) triangle-attention block.
+ *
+ * Plain pointers and sizes only: no torch or HIP types appear in the
+ * signatures (streams are passed as void* hipStream_t).  Every entry point
+ *   - validates its arguments on the host before any device pointer is
+ *     dereferenced,
+ *   - enqueues its kernels on the caller's stream for the caller's current
+ *     device and returns without synchronising,
+ *   - allocates nothing: outputs and workspace belong to the caller,
+ *   - leaves its inputs unmodified,
+ *   - is stateless and reentrant.
+ *
+ * Status codes follow the reference C ABI (kernels/amd/fireprot_ck_attention.cpp:
+ * 35, 47, 106-108): 0 success; 2 unsupported sizes or layout; 3 a null or
+ * misaligned pointer; 4 workspace too small; any other value is the
+ * hipError_t of the failed launch.
+ *
+ * Paths in citations are relative to the reference checkout.
+ */
+#ifndef FIREPROT_AMD_H
+#define FIREPROT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FPX_ABI_VERSION 1
+
+#define FPX_OK 0
+#define FPX_ERR_DIMS 2
+#define FPX_ERR_POINTER 3
+#define FPX_ERR_WORKSPACE 4
+
+#define FPX_F32 0
+#define FPX_BF16 1
+
+/* ABI version of the loaded library (FPX_ABI_VERSION).
+ * Replaces the reference bridge's ABI_VERSION probe
+ * (crates/fireprot-bridge/src/lib.rs:151). */
+int fpx_abi_version(void);
+
+/* Bytes of device workspace fpx_tri_attn_block needs for an n x n pair
+ * representation; 0 for unsupported sizes.  No reference counterpart: the
+ * reference's native path allocates per call (docs/protenix-long1536.md:60-66). */
+size_t fpx_tri_attn_workspace_bytes(int n, int c, int heads, int head_dim, int dtype);
+
+/* The whole triangle-attention block (z[N,N,C], mask[N,N]) -> dz[N,N,C]:
+ * pair LayerNorm, fused q/k/v/gate projection, triangle-bias projection,
+ * row-wise attention with additive mask bias and pair bias, sigmoid gate and
+ * output projection.  Replaces the Protenix module call
+ * TriangleAttention.forward (patches/protenix/0005-*.patch:14-48, with
+ * Attention.forward from patches/protenix/0002-*.patch:31-58) and AtlasFold's
+ * triangle_attention(module, z, mask, ending) (python/fireprot/adapters/
+ * atlasfold/runtime.py:32-71).  The residual z += dz stays with the caller
+ * (patches/protenix/0006-*.patch:25).
+ *
+ *   z        [n][n][c] with element strides (z_stride0, z_stride1, 1)
+ *   mask     nullable float {0,1} [n][n], strides (m_stride0, m_stride1);
+ *            null omits the mask bias (patch 0005:18-19, 36-39)
+ *   ln_w/b   nullable LayerNorm affine [c]; eps as in the module (1e-5)
+ *   w_qkvg   [4*heads*head_dim][c]: W_q, W_k, W_v, W_g stacked, each torch
+ *            nn.Linear [out, in]
+ *   b_g      nullable gate bias [heads*head_dim]
+ *   w_bias   [heads][c] triangle-bias projection (no bias term)
+ *   w_o      [c][heads*head_dim]; b_o nullable [c]
+ *   mask_inf the module's inf (1e9)
+ *   ending   0: starting node; 1: ending node, dz = T(block(T(z), T(mask)))
+ *            read and written through strides, with no transposed copies
+ *   dz       [n][n][c] with strides (dz_stride0, dz_stride1, 1), z's frame
+ *   workspace at least fpx_tri_attn_workspace_bytes(...) bytes, 256-aligned
+ * Supported: dtype FPX_F32, c = 128, heads = 4, head_dim = 32, 1 <= n <= 4096.
+ */
+int fpx_tri_attn_block(int dtype, const void* z, int64_t z_stride0, int64_t z_stride1,
+                       const float* mask, int64_t m_stride0, int64_t m_stride1,
+                       const void* ln_w, const void* ln_b, float eps, const void* w_qkvg,
+                       const void* b_g, const void* w_bias, const void* w_o, const void* b_o,
+                       float mask_inf, int n, int c, int heads, int head_dim, int ending,
+                       void* dz, int64_t dz_stride0, int64_t dz_stride1, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/* The block's three stages, run in this order on one workspace;
+ * fpx_tri_attn_block is exactly prepare + attend + finish.  Split so a caller
+ * (or a profiler) can time or overlap the stages; the workspace carries the
+ * intermediate q/k/v^T/gate/bias between them.  No reference counterpart as
+ * separate calls: together they replace the same module call as
+ * fpx_tri_attn_block.
+ *   prepare: mask bias, pair LayerNorm, q/k/v/gate and triangle-bias
+ *            projections (patch 0005:32-45; qkv_projection.py:54-66)
+ *   attend:  flash attention with the gate multiplied in the epilogue
+ *            (patch 0002:57; attention_gate.py:52-53)
+ *   finish:  output projection into dz (attention_gate.py:54) */
+int fpx_tri_attn_prepare(int dtype, const void* z, int64_t z_stride0, int64_t z_stride1,
+                         const float* mask, int64_t m_stride0, int64_t m_stride1,
+                         const void* ln_w, const void* ln_b, float eps, const void* w_qkvg,
+                         const void* b_g, const void* w_bias, float mask_inf, int n, int ending,
+                         void* workspace, size_t workspace_bytes, void* stream);
+int fpx_tri_attn_attend(int dtype, int n, void* workspace, size_t workspace_bytes, void* stream);
+int fpx_tri_attn_finish(int dtype, const void* w_o, const void* b_o, int n, int ending, void* dz,
+                        int64_t dz_stride0, int64_t dz_stride1, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/* Attention core, argument-compatible with the reference's
+ *   int ck_attention(float* q, float* k, float* v, float* bias, float* out,
+ *                    int batch, int n, void* stream)
+ * (kernels/amd/fireprot_ck_attention.cpp:34, 66, 102; ctypes binding at
+ * python/fireprot/backends/amd/ck_attention.py:65-73).
+ * q, k, v, out: [batch][heads=4][n][32] viewed with strides (n*128, 32, 128, 1),
+ * i.e. memory [batch][n][4][32]; q already scaled by 1/sqrt(32).
+ * bias: [1][4][n][n] contiguous, shared by every batch row.
+ * Requires n % 4 == 0 and 16-byte aligned pointers. */
+int fpx_attn_core(float* q, float* k, float* v, float* bias, float* out, int batch, int n,
+                  void* stream);
+
+/* Attention core with the additive mask bias of the two-bias form
+ * biases = [mask_bias[batch,1,1,n], tri_bias[1,4,n,n]]
+ * (python/fireprot/backends/amd/triangle_attention.py:199-256, native lambda of
+ * patches/protenix/0002-*.patch:57).  mask_bias row b holds n values at
+ * mask_bias + b*mask_bias_stride (nullable: no mask); bias rows are
+ * bias_row_stride floats apart (>= n, multiple of 4), so padded rows such as
+ * the reference's 1552-float N1536 rows (ck_attention.py:126-130) are accepted.
+ * Logits are fl(fl(q.k + mask_bias) + bias) in that order. */
+int fpx_attn_core_masked(const float* q, const float* k, const float* v, const float* mask_bias,
+                         int64_t mask_bias_stride, const float* bias, int64_t bias_row_stride,
+                         float* out, int batch, int n, void* stream);
+
+/* LayerNorm over 128 channels of rows x[i][j] read at x + i*stride_i + j*stride_j
+ * (channel stride 1), written contiguously to y[rows_i][rows_j][128].  Covers
+ * both the contiguous pair LN (kernels/amd/fireprot_amd_ops.cu:27-64,
+ * layer_norm_f32_128*) and the transposed-view LN of the ending node
+ * (fireprot_amd_ops.cu:957-1104, transposed_layer_norm; dispatch at
+ * python/fireprot/backends/amd/recycle.py:293-357).  w, b nullable. */
+int fpx_layer_norm_c128(const float* x, int64_t rows_i, int64_t rows_j, int64_t stride_i,
+                        int64_t stride_j, const float* w, const float* b, float eps, float* y,
+                        void* stream);
+
+/* Fused q/k/v projection of already-normalised rows x[rows][128] with torch
+ * [128,128] weights; out is [3][rows][128] (q, k, v), q scaled by 1/sqrt(32).
+ * Replaces qkv_projection (kernels/amd/fireprot_amd_ops.cu:865-955; hook at
+ * python/fireprot/backends/amd/qkv_projection.py:54-66). */
+int fpx_qkv_projection(const float* x, int64_t rows, const float* wq, const float* wk,
+                       const float* wv, float* out, void* stream);
+
+/* out = value * sigmoid(gate) over count floats (count % 4 == 0), out of place.
+ * Replaces sigmoid_mul_out_f32 (kernels/amd/fireprot_amd_ops.cu:536-565; hook at
+ * python/fireprot/backends/amd/attention_gate.py:28-56). */
+int fpx_sigmoid_mul_out(const float* gate, const float* value, float* out, int64_t count,
+                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FIREPROT_AMD_H */

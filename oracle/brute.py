@@ -1,0 +1,144 @@
+"""Float64 brute force of the triangle-attention block -- TEST INFRASTRUCTURE ONLY.
+
+An independent formulation of the same native arithmetic as
+``oracle/triangle_attention.py``, written as explicit index loops in plain
+Python/NumPy float64 with no torch, no permutes and no broadcasting of the
+biases.  Each logit is formed element by element from the definitions
+
+    x[a, b, :]      = z[a, b, :]   (starting node)   or  z[b, a, :] (ending node)
+    xn[a, b, :]     = LayerNorm(x[a, b, :])                          (0005:32)
+    bias[h, a, b]   = sum_c xn[a, b, c] * w_bias[h, c]               (0005:42-45)
+    mb[i, k]        = inf * (mask_x[i, k] - 1)                       (0005:36-39)
+    q[i, h, j, d]   = sum_c xn[i, j, c] * w_q[h*D + d, c] / sqrt(D)  (0002:34-39)
+    logit[i,h,j,k]  = sum_d q[i,h,j,d] * k[i,h,k,d] + mb[i,k] + bias[h, j, k]
+    o[i, j, h, d]   = sum_k softmax_k(logit[i, h, j, :])[k] * v[i, h, k, d]
+    dz_x[i, j, :]   = w_o @ (o[i, j, :, :].flatten() * sigmoid(w_g @ xn[i, j] + b_g)) + b_o
+    dz[a, b]        = dz_x[a, b] (start) or dz_x[b, a] (end)
+
+so an index swap, a transposed operand or a dropped term in the vectorised
+oracle shows up as a mismatch.  It is used to write the committed fixtures under
+tests/golden/ and is only practical for N up to ~20.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+
+def _layer_norm_row(row: np.ndarray, w, b, eps: float) -> np.ndarray:
+    n = len(row)
+    mean = 0.0
+    for value in row:
+        mean += float(value)
+    mean /= n
+    var = 0.0
+    for value in row:
+        var += (float(value) - mean) ** 2
+    var /= n
+    inv = 1.0 / math.sqrt(var + eps)
+    out = np.empty(n, dtype=np.float64)
+    for c in range(n):
+        y = (float(row[c]) - mean) * inv
+        if w is not None:
+            y *= float(w[c])
+        if b is not None:
+            y += float(b[c])
+        out[c] = y
+    return out
+
+
+def block(z: np.ndarray, mask: np.ndarray | None, params: dict, *, ending: bool) -> np.ndarray:
+    """Return dz[N, N, C] in float64 for a tiny pair representation.
+
+    ``params`` holds numpy arrays ``ln_w, ln_b, w_q, w_k, w_v, w_g, b_g,
+    w_bias, w_o, b_o`` (torch ``[out, in]`` layout; ``ln_*``, ``b_g``, ``b_o``
+    may be None) and floats ``inf``, ``eps``.
+    """
+    z = np.asarray(z, dtype=np.float64)
+    n = z.shape[0]
+    heads, channels = params["w_bias"].shape
+    hd = params["w_q"].shape[0]
+    dim = hd // heads
+    inf = float(params["inf"])
+    eps = float(params["eps"])
+    f64 = {k: (None if v is None or isinstance(v, float) else np.asarray(v, dtype=np.float64))
+           for k, v in params.items()}
+
+    def x_of(a, b):
+        return z[b, a] if ending else z[a, b]
+
+    def mask_x(i, k):
+        if mask is None:
+            return None
+        return float(mask[k, i]) if ending else float(mask[i, k])
+
+    xn = np.empty((n, n, channels))
+    for a in range(n):
+        for b in range(n):
+            xn[a, b] = _layer_norm_row(x_of(a, b), f64["ln_w"], f64["ln_b"], eps)
+
+    def project(w, row):
+        out = np.zeros(w.shape[0])
+        for o in range(w.shape[0]):
+            acc = 0.0
+            for c in range(w.shape[1]):
+                acc += w[o, c] * row[c]
+            out[o] = acc
+        return out
+
+    bias = np.empty((heads, n, n))
+    q = np.empty((n, heads, n, dim))
+    k = np.empty((n, heads, n, dim))
+    v = np.empty((n, heads, n, dim))
+    gate = np.empty((n, n, hd))
+    scale = 1.0 / math.sqrt(dim)
+    for a in range(n):
+        for b in range(n):
+            row = xn[a, b]
+            pb = project(f64["w_bias"], row)
+            pq = project(f64["w_q"], row)
+            pk = project(f64["w_k"], row)
+            pv = project(f64["w_v"], row)
+            pg = project(f64["w_g"], row)
+            for h in range(heads):
+                bias[h, a, b] = pb[h]
+                for d in range(dim):
+                    q[a, h, b, d] = pq[h * dim + d] * scale
+                    k[a, h, b, d] = pk[h * dim + d]
+                    v[a, h, b, d] = pv[h * dim + d]
+            for e in range(hd):
+                g = pg[e] + (0.0 if f64["b_g"] is None else f64["b_g"][e])
+                gate[a, b, e] = 1.0 / (1.0 + math.exp(-g))
+
+    dz_x = np.empty((n, n, channels))
+    for i in range(n):
+        for j in range(n):
+            gated = np.empty(hd)
+            for h in range(heads):
+                logits = []
+                for kk in range(n):
+                    s = 0.0
+                    for d in range(dim):
+                        s += q[i, h, j, d] * k[i, h, kk, d]
+                    m = mask_x(i, kk)
+                    if m is not None:
+                        s += inf * (m - 1.0)
+                    s += bias[h, j, kk]
+                    logits.append(s)
+                top = max(logits)
+                weights = [math.exp(value - top) for value in logits]
+                total = sum(weights)
+                for d in range(dim):
+                    acc = 0.0
+                    for kk in range(n):
+                        acc += weights[kk] / total * v[i, h, kk, d]
+                    gated[h * dim + d] = acc * gate[i, j, h * dim + d]
+            out = project(f64["w_o"], gated)
+            if f64["b_o"] is not None:
+                out = out + f64["b_o"]
+            dz_x[i, j] = out
+
+    if ending:
+        return np.ascontiguousarray(dz_x.transpose(1, 0, 2))
+    return dz_x

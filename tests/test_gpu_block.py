@@ -1,0 +1,145 @@
+"""GPU parity of the whole block (fpx_tri_attn_block) against the CPU oracle.
+
+Bar (FP32): max-abs 1e-4 and rel 1e-4 elementwise against the native-order
+oracle on identical seeded inputs; NaN positions must agree.  Small and
+medium sizes compare every element; the N=1000 and N=1536 configurations
+compare a seeded subset of outer rows (rows are independent, so the oracle
+computes only those) and check size-independent properties on the full
+output.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from fireprot_amd import block as hip_block
+from fireprot_amd import workloads
+from oracle import triangle_attention as oracle
+from tests.helpers import assert_f32_parity, hip_weights, oracle_params, region_reports
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(z, mask, weights, ending):
+    with torch.inference_mode():
+        out = hip_block.triangle_attention_block(
+            z.cuda(), None if mask is None else mask.cuda(), hip_weights(weights), ending=ending)
+        torch.cuda.synchronize()
+    return out.cpu()
+
+
+@pytest.mark.parametrize("ending", [False, True])
+@pytest.mark.parametrize("n,valid", [(1, None), (5, None), (7, 5), (37, 30), (124, None),
+                                     (124, 101), (129, 100), (160, None)])
+def test_block_small_matches_oracle(n, valid, ending):
+    print(f"case n={n} valid={valid} ending={ending}", flush=True)
+    z = workloads.make_pair(n)
+    mask = workloads.make_mask(n, valid)
+    w = workloads.make_weights()
+    actual = _run(z, mask, w, ending)
+    expected = oracle.block(z, mask, oracle_params(w), ending=ending)
+    assert_f32_parity(f"n={n} valid={valid} ending={ending}", actual, expected)
+
+
+def test_block_with_affine_ln_and_gate_biases():
+    n = 48
+    z = workloads.make_pair(n)
+    mask = workloads.make_mask(n, 40)
+    g = torch.Generator().manual_seed(5)
+    w = workloads.make_weights()
+    w["ln_w"] = 1.0 + 0.1 * torch.randn(128, generator=g)
+    w["ln_b"] = 0.1 * torch.randn(128, generator=g)
+    w["b_g"] = torch.randn(128, generator=g)
+    w["b_o"] = 0.1 * torch.randn(128, generator=g)
+    for ending in (False, True):
+        actual = _run(z, mask, w, ending)
+        expected = oracle.block(z, mask, oracle_params(w), ending=ending)
+        assert_f32_parity(f"affine ending={ending}", actual, expected)
+
+
+@pytest.mark.parametrize("ending", [False, True])
+def test_c2_n512_masked_full(ending):
+    cfg = workloads.CONFIGS["c2"]
+    print(f"case {cfg.name} ending={ending}", flush=True)
+    z, mask, w = workloads.make_inputs(cfg)
+    actual = _run(z, mask, w, ending)
+    expected = oracle.block(z, mask, oracle_params(w), ending=ending)
+    region_reports(f"{cfg.name} ending={ending}", actual.transpose(0, 1) if ending else actual,
+                   expected.transpose(0, 1) if ending else expected, cfg.valid)
+    assert_f32_parity(f"{cfg.name} ending={ending}", actual, expected)
+
+
+def _sample_rows(n, valid, count=12, seed=11):
+    g = torch.Generator().manual_seed(seed)
+    rows = {0, 1, n - 1, n // 2}
+    if valid is not None and valid < n:
+        rows |= {valid - 1, valid, min(valid + 1, n - 1)}
+    rows |= set(torch.randint(0, n, (count,), generator=g).tolist())
+    return torch.tensor(sorted(rows))
+
+
+@pytest.mark.parametrize("key", ["c3", "c4"])
+def test_long_configs_row_subset_and_transpose_identity(key):
+    cfg = workloads.CONFIGS[key]
+    print(f"case {cfg.name}", flush=True)
+    z, mask, w = workloads.make_inputs(cfg)
+    params = oracle_params(w)
+    rows = _sample_rows(cfg.n, cfg.valid)
+    zc = z.cuda()
+    mc = None if mask is None else mask.cuda()
+    weights = hip_weights(w)
+    with torch.inference_mode():
+        start = hip_block.triangle_attention_block(zc, mc, weights, ending=False)
+        end = hip_block.triangle_attention_block(zc, mc, weights, ending=True)
+        # ending node == T(starting node on T(z), T(mask)), bit for bit
+        zt = zc.transpose(0, 1).contiguous()
+        mt = None if mc is None else mc.transpose(0, 1).contiguous()
+        end_ref = hip_block.triangle_attention_block(zt, mt, weights, ending=False).transpose(0, 1)
+        again = hip_block.triangle_attention_block(zc, mc, weights, ending=False)
+        torch.cuda.synchronize()
+        assert torch.equal(end, end_ref), "ending node differs from T(start(T(z)))"
+        assert torch.equal(start, again), "block is not deterministic"
+        assert torch.isfinite(start).all() and torch.isfinite(end).all()
+        start_rows = start[rows.cuda()].cpu()
+        end_rows = end.transpose(0, 1)[rows.cuda()].cpu()
+    del zc, zt, start, end, end_ref, again
+    torch.cuda.empty_cache()
+    exp_start = oracle.block(z, mask, params, ending=False, outer_rows=rows)
+    exp_end = oracle.block(z, mask, params, ending=True, outer_rows=rows)
+    region_reports(f"{cfg.name} start", start_rows, exp_start, cfg.valid, rows)
+    region_reports(f"{cfg.name} end", end_rows, exp_end, cfg.valid, rows)
+    assert_f32_parity(f"{cfg.name} start rows", start_rows, exp_start)
+    assert_f32_parity(f"{cfg.name} end rows", end_rows, exp_end)
+
+
+def test_block_inputs_unchanged_streams_and_queue():
+    n = 96
+    z, mask, w = workloads.make_pair(n), workloads.make_mask(n, 80), workloads.make_weights()
+    expected = oracle.block(z, mask, oracle_params(w), ending=False)
+    zc, mc, weights = z.cuda(), mask.cuda(), hip_weights(w)
+    saved = [t.clone() for t in (zc, mc, weights.w_qkvg, weights.w_bias, weights.w_o)]
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.inference_mode(), torch.cuda.stream(stream):
+        outs = [hip_block.triangle_attention_block(zc, mc, weights) for _ in range(3)]
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    for out in outs:
+        assert out.is_contiguous()
+        assert_f32_parity("queued", out.cpu(), expected)
+    for t, before in zip((zc, mc, weights.w_qkvg, weights.w_bias, weights.w_o), saved):
+        assert torch.equal(t, before)
+
+
+def test_block_output_canaries_and_strided_dz():
+    n = 64
+    z, mask, w = workloads.make_pair(n), workloads.make_mask(n, 50), workloads.make_weights()
+    expected = oracle.block(z, mask, oracle_params(w), ending=True)
+    storage = torch.full((n * n * 128 + 8192,), 123.5, device="cuda")
+    out = storage[4096:-4096].view(n, n, 128)
+    with torch.inference_mode():
+        hip_block.triangle_attention_block(z.cuda(), mask.cuda(), hip_weights(w), ending=True,
+                                           out=out)
+        torch.cuda.synchronize()
+    assert bool((storage[:4096] == 123.5).all()) and bool((storage[-4096:] == 123.5).all())
+    assert_f32_parity("canary", out.cpu(), expected)
