@@ -16,8 +16,17 @@ biases.  Each logit is formed element by element from the definitions
     dz[a, b]        = dz_x[a, b] (start) or dz_x[b, a] (end)
 
 so an index swap, a transposed operand or a dropped term in the vectorised
-oracle shows up as a mismatch.  It is used to write the committed fixtures under
-tests/golden/ and is only practical for N up to ~20.
+oracle shows up as a mismatch.
+
+``logits="f32"`` rounds each logit to float32 at the two native add points,
+fl32(fl32(fl32(s) + fl32(mb)) + fl32(bias)) (mask first, then bias:
+patches/protenix/0005-*.patch:36-45), and keeps everything else in float64.
+That reproduces what the FP32 native path does to fully masked rows: -1e9 has
+a float32 spacing of 64, so their logits collapse onto a few values and the
+softmax weights follow those ties, which plain float64 does not show.
+
+It is used to write the committed fixtures under tests/golden/ and is only
+practical for N up to ~20.
 """
 from __future__ import annotations
 
@@ -48,13 +57,17 @@ def _layer_norm_row(row: np.ndarray, w, b, eps: float) -> np.ndarray:
     return out
 
 
-def block(z: np.ndarray, mask: np.ndarray | None, params: dict, *, ending: bool) -> np.ndarray:
+def block(z: np.ndarray, mask: np.ndarray | None, params: dict, *, ending: bool,
+          logits: str = "f64") -> np.ndarray:
     """Return dz[N, N, C] in float64 for a tiny pair representation.
 
     ``params`` holds numpy arrays ``ln_w, ln_b, w_q, w_k, w_v, w_g, b_g,
     w_bias, w_o, b_o`` (torch ``[out, in]`` layout; ``ln_*``, ``b_g``, ``b_o``
     may be None) and floats ``inf``, ``eps``.
     """
+    if logits not in ("f64", "f32"):
+        raise ValueError("logits must be 'f64' or 'f32'")
+    f32 = logits == "f32"
     z = np.asarray(z, dtype=np.float64)
     n = z.shape[0]
     heads, channels = params["w_bias"].shape
@@ -116,18 +129,25 @@ def block(z: np.ndarray, mask: np.ndarray | None, params: dict, *, ending: bool)
         for j in range(n):
             gated = np.empty(hd)
             for h in range(heads):
-                logits = []
+                row_logits = []
                 for kk in range(n):
                     s = 0.0
                     for d in range(dim):
                         s += q[i, h, j, d] * k[i, h, kk, d]
                     m = mask_x(i, kk)
-                    if m is not None:
-                        s += inf * (m - 1.0)
-                    s += bias[h, j, kk]
-                    logits.append(s)
-                top = max(logits)
-                weights = [math.exp(value - top) for value in logits]
+                    if f32:
+                        s = float(np.float32(s))
+                        if m is not None:
+                            mb = float(np.float32(np.float32(inf) * np.float32(m - 1.0)))
+                            s = float(np.float32(s + mb))
+                        s = float(np.float32(s + float(np.float32(bias[h, j, kk]))))
+                    else:
+                        if m is not None:
+                            s += inf * (m - 1.0)
+                        s += bias[h, j, kk]
+                    row_logits.append(s)
+                top = max(row_logits)
+                weights = [math.exp(value - top) for value in row_logits]
                 total = sum(weights)
                 for d in range(dim):
                     acc = 0.0

@@ -1,0 +1,112 @@
+"""The C-ABI library on the CPU: it loads without a GPU, exports every entry
+point include/fireprot_amd.h declares (and the ctypes bindings cover them),
+and rejects bad arguments on the host before touching any device pointer
+(status 2 sizes/layout, 3 pointers, 4 workspace), as the reference's C ABI
+does (kernels/amd/fireprot_ck_attention.cpp:35, 47, 106-108;
+tests/operators/test_ck_attention_vector1000.py:16-18).  No call here
+reaches a kernel launch."""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import re
+
+import pytest
+
+from fireprot_amd import _native
+
+HEADER = pathlib.Path(__file__).resolve().parents[1] / "include" / "fireprot_amd.h"
+
+
+def _declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(fpx_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _native.LIB_PATH.exists():
+        from fireprot_amd import build
+        build.build()
+    return _native.library()
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    declared = _declared()
+    assert len(declared) >= 10
+    raw = ctypes.CDLL(str(_native.LIB_PATH))
+    for name in declared:
+        assert hasattr(raw, name), f"{name} declared but not exported"
+    assert sorted(_native.SIGNATURES) == declared
+
+
+def test_abi_version_and_workspace_sizes(lib):
+    assert lib.fpx_abi_version() == _native.ABI_VERSION == 1
+    for n in (1, 124, 512, 1000, 1536, 2048):
+        np_ = -(-n // 128) * 128
+        seg = lambda b: -(-b // 256) * 256  # noqa: E731
+        expected = (3 * seg(n * 4 * np_ * 32 * 4) + 2 * seg(n * n * 128 * 4)
+                    + seg(4 * np_ * np_ * 4) + seg(n * np_ * 4))
+        assert lib.fpx_tri_attn_workspace_bytes(n, 128, 4, 32, 0) == expected
+    for bad in ((0, 128, 4, 32, 0), (4097, 128, 4, 32, 0), (64, 64, 4, 32, 0),
+                (64, 128, 8, 32, 0), (64, 128, 4, 16, 0), (64, 128, 4, 32, 7)):
+        assert lib.fpx_tri_attn_workspace_bytes(*bad) == 0
+
+
+def _block_args(**override):
+    args = dict(dtype=0, z=256, zs0=64 * 128, zs1=128, mask=None, ms0=0, ms1=0, ln_w=None,
+                ln_b=None, eps=1e-5, w_qkvg=256, b_g=None, w_bias=256, w_o=256, b_o=None,
+                inf=1e9, n=64, c=128, heads=4, head_dim=32, ending=0, dz=256, ds0=64 * 128,
+                ds1=128, ws=256, ws_bytes=1, stream=None)
+    args.update(override)
+    return list(args.values())
+
+
+def test_block_guards(lib):
+    f = lib.fpx_tri_attn_block
+    assert f(*_block_args()) == 4                                   # workspace too small
+    assert f(*_block_args(n=0)) == 2
+    assert f(*_block_args(c=64)) == 2
+    assert f(*_block_args(dtype=1)) == 2                            # BF16 block not built
+    assert f(*_block_args(ending=2)) == 2
+    assert f(*_block_args(zs1=126)) == 2                            # rows not 16-byte aligned
+    assert f(*_block_args(eps=-1.0)) == 2
+    assert f(*_block_args(inf=float("inf"))) == 2
+    assert f(*_block_args(z=None)) == 3
+    assert f(*_block_args(z=260)) == 3
+    assert f(*_block_args(w_o=None)) == 3
+    assert f(*_block_args(ws=128)) == 3                              # 256-byte workspace
+    assert f(*_block_args(mask=2)) == 3
+    assert lib.fpx_tri_attn_attend(0, 64, 256, 1, None) == 4
+    assert lib.fpx_tri_attn_attend(0, 0, 256, 1, None) == 2
+    assert lib.fpx_tri_attn_attend(0, 64, None, 1 << 40, None) == 3
+
+
+def test_core_and_stage_op_guards(lib):
+    core = lib.fpx_attn_core
+    assert core(None, None, None, None, None, 1000, 999, None) == 2
+    assert core(None, None, None, None, None, 0, 1000, None) == 2
+    assert core(None, None, None, None, None, 1000, 1000, None) == 3
+    assert core(4, 16, 16, 16, 16, 1000, 1000, None) == 3
+    masked = lib.fpx_attn_core_masked
+    assert masked(16, 16, 16, None, 0, 16, 1000, 16, 1, 1004, None) == 2   # stride < n
+    assert masked(16, 16, 16, None, 0, 16, 1002, 16, 1, 1000, None) == 2   # stride % 4
+    assert masked(16, 16, 16, 2, 1000, 16, 1000, 16, 1, 1000, None) == 3   # mask alignment
+    ln = lib.fpx_layer_norm_c128
+    assert ln(16, -1, 1, 128, 128, None, None, 1e-5, 16, None) == 2
+    assert ln(16, 1, 1, 127, 128, None, None, 1e-5, 16, None) == 2
+    assert ln(None, 1, 1, 128, 128, None, None, 1e-5, 16, None) == 3
+    assert ln(16, 1, 1, 128, 128, 4, None, 1e-5, 16, None) == 3
+    qkv = lib.fpx_qkv_projection
+    assert qkv(16, -1, 16, 16, 16, 16, None) == 2
+    assert qkv(16, 10, 16, None, 16, 16, None) == 3
+    sig = lib.fpx_sigmoid_mul_out
+    assert sig(16, 16, 16, 6, None) == 2
+    assert sig(16, 8, 16, 8, None) == 3
+
+
+def test_status_errors_raise():
+    _native.check(0, "ok")
+    for code, word in ((2, "unsupported"), (3, "pointer"), (4, "workspace"), (98, "HIP")):
+        with pytest.raises(RuntimeError, match=word):
+            _native.check(code, "call")

@@ -1,0 +1,140 @@
+"""Capability predicates and native fallback of the dispatch surfaces on the
+CPU (mirrors tests/operators/test_triangle_attention.py:99-189,
+test_ck_attention.py:14-41 and the hook fallback tests of the reference)."""
+from __future__ import annotations
+
+import dataclasses
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from fireprot_amd import _native, attention_gate, block, layer_norm, pair_layout, qkv_projection
+from fireprot_amd import triangle_attention as ta
+from fireprot_amd.registry import OperationSignature, registry
+
+
+def _core_signature(**change):
+    n = 1536
+    base = dict(operation=ta.OPERATION, device_type="cuda", architecture="gfx950",
+                dtype="float32", shape=(512, 4, n, 32), layout="strided", mode="inference",
+                mask="triangle-bias", inplace=False,
+                attributes={"bias_shapes": repr(((1, 4, n, n),)),
+                            "qkv_strides": repr(((n * 128, 32, 128, 1),) * 3),
+                            "ck_tile_compatible": True})
+    base.update(change)
+    return OperationSignature.create(**base)
+
+
+def test_core_capability_accepts_validated_signature(monkeypatch):
+    monkeypatch.setattr(_native, "available", lambda: True)
+    assert ta._supports_core(_core_signature()) is True
+    masked = _core_signature(mask="additive-mask-and-triangle-bias", attributes={
+        "bias_shapes": repr(((512, 1, 1, 1536), (1, 4, 1536, 1536))),
+        "qkv_strides": repr(((1536 * 128, 32, 128, 1),) * 3), "ck_tile_compatible": True})
+    assert ta._supports_core(masked) is True
+    for change in (dict(device_type="cpu"), dict(architecture="gfx90a"),
+                   dict(dtype="bfloat16"), dict(mode="training"), dict(shape=(512, 8, 1536, 16)),
+                   dict(shape=(512, 4, 1534, 32))):
+        assert ta._supports_core(_core_signature(**change))[0] is False
+    sig = _core_signature()
+    for key, value in (("ck_tile_compatible", "False"), ("qkv_strides", "other"),
+                       ("bias_shapes", repr(((1, 4, 7, 7),)))):
+        attributes = dict(sig.attributes)
+        attributes[key] = value
+        changed = dataclasses.replace(sig, attributes=tuple(sorted(attributes.items())))
+        assert ta._supports_core(changed)[0] is False
+    monkeypatch.setattr(_native, "available", lambda: False)
+    assert ta._supports_core(sig) == (False, "HIP extension unavailable")
+
+
+def test_core_dispatch_falls_back_for_cpu_tensors():
+    q = torch.randn(5, 4, 8, 32).transpose(1, 2).contiguous().transpose(1, 2)
+    biases = [torch.zeros(5, 1, 1, 8), torch.zeros(1, 4, 8, 8)]
+    registry.clear_runtime_state()
+    with torch.inference_mode():
+        result = ta.dispatch_triangle_attention(module=SimpleNamespace(training=False), q=q, k=q,
+                                                v=q, biases=biases, native=lambda **_: "native")
+    assert result == "native"
+    decision = registry.manifest()["decisions"][0]
+    assert decision["signature"]["mode"] == "inference"
+    assert decision["rejected"][0]["reason"] == "device is not CUDA/HIP"
+    with torch.enable_grad():
+        qg = q.clone().requires_grad_()
+        ta.dispatch_triangle_attention(module=SimpleNamespace(training=False), q=qg, k=q, v=q,
+                                       biases=biases, native=lambda **_: None)
+    modes = {d["signature"]["mode"] for d in registry.manifest()["decisions"]}
+    assert modes == {"inference", "training"}
+
+
+class _Linear(torch.nn.Linear):
+    pass
+
+
+def _protenix_like(bias_g=True):
+    mha = SimpleNamespace(linear_q=torch.nn.Linear(128, 128, bias=False),
+                          linear_k=torch.nn.Linear(128, 128, bias=False),
+                          linear_v=torch.nn.Linear(128, 128, bias=False),
+                          linear_g=torch.nn.Linear(128, 128, bias=bias_g),
+                          linear_o=torch.nn.Linear(128, 128), no_heads=4, c_hidden=32)
+    return SimpleNamespace(layer_norm=torch.nn.LayerNorm(128), linear=torch.nn.Linear(128, 4, bias=False),
+                           mha=mha, inf=1e9, training=False)
+
+
+def test_block_weights_from_protenix_and_atlasfold():
+    m = _protenix_like()
+    w = block.BlockWeights.from_protenix(m)
+    assert w.w_qkvg.shape == (512, 128) and w.w_qkvg.is_contiguous()
+    assert torch.equal(w.w_qkvg[256:384], m.mha.linear_v.weight)
+    assert torch.equal(w.b_g, m.mha.linear_g.bias) and w.inf == 1e9 and w.eps == 1e-5
+    m.mha.linear_q = torch.nn.Linear(128, 128)
+    with pytest.raises(ValueError):
+        block.BlockWeights.from_protenix(m)
+    a = SimpleNamespace(layernorm=torch.nn.LayerNorm(128), linear_qkv=torch.nn.Linear(128, 384, bias=False),
+                        linear_bias=torch.nn.Linear(128, 4, bias=False),
+                        linear_g=torch.nn.Linear(128, 128, bias=False),
+                        linear_out=torch.nn.Linear(128, 128, bias=False), inf=1e9)
+    w = block.BlockWeights.from_atlasfold(a)
+    assert torch.equal(w.w_qkvg[:384], a.linear_qkv.weight) and w.b_g is None and w.b_o is None
+
+
+def test_block_dispatch_falls_back_on_cpu_and_reports_reason():
+    m = _protenix_like()
+    z = torch.randn(8, 8, 128)
+    registry.clear_runtime_state()
+    with torch.inference_mode():
+        assert ta.dispatch_triangle_attention_block(module=m, z=z, mask=None, ending=False,
+                                                    native=lambda **_: "native") == "native"
+    decision = registry.manifest()["decisions"][0]
+    assert decision["selected"] == "native"
+    assert decision["rejected"][0]["reason"] == "device is not CUDA/HIP"
+    assert ta.block_eligible(m, z, None) == (False, "z is not a float32 HIP tensor")
+
+
+def test_block_entry_raises_without_a_device():
+    z = torch.randn(4, 4, 128)
+    w = block.BlockWeights.from_protenix(_protenix_like())
+    with pytest.raises((ValueError, RuntimeError)):
+        block.triangle_attention_block(z, None, w)
+
+
+def test_stage_hooks_fall_back_on_cpu():
+    sentinel = object()
+    module = torch.nn.LayerNorm(128).eval()
+    x = torch.randn(4, 4, 128)
+    with torch.inference_mode():
+        assert layer_norm.dispatch_layer_norm(module=module, x=x, native=lambda: sentinel) is sentinel
+    attn = SimpleNamespace(training=False, no_heads=4, c_hidden=32)
+    assert qkv_projection.prepare(module=attn, q_x=x, kv_x=x, apply_scale=True,
+                                  native=lambda: sentinel) is sentinel
+    assert attention_gate.wrap_up(module=SimpleNamespace(training=False, linear_g=None), o=None,
+                                  x=x, native=lambda: sentinel) is sentinel
+    y = pair_layout.transpose_pair(x, training=False)
+    assert y.is_contiguous() and y.data_ptr() != x.data_ptr()
+    assert torch.equal(y, x.transpose(0, 1))
+
+
+def test_registered_implementations():
+    impl = registry.manifest()["implementations"]
+    assert impl[ta.OPERATION][0]["name"] == ta.IMPLEMENTATION
+    assert impl[ta.BLOCK_OPERATION][0]["name"] == ta.BLOCK_IMPLEMENTATION

@@ -143,3 +143,18 @@ def test_block_output_canaries_and_strided_dz():
         torch.cuda.synchronize()
     assert bool((storage[:4096] == 123.5).all()) and bool((storage[-4096:] == 123.5).all())
     assert_f32_parity("canary", out.cpu(), expected)
+
+
+@pytest.mark.parametrize("name", ["n5_plain", "n7_tail", "n9_random_x8", "n6_order"])
+@pytest.mark.parametrize("ending", [False, True])
+def test_block_matches_golden_fixtures(name, ending):
+    """The HIP block against the brute-force fixtures' FP32-logit expectation,
+    fully masked rows included (their -1e9-quantised ties must match)."""
+    from tests.test_oracle import load_case
+
+    z, mask, params, expected = load_case(name, torch.float32)
+    weights = {k: getattr(params, k) for k in ("ln_w", "ln_b", "w_q", "w_k", "w_v", "w_g",
+                                                "b_g", "w_bias", "w_o", "b_o")}
+    actual = _run(z, mask, weights, ending)
+    tag = "end" if ending else "start"
+    torch.testing.assert_close(actual.double(), expected[f"dz_{tag}_f32l"], atol=2e-6, rtol=1e-4)

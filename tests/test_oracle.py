@@ -1,0 +1,222 @@
+"""Pin the CPU oracle (oracle/triangle_attention.py) before trusting it.
+
+* against the committed fixtures written by the independent float64 brute
+  force (tests/golden/make_golden.py): the float64 oracle to 1e-10, the FP32
+  oracle to the float32-logit expectation (which fixes the native treatment of
+  fully masked rows);
+* against closed forms of the core (N=1, uniform logits, a +80 key, an all
+  -inf row, v = 1) and of LayerNorm and the gate;
+* against invariants (key permutation, masked keys, outer-row chunking, the
+  ending node as T o start o T);
+* and by planting plausible mistakes in a copy of the oracle (a transposed
+  bias, a transposed mask, a dropped gate, an unbiased variance, bias added
+  before the mask) and checking that the fixtures reject each one.
+"""
+from __future__ import annotations
+
+import pathlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import triangle_attention as oracle
+
+GOLDEN = pathlib.Path(__file__).resolve().parent / "golden"
+CASES = ("n5_plain", "n7_tail", "n9_random_x8", "n6_order")
+PARAM_KEYS = ("ln_w", "ln_b", "w_q", "w_k", "w_v", "w_g", "b_g", "w_bias", "w_o", "b_o")
+
+
+def load_case(name: str, dtype=torch.float64):
+    data = np.load(GOLDEN / f"{name}.npz")
+
+    def get(key):
+        for candidate in (key, f"w_{key}"):
+            if candidate in data.files:
+                return torch.from_numpy(data[candidate]).to(dtype)
+        return None
+
+    params = oracle.BlockParams(**{k: get(k) for k in PARAM_KEYS})
+    z = torch.from_numpy(data["z"]).to(dtype)
+    mask = get("mask") if "mask" in data.files else None
+    expected = {k: torch.from_numpy(data[k]) for k in data.files if k.startswith("dz_")}
+    return z, mask, params, expected
+
+
+@pytest.mark.parametrize("name", CASES)
+@pytest.mark.parametrize("ending", [False, True])
+def test_float64_oracle_matches_brute_force(name, ending):
+    z, mask, params, expected = load_case(name)
+    dz = oracle.block(z, mask, params, ending=ending)
+    tag = "end" if ending else "start"
+    torch.testing.assert_close(dz, expected[f"dz_{tag}_f64"], atol=1e-12, rtol=1e-10)
+
+
+@pytest.mark.parametrize("name", CASES)
+@pytest.mark.parametrize("ending", [False, True])
+def test_float32_oracle_matches_float32_logit_brute_force(name, ending):
+    z, mask, params, expected = load_case(name, torch.float32)
+    dz = oracle.block(z, mask, params, ending=ending)
+    tag = "end" if ending else "start"
+    torch.testing.assert_close(dz.double(), expected[f"dz_{tag}_f32l"], atol=2e-6, rtol=1e-4)
+
+
+def test_fixture_pins_fully_masked_row_quantisation():
+    """Row 4 of n9_random_x8 is fully masked: its FP32 logits tie at -1e9 + 64k,
+    so the FP32 result differs from float64 there, and the FP32 oracle follows
+    the FP32 expectation, not the float64 one."""
+    z, mask, params, expected = load_case("n9_random_x8", torch.float32)
+    f64 = expected["dz_start_f64"][4]
+    f32l = expected["dz_start_f32l"][4]
+    assert (f64 - f32l).abs().max() > 1e-3
+    dz = oracle.block(z, mask, params, ending=False)[4].double()
+    torch.testing.assert_close(dz, f32l, atol=2e-6, rtol=1e-4)
+    valid = [0, 1, 2, 3, 5, 6, 7, 8]
+    torch.testing.assert_close(expected["dz_start_f64"][valid], expected["dz_start_f32l"][valid],
+                               atol=1e-6, rtol=1e-4)
+
+
+# ---------------------------------------------------------------- closed forms
+
+def _qkv(b, h, n, d, seed):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(b, h, n, d, generator=g, dtype=torch.float64) for _ in range(3)]
+
+
+def test_core_single_key_returns_v():
+    q, k, v = _qkv(2, 4, 1, 32, 1)
+    bias = torch.randn(1, 4, 1, 1, dtype=torch.float64)
+    torch.testing.assert_close(oracle.attention_core(q, k, v, [bias]), v)
+
+
+def test_core_uniform_logits_give_mean_of_v():
+    _, k, v = _qkv(2, 4, 9, 32, 2)
+    q = torch.zeros_like(k)
+    bias = torch.zeros(1, 4, 9, 9, dtype=torch.float64)
+    out = oracle.attention_core(q, k, v, [bias])
+    torch.testing.assert_close(out, v.mean(dim=-2, keepdim=True).expand_as(out))
+
+
+def test_core_dominant_key_and_all_inf_row():
+    q, k, v = _qkv(1, 4, 6, 32, 3)
+    q = q * 0.01
+    bias = torch.zeros(1, 4, 6, 6, dtype=torch.float64)
+    bias[..., 2, 4] = 80.0
+    bias[..., 3, :] = float("-inf")
+    out = oracle.attention_core(q, k, v, [bias])
+    torch.testing.assert_close(out[..., 2, :], v[..., 4, :], atol=1e-30, rtol=1e-12)
+    assert torch.isnan(out[..., 3, :]).all()
+    assert torch.isfinite(out[..., [0, 1, 2, 4, 5], :]).all()
+
+
+def test_core_weights_sum_to_one():
+    q, k, _ = _qkv(3, 4, 11, 32, 4)
+    v = torch.ones(3, 4, 11, 32, dtype=torch.float64)
+    bias = torch.randn(1, 4, 11, 11, dtype=torch.float64) * 5
+    torch.testing.assert_close(oracle.attention_core(q, k, v, [bias]), v)
+
+
+def test_core_key_permutation_equivariance_and_masked_key():
+    q, k, v = _qkv(2, 4, 8, 32, 5)
+    bias = torch.randn(1, 4, 8, 8, dtype=torch.float64)
+    mask = torch.ones(2, 8, dtype=torch.float64)
+    mask[0, 3] = 0.0
+    out = oracle.attention_core(q, k, v, [oracle.mask_bias(mask), bias])
+    perm = torch.randperm(8, generator=torch.Generator().manual_seed(6))
+    out_p = oracle.attention_core(q, k[..., perm, :], v[..., perm, :],
+                                  [oracle.mask_bias(mask[:, perm]), bias[..., perm]])
+    torch.testing.assert_close(out, out_p)
+    keep = [i for i in range(8) if i != 3]
+    dropped = oracle.attention_core(q[:1], k[:1, :, keep], v[:1, :, keep], [bias[..., keep]])
+    torch.testing.assert_close(out[:1], dropped)
+
+
+def test_layer_norm_closed_form():
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(5, 128, generator=g, dtype=torch.float64) * 3 + 2
+    y = oracle.layer_norm(x, None, None, 0.0)
+    torch.testing.assert_close(y.mean(-1), torch.zeros(5, dtype=torch.float64), atol=1e-12, rtol=0)
+    torch.testing.assert_close((y * y).mean(-1), torch.ones(5, dtype=torch.float64))
+    const = torch.full((1, 128), 1000.0, dtype=torch.float64)
+    b = torch.randn(128, generator=g, dtype=torch.float64)
+    torch.testing.assert_close(oracle.layer_norm(const, torch.ones(128, dtype=torch.float64), b),
+                               b.unsqueeze(0))
+
+
+def test_gate_closed_form():
+    x = torch.zeros(2, 3, 128, dtype=torch.float64)
+    o = torch.randn(2, 3, 4, 32, dtype=torch.float64)
+    gate = torch.linspace(-1000, 1000, 128, dtype=torch.float64)
+    eye = torch.eye(128, dtype=torch.float64)
+    p = oracle.BlockParams(None, None, eye, eye, eye, eye, gate, torch.zeros(4, 128), eye, None)
+    out = oracle.wrap_up(o, x, p)
+    expected = o.reshape(2, 3, 128) * (1.0 / (1.0 + torch.exp(-gate)))
+    torch.testing.assert_close(out, expected)
+    assert (out[..., 0] == 0).all() and torch.equal(out[..., -1], o.reshape(2, 3, 128)[..., -1])
+
+
+# ------------------------------------------------------------------ invariants
+
+def test_block_chunking_rows_and_ending_transpose():
+    z, mask, params, _ = load_case("n9_random_x8")
+    full = oracle.block(z, mask, params, ending=False, chunk=64)
+    torch.testing.assert_close(oracle.block(z, mask, params, ending=False, chunk=1), full)
+    rows = torch.tensor([0, 4, 8])
+    torch.testing.assert_close(oracle.block(z, mask, params, ending=False, outer_rows=rows),
+                               full[rows])
+    end = oracle.block(z, mask, params, ending=True)
+    end_t = oracle.block(z.transpose(0, 1), mask.transpose(0, 1), params, ending=False)
+    torch.testing.assert_close(end, end_t.transpose(0, 1))
+    end_rows = oracle.block(z, mask, params, ending=True, outer_rows=rows)
+    torch.testing.assert_close(end_rows, end.transpose(0, 1)[rows])
+
+
+# ------------------------------------------------------ planted mistakes fail
+
+def _mutated_block(monkeypatch, kind):
+    if kind == "bias_transposed":
+        orig = oracle.triangle_bias
+        monkeypatch.setattr(oracle, "triangle_bias",
+                            lambda x, p: orig(x, p).transpose(-1, -2))
+    elif kind == "mask_transposed":
+        orig = oracle.mask_bias
+        monkeypatch.setattr(oracle, "mask_bias",
+                            lambda m, inf=1e9: orig(m.transpose(-1, -2), inf))
+    elif kind == "gate_dropped":
+        orig = oracle.wrap_up
+
+        def no_gate(o, x, p):
+            q = oracle.BlockParams(**{**p.__dict__, "w_g": torch.zeros_like(p.w_g),
+                                      "b_g": torch.full((128,), 40.0, dtype=p.w_g.dtype)})
+            return orig(o, x, q)
+        monkeypatch.setattr(oracle, "wrap_up", no_gate)
+    elif kind == "unbiased_variance":
+        def ln(x, w, b, eps=1e-5):
+            mean = x.mean(-1, keepdim=True)
+            var = x.var(-1, keepdim=True, unbiased=True)
+            y = (x - mean) / torch.sqrt(var + eps)
+            return y * (1 if w is None else w) + (0 if b is None else b)
+        monkeypatch.setattr(oracle, "layer_norm", ln)
+    elif kind == "bias_before_mask":
+        orig = oracle.attention_core
+        monkeypatch.setattr(oracle, "attention_core",
+                            lambda q, k, v, biases: orig(q, k, v, list(reversed(biases))))
+    else:
+        raise ValueError(kind)
+
+
+@pytest.mark.parametrize("kind", ["bias_transposed", "mask_transposed", "gate_dropped",
+                                  "unbiased_variance", "bias_before_mask"])
+def test_planted_mistakes_are_rejected(kind, monkeypatch):
+    _mutated_block(monkeypatch, kind)
+    rejected = False
+    for name in CASES:
+        z, mask, params, expected = load_case(name, torch.float32)
+        if kind in ("mask_transposed", "bias_before_mask") and mask is None:
+            continue
+        for ending, tag in ((False, "start"), (True, "end")):
+            dz = oracle.block(z, mask, params, ending=ending).double()
+            if not torch.allclose(dz, expected[f"dz_{tag}_f32l"], atol=2e-6, rtol=1e-4,
+                                  equal_nan=True):
+                rejected = True
+    assert rejected, f"fixtures did not catch the planted mistake {kind}"
