@@ -30,6 +30,9 @@ HIPCC_FLAGS = (
     "-Wall",
     # Keep the compiler from forming packed FP32 (v_pk_*_f32) instructions.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Keep MFMA accumulators in ordinary VGPRs (gfx950 reads/writes them
+    # directly): no v_accvgpr_read/write shuffles in the attention loop.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 )
 
 

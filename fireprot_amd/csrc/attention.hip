@@ -30,23 +30,41 @@ constexpr int kBq = 128;   // queries per work-group
 constexpr int kBk = 32;    // keys per tile
 constexpr int kPad = 4;    // LDS row padding (floats): conflict-free b128 reads
 constexpr int kThreads = 256;
+#ifndef FPX_ATTN_ROW_GROUP
+#define FPX_ATTN_ROW_GROUP 8
+#endif
+constexpr int kRowGroup = FPX_ATTN_ROW_GROUP;  // outer rows that share a bias slice in L2
 
 struct TileRegs {
-  f32x4 k;
   f32x4 v;
   f32x4 b[4];
   f32x4 m;
 };
 
+// K rows of tile k0 (thread: key row8, channels col4..col4+3).
 template <int LAYOUT>
-__device__ __forceinline__ void load_tile(const AttnArgs& a, int b, int h, int j0, int k0, int tid,
-                                          TileRegs& t) {
+__device__ __forceinline__ f32x4 load_k(const AttnArgs& a, int b, int h, int k0, int tid) {
+  const int row8 = tid >> 3;
+  const int col4 = (tid & 7) * 4;
+  if (LAYOUT == kAttnBlock) {
+    const int64_t bh = (int64_t)b * kHeads + h;
+    return *(const f32x4*)(a.k + (bh * a.np + k0 + row8) * kHeadDim + col4);
+  }
+  const int key = k0 + row8;
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  return key < a.n ? *(const f32x4*)(a.k + (((int64_t)b * a.n + key) * kHeads + h) * kHeadDim + col4)
+                   : zero;
+}
+
+// V^T, triangle-bias and mask-bias slices of tile k0.
+template <int LAYOUT>
+__device__ __forceinline__ void load_vbm(const AttnArgs& a, int b, int h, int j0, int k0, int tid,
+                                         TileRegs& t) {
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   const int row8 = tid >> 3;        // 0..31
   const int col4 = (tid & 7) * 4;   // 0..28
   if (LAYOUT == kAttnBlock) {
     const int64_t bh = (int64_t)b * kHeads + h;
-    t.k = *(const f32x4*)(a.k + (bh * a.np + k0 + row8) * kHeadDim + col4);
     t.v = *(const f32x4*)(a.v + (bh * kHeadDim + row8) * a.np + k0 + col4);
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
@@ -56,10 +74,8 @@ __device__ __forceinline__ void load_tile(const AttnArgs& a, int b, int h, int j
     if (tid < 8) t.m = *(const f32x4*)(a.mbias + (int64_t)b * a.mb_stride + k0 + 4 * tid);
   } else {
     const int key = k0 + row8;
-    const bool kin = key < a.n;
-    const int64_t kv = (((int64_t)b * a.n + key) * kHeads + h) * kHeadDim + col4;
-    t.k = kin ? *(const f32x4*)(a.k + kv) : zero;
-    t.v = kin ? *(const f32x4*)(a.v + kv) : zero;
+    t.v = key < a.n ? *(const f32x4*)(a.v + (((int64_t)b * a.n + key) * kHeads + h) * kHeadDim + col4)
+                    : zero;
     const bool cin = k0 + col4 < a.n;  // n % 4 == 0: a float4 is all-in or all-out
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
@@ -78,6 +94,36 @@ __device__ __forceinline__ void load_tile(const AttnArgs& a, int b, int h, int j
   }
 }
 
+// max / sum of v over the lane pair (l, l ^ 32) with v_permlane32_swap
+// (no LDS round trip): after the swap one copy holds the low half in both
+// halves and the other the high half.
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v),
+                                                  __builtin_bit_cast(unsigned, v), false, false);
+  return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v),
+                                                  __builtin_bit_cast(unsigned, v), false, false);
+  return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+}
+
+// S^T[key][q] = sum_c K[key][c] Q[q][c] for the 32 keys in Ks; the channel of
+// step s in lane half hb is 16*hb + s.
+__device__ __forceinline__ f32x16 qk_tile(const float (*Ks)[kHeadDim + kPad], const float* qf,
+                                          int l32, int half) {
+  f32x16 s = {};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const f32x4 kv = *(const f32x4*)&Ks[l32][16 * half + 4 * t];
+    s = mfma32(kv.x, qf[4 * t + 0], s);
+    s = mfma32(kv.y, qf[4 * t + 1], s);
+    s = mfma32(kv.z, qf[4 * t + 2], s);
+    s = mfma32(kv.w, qf[4 * t + 3], s);
+  }
+  return s;
+}
+
 template <int LAYOUT>
 __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a, int nqt, int nkt,
                                                             uint32_t total) {
@@ -86,10 +132,20 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a, int nqt
   __shared__ __attribute__((aligned(16))) float Bs[kBq][kBk + kPad];
   __shared__ __attribute__((aligned(16))) float Ms[kBk];
 
+  // Logical order, slowest to fastest: head, block of kRowGroup outer rows,
+  // query tile, outer row in the block.  The work-groups that run together
+  // on one XCD then share each triangle-bias slice across kRowGroup outer rows
+  // and each K/V slice across all query tiles, in that XCD's L2.
   const uint32_t logical = xcd_remap(blockIdx.x, total);
-  const int qt = logical % nqt;
-  const int h = (logical / nqt) % kHeads;
-  const int b = logical / (nqt * kHeads);
+  const int groups = (a.batch + kRowGroup - 1) / kRowGroup;
+  const int per_head = groups * kRowGroup * nqt;
+  const int h = (int)(logical / per_head);
+  const int rem = (int)(logical % per_head);
+  const int grp = rem / (kRowGroup * nqt);
+  const int in_grp = rem % (kRowGroup * nqt);
+  const int qt = in_grp / kRowGroup;
+  const int b = grp * kRowGroup + in_grp % kRowGroup;
+  if (b >= a.batch) return;  // padding of the last row group; uniform per work-group
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = tid >> 6;
@@ -120,18 +176,22 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a, int nqt
     }
   }
 
+  // Online-softmax state per query (this lane's column): running max m_run,
+  // its log2-scaled value c_run = fl(m_run * log2 e) (-inf until a finite max
+  // appears) and the running sum l_run.  p = exp2(fma(x, log2 e, -c)) with the
+  // same rounded c used for the rescale alpha = exp2(c_old - c_new), so every
+  // weight carries one common factor that cancels in O / l: the ratios
+  // e^(x - x') stay exact, -1e9-quantised masked logits included.
   f32x16 o = {};
   float m_run = -INFINITY;
+  float c_run = -INFINITY;
   float l_run = 0.f;
-
-  TileRegs regs;
-  load_tile<LAYOUT>(a, b, h, j0, 0, tid, regs);
 
   const int row8 = tid >> 3;
   const int col4 = (tid & 7) * 4;
-  for (int kt = 0; kt < nkt; ++kt) {
-    __syncthreads();  // previous tile's LDS reads are complete
-    *(f32x4*)&Ks[row8][col4] = regs.k;
+  TileRegs regs;
+
+  auto store_vbm = [&]() {
     if (LAYOUT == kAttnBlock) {
       *(f32x4*)&Vs[row8][col4] = regs.v;
     } else {
@@ -143,61 +203,78 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a, int nqt
 #pragma unroll
     for (int m = 0; m < 4; ++m) *(f32x4*)&Bs[row8 + 32 * m][col4] = regs.b[m];
     if (tid < 8) *(f32x4*)&Ms[4 * tid] = regs.m;
-    __syncthreads();
-    if (kt + 1 < nkt) load_tile<LAYOUT>(a, b, h, j0, (kt + 1) * kBk, tid, regs);
+  };
 
-    // S^T[key][q] = sum_c K[key][c] Q[q][c]; channel for step s, half hb is 16*hb + s.
-    f32x16 s = {};
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const f32x4 kv = *(const f32x4*)&Ks[l32][16 * half + 4 * t];
-      s = mfma32(kv.x, qf[4 * t + 0], s);
-      s = mfma32(kv.y, qf[4 * t + 1], s);
-      s = mfma32(kv.z, qf[4 * t + 2], s);
-      s = mfma32(kv.w, qf[4 * t + 3], s);
-    }
-
-    // Register r of this lane is key 8*(r/4) + 4*half + r%4 of the tile.
-    float x[16];
+  // Softmax of the current tile's logits (in s, lane register r = key
+  // 8*(r/4) + 4*half + r%4) and O^T[c][q] += V^T[c][key] P^T[key][q].
+  auto softmax_pv = [&](f32x16 s) {
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const f32x4 mb = *(const f32x4*)&Ms[8 * rr + 4 * half];
       const f32x4 bb = *(const f32x4*)&Bs[32 * w + l32][8 * rr + 4 * half];
-      x[4 * rr + 0] = (s[4 * rr + 0] + mb.x) + bb.x;
-      x[4 * rr + 1] = (s[4 * rr + 1] + mb.y) + bb.y;
-      x[4 * rr + 2] = (s[4 * rr + 2] + mb.z) + bb.z;
-      x[4 * rr + 3] = (s[4 * rr + 3] + mb.w) + bb.w;
+      s[4 * rr + 0] = (s[4 * rr + 0] + mb.x) + bb.x;
+      s[4 * rr + 1] = (s[4 * rr + 1] + mb.y) + bb.y;
+      s[4 * rr + 2] = (s[4 * rr + 2] + mb.z) + bb.z;
+      s[4 * rr + 3] = (s[4 * rr + 3] + mb.w) + bb.w;
     }
-    float mt = x[0];
+    float mt = s[0];
 #pragma unroll
-    for (int r = 1; r < 16; ++r) mt = fmaxf(mt, x[r]);
-    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+    for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
+    mt = xor32_max(mt);
     const float m_new = fmaxf(m_run, mt);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = exp2_fast((m_run - m_use) * kLog2e);
+    const float c_new = m_new == -INFINITY ? -INFINITY : m_new * kLog2e;
+    const float c_use = m_new == -INFINITY ? 0.f : c_new;
+    const float alpha = exp2_fast(c_run - c_use);
     float psum = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      x[r] = exp2_fast((x[r] - m_use) * kLog2e);
-      psum += x[r];
+      s[r] = exp2_fast(__builtin_fmaf(s[r], kLog2e, -c_use));
+      psum += s[r];
     }
     l_run = l_run * alpha + psum;
     m_run = m_new;
+    c_run = c_new;
+    if (__any(alpha != 1.0f)) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) o[r] *= alpha;
-
-    // O^T[c][q] += sum_key V^T[c][key] P^T[key][q]; MFMA r pairs keys of register r.
+      for (int r = 0; r < 16; ++r) o[r] *= alpha;
+    }
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const f32x4 vv = *(const f32x4*)&Vs[l32][8 * rr + 4 * half];
-      o = mfma32(vv.x, x[4 * rr + 0], o);
-      o = mfma32(vv.y, x[4 * rr + 1], o);
-      o = mfma32(vv.z, x[4 * rr + 2], o);
-      o = mfma32(vv.w, x[4 * rr + 3], o);
+      o = mfma32(vv.x, s[4 * rr + 0], o);
+      o = mfma32(vv.y, s[4 * rr + 1], o);
+      o = mfma32(vv.z, s[4 * rr + 2], o);
+      o = mfma32(vv.w, s[4 * rr + 3], o);
     }
-  }
+  };
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
+  // Prologue: K of tile 0 into LDS, S^T of tile 0; stage K(1) and V/bias/mask(0).
+  *(f32x4*)&Ks[row8][col4] = load_k<LAYOUT>(a, b, h, 0, tid);
+  __syncthreads();
+  f32x16 s_cur = qk_tile(Ks, qf, l32, half);
+  f32x4 kreg = {0.f, 0.f, 0.f, 0.f};
+  if (nkt > 1) kreg = load_k<LAYOUT>(a, b, h, kBk, tid);
+  load_vbm<LAYOUT>(a, b, h, j0, 0, tid, regs);
+
+  // Steady state: LDS holds K of tile kt+1 and V/bias/mask of tile kt, so
+  // the 16 MFMAs of S^T(kt+1) are independent of the softmax of tile kt.
+  for (int kt = 0; kt + 1 < nkt; ++kt) {
+    __syncthreads();  // every wave is done with K(kt) and V/bias/mask(kt-1)
+    *(f32x4*)&Ks[row8][col4] = kreg;
+    store_vbm();
+    __syncthreads();
+    if (kt + 2 < nkt) kreg = load_k<LAYOUT>(a, b, h, (kt + 2) * kBk, tid);
+    load_vbm<LAYOUT>(a, b, h, j0, (kt + 1) * kBk, tid, regs);
+    const f32x16 s_next = qk_tile(Ks, qf, l32, half);
+    softmax_pv(s_cur);
+    s_cur = s_next;
+  }
+  __syncthreads();
+  store_vbm();
+  __syncthreads();
+  softmax_pv(s_cur);
+
+  const float l_tot = xor32_sum(l_run);
   if (jq < a.n) {
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
@@ -220,7 +297,8 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a, int nqt
 hipError_t launch_attention(int layout, const AttnArgs& a, hipStream_t stream) {
   const int nqt = (int)((layout == kAttnBlock ? a.np : round_up(a.n, kBq)) / kBq);
   const int nkt = (int)((layout == kAttnBlock ? a.np : round_up(a.n, kBk)) / kBk);
-  const uint64_t total = (uint64_t)a.batch * kHeads * nqt;
+  const uint64_t groups = ((uint64_t)a.batch + kRowGroup - 1) / kRowGroup;
+  const uint64_t total = groups * kRowGroup * kHeads * nqt;
   if (total == 0) return hipSuccess;
   if (total > 0x7fffffffull) return hipErrorInvalidValue;
   if (layout == kAttnBlock) {
