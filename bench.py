@@ -32,6 +32,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "triangle-attn block ms + TFLOP/s (% MFMA peak) at N=1536 FP32, 1 GPU"
 FP32_MFMA_PEAK_TFLOPS = 157.3
+BF16_MFMA_PEAK_TFLOPS = 2500.0
 HBM_PEAK_GBPS = 8000.0
 TRAFFIC_FILE = ROOT / "profiles" / "attention_traffic.json"
 
@@ -41,11 +42,13 @@ def log(msg: str) -> None:
 
 
 def cpu_baseline(cfg, z, mask, weights, budget_s: float = 40.0) -> dict:
-    """Time the CPU oracle (native op order, FP32) on the whole workload.
+    """Time the CPU oracle (native op order) on the host cores.
 
-    Both directions run in full when the starting node finishes within
-    ``budget_s``; otherwise the ending node is taken as equal to the starting
-    node and the sample says so.
+    FP32 configurations run both directions in full (the starting node alone
+    when it exceeds ``budget_s``, the ending node then taken as equal).  The
+    BF16 configuration runs the native path on bfloat16 tensors for 8 and 24
+    evenly spaced outer rows per direction and extrapolates linearly in rows
+    (rows are independent), since the full N=2048 BF16 CPU run takes minutes.
     """
     import torch
 
@@ -56,29 +59,47 @@ def cpu_baseline(cfg, z, mask, weights, budget_s: float = 40.0) -> dict:
     params = oracle.BlockParams(**weights)
     times = {}
     both = True
+    bf16 = cfg.dtype == "bf16"
+    run = oracle.block_bf16 if bf16 else oracle.block
     with torch.inference_mode():
         for ending in (False, True):
+            key = "end" if ending else "start"
+            if bf16:
+                spent = []
+                for rows in (8, 24):
+                    sel = torch.linspace(0, cfg.n - 1, rows).round().long()
+                    t0 = time.perf_counter()
+                    run(z, mask, params, ending=ending, outer_rows=sel)
+                    spent.append(time.perf_counter() - t0)
+                per_row = max((spent[1] - spent[0]) / 16, 0.0)
+                times[key] = max(spent[0] - 8 * per_row, 0.0) + per_row * cfg.n
+                log(f"cpu oracle ending={ending}: 8 rows {spent[0]:.2f} s, 24 rows {spent[1]:.2f} s")
+                continue
             if ending and times["start"] > budget_s:
                 times["end"] = times["start"]
                 both = False
                 break
             t0 = time.perf_counter()
-            oracle.block(z, mask, params, ending=ending)
-            times["end" if ending else "start"] = time.perf_counter() - t0
-            log(f"cpu oracle ending={ending}: {time.perf_counter() - t0:.2f} s")
+            run(z, mask, params, ending=ending)
+            times[key] = time.perf_counter() - t0
+            log(f"cpu oracle ending={ending}: {times[key]:.2f} s")
     from oracle.triangle_attention import block_flops
 
     total = times["start"] + times["end"]
     flop = 2 * block_flops(cfg.n)["block"]
-    measured = ("both directions in full" if both
-                else "the starting node in full (ending node taken as equal)")
+    if bf16:
+        measured = ("native path on bfloat16 tensors, 8 and 24 evenly spaced outer rows per "
+                    "direction, fitted linearly in rows and extrapolated to all rows")
+    else:
+        measured = ("both directions in full" if both
+                    else "the starting node in full (ending node taken as equal)")
     return {
         "value": round(flop / total / 1e12, 5),
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"CPU oracle (native PyTorch op order, FP32, {threads} threads, outer rows in "
-                   f"chunks of 64) on the same {cfg.name} inputs, {measured}: "
+        "sample": (f"CPU oracle (native PyTorch op order, {threads} threads, outer rows in "
+                   f"chunks) on the same {cfg.name} inputs, {measured}: "
                    f"start {times['start']:.1f} s + end {times['end']:.1f} s per step"),
         "step_s": round(total, 2),
         "cpu": platform.processor() or platform.machine(),
@@ -90,7 +111,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c4", choices=["c1", "c2", "c3", "c4"])
+    ap.add_argument("--config", default="c4", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 1 GiB device-to-device copy (the known-size "
@@ -116,12 +137,15 @@ def main() -> int:
     log(f"inputs {cfg.name}")
     z_cpu, mask_cpu, w = workloads.make_inputs(cfg)
     dev = torch.device("cuda:0")
-    z = z_cpu.to(dev)
+    dtype = torch.bfloat16 if cfg.dtype == "bf16" else torch.float32
+    dtype_code = block.DTYPES[dtype]
+    peak = BF16_MFMA_PEAK_TFLOPS if cfg.dtype == "bf16" else FP32_MFMA_PEAK_TFLOPS
+    z = z_cpu.to(dtype).to(dev)
     mask = None if mask_cpu is None else mask_cpu.to(dev)
-    weights = block.BlockWeights.from_tensors(**w).to(dev)
+    weights = block.BlockWeights.from_tensors(**w, dtype=dtype).to(dev)
     out_s = torch.empty_like(z)
     out_e = torch.empty_like(z)
-    ws = torch.empty(block.workspace_bytes(n), dtype=torch.uint8, device=dev)
+    ws = torch.empty(block.workspace_bytes(n, dtype), dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream(dev)
 
     def step():
@@ -153,16 +177,17 @@ def main() -> int:
 
         def prepare():
             _native.check(lib.fpx_tri_attn_prepare(
-                0, z.data_ptr(), z.stride(0), z.stride(1), mptr, mstr[0], mstr[1],
+                dtype_code, z.data_ptr(), z.stride(0), z.stride(1), mptr, mstr[0], mstr[1],
                 weights.ln_w.data_ptr(), weights.ln_b.data_ptr(), weights.eps,
                 weights.w_qkvg.data_ptr(), None, weights.w_bias.data_ptr(), weights.inf, n, 0,
                 ws.data_ptr(), ws_bytes, sptr), "prepare")
 
         def attend():
-            _native.check(lib.fpx_tri_attn_attend(0, n, ws.data_ptr(), ws_bytes, sptr), "attend")
+            _native.check(lib.fpx_tri_attn_attend(dtype_code, n, ws.data_ptr(), ws_bytes, sptr),
+                          "attend")
 
         def finish():
-            _native.check(lib.fpx_tri_attn_finish(0, weights.w_o.data_ptr(), None, n, 0,
+            _native.check(lib.fpx_tri_attn_finish(dtype_code, weights.w_o.data_ptr(), None, n, 0,
                                                   out_s.data_ptr(), out_s.stride(0),
                                                   out_s.stride(1), ws.data_ptr(), ws_bytes,
                                                   sptr), "finish")
@@ -212,7 +237,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": cfg.dtype,
         "data": "synthetic (seeded torch.Generator inputs and N(0,0.02) random-init weights)",
         "config": {
             "workload": f"{cfg.name}: starting + ending triangle-attention block",
@@ -221,17 +246,18 @@ def main() -> int:
             "bias_scale": cfg.bias_scale,
             "block_ms": round(ms_per_step / 2, 4),
             "block_tflops": round(value, 3),
-            "block_mfma_peak_frac": round(value / FP32_MFMA_PEAK_TFLOPS, 4),
+            "block_mfma_peak_frac": round(value / peak, 4),
             "step_flop": step_flop,
             "stage_ms_start_node": {k: round(v, 4) for k, v in stages.items()},
         },
         "roofline": {
-            "kernel": "attention_kernel<kAttnBlock> (fpx_tri_attn_attend)",
+            "kernel": ("attention_bf16_kernel (fpx_tri_attn_attend, BF16)" if cfg.dtype == "bf16"
+                       else "attention_kernel<kAttnBlock> (fpx_tri_attn_attend)"),
             "bound": "mfma",
             "achieved": round(attend_tflops, 3),
-            "peak": FP32_MFMA_PEAK_TFLOPS,
+            "peak": peak,
             "unit": "TFLOP/s",
-            "frac": round(attend_tflops / FP32_MFMA_PEAK_TFLOPS, 4),
+            "frac": round(attend_tflops / peak, 4),
             "traffic": traffic,
             "flop_per_launch": flops["core"],
             "avg_launch_ms": round(stages["attend"], 4),

@@ -9,8 +9,10 @@ AtlasFold's ``triangle_attention(module, z, mask, ending)``
 (python/fireprot/adapters/atlasfold/runtime.py:32-71); the residual
 ``z += dz`` stays with the caller (patches/protenix/0006-*.patch:25).
 
-This module has no CPU path: inputs must be float32 tensors on a HIP device
-and the native library must be loaded, otherwise it raises.  Capability-gated
+Two storage types: float32 (FP32 throughout) and bfloat16 (BF16 storage of z,
+weights, intermediates and dz with FP32 accumulation and softmax).  This
+module has no CPU path: inputs must be tensors on a HIP device and the native
+library must be loaded, otherwise it raises.  Capability-gated
 fallback to the *caller's* native function lives in
 ``fireprot_amd.triangle_attention``.
 """
@@ -50,15 +52,20 @@ class BlockWeights:
 
     @classmethod
     def from_tensors(cls, *, ln_w, ln_b, w_q, w_k, w_v, w_g, b_g, w_bias, w_o, b_o,
-                     inf: float = 1e9, eps: float = 1e-5) -> "BlockWeights":
+                     inf: float = 1e9, eps: float = 1e-5,
+                     dtype: torch.dtype = torch.float32) -> "BlockWeights":
         def prep(t):
-            return None if t is None else t.detach().to(torch.float32).contiguous()
-        w_qkvg = torch.cat([w.detach().to(torch.float32) for w in (w_q, w_k, w_v, w_g)], 0)
+            return None if t is None else t.detach().to(dtype).contiguous()
+        w_qkvg = torch.cat([w.detach().to(dtype) for w in (w_q, w_k, w_v, w_g)], 0)
         return cls(prep(ln_w), prep(ln_b), w_qkvg.contiguous(), prep(b_g), prep(w_bias),
                    prep(w_o), prep(b_o), float(inf), float(eps))
 
+    @property
+    def dtype(self) -> torch.dtype:
+        return self.w_qkvg.dtype
+
     @classmethod
-    def from_protenix(cls, module: Any) -> "BlockWeights":
+    def from_protenix(cls, module: Any, dtype: torch.dtype | None = None) -> "BlockWeights":
         """Protenix/OpenFold ``TriangleAttention``: ``layer_norm``, ``linear``,
         ``mha.linear_{q,k,v,g,o}``, ``inf`` (patch 0005:32-45; 0002:31-58)."""
         mha = module.mha
@@ -70,10 +77,11 @@ class BlockWeights:
             w_q=mha.linear_q.weight, w_k=mha.linear_k.weight, w_v=mha.linear_v.weight,
             w_g=mha.linear_g.weight, b_g=mha.linear_g.bias, w_bias=module.linear.weight,
             w_o=mha.linear_o.weight, b_o=mha.linear_o.bias,
-            inf=float(getattr(module, "inf", 1e9)), eps=float(module.layer_norm.eps))
+            inf=float(getattr(module, "inf", 1e9)), eps=float(module.layer_norm.eps),
+            dtype=dtype or mha.linear_q.weight.dtype)
 
     @classmethod
-    def from_atlasfold(cls, module: Any) -> "BlockWeights":
+    def from_atlasfold(cls, module: Any, dtype: torch.dtype | None = None) -> "BlockWeights":
         """AtlasFold triangle node: ``layernorm``, fused ``linear_qkv``,
         ``linear_bias``, ``linear_g``, ``linear_out`` (atlasfold/runtime.py:38-70)."""
         w_q, w_k, w_v = module.linear_qkv.weight.chunk(3, dim=0)
@@ -82,7 +90,8 @@ class BlockWeights:
             w_q=w_q, w_k=w_k, w_v=w_v, w_g=module.linear_g.weight,
             b_g=getattr(module.linear_g, "bias", None), w_bias=module.linear_bias.weight,
             w_o=module.linear_out.weight, b_o=getattr(module.linear_out, "bias", None),
-            inf=float(module.inf), eps=float(getattr(module.layernorm, "eps", 1e-5)))
+            inf=float(module.inf), eps=float(getattr(module.layernorm, "eps", 1e-5)),
+            dtype=dtype or module.linear_qkv.weight.dtype)
 
     def tensors(self) -> tuple[torch.Tensor | None, ...]:
         return (self.ln_w, self.ln_b, self.w_qkvg, self.b_g, self.w_bias, self.w_o, self.b_o)
@@ -94,10 +103,13 @@ class BlockWeights:
                                             ("ln_w", "ln_b", "w_qkvg", "b_g", "w_bias", "w_o", "b_o")})
 
 
-def workspace_bytes(n: int) -> int:
-    """Device workspace for one block call at pair size n (FP32)."""
+DTYPES = {torch.float32: _native.FPX_F32, torch.bfloat16: _native.FPX_BF16}
+
+
+def workspace_bytes(n: int, dtype: torch.dtype = torch.float32) -> int:
+    """Device workspace for one block call at pair size n and storage dtype."""
     return int(_native.library().fpx_tri_attn_workspace_bytes(n, CHANNELS, HEADS, HEAD_DIM,
-                                                              _native.FPX_F32))
+                                                              DTYPES[dtype]))
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -106,11 +118,12 @@ def _ptr(t: torch.Tensor | None) -> int | None:
 
 def check_block_inputs(z: torch.Tensor, mask: torch.Tensor | None, weights: BlockWeights) -> None:
     """Raise ``ValueError`` unless the tensors fit the native block's contract."""
-    if not z.is_cuda or z.dtype != torch.float32:
-        raise ValueError("z must be a float32 tensor on a HIP device")
+    if not z.is_cuda or z.dtype not in DTYPES:
+        raise ValueError("z must be a float32 or bfloat16 tensor on a HIP device")
     if z.dim() != 3 or z.shape[0] != z.shape[1] or z.shape[2] != CHANNELS:
         raise ValueError(f"z must be [N, N, {CHANNELS}], got {tuple(z.shape)}")
-    if z.stride(2) != 1 or z.stride(0) % 4 or z.stride(1) % 4:
+    align = 16 // z.element_size()
+    if z.stride(2) != 1 or z.stride(0) % align or z.stride(1) % align:
         raise ValueError("z needs unit channel stride and 16-byte aligned rows")
     if mask is not None and (mask.device != z.device or tuple(mask.shape) != tuple(z.shape[:2])):
         raise ValueError("mask must be [N, N] on z's device")
@@ -121,9 +134,9 @@ def check_block_inputs(z: torch.Tensor, mask: torch.Tensor | None, weights: Bloc
         if tuple(t.shape) != shape:
             raise ValueError(f"{name} must be {shape}, got {tuple(t.shape)}")
     for t in weights.tensors():
-        if t is not None and (t.device != z.device or t.dtype != torch.float32
+        if t is not None and (t.device != z.device or t.dtype != z.dtype
                               or not t.is_contiguous()):
-            raise ValueError("weights must be contiguous float32 tensors on z's device")
+            raise ValueError("weights must be contiguous tensors of z's dtype on z's device")
 
 
 def triangle_attention_block(z: torch.Tensor, mask: torch.Tensor | None, weights: BlockWeights,
@@ -141,19 +154,19 @@ def triangle_attention_block(z: torch.Tensor, mask: torch.Tensor | None, weights
     if mask is not None and mask.dtype != torch.float32:
         mask = mask.to(torch.float32)
     if out is None:
-        out = torch.empty((n, n, CHANNELS), device=z.device, dtype=torch.float32)
-    elif (tuple(out.shape) != (n, n, CHANNELS) or out.dtype != torch.float32
+        out = torch.empty((n, n, CHANNELS), device=z.device, dtype=z.dtype)
+    elif (tuple(out.shape) != (n, n, CHANNELS) or out.dtype != z.dtype
           or out.device != z.device or out.stride(2) != 1):
-        raise ValueError("out must be a float32 [N, N, 128] tensor on z's device")
+        raise ValueError("out must be a [N, N, 128] tensor of z's dtype on z's device")
     with torch.cuda.device(z.device):
-        need = workspace_bytes(n)
+        need = workspace_bytes(n, z.dtype)
         if workspace is None:
             workspace = torch.empty(need, dtype=torch.uint8, device=z.device)
         elif workspace.numel() * workspace.element_size() < need:
             raise ValueError(f"workspace needs {need} bytes")
         stream = torch.cuda.current_stream(z.device).cuda_stream
         code = lib.fpx_tri_attn_block(
-            _native.FPX_F32, z.data_ptr(), z.stride(0), z.stride(1),
+            DTYPES[z.dtype], z.data_ptr(), z.stride(0), z.stride(1),
             _ptr(mask), mask.stride(0) if mask is not None else 0,
             mask.stride(1) if mask is not None else 0,
             _ptr(weights.ln_w), _ptr(weights.ln_b), weights.eps,

@@ -25,19 +25,23 @@ bool aligned_or_null(const void* p, uintptr_t bytes) {
 constexpr int kMaxN = 4096;
 constexpr int kQueryTile = 128;  // attention query tile: every block extent pads to it
 
-// Workspace segments of the F32 block, all 256-byte aligned:
+size_t elem_bytes(int dtype) { return dtype == FPX_BF16 ? 2 : 4; }
+
+// Workspace segments of the block, all 256-byte aligned, element size e
+// (4 for FPX_F32, 2 for FPX_BF16; the mask bias is always float):
 //   qh, kh [n][4][np][32]; vt [n][4][32][np]; gs, og [n][n][128];
-//   tri_bias [4][np][np]; mbias [n][np]
+//   tri_bias [4][np][np]; mbias [n][np] float
 struct BlockWorkspace {
   size_t qh, kh, vt, gs, og, bias, mbias, total;
 };
 
-BlockWorkspace block_workspace(int n) {
+BlockWorkspace block_workspace(int n, int dtype) {
   const size_t np = (size_t)round_up(n, kQueryTile);
+  const size_t e = elem_bytes(dtype);
   auto seg = [](size_t bytes) { return (size_t)round_up((int64_t)bytes, 256); };
-  const size_t qkv = seg((size_t)n * fpx::kHeads * np * fpx::kHeadDim * sizeof(float));
-  const size_t g = seg((size_t)n * n * fpx::kHidden * sizeof(float));
-  const size_t bias = seg((size_t)fpx::kHeads * np * np * sizeof(float));
+  const size_t qkv = seg((size_t)n * fpx::kHeads * np * fpx::kHeadDim * e);
+  const size_t g = seg((size_t)n * n * fpx::kHidden * e);
+  const size_t bias = seg((size_t)fpx::kHeads * np * np * e);
   const size_t mb = seg((size_t)n * np * sizeof(float));
   BlockWorkspace w{};
   w.qh = 0;
@@ -52,11 +56,43 @@ BlockWorkspace block_workspace(int n) {
 }
 
 bool block_dims_ok(int n, int c, int heads, int head_dim, int dtype) {
-  return dtype == FPX_F32 && c == fpx::kChannels && heads == fpx::kHeads &&
-         head_dim == fpx::kHeadDim && n >= 1 && n <= kMaxN;
+  return (dtype == FPX_F32 || dtype == FPX_BF16) && c == fpx::kChannels &&
+         heads == fpx::kHeads && head_dim == fpx::kHeadDim && n >= 1 && n <= kMaxN;
 }
 
 int status(hipError_t e) { return e == hipSuccess ? FPX_OK : (int)e; }
+
+struct BlockPointers {
+  char *qh, *kh, *vt, *gs, *og, *tri;
+  float* mbias;
+  int np;
+};
+
+BlockPointers block_pointers(void* workspace, int n, int dtype) {
+  const BlockWorkspace ws = block_workspace(n, dtype);
+  char* base = static_cast<char*>(workspace);
+  BlockPointers p{};
+  p.qh = base + ws.qh;
+  p.kh = base + ws.kh;
+  p.vt = base + ws.vt;
+  p.gs = base + ws.gs;
+  p.og = base + ws.og;
+  p.tri = base + ws.bias;
+  p.mbias = reinterpret_cast<float*>(base + ws.mbias);
+  p.np = (int)round_up(n, kQueryTile);
+  return p;
+}
+
+int check_workspace(int n, int dtype, const void* workspace, size_t workspace_bytes) {
+  if (!aligned(workspace, 256)) return FPX_ERR_POINTER;
+  if (workspace_bytes < block_workspace(n, dtype).total) return FPX_ERR_WORKSPACE;
+  return FPX_OK;
+}
+
+template <typename T>
+T* as(char* p) {
+  return reinterpret_cast<T*>(p);
+}
 
 }  // namespace
 
@@ -66,38 +102,8 @@ int fpx_abi_version(void) { return FPX_ABI_VERSION; }
 
 size_t fpx_tri_attn_workspace_bytes(int n, int c, int heads, int head_dim, int dtype) {
   if (!block_dims_ok(n, c, heads, head_dim, dtype)) return 0;
-  return block_workspace(n).total;
+  return block_workspace(n, dtype).total;
 }
-
-namespace {
-
-struct BlockPointers {
-  float *qh, *kh, *vt, *gs, *og, *tri, *mbias;
-  int np;
-};
-
-BlockPointers block_pointers(void* workspace, int n) {
-  const BlockWorkspace ws = block_workspace(n);
-  char* base = static_cast<char*>(workspace);
-  BlockPointers p{};
-  p.qh = reinterpret_cast<float*>(base + ws.qh);
-  p.kh = reinterpret_cast<float*>(base + ws.kh);
-  p.vt = reinterpret_cast<float*>(base + ws.vt);
-  p.gs = reinterpret_cast<float*>(base + ws.gs);
-  p.og = reinterpret_cast<float*>(base + ws.og);
-  p.tri = reinterpret_cast<float*>(base + ws.bias);
-  p.mbias = reinterpret_cast<float*>(base + ws.mbias);
-  p.np = (int)round_up(n, kQueryTile);
-  return p;
-}
-
-int check_workspace(int n, const void* workspace, size_t workspace_bytes) {
-  if (!aligned(workspace, 256)) return FPX_ERR_POINTER;
-  if (workspace_bytes < block_workspace(n).total) return FPX_ERR_WORKSPACE;
-  return FPX_OK;
-}
-
-}  // namespace
 
 int fpx_tri_attn_prepare(int dtype, const void* z, int64_t z_stride0, int64_t z_stride1,
                          const float* mask, int64_t m_stride0, int64_t m_stride1,
@@ -106,28 +112,57 @@ int fpx_tri_attn_prepare(int dtype, const void* z, int64_t z_stride0, int64_t z_
                          void* workspace, size_t workspace_bytes, void* stream) {
   if (!block_dims_ok(n, fpx::kChannels, fpx::kHeads, fpx::kHeadDim, dtype)) return FPX_ERR_DIMS;
   if (ending != 0 && ending != 1) return FPX_ERR_DIMS;
-  if (z_stride0 % 4 || z_stride1 % 4 || z_stride0 < 0 || z_stride1 < 0) return FPX_ERR_DIMS;
+  // rows must be 16-byte aligned: 4 floats or 8 bf16
+  const int64_t row_align = dtype == FPX_BF16 ? 8 : 4;
+  if (z_stride0 % row_align || z_stride1 % row_align || z_stride0 < 0 || z_stride1 < 0)
+    return FPX_ERR_DIMS;
   if (m_stride0 < 0 || m_stride1 < 0) return FPX_ERR_DIMS;
   if (!(eps >= 0.0f) || !std::isfinite(mask_inf)) return FPX_ERR_DIMS;
   if (!aligned(z, 16) || !aligned(w_qkvg, 16) || !aligned(w_bias, 16)) return FPX_ERR_POINTER;
   if (!aligned_or_null(mask, 4) || !aligned_or_null(ln_w, 8) || !aligned_or_null(ln_b, 8) ||
       !aligned_or_null(b_g, 4))
     return FPX_ERR_POINTER;
-  if (int rc = check_workspace(n, workspace, workspace_bytes)) return rc;
+  if (int rc = check_workspace(n, dtype, workspace, workspace_bytes)) return rc;
 
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const BlockPointers w = block_pointers(workspace, n);
+  const BlockPointers w = block_pointers(workspace, n, dtype);
   // x-frame strides: the ending node reads x[i][j] = z[j][i] (and the mask alike).
   const int64_t xs_i = ending ? z_stride1 : z_stride0;
   const int64_t xs_j = ending ? z_stride0 : z_stride1;
   const int64_t ms_i = ending ? m_stride1 : m_stride0;
   const int64_t ms_j = ending ? m_stride0 : m_stride1;
 
-  hipError_t e = fpx::launch_mask_bias(mask, ms_i, ms_j, n, w.np, mask_inf, w.mbias, w.tri, s);
+  hipError_t e = fpx::launch_mask_bias(mask, ms_i, ms_j, n, w.np, mask_inf, w.mbias, w.tri,
+                                       dtype == FPX_BF16, s);
   if (e != hipSuccess) return status(e);
 
-  const float* wq = static_cast<const float*>(w_qkvg);
+  const float q_scale = 1.0f / std::sqrt((float)fpx::kHeadDim);
   const int64_t wstride = (int64_t)fpx::kHidden * fpx::kChannels;
+  if (dtype == FPX_BF16) {
+    const __bf16* wq = static_cast<const __bf16*>(w_qkvg);
+    fpx::Bf16ProjArgs p{};
+    p.x = static_cast<const __bf16*>(z);
+    p.xs_i = xs_i;
+    p.xs_j = xs_j;
+    p.rows_i = n;
+    p.rows_j = n;
+    p.span_j = w.np;
+    p.ln_w = static_cast<const __bf16*>(ln_w);
+    p.ln_b = static_cast<const __bf16*>(ln_b);
+    p.eps = eps;
+    for (int g = 0; g < 4; ++g) p.w[g] = wq + g * wstride;
+    p.bias_vec = static_cast<const __bf16*>(b_g);
+    p.w_bias = static_cast<const __bf16*>(w_bias);
+    p.q_scale = q_scale;
+    p.qh = as<__bf16>(w.qh);
+    p.kh = as<__bf16>(w.kh);
+    p.vt = as<__bf16>(w.vt);
+    p.gs = as<__bf16>(w.gs);
+    p.tri_bias = as<__bf16>(w.tri);
+    p.np = w.np;
+    return status(fpx::launch_projection_bf16(fpx::kProjBlock, p, s));
+  }
+  const float* wq = static_cast<const float*>(w_qkvg);
   fpx::ProjArgs p{};
   p.x = static_cast<const float*>(z);
   p.xs_i = xs_i;
@@ -141,35 +176,50 @@ int fpx_tri_attn_prepare(int dtype, const void* z, int64_t z_stride0, int64_t z_
   for (int g = 0; g < 4; ++g) p.w[g] = wq + g * wstride;
   p.b_g = static_cast<const float*>(b_g);
   p.w_bias = static_cast<const float*>(w_bias);
-  p.q_scale = 1.0f / std::sqrt((float)fpx::kHeadDim);
-  p.qh = w.qh;
-  p.kh = w.kh;
-  p.vt = w.vt;
-  p.gs = w.gs;
-  p.tri_bias = w.tri;
+  p.q_scale = q_scale;
+  p.qh = as<float>(w.qh);
+  p.kh = as<float>(w.kh);
+  p.vt = as<float>(w.vt);
+  p.gs = as<float>(w.gs);
+  p.tri_bias = as<float>(w.tri);
   p.np = w.np;
   return status(fpx::launch_projection(fpx::kProjBlock, p, s));
 }
 
 int fpx_tri_attn_attend(int dtype, int n, void* workspace, size_t workspace_bytes, void* stream) {
   if (!block_dims_ok(n, fpx::kChannels, fpx::kHeads, fpx::kHeadDim, dtype)) return FPX_ERR_DIMS;
-  if (int rc = check_workspace(n, workspace, workspace_bytes)) return rc;
-  const BlockPointers w = block_pointers(workspace, n);
+  if (int rc = check_workspace(n, dtype, workspace, workspace_bytes)) return rc;
+  const BlockPointers w = block_pointers(workspace, n, dtype);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == FPX_BF16) {
+    fpx::Bf16AttnArgs a{};
+    a.q = as<__bf16>(w.qh);
+    a.k = as<__bf16>(w.kh);
+    a.v = as<__bf16>(w.vt);
+    a.mbias = w.mbias;
+    a.bias = as<__bf16>(w.tri);
+    a.gate = as<__bf16>(w.gs);
+    a.out = as<__bf16>(w.og);
+    a.batch = n;
+    a.n = n;
+    a.np = w.np;
+    return status(fpx::launch_attention_bf16(a, s));
+  }
   fpx::AttnArgs a{};
-  a.q = w.qh;
-  a.k = w.kh;
-  a.v = w.vt;
+  a.q = as<float>(w.qh);
+  a.k = as<float>(w.kh);
+  a.v = as<float>(w.vt);
   a.mbias = w.mbias;
   a.mb_stride = w.np;
-  a.bias = w.tri;
+  a.bias = as<float>(w.tri);
   a.bias_stride = w.np;
   a.bias_rows = w.np;
-  a.gate = w.gs;
-  a.out = w.og;
+  a.gate = as<float>(w.gs);
+  a.out = as<float>(w.og);
   a.batch = n;
   a.n = n;
   a.np = w.np;
-  return status(fpx::launch_attention(fpx::kAttnBlock, a, static_cast<hipStream_t>(stream)));
+  return status(fpx::launch_attention(fpx::kAttnBlock, a, s));
 }
 
 int fpx_tri_attn_finish(int dtype, const void* w_o, const void* b_o, int n, int ending, void* dz,
@@ -178,11 +228,30 @@ int fpx_tri_attn_finish(int dtype, const void* w_o, const void* b_o, int n, int 
   if (!block_dims_ok(n, fpx::kChannels, fpx::kHeads, fpx::kHeadDim, dtype)) return FPX_ERR_DIMS;
   if (ending != 0 && ending != 1) return FPX_ERR_DIMS;
   if (dz_stride0 < 0 || dz_stride1 < 0) return FPX_ERR_DIMS;
-  if (!aligned(w_o, 16) || !aligned(dz, 16) || !aligned_or_null(b_o, 4)) return FPX_ERR_POINTER;
-  if (int rc = check_workspace(n, workspace, workspace_bytes)) return rc;
-  const BlockPointers w = block_pointers(workspace, n);
+  if (!aligned(w_o, 16) || !aligned(dz, 16) || !aligned_or_null(b_o, 2)) return FPX_ERR_POINTER;
+  if (dtype == FPX_F32 && !aligned_or_null(b_o, 4)) return FPX_ERR_POINTER;
+  if (int rc = check_workspace(n, dtype, workspace, workspace_bytes)) return rc;
+  const BlockPointers w = block_pointers(workspace, n, dtype);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t os_i = ending ? dz_stride1 : dz_stride0;
+  const int64_t os_j = ending ? dz_stride0 : dz_stride1;
+  if (dtype == FPX_BF16) {
+    fpx::Bf16ProjArgs o{};
+    o.x = as<__bf16>(w.og);
+    o.xs_i = (int64_t)n * fpx::kHidden;
+    o.xs_j = fpx::kHidden;
+    o.rows_i = n;
+    o.rows_j = n;
+    o.span_j = n;
+    o.w[0] = static_cast<const __bf16*>(w_o);
+    o.bias_vec = static_cast<const __bf16*>(b_o);
+    o.out = static_cast<__bf16*>(dz);
+    o.os_i = os_i;
+    o.os_j = os_j;
+    return status(fpx::launch_projection_bf16(fpx::kProjOut, o, s));
+  }
   fpx::ProjArgs o{};
-  o.x = w.og;
+  o.x = as<float>(w.og);
   o.xs_i = (int64_t)n * fpx::kHidden;
   o.xs_j = fpx::kHidden;
   o.rows_i = n;
@@ -191,9 +260,9 @@ int fpx_tri_attn_finish(int dtype, const void* w_o, const void* b_o, int n, int 
   o.w[0] = static_cast<const float*>(w_o);
   o.b_g = static_cast<const float*>(b_o);
   o.out = static_cast<float*>(dz);
-  o.os_i = ending ? dz_stride1 : dz_stride0;
-  o.os_j = ending ? dz_stride0 : dz_stride1;
-  return status(fpx::launch_projection(fpx::kProjOut, o, static_cast<hipStream_t>(stream)));
+  o.os_i = os_i;
+  o.os_j = os_j;
+  return status(fpx::launch_projection(fpx::kProjOut, o, s));
 }
 
 int fpx_tri_attn_block(int dtype, const void* z, int64_t z_stride0, int64_t z_stride1,
@@ -206,7 +275,8 @@ int fpx_tri_attn_block(int dtype, const void* z, int64_t z_stride0, int64_t z_st
   if (!block_dims_ok(n, c, heads, head_dim, dtype)) return FPX_ERR_DIMS;
   if (ending != 0 && ending != 1) return FPX_ERR_DIMS;
   if (dz_stride0 < 0 || dz_stride1 < 0) return FPX_ERR_DIMS;
-  if (!aligned(w_o, 16) || !aligned(dz, 16) || !aligned_or_null(b_o, 4)) return FPX_ERR_POINTER;
+  if (!aligned(w_o, 16) || !aligned(dz, 16) || !aligned_or_null(b_o, 2)) return FPX_ERR_POINTER;
+  if (dtype == FPX_F32 && !aligned_or_null(b_o, 4)) return FPX_ERR_POINTER;
   int rc = fpx_tri_attn_prepare(dtype, z, z_stride0, z_stride1, mask, m_stride0, m_stride1, ln_w,
                                 ln_b, eps, w_qkvg, b_g, w_bias, mask_inf, n, ending, workspace,
                                 workspace_bytes, stream);

@@ -12,9 +12,10 @@ namespace {
 // mbias[i][k] (i < n, k < np) followed by zero rows [n, np) of each head of
 // the triangle bias.  inf * (mask - 1) is evaluated as two rounded fp32 ops,
 // as the native expression is (patches/protenix/0005-*.patch:36-39).
+template <typename BiasT>
 __global__ void mask_bias_kernel(const float* __restrict__ mask, int64_t ms_i, int64_t ms_j, int n,
                                  int np, float inf, float* __restrict__ mbias,
-                                 float* __restrict__ tri_bias) {
+                                 BiasT* __restrict__ tri_bias) {
   const int64_t head_rows = (int64_t)(np - n) * np;
   const int64_t total = (int64_t)n * np + kHeads * head_rows;
   for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
@@ -29,7 +30,7 @@ __global__ void mask_bias_kernel(const float* __restrict__ mask, int64_t ms_i, i
       const int64_t r = idx - (int64_t)n * np;
       const int64_t h = r / head_rows;
       const int64_t rest = r % head_rows;
-      tri_bias[(h * np + n) * np + rest] = 0.0f;
+      tri_bias[(h * np + n) * np + rest] = (BiasT)0.0f;
     }
   }
 }
@@ -74,14 +75,20 @@ __global__ __launch_bounds__(256) void sigmoid_mul_kernel(const f32x4* __restric
 }  // namespace
 
 hipError_t launch_mask_bias(const float* mask, int64_t ms_i, int64_t ms_j, int n, int np,
-                            float inf, float* mbias, float* tri_bias, hipStream_t stream) {
+                            float inf, float* mbias, void* tri_bias, bool bias_bf16,
+                            hipStream_t stream) {
   const int64_t total = (int64_t)n * np + (int64_t)kHeads * (np - n) * np;
   if (total == 0) return hipSuccess;
   int64_t blocks = (total + 255) / 256;
   const int64_t cap = (int64_t)device_cu_count() * 16;
   if (blocks > cap) blocks = cap;
-  hipLaunchKernelGGL(mask_bias_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream, mask, ms_i,
-                     ms_j, n, np, inf, mbias, tri_bias);
+  if (bias_bf16) {
+    hipLaunchKernelGGL(mask_bias_kernel<__bf16>, dim3((uint32_t)blocks), dim3(256), 0, stream, mask,
+                       ms_i, ms_j, n, np, inf, mbias, static_cast<__bf16*>(tri_bias));
+  } else {
+    hipLaunchKernelGGL(mask_bias_kernel<float>, dim3((uint32_t)blocks), dim3(256), 0, stream, mask,
+                       ms_i, ms_j, n, np, inf, mbias, static_cast<float*>(tri_bias));
+  }
   return hipGetLastError();
 }
 

@@ -84,9 +84,11 @@ hipError_t launch_projection(int mode, const ProjArgs& args, hipStream_t stream)
 
 // -------------------------------------------------------------- elementwise
 // mbias[i][k] = k < n ? inf * (mask_x[i][k] - 1) : -inf  (0 for k < n when
-// mask is null), and zero rows [n, np) of every head of the triangle bias.
+// mask is null), and zero rows [n, np) of every head of the triangle bias
+// (float, or bf16 when bias_bf16).
 hipError_t launch_mask_bias(const float* mask, int64_t ms_i, int64_t ms_j, int n, int np,
-                            float inf, float* mbias, float* tri_bias, hipStream_t stream);
+                            float inf, float* mbias, void* tri_bias, bool bias_bf16,
+                            hipStream_t stream);
 
 // LayerNorm over 128 channels of rows x[i][j] at x + i*xs_i + j*xs_j,
 // written contiguously to y[(i*rows_j + j)*128 + c].
@@ -97,6 +99,52 @@ hipError_t launch_layer_norm(const float* x, int64_t rows_i, int64_t rows_j, int
 // out = value * sigmoid(gate), float4 vectors.
 hipError_t launch_sigmoid_mul(const float* gate, const float* value, float* out, int64_t count4,
                               hipStream_t stream);
+
+// ------------------------------------------------------------ BF16 block
+// BF16 storage / FP32 accumulation variant of the block (gfx950
+// v_mfma_f32_32x32x16_bf16).  Same workspace roles and strides as the FP32
+// block, with q, k, v^T, gate, gated output and triangle bias held as bf16;
+// the mask bias stays float.
+struct Bf16ProjArgs {
+  const __bf16* x;
+  int64_t xs_i;
+  int64_t xs_j;
+  int rows_i;
+  int rows_j;
+  int span_j;
+  const __bf16* ln_w;
+  const __bf16* ln_b;
+  float eps;
+  const __bf16* w[4];
+  const __bf16* bias_vec;   // gate bias (prepare) or output bias (finish), nullable
+  const __bf16* w_bias;
+  float q_scale;
+  __bf16* qh;
+  __bf16* kh;
+  __bf16* vt;
+  __bf16* gs;
+  __bf16* tri_bias;
+  int np;
+  __bf16* out;
+  int64_t os_i;
+  int64_t os_j;
+};
+
+struct Bf16AttnArgs {
+  const __bf16* q;
+  const __bf16* k;
+  const __bf16* v;
+  const float* mbias;
+  const __bf16* bias;
+  const __bf16* gate;
+  __bf16* out;
+  int batch;
+  int n;
+  int np;
+};
+
+hipError_t launch_projection_bf16(int mode, const Bf16ProjArgs& args, hipStream_t stream);
+hipError_t launch_attention_bf16(const Bf16AttnArgs& args, hipStream_t stream);
 
 int device_cu_count();
 

@@ -36,6 +36,7 @@ OPERATION = "triangle_attention"
 BLOCK_OPERATION = "triangle_attention_block"
 IMPLEMENTATION = "amd-gfx950-hip-attention-f32"
 BLOCK_IMPLEMENTATION = "amd-gfx950-hip-block-f32"
+BLOCK_BF16_IMPLEMENTATION = "amd-gfx950-hip-block-bf16"
 ARCHITECTURE = "gfx950"
 HEADS = 4
 HEAD_DIM = 32
@@ -168,11 +169,12 @@ def block_eligible(module: Any, z: Any, mask: Any) -> tuple[bool, str]:
     """Check the tensor/module contract that the signature cannot carry."""
     import torch
 
-    if not getattr(z, "is_cuda", False) or z.dtype != torch.float32:
-        return False, "z is not a float32 HIP tensor"
+    if not getattr(z, "is_cuda", False) or z.dtype not in (torch.float32, torch.bfloat16):
+        return False, "z is not a float32 or bfloat16 HIP tensor"
     if z.dim() != 3 or z.shape[0] != z.shape[1] or z.shape[2] != 128 or z.stride(2) != 1:
         return False, "z must be [N, N, 128] with unit channel stride"
-    if z.stride(0) % 4 or z.stride(1) % 4 or z.data_ptr() % 16:
+    align = 16 // z.element_size()
+    if z.stride(0) % align or z.stride(1) % align or z.data_ptr() % 16:
         return False, "z rows are not 16-byte aligned"
     if mask is not None and (tuple(mask.shape) != tuple(z.shape[:2]) or mask.device != z.device):
         return False, "mask must be [N, N] on z's device"
@@ -185,20 +187,21 @@ def block_eligible(module: Any, z: Any, mask: Any) -> tuple[bool, str]:
         weights = _weights_of(module)
     except (AttributeError, TypeError, ValueError) as error:
         return False, f"module layout: {error}"
-    if any(t is not None and (t.device != z.device or t.dtype != torch.float32)
+    if any(t is not None and (t.device != z.device or t.dtype != z.dtype)
            for t in weights.tensors()):
-        return False, "weights are not float32 on z's device"
+        return False, "weights do not have z's dtype and device"
     return True, ""
 
 
-def _supports_block(signature: OperationSignature) -> bool | tuple[bool, str]:
+def _supports_block(signature: OperationSignature, *,
+                    dtype: str = "float32") -> bool | tuple[bool, str]:
     attributes = dict(signature.attributes)
     if signature.device_type != "cuda":
         return False, "device is not CUDA/HIP"
     if signature.architecture != ARCHITECTURE:
         return False, f"architecture is not {ARCHITECTURE}"
-    if signature.dtype != "float32":
-        return False, "dtype is not float32"
+    if signature.dtype != dtype:
+        return False, f"dtype is not {dtype}"
     if signature.mode != "inference":
         return False, "training or autograd is enabled"
     if attributes.get("eligible") != "True":
@@ -211,6 +214,7 @@ def _supports_block(signature: OperationSignature) -> bool | tuple[bool, str]:
 def _block(*, module: Any, z: Any, mask: Any, ending: bool, native: Any) -> Any:
     del native
     return triangle_attention_block(z, mask, _weights_of(module).to(z.device), ending=ending)
+
 
 
 def dispatch_triangle_attention_block(*, module: Any, z: Any, mask: Any, ending: bool,
@@ -229,3 +233,6 @@ registry.register(operation=OPERATION, name=IMPLEMENTATION, function=attention,
                   supports=_supports_core, priority=30, version="1")
 registry.register(operation=BLOCK_OPERATION, name=BLOCK_IMPLEMENTATION, function=_block,
                   supports=_supports_block, priority=30, version="1")
+registry.register(operation=BLOCK_OPERATION, name=BLOCK_BF16_IMPLEMENTATION, function=_block,
+                  supports=lambda signature: _supports_block(signature, dtype="bfloat16"),
+                  priority=30, version="1")

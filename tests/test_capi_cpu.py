@@ -45,9 +45,10 @@ def test_abi_version_and_workspace_sizes(lib):
     for n in (1, 124, 512, 1000, 1536, 2048):
         np_ = -(-n // 128) * 128
         seg = lambda b: -(-b // 256) * 256  # noqa: E731
-        expected = (3 * seg(n * 4 * np_ * 32 * 4) + 2 * seg(n * n * 128 * 4)
-                    + seg(4 * np_ * np_ * 4) + seg(n * np_ * 4))
-        assert lib.fpx_tri_attn_workspace_bytes(n, 128, 4, 32, 0) == expected
+        for dtype, e in ((0, 4), (1, 2)):
+            expected = (3 * seg(n * 4 * np_ * 32 * e) + 2 * seg(n * n * 128 * e)
+                        + seg(4 * np_ * np_ * e) + seg(n * np_ * 4))
+            assert lib.fpx_tri_attn_workspace_bytes(n, 128, 4, 32, dtype) == expected
     for bad in ((0, 128, 4, 32, 0), (4097, 128, 4, 32, 0), (64, 64, 4, 32, 0),
                 (64, 128, 8, 32, 0), (64, 128, 4, 16, 0), (64, 128, 4, 32, 7)):
         assert lib.fpx_tri_attn_workspace_bytes(*bad) == 0
@@ -67,7 +68,9 @@ def test_block_guards(lib):
     assert f(*_block_args()) == 4                                   # workspace too small
     assert f(*_block_args(n=0)) == 2
     assert f(*_block_args(c=64)) == 2
-    assert f(*_block_args(dtype=1)) == 2                            # BF16 block not built
+    assert f(*_block_args(dtype=7)) == 2                            # unknown storage type
+    assert f(*_block_args(dtype=1)) == 4                            # BF16: workspace too small
+    assert f(*_block_args(dtype=1, zs1=132)) == 2                   # bf16 rows need 8-element strides
     assert f(*_block_args(ending=2)) == 2
     assert f(*_block_args(zs1=126)) == 2                            # rows not 16-byte aligned
     assert f(*_block_args(eps=-1.0)) == 2

@@ -108,7 +108,7 @@ def test_block_dispatch_falls_back_on_cpu_and_reports_reason():
     decision = registry.manifest()["decisions"][0]
     assert decision["selected"] == "native"
     assert decision["rejected"][0]["reason"] == "device is not CUDA/HIP"
-    assert ta.block_eligible(m, z, None) == (False, "z is not a float32 HIP tensor")
+    assert ta.block_eligible(m, z, None) == (False, "z is not a float32 or bfloat16 HIP tensor")
 
 
 def test_block_entry_raises_without_a_device():
@@ -137,4 +137,5 @@ def test_stage_hooks_fall_back_on_cpu():
 def test_registered_implementations():
     impl = registry.manifest()["implementations"]
     assert impl[ta.OPERATION][0]["name"] == ta.IMPLEMENTATION
-    assert impl[ta.BLOCK_OPERATION][0]["name"] == ta.BLOCK_IMPLEMENTATION
+    assert {c["name"] for c in impl[ta.BLOCK_OPERATION]} == {ta.BLOCK_IMPLEMENTATION,
+                                                             ta.BLOCK_BF16_IMPLEMENTATION}

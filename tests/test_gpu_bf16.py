@@ -1,0 +1,86 @@
+"""GPU parity of the BF16-storage / FP32-accumulate block (config c5 family).
+
+Bar: max|actual - native| <= 2e-2 * max|native|, where native is the oracle's
+``block_bf16`` -- the native path run on bfloat16 tensors, rounding every
+intermediate where the native BF16 path rounds it.  The FP32 oracle on the
+same bf16-rounded inputs is reported beside it.  At N=2048 a seeded set of
+outer rows is compared and the full output is checked for the ending-node
+transpose identity and determinism.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from fireprot_amd import block as hip_block
+from fireprot_amd import workloads
+from oracle import triangle_attention as oracle
+
+pytestmark = pytest.mark.gpu
+
+BF16_REL = 2e-2
+
+
+def _rel(actual, expected):
+    return ((actual.float() - expected.float()).abs().max() / expected.float().abs().max()).item()
+
+
+def _weights(w):
+    return hip_block.BlockWeights.from_tensors(**w, dtype=torch.bfloat16).to("cuda")
+
+
+def _fp32_on_bf16_inputs(z, mask, w, ending, outer_rows=None):
+    wr = {k: (None if v is None else v.to(torch.bfloat16).float()) for k, v in w.items()}
+    return oracle.block(z.to(torch.bfloat16).float(), mask, oracle.BlockParams(**wr),
+                        ending=ending, outer_rows=outer_rows)
+
+
+@pytest.mark.parametrize("ending", [False, True])
+@pytest.mark.parametrize("n,valid", [(5, None), (37, 30), (124, None), (160, 140)])
+def test_bf16_block_matches_native_bf16(n, valid, ending):
+    print(f"case bf16 n={n} valid={valid} ending={ending}", flush=True)
+    z = workloads.make_pair(n)
+    mask = workloads.make_mask(n, valid)
+    w = workloads.make_weights()
+    with torch.inference_mode():
+        actual = hip_block.triangle_attention_block(
+            z.to(torch.bfloat16).cuda(), None if mask is None else mask.cuda(), _weights(w),
+            ending=ending)
+        torch.cuda.synchronize()
+    actual = actual.cpu()
+    assert actual.dtype == torch.bfloat16 and torch.isfinite(actual.float()).all()
+    native = oracle.block_bf16(z, mask, oracle.BlockParams(**w), ending=ending)
+    fp32 = _fp32_on_bf16_inputs(z, mask, w, ending)
+    rel_native, rel_fp32 = _rel(actual, native), _rel(actual, fp32)
+    print(f"bf16 n={n} ending={ending}: rel vs native-bf16 {rel_native:.2e}, vs fp32 {rel_fp32:.2e}",
+          flush=True)
+    assert rel_native <= BF16_REL
+
+
+def test_c5_n2048_row_subset_transpose_and_determinism():
+    cfg = workloads.CONFIGS["c5"]
+    print(f"case {cfg.name}", flush=True)
+    z, mask, w = workloads.make_inputs(cfg)
+    zc = z.to(torch.bfloat16).cuda()
+    weights = _weights(w)
+    rows = torch.tensor([0, 1, 777, 1024, 2046, 2047])
+    with torch.inference_mode():
+        start = hip_block.triangle_attention_block(zc, None, weights, ending=False)
+        end = hip_block.triangle_attention_block(zc, None, weights, ending=True)
+        zt = zc.transpose(0, 1).contiguous()
+        end_ref = hip_block.triangle_attention_block(zt, None, weights, ending=False).transpose(0, 1)
+        again = hip_block.triangle_attention_block(zc, None, weights, ending=False)
+        torch.cuda.synchronize()
+        assert torch.equal(end, end_ref), "ending node differs from T(start(T(z)))"
+        assert torch.equal(start, again), "block is not deterministic"
+        assert torch.isfinite(start.float()).all() and torch.isfinite(end.float()).all()
+        start_rows = start[rows.cuda()].cpu()
+        end_rows = end.transpose(0, 1)[rows.cuda()].cpu()
+    del zc, zt, start, end, end_ref, again
+    torch.cuda.empty_cache()
+    params = oracle.BlockParams(**w)
+    for name, actual, ending in (("start", start_rows, False), ("end", end_rows, True)):
+        native = oracle.block_bf16(z, None, params, ending=ending, outer_rows=rows)
+        rel = _rel(actual, native)
+        print(f"{cfg.name} {name} rows: rel vs native-bf16 {rel:.2e}", flush=True)
+        assert rel <= BF16_REL

@@ -220,3 +220,25 @@ def test_planted_mistakes_are_rejected(kind, monkeypatch):
                                   equal_nan=True):
                 rejected = True
     assert rejected, f"fixtures did not catch the planted mistake {kind}"
+
+
+# ---------------------------------------------------------------- BF16 oracle
+
+@pytest.mark.parametrize("ending", [False, True])
+def test_bf16_oracle_tracks_fp32_oracle_within_bf16_error(ending):
+    """block_bf16 runs the native ops on bfloat16 tensors; against the FP32
+    oracle on the same bf16-rounded inputs it must differ by bf16 rounding
+    only: more than float32 noise, well inside the 2e-2 BF16 bar."""
+    from fireprot_amd import workloads
+
+    n = 24
+    z = workloads.make_pair(n)
+    mask = workloads.make_mask(n, 20)
+    w = workloads.make_weights()
+    native = oracle.block_bf16(z, mask, oracle.BlockParams(**w), ending=ending)
+    assert native.dtype == torch.bfloat16
+    wr = {k: (None if v is None else v.to(torch.bfloat16).float()) for k, v in w.items()}
+    fp32 = oracle.block(z.to(torch.bfloat16).float(), mask, oracle.BlockParams(**wr),
+                        ending=ending)
+    rel = ((native.float() - fp32).abs().max() / fp32.abs().max()).item()
+    assert 1e-4 < rel < 2e-2
