@@ -1,27 +1,45 @@
 // Flash-style triangle attention on the CDNA4 FP32 matrix cores.
 //
 // One work-group = (outer row b, head h, 128 queries); four wavefronts, each
-// owning 32 queries.  Keys are streamed in tiles of 32: K and V^T tiles are
-// staged once in LDS for the four waves, the [128 x 32] triangle-bias tile and
-// the 32 mask-bias values beside them.  The N x N logits of a row and the
-// N^3 score volume never reach HBM.
+// owning 32 queries.  Keys are streamed in tiles of 32.  K and V^T tiles are
+// staged once in LDS for the four waves, in double buffers, so there is one
+// barrier per tile.  The N x N logits of a row and the N^3 score volume never
+// reach HBM.
 //
 // Per key tile each wave computes S^T = K Q^T (16 x v_mfma_f32_32x32x2_f32)
-// and O^T += V^T P^T (16 more).  Computing the transposed products puts one
-// query per lane column (lane % 32) in both results, so the online-softmax
-// row statistics, the P operand and the O rescale all live in the lane that
-// needs them: the only cross-lane step is one xor-32 exchange of the tile max.
+// and O^T += V^T P^T (16 more).  With the transposed products, each lane
+// column (lane % 32) holds one query in both results.  The online-softmax row
+// statistics, the P operand and the O rescale therefore all live in the lane
+// that needs them.  The only cross-lane step is one xor-32 exchange of the
+// tile max.
 //
-// Logits are formed in the native order fl(fl(s + mask_bias) + bias)
-// (patches/protenix/0005-*.patch:36-45; kernels/amd/fireprot_softmax_fp32.cpp:
-// 33-35), so fully masked padding rows reproduce the native tie structure of
-// the -1e9-quantised logits.  exp is taken of (x - max) formed in the natural
-// domain before scaling by log2(e), which keeps those ties exact.  A row whose
-// logits are all -inf gives NaN, as torch.softmax does.
+// Cost model.  On gfx950 an FP32 MFMA and VALU work never overlap, whether
+// they come from one wave or from several waves of a SIMD: a tile costs its
+// 32 x 64 matrix cycles plus every VALU instruction around them.  The loop is
+// therefore built to issue as few VALU instructions per tile as possible:
+//   - In a row with at least one unmasked key, the triangle bias is the
+//     accumulator input of the first S^T MFMA.  It is loaded from a
+//     fragment-major copy straight into registers, so the add costs nothing.
+//     The mask bias is then added only on tiles flagged as masked.  A masked
+//     key of such a row gets weight exactly 0 whatever the rounding of its
+//     logit, because its logit is about -1e9 below the row max.
+//   - A row whose keys are all masked takes the exact path on every tile:
+//     fl(fl(s + mask_bias) + bias), the native order (patches/protenix/
+//     0005-*.patch:36-45; kernels/amd/fireprot_softmax_fp32.cpp:33-35).  Its
+//     logits are quantised to the FP32 spacing of -1e9 (64), and this order
+//     reproduces which keys tie at the max.
+//   - The running max is a lazy reference.  O and l are rescaled only when a
+//     tile's max exceeds it by more than 8 binary orders, so the weights
+//     exp2(x log2e - c) stay below 2^8.  Every weight shares the one rounded
+//     c, and the common factor cancels in O / l.
+//   - The loop is unrolled by two so the S^T accumulators swap roles with no
+//     register copies.
+// A row whose logits are all -inf gives NaN, as torch.softmax does.
 #include "common.hpp"
 #include "kernels.hpp"
 
 #include <cmath>
+#include <type_traits>
 
 namespace fpx {
 namespace {
@@ -30,69 +48,130 @@ constexpr int kBq = 128;   // queries per work-group
 constexpr int kBk = 32;    // keys per tile
 constexpr int kPad = 4;    // LDS row padding (floats): conflict-free b128 reads
 constexpr int kThreads = 256;
-#ifndef FPX_ATTN_ROW_GROUP
-#define FPX_ATTN_ROW_GROUP 8
+constexpr int kRowGroup = 8;  // outer rows that share a bias slice in L2
+// Occupancy the register budget is set for (waves per SIMD).
+#ifndef FPX_ATTN_WAVES_PER_SIMD
+#define FPX_ATTN_WAVES_PER_SIMD 2
 #endif
-constexpr int kRowGroup = FPX_ATTN_ROW_GROUP;  // outer rows that share a bias slice in L2
+// Rescale threshold in logit units: 8 binary orders of magnitude.
+constexpr float kRescaleNat = 8.0f * 0.69314718055994531f;
 
-struct TileRegs {
-  f32x4 v;
-  f32x4 b[4];
-  f32x4 m;
+typedef float KTile[kBk][kHeadDim + kPad];  // [key][channel]
+typedef float VTile[kHeadDim][kBk + kPad];  // [channel][key]
+
+constexpr int kMaxKeys = kTileFlagWords * 32 * kBk;  // 4096: the block's np bound
+
+__device__ __forceinline__ f32x16 cat4(f32x4 a, f32x4 b, f32x4 c, f32x4 d) {
+  f32x16 r;
+  r[0] = a.x; r[1] = a.y; r[2] = a.z; r[3] = a.w;
+  r[4] = b.x; r[5] = b.y; r[6] = b.z; r[7] = b.w;
+  r[8] = c.x; r[9] = c.y; r[10] = c.z; r[11] = c.w;
+  r[12] = d.x; r[13] = d.y; r[14] = d.z; r[15] = d.w;
+  return r;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer(const float* base, int64_t bytes) {
+  // dword 3 = 0x00020000: raw 32-bit buffer access on gfx9-family parts.
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+__device__ __forceinline__ f32x4 buffer_f4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+// Tile sources of one work-group.  Every tile index passed in is in range.
+template <int LAYOUT>
+struct Tiles;
+
+// The block's workspace: q, k [B][H][np][32]; v^T [B][H][32][np]; bias in
+// fragment order (bias_frag_index).  Buffer descriptors per work-group, so a
+// tile's address is one scalar offset and the loop spends no VALU on it.
+template <>
+struct Tiles<kAttnBlock> {
+  __amdgpu_buffer_rsrc_t rk, rv, rb;
+  uint32_t ok, ov, ob;
+  __device__ __forceinline__ Tiles(const AttnArgs& a, int b, int h, int qt32, int tid, int lane,
+                                   int /*half*/, int /*jq*/) {
+    const int64_t bh = (int64_t)b * kHeads + h;
+    const int64_t nt = a.np >> 5;
+    const int64_t slice = (int64_t)a.np * kHeadDim;
+    rk = buffer(a.k + bh * slice, slice * 4);
+    rv = buffer(a.v + bh * slice, slice * 4);
+    rb = buffer(a.bias + ((int64_t)h * nt + qt32) * nt * 1024, nt * 4096);
+    const int row8 = tid >> 3;
+    const int col4 = (tid & 7) * 4;
+    ok = (uint32_t)(row8 * kHeadDim + col4) * 4;
+    ov = (uint32_t)(row8 * a.np + col4) * 4;
+    ob = (uint32_t)lane * 16;
+  }
+  // thread (row8 = key, col4 = channel group)
+  __device__ __forceinline__ f32x4 k(int t) const { return buffer_f4(rk, ok, (uint32_t)t * 4096); }
+  // thread (row8 = channel, col4 = key group)
+  __device__ __forceinline__ f32x4 v(int t) const { return buffer_f4(rv, ov, (uint32_t)t * 128); }
+  static __device__ __forceinline__ void store_v(VTile& vs, f32x4 v, int row8, int col4) {
+    *(f32x4*)&vs[row8][col4] = v;
+  }
+  // The wave's [32 queries x 32 keys] bias fragment of key tile t: one
+  // contiguous 4 KB block, four coalesced 1 KB loads.
+  __device__ __forceinline__ f32x16 bias(int t) const {
+    const uint32_t s = (uint32_t)t * 4096;
+    return cat4(buffer_f4(rb, ob, s), buffer_f4(rb, ob + 1024, s), buffer_f4(rb, ob + 2048, s),
+                buffer_f4(rb, ob + 3072, s));
+  }
 };
 
-// K rows of tile k0 (thread: key row8, channels col4..col4+3).
-template <int LAYOUT>
-__device__ __forceinline__ f32x4 load_k(const AttnArgs& a, int b, int h, int k0, int tid) {
-  const int row8 = tid >> 3;
-  const int col4 = (tid & 7) * 4;
-  if (LAYOUT == kAttnBlock) {
-    const int64_t bh = (int64_t)b * kHeads + h;
-    return *(const f32x4*)(a.k + (bh * a.np + k0 + row8) * kHeadDim + col4);
+// The reference C-ABI layout (kernels/amd/fireprot_ck_attention.cpp:34-43):
+// q, k, v, out [B][n][H][32]; bias [H][n][bias_stride]; mask bias nullable.
+template <>
+struct Tiles<kAttnHeadLast> {
+  const AttnArgs& a;
+  int b, h, row8, col4, half, jq;
+  __device__ __forceinline__ Tiles(const AttnArgs& args, int b_, int h_, int /*qt32*/, int tid,
+                                   int /*lane*/, int half_, int jq_)
+      : a(args), b(b_), h(h_), row8(tid >> 3), col4((tid & 7) * 4), half(half_), jq(jq_) {}
+  __device__ __forceinline__ f32x4 row(const float* base, int t) const {
+    const int key = t * kBk + row8;
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    return key < a.n
+               ? *(const f32x4*)(base + (((int64_t)b * a.n + key) * kHeads + h) * kHeadDim + col4)
+               : zero;
   }
-  const int key = k0 + row8;
-  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-  return key < a.n ? *(const f32x4*)(a.k + (((int64_t)b * a.n + key) * kHeads + h) * kHeadDim + col4)
-                   : zero;
-}
-
-// V^T, triangle-bias and mask-bias slices of tile k0.
-template <int LAYOUT>
-__device__ __forceinline__ void load_vbm(const AttnArgs& a, int b, int h, int j0, int k0, int tid,
-                                         TileRegs& t) {
-  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-  const int row8 = tid >> 3;        // 0..31
-  const int col4 = (tid & 7) * 4;   // 0..28
-  if (LAYOUT == kAttnBlock) {
-    const int64_t bh = (int64_t)b * kHeads + h;
-    t.v = *(const f32x4*)(a.v + (bh * kHeadDim + row8) * a.np + k0 + col4);
+  // thread (row8 = key, col4 = channel group) for both K and V
+  __device__ __forceinline__ f32x4 k(int t) const { return row(a.k, t); }
+  __device__ __forceinline__ f32x4 v(int t) const { return row(a.v, t); }
+  static __device__ __forceinline__ void store_v(VTile& vs, f32x4 v, int row8, int col4) {
+    vs[col4 + 0][row8] = v.x;
+    vs[col4 + 1][row8] = v.y;
+    vs[col4 + 2][row8] = v.z;
+    vs[col4 + 3][row8] = v.w;
+  }
+  __device__ __forceinline__ f32x16 bias(int t) const {
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    f32x4 x[4];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int64_t row = j0 + row8 + 32 * m;
-      t.b[m] = *(const f32x4*)(a.bias + ((int64_t)h * a.bias_rows + row) * a.bias_stride + k0 + col4);
+    for (int rr = 0; rr < 4; ++rr) {
+      const int key = t * kBk + 8 * rr + 4 * half;  // n % 4 == 0: all-in or all-out
+      x[rr] = (jq < a.n && key < a.n)
+                  ? *(const f32x4*)(a.bias + ((int64_t)h * a.bias_rows + jq) * a.bias_stride + key)
+                  : zero;
     }
-    if (tid < 8) t.m = *(const f32x4*)(a.mbias + (int64_t)b * a.mb_stride + k0 + 4 * tid);
-  } else {
-    const int key = k0 + row8;
-    t.v = key < a.n ? *(const f32x4*)(a.v + (((int64_t)b * a.n + key) * kHeads + h) * kHeadDim + col4)
-                    : zero;
-    const bool cin = k0 + col4 < a.n;  // n % 4 == 0: a float4 is all-in or all-out
+    return cat4(x[0], x[1], x[2], x[3]);
+  }
+  __device__ __forceinline__ f32x16 mask(int t) const {
+    f32x16 r;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int row = j0 + row8 + 32 * m;
-      t.b[m] = (cin && row < a.n)
-                   ? *(const f32x4*)(a.bias + ((int64_t)h * a.bias_rows + row) * a.bias_stride + k0 + col4)
-                   : zero;
-    }
-    if (tid < 8) {
+    for (int rr = 0; rr < 4; ++rr) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int kk = k0 + 4 * tid + e;
-        t.m[e] = kk < a.n ? (a.mbias ? a.mbias[(int64_t)b * a.mb_stride + kk] : 0.f) : -INFINITY;
+        const int key = t * kBk + 8 * rr + 4 * half + e;
+        r[4 * rr + e] = key < a.n ? (a.mbias ? a.mbias[(int64_t)b * a.mb_stride + key] : 0.f)
+                                  : -INFINITY;
       }
     }
+    return r;
   }
-}
+};
 
 // max / sum of v over the lane pair (l, l ^ 32) with v_permlane32_swap
 // (no LDS round trip): after the swap one copy holds the low half in both
@@ -100,7 +179,8 @@ __device__ __forceinline__ void load_vbm(const AttnArgs& a, int b, int h, int j0
 __device__ __forceinline__ float xor32_max(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v),
                                                   __builtin_bit_cast(unsigned, v), false, false);
-  return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+  return __builtin_elementwise_maximum(__builtin_bit_cast(float, (unsigned)r[0]),
+                                       __builtin_bit_cast(float, (unsigned)r[1]));
 }
 __device__ __forceinline__ float xor32_sum(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v),
@@ -108,14 +188,14 @@ __device__ __forceinline__ float xor32_sum(float v) {
   return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
 }
 
-// S^T[key][q] = sum_c K[key][c] Q[q][c] for the 32 keys in Ks; the channel of
-// step s in lane half hb is 16*hb + s.
-__device__ __forceinline__ f32x16 qk_tile(const float (*Ks)[kHeadDim + kPad], const float* qf,
-                                          int l32, int half) {
-  f32x16 s = {};
+// S^T[key][q] = c + sum_ch K[key][ch] Q[q][ch] for the 32 keys of ks; lane
+// half hb supplies channel 16*hb + s at step s.
+__device__ __forceinline__ f32x16 qk_chain(const KTile& ks, const float* qf, int l32, int half,
+                                           f32x16 c) {
+  f32x16 s = c;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    const f32x4 kv = *(const f32x4*)&Ks[l32][16 * half + 4 * t];
+    const f32x4 kv = *(const f32x4*)&ks[l32][16 * half + 4 * t];
     s = mfma32(kv.x, qf[4 * t + 0], s);
     s = mfma32(kv.y, qf[4 * t + 1], s);
     s = mfma32(kv.z, qf[4 * t + 2], s);
@@ -125,12 +205,11 @@ __device__ __forceinline__ f32x16 qk_tile(const float (*Ks)[kHeadDim + kPad], co
 }
 
 template <int LAYOUT>
-__global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a, int nqt, int nkt,
+__global__ __launch_bounds__(kThreads, FPX_ATTN_WAVES_PER_SIMD) void attention_kernel(AttnArgs a, int nqt, int nkt,
                                                             uint32_t total) {
-  __shared__ __attribute__((aligned(16))) float Ks[kBk][kHeadDim + kPad];
-  __shared__ __attribute__((aligned(16))) float Vs[kHeadDim][kBk + kPad];
-  __shared__ __attribute__((aligned(16))) float Bs[kBq][kBk + kPad];
-  __shared__ __attribute__((aligned(16))) float Ms[kBk];
+  __shared__ __attribute__((aligned(16))) KTile Ks[2];
+  __shared__ __attribute__((aligned(16))) VTile Vs[2];
+  __shared__ __attribute__((aligned(16))) float Ms[LAYOUT == kAttnBlock ? kMaxKeys : 4];
 
   // Logical order, slowest to fastest: head, block of kRowGroup outer rows,
   // query tile, outer row in the block.  The work-groups that run together
@@ -148,11 +227,66 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a, int nqt
   if (b >= a.batch) return;  // padding of the last row group; uniform per work-group
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5;
   const int l32 = lane & 31;
   const int j0 = qt * kBq;
   const int jq = j0 + 32 * w + l32;
+  const int qt32 = (j0 >> 5) + w;
+  const int row8 = tid >> 3;
+  const int col4 = (tid & 7) * 4;
+  const int last = nkt - 1;
+  const Tiles<LAYOUT> io(a, b, h, qt32, tid, lane, half, jq);
+
+  // Row classification.  masked(t): some key of tile t has a nonzero mask
+  // bias.  has_unmasked: some key k < n of the row has a zero mask bias.
+  uint32_t mw[kTileFlagWords] = {0u, 0u, 0u, 0u};
+  bool any_masked, has_unmasked;
+  if (LAYOUT == kAttnBlock) {
+    const uint32_t* f = a.tile_flags + (int64_t)b * 2 * kTileFlagWords;
+    uint32_t any = 0u, open = 0u;
+#pragma unroll
+    for (int i = 0; i < kTileFlagWords; ++i) {
+      const int lo = 32 * i;
+      const uint32_t valid = nkt >= lo + 32 ? 0xffffffffu : nkt > lo ? (1u << (nkt - lo)) - 1u : 0u;
+      mw[i] = f[i];
+      any |= mw[i] & valid;
+      open |= ~f[kTileFlagWords + i] & valid;
+    }
+    any_masked = any != 0u;
+    has_unmasked = open != 0u;
+  } else {
+    any_masked = a.mbias != nullptr || a.n % kBk != 0;
+    int found = a.mbias == nullptr;
+    if (!found) {
+      for (int k = tid; k < a.n; k += kThreads)
+        found |= a.mbias[(int64_t)b * a.mb_stride + k] == 0.0f;
+    }
+    has_unmasked = __syncthreads_or(found) != 0;
+  }
+  auto masked = [&](int t) -> bool {
+    if (LAYOUT == kAttnBlock) {
+      const uint32_t word = t < 32 ? mw[0] : t < 64 ? mw[1] : t < 96 ? mw[2] : mw[3];
+      return (word >> (t & 31)) & 1u;
+    }
+    return any_masked && (a.mbias != nullptr || (t + 1) * kBk > a.n);
+  };
+  // The block's mask-bias row goes to LDS once (made visible by the prologue
+  // barrier); masked tiles then read their values with four b128 loads.
+  if (LAYOUT == kAttnBlock && any_masked) {
+    const float* src = a.mbias + (int64_t)b * a.mb_stride;
+    for (int k = 4 * tid; k < nkt * kBk; k += 4 * kThreads)
+      *(f32x4*)&Ms[k] = *(const f32x4*)(src + k);
+  }
+  auto mask_vals = [&](int t) -> f32x16 {
+    if constexpr (LAYOUT == kAttnBlock) {
+      const float* m = &Ms[t * kBk + 4 * half];
+      return cat4(*(const f32x4*)(m), *(const f32x4*)(m + 8), *(const f32x4*)(m + 16),
+                  *(const f32x4*)(m + 24));
+    } else {
+      return io.mask(t);
+    }
+  };
 
   // Q fragment (B operand of S^T = K Q^T): lane holds Q[jq][16*half + s].
   float qf[16];
@@ -176,103 +310,154 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a, int nqt
     }
   }
 
-  // Online-softmax state per query (this lane's column): running max m_run,
-  // its log2-scaled value c_run = fl(m_run * log2 e) (-inf until a finite max
-  // appears) and the running sum l_run.  p = exp2(fma(x, log2 e, -c)) with the
-  // same rounded c used for the rescale alpha = exp2(c_old - c_new), so every
-  // weight carries one common factor that cancels in O / l: the ratios
-  // e^(x - x') stay exact, -1e9-quantised masked logits included.
+  // Online-softmax state of this lane's query: the reference max m_ref (-inf
+  // until a finite logit appears), the threshold that triggers a rescale, the
+  // rounded log2-domain reference c (0 while m_ref is -inf, so all-(-inf)
+  // tiles give weight exp2(-inf) = 0), and the running sum of the weights.
   f32x16 o = {};
-  float m_run = -INFINITY;
-  float c_run = -INFINITY;
+  float m_ref = -INFINITY;
+  float m_thr = -INFINITY;
+  float c_ref = 0.f;
   float l_run = 0.f;
 
-  const int row8 = tid >> 3;
-  const int col4 = (tid & 7) * 4;
-  TileRegs regs;
-
-  auto store_vbm = [&]() {
-    if (LAYOUT == kAttnBlock) {
-      *(f32x4*)&Vs[row8][col4] = regs.v;
-    } else {
-      Vs[col4 + 0][row8] = regs.v.x;
-      Vs[col4 + 1][row8] = regs.v.y;
-      Vs[col4 + 2][row8] = regs.v.z;
-      Vs[col4 + 3][row8] = regs.v.w;
-    }
-#pragma unroll
-    for (int m = 0; m < 4; ++m) *(f32x4*)&Bs[row8 + 32 * m][col4] = regs.b[m];
-    if (tid < 8) *(f32x4*)&Ms[4 * tid] = regs.m;
-  };
-
-  // Softmax of the current tile's logits (in s, lane register r = key
-  // 8*(r/4) + 4*half + r%4) and O^T[c][q] += V^T[c][key] P^T[key][q].
-  auto softmax_pv = [&](f32x16 s) {
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const f32x4 mb = *(const f32x4*)&Ms[8 * rr + 4 * half];
-      const f32x4 bb = *(const f32x4*)&Bs[32 * w + l32][8 * rr + 4 * half];
-      s[4 * rr + 0] = (s[4 * rr + 0] + mb.x) + bb.x;
-      s[4 * rr + 1] = (s[4 * rr + 1] + mb.y) + bb.y;
-      s[4 * rr + 2] = (s[4 * rr + 2] + mb.z) + bb.z;
-      s[4 * rr + 3] = (s[4 * rr + 3] + mb.w) + bb.w;
-    }
-    float mt = s[0];
-#pragma unroll
-    for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
-    mt = xor32_max(mt);
-    const float m_new = fmaxf(m_run, mt);
-    const float c_new = m_new == -INFINITY ? -INFINITY : m_new * kLog2e;
-    const float c_use = m_new == -INFINITY ? 0.f : c_new;
-    const float alpha = exp2_fast(c_run - c_use);
-    float psum = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s[r] = exp2_fast(__builtin_fmaf(s[r], kLog2e, -c_use));
-      psum += s[r];
-    }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-    c_run = c_new;
-    if (__any(alpha != 1.0f)) {
+  auto softmax = [&](f32x16& s) {
+    // NaN-propagating maxima (v_maximum3_f32): a NaN logit poisons its row,
+    // as in the native softmax.
+    auto mx = [](float x, float y) { return __builtin_elementwise_maximum(x, y); };
+    float m0 = mx(mx(s[0], s[1]), s[2]);
+    float m1 = mx(mx(s[3], s[4]), s[5]);
+    float m2 = mx(mx(s[6], s[7]), s[8]);
+    float m3 = mx(mx(s[9], s[10]), s[11]);
+    float m4 = mx(mx(s[12], s[13]), s[14]);
+    m0 = mx(mx(m0, m1), s[15]);
+    m2 = mx(mx(m2, m3), m4);
+    const float mt = xor32_max(mx(m0, m2));
+    if (__any(mt > m_thr)) {
+      const float m_new = mx(m_ref, mt);
+      const float c_new = m_new == -INFINITY ? 0.f : m_new * kLog2e;
+      const float alpha = m_ref == -INFINITY ? 0.f : exp2_fast(c_ref - c_new);
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[r] *= alpha;
+      l_run *= alpha;
+      m_ref = m_new;
+      c_ref = c_new;
+      m_thr = m_new + kRescaleNat;
     }
 #pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = exp2_fast(__builtin_fmaf(s[r], kLog2e, -c_ref));
+    float p[4] = {s[0], s[1], s[2], s[3]};
+#pragma unroll
+    for (int r = 4; r < 16; ++r) p[r & 3] += s[r];
+    l_run += (p[0] + p[1]) + (p[2] + p[3]);
+  };
+
+  // O^T[c][q] += V^T[c][key] P^T[key][q]; lane register r of p is key
+  // 8*(r/4) + 4*half + r%4, as in the S^T accumulator.
+  auto pv = [&](const VTile& vs, const f32x16& p) {
+#pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-      const f32x4 vv = *(const f32x4*)&Vs[l32][8 * rr + 4 * half];
-      o = mfma32(vv.x, s[4 * rr + 0], o);
-      o = mfma32(vv.y, s[4 * rr + 1], o);
-      o = mfma32(vv.z, s[4 * rr + 2], o);
-      o = mfma32(vv.w, s[4 * rr + 3], o);
+      const f32x4 vv = *(const f32x4*)&vs[l32][8 * rr + 4 * half];
+      o = mfma32(vv.x, p[4 * rr + 0], o);
+      o = mfma32(vv.y, p[4 * rr + 1], o);
+      o = mfma32(vv.z, p[4 * rr + 2], o);
+      o = mfma32(vv.w, p[4 * rr + 3], o);
     }
   };
 
-  // Prologue: K of tile 0 into LDS, S^T of tile 0; stage K(1) and V/bias/mask(0).
-  *(f32x4*)&Ks[row8][col4] = load_k<LAYOUT>(a, b, h, 0, tid);
-  __syncthreads();
-  f32x16 s_cur = qk_tile(Ks, qf, l32, half);
-  f32x4 kreg = {0.f, 0.f, 0.f, 0.f};
-  if (nkt > 1) kreg = load_k<LAYOUT>(a, b, h, kBk, tid);
-  load_vbm<LAYOUT>(a, b, h, j0, 0, tid, regs);
+  // One pass over the key tiles.  Three register sets rotate through the
+  // roles "S^T of the current tile", "S^T of the next tile" and "bias of the
+  // tile after": a tile's bias is loaded into the registers where its scores
+  // are then accumulated.
+  //   kExact = false: the S^T chain accumulates onto the bias in place, and
+  //     masked tiles add their mask bias afterwards.
+  //   kExact = true: the chain starts from zero into a temporary, and every
+  //     tile forms fl(fl(s + mask) + bias) into the bias registers.
+  auto run = [&](auto exact_tag) {
+    constexpr bool kExact = decltype(exact_tag)::value;
+    const f32x16 zero16 = {};
+    f32x16 tmp;
+    // S^T of tile t from K in ks, onto set x (which holds bias(t)).
+    auto scores = [&](const KTile& ks, f32x16& x) {
+      if (kExact) {
+        tmp = qk_chain(ks, qf, l32, half, zero16);
+      } else {
+        x = qk_chain(ks, qf, l32, half, x);
+      }
+    };
+    auto finish_scores = [&](f32x16& x, int t) {
+      if (kExact) {
+        const f32x16 mb = mask_vals(t);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[r] = (tmp[r] + mb[r]) + x[r];
+      } else if (masked(t)) {
+        const f32x16 mb = mask_vals(t);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[r] += mb[r];
+      }
+    };
 
-  // Steady state: LDS holds K of tile kt+1 and V/bias/mask of tile kt, so
-  // the 16 MFMAs of S^T(kt+1) are independent of the softmax of tile kt.
-  for (int kt = 0; kt + 1 < nkt; ++kt) {
-    __syncthreads();  // every wave is done with K(kt) and V/bias/mask(kt-1)
-    *(f32x4*)&Ks[row8][col4] = kreg;
-    store_vbm();
+    // Prologue: K(0), K(1), V(0) into LDS; S^T(0); K(2) and V(1) in flight.
+    f32x4 kreg = io.k(0);
+    f32x4 vreg = io.v(0);
+    const f32x4 k1 = io.k(last < 1 ? last : 1);
+    f32x16 set_a = io.bias(0);
+    f32x16 set_b = io.bias(last < 1 ? last : 1);
+    f32x16 set_c;
+    *(f32x4*)&Ks[0][row8][col4] = kreg;
+    *(f32x4*)&Ks[1][row8][col4] = k1;
+    Tiles<LAYOUT>::store_v(Vs[0], vreg, row8, col4);
     __syncthreads();
-    if (kt + 2 < nkt) kreg = load_k<LAYOUT>(a, b, h, (kt + 2) * kBk, tid);
-    load_vbm<LAYOUT>(a, b, h, j0, (kt + 1) * kBk, tid, regs);
-    const f32x16 s_next = qk_tile(Ks, qf, l32, half);
-    softmax_pv(s_cur);
-    s_cur = s_next;
+    scores(Ks[0], set_a);
+    finish_scores(set_a, 0);
+    kreg = io.k(last < 2 ? last : 2);
+    vreg = io.v(last < 1 ? last : 1);
+    __syncthreads();  // every wave is done with K(0) before Ks[0] is refilled
+
+    // Iteration kt starts with: Ks[(kt+1)&1] = K(kt+1), Vs[kt&1] = V(kt),
+    // kreg = K(kt+2), vreg = V(kt+1) (loads in flight), cur = S^T(kt) with
+    // its biases, nxt = bias(kt+1); far is free.  Tile indices past the last
+    // are clamped (in range, never used).
+    auto body = [&](int kt, f32x16& cur, f32x16& nxt, f32x16& far) {
+      const int t2 = kt + 2 < last ? kt + 2 : last;
+      const int t3 = kt + 3 < last ? kt + 3 : last;
+      far = io.bias(t2);
+      scores(Ks[(kt + 1) & 1], nxt);
+      softmax(cur);
+      pv(Vs[kt & 1], cur);
+      finish_scores(nxt, kt + 1);
+      *(f32x4*)&Ks[kt & 1][row8][col4] = kreg;
+      Tiles<LAYOUT>::store_v(Vs[(kt + 1) & 1], vreg, row8, col4);
+      kreg = io.k(t3);
+      vreg = io.v(t2);
+      __syncthreads();
+    };
+    auto tail = [&](f32x16& cur, int kt) {
+      softmax(cur);
+      pv(Vs[kt & 1], cur);
+    };
+
+    int kt = 0;
+    for (; kt + 3 < nkt; kt += 3) {
+      body(kt, set_a, set_b, set_c);
+      body(kt + 1, set_b, set_c, set_a);
+      body(kt + 2, set_c, set_a, set_b);
+    }
+    if (kt + 1 == nkt) {
+      tail(set_a, kt);
+    } else if (kt + 2 == nkt) {
+      body(kt, set_a, set_b, set_c);
+      tail(set_b, kt + 1);
+    } else {
+      body(kt, set_a, set_b, set_c);
+      body(kt + 1, set_b, set_c, set_a);
+      tail(set_c, kt + 2);
+    }
+  };
+  if (has_unmasked) {
+    run(std::false_type{});
+  } else {
+    run(std::true_type{});
   }
-  __syncthreads();
-  store_vbm();
-  __syncthreads();
-  softmax_pv(s_cur);
 
   const float l_tot = xor32_sum(l_run);
   if (jq < a.n) {
@@ -295,13 +480,16 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a, int nqt
 }  // namespace
 
 hipError_t launch_attention(int layout, const AttnArgs& a, hipStream_t stream) {
+  // Query tiles cover the padded extent; key tiles stop at the last real key
+  // (tiles wholly past n hold only -inf mask bias and contribute nothing).
   const int nqt = (int)((layout == kAttnBlock ? a.np : round_up(a.n, kBq)) / kBq);
-  const int nkt = (int)((layout == kAttnBlock ? a.np : round_up(a.n, kBk)) / kBk);
+  const int nkt = (int)(round_up(a.n, kBk) / kBk);
   const uint64_t groups = ((uint64_t)a.batch + kRowGroup - 1) / kRowGroup;
   const uint64_t total = groups * kRowGroup * kHeads * nqt;
   if (total == 0) return hipSuccess;
   if (total > 0x7fffffffull) return hipErrorInvalidValue;
   if (layout == kAttnBlock) {
+    if (a.tile_flags == nullptr || nkt > kTileFlagWords * 32) return hipErrorInvalidValue;
     hipLaunchKernelGGL(attention_kernel<kAttnBlock>, dim3((uint32_t)total), dim3(kThreads), 0,
                        stream, a, nqt, nkt, (uint32_t)total);
   } else {

@@ -30,9 +30,10 @@ size_t elem_bytes(int dtype) { return dtype == FPX_BF16 ? 2 : 4; }
 // Workspace segments of the block, all 256-byte aligned, element size e
 // (4 for FPX_F32, 2 for FPX_BF16; the mask bias is always float):
 //   qh, kh [n][4][np][32]; vt [n][4][32][np]; gs, og [n][n][128];
-//   tri_bias [4][np][np]; mbias [n][np] float
+//   tri_bias [4][np][np] (FP32: fragment order); mbias [n][np] float;
+//   tile flags [n][2 * kTileFlagWords] uint32
 struct BlockWorkspace {
-  size_t qh, kh, vt, gs, og, bias, mbias, total;
+  size_t qh, kh, vt, gs, og, bias, mbias, flags, total;
 };
 
 BlockWorkspace block_workspace(int n, int dtype) {
@@ -43,6 +44,7 @@ BlockWorkspace block_workspace(int n, int dtype) {
   const size_t g = seg((size_t)n * n * fpx::kHidden * e);
   const size_t bias = seg((size_t)fpx::kHeads * np * np * e);
   const size_t mb = seg((size_t)n * np * sizeof(float));
+  const size_t fl = seg((size_t)n * 2 * fpx::kTileFlagWords * sizeof(uint32_t));
   BlockWorkspace w{};
   w.qh = 0;
   w.kh = w.qh + qkv;
@@ -51,7 +53,8 @@ BlockWorkspace block_workspace(int n, int dtype) {
   w.og = w.gs + g;
   w.bias = w.og + g;
   w.mbias = w.bias + bias;
-  w.total = w.mbias + mb;
+  w.flags = w.mbias + mb;
+  w.total = w.flags + fl;
   return w;
 }
 
@@ -65,6 +68,7 @@ int status(hipError_t e) { return e == hipSuccess ? FPX_OK : (int)e; }
 struct BlockPointers {
   char *qh, *kh, *vt, *gs, *og, *tri;
   float* mbias;
+  uint32_t* flags;
   int np;
 };
 
@@ -79,6 +83,7 @@ BlockPointers block_pointers(void* workspace, int n, int dtype) {
   p.og = base + ws.og;
   p.tri = base + ws.bias;
   p.mbias = reinterpret_cast<float*>(base + ws.mbias);
+  p.flags = reinterpret_cast<uint32_t*>(base + ws.flags);
   p.np = (int)round_up(n, kQueryTile);
   return p;
 }
@@ -132,8 +137,8 @@ int fpx_tri_attn_prepare(int dtype, const void* z, int64_t z_stride0, int64_t z_
   const int64_t ms_i = ending ? m_stride1 : m_stride0;
   const int64_t ms_j = ending ? m_stride0 : m_stride1;
 
-  hipError_t e = fpx::launch_mask_bias(mask, ms_i, ms_j, n, w.np, mask_inf, w.mbias, w.tri,
-                                       dtype == FPX_BF16, s);
+  hipError_t e = fpx::launch_mask_bias(mask, ms_i, ms_j, n, w.np, mask_inf, w.mbias, w.flags,
+                                       w.tri, dtype == FPX_BF16, s);
   if (e != hipSuccess) return status(e);
 
   const float q_scale = 1.0f / std::sqrt((float)fpx::kHeadDim);
@@ -216,6 +221,7 @@ int fpx_tri_attn_attend(int dtype, int n, void* workspace, size_t workspace_byte
   a.bias_rows = w.np;
   a.gate = as<float>(w.gs);
   a.out = as<float>(w.og);
+  a.tile_flags = w.flags;
   a.batch = n;
   a.n = n;
   a.np = w.np;

@@ -88,4 +88,17 @@ __host__ __device__ __forceinline__ int64_t round_up(int64_t x, int64_t m) {
   return (x + m - 1) / m * m;
 }
 
+// Position of triangle-bias element (head h, query q, key k) in the FP32
+// block's fragment-major copy: for every (head, 32-query tile, 32-key tile)
+// one contiguous 4 KB block laid out exactly as the S^T accumulator of
+// v_mfma_f32_32x32x2_f32 (lane = q%32 + 32*((k%32/4)%2), register
+// r = 4*(k%32/8) + k%4), so a wave loads its fragment with four coalesced
+// 1 KB reads.  np is the padded extent (a multiple of 32).
+__host__ __device__ __forceinline__ int64_t bias_frag_index(int h, int q, int k, int np) {
+  const int64_t nt = np >> 5;
+  const int t = k & 31;
+  return (((int64_t)h * nt + (q >> 5)) * nt + (k >> 5)) * 1024 + (t >> 3) * 256 +
+         ((q & 31) + 32 * ((t >> 2) & 1)) * 4 + (t & 3);
+}
+
 }  // namespace fpx

@@ -9,28 +9,66 @@
 namespace fpx {
 namespace {
 
-// mbias[i][k] (i < n, k < np) followed by zero rows [n, np) of each head of
-// the triangle bias.  inf * (mask - 1) is evaluated as two rounded fp32 ops,
-// as the native expression is (patches/protenix/0005-*.patch:36-39).
-template <typename BiasT>
-__global__ void mask_bias_kernel(const float* __restrict__ mask, int64_t ms_i, int64_t ms_j, int n,
-                                 int np, float inf, float* __restrict__ mbias,
-                                 BiasT* __restrict__ tri_bias) {
-  const int64_t head_rows = (int64_t)(np - n) * np;
-  const int64_t total = (int64_t)n * np + kHeads * head_rows;
+// One wavefront per outer row i: mbias[i][k] for k < np and the row's tile
+// flags.  Word w of the first kTileFlagWords has bit t % 32 of tile t = 32w +
+// t % 32 set when some key of that 32-key tile has a nonzero mask bias (-0
+// counts as zero, since s + -0 == s); the next kTileFlagWords words do the
+// same for "every key of the tile has a nonzero mask bias".  Padded keys
+// (k >= n, -inf) count as masked.  inf * (mask - 1) is evaluated as two
+// rounded fp32 ops, as the native expression is
+// (patches/protenix/0005-*.patch:36-39).  np is a multiple of 64.
+__global__ __launch_bounds__(256) void mask_rows_kernel(const float* __restrict__ mask,
+                                                        int64_t ms_i, int64_t ms_j, int n, int np,
+                                                        float inf, float* __restrict__ mbias,
+                                                        uint32_t* __restrict__ flags) {
+  const int lane = threadIdx.x & 63;
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (i >= n) return;
+  uint32_t any[kTileFlagWords] = {};
+  uint32_t all[kTileFlagWords] = {};
+  for (int k0 = 0; k0 < np; k0 += 64) {
+    const int k = k0 + lane;
+    float v = -INFINITY;
+    if (k < n) v = mask ? inf * (mask[i * ms_i + k * ms_j] - 1.0f) : 0.0f;
+    mbias[(int64_t)i * np + k] = v;
+    const uint64_t nz = __ballot(v != 0.0f);
+    const uint32_t lo = (uint32_t)nz;
+    const uint32_t hi = (uint32_t)(nz >> 32);
+    const int t = k0 >> 5;  // tiles t and t + 1 (t even)
+    const uint32_t any_bits = (uint32_t)(lo != 0u) | ((uint32_t)(hi != 0u) << 1);
+    const uint32_t all_bits = (uint32_t)(lo == ~0u) | ((uint32_t)(hi == ~0u) << 1);
+#pragma unroll
+    for (int wd = 0; wd < kTileFlagWords; ++wd) {
+      if (wd == (t >> 5)) {
+        any[wd] |= any_bits << (t & 31);
+        all[wd] |= all_bits << (t & 31);
+      }
+    }
+  }
+  uint32_t* dst = flags + (int64_t)i * 2 * kTileFlagWords;
+#pragma unroll
+  for (int wd = 0; wd < kTileFlagWords; ++wd) {
+    if (lane == wd) dst[wd] = any[wd];
+    if (lane == kTileFlagWords + wd) dst[kTileFlagWords + wd] = all[wd];
+  }
+}
+
+// Zero rows [n, np) of every head of the triangle bias (padded queries), in
+// the FP32 fragment order or row-major.
+template <typename BiasT, bool kFrag>
+__global__ void bias_pad_kernel(int n, int np, BiasT* __restrict__ tri_bias) {
+  const int64_t per_head = (int64_t)(np - n) * np;
+  const int64_t total = kHeads * per_head;
   for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
        idx += (int64_t)gridDim.x * blockDim.x) {
-    if (idx < (int64_t)n * np) {
-      const int i = (int)(idx / np);
-      const int k = (int)(idx % np);
-      float v = -INFINITY;
-      if (k < n) v = mask ? inf * (mask[i * ms_i + k * ms_j] - 1.0f) : 0.0f;
-      mbias[idx] = v;
+    const int h = (int)(idx / per_head);
+    const int64_t r = idx % per_head;
+    const int q = n + (int)(r / np);
+    const int k = (int)(r % np);
+    if (kFrag) {
+      tri_bias[bias_frag_index(h, q, k, np)] = (BiasT)0.0f;
     } else {
-      const int64_t r = idx - (int64_t)n * np;
-      const int64_t h = r / head_rows;
-      const int64_t rest = r % head_rows;
-      tri_bias[(h * np + n) * np + rest] = (BiasT)0.0f;
+      tri_bias[((int64_t)h * np + q) * np + k] = (BiasT)0.0f;
     }
   }
 }
@@ -75,19 +113,24 @@ __global__ __launch_bounds__(256) void sigmoid_mul_kernel(const f32x4* __restric
 }  // namespace
 
 hipError_t launch_mask_bias(const float* mask, int64_t ms_i, int64_t ms_j, int n, int np,
-                            float inf, float* mbias, void* tri_bias, bool bias_bf16,
-                            hipStream_t stream) {
-  const int64_t total = (int64_t)n * np + (int64_t)kHeads * (np - n) * np;
-  if (total == 0) return hipSuccess;
+                            float inf, float* mbias, uint32_t* tile_flags, void* tri_bias,
+                            bool bias_bf16, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  if (np % 64 || np > kTileFlagWords * 32 * 32) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(mask_rows_kernel, dim3((uint32_t)((n + 3) / 4)), dim3(256), 0, stream, mask,
+                     ms_i, ms_j, n, np, inf, mbias, tile_flags);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || np == n) return e;
+  const int64_t total = (int64_t)kHeads * (np - n) * np;
   int64_t blocks = (total + 255) / 256;
   const int64_t cap = (int64_t)device_cu_count() * 16;
   if (blocks > cap) blocks = cap;
   if (bias_bf16) {
-    hipLaunchKernelGGL(mask_bias_kernel<__bf16>, dim3((uint32_t)blocks), dim3(256), 0, stream, mask,
-                       ms_i, ms_j, n, np, inf, mbias, static_cast<__bf16*>(tri_bias));
+    hipLaunchKernelGGL((bias_pad_kernel<__bf16, false>), dim3((uint32_t)blocks), dim3(256), 0,
+                       stream, n, np, static_cast<__bf16*>(tri_bias));
   } else {
-    hipLaunchKernelGGL(mask_bias_kernel<float>, dim3((uint32_t)blocks), dim3(256), 0, stream, mask,
-                       ms_i, ms_j, n, np, inf, mbias, static_cast<float*>(tri_bias));
+    hipLaunchKernelGGL((bias_pad_kernel<float, true>), dim3((uint32_t)blocks), dim3(256), 0,
+                       stream, n, np, static_cast<float*>(tri_bias));
   }
   return hipGetLastError();
 }

@@ -16,7 +16,10 @@ namespace fpx {
 //                q, k : [B][H][np][32]   (q pre-scaled by 1/sqrt(32))
 //                v    : [B][H][32][np]   (transposed per head)
 //                mbias: [B][np]          (required)
-//                bias : [H][np][np]
+//                tile_flags: [B][2][kTileFlagWords] bit t of part 0 = some
+//                        key of 32-key tile t has a nonzero mask bias; of
+//                        part 1 = every key of tile t has one
+//                bias : [H][np][np] in fragment order (bias_frag_index)
 //                gate : [B][n][128] sigmoid(g), multiplied in the epilogue
 //                out  : [B][n][128]      (o * gate, head-last)
 // kAttnHeadLast: the reference C-ABI layout (fireprot_ck_attention.cpp:34-43):
@@ -24,6 +27,9 @@ namespace fpx {
 //                bias : [H][n][bias_stride]  (batch stride 0)
 //                mbias: nullable, [B] rows of n values, row stride mb_stride
 enum AttnLayout { kAttnBlock = 0, kAttnHeadLast = 1 };
+
+// Words of per-row tile flags: 32-key tiles of np <= 4096 keys.
+constexpr int kTileFlagWords = 4;
 
 struct AttnArgs {
   const float* q;
@@ -36,6 +42,7 @@ struct AttnArgs {
   int64_t bias_rows;
   const float* gate;
   float* out;
+  const uint32_t* tile_flags;
   int batch;
   int n;
   int np;
@@ -84,11 +91,12 @@ hipError_t launch_projection(int mode, const ProjArgs& args, hipStream_t stream)
 
 // -------------------------------------------------------------- elementwise
 // mbias[i][k] = k < n ? inf * (mask_x[i][k] - 1) : -inf  (0 for k < n when
-// mask is null), and zero rows [n, np) of every head of the triangle bias
-// (float, or bf16 when bias_bf16).
+// mask is null), the per-row tile flags of the attention kernel, and zero
+// rows [n, np) of every head of the triangle bias: float in fragment order
+// (bias_frag_index), or row-major bf16 when bias_bf16.
 hipError_t launch_mask_bias(const float* mask, int64_t ms_i, int64_t ms_j, int n, int np,
-                            float inf, float* mbias, void* tri_bias, bool bias_bf16,
-                            hipStream_t stream);
+                            float inf, float* mbias, uint32_t* tile_flags, void* tri_bias,
+                            bool bias_bf16, hipStream_t stream);
 
 // LayerNorm over 128 channels of rows x[i][j] at x + i*xs_i + j*xs_j,
 // written contiguously to y[(i*rows_j + j)*128 + c].
