@@ -10,30 +10,39 @@
 // and O^T += V^T P^T (16 more).  With the transposed products, each lane
 // column (lane % 32) holds one query in both results.  The online-softmax row
 // statistics, the P operand and the O rescale therefore all live in the lane
-// that needs them.  The only cross-lane step is one xor-32 exchange of the
-// tile max.
+// that needs them.  The only cross-lane step is an xor-32 exchange of a tile
+// max.
 //
 // Cost model.  On gfx950 an FP32 MFMA and VALU work never overlap, whether
 // they come from one wave or from several waves of a SIMD: a tile costs its
-// 32 x 64 matrix cycles plus every VALU instruction around them.  The loop is
-// therefore built to issue as few VALU instructions per tile as possible:
-//   - In a row with at least one unmasked key, the triangle bias is the
+// 32 x 64 matrix cycles plus every VALU instruction around them, and a
+// v_exp_f32 costs about as much as three other VALU instructions while the
+// matrix cores are busy.  Software pipelining inside a wave buys nothing but
+// load slack, so each tile runs S^T, softmax and O^T += V^T P^T in order, and
+// the loop is built to issue as few VALU instructions as possible.
+//
+// Rows with at least one unmasked key (the fast path):
+//   - q and the triangle bias are pre-scaled by log2(e), and the bias is the
 //     accumulator input of the first S^T MFMA.  It is loaded from a
-//     fragment-major copy straight into registers, so the add costs nothing.
-//     The mask bias is then added only on tiles flagged as masked.  A masked
-//     key of such a row gets weight exactly 0 whatever the rounding of its
-//     logit, because its logit is about -1e9 below the row max.
-//   - A row whose keys are all masked takes the exact path on every tile:
-//     fl(fl(s + mask_bias) + bias), the native order (patches/protenix/
-//     0005-*.patch:36-45; kernels/amd/fireprot_softmax_fp32.cpp:33-35).  Its
-//     logits are quantised to the FP32 spacing of -1e9 (64), and this order
-//     reproduces which keys tie at the max.
-//   - The running max is a lazy reference.  O and l are rescaled only when a
-//     tile's max exceeds it by more than 8 binary orders, so the weights
-//     exp2(x log2e - c) stay below 2^8.  Every weight shares the one rounded
-//     c, and the common factor cancels in O / l.
-//   - The loop is unrolled by two so the S^T accumulators swap roles with no
-//     register copies.
+//     fragment-major copy straight into registers, so the MFMAs emit logits
+//     in log2 units with the bias already added.
+//   - The mask bias is added only on tiles flagged as masked.  A masked key
+//     of such a row gets weight exactly 0 whatever the rounding of its logit,
+//     because its logit is about -1e9 below the row max.
+//   - Weights are exp2(x - c) with one reference c per query, and c = 0
+//     whenever the row max lies within 2^+-56.  Then a tile needs neither a
+//     max nor a subtraction: 16 exp2 and the adds of the row sum.  A tile max
+//     is formed only for the first tile and when the running sum passes
+//     2^64; O and l are then rescaled to the new reference.
+// Rows whose keys are all masked (the exact path):
+//   - Every tile forms fl(fl(s + mask_bias) + bias) in natural units, the
+//     native order (patches/protenix/0005-*.patch:36-45; kernels/amd/
+//     fireprot_softmax_fp32.cpp:33-35), from the unscaled q and an unscaled
+//     bias copy.  These logits are quantised to the FP32 spacing of -1e9 (64),
+//     and this order reproduces which keys tie at the max.  Weights are
+//     exp2(fma(x, log2 e, -c)) with c = fl(m log2 e) of a lazy running max m
+//     (rescaled when a tile max exceeds it by 2^8), so equal logits get equal
+//     weights.
 // A row whose logits are all -inf gives NaN, as torch.softmax does.
 #include "common.hpp"
 #include "kernels.hpp"
@@ -51,10 +60,17 @@ constexpr int kThreads = 256;
 constexpr int kRowGroup = 8;  // outer rows that share a bias slice in L2
 // Occupancy the register budget is set for (waves per SIMD).
 #ifndef FPX_ATTN_WAVES_PER_SIMD
-#define FPX_ATTN_WAVES_PER_SIMD 2
+#define FPX_ATTN_WAVES_PER_SIMD 3
 #endif
-// Rescale threshold in logit units: 8 binary orders of magnitude.
+// Exact path: rescale when a tile max exceeds the reference by 8 binary
+// orders (in logit units).
 constexpr float kRescaleNat = 8.0f * 0.69314718055994531f;
+// Fast path (log2 units): the reference snaps to 0 while the row max lies in
+// [-kSnap, kSnap]; the running sum may grow to kSumLimit before a rescale; a
+// rescale forced by the sum moves the reference up by at least kLift.
+constexpr float kSnap = 56.0f;
+constexpr float kSumLimit = 18446744073709551616.0f;  // 2^64
+constexpr float kLift = 40.0f;
 
 typedef float KTile[kBk][kHeadDim + kPad];  // [key][channel]
 typedef float VTile[kHeadDim][kBk + kPad];  // [channel][key]
@@ -84,21 +100,24 @@ __device__ __forceinline__ f32x4 buffer_f4(__amdgpu_buffer_rsrc_t r, uint32_t vo
 template <int LAYOUT>
 struct Tiles;
 
-// The block's workspace: q, k [B][H][np][32]; v^T [B][H][32][np]; bias in
-// fragment order (bias_frag_index).  Buffer descriptors per work-group, so a
-// tile's address is one scalar offset and the loop spends no VALU on it.
+// The block's workspace: q, k [B][H][np][32]; v^T [B][H][32][np]; the bias in
+// fragment order (bias_frag_index), unscaled and scaled by log2(e).  Buffer
+// descriptors per work-group, so a tile's address is one scalar offset and
+// the loop spends no VALU on it.
 template <>
 struct Tiles<kAttnBlock> {
-  __amdgpu_buffer_rsrc_t rk, rv, rb;
+  __amdgpu_buffer_rsrc_t rk, rv, rb, rb2;
   uint32_t ok, ov, ob;
   __device__ __forceinline__ Tiles(const AttnArgs& a, int b, int h, int qt32, int tid, int lane,
                                    int /*half*/, int /*jq*/) {
     const int64_t bh = (int64_t)b * kHeads + h;
     const int64_t nt = a.np >> 5;
     const int64_t slice = (int64_t)a.np * kHeadDim;
+    const int64_t frag = ((int64_t)h * nt + qt32) * nt * 1024;
     rk = buffer(a.k + bh * slice, slice * 4);
     rv = buffer(a.v + bh * slice, slice * 4);
-    rb = buffer(a.bias + ((int64_t)h * nt + qt32) * nt * 1024, nt * 4096);
+    rb = buffer(a.bias + frag, nt * 4096);
+    rb2 = buffer(a.bias_l2 + frag, nt * 4096);
     const int row8 = tid >> 3;
     const int col4 = (tid & 7) * 4;
     ok = (uint32_t)(row8 * kHeadDim + col4) * 4;
@@ -114,11 +133,13 @@ struct Tiles<kAttnBlock> {
   }
   // The wave's [32 queries x 32 keys] bias fragment of key tile t: one
   // contiguous 4 KB block, four coalesced 1 KB loads.
-  __device__ __forceinline__ f32x16 bias(int t) const {
+  __device__ __forceinline__ f32x16 frag(__amdgpu_buffer_rsrc_t r, int t) const {
     const uint32_t s = (uint32_t)t * 4096;
-    return cat4(buffer_f4(rb, ob, s), buffer_f4(rb, ob + 1024, s), buffer_f4(rb, ob + 2048, s),
-                buffer_f4(rb, ob + 3072, s));
+    return cat4(buffer_f4(r, ob, s), buffer_f4(r, ob + 1024, s), buffer_f4(r, ob + 2048, s),
+                buffer_f4(r, ob + 3072, s));
   }
+  __device__ __forceinline__ f32x16 bias(int t) const { return frag(rb, t); }
+  __device__ __forceinline__ f32x16 bias_l2(int t) const { return frag(rb2, t); }
 };
 
 // The reference C-ABI layout (kernels/amd/fireprot_ck_attention.cpp:34-43):
@@ -158,6 +179,12 @@ struct Tiles<kAttnHeadLast> {
     }
     return cat4(x[0], x[1], x[2], x[3]);
   }
+  __device__ __forceinline__ f32x16 bias_l2(int t) const {
+    f32x16 r = bias(t);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) r[i] *= kLog2e;
+    return r;
+  }
   __device__ __forceinline__ f32x16 mask(int t) const {
     f32x16 r;
 #pragma unroll
@@ -188,6 +215,33 @@ __device__ __forceinline__ float xor32_sum(float v) {
   return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
 }
 
+// NaN-propagating max of 16 values (v_maximum3_f32): a NaN logit poisons its
+// row, as in the native softmax.
+__device__ __forceinline__ float max16(const f32x16& s) {
+  auto mx = [](float x, float y) { return __builtin_elementwise_maximum(x, y); };
+  float m0 = mx(mx(s[0], s[1]), s[2]);
+  float m1 = mx(mx(s[3], s[4]), s[5]);
+  float m2 = mx(mx(s[6], s[7]), s[8]);
+  float m3 = mx(mx(s[9], s[10]), s[11]);
+  float m4 = mx(mx(s[12], s[13]), s[14]);
+  m0 = mx(mx(m0, m1), s[15]);
+  m2 = mx(mx(m2, m3), m4);
+  return mx(m0, m2);
+}
+
+__device__ __forceinline__ float sum16(const f32x16& p) {
+  float a0 = p[0] + p[4], a1 = p[1] + p[5], a2 = p[2] + p[6], a3 = p[3] + p[7];
+  a0 += p[8];
+  a1 += p[9];
+  a2 += p[10];
+  a3 += p[11];
+  a0 += p[12];
+  a1 += p[13];
+  a2 += p[14];
+  a3 += p[15];
+  return (a0 + a1) + (a2 + a3);
+}
+
 // S^T[key][q] = c + sum_ch K[key][ch] Q[q][ch] for the 32 keys of ks; lane
 // half hb supplies channel 16*hb + s at step s.
 __device__ __forceinline__ f32x16 qk_chain(const KTile& ks, const float* qf, int l32, int half,
@@ -205,8 +259,8 @@ __device__ __forceinline__ f32x16 qk_chain(const KTile& ks, const float* qf, int
 }
 
 template <int LAYOUT>
-__global__ __launch_bounds__(kThreads, FPX_ATTN_WAVES_PER_SIMD) void attention_kernel(AttnArgs a, int nqt, int nkt,
-                                                            uint32_t total) {
+__global__ __launch_bounds__(kThreads, FPX_ATTN_WAVES_PER_SIMD) void attention_kernel(
+    AttnArgs a, int nqt, int nkt, uint32_t total) {
   __shared__ __attribute__((aligned(16))) KTile Ks[2];
   __shared__ __attribute__((aligned(16))) VTile Vs[2];
   __shared__ __attribute__((aligned(16))) float Ms[LAYOUT == kAttnBlock ? kMaxKeys : 4];
@@ -310,46 +364,8 @@ __global__ __launch_bounds__(kThreads, FPX_ATTN_WAVES_PER_SIMD) void attention_k
     }
   }
 
-  // Online-softmax state of this lane's query: the reference max m_ref (-inf
-  // until a finite logit appears), the threshold that triggers a rescale, the
-  // rounded log2-domain reference c (0 while m_ref is -inf, so all-(-inf)
-  // tiles give weight exp2(-inf) = 0), and the running sum of the weights.
   f32x16 o = {};
-  float m_ref = -INFINITY;
-  float m_thr = -INFINITY;
-  float c_ref = 0.f;
   float l_run = 0.f;
-
-  auto softmax = [&](f32x16& s) {
-    // NaN-propagating maxima (v_maximum3_f32): a NaN logit poisons its row,
-    // as in the native softmax.
-    auto mx = [](float x, float y) { return __builtin_elementwise_maximum(x, y); };
-    float m0 = mx(mx(s[0], s[1]), s[2]);
-    float m1 = mx(mx(s[3], s[4]), s[5]);
-    float m2 = mx(mx(s[6], s[7]), s[8]);
-    float m3 = mx(mx(s[9], s[10]), s[11]);
-    float m4 = mx(mx(s[12], s[13]), s[14]);
-    m0 = mx(mx(m0, m1), s[15]);
-    m2 = mx(mx(m2, m3), m4);
-    const float mt = xor32_max(mx(m0, m2));
-    if (__any(mt > m_thr)) {
-      const float m_new = mx(m_ref, mt);
-      const float c_new = m_new == -INFINITY ? 0.f : m_new * kLog2e;
-      const float alpha = m_ref == -INFINITY ? 0.f : exp2_fast(c_ref - c_new);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[r] *= alpha;
-      l_run *= alpha;
-      m_ref = m_new;
-      c_ref = c_new;
-      m_thr = m_new + kRescaleNat;
-    }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] = exp2_fast(__builtin_fmaf(s[r], kLog2e, -c_ref));
-    float p[4] = {s[0], s[1], s[2], s[3]};
-#pragma unroll
-    for (int r = 4; r < 16; ++r) p[r & 3] += s[r];
-    l_run += (p[0] + p[1]) + (p[2] + p[3]);
-  };
 
   // O^T[c][q] += V^T[c][key] P^T[key][q]; lane register r of p is key
   // 8*(r/4) + 4*half + r%4, as in the S^T accumulator.
@@ -364,94 +380,145 @@ __global__ __launch_bounds__(kThreads, FPX_ATTN_WAVES_PER_SIMD) void attention_k
     }
   };
 
-  // One pass over the key tiles.  Three register sets rotate through the
-  // roles "S^T of the current tile", "S^T of the next tile" and "bias of the
-  // tile after": a tile's bias is loaded into the registers where its scores
-  // are then accumulated.
-  //   kExact = false: the S^T chain accumulates onto the bias in place, and
-  //     masked tiles add their mask bias afterwards.
-  //   kExact = true: the chain starts from zero into a temporary, and every
-  //     tile forms fl(fl(s + mask) + bias) into the bias registers.
+  // One pass over the key tiles.  Two register sets alternate between even
+  // and odd tiles: a tile's bias is loaded into its set two tiles ahead, the
+  // S^T chain of the tile accumulates there, and the weights go to p.
   auto run = [&](auto exact_tag) {
     constexpr bool kExact = decltype(exact_tag)::value;
     const f32x16 zero16 = {};
-    f32x16 tmp;
-    // S^T of tile t from K in ks, onto set x (which holds bias(t)).
-    auto scores = [&](const KTile& ks, f32x16& x) {
-      if (kExact) {
-        tmp = qk_chain(ks, qf, l32, half, zero16);
-      } else {
-        x = qk_chain(ks, qf, l32, half, x);
-      }
-    };
-    auto finish_scores = [&](f32x16& x, int t) {
-      if (kExact) {
-        const f32x16 mb = mask_vals(t);
+    f32x16 p;
+
+    // Reference state of this lane's query.
+    //   exact: m_ref = lazy running max (logit units), m_thr = the tile max
+    //     that triggers a rescale, c_ref = fl(m_ref log2 e) (0 while m_ref is
+    //     -inf, so all-(-inf) tiles give weight exp2(-inf) = 0).
+    //   fast: m_ref = largest tile max seen on the rare path (log2 units;
+    //     -inf while the query has no reference), c_ref = the reference;
+    //     has_ref / c_zero are wave-uniform.
+    float m_ref = -INFINITY;
+    float m_thr = -INFINITY;
+    float c_ref = 0.f;
+    bool has_ref = false;
+    bool c_zero = true;
+    if (!kExact) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) x[r] = (tmp[r] + mb[r]) + x[r];
-      } else if (masked(t)) {
-        const f32x16 mb = mask_vals(t);
+      for (int i = 0; i < 16; ++i) qf[i] *= kLog2e;
+    }
+
+    // x: this tile's logits (exact: logit units; fast: log2 units) -> p.
+    auto softmax = [&](const f32x16& x) {
+      if (kExact) {
+        const float mt = xor32_max(max16(x));
+        if (__any(mt > m_thr)) {
+          const float m_new = __builtin_elementwise_maximum(m_ref, mt);
+          const float c_new = m_new == -INFINITY ? 0.f : m_new * kLog2e;
+          const float alpha = m_ref == -INFINITY ? 0.f : exp2_fast(c_ref - c_new);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) x[r] += mb[r];
+          for (int r = 0; r < 16; ++r) o[r] *= alpha;
+          l_run *= alpha;
+          m_ref = m_new;
+          c_ref = c_new;
+          m_thr = m_new + kRescaleNat;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[r] = exp2_fast(__builtin_fmaf(x[r], kLog2e, -c_ref));
+        l_run += sum16(p);
+        return;
       }
+      float ovf = 0.f;
+      if (has_ref) {
+        if (c_zero) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) p[r] = exp2_fast(x[r]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) p[r] = exp2_fast(x[r] - c_ref);
+        }
+        const float l_new = l_run + sum16(p);
+        const bool over = !(l_new <= kSumLimit);  // NaN or inf count as overflow
+        if (!__any(over)) {
+          l_run = l_new;
+          return;
+        }
+        ovf = over ? 1.f : 0.f;
+      }
+      // Rare path, taken by the whole wavefront.  A lane moves its reference
+      // only when it has none yet, when its own running sum overflowed, or
+      // when this tile's max lies more than kSnap above the reference; the
+      // decision is shared by the lane pair (l, l ^ 32) that holds the query.
+      // After a sum overflow the true row max is at least c_ref + 52, so the
+      // reference moves up by at least kLift and the weights stay below 2^24.
+      const float mt = xor32_max(max16(x));
+      const bool fresh = m_ref == -INFINITY;
+      const bool need = fresh || xor32_max(ovf) > 0.f || mt > c_ref + kSnap;
+      m_ref = __builtin_elementwise_maximum(m_ref, mt);
+      const float snapped =
+          (m_ref == -INFINITY || (m_ref >= -kSnap && m_ref <= kSnap)) ? 0.f : m_ref;
+      const float c_new = fresh ? snapped
+                          : need ? __builtin_elementwise_maximum(snapped, c_ref + kLift)
+                                 : c_ref;
+      const float alpha = fresh ? 0.f : exp2_fast(c_ref - c_new);  // 1 when unchanged
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[r] *= alpha;
+      l_run *= alpha;
+      c_ref = c_new;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) p[r] = exp2_fast(x[r] - c_ref);
+      l_run += sum16(p);
+      has_ref = __all(m_ref != -INFINITY);
+      c_zero = __all(c_ref == 0.f);
     };
 
-    // Prologue: K(0), K(1), V(0) into LDS; S^T(0); K(2) and V(1) in flight.
-    f32x4 kreg = io.k(0);
-    f32x4 vreg = io.v(0);
-    const f32x4 k1 = io.k(last < 1 ? last : 1);
-    f32x16 set_a = io.bias(0);
-    f32x16 set_b = io.bias(last < 1 ? last : 1);
-    f32x16 set_c;
-    *(f32x4*)&Ks[0][row8][col4] = kreg;
-    *(f32x4*)&Ks[1][row8][col4] = k1;
-    Tiles<LAYOUT>::store_v(Vs[0], vreg, row8, col4);
+    auto bias_of = [&](int t) -> f32x16 { return kExact ? io.bias(t) : io.bias_l2(t); };
+
+    // Prologue: K(0), V(0) into LDS; K(1), V(1) and the biases of tiles 0
+    // and 1 in flight.
+    f32x16 set_a = bias_of(0);
+    f32x16 set_b = bias_of(last < 1 ? last : 1);
+    {
+      const f32x4 k0 = io.k(0);
+      const f32x4 v0 = io.v(0);
+      *(f32x4*)&Ks[0][row8][col4] = k0;
+      Tiles<LAYOUT>::store_v(Vs[0], v0, row8, col4);
+    }
+    f32x4 kreg = io.k(last < 1 ? last : 1);
+    f32x4 vreg = io.v(last < 1 ? last : 1);
     __syncthreads();
-    scores(Ks[0], set_a);
-    finish_scores(set_a, 0);
-    kreg = io.k(last < 2 ? last : 2);
-    vreg = io.v(last < 1 ? last : 1);
-    __syncthreads();  // every wave is done with K(0) before Ks[0] is refilled
 
-    // Iteration kt starts with: Ks[(kt+1)&1] = K(kt+1), Vs[kt&1] = V(kt),
-    // kreg = K(kt+2), vreg = V(kt+1) (loads in flight), cur = S^T(kt) with
-    // its biases, nxt = bias(kt+1); far is free.  Tile indices past the last
+    // Tile kt: Ks/Vs[kt&1] hold K(kt), V(kt); x holds bias(kt); kreg/vreg
+    // hold K(kt+1), V(kt+1) (loads in flight).  Indices past the last tile
     // are clamped (in range, never used).
-    auto body = [&](int kt, f32x16& cur, f32x16& nxt, f32x16& far) {
-      const int t2 = kt + 2 < last ? kt + 2 : last;
-      const int t3 = kt + 3 < last ? kt + 3 : last;
-      far = io.bias(t2);
-      scores(Ks[(kt + 1) & 1], nxt);
-      softmax(cur);
-      pv(Vs[kt & 1], cur);
-      finish_scores(nxt, kt + 1);
-      *(f32x4*)&Ks[kt & 1][row8][col4] = kreg;
-      Tiles<LAYOUT>::store_v(Vs[(kt + 1) & 1], vreg, row8, col4);
-      kreg = io.k(t3);
-      vreg = io.v(t2);
+    auto body = [&](int kt, f32x16& x) {
+      const int par = kt & 1;
+      if (kExact) {
+        p = qk_chain(Ks[par], qf, l32, half, zero16);
+        const f32x16 mb = mask_vals(kt);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[r] = (p[r] + mb[r]) + x[r];
+      } else {
+        x = qk_chain(Ks[par], qf, l32, half, x);
+        if (masked(kt)) {
+          const f32x16 mb = mask_vals(kt);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) x[r] += mb[r];
+        }
+      }
+      softmax(x);
+      x = bias_of(kt + 2 < last ? kt + 2 : last);
+      pv(Vs[par], p);
+      *(f32x4*)&Ks[par ^ 1][row8][col4] = kreg;
+      Tiles<LAYOUT>::store_v(Vs[par ^ 1], vreg, row8, col4);
+      kreg = io.k(kt + 2 < last ? kt + 2 : last);
+      vreg = io.v(kt + 2 < last ? kt + 2 : last);
       __syncthreads();
-    };
-    auto tail = [&](f32x16& cur, int kt) {
-      softmax(cur);
-      pv(Vs[kt & 1], cur);
     };
 
     int kt = 0;
-    for (; kt + 3 < nkt; kt += 3) {
-      body(kt, set_a, set_b, set_c);
-      body(kt + 1, set_b, set_c, set_a);
-      body(kt + 2, set_c, set_a, set_b);
+    for (; kt + 1 < nkt; kt += 2) {
+      body(kt, set_a);
+      body(kt + 1, set_b);
     }
-    if (kt + 1 == nkt) {
-      tail(set_a, kt);
-    } else if (kt + 2 == nkt) {
-      body(kt, set_a, set_b, set_c);
-      tail(set_b, kt + 1);
-    } else {
-      body(kt, set_a, set_b, set_c);
-      body(kt + 1, set_b, set_c, set_a);
-      tail(set_c, kt + 2);
-    }
+    if (kt < nkt) body(kt, set_a);
   };
   if (has_unmasked) {
     run(std::false_type{});
@@ -489,7 +556,8 @@ hipError_t launch_attention(int layout, const AttnArgs& a, hipStream_t stream) {
   if (total == 0) return hipSuccess;
   if (total > 0x7fffffffull) return hipErrorInvalidValue;
   if (layout == kAttnBlock) {
-    if (a.tile_flags == nullptr || nkt > kTileFlagWords * 32) return hipErrorInvalidValue;
+    if (a.tile_flags == nullptr || a.bias_l2 == nullptr || nkt > kTileFlagWords * 32)
+      return hipErrorInvalidValue;
     hipLaunchKernelGGL(attention_kernel<kAttnBlock>, dim3((uint32_t)total), dim3(kThreads), 0,
                        stream, a, nqt, nkt, (uint32_t)total);
   } else {

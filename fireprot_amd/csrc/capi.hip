@@ -30,7 +30,8 @@ size_t elem_bytes(int dtype) { return dtype == FPX_BF16 ? 2 : 4; }
 // Workspace segments of the block, all 256-byte aligned, element size e
 // (4 for FPX_F32, 2 for FPX_BF16; the mask bias is always float):
 //   qh, kh [n][4][np][32]; vt [n][4][32][np]; gs, og [n][n][128];
-//   tri_bias [4][np][np] (FP32: fragment order); mbias [n][np] float;
+//   tri_bias [4][np][np] (FP32: fragment order, twice: as is and scaled by
+//   log2(e)); mbias [n][np] float;
 //   tile flags [n][2 * kTileFlagWords] uint32
 struct BlockWorkspace {
   size_t qh, kh, vt, gs, og, bias, mbias, flags, total;
@@ -42,7 +43,7 @@ BlockWorkspace block_workspace(int n, int dtype) {
   auto seg = [](size_t bytes) { return (size_t)round_up((int64_t)bytes, 256); };
   const size_t qkv = seg((size_t)n * fpx::kHeads * np * fpx::kHeadDim * e);
   const size_t g = seg((size_t)n * n * fpx::kHidden * e);
-  const size_t bias = seg((size_t)fpx::kHeads * np * np * e);
+  const size_t bias = seg((size_t)fpx::kHeads * np * np * e * (dtype == FPX_F32 ? 2 : 1));
   const size_t mb = seg((size_t)n * np * sizeof(float));
   const size_t fl = seg((size_t)n * 2 * fpx::kTileFlagWords * sizeof(uint32_t));
   BlockWorkspace w{};
@@ -187,6 +188,7 @@ int fpx_tri_attn_prepare(int dtype, const void* z, int64_t z_stride0, int64_t z_
   p.vt = as<float>(w.vt);
   p.gs = as<float>(w.gs);
   p.tri_bias = as<float>(w.tri);
+  p.tri_bias_l2 = as<float>(w.tri) + (size_t)fpx::kHeads * w.np * w.np;
   p.np = w.np;
   return status(fpx::launch_projection(fpx::kProjBlock, p, s));
 }
@@ -217,6 +219,7 @@ int fpx_tri_attn_attend(int dtype, int n, void* workspace, size_t workspace_byte
   a.mbias = w.mbias;
   a.mb_stride = w.np;
   a.bias = as<float>(w.tri);
+  a.bias_l2 = as<float>(w.tri) + (size_t)fpx::kHeads * w.np * w.np;
   a.bias_stride = w.np;
   a.bias_rows = w.np;
   a.gate = as<float>(w.gs);

@@ -128,11 +128,16 @@ hipError_t launch_mask_bias(const float* mask, int64_t ms_i, int64_t ms_j, int n
   if (bias_bf16) {
     hipLaunchKernelGGL((bias_pad_kernel<__bf16, false>), dim3((uint32_t)blocks), dim3(256), 0,
                        stream, n, np, static_cast<__bf16*>(tri_bias));
-  } else {
-    hipLaunchKernelGGL((bias_pad_kernel<float, true>), dim3((uint32_t)blocks), dim3(256), 0,
-                       stream, n, np, static_cast<float*>(tri_bias));
+    return hipGetLastError();
   }
-  return hipGetLastError();
+  float* copy = static_cast<float*>(tri_bias);
+  for (int c = 0; c < 2; ++c) {
+    hipLaunchKernelGGL((bias_pad_kernel<float, true>), dim3((uint32_t)blocks), dim3(256), 0,
+                       stream, n, np, copy + (int64_t)c * kHeads * np * np);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t launch_layer_norm(const float* x, int64_t rows_i, int64_t rows_j, int64_t xs_i,

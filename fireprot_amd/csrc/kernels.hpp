@@ -20,6 +20,7 @@ namespace fpx {
 //                        key of 32-key tile t has a nonzero mask bias; of
 //                        part 1 = every key of tile t has one
 //                bias : [H][np][np] in fragment order (bias_frag_index)
+//                bias_l2: the same scaled by log2(e)
 //                gate : [B][n][128] sigmoid(g), multiplied in the epilogue
 //                out  : [B][n][128]      (o * gate, head-last)
 // kAttnHeadLast: the reference C-ABI layout (fireprot_ck_attention.cpp:34-43):
@@ -38,6 +39,7 @@ struct AttnArgs {
   const float* mbias;
   int64_t mb_stride;
   const float* bias;
+  const float* bias_l2;  // kAttnBlock only
   int64_t bias_stride;
   int64_t bias_rows;
   const float* gate;
@@ -79,7 +81,8 @@ struct ProjArgs {
   float* kh;
   float* vt;
   float* gs;
-  float* tri_bias;
+  float* tri_bias;     // fragment order (bias_frag_index)
+  float* tri_bias_l2;  // the same scaled by log2(e)
   int np;
   // kProjQkv / kProjOut outputs
   float* out;
@@ -92,8 +95,9 @@ hipError_t launch_projection(int mode, const ProjArgs& args, hipStream_t stream)
 // -------------------------------------------------------------- elementwise
 // mbias[i][k] = k < n ? inf * (mask_x[i][k] - 1) : -inf  (0 for k < n when
 // mask is null), the per-row tile flags of the attention kernel, and zero
-// rows [n, np) of every head of the triangle bias: float in fragment order
-// (bias_frag_index), or row-major bf16 when bias_bf16.
+// rows [n, np) of every head of the triangle bias: both float copies in
+// fragment order (bias_frag_index, unscaled then log2(e)-scaled, contiguous),
+// or the one row-major bf16 copy when bias_bf16.
 hipError_t launch_mask_bias(const float* mask, int64_t ms_i, int64_t ms_j, int n, int np,
                             float inf, float* mbias, uint32_t* tile_flags, void* tri_bias,
                             bool bias_bf16, hipStream_t stream);

@@ -10,8 +10,8 @@
 // register-level reductions per row on pivot-shifted values: mean, then the
 // biased variance of the centred values) and the triangle-bias projection
 // (4 wave reductions per row), and writes q (scaled by 1/sqrt(32)), k, v^T,
-// sigmoid(g) and the bias (fragment order, bias_frag_index) straight into the
-// layouts the attention kernel reads.  The row addressing
+// sigmoid(g) and the bias (fragment order, bias_frag_index; once as is and once
+// scaled by log2(e)) straight into the layouts the attention kernel reads.  The row addressing
 // x + i*xs_i + j*xs_j makes the ending-node read of z^T free of copies.
 #include "common.hpp"
 #include "kernels.hpp"
@@ -140,7 +140,9 @@ __global__ __launch_bounds__(ProjTraits<MODE>::kWaves * 64) void projection_kern
           for (int h = 0; h < kHeads; ++h) p[h] = wave_sum(y0 * wb[h][0] + y1 * wb[h][1]);
           if (lane < kHeads) {
             const float v = lane == 0 ? p[0] : lane == 1 ? p[1] : lane == 2 ? p[2] : p[3];
-            a.tri_bias[bias_frag_index(lane, i, j, a.np)] = valid ? v : 0.f;
+            const int64_t at = bias_frag_index(lane, i, j, a.np);
+            a.tri_bias[at] = valid ? v : 0.f;
+            a.tri_bias_l2[at] = valid ? v * kLog2e : 0.f;
           }
         }
       }

@@ -112,6 +112,18 @@ def test_long_configs_row_subset_and_transpose_identity(key):
     assert_f32_parity(f"{cfg.name} end rows", end_rows, exp_end)
 
 
+@pytest.mark.parametrize("ending", [False, True])
+def test_block_large_bias_scale(ending):
+    """Triangle-bias weights x60: logits of a few hundred, far outside the
+    range where the kernel's softmax reference stays at 0."""
+    n = 200
+    z = workloads.make_pair(n)
+    w = workloads.make_weights(bias_scale=60.0)
+    actual = _run(z, None, w, ending)
+    expected = oracle.block(z, None, oracle_params(w), ending=ending)
+    assert_f32_parity(f"bias x60 ending={ending}", actual, expected)
+
+
 def test_block_inputs_unchanged_streams_and_queue():
     n = 96
     z, mask, w = workloads.make_pair(n), workloads.make_mask(n, 80), workloads.make_weights()

@@ -89,6 +89,34 @@ def test_core_extreme_bias_rows_and_inputs_unchanged():
         assert torch.equal(t, before)
 
 
+def test_core_reference_regimes():
+    """Rows that drive every branch of the kernel's softmax reference: a large
+    positive and a large negative row max (reference away from 0), a row
+    whose running sum passes 2^64 without any single weight doing so, a late
+    +200 key, and leading -inf tiles, side by side in one wavefront."""
+    batch, n = 2, 1000
+    q, k, v, biases = _inputs(batch, n, 31)
+    g = torch.Generator().manual_seed(32)
+    bias = biases[0].clone()
+    noise = torch.randn(4, n, generator=g)
+    bias[0, :, 0, :] = 300.0 + noise          # log2 logits ~433: reference c = max
+    bias[0, :, 1, :32] = 30.0                  # first tile ~43 (log2): c snaps to 0 ...
+    bias[0, :, 1, 32:] = 38.5                  # ... then 968 keys at ~55.5 push the sum past 2^64
+    bias[0, :, 2, :] = noise
+    bias[0, :, 2, 700] = 200.0                 # a late dominant key
+    bias[0, :, 3, :] = -300.0 + noise          # large negative row
+    bias[0, :, 4, :96] = float("-inf")         # three leading -inf tiles
+    bias[0, :, 33, :] = 150.0 + noise          # second wavefront: large row
+    biases = [bias]
+    expected = _expected(q, k, v, biases)
+    assert torch.isfinite(expected).all()
+    qc, kc, vc, bc = _cuda(q, k, v, biases)
+    with torch.inference_mode():
+        out = ta.attention(module=None, q=qc, k=kc, v=vc, biases=bc, native=None)
+        torch.cuda.synchronize()
+    assert_f32_parity("reference regimes", out.cpu(), expected)
+
+
 def test_core_c_abi_guards_and_canaries():
     lib = _native.library()
     # invalid sizes are rejected before any pointer is dereferenced
