@@ -534,9 +534,9 @@ __global__ __launch_bounds__(kThreads, FPX_ATTN_WAVES_PER_SIMD) void attention_k
       f32x4 ov = {o[4 * rr + 0] / l_tot, o[4 * rr + 1] / l_tot, o[4 * rr + 2] / l_tot,
                   o[4 * rr + 3] / l_tot};
       if (LAYOUT == kAttnBlock) {
-        const int64_t off = ((int64_t)b * a.n + jq) * kHidden + h * kHeadDim + c;
-        if (a.gate) ov = ov * *(const f32x4*)(a.gate + off);
-        *(f32x4*)(a.out + off) = ov;
+        const int64_t col = h * kHeadDim + c;
+        if (a.gate) ov = ov * *(const f32x4*)(a.gate + ((int64_t)b * a.np + jq) * kHidden + col);
+        *(f32x4*)(a.out + ((int64_t)b * a.n + jq) * kHidden + col) = ov;
       } else {
         *(f32x4*)(a.out + (((int64_t)b * a.n + jq) * kHeads + h) * kHeadDim + c) = ov;
       }

@@ -39,10 +39,28 @@ __device__ __forceinline__ int mfma_row(int r, int half) {
   return 8 * (r >> 2) + 4 * half + (r & 3);
 }
 
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, false));
+}
+
+// Sum over the 64 lanes, returned in every lane, with no LDS traffic: DPP
+// adds across lane pairs, quads, 8 and 16 lanes (quad_perm [1,0,3,2] and
+// [2,3,0,1], row_half_mirror, row_mirror), then v_permlane16_swap and
+// v_permlane32_swap across rows.  Every lane adds the same two partial sums,
+// so all lanes hold the identical value.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  v += dpp<0x140>(v);
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v),
+                                                  __builtin_bit_cast(unsigned, v), false, false);
+  v = __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+  const auto s = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v),
+                                                  __builtin_bit_cast(unsigned, v), false, false);
+  return __builtin_bit_cast(float, (unsigned)s[0]) + __builtin_bit_cast(float, (unsigned)s[1]);
 }
 
 // Two-pass LayerNorm statistics of a 128-channel row held as two values per
@@ -60,15 +78,17 @@ __device__ __forceinline__ void ln_stats_c128(float a, float b, float eps, float
   da = sa - mean_s;
   db = sb - mean_s;
   const float var = wave_sum(da * da + db * db) * (1.0f / kChannels);
-  rstd = 1.0f / sqrtf(var + eps);
+  rstd = __builtin_amdgcn_rsqf(var + eps);  // v_rsq_f32, within 1 ulp
 }
 
 __device__ __forceinline__ float exp2_fast(float x) {
   return __builtin_amdgcn_exp2f(x);
 }
 
+// 1 / (1 + e^-x) with v_exp_f32 and v_rcp_f32 (within 1 ulp each); the
+// limits are exact: 1 / inf = 0 and 1 / 1 = 1.
 __device__ __forceinline__ float sigmoidf_(float x) {
-  return 1.0f / (1.0f + __expf(-x));
+  return __builtin_amdgcn_rcpf(1.0f + __expf(-x));
 }
 
 // Work-groups are dispatched round-robin over the XCDs: hardware block b runs

@@ -21,7 +21,7 @@ namespace fpx {
 //                        part 1 = every key of tile t has one
 //                bias : [H][np][np] in fragment order (bias_frag_index)
 //                bias_l2: the same scaled by log2(e)
-//                gate : [B][n][128] sigmoid(g), multiplied in the epilogue
+//                gate : [B][np][128] sigmoid(g), multiplied in the epilogue
 //                out  : [B][n][128]      (o * gate, head-last)
 // kAttnHeadLast: the reference C-ABI layout (fireprot_ck_attention.cpp:34-43):
 //                q, k, v, out : [B][n][H][32] (strides n*128, 32, 128, 1)
