@@ -19,6 +19,7 @@
 #include "kernels.hpp"
 
 #include <cmath>
+#include <type_traits>
 
 namespace fpx {
 namespace {
@@ -152,7 +153,7 @@ __global__ __launch_bounds__(Bf16ProjTraits<MODE>::kWaves * 64) void projection_
           for (int h = 0; h < kHeads; ++h) p[h] = wave_sum(r0 * wb[h][0] + r1 * wb[h][1]);
           if (lane < kHeads) {
             const float v = lane == 0 ? p[0] : lane == 1 ? p[1] : lane == 2 ? p[2] : p[3];
-            a.tri_bias[((int64_t)lane * a.np + i) * a.np + j] = (__bf16)(valid ? v : 0.f);
+            a.tri_bias[bias_frag_index_bf16(lane, i, j, a.np)] = (__bf16)(valid ? v : 0.f);
           }
         }
       }
@@ -223,56 +224,88 @@ hipError_t launch_proj_mode(const Bf16ProjArgs& a, hipStream_t stream, int wgs_p
 }
 
 // ------------------------------------------------------------------- attention
+//
+// Same work-group shape and order as the FP32 kernel: (outer row b, head h,
+// 128 queries), four waves of 32 queries, 32-key tiles, K and V^T
+// double-buffered in LDS, one barrier per tile.  BF16 matrix instructions run
+// beside VALU work on gfx950, so the S^T MFMAs of the next tile are issued
+// before the softmax of this one, and the kernel is bound by its VALU work,
+// which v_exp_f32 (quarter rate, about 8 cycles per wave) dominates.  Per tile
+// a wave issues 6 MFMAs and about 67 VALU instructions:
+//   - The triangle bias (bf16, fragment-major) enters the S^T accumulator
+//     through two MFMAs with an identity A operand: I * Bias^T adds each bf16
+//     bias value exactly, with no conversion instructions.
+//   - Softmax: lazy running max (a rescale when a tile max exceeds it by
+//     2^8), p = exp2(fma(x, log2 e, -c)) with one rounded c per query, P
+//     packed to bf16 with v_cvt_pk_bf16_f32.  The row sum l adds the FP32
+//     weights (their bf16 roundings are unbiased, so O / l stays a weighted
+//     mean to well within the bf16 bar).
+// Rows whose keys are all masked form fl(fl(s + mask_bias) + bias) in FP32
+// in that order (the identity MFMAs add the bias last); other rows start the
+// accumulator from the bias and add the mask bias only on masked tiles.
 
 constexpr int kBq = 128;
 constexpr int kBk = 32;
-constexpr int kLdsPad = 8;        // bf16 elements: rows of 80 bytes
+constexpr int kRowB = kHeadDim + 8;  // bf16 per LDS row: 80 bytes, conflict-free b128 reads
 constexpr int kThreads = 256;
 constexpr int kRowGroup = 8;
+constexpr int kMaxKeysB = kTileFlagWords * 32 * kBk;
+constexpr float kRescaleNatB = 8.0f * 0.69314718055994531f;
 
-struct Bf16Tile {
-  bf16x4 v;
-  bf16x4 b[4];
-  f32x4 m;
-};
+typedef __bf16 KTileB[kBk][kRowB];      // [key][channel]
+typedef __bf16 VTileB[kHeadDim][kRowB];  // [channel][key position], see kVPos
 
-__device__ __forceinline__ bf16x4 load_k_bf16(const Bf16AttnArgs& a, int b, int h, int k0, int tid) {
-  const int64_t bh = (int64_t)b * kHeads + h;
-  return *(const bf16x4*)(a.k + (bh * a.np + k0 + (tid >> 3)) * kHeadDim + (tid & 7) * 4);
+// V^T keys are stored in the order in which the S^T accumulator registers
+// hold them: within each 16-key block, keys 0-3, 8-11, 4-7, 12-15.  Position
+// of the 4-key group g (keys 4g..4g+3) of a tile:
+__device__ __forceinline__ int v_position(int g) {
+  const int perm = (g & 1) * 2 + ((g >> 1) & 1);  // 0, 2, 1, 3
+  return (g >> 2) * 16 + perm * 4;
 }
 
-__device__ __forceinline__ void load_vbm_bf16(const Bf16AttnArgs& a, int b, int h, int j0, int k0,
-                                              int tid, Bf16Tile& t) {
-  const int row8 = tid >> 3;
-  const int col4 = (tid & 7) * 4;
-  const int64_t bh = (int64_t)b * kHeads + h;
-  t.v = *(const bf16x4*)(a.v + (bh * kHeadDim + row8) * a.np + k0 + col4);
-#pragma unroll
-  for (int m = 0; m < 4; ++m)
-    t.b[m] = *(const bf16x4*)(a.bias + ((int64_t)h * a.np + j0 + row8 + 32 * m) * a.np + k0 + col4);
-  if (tid < 8) t.m = *(const f32x4*)(a.mbias + (int64_t)b * a.np + k0 + 4 * tid);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_b(const __bf16* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<__bf16*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ bf16x4 buffer_b64(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+}
+__device__ __forceinline__ bf16x8 buffer_b128(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                              uint32_t soff) {
+  return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
 __device__ __forceinline__ float xor32_max_bf(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v),
                                                   __builtin_bit_cast(unsigned, v), false, false);
-  return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
-}
-__device__ __forceinline__ float xor32_sum_bf(float v) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v),
-                                                  __builtin_bit_cast(unsigned, v), false, false);
-  return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+  return __builtin_elementwise_maximum(__builtin_bit_cast(float, (unsigned)r[0]),
+                                       __builtin_bit_cast(float, (unsigned)r[1]));
 }
 
-// One work-group = (outer row b, head h, 128 queries), four waves of 32
-// queries, 32-key tiles; the order of work-groups and the online softmax
-// (shared log2 reference, exp2(fma)) are those of the FP32 attention kernel.
-__global__ __launch_bounds__(kThreads) void attention_bf16_kernel(Bf16AttnArgs a, int nqt, int nkt,
-                                                                  uint32_t total) {
-  __shared__ __attribute__((aligned(16))) __bf16 Ks[kBk][kHeadDim + kLdsPad];   // [key][channel]
-  __shared__ __attribute__((aligned(16))) __bf16 Vs[kHeadDim][kBk + kLdsPad];   // [channel][key]
-  __shared__ __attribute__((aligned(16))) __bf16 Bs[kBq][kBk + kLdsPad];        // [query][key]
-  __shared__ __attribute__((aligned(16))) float Ms[kBk];
+__device__ __forceinline__ float max16_bf(const f32x16& s) {
+  auto mx = [](float x, float y) { return __builtin_elementwise_maximum(x, y); };
+  float m0 = mx(mx(s[0], s[1]), s[2]);
+  float m1 = mx(mx(s[3], s[4]), s[5]);
+  float m2 = mx(mx(s[6], s[7]), s[8]);
+  float m3 = mx(mx(s[9], s[10]), s[11]);
+  float m4 = mx(mx(s[12], s[13]), s[14]);
+  m0 = mx(mx(m0, m1), s[15]);
+  m2 = mx(mx(m2, m3), m4);
+  return mx(m0, m2);
+}
+
+__device__ __forceinline__ bf16x8 pack8(const f32x16& p, int m) {
+  typedef float f32x8 __attribute__((ext_vector_type(8)));
+  const f32x8 v = {p[8 * m + 0], p[8 * m + 1], p[8 * m + 2], p[8 * m + 3],
+                   p[8 * m + 4], p[8 * m + 5], p[8 * m + 6], p[8 * m + 7]};
+  return __builtin_convertvector(v, bf16x8);  // v_cvt_pk_bf16_f32, round to nearest even
+}
+
+__global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArgs a, int nqt,
+                                                                     int nkt, uint32_t total) {
+  __shared__ __attribute__((aligned(16))) KTileB Ks[2];
+  __shared__ __attribute__((aligned(16))) VTileB Vs[2];
+  __shared__ __attribute__((aligned(16))) float Ms[kMaxKeysB];
 
   const uint32_t logical = xcd_remap(blockIdx.x, total);
   const int groups = (a.batch + kRowGroup - 1) / kRowGroup;
@@ -286,104 +319,213 @@ __global__ __launch_bounds__(kThreads) void attention_bf16_kernel(Bf16AttnArgs a
   if (b >= a.batch) return;  // padding of the last row group; uniform per work-group
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5;
   const int l32 = lane & 31;
   const int j0 = qt * kBq;
   const int jq = j0 + 32 * w + l32;
+  const int qt32 = (j0 >> 5) + w;
+  const int row8 = tid >> 3;
+  const int col4 = (tid & 7) * 4;
+  const int last = nkt - 1;
 
-  // Q^T operand: lane holds Q[jq][16*m + 8*half + e].
+  // Per-work-group buffer descriptors: K [np][32], V^T [32][np] of (b, h);
+  // the wave's bias fragments (h, qt32, all key tiles), 2 KB each.
+  const int64_t bh = (int64_t)b * kHeads + h;
+  const int64_t slice = (int64_t)a.np * kHeadDim;
+  const int64_t nt = a.np >> 5;
+  const __amdgpu_buffer_rsrc_t rk = buffer_b(a.k + bh * slice, slice * 2);
+  const __amdgpu_buffer_rsrc_t rv = buffer_b(a.v + bh * slice, slice * 2);
+  const __amdgpu_buffer_rsrc_t rb = buffer_b(a.bias + ((int64_t)h * nt + qt32) * nt * 1024, nt * 2048);
+  const uint32_t ok = (uint32_t)(row8 * kHeadDim + col4) * 2;
+  const uint32_t ov = (uint32_t)(row8 * a.np + col4) * 2;
+  const uint32_t ob = (uint32_t)lane * 16;
+  auto load_k = [&](int t) { return buffer_b64(rk, ok, (uint32_t)t * 2048); };
+  auto load_v = [&](int t) { return buffer_b64(rv, ov, (uint32_t)t * 64); };
+  struct BiasFrag {
+    bf16x8 m0, m1;
+  };
+  auto load_bias = [&](int t) {
+    return BiasFrag{buffer_b128(rb, ob, (uint32_t)t * 2048),
+                    buffer_b128(rb, ob + 1024, (uint32_t)t * 2048)};
+  };
+  const int vpos = v_position(col4 >> 2);
+  auto store_kv = [&](int buf, bf16x4 k, bf16x4 v) {
+    *(bf16x4*)&Ks[buf][row8][col4] = k;
+    *(bf16x4*)&Vs[buf][row8][vpos] = v;
+  };
+
+  // Row classification, as in the FP32 kernel.
+  uint32_t mw[kTileFlagWords];
+  uint32_t any = 0u, open = 0u;
+  {
+    const uint32_t* f = a.tile_flags + (int64_t)b * 2 * kTileFlagWords;
+#pragma unroll
+    for (int i = 0; i < kTileFlagWords; ++i) {
+      const int lo = 32 * i;
+      const uint32_t valid = nkt >= lo + 32 ? 0xffffffffu : nkt > lo ? (1u << (nkt - lo)) - 1u : 0u;
+      mw[i] = f[i];
+      any |= mw[i] & valid;
+      open |= ~f[kTileFlagWords + i] & valid;
+    }
+  }
+  const bool has_unmasked = open != 0u;
+  auto masked = [&](int t) -> bool {
+    const uint32_t word = t < 32 ? mw[0] : t < 64 ? mw[1] : t < 96 ? mw[2] : mw[3];
+    return (word >> (t & 31)) & 1u;
+  };
+  if (any != 0u) {
+    const float* src = a.mbias + (int64_t)b * a.np;
+    for (int k = 4 * tid; k < nkt * kBk; k += 4 * kThreads) *(f32x4*)&Ms[k] = *(const f32x4*)(src + k);
+  }
+  auto add_mask = [&](f32x16& x, int t) {
+    const float* m = &Ms[t * kBk + 4 * half];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const f32x4 mb = *(const f32x4*)(m + 8 * rr);
+      x[4 * rr + 0] += mb.x;
+      x[4 * rr + 1] += mb.y;
+      x[4 * rr + 2] += mb.z;
+      x[4 * rr + 3] += mb.w;
+    }
+  };
+
+  // Constant operands: Q (B of S^T, lane holds Q[jq][16m + 8half + e]) and the
+  // identity (A of the bias MFMAs: key l32 against key 16m + 8half + e).
   bf16x8 qf[2];
   {
-    const __bf16* src = a.q + (((int64_t)b * kHeads + h) * a.np + jq) * kHeadDim + 8 * half;
+    const __bf16* src = a.q + (bh * a.np + jq) * kHeadDim + 8 * half;
     qf[0] = *(const bf16x8*)(src);
     qf[1] = *(const bf16x8*)(src + 16);
   }
+  bf16x8 eye[2];
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) eye[m][e] = (__bf16)(l32 == 16 * m + 8 * half + e ? 1.0f : 0.0f);
 
   f32x16 o = {};
-  float c_run = -INFINITY;
   float l_run = 0.f;
-  const int row8 = tid >> 3;
-  const int col4 = (tid & 7) * 4;
-  Bf16Tile regs;
+  float m_ref = -INFINITY, m_thr = -INFINITY, c_ref = 0.f;
 
-  auto qk = [&]() {
-    f32x16 s = {};
-    s = mfma_bf16(*(const bf16x8*)&Ks[l32][8 * half], qf[0], s);
-    s = mfma_bf16(*(const bf16x8*)&Ks[l32][16 + 8 * half], qf[1], s);
-    return s;
-  };
-  auto store_vbm = [&]() {
-    *(bf16x4*)&Vs[row8][col4] = regs.v;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) *(bf16x4*)&Bs[row8 + 32 * m][col4] = regs.b[m];
-    if (tid < 8) *(f32x4*)&Ms[4 * tid] = regs.m;
-  };
-  auto softmax_pv = [&](f32x16 s) {
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const f32x4 mb = *(const f32x4*)&Ms[8 * rr + 4 * half];
-      const bf16x4 bb = *(const bf16x4*)&Bs[32 * w + l32][8 * rr + 4 * half];
-      s[4 * rr + 0] = (s[4 * rr + 0] + mb.x) + (float)bb.x;
-      s[4 * rr + 1] = (s[4 * rr + 1] + mb.y) + (float)bb.y;
-      s[4 * rr + 2] = (s[4 * rr + 2] + mb.z) + (float)bb.z;
-      s[4 * rr + 3] = (s[4 * rr + 3] + mb.w) + (float)bb.w;
-    }
-    float mt = s[0];
-#pragma unroll
-    for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
-    mt = xor32_max_bf(mt);
-    const float c_new = mt == -INFINITY ? c_run : fmaxf(c_run, mt * kLog2e);
-    const float c_use = c_new == -INFINITY ? 0.f : c_new;
-    const float alpha = exp2_fast(c_run - c_use);
-    if (__any(alpha != 1.0f)) {
+  auto softmax = [&](const f32x16& x, bf16x8& p0, bf16x8& p1) {
+    const float mt = xor32_max_bf(max16_bf(x));
+    if (__any(mt > m_thr)) {
+      const float m_new = __builtin_elementwise_maximum(m_ref, mt);
+      const float c_new = m_new == -INFINITY ? 0.f : m_new * kLog2e;
+      const float alpha = m_ref == -INFINITY ? 0.f : exp2_fast(c_ref - c_new);
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[r] *= alpha;
+      l_run *= alpha;
+      m_ref = m_new;
+      c_ref = c_new;
+      m_thr = m_new + kRescaleNatB;
     }
-    l_run *= alpha;
-    c_run = c_new;
-    // P in bf16, summed as rounded so O / l is a proper weighted mean.
-    bf16x8 pm[2];
-    float psum = 0.f;
+    f32x16 p;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const __bf16 pb = (__bf16)exp2_fast(__builtin_fmaf(s[r], kLog2e, -c_use));
-      pm[r >> 3][r & 7] = pb;
-      psum += (float)pb;
-    }
-    l_run += psum;
+    for (int r = 0; r < 16; ++r) p[r] = exp2_fast(__builtin_fmaf(x[r], kLog2e, -c_ref));
+    float s4[4] = {p[0], p[1], p[2], p[3]};
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const bf16x4 lo = *(const bf16x4*)&Vs[l32][16 * m + 4 * half];
-      const bf16x4 hi = *(const bf16x4*)&Vs[l32][16 * m + 8 + 4 * half];
-      const bf16x8 va = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-      o = mfma_bf16(va, pm[m], o);
-    }
+    for (int r = 4; r < 16; ++r) s4[r & 3] += p[r];
+    l_run += (s4[0] + s4[1]) + (s4[2] + s4[3]);
+    p0 = pack8(p, 0);
+    p1 = pack8(p, 1);
   };
 
-  *(bf16x4*)&Ks[row8][col4] = load_k_bf16(a, b, h, 0, tid);
-  __syncthreads();
-  f32x16 s_cur = qk();
-  bf16x4 kreg = {};
-  if (nkt > 1) kreg = load_k_bf16(a, b, h, kBk, tid);
-  load_vbm_bf16(a, b, h, j0, 0, tid, regs);
-  for (int kt = 0; kt + 1 < nkt; ++kt) {
-    __syncthreads();
-    *(bf16x4*)&Ks[row8][col4] = kreg;
-    store_vbm();
-    __syncthreads();
-    if (kt + 2 < nkt) kreg = load_k_bf16(a, b, h, (kt + 2) * kBk, tid);
-    load_vbm_bf16(a, b, h, j0, (kt + 1) * kBk, tid, regs);
-    const f32x16 s_next = qk();
-    softmax_pv(s_cur);
-    s_cur = s_next;
-  }
-  __syncthreads();
-  store_vbm();
-  __syncthreads();
-  softmax_pv(s_cur);
+  // Software pipeline (BF16 MFMAs run beside VALU work): the S^T MFMAs of
+  // tile kt+1 are issued before the softmax of tile kt.  LDS holds K of tile
+  // kt+1 and V of tile kt during iteration kt; two bias sets alternate
+  // between even and odd tiles and are loaded two tiles ahead.
+  auto run = [&](auto exact_tag) {
+    constexpr bool kExact = decltype(exact_tag)::value;
+    const f32x16 zero16 = {};
+    // S^T of tile t from Ks[buf]: fast rows start from the bias; exact rows
+    // get K Q^T only (the mask and then the bias follow in finish()).
+    auto scores = [&](int buf, const BiasFrag& bias) -> f32x16 {
+      const bf16x8 k0 = *(const bf16x8*)&Ks[buf][l32][8 * half];
+      const bf16x8 k1 = *(const bf16x8*)&Ks[buf][l32][16 + 8 * half];
+      f32x16 x = zero16;
+      if (!kExact) {
+        x = mfma_bf16(eye[0], bias.m0, x);
+        x = mfma_bf16(eye[1], bias.m1, x);
+      }
+      x = mfma_bf16(k0, qf[0], x);
+      return mfma_bf16(k1, qf[1], x);
+    };
+    auto finish = [&](f32x16& x, const BiasFrag& bias, int t) {
+      if (kExact) {
+        add_mask(x, t);
+        x = mfma_bf16(eye[0], bias.m0, x);
+        x = mfma_bf16(eye[1], bias.m1, x);
+      } else if (masked(t)) {
+        add_mask(x, t);
+      }
+    };
+    auto pv = [&](int buf, const bf16x8& p0, const bf16x8& p1) {
+      const bf16x8 v0 = *(const bf16x8*)&Vs[buf][l32][8 * half];
+      const bf16x8 v1 = *(const bf16x8*)&Vs[buf][l32][16 + 8 * half];
+      o = mfma_bf16(v0, p0, o);
+      o = mfma_bf16(v1, p1, o);
+    };
 
-  const float l_tot = xor32_sum_bf(l_run);
+    // Prologue: K(0), K(1), V(0) into LDS; S^T(0); K(2), V(1) in flight.
+    BiasFrag bias_e = load_bias(0);
+    BiasFrag bias_o = load_bias(last < 1 ? last : 1);
+    store_kv(0, load_k(0), load_v(0));
+    *(bf16x4*)&Ks[1][row8][col4] = load_k(last < 1 ? last : 1);
+    bf16x4 kreg = load_k(last < 2 ? last : 2);
+    bf16x4 vreg = load_v(last < 1 ? last : 1);
+    __syncthreads();
+    f32x16 x_a = scores(0, bias_e);
+    finish(x_a, bias_e, 0);
+    bias_e = load_bias(last < 2 ? last : 2);
+    __syncthreads();  // every wave is done with K(0) before Ks[0] is refilled
+    f32x16 x_b;
+
+    // Iteration kt: Ks[(kt+1)&1] = K(kt+1), Vs[kt&1] = V(kt), cur = S^T(kt),
+    // bias_n = bias(kt+1); kreg = K(kt+2), vreg = V(kt+1) in flight.
+    auto body = [&](int kt, f32x16& cur, f32x16& nxt, BiasFrag& bias_n) {
+      nxt = scores((kt + 1) & 1, bias_n);
+      bf16x8 p0, p1;
+      softmax(cur, p0, p1);
+      pv(kt & 1, p0, p1);
+      finish(nxt, bias_n, kt + 1);
+      bias_n = load_bias(kt + 3 < last ? kt + 3 : last);
+      *(bf16x4*)&Ks[kt & 1][row8][col4] = kreg;
+      *(bf16x4*)&Vs[(kt + 1) & 1][row8][vpos] = vreg;
+      kreg = load_k(kt + 3 < last ? kt + 3 : last);
+      vreg = load_v(kt + 2 < last ? kt + 2 : last);
+      __syncthreads();
+    };
+    auto tail = [&](const f32x16& cur, int kt) {
+      bf16x8 p0, p1;
+      softmax(cur, p0, p1);
+      pv(kt & 1, p0, p1);
+    };
+    int kt = 0;
+    for (; kt + 2 < nkt; kt += 2) {
+      body(kt, x_a, x_b, bias_o);
+      body(kt + 1, x_b, x_a, bias_e);
+    }
+    if (kt + 1 < nkt) {
+      body(kt, x_a, x_b, bias_o);
+      tail(x_b, kt + 1);
+    } else {
+      tail(x_a, kt);
+    }
+  };
+  if (has_unmasked) {
+    run(std::false_type{});
+  } else {
+    run(std::true_type{});
+  }
+
+  const float l_tot = __builtin_bit_cast(float, (unsigned)__builtin_amdgcn_permlane32_swap(
+                          __builtin_bit_cast(unsigned, l_run), __builtin_bit_cast(unsigned, l_run),
+                          false, false)[0]) +
+                      __builtin_bit_cast(float, (unsigned)__builtin_amdgcn_permlane32_swap(
+                          __builtin_bit_cast(unsigned, l_run), __builtin_bit_cast(unsigned, l_run),
+                          false, false)[1]);
   if (jq < a.n) {
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
@@ -413,7 +555,8 @@ hipError_t launch_projection_bf16(int mode, const Bf16ProjArgs& a, hipStream_t s
 
 hipError_t launch_attention_bf16(const Bf16AttnArgs& a, hipStream_t stream) {
   const int nqt = a.np / kBq;
-  const int nkt = a.np / kBk;
+  const int nkt = (int)(round_up(a.n, kBk) / kBk);  // tiles wholly past n are not visited
+  if (a.tile_flags == nullptr || nkt > kTileFlagWords * 32) return hipErrorInvalidValue;
   const uint64_t groups = ((uint64_t)a.batch + kRowGroup - 1) / kRowGroup;
   const uint64_t total = groups * kRowGroup * kHeads * nqt;
   if (total == 0) return hipSuccess;

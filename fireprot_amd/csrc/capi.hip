@@ -206,6 +206,7 @@ int fpx_tri_attn_attend(int dtype, int n, void* workspace, size_t workspace_byte
     a.k = as<__bf16>(w.kh);
     a.v = as<__bf16>(w.vt);
     a.mbias = w.mbias;
+    a.tile_flags = w.flags;
     a.bias = as<__bf16>(w.tri);
     a.gate = as<__bf16>(w.gs);
     a.out = as<__bf16>(w.og);

@@ -54,7 +54,7 @@ __global__ __launch_bounds__(256) void mask_rows_kernel(const float* __restrict_
 }
 
 // Zero rows [n, np) of every head of the triangle bias (padded queries), in
-// the FP32 fragment order or row-major.
+// the FP32 or the BF16 fragment order.
 template <typename BiasT, bool kFrag>
 __global__ void bias_pad_kernel(int n, int np, BiasT* __restrict__ tri_bias) {
   const int64_t per_head = (int64_t)(np - n) * np;
@@ -65,11 +65,8 @@ __global__ void bias_pad_kernel(int n, int np, BiasT* __restrict__ tri_bias) {
     const int64_t r = idx % per_head;
     const int q = n + (int)(r / np);
     const int k = (int)(r % np);
-    if (kFrag) {
-      tri_bias[bias_frag_index(h, q, k, np)] = (BiasT)0.0f;
-    } else {
-      tri_bias[((int64_t)h * np + q) * np + k] = (BiasT)0.0f;
-    }
+    tri_bias[kFrag ? bias_frag_index(h, q, k, np) : bias_frag_index_bf16(h, q, k, np)] =
+        (BiasT)0.0f;
   }
 }
 

@@ -97,7 +97,7 @@ hipError_t launch_projection(int mode, const ProjArgs& args, hipStream_t stream)
 // mask is null), the per-row tile flags of the attention kernel, and zero
 // rows [n, np) of every head of the triangle bias: both float copies in
 // fragment order (bias_frag_index, unscaled then log2(e)-scaled, contiguous),
-// or the one row-major bf16 copy when bias_bf16.
+// or the one bf16 copy (bias_frag_index_bf16) when bias_bf16.
 hipError_t launch_mask_bias(const float* mask, int64_t ms_i, int64_t ms_j, int n, int np,
                             float inf, float* mbias, uint32_t* tile_flags, void* tri_bias,
                             bool bias_bf16, hipStream_t stream);
@@ -147,7 +147,8 @@ struct Bf16AttnArgs {
   const __bf16* k;
   const __bf16* v;
   const float* mbias;
-  const __bf16* bias;
+  const uint32_t* tile_flags;
+  const __bf16* bias;  // fragment order (bias_frag_index_bf16)
   const __bf16* gate;
   __bf16* out;
   int batch;
