@@ -59,11 +59,13 @@ __global__ __launch_bounds__(Bf16ProjTraits<MODE>::kWaves * 64) void projection_
   constexpr int kRowsPerWave = kRows / NW;
   constexpr int kVecs = kRows * kChannels / 8;               // 16-byte vectors per tile
   constexpr int kLoads = (kVecs + kThreads - 1) / kThreads;
-  __shared__ __attribute__((aligned(16))) __bf16 xs[kRows][kXsStride];
+  // Two row tiles: the MFMAs read one while the next is normalised into the
+  // other, so a tile needs one barrier (the FP32 kernel's structure).
+  __shared__ __attribute__((aligned(16))) __bf16 xs[2][kRows][kXsStride];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5;
   const int l32 = lane & 31;
 
@@ -74,6 +76,8 @@ __global__ __launch_bounds__(Bf16ProjTraits<MODE>::kWaves * 64) void projection_
 #pragma unroll
     for (int m = 0; m < 8; ++m) wf[m] = *(const bf16x8*)(src + 16 * m);
   }
+  const int col_w = MODE == kProjOut ? 32 * w + l32 : 32 * (w & 3) + l32;
+  const float col_bias = a.bias_vec != nullptr ? (float)a.bias_vec[col_w] : 0.f;
 
   float lnw[2] = {1.f, 1.f}, lnb[2] = {0.f, 0.f};
   float wb[kHeads][2] = {};
@@ -127,9 +131,7 @@ __global__ __launch_bounds__(Bf16ProjTraits<MODE>::kWaves * 64) void projection_
     }
   };
 
-  int tile = blockIdx.x;
-  if (tile < ntiles) fetch(tile);
-  for (; tile < ntiles; tile += gridDim.x) {
+  auto stage_rows = [&](int tile, int buf) {
     const int i = tile / tiles_j;
     const int j0 = (tile % tiles_j) * kRows;
     if (kLn) {
@@ -144,7 +146,7 @@ __global__ __launch_bounds__(Bf16ProjTraits<MODE>::kWaves * 64) void projection_
         float y1 = d1 * rstd * lnw[1] + lnb[1];
         if (!valid) y0 = y1 = 0.f;
         const bf16x2 yb = {(__bf16)y0, (__bf16)y1};
-        *(bf16x2*)&xs[row][2 * lane] = yb;
+        *(bf16x2*)&xs[buf][row][2 * lane] = yb;
         if (MODE == kProjBlock) {
           const float r0 = (float)yb.x;
           const float r1 = (float)yb.y;
@@ -161,16 +163,23 @@ __global__ __launch_bounds__(Bf16ProjTraits<MODE>::kWaves * 64) void projection_
 #pragma unroll
       for (int t = 0; t < kLoads; ++t) {
         const int idx = tid + t * kThreads;
-        if (idx < kVecs) *(bf16x8*)&xs[idx >> 4][(idx & 15) * 8] = stage_vec[t];
+        if (idx < kVecs) *(bf16x8*)&xs[buf][idx >> 4][(idx & 15) * 8] = stage_vec[t];
       }
     }
-    __syncthreads();
-    if (tile + (int)gridDim.x < ntiles) fetch(tile + gridDim.x);
+  };
 
+  auto mfma_tile = [&](int buf) -> f32x16 {
     f32x16 acc = {};
 #pragma unroll
-    for (int m = 0; m < 8; ++m) acc = mfma_bf16(*(const bf16x8*)&xs[l32][16 * m + 8 * half], wf[m], acc);
+    for (int m = 0; m < 8; ++m)
+      acc = mfma_bf16(*(const bf16x8*)&xs[buf][l32][16 * m + 8 * half], wf[m], acc);
+    return acc;
+  };
 
+  // Lane holds rows 4*half + 8*(r/4) + r%4 of the tile, column col_w.
+  auto epilogue = [&](int tile, const f32x16& acc) {
+    const int i = tile / tiles_j;
+    const int j0 = (tile % tiles_j) * kRows + 4 * half;
     const int group = w >> 2;
     const int hw = w & 3;
     if (MODE == kProjBlock) {
@@ -179,34 +188,57 @@ __global__ __launch_bounds__(Bf16ProjTraits<MODE>::kWaves * 64) void projection_
         __bf16* dst = (group == 0 ? a.qh : a.kh) + (bh * a.np + j0) * kHeadDim + l32;
         const float scale = group == 0 ? a.q_scale : 1.0f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) dst[(int64_t)mfma_row(r, half) * kHeadDim] = (__bf16)(acc[r] * scale);
+        for (int r = 0; r < 16; ++r)
+          dst[(8 * (r >> 2) + (r & 3)) * kHeadDim] = (__bf16)(acc[r] * scale);
       } else if (group == 2) {
-        __bf16* dst = a.vt + (bh * kHeadDim + l32) * a.np + j0 + 4 * half;
+        __bf16* dst = a.vt + (bh * kHeadDim + l32) * a.np + j0;
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr)
           *(bf16x4*)(dst + 8 * rr) = bf16x4{(__bf16)acc[4 * rr + 0], (__bf16)acc[4 * rr + 1],
                                             (__bf16)acc[4 * rr + 2], (__bf16)acc[4 * rr + 3]};
       } else {
-        const int col = 32 * hw + l32;
-        const float bg = a.bias_vec ? (float)a.bias_vec[col] : 0.f;
-        __bf16* dst = a.gs + ((int64_t)i * a.rows_j) * kHidden + col;
+        // gate rows are padded to np: the tile is always stored whole
+        __bf16* dst = a.gs + ((int64_t)i * a.np + j0) * kHidden + col_w;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int j = j0 + mfma_row(r, half);
-          if (j < a.rows_j) dst[(int64_t)j * kHidden] = (__bf16)sigmoidf_(acc[r] + bg);
-        }
+        for (int r = 0; r < 16; ++r)
+          dst[(8 * (r >> 2) + (r & 3)) * kHidden] = (__bf16)sigmoidf_(acc[r] + col_bias);
       }
     } else {
-      const int col = 32 * w + l32;
-      const float bo = a.bias_vec ? (float)a.bias_vec[col] : 0.f;
-      __bf16* dst = a.out + (int64_t)i * a.os_i + col;
+      const bool full = (tile % tiles_j + 1) * kRows <= a.rows_j;
+      __bf16* dst = a.out + (int64_t)i * a.os_i + (int64_t)j0 * a.os_j + col_w;
+      if (full) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int j = j0 + mfma_row(r, half);
-        if (j < a.rows_j) dst[(int64_t)j * a.os_j] = (__bf16)(acc[r] + bo);
+        for (int r = 0; r < 16; ++r)
+          dst[(int64_t)(8 * (r >> 2) + (r & 3)) * a.os_j] = (__bf16)(acc[r] + col_bias);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dj = 8 * (r >> 2) + (r & 3);
+          if (j0 + dj < a.rows_j) dst[(int64_t)dj * a.os_j] = (__bf16)(acc[r] + col_bias);
+        }
       }
     }
+  };
+
+  // The weight fragment and bias must have landed before the loop: the
+  // loop's waits then track only the row fetches and the output stores.
+  __builtin_amdgcn_s_waitcnt(0);
+  int tile = blockIdx.x;  // grid <= ntiles, so every work-group has a tile
+  fetch(tile);
+  stage_rows(tile, 0);
+  int next = tile + (int)gridDim.x;
+  if (next < ntiles) fetch(next);
+  __syncthreads();
+  for (int buf = 0; tile < ntiles; buf ^= 1) {
+    const f32x16 acc = mfma_tile(buf);
+    if (next < ntiles) {
+      stage_rows(next, buf ^ 1);
+      if (next + (int)gridDim.x < ntiles) fetch(next + gridDim.x);
+    }
+    epilogue(tile, acc);
     __syncthreads();
+    tile = next;
+    next += gridDim.x;
   }
 }
 
@@ -530,9 +562,9 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int c = 8 * rr + 4 * half;
-      const int64_t off = ((int64_t)b * a.n + jq) * kHidden + h * kHeadDim + c;
-      const bf16x4 g = *(const bf16x4*)(a.gate + off);
-      *(bf16x4*)(a.out + off) = bf16x4{(__bf16)(o[4 * rr + 0] / l_tot * (float)g.x),
+      const int64_t col = h * kHeadDim + c;
+      const bf16x4 g = *(const bf16x4*)(a.gate + ((int64_t)b * a.np + jq) * kHidden + col);
+      *(bf16x4*)(a.out + ((int64_t)b * a.n + jq) * kHidden + col) = bf16x4{(__bf16)(o[4 * rr + 0] / l_tot * (float)g.x),
                                        (__bf16)(o[4 * rr + 1] / l_tot * (float)g.y),
                                        (__bf16)(o[4 * rr + 2] / l_tot * (float)g.z),
                                        (__bf16)(o[4 * rr + 3] / l_tot * (float)g.w)};

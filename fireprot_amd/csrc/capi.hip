@@ -29,8 +29,7 @@ size_t elem_bytes(int dtype) { return dtype == FPX_BF16 ? 2 : 4; }
 
 // Workspace segments of the block, all 256-byte aligned, element size e
 // (4 for FPX_F32, 2 for FPX_BF16; the mask bias is always float):
-//   qh, kh [n][4][np][32]; vt [n][4][32][np]; gs [n][np][128] (FP32; BF16
-//   [n][n][128]); og [n][n][128];
+//   qh, kh [n][4][np][32]; vt [n][4][32][np]; gs [n][np][128]; og [n][n][128];
 //   tri_bias [4][np][np] (FP32: fragment order, twice: as is and scaled by
 //   log2(e)); mbias [n][np] float;
 //   tile flags [n][2 * kTileFlagWords] uint32
@@ -44,7 +43,7 @@ BlockWorkspace block_workspace(int n, int dtype) {
   auto seg = [](size_t bytes) { return (size_t)round_up((int64_t)bytes, 256); };
   const size_t qkv = seg((size_t)n * fpx::kHeads * np * fpx::kHeadDim * e);
   const size_t g = seg((size_t)n * n * fpx::kHidden * e);
-  const size_t gate = seg((size_t)n * (dtype == FPX_F32 ? np : (size_t)n) * fpx::kHidden * e);
+  const size_t gate = seg((size_t)n * np * fpx::kHidden * e);
   const size_t bias = seg((size_t)fpx::kHeads * np * np * e * (dtype == FPX_F32 ? 2 : 1));
   const size_t mb = seg((size_t)n * np * sizeof(float));
   const size_t fl = seg((size_t)n * 2 * fpx::kTileFlagWords * sizeof(uint32_t));

@@ -115,8 +115,9 @@ hipError_t launch_sigmoid_mul(const float* gate, const float* value, float* out,
 // ------------------------------------------------------------ BF16 block
 // BF16 storage / FP32 accumulation variant of the block (gfx950
 // v_mfma_f32_32x32x16_bf16).  Same workspace roles and strides as the FP32
-// block, with q, k, v^T, gate, gated output and triangle bias held as bf16;
-// the mask bias stays float.
+// block, with q, k, v^T, gate (rows padded to np), gated output and one
+// triangle-bias copy (bias_frag_index_bf16) held as bf16; the mask bias and
+// tile flags are shared with the FP32 layout.
 struct Bf16ProjArgs {
   const __bf16* x;
   int64_t xs_i;

@@ -46,10 +46,9 @@ def test_abi_version_and_workspace_sizes(lib):
         np_ = -(-n // 128) * 128
         seg = lambda b: -(-b // 256) * 256  # noqa: E731
         for dtype, e in ((0, 4), (1, 2)):
-            # q, k, v^T; gate, gated output; triangle bias; mask bias; tile flags
             copies = 2 if dtype == 0 else 1  # FP32: unscaled and log2(e)-scaled bias
-            gate_rows = np_ if dtype == 0 else n  # FP32 gate rows padded to np
-            expected = (3 * seg(n * 4 * np_ * 32 * e) + seg(n * gate_rows * 128 * e)
+            # q, k, v^T; gate (rows padded to np); gated output; bias; mask bias; flags
+            expected = (3 * seg(n * 4 * np_ * 32 * e) + seg(n * np_ * 128 * e)
                         + seg(n * n * 128 * e)
                         + seg(4 * np_ * np_ * e * copies) + seg(n * np_ * 4) + seg(n * 8 * 4))
             assert lib.fpx_tri_attn_workspace_bytes(n, 128, 4, 32, dtype) == expected
