@@ -141,12 +141,17 @@ def check_block_inputs(z: torch.Tensor, mask: torch.Tensor | None, weights: Bloc
 
 def triangle_attention_block(z: torch.Tensor, mask: torch.Tensor | None, weights: BlockWeights,
                              *, ending: bool = False, out: torch.Tensor | None = None,
-                             workspace: torch.Tensor | None = None) -> torch.Tensor:
+                             workspace: torch.Tensor | None = None,
+                             residual: bool = False) -> torch.Tensor:
     """Return dz for the starting (``ending=False``) or ending node.
 
     The ending node reads ``z`` and ``mask`` through swapped strides and writes
     ``dz`` transposed, so ``dz_end(z, m) == T(dz_start(T(z), T(m)))`` with no
-    transposed copies.  Runs asynchronously on the current stream.
+    transposed copies.  With ``residual=True`` the update is added instead:
+    ``out += dz`` (``out`` defaults to ``z`` itself, an in-place update), the
+    Pairformer's ``z += tri_att_start(z)`` / ``z += tri_att_end(z)``
+    (patches/protenix/0006-*.patch:17-37).  Runs asynchronously on the
+    current stream.
     """
     lib = _native.library()
     check_block_inputs(z, mask, weights)
@@ -154,10 +159,15 @@ def triangle_attention_block(z: torch.Tensor, mask: torch.Tensor | None, weights
     if mask is not None and mask.dtype != torch.float32:
         mask = mask.to(torch.float32)
     if out is None:
-        out = torch.empty((n, n, CHANNELS), device=z.device, dtype=z.dtype)
+        out = z if residual else torch.empty((n, n, CHANNELS), device=z.device, dtype=z.dtype)
     elif (tuple(out.shape) != (n, n, CHANNELS) or out.dtype != z.dtype
           or out.device != z.device or out.stride(2) != 1):
         raise ValueError("out must be a [N, N, 128] tensor of z's dtype on z's device")
+    align = 16 // z.element_size()
+    if out.stride(0) % align or out.stride(1) % align:
+        raise ValueError("out rows must be 16-byte aligned")
+    if residual and out.data_ptr() == z.data_ptr() and out.stride() != z.stride():
+        raise ValueError("an in-place update needs out and z with the same strides")
     with torch.cuda.device(z.device):
         need = workspace_bytes(n, z.dtype)
         if workspace is None:
@@ -165,7 +175,8 @@ def triangle_attention_block(z: torch.Tensor, mask: torch.Tensor | None, weights
         elif workspace.numel() * workspace.element_size() < need:
             raise ValueError(f"workspace needs {need} bytes")
         stream = torch.cuda.current_stream(z.device).cuda_stream
-        code = lib.fpx_tri_attn_block(
+        entry = lib.fpx_tri_attn_block_residual if residual else lib.fpx_tri_attn_block
+        code = entry(
             DTYPES[z.dtype], z.data_ptr(), z.stride(0), z.stride(1),
             _ptr(mask), mask.stride(0) if mask is not None else 0,
             mask.stride(1) if mask is not None else 0,
@@ -175,8 +186,22 @@ def triangle_attention_block(z: torch.Tensor, mask: torch.Tensor | None, weights
             n, CHANNELS, HEADS, HEAD_DIM, int(bool(ending)),
             out.data_ptr(), out.stride(0), out.stride(1),
             workspace.data_ptr(), workspace.numel() * workspace.element_size(), stream)
-    _native.check(code, "fpx_tri_attn_block")
+    _native.check(code, "fpx_tri_attn_block_residual" if residual else "fpx_tri_attn_block")
     return out
+
+
+def pair_step_triangle_attention(z: torch.Tensor, mask: torch.Tensor | None,
+                                 start: BlockWeights, end: BlockWeights, *,
+                                 workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """The Pairformer's two triangle-attention updates on ``z`` in place:
+    ``z += tri_att_start(z, mask)``, then the ending node on the updated ``z``
+    (patches/protenix/0006-*.patch:17-37), with no transposed copies."""
+    if workspace is None:
+        workspace = torch.empty(workspace_bytes(z.shape[0], z.dtype), dtype=torch.uint8,
+                                device=z.device)
+    triangle_attention_block(z, mask, start, ending=False, workspace=workspace, residual=True)
+    triangle_attention_block(z, mask, end, ending=True, workspace=workspace, residual=True)
+    return z
 
 
 def block_flops(n: int) -> dict[str, int]:

@@ -206,15 +206,22 @@ __global__ __launch_bounds__(Bf16ProjTraits<MODE>::kWaves * 64) void projection_
     } else {
       const bool full = (tile % tiles_j + 1) * kRows <= a.rows_j;
       __bf16* dst = a.out + (int64_t)i * a.os_i + (int64_t)j0 * a.os_j + col_w;
+      // The residual update adds the bf16 update to the old value, rounding
+      // where the native bf16 z += dz rounds.
+      const bool residual = a.accumulate != 0;
+      auto put = [&](__bf16* d, float v) {
+        const __bf16 u = (__bf16)v;
+        *d = residual ? (__bf16)((float)*d + (float)u) : u;
+      };
       if (full) {
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          dst[(int64_t)(8 * (r >> 2) + (r & 3)) * a.os_j] = (__bf16)(acc[r] + col_bias);
+          put(dst + (int64_t)(8 * (r >> 2) + (r & 3)) * a.os_j, acc[r] + col_bias);
       } else {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int dj = 8 * (r >> 2) + (r & 3);
-          if (j0 + dj < a.rows_j) dst[(int64_t)dj * a.os_j] = (__bf16)(acc[r] + col_bias);
+          if (j0 + dj < a.rows_j) put(dst + (int64_t)dj * a.os_j, acc[r] + col_bias);
         }
       }
     }

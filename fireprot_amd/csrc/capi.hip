@@ -101,6 +101,75 @@ T* as(char* p) {
   return reinterpret_cast<T*>(p);
 }
 
+// Output projection into dz, or added to dz (accumulate), in z's frame.
+int finish_stage(int dtype, const void* w_o, const void* b_o, int n, int ending, void* dz,
+                 int64_t dz_stride0, int64_t dz_stride1, void* workspace, size_t workspace_bytes,
+                 void* stream, int accumulate) {
+  if (!block_dims_ok(n, fpx::kChannels, fpx::kHeads, fpx::kHeadDim, dtype)) return FPX_ERR_DIMS;
+  if (ending != 0 && ending != 1) return FPX_ERR_DIMS;
+  if (dz_stride0 < 0 || dz_stride1 < 0) return FPX_ERR_DIMS;
+  if (!aligned(w_o, 16) || !aligned(dz, 16) || !aligned_or_null(b_o, 2)) return FPX_ERR_POINTER;
+  if (dtype == FPX_F32 && !aligned_or_null(b_o, 4)) return FPX_ERR_POINTER;
+  if (int rc = check_workspace(n, dtype, workspace, workspace_bytes)) return rc;
+  const BlockPointers w = block_pointers(workspace, n, dtype);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t os_i = ending ? dz_stride1 : dz_stride0;
+  const int64_t os_j = ending ? dz_stride0 : dz_stride1;
+  if (dtype == FPX_BF16) {
+    fpx::Bf16ProjArgs o{};
+    o.x = as<__bf16>(w.og);
+    o.xs_i = (int64_t)n * fpx::kHidden;
+    o.xs_j = fpx::kHidden;
+    o.rows_i = n;
+    o.rows_j = n;
+    o.span_j = n;
+    o.w[0] = static_cast<const __bf16*>(w_o);
+    o.bias_vec = static_cast<const __bf16*>(b_o);
+    o.out = static_cast<__bf16*>(dz);
+    o.os_i = os_i;
+    o.os_j = os_j;
+    o.accumulate = accumulate;
+    return status(fpx::launch_projection_bf16(fpx::kProjOut, o, s));
+  }
+  fpx::ProjArgs o{};
+  o.x = as<float>(w.og);
+  o.xs_i = (int64_t)n * fpx::kHidden;
+  o.xs_j = fpx::kHidden;
+  o.rows_i = n;
+  o.rows_j = n;
+  o.span_j = n;
+  o.w[0] = static_cast<const float*>(w_o);
+  o.b_g = static_cast<const float*>(b_o);
+  o.out = static_cast<float*>(dz);
+  o.os_i = os_i;
+  o.os_j = os_j;
+  o.accumulate = accumulate;
+  return status(fpx::launch_projection(fpx::kProjOut, o, s));
+}
+
+// The whole block: prepare, attend, then the output projection written to or
+// (accumulate) added to dz.
+int block_impl(int dtype, const void* z, int64_t z_stride0, int64_t z_stride1, const float* mask,
+               int64_t m_stride0, int64_t m_stride1, const void* ln_w, const void* ln_b,
+               float eps, const void* w_qkvg, const void* b_g, const void* w_bias,
+               const void* w_o, const void* b_o, float mask_inf, int n, int c, int heads,
+               int head_dim, int ending, void* dz, int64_t dz_stride0, int64_t dz_stride1,
+               void* workspace, size_t workspace_bytes, void* stream, int accumulate) {
+  if (!block_dims_ok(n, c, heads, head_dim, dtype)) return FPX_ERR_DIMS;
+  if (ending != 0 && ending != 1) return FPX_ERR_DIMS;
+  if (dz_stride0 < 0 || dz_stride1 < 0) return FPX_ERR_DIMS;
+  if (!aligned(w_o, 16) || !aligned(dz, 16) || !aligned_or_null(b_o, 2)) return FPX_ERR_POINTER;
+  if (dtype == FPX_F32 && !aligned_or_null(b_o, 4)) return FPX_ERR_POINTER;
+  int rc = fpx_tri_attn_prepare(dtype, z, z_stride0, z_stride1, mask, m_stride0, m_stride1, ln_w,
+                                ln_b, eps, w_qkvg, b_g, w_bias, mask_inf, n, ending, workspace,
+                                workspace_bytes, stream);
+  if (rc) return rc;
+  rc = fpx_tri_attn_attend(dtype, n, workspace, workspace_bytes, stream);
+  if (rc) return rc;
+  return finish_stage(dtype, w_o, b_o, n, ending, dz, dz_stride0, dz_stride1, workspace,
+                      workspace_bytes, stream, accumulate);
+}
+
 }  // namespace
 
 extern "C" {
@@ -236,44 +305,8 @@ int fpx_tri_attn_attend(int dtype, int n, void* workspace, size_t workspace_byte
 int fpx_tri_attn_finish(int dtype, const void* w_o, const void* b_o, int n, int ending, void* dz,
                         int64_t dz_stride0, int64_t dz_stride1, void* workspace,
                         size_t workspace_bytes, void* stream) {
-  if (!block_dims_ok(n, fpx::kChannels, fpx::kHeads, fpx::kHeadDim, dtype)) return FPX_ERR_DIMS;
-  if (ending != 0 && ending != 1) return FPX_ERR_DIMS;
-  if (dz_stride0 < 0 || dz_stride1 < 0) return FPX_ERR_DIMS;
-  if (!aligned(w_o, 16) || !aligned(dz, 16) || !aligned_or_null(b_o, 2)) return FPX_ERR_POINTER;
-  if (dtype == FPX_F32 && !aligned_or_null(b_o, 4)) return FPX_ERR_POINTER;
-  if (int rc = check_workspace(n, dtype, workspace, workspace_bytes)) return rc;
-  const BlockPointers w = block_pointers(workspace, n, dtype);
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t os_i = ending ? dz_stride1 : dz_stride0;
-  const int64_t os_j = ending ? dz_stride0 : dz_stride1;
-  if (dtype == FPX_BF16) {
-    fpx::Bf16ProjArgs o{};
-    o.x = as<__bf16>(w.og);
-    o.xs_i = (int64_t)n * fpx::kHidden;
-    o.xs_j = fpx::kHidden;
-    o.rows_i = n;
-    o.rows_j = n;
-    o.span_j = n;
-    o.w[0] = static_cast<const __bf16*>(w_o);
-    o.bias_vec = static_cast<const __bf16*>(b_o);
-    o.out = static_cast<__bf16*>(dz);
-    o.os_i = os_i;
-    o.os_j = os_j;
-    return status(fpx::launch_projection_bf16(fpx::kProjOut, o, s));
-  }
-  fpx::ProjArgs o{};
-  o.x = as<float>(w.og);
-  o.xs_i = (int64_t)n * fpx::kHidden;
-  o.xs_j = fpx::kHidden;
-  o.rows_i = n;
-  o.rows_j = n;
-  o.span_j = n;
-  o.w[0] = static_cast<const float*>(w_o);
-  o.b_g = static_cast<const float*>(b_o);
-  o.out = static_cast<float*>(dz);
-  o.os_i = os_i;
-  o.os_j = os_j;
-  return status(fpx::launch_projection(fpx::kProjOut, o, s));
+  return finish_stage(dtype, w_o, b_o, n, ending, dz, dz_stride0, dz_stride1, workspace,
+                      workspace_bytes, stream, 0);
 }
 
 int fpx_tri_attn_block(int dtype, const void* z, int64_t z_stride0, int64_t z_stride1,
@@ -283,19 +316,23 @@ int fpx_tri_attn_block(int dtype, const void* z, int64_t z_stride0, int64_t z_st
                        float mask_inf, int n, int c, int heads, int head_dim, int ending,
                        void* dz, int64_t dz_stride0, int64_t dz_stride1, void* workspace,
                        size_t workspace_bytes, void* stream) {
-  if (!block_dims_ok(n, c, heads, head_dim, dtype)) return FPX_ERR_DIMS;
-  if (ending != 0 && ending != 1) return FPX_ERR_DIMS;
-  if (dz_stride0 < 0 || dz_stride1 < 0) return FPX_ERR_DIMS;
-  if (!aligned(w_o, 16) || !aligned(dz, 16) || !aligned_or_null(b_o, 2)) return FPX_ERR_POINTER;
-  if (dtype == FPX_F32 && !aligned_or_null(b_o, 4)) return FPX_ERR_POINTER;
-  int rc = fpx_tri_attn_prepare(dtype, z, z_stride0, z_stride1, mask, m_stride0, m_stride1, ln_w,
-                                ln_b, eps, w_qkvg, b_g, w_bias, mask_inf, n, ending, workspace,
-                                workspace_bytes, stream);
-  if (rc) return rc;
-  rc = fpx_tri_attn_attend(dtype, n, workspace, workspace_bytes, stream);
-  if (rc) return rc;
-  return fpx_tri_attn_finish(dtype, w_o, b_o, n, ending, dz, dz_stride0, dz_stride1, workspace,
-                             workspace_bytes, stream);
+  return block_impl(dtype, z, z_stride0, z_stride1, mask, m_stride0, m_stride1, ln_w, ln_b, eps,
+                    w_qkvg, b_g, w_bias, w_o, b_o, mask_inf, n, c, heads, head_dim, ending, dz,
+                    dz_stride0, dz_stride1, workspace, workspace_bytes, stream, 0);
+}
+
+int fpx_tri_attn_block_residual(int dtype, const void* z, int64_t z_stride0, int64_t z_stride1,
+                                const float* mask, int64_t m_stride0, int64_t m_stride1,
+                                const void* ln_w, const void* ln_b, float eps,
+                                const void* w_qkvg, const void* b_g, const void* w_bias,
+                                const void* w_o, const void* b_o, float mask_inf, int n, int c,
+                                int heads, int head_dim, int ending, void* z_out,
+                                int64_t out_stride0, int64_t out_stride1, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  if (z_out == z && (out_stride0 != z_stride0 || out_stride1 != z_stride1)) return FPX_ERR_DIMS;
+  return block_impl(dtype, z, z_stride0, z_stride1, mask, m_stride0, m_stride1, ln_w, ln_b, eps,
+                    w_qkvg, b_g, w_bias, w_o, b_o, mask_inf, n, c, heads, head_dim, ending, z_out,
+                    out_stride0, out_stride1, workspace, workspace_bytes, stream, 1);
 }
 
 int fpx_attn_core_masked(const float* q, const float* k, const float* v, const float* mask_bias,

@@ -88,6 +88,7 @@ struct ProjArgs {
   float* out;
   int64_t os_i;
   int64_t os_j;
+  int accumulate;  // kProjOut: out = out + (x W_o^T + b_o), the residual update
 };
 
 hipError_t launch_projection(int mode, const ProjArgs& args, hipStream_t stream);
@@ -141,6 +142,7 @@ struct Bf16ProjArgs {
   __bf16* out;
   int64_t os_i;
   int64_t os_j;
+  int accumulate;  // finish: out = bf16(out + bf16(x W_o^T + b_o))
 };
 
 struct Bf16AttnArgs {

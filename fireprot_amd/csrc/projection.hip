@@ -226,15 +226,19 @@ __global__ __launch_bounds__(ProjTraits<MODE>::kWaves * 64) void projection_kern
         stride = a.os_j;
         add = col_bias;
       }
+      // The residual update adds the rounded update to the old value, as
+      // the native z += dz does.
+      const bool residual = MODE == kProjOut && a.accumulate != 0;
+      auto put = [&](float* d, float v) { *d = residual ? *d + v : v; };
       if (full) {
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          dst[(int64_t)(8 * (r >> 2) + (r & 3)) * stride] = acc[r] * scale + add;
+          put(dst + (int64_t)(8 * (r >> 2) + (r & 3)) * stride, acc[r] * scale + add);
       } else {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int dj = 8 * (r >> 2) + (r & 3);
-          if (j0 + dj < a.rows_j) dst[(int64_t)dj * stride] = acc[r] * scale + add;
+          if (j0 + dj < a.rows_j) put(dst + (int64_t)dj * stride, acc[r] * scale + add);
         }
       }
     }

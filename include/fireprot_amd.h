@@ -82,6 +82,27 @@ int fpx_tri_attn_block(int dtype, const void* z, int64_t z_stride0, int64_t z_st
                        void* dz, int64_t dz_stride0, int64_t dz_stride1, void* workspace,
                        size_t workspace_bytes, void* stream);
 
+/* The block as a residual update: z_out += dz, with dz the result
+ * fpx_tri_attn_block would write, rounded first and then added (the native
+ * z += dz).  z_out may be z itself (same pointer and strides: an in-place
+ * update, safe because z is read in full before dz is added); any other
+ * overlap is unsupported.  With ending = 1 the update lands in z's frame, so
+ * the Pairformer pair step
+ *     z += tri_att_start(z, mask)
+ *     z = z^T; z += tri_att_end(z, mask^T); z = z^T
+ * (patches/protenix/0006-*.patch:17-37, around PairformerBlock.forward) is two
+ * calls with ending = 0 and ending = 1 on the same z, with no transposed
+ * copies.  Same sizes, status codes and contract as fpx_tri_attn_block;
+ * status 2 when z_out == z with different strides. */
+int fpx_tri_attn_block_residual(int dtype, const void* z, int64_t z_stride0, int64_t z_stride1,
+                                const float* mask, int64_t m_stride0, int64_t m_stride1,
+                                const void* ln_w, const void* ln_b, float eps,
+                                const void* w_qkvg, const void* b_g, const void* w_bias,
+                                const void* w_o, const void* b_o, float mask_inf, int n, int c,
+                                int heads, int head_dim, int ending, void* z_out,
+                                int64_t out_stride0, int64_t out_stride1, void* workspace,
+                                size_t workspace_bytes, void* stream);
+
 /* The block's three stages, run in this order on one workspace;
  * fpx_tri_attn_block is exactly prepare + attend + finish.  Split so a caller
  * (or a profiler) can time or overlap the stages; the workspace carries the

@@ -84,3 +84,22 @@ def test_c5_n2048_row_subset_transpose_and_determinism():
         rel = _rel(actual, native)
         print(f"{cfg.name} {name} rows: rel vs native-bf16 {rel:.2e}", flush=True)
         assert rel <= BF16_REL
+
+
+def test_bf16_pair_step_residual_in_place():
+    """The Pairformer's two residual updates in bf16, against the native bf16
+    ops (z is rounded after each += dz, as the native in-place add does)."""
+    n = 96
+    z = workloads.make_pair(n).to(torch.bfloat16)
+    mask = workloads.make_mask(n, 80)
+    ws = workloads.make_weights()
+    we = {k: (None if v is None else torch.roll(v, 7, 0).contiguous()) for k, v in ws.items()}
+    z1 = z + oracle.block_bf16(z.float(), mask, oracle.BlockParams(**ws), ending=False)
+    expected = z1 + oracle.block_bf16(z1.float(), mask, oracle.BlockParams(**we), ending=True)
+    zc = z.cuda()
+    with torch.inference_mode():
+        hip_block.pair_step_triangle_attention(zc, mask.cuda(), _weights(ws), _weights(we))
+        torch.cuda.synchronize()
+    rel = _rel(zc.cpu(), expected)
+    print(f"bf16 pair step rel={rel:.3e}", flush=True)
+    assert rel <= BF16_REL

@@ -12,6 +12,7 @@ from __future__ import annotations
 import pytest
 import torch
 
+from fireprot_amd import _native
 from fireprot_amd import block as hip_block
 from fireprot_amd import workloads
 from oracle import triangle_attention as oracle
@@ -122,6 +123,56 @@ def test_block_large_bias_scale(ending):
     actual = _run(z, None, w, ending)
     expected = oracle.block(z, None, oracle_params(w), ending=ending)
     assert_f32_parity(f"bias x60 ending={ending}", actual, expected)
+
+
+def _end_weights(w):
+    """A second weight set for the ending node (rows rolled, bias rescaled)."""
+    out = {k: (None if v is None else torch.roll(v, 7, 0).contiguous()) for k, v in w.items()}
+    out["w_bias"] = out["w_bias"] * 1.5
+    return out
+
+
+@pytest.mark.parametrize("n,valid", [(124, 101), (200, None)])
+def test_pair_step_residual_in_place(n, valid):
+    """z += tri_att_start(z); z += tri_att_end(z) in place, as the Pairformer
+    step does it (patches/protenix/0006-*.patch:17-37)."""
+    z = workloads.make_pair(n)
+    mask = workloads.make_mask(n, valid)
+    ws, we = workloads.make_weights(), _end_weights(workloads.make_weights())
+    z1 = z + oracle.block(z, mask, oracle_params(ws), ending=False)
+    expected = z1 + oracle.block(z1, mask, oracle_params(we), ending=True)
+    zc = z.cuda()
+    with torch.inference_mode():
+        out = hip_block.pair_step_triangle_attention(
+            zc, None if mask is None else mask.cuda(), hip_weights(ws), hip_weights(we))
+        torch.cuda.synchronize()
+    assert out.data_ptr() == zc.data_ptr()
+    assert_f32_parity(f"pair step n={n}", zc.cpu(), expected)
+
+
+def test_residual_into_separate_buffer_and_alias_guard():
+    n = 64
+    z, mask, w = workloads.make_pair(n), workloads.make_mask(n, 50), workloads.make_weights()
+    base = torch.randn(n, n, 128, generator=torch.Generator().manual_seed(3))
+    expected = base + oracle.block(z, mask, oracle_params(w), ending=True)
+    out = base.cuda()
+    zc = z.cuda()
+    with torch.inference_mode():
+        hip_block.triangle_attention_block(zc, mask.cuda(), hip_weights(w), ending=True, out=out,
+                                           residual=True)
+        torch.cuda.synchronize()
+    assert torch.equal(zc.cpu(), z)
+    assert_f32_parity("residual into out", out.cpu(), expected)
+    # z_out == z with different strides is rejected before any launch
+    lib = _native.library()
+    wt = hip_weights(w)
+    ws = torch.empty(hip_block.workspace_bytes(n), dtype=torch.uint8, device="cuda")
+    code = lib.fpx_tri_attn_block_residual(
+        0, zc.data_ptr(), zc.stride(0), zc.stride(1), None, 0, 0, None, None, 1e-5,
+        wt.w_qkvg.data_ptr(), None, wt.w_bias.data_ptr(), wt.w_o.data_ptr(), None, 1e9,
+        n, 128, 4, 32, 0, zc.data_ptr(), zc.stride(1), zc.stride(0), ws.data_ptr(), ws.numel(),
+        torch.cuda.current_stream().cuda_stream)
+    assert code == 2
 
 
 def test_block_inputs_unchanged_streams_and_queue():
