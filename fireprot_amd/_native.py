@@ -63,6 +63,16 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "fpx_tri_attn_finish": (_i, [_i, _p, _p, _i, _i, _p, _i64, _i64, _p, _sz, _p]),
     "fpx_attn_core": (_i, [_p, _p, _p, _p, _p, _i, _i, _p]),
     "fpx_attn_core_masked": (_i, [_p, _p, _p, _p, _i64, _p, _i64, _p, _i, _i, _p]),
+    "fpx_attn_strided_workspace_bytes": (_sz, [_i, _i]),
+    "fpx_attn_strided": (_i, [
+        _p, _i64, _i64, _i64,        # q, strides (batch, head, row)
+        _p, _i64, _i64, _i64,        # k
+        _p, _i64, _i64, _i64,        # v
+        _p, _i64, _i64,              # mask bias, strides (batch, key)
+        _p, _i64, _i64, _i64,        # triangle bias, strides (head, query, key)
+        _p, _i64, _i64, _i64,        # out
+        _i, _i, _p, _sz, _p,         # batch, n, workspace, bytes, stream
+    ]),
     "fpx_layer_norm_c128": (_i, [_p, _i64, _i64, _i64, _i64, _p, _p, _f, _p, _p]),
     "fpx_qkv_projection": (_i, [_p, _i64, _p, _p, _p, _p, _p]),
     "fpx_sigmoid_mul_out": (_i, [_p, _p, _p, _i64, _p]),

@@ -200,6 +200,50 @@ struct Tiles<kAttnHeadLast> {
   }
 };
 
+// A caller's strided q/k/v/out (kAttnStrided) with the staged bias of the
+// block layout.  K and V rows are read through buffer descriptors over the
+// (b, h) slice; keys past n are clamped to key n - 1 (finite values whose
+// weights are exactly 0, since their staged mask bias is -inf).  V rows are
+// transposed on their way into LDS.
+template <>
+struct Tiles<kAttnStrided> {
+  __amdgpu_buffer_rsrc_t rk, rv, rb, rb2;
+  uint32_t ob, ck, cv, sk, sv;
+  int key, last_key;
+  __device__ __forceinline__ Tiles(const AttnArgs& a, int b, int h, int qt32, int tid, int lane,
+                                   int /*half*/, int /*jq*/) {
+    const int64_t nt = a.np >> 5;
+    const int64_t frag = ((int64_t)h * nt + qt32) * nt * 1024;
+    rk = buffer(a.k + b * a.ks[0] + h * a.ks[1], ((int64_t)(a.n - 1) * a.ks[2] + kHeadDim) * 4);
+    rv = buffer(a.v + b * a.vs[0] + h * a.vs[1], ((int64_t)(a.n - 1) * a.vs[2] + kHeadDim) * 4);
+    rb = buffer(a.bias + frag, nt * 4096);
+    rb2 = buffer(a.bias_l2 + frag, nt * 4096);
+    ob = (uint32_t)lane * 16;
+    key = tid >> 3;
+    last_key = a.n - 1;
+    ck = (uint32_t)((tid & 7) * 4) * 4;
+    sk = (uint32_t)a.ks[2] * 4;
+    sv = (uint32_t)a.vs[2] * 4;
+  }
+  __device__ __forceinline__ uint32_t row(int t) const {
+    const int j = t * kBk + key;
+    return (uint32_t)(j < last_key ? j : last_key);
+  }
+  // thread (row8 = key, col4 = channel group) for both K and V
+  __device__ __forceinline__ f32x4 k(int t) const { return buffer_f4(rk, row(t) * sk + ck, 0); }
+  __device__ __forceinline__ f32x4 v(int t) const { return buffer_f4(rv, row(t) * sv + ck, 0); }
+  static __device__ __forceinline__ void store_v(VTile& vs, f32x4 v, int row8, int col4) {
+    Tiles<kAttnHeadLast>::store_v(vs, v, row8, col4);
+  }
+  __device__ __forceinline__ f32x16 frag(__amdgpu_buffer_rsrc_t r, int t) const {
+    const uint32_t s = (uint32_t)t * 4096;
+    return cat4(buffer_f4(r, ob, s), buffer_f4(r, ob + 1024, s), buffer_f4(r, ob + 2048, s),
+                buffer_f4(r, ob + 3072, s));
+  }
+  __device__ __forceinline__ f32x16 bias(int t) const { return frag(rb, t); }
+  __device__ __forceinline__ f32x16 bias_l2(int t) const { return frag(rb2, t); }
+};
+
 // max / sum of v over the lane pair (l, l ^ 32) with v_permlane32_swap
 // (no LDS round trip): after the swap one copy holds the low half in both
 // halves and the other the high half.
@@ -261,9 +305,11 @@ __device__ __forceinline__ f32x16 qk_chain(const KTile& ks, const float* qf, int
 template <int LAYOUT>
 __global__ __launch_bounds__(kThreads, FPX_ATTN_WAVES_PER_SIMD) void attention_kernel(
     AttnArgs a, int nqt, int nkt, uint32_t total) {
+  // Staged layouts carry the mask as a padded row plus tile flags.
+  constexpr bool kStaged = LAYOUT != kAttnHeadLast;
   __shared__ __attribute__((aligned(16))) KTile Ks[2];
   __shared__ __attribute__((aligned(16))) VTile Vs[2];
-  __shared__ __attribute__((aligned(16))) float Ms[LAYOUT == kAttnBlock ? kMaxKeys : 4];
+  __shared__ __attribute__((aligned(16))) float Ms[kStaged ? kMaxKeys : 4];
 
   // Logical order, slowest to fastest: head, block of kRowGroup outer rows,
   // query tile, outer row in the block.  The work-groups that run together
@@ -296,7 +342,7 @@ __global__ __launch_bounds__(kThreads, FPX_ATTN_WAVES_PER_SIMD) void attention_k
   // bias.  has_unmasked: some key k < n of the row has a zero mask bias.
   uint32_t mw[kTileFlagWords] = {0u, 0u, 0u, 0u};
   bool any_masked, has_unmasked;
-  if (LAYOUT == kAttnBlock) {
+  if (kStaged) {
     const uint32_t* f = a.tile_flags + (int64_t)b * 2 * kTileFlagWords;
     uint32_t any = 0u, open = 0u;
 #pragma unroll
@@ -319,7 +365,7 @@ __global__ __launch_bounds__(kThreads, FPX_ATTN_WAVES_PER_SIMD) void attention_k
     has_unmasked = __syncthreads_or(found) != 0;
   }
   auto masked = [&](int t) -> bool {
-    if (LAYOUT == kAttnBlock) {
+    if (kStaged) {
       const uint32_t word = t < 32 ? mw[0] : t < 64 ? mw[1] : t < 96 ? mw[2] : mw[3];
       return (word >> (t & 31)) & 1u;
     }
@@ -327,13 +373,13 @@ __global__ __launch_bounds__(kThreads, FPX_ATTN_WAVES_PER_SIMD) void attention_k
   };
   // The block's mask-bias row goes to LDS once (made visible by the prologue
   // barrier); masked tiles then read their values with four b128 loads.
-  if (LAYOUT == kAttnBlock && any_masked) {
+  if (kStaged && any_masked) {
     const float* src = a.mbias + (int64_t)b * a.mb_stride;
     for (int k = 4 * tid; k < nkt * kBk; k += 4 * kThreads)
       *(f32x4*)&Ms[k] = *(const f32x4*)(src + k);
   }
   auto mask_vals = [&](int t) -> f32x16 {
-    if constexpr (LAYOUT == kAttnBlock) {
+    if constexpr (kStaged) {
       const float* m = &Ms[t * kBk + 4 * half];
       return cat4(*(const f32x4*)(m), *(const f32x4*)(m + 8), *(const f32x4*)(m + 16),
                   *(const f32x4*)(m + 24));
@@ -350,6 +396,9 @@ __global__ __launch_bounds__(kThreads, FPX_ATTN_WAVES_PER_SIMD) void attention_k
     bool ok = true;
     if (LAYOUT == kAttnBlock) {
       src = a.q + (((int64_t)b * kHeads + h) * a.np + jq) * kHeadDim + 16 * half;
+    } else if (LAYOUT == kAttnStrided) {
+      ok = jq < a.n;
+      src = a.q + b * a.qs[0] + h * a.qs[1] + (int64_t)(ok ? jq : 0) * a.qs[2] + 16 * half;
     } else {
       ok = jq < a.n;
       src = a.q + (((int64_t)b * a.n + (ok ? jq : 0)) * kHeads + h) * kHeadDim + 16 * half;
@@ -500,7 +549,7 @@ __global__ __launch_bounds__(kThreads, FPX_ATTN_WAVES_PER_SIMD) void attention_k
         if (masked(kt)) {
           const f32x16 mb = mask_vals(kt);
 #pragma unroll
-          for (int r = 0; r < 16; ++r) x[r] += mb[r];
+          for (int r = 0; r < 16; ++r) x[r] = __builtin_fmaf(mb[r], kLog2e, x[r]);
         }
       }
       softmax(x);
@@ -537,6 +586,8 @@ __global__ __launch_bounds__(kThreads, FPX_ATTN_WAVES_PER_SIMD) void attention_k
         const int64_t col = h * kHeadDim + c;
         if (a.gate) ov = ov * *(const f32x4*)(a.gate + ((int64_t)b * a.np + jq) * kHidden + col);
         *(f32x4*)(a.out + ((int64_t)b * a.n + jq) * kHidden + col) = ov;
+      } else if (LAYOUT == kAttnStrided) {
+        *(f32x4*)(a.out + b * a.os[0] + h * a.os[1] + (int64_t)jq * a.os[2] + c) = ov;
       } else {
         *(f32x4*)(a.out + (((int64_t)b * a.n + jq) * kHeads + h) * kHeadDim + c) = ov;
       }
@@ -549,17 +600,22 @@ __global__ __launch_bounds__(kThreads, FPX_ATTN_WAVES_PER_SIMD) void attention_k
 hipError_t launch_attention(int layout, const AttnArgs& a, hipStream_t stream) {
   // Query tiles cover the padded extent; key tiles stop at the last real key
   // (tiles wholly past n hold only -inf mask bias and contribute nothing).
-  const int nqt = (int)((layout == kAttnBlock ? a.np : round_up(a.n, kBq)) / kBq);
+  const int nqt = (int)((layout != kAttnHeadLast ? a.np : round_up(a.n, kBq)) / kBq);
   const int nkt = (int)(round_up(a.n, kBk) / kBk);
   const uint64_t groups = ((uint64_t)a.batch + kRowGroup - 1) / kRowGroup;
   const uint64_t total = groups * kRowGroup * kHeads * nqt;
   if (total == 0) return hipSuccess;
   if (total > 0x7fffffffull) return hipErrorInvalidValue;
-  if (layout == kAttnBlock) {
+  if (layout != kAttnHeadLast) {
     if (a.tile_flags == nullptr || a.bias_l2 == nullptr || nkt > kTileFlagWords * 32)
       return hipErrorInvalidValue;
-    hipLaunchKernelGGL(attention_kernel<kAttnBlock>, dim3((uint32_t)total), dim3(kThreads), 0,
-                       stream, a, nqt, nkt, (uint32_t)total);
+    if (layout == kAttnBlock) {
+      hipLaunchKernelGGL(attention_kernel<kAttnBlock>, dim3((uint32_t)total), dim3(kThreads), 0,
+                         stream, a, nqt, nkt, (uint32_t)total);
+    } else {
+      hipLaunchKernelGGL(attention_kernel<kAttnStrided>, dim3((uint32_t)total), dim3(kThreads),
+                         0, stream, a, nqt, nkt, (uint32_t)total);
+    }
   } else {
     hipLaunchKernelGGL(attention_kernel<kAttnHeadLast>, dim3((uint32_t)total), dim3(kThreads), 0,
                        stream, a, nqt, nkt, (uint32_t)total);

@@ -170,6 +170,34 @@ int block_impl(int dtype, const void* z, int64_t z_stride0, int64_t z_stride1, c
                       workspace_bytes, stream, accumulate);
 }
 
+// Workspace of fpx_attn_strided, 256-byte aligned segments:
+//   bias [4][np][np] float in fragment order, twice (as is, scaled by log2(e));
+//   mbias [batch][np] float; tile flags [batch][2 * kTileFlagWords] uint32.
+struct StridedWorkspace {
+  size_t bias, bias_l2, mbias, flags, total;
+};
+
+StridedWorkspace strided_workspace(int batch, int n) {
+  const size_t np = (size_t)round_up(n, kQueryTile);
+  auto seg = [](size_t bytes) { return (size_t)round_up((int64_t)bytes, 256); };
+  StridedWorkspace w{};
+  w.bias = 0;
+  w.bias_l2 = seg((size_t)fpx::kHeads * np * np * sizeof(float));
+  w.mbias = 2 * w.bias_l2;
+  w.flags = w.mbias + seg((size_t)batch * np * sizeof(float));
+  w.total = w.flags + seg((size_t)batch * 2 * fpx::kTileFlagWords * sizeof(uint32_t));
+  return w;
+}
+
+// A [batch][4][n][32] operand with channel stride 1 the strided attention
+// kernel can read: non-negative strides that keep 16-byte rows aligned, and
+// (for K and V) a (b, h) slice that a buffer descriptor covers.
+bool strided_operand_ok(const int64_t s[3], int n, bool slice) {
+  for (int d = 0; d < 3; ++d)
+    if (s[d] < 0 || s[d] % 4 != 0) return false;
+  return !slice || ((int64_t)(n - 1) * s[2] + fpx::kHeadDim) * 4 < 0x7fffffffll;
+}
+
 }  // namespace
 
 extern "C" {
@@ -367,6 +395,64 @@ int fpx_attn_core_masked(const float* q, const float* k, const float* v, const f
 int fpx_attn_core(float* q, float* k, float* v, float* bias, float* out, int batch, int n,
                   void* stream) {
   return fpx_attn_core_masked(q, k, v, nullptr, 0, bias, n, out, batch, n, stream);
+}
+
+size_t fpx_attn_strided_workspace_bytes(int batch, int n) {
+  if (batch < 1 || n < 1 || n > kMaxN) return 0;
+  return strided_workspace(batch, n).total;
+}
+
+int fpx_attn_strided(const float* q, int64_t q_sb, int64_t q_sh, int64_t q_sn, const float* k,
+                     int64_t k_sb, int64_t k_sh, int64_t k_sn, const float* v, int64_t v_sb,
+                     int64_t v_sh, int64_t v_sn, const float* mask_bias, int64_t m_sb,
+                     int64_t m_sk, const float* bias, int64_t b_sh, int64_t b_sq, int64_t b_sk,
+                     float* out, int64_t o_sb, int64_t o_sh, int64_t o_sn, int batch, int n,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+  if (batch < 1 || n < 1 || n > kMaxN) return FPX_ERR_DIMS;
+  const int np = (int)round_up(n, kQueryTile);
+  if ((int64_t)batch * fpx::kHeads * (np / kQueryTile) > 0x7fffffffll) return FPX_ERR_DIMS;
+  fpx::AttnArgs a{};
+  const int64_t qs[3] = {q_sb, q_sh, q_sn}, ks[3] = {k_sb, k_sh, k_sn};
+  const int64_t vs[3] = {v_sb, v_sh, v_sn}, os[3] = {o_sb, o_sh, o_sn};
+  if (!strided_operand_ok(qs, n, false) || !strided_operand_ok(ks, n, true) ||
+      !strided_operand_ok(vs, n, true) || !strided_operand_ok(os, n, false))
+    return FPX_ERR_DIMS;
+  if (m_sb < 0 || m_sk < 0 || b_sh < 0 || b_sq < 0 || b_sk < 0) return FPX_ERR_DIMS;
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(out, 16))
+    return FPX_ERR_POINTER;
+  if (!aligned_or_null(mask_bias, 4) || !aligned_or_null(bias, 4)) return FPX_ERR_POINTER;
+  if (!aligned(workspace, 256)) return FPX_ERR_POINTER;
+  const StridedWorkspace ws = strided_workspace(batch, n);
+  if (workspace_bytes < ws.total) return FPX_ERR_WORKSPACE;
+  char* base = static_cast<char*>(workspace);
+  float* frag = as<float>(base + ws.bias);
+  float* frag_l2 = as<float>(base + ws.bias_l2);
+  float* mbias = as<float>(base + ws.mbias);
+  uint32_t* flags = as<uint32_t>(base + ws.flags);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e = fpx::launch_mask_rows(mask_bias, m_sb, m_sk, batch, n, np, mbias, flags, st);
+  if (e != hipSuccess) return status(e);
+  e = fpx::launch_stage_bias(bias, b_sh, b_sq, b_sk, n, np, frag, frag_l2, st);
+  if (e != hipSuccess) return status(e);
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.mbias = mbias;
+  a.mb_stride = np;
+  a.bias = frag;
+  a.bias_l2 = frag_l2;
+  a.out = out;
+  a.tile_flags = flags;
+  for (int d = 0; d < 3; ++d) {
+    a.qs[d] = qs[d];
+    a.ks[d] = ks[d];
+    a.vs[d] = vs[d];
+    a.os[d] = os[d];
+  }
+  a.batch = batch;
+  a.n = n;
+  a.np = np;
+  return status(fpx::launch_attention(fpx::kAttnStrided, a, st));
 }
 
 int fpx_layer_norm_c128(const float* x, int64_t rows_i, int64_t rows_j, int64_t stride_i,

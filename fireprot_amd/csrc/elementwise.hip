@@ -9,27 +9,33 @@
 namespace fpx {
 namespace {
 
-// One wavefront per outer row i: mbias[i][k] for k < np and the row's tile
+// One wavefront per row i < rows: mbias[i][k] for k < np and the row's tile
 // flags.  Word w of the first kTileFlagWords has bit t % 32 of tile t = 32w +
 // t % 32 set when some key of that 32-key tile has a nonzero mask bias (-0
 // counts as zero, since s + -0 == s); the next kTileFlagWords words do the
 // same for "every key of the tile has a nonzero mask bias".  Padded keys
-// (k >= n, -inf) count as masked.  inf * (mask - 1) is evaluated as two
-// rounded fp32 ops, as the native expression is
-// (patches/protenix/0005-*.patch:36-39).  np is a multiple of 64.
+// (k >= n, -inf) count as masked.  kFromMask: the source is a {0, 1} mask and
+// inf * (mask - 1) is evaluated as two rounded fp32 ops, as the native
+// expression is (patches/protenix/0005-*.patch:36-39); otherwise the source
+// already holds mask-bias values and is copied.  np is a multiple of 64.
+template <bool kFromMask>
 __global__ __launch_bounds__(256) void mask_rows_kernel(const float* __restrict__ mask,
-                                                        int64_t ms_i, int64_t ms_j, int n, int np,
-                                                        float inf, float* __restrict__ mbias,
+                                                        int64_t ms_i, int64_t ms_j, int rows,
+                                                        int n, int np, float inf,
+                                                        float* __restrict__ mbias,
                                                         uint32_t* __restrict__ flags) {
   const int lane = threadIdx.x & 63;
   const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (i >= n) return;
+  if (i >= rows) return;
   uint32_t any[kTileFlagWords] = {};
   uint32_t all[kTileFlagWords] = {};
   for (int k0 = 0; k0 < np; k0 += 64) {
     const int k = k0 + lane;
     float v = -INFINITY;
-    if (k < n) v = mask ? inf * (mask[i * ms_i + k * ms_j] - 1.0f) : 0.0f;
+    if (k < n) {
+      const float m = mask ? mask[i * ms_i + k * ms_j] : 0.0f;
+      v = !mask ? 0.0f : kFromMask ? inf * (m - 1.0f) : m;
+    }
     mbias[(int64_t)i * np + k] = v;
     const uint64_t nz = __ballot(v != 0.0f);
     const uint32_t lo = (uint32_t)nz;
@@ -67,6 +73,38 @@ __global__ void bias_pad_kernel(int n, int np, BiasT* __restrict__ tri_bias) {
     const int k = (int)(r % np);
     tri_bias[kFrag ? bias_frag_index(h, q, k, np) : bias_frag_index_bf16(h, q, k, np)] =
         (BiasT)0.0f;
+  }
+}
+
+// Both fragment-order copies of a caller's [4][n][n] bias with any strides.
+// One thread per 4 consecutive fragment floats (keys t..t+3 of one query, the
+// inverse of bias_frag_index): coalesced 16-byte stores, gathered loads that
+// the caches absorb (the bias is 4 n^2 floats, read once).
+__global__ __launch_bounds__(256) void stage_bias_kernel(const float* __restrict__ bias,
+                                                         int64_t sh, int64_t sq, int64_t sk,
+                                                         int n, int np, float* __restrict__ frag,
+                                                         float* __restrict__ frag_l2) {
+  const int64_t nt = np >> 5;
+  const int64_t total4 = (int64_t)kHeads * np * np / 4;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total4;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t f = idx * 4;
+    const int64_t blk = f >> 10;
+    const int within = (int)(f & 1023);
+    const int slot = (within >> 2) & 63;
+    const int q = (int)((blk / nt) % nt) * 32 + (slot & 31);
+    const int k0 = (int)(blk % nt) * 32 + (within >> 8) * 8 + (slot >> 5) * 4;
+    const int h = (int)(blk / (nt * nt));
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (bias != nullptr && q < n) {
+      const float* row = bias + h * sh + (int64_t)q * sq;
+      if (k0 + 0 < n) v.x = row[(int64_t)(k0 + 0) * sk];
+      if (k0 + 1 < n) v.y = row[(int64_t)(k0 + 1) * sk];
+      if (k0 + 2 < n) v.z = row[(int64_t)(k0 + 2) * sk];
+      if (k0 + 3 < n) v.w = row[(int64_t)(k0 + 3) * sk];
+    }
+    *(f32x4*)(frag + f) = v;
+    *(f32x4*)(frag_l2 + f) = v * kLog2e;
   }
 }
 
@@ -114,8 +152,8 @@ hipError_t launch_mask_bias(const float* mask, int64_t ms_i, int64_t ms_j, int n
                             bool bias_bf16, hipStream_t stream) {
   if (n <= 0) return hipSuccess;
   if (np % 64 || np > kTileFlagWords * 32 * 32) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(mask_rows_kernel, dim3((uint32_t)((n + 3) / 4)), dim3(256), 0, stream, mask,
-                     ms_i, ms_j, n, np, inf, mbias, tile_flags);
+  hipLaunchKernelGGL(mask_rows_kernel<true>, dim3((uint32_t)((n + 3) / 4)), dim3(256), 0, stream,
+                     mask, ms_i, ms_j, n, n, np, inf, mbias, tile_flags);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || np == n) return e;
   const int64_t total = (int64_t)kHeads * (np - n) * np;
@@ -135,6 +173,28 @@ hipError_t launch_mask_bias(const float* mask, int64_t ms_i, int64_t ms_j, int n
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
+}
+
+hipError_t launch_mask_rows(const float* values, int64_t vs_i, int64_t vs_k, int rows, int n,
+                            int np, float* mbias, uint32_t* tile_flags, hipStream_t stream) {
+  if (rows <= 0 || n <= 0) return hipSuccess;
+  if (np % 64 || np < n || np > kTileFlagWords * 32 * 32) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(mask_rows_kernel<false>, dim3((uint32_t)((rows + 3) / 4)), dim3(256), 0,
+                     stream, values, vs_i, vs_k, rows, n, np, 0.0f, mbias, tile_flags);
+  return hipGetLastError();
+}
+
+hipError_t launch_stage_bias(const float* bias, int64_t sh, int64_t sq, int64_t sk, int n, int np,
+                             float* frag, float* frag_l2, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  if (np % 32 || np < n) return hipErrorInvalidValue;
+  const int64_t total4 = (int64_t)kHeads * np * np / 4;
+  int64_t blocks = (total4 + 255) / 256;
+  const int64_t cap = (int64_t)device_cu_count() * 32;
+  if (blocks > cap) blocks = cap;
+  hipLaunchKernelGGL(stage_bias_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream, bias, sh, sq,
+                     sk, n, np, frag, frag_l2);
+  return hipGetLastError();
 }
 
 hipError_t launch_layer_norm(const float* x, int64_t rows_i, int64_t rows_j, int64_t xs_i,

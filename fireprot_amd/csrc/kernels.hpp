@@ -27,7 +27,13 @@ namespace fpx {
 //                q, k, v, out : [B][n][H][32] (strides n*128, 32, 128, 1)
 //                bias : [H][n][bias_stride]  (batch stride 0)
 //                mbias: nullable, [B] rows of n values, row stride mb_stride
-enum AttnLayout { kAttnBlock = 0, kAttnHeadLast = 1 };
+// kAttnStrided: any caller layout with channel stride 1:
+//                q, k, v, out : element (b, h, j, c) at b*s[0] + h*s[1] + j*s[2] + c
+//                               (qs, ks, vs, os), rows 16-byte aligned
+//                mbias, tile_flags, bias, bias_l2 : staged as for kAttnBlock
+//                               (launch_mask_rows, launch_stage_bias), np a
+//                               multiple of 128
+enum AttnLayout { kAttnBlock = 0, kAttnHeadLast = 1, kAttnStrided = 2 };
 
 // Words of per-row tile flags: 32-key tiles of np <= 4096 keys.
 constexpr int kTileFlagWords = 4;
@@ -45,6 +51,10 @@ struct AttnArgs {
   const float* gate;
   float* out;
   const uint32_t* tile_flags;
+  int64_t qs[3];  // kAttnStrided: (batch, head, row) element strides
+  int64_t ks[3];
+  int64_t vs[3];
+  int64_t os[3];
   int batch;
   int n;
   int np;
@@ -102,6 +112,16 @@ hipError_t launch_projection(int mode, const ProjArgs& args, hipStream_t stream)
 hipError_t launch_mask_bias(const float* mask, int64_t ms_i, int64_t ms_j, int n, int np,
                             float inf, float* mbias, uint32_t* tile_flags, void* tri_bias,
                             bool bias_bf16, hipStream_t stream);
+
+// Staging for kAttnStrided.  launch_mask_rows: mbias[i][k] = values[i*vs_i +
+// k*vs_k] for k < n (0 when values is null), -inf for n <= k < np, and the
+// tile flags, for rows i < rows.  launch_stage_bias: both fragment-order
+// copies (as is, and scaled by log2(e)) of bias[h][q][k] read at h*sh + q*sq +
+// k*sk, 0 for q or k >= n (and everywhere when bias is null).
+hipError_t launch_mask_rows(const float* values, int64_t vs_i, int64_t vs_k, int rows, int n,
+                            int np, float* mbias, uint32_t* tile_flags, hipStream_t stream);
+hipError_t launch_stage_bias(const float* bias, int64_t sh, int64_t sq, int64_t sk, int n, int np,
+                             float* frag, float* frag_l2, hipStream_t stream);
 
 // LayerNorm over 128 channels of rows x[i][j] at x + i*xs_i + j*xs_j,
 // written contiguously to y[(i*rows_j + j)*128 + c].

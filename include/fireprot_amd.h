@@ -148,6 +148,37 @@ int fpx_attn_core_masked(const float* q, const float* k, const float* v, const f
                          int64_t mask_bias_stride, const float* bias, int64_t bias_row_stride,
                          float* out, int batch, int n, void* stream);
 
+/* Bytes of workspace fpx_attn_strided needs for (batch, n); 0 for unsupported
+ * sizes. */
+size_t fpx_attn_strided_workspace_bytes(int batch, int n);
+
+/* OpenFold3's _attention(query, key, value, [mask_bias, tri_bias]) in one
+ * call, for any strides: out = softmax(fl(fl(q.k^T + mask_bias) + tri_bias)) v
+ * per (b, h), the order of `for b in biases: a += b`.  Replaces the scoped
+ * dispatch of adapters/openfold3/attention.py:121-148 (whose fused path is a
+ * QK einsum, the fireprot_softmax_f32 C ABI of backends/amd/softmax_fp32.py:
+ * 57-84 and a PV einsum) with a single fused launch; the wire layouts are
+ * those accepted by softmax_fp32.py:19-38 and attention.py:99-119.
+ *   q, k, v, out  [batch][4][n][32]; element (b, h, j, c) at
+ *                 b*s_b + h*s_h + j*s_n + c.  Strides >= 0 and multiples of 4,
+ *                 pointers 16-byte aligned; q already scaled by 1/sqrt(32);
+ *                 out must not overlap q, k, v or the workspace.
+ *   mask_bias     nullable additive bias [batch or 1][1][1][n]: value (b, k) at
+ *                 b*m_sb + k*m_sk (m_sb = 0 broadcasts one row, m_sk = n is the
+ *                 transposed pair mask of the ending node)
+ *   bias          nullable [1][4][n][n]: value (h, q, k) at h*b_sh + q*b_sq +
+ *                 k*b_sk (head-first, head-last and transposed views alike)
+ *   workspace     fpx_attn_strided_workspace_bytes(batch, n) bytes, 256-aligned;
+ *                 the bias and mask are staged there in the kernel's order
+ * Supported: 1 <= n <= 4096, batch >= 1.  Logits keep FP32 throughout, so
+ * OpenFold3's use_high_precision flag needs no separate path. */
+int fpx_attn_strided(const float* q, int64_t q_sb, int64_t q_sh, int64_t q_sn, const float* k,
+                     int64_t k_sb, int64_t k_sh, int64_t k_sn, const float* v, int64_t v_sb,
+                     int64_t v_sh, int64_t v_sn, const float* mask_bias, int64_t m_sb,
+                     int64_t m_sk, const float* bias, int64_t b_sh, int64_t b_sq, int64_t b_sk,
+                     float* out, int64_t o_sb, int64_t o_sh, int64_t o_sn, int batch, int n,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
 /* LayerNorm over 128 channels of rows x[i][j] read at x + i*stride_i + j*stride_j
  * (channel stride 1), written contiguously to y[rows_i][rows_j][128].  Covers
  * both the contiguous pair LN (kernels/amd/fireprot_amd_ops.cu:27-64,

@@ -57,6 +57,43 @@ def test_abi_version_and_workspace_sizes(lib):
         assert lib.fpx_tri_attn_workspace_bytes(*bad) == 0
 
 
+def test_strided_workspace_sizes(lib):
+    seg = lambda b: -(-b // 256) * 256  # noqa: E731
+    for batch, n in ((1, 1), (7, 96), (1536, 1000), (1536, 1536), (3, 4096)):
+        np_ = -(-n // 128) * 128
+        # two fragment-order bias copies; mask-bias rows; tile flags
+        expected = 2 * seg(4 * np_ * np_ * 4) + seg(batch * np_ * 4) + seg(batch * 8 * 4)
+        assert lib.fpx_attn_strided_workspace_bytes(batch, n) == expected
+    for bad in ((0, 8), (2, 0), (2, 4097)):
+        assert lib.fpx_attn_strided_workspace_bytes(*bad) == 0
+
+
+def _strided_args(**override):
+    args = dict(q=256, qb=1024, qh=32, qn=128, k=256, kb=1024, kh=32, kn=128, v=256, vb=1024,
+                vh=32, vn=128, mask=None, mb=0, mk=1, bias=None, bh=0, bq=0, bk=0, out=512,
+                ob=1024, oh=32, on=128, batch=2, n=8, ws=256, ws_bytes=1 << 30, stream=None)
+    args.update(override)
+    return list(args.values())
+
+
+def test_strided_guards(lib):
+    f = lib.fpx_attn_strided
+    assert f(*_strided_args(n=0)) == 2
+    assert f(*_strided_args(n=4097)) == 2
+    assert f(*_strided_args(batch=0)) == 2
+    assert f(*_strided_args(qn=130)) == 2                           # rows not 16-byte aligned
+    assert f(*_strided_args(kh=-32)) == 2
+    assert f(*_strided_args(vn=1 << 30, n=4096)) == 2               # (b, h) slice beyond 2 GiB
+    assert f(*_strided_args(mk=-1)) == 2
+    assert f(*_strided_args(bq=-1)) == 2
+    assert f(*_strided_args(q=None)) == 3
+    assert f(*_strided_args(out=260)) == 3
+    assert f(*_strided_args(mask=2)) == 3
+    assert f(*_strided_args(bias=6)) == 3
+    assert f(*_strided_args(ws=128)) == 3
+    assert f(*_strided_args(ws_bytes=1)) == 4
+
+
 def _block_args(**override):
     args = dict(dtype=0, z=256, zs0=64 * 128, zs1=128, mask=None, ms0=0, ms1=0, ln_w=None,
                 ln_b=None, eps=1e-5, w_qkvg=256, b_g=None, w_bias=256, w_o=256, b_o=None,
