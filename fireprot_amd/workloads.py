@@ -75,6 +75,37 @@ def make_weights(bias_scale: float = 1.0, channels: int = 128, heads: int = 4,
     return weights
 
 
+TRIMUL_WEIGHT_SEED = 4242
+
+
+def make_trimul_weights(std: float = 0.1, *, biases: bool = False, affine: bool = False,
+                        seed: int = TRIMUL_WEIGHT_SEED,
+                        channels: int = 128) -> dict[str, torch.Tensor | None]:
+    """Random-init weights of a triangle multiplicative update (c_z = c_hidden =
+    128), every projection N(0, std^2) as the reference's operator tests draw
+    them (tests/operators/test_packed_triangle.py:96-97).  ``biases`` adds
+    N(0, std^2) biases to the six projections (OpenFold-style modules);
+    ``affine`` draws non-trivial LayerNorm scales and shifts."""
+    g = torch.Generator().manual_seed(seed)
+
+    def normal(*shape, scale=std):
+        return torch.randn(*shape, generator=g, dtype=torch.float32) * scale
+
+    w: dict[str, torch.Tensor | None] = {
+        "ln_in_w": torch.ones(channels), "ln_in_b": torch.zeros(channels),
+        "ln_out_w": torch.ones(channels), "ln_out_b": torch.zeros(channels),
+    }
+    for name in ("w_a_p", "w_a_g", "w_b_p", "w_b_g", "w_z", "w_g"):
+        w[name] = normal(channels, channels)
+    for name in ("b_a_p", "b_a_g", "b_b_p", "b_b_g", "b_z", "b_g"):
+        w[name] = normal(channels) if biases else None
+    if affine:
+        for side in ("in", "out"):
+            w[f"ln_{side}_w"] = 1.0 + normal(channels, scale=0.1)
+            w[f"ln_{side}_b"] = normal(channels, scale=0.1)
+    return w
+
+
 def make_pair(n: int, z_scale: float = 1.0, channels: int = 128) -> torch.Tensor:
     g = torch.Generator().manual_seed(Z_SEED_BASE + n)
     z = torch.randn(n, n, channels, generator=g, dtype=torch.float32)
