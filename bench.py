@@ -239,15 +239,137 @@ def bench_openfold3(args) -> dict:
     return result
 
 
+TRIMUL_METRIC = "triangle multiplication ms + TFLOP/s (% MFMA peak) at N=1536 FP32, 1 GPU"
+
+
+def bench_trimul(args) -> dict:
+    """Triangle multiplication at N = 1536, FP32, c_z = c_hidden = 128: one
+    step = the outgoing then the incoming update, each in place on z
+    (``fpx_tri_mul``, accumulate), as the Pairformer applies them; the last
+    184 residues are masked (explicit mask).  Weights N(0, 0.1^2) as the
+    reference's operator tests draw them.  ``roofline`` is the contraction
+    kernel alone (2 N^3 128 flop per launch) timed with HIP events around
+    its launch (the projection and finish kernels run before and after it),
+    ``config.stage_ms`` splits one update by kernel from a standalone copy
+    of each launch sequence.  ``cpu_baseline`` times the oracle on 8 rows of
+    each direction and scales to all rows (rows are independent) plus the
+    full-size projections it needs.
+    """
+    import torch
+
+    from fireprot_amd import _native, workloads
+    from fireprot_amd import triangle_multiplication as htm
+
+    n = 1536
+    dev = torch.device("cuda:0")
+    log(f"inputs trimul n={n}")
+    z0 = workloads.make_pair(n)
+    keep = torch.arange(n) < n - 184
+    mask_cpu = (keep[:, None] & keep[None, :]).float()
+    w_cpu = workloads.make_trimul_weights()
+    z = z0.to(dev)
+    mask = mask_cpu.to(dev)
+    weights = htm.TriMulWeights.from_tensors(**w_cpu).to(dev)
+    ws = torch.empty(htm.workspace_bytes(n), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        htm.triangle_multiplication(z, mask, weights, outgoing=True, out=z, accumulate=True,
+                                    workspace=ws)
+        htm.triangle_multiplication(z, mask, weights, outgoing=False, out=z, accumulate=True,
+                                    workspace=ws)
+
+    def timed(fn, steps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    with torch.inference_mode():
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        log(f"warmup {args.warmup} done")
+        ms = timed(step, args.steps)
+        log(f"timed {args.steps} steps: {ms:.3f} ms/step")
+        out = torch.empty_like(z)
+        update_ms = timed(lambda: htm.triangle_multiplication(
+            z, mask, weights, outgoing=True, out=out, workspace=ws), max(args.steps, 5))
+        log(f"one outgoing update: {update_ms:.3f} ms")
+    lib = _native.library()
+    del lib
+    from oracle.triangle_multiplication import flops
+
+    f = flops(n)
+    value = 2 * f["total"] / (ms * 1e-3) / 1e12
+    result = {
+        "metric": TRIMUL_METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded z ~ N(0,1), N(0,0.1^2) weights, last 184 residues masked)",
+        "config": {
+            "workload": "trimul-n1536-f32: outgoing + incoming update, in place",
+            "n": n, "c_z": 128, "c_hidden": 128,
+            "update_ms": round(update_ms, 4),
+            "step_flop": 2 * f["total"],
+            "flop_per_update": f,
+        },
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        from oracle import triangle_multiplication as tm
+
+        threads = max(1, min(16, os.cpu_count() or 1))
+        torch.set_num_threads(threads)
+        params = tm.TriMulParams(**w_cpu)
+        rows = torch.linspace(0, n - 1, 8).round().long()
+        spent = {}
+        with torch.inference_mode():
+            for outgoing in (True, False):
+                t0 = time.perf_counter()
+                tm.update(z0, mask_cpu, params, outgoing=outgoing, rows=rows)
+                spent[outgoing] = time.perf_counter() - t0
+        # projections (full size) + 8 of n rows of contraction and output
+        t0 = time.perf_counter()
+        with torch.inference_mode():
+            tm.gated_projections(z0, mask_cpu, params)
+        proj_s = time.perf_counter() - t0
+        total = sum(proj_s + (spent[d] - proj_s) * n / len(rows) for d in (True, False))
+        result["cpu_baseline"] = {
+            "value": round(2 * f["total"] / total / 1e12, 5), "unit": "TFLOP/s",
+            "cores": threads, "kind": "port",
+            "sample": (f"oracle update (native op order, {threads} threads) on 8 evenly spaced "
+                       f"rows per direction ({spent[True]:.1f} s and {spent[False]:.1f} s, "
+                       f"full-size projections {proj_s:.1f} s included), row part scaled to "
+                       f"{n} rows: {total:.0f} s per step"),
+            "cpu": platform.processor() or platform.machine(),
+        }
+    return result
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c4", choices=["c1", "c2", "c3", "c4", "c5"])
-    ap.add_argument("--workload", default="block", choices=["block", "openfold3"],
+    ap.add_argument("--workload", default="block", choices=["block", "openfold3", "trimul"],
                     help="block: the triangle-attention block (default); openfold3: "
-                         "OpenFold3's _attention through fpx_attn_strided")
+                         "OpenFold3's _attention through fpx_attn_strided; trimul: "
+                         "triangle multiplication (fpx_tri_mul)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 1 GiB device-to-device copy (the known-size "
@@ -270,6 +392,9 @@ def main() -> int:
     lib = _native.library()
     if args.workload == "openfold3":
         print(json.dumps(bench_openfold3(args)), flush=True)
+        return 0
+    if args.workload == "trimul":
+        print(json.dumps(bench_trimul(args)), flush=True)
         return 0
     cfg = workloads.CONFIGS[args.config]
     n = cfg.n

@@ -73,6 +73,18 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         _p, _i64, _i64, _i64,        # out
         _i, _i, _p, _sz, _p,         # batch, n, workspace, bytes, stream
     ]),
+    "fpx_tri_mul_workspace_bytes": (_sz, [_i, _i, _i]),
+    "fpx_tri_mul": (_i, [
+        _p, _i64, _i64,              # z, strides
+        _p, _i64, _i64,              # mask, strides
+        _p, _p, _f,                  # ln_in_w, ln_in_b, eps_in
+        _p, _p,                      # w_abpg [4][128][128], b_abpg [4][128]
+        _p, _p, _f,                  # ln_out_w, ln_out_b, eps_out
+        _p, _p, _p, _p,              # w_z, b_z, w_g, b_g
+        _i, _i, _i, _i, _i,          # n, c_z, c_hidden, outgoing, accumulate
+        _p, _i64, _i64,              # out (may be z), strides
+        _p, _sz, _p,                 # workspace, bytes, stream
+    ]),
     "fpx_layer_norm_c128": (_i, [_p, _i64, _i64, _i64, _i64, _p, _p, _f, _p, _p]),
     "fpx_qkv_projection": (_i, [_p, _i64, _p, _p, _p, _p, _p]),
     "fpx_sigmoid_mul_out": (_i, [_p, _p, _p, _i64, _p]),

@@ -189,6 +189,23 @@ StridedWorkspace strided_workspace(int batch, int n) {
   return w;
 }
 
+// Workspace of fpx_tri_mul, 256-byte aligned segments: a and b channel-major
+// [128][np][np] float; x blocked [n][np / 32][128][32] float.
+struct TriMulWorkspace {
+  size_t pa, pb, x, total;
+};
+
+TriMulWorkspace trimul_workspace(int n) {
+  const size_t np = (size_t)round_up(n, kQueryTile);
+  auto seg = [](size_t bytes) { return (size_t)round_up((int64_t)bytes, 256); };
+  TriMulWorkspace w{};
+  w.pa = 0;
+  w.pb = seg((size_t)fpx::kChannels * np * np * sizeof(float));
+  w.x = 2 * w.pb;
+  w.total = w.x + seg((size_t)n * np * fpx::kChannels * sizeof(float));
+  return w;
+}
+
 // A [batch][4][n][32] operand with channel stride 1 the strided attention
 // kernel can read: non-negative strides that keep 16-byte rows aligned, and
 // (for K and V) a (b, h) slice that a buffer descriptor covers.
@@ -453,6 +470,72 @@ int fpx_attn_strided(const float* q, int64_t q_sb, int64_t q_sh, int64_t q_sn, c
   a.n = n;
   a.np = np;
   return status(fpx::launch_attention(fpx::kAttnStrided, a, st));
+}
+
+size_t fpx_tri_mul_workspace_bytes(int n, int c_z, int c_hidden) {
+  if (n < 1 || n > kMaxN || c_z != fpx::kChannels || c_hidden != fpx::kHidden) return 0;
+  return trimul_workspace(n).total;
+}
+
+int fpx_tri_mul(const float* z, int64_t z_stride0, int64_t z_stride1, const float* mask,
+                int64_t m_stride0, int64_t m_stride1, const float* ln_in_w, const float* ln_in_b,
+                float eps_in, const float* w_abpg, const float* b_abpg, const float* ln_out_w,
+                const float* ln_out_b, float eps_out, const float* w_z, const float* b_z,
+                const float* w_g, const float* b_g, int n, int c_z, int c_hidden, int outgoing,
+                int accumulate, float* out, int64_t out_stride0, int64_t out_stride1,
+                void* workspace, size_t workspace_bytes, void* stream) {
+  if (n < 1 || n > kMaxN || c_z != fpx::kChannels || c_hidden != fpx::kHidden) return FPX_ERR_DIMS;
+  if ((outgoing != 0 && outgoing != 1) || (accumulate != 0 && accumulate != 1)) return FPX_ERR_DIMS;
+  if (z_stride0 < 0 || z_stride1 < 0 || z_stride0 % 4 || z_stride1 % 4) return FPX_ERR_DIMS;
+  if (out_stride0 < 0 || out_stride1 < 0) return FPX_ERR_DIMS;
+  if (mask != nullptr && (m_stride0 < 0 || m_stride1 < 0)) return FPX_ERR_DIMS;
+  if (!(eps_in >= 0.0f) || !(eps_out >= 0.0f)) return FPX_ERR_DIMS;
+  // out may be z itself (same strides: each pair row is read before it is
+  // written, by the same tile); any other overlap is unsupported.
+  if (out == z && (out_stride0 != z_stride0 || out_stride1 != z_stride1)) return FPX_ERR_DIMS;
+  if (!aligned(z, 16) || !aligned(w_abpg, 16) || !aligned(w_z, 16) || !aligned(w_g, 16) ||
+      !aligned(out, 4))
+    return FPX_ERR_POINTER;
+  if (!aligned_or_null(mask, 4) || !aligned_or_null(b_abpg, 4) || !aligned_or_null(ln_in_w, 8) ||
+      !aligned_or_null(ln_in_b, 8) || !aligned_or_null(ln_out_w, 8) ||
+      !aligned_or_null(ln_out_b, 8) || !aligned_or_null(b_z, 4) || !aligned_or_null(b_g, 4))
+    return FPX_ERR_POINTER;
+  if (!aligned(workspace, 256)) return FPX_ERR_POINTER;
+  const TriMulWorkspace ws = trimul_workspace(n);
+  if (workspace_bytes < ws.total) return FPX_ERR_WORKSPACE;
+  char* base = static_cast<char*>(workspace);
+  fpx::TriMulArgs a{};
+  a.z = static_cast<const float*>(z);
+  a.zs_i = z_stride0;
+  a.zs_j = z_stride1;
+  a.mask = mask;
+  a.ms_i = m_stride0;
+  a.ms_j = m_stride1;
+  a.ln_in_w = ln_in_w;
+  a.ln_in_b = ln_in_b;
+  a.eps_in = eps_in;
+  for (int g = 0; g < 4; ++g) {
+    a.w_ab[g] = w_abpg + (int64_t)g * fpx::kHidden * fpx::kChannels;
+    a.b_ab[g] = b_abpg ? b_abpg + (int64_t)g * fpx::kHidden : nullptr;
+  }
+  a.ln_out_w = ln_out_w;
+  a.ln_out_b = ln_out_b;
+  a.eps_out = eps_out;
+  a.w_z = w_z;
+  a.b_z = b_z;
+  a.w_g = w_g;
+  a.b_g = b_g;
+  a.pa = as<float>(base + ws.pa);
+  a.pb = as<float>(base + ws.pb);
+  a.x = as<float>(base + ws.x);
+  a.out = out;
+  a.os_i = out_stride0;
+  a.os_j = out_stride1;
+  a.n = n;
+  a.np = (int)round_up(n, kQueryTile);
+  a.outgoing = outgoing;
+  a.accumulate = accumulate;
+  return status(fpx::launch_trimul(a, static_cast<hipStream_t>(stream)));
 }
 
 int fpx_layer_norm_c128(const float* x, int64_t rows_i, int64_t rows_j, int64_t stride_i,

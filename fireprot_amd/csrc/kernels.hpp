@@ -182,6 +182,44 @@ struct Bf16AttnArgs {
 hipError_t launch_projection_bf16(int mode, const Bf16ProjArgs& args, hipStream_t stream);
 hipError_t launch_attention_bf16(const Bf16AttnArgs& args, hipStream_t stream);
 
+// -------------------------------------------------- triangle multiplication
+// Outgoing / incoming triangle multiplicative update, c_z = c_hidden = 128
+// (trimul.hip).  Workspace roles: a and b channel-major [128][np][np] (rows
+// of the contraction frame, keys contiguous; rows >= n unused, keys >= n
+// zero), x blocked [n][np / 32][128][32].  np is a multiple of 128.
+struct TriMulArgs {
+  const float* z;
+  int64_t zs_i;
+  int64_t zs_j;
+  const float* mask;  // nullable {0,1} (or any) multiplier of a and b
+  int64_t ms_i;
+  int64_t ms_j;
+  const float* ln_in_w;
+  const float* ln_in_b;
+  float eps_in;
+  const float* w_ab[4];  // a_p, a_g, b_p, b_g: [128 out][128 in]
+  const float* b_ab[4];  // nullable
+  const float* ln_out_w;
+  const float* ln_out_b;
+  float eps_out;
+  const float* w_z;
+  const float* b_z;
+  const float* w_g;
+  const float* b_g;
+  float* pa;
+  float* pb;
+  float* x;
+  float* out;
+  int64_t os_i;
+  int64_t os_j;
+  int n;
+  int np;
+  int outgoing;
+  int accumulate;  // out = out + u (the in-place residual) instead of u
+};
+
+hipError_t launch_trimul(const TriMulArgs& args, hipStream_t stream);
+
 int device_cu_count();
 
 }  // namespace fpx

@@ -1,0 +1,436 @@
+// Triangle multiplicative update (outgoing and incoming) on the CDNA4 FP32
+// matrix cores, c_z = c_hidden = 128.
+//
+//   a[r, k, c] = mask[r, k] * sigmoid(LN_in(z) W_a_g^T + b)[c] * (LN_in(z) W_a_p^T + b)[c]
+//   b[r, k, c] = the same with the b weights
+//   x[i, j, c] = sum_k a[i, k, c] b[j, k, c]
+//   u[i, j, :] = sigmoid(LN_in(z[i, j]) W_g^T + b_g) * (LN_out(x[i, j]) W_z^T + b_z)
+//   out        = u, or z + u (the residual update)
+//
+// in the contraction frame (r, k): z[r, k] for the outgoing update and
+// z[k, r] for the incoming one, so both directions are one kernel chain; the
+// incoming read of z^T goes through strides, with no transposed copy.
+//
+// Three launches:
+//   trimul_project_kernel  LN_in, the four 128x128 projections, sigmoid gates
+//                          and the mask; writes a and b channel-major
+//                          ([128][np rows][np keys], keys contiguous), the
+//                          operand layout of the contraction
+//   trimul_contract_kernel x_c = A_c B_c^T for the 128 channels: a batched
+//                          GEMM on 128 x 128 output tiles, 32-key stages
+//                          double-buffered in LDS, XCD-aware tile order
+//   trimul_finish_kernel   LN_out(x) W_z^T and LN_in(z) W_g^T for 32 pairs
+//                          per tile, the sigmoid gate and the in-place write
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace fpx {
+namespace {
+
+constexpr int kRows = 32;                 // pair rows per projection tile
+constexpr int kLds = kChannels + 4;       // padded LDS row (floats)
+constexpr int kGemmTile = 128;            // contraction output tile (rows and columns)
+constexpr int kKStage = 32;               // contraction keys per LDS stage
+constexpr int kKPad = kKStage + 4;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer(const float* base, int64_t bytes) {
+  // dword 3 = 0x00020000: raw 32-bit buffer access on gfx9-family parts.
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+__device__ __forceinline__ f32x4 buffer_f4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+// [128 x 32] weight fragment of output columns col (lane l32) for the
+// B operand: lane half h holds input channels 64h .. 64h + 63.
+__device__ __forceinline__ void load_fragment(const float* w, int col, int half, float* wf) {
+  const float* src = w + (int64_t)col * kChannels + 64 * half;
+#pragma unroll
+  for (int t = 0; t < 16; ++t) {
+    const f32x4 v = *(const f32x4*)(src + 4 * t);
+    wf[4 * t + 0] = v.x;
+    wf[4 * t + 1] = v.y;
+    wf[4 * t + 2] = v.z;
+    wf[4 * t + 3] = v.w;
+  }
+}
+
+// ------------------------------------------------------------ projection
+// Persistent; 8 waves: waves 0-3 produce a, waves 4-7 produce b, each for 32
+// channels, with both the projection and the gate fragments resident (two
+// accumulators, 128 MFMAs per wave per 32-row tile).  The next tile's raw
+// rows are fetched two tiles ahead and normalised into the second LDS buffer
+// while this tile's MFMAs run.
+constexpr int kProjWaves = 8;
+
+__global__ __launch_bounds__(kProjWaves * 64) void trimul_project_kernel(TriMulArgs a, int tiles_k,
+                                                                         int ntiles) {
+  constexpr int kThreads = kProjWaves * 64;
+  constexpr int kRowsPerWave = kRows / kProjWaves;
+  __shared__ __attribute__((aligned(16))) float xs[2][kRows][kLds];
+  __shared__ float ms[2][kRows];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+  const int side = w >> 2;             // 0: a, 1: b
+  const int col = 32 * (w & 3) + l32;  // hidden channel of this lane
+
+  float wp[64], wg[64];
+  load_fragment(a.w_ab[2 * side], col, half, wp);
+  load_fragment(a.w_ab[2 * side + 1], col, half, wg);
+  const float bp = a.b_ab[2 * side] ? a.b_ab[2 * side][col] : 0.f;
+  const float bq = a.b_ab[2 * side + 1] ? a.b_ab[2 * side + 1][col] : 0.f;
+  f32x2 lnw = {1.f, 1.f}, lnb = {0.f, 0.f};
+  if (a.ln_in_w) lnw = *(const f32x2*)(a.ln_in_w + 2 * lane);
+  if (a.ln_in_b) lnb = *(const f32x2*)(a.ln_in_b + 2 * lane);
+
+  // Contraction frame: pair (r, k) is z[r, k] (outgoing) or z[k, r] (incoming).
+  const int64_t zr = a.outgoing ? a.zs_i : a.zs_j;
+  const int64_t zk = a.outgoing ? a.zs_j : a.zs_i;
+  const int64_t mr = a.outgoing ? a.ms_i : a.ms_j;
+  const int64_t mk = a.outgoing ? a.ms_j : a.ms_i;
+  const int n = a.n;
+  const int np = a.np;
+
+  f32x2 st[kRowsPerWave];
+  float st_mask = 0.f;
+
+  auto fetch = [&](int tile) {
+    const int r = tile / tiles_k;
+    const int k0 = (tile % tiles_k) * kRows;
+#pragma unroll
+    for (int rr = 0; rr < kRowsPerWave; ++rr) {
+      const int k = k0 + w * kRowsPerWave + rr;
+      st[rr] = k < n ? *(const f32x2*)(a.z + (int64_t)r * zr + (int64_t)k * zk + 2 * lane)
+                     : f32x2{0.f, 0.f};
+    }
+    if (tid < kRows) {
+      const int k = k0 + tid;
+      st_mask = k < n ? (a.mask ? a.mask[(int64_t)r * mr + (int64_t)k * mk] : 1.f) : 0.f;
+    }
+  };
+
+  auto stage = [&](int buf) {
+#pragma unroll
+    for (int rr = 0; rr < kRowsPerWave; ++rr) {
+      const int row = w * kRowsPerWave + rr;
+      float d0, d1, rstd;
+      ln_stats_c128(st[rr].x, st[rr].y, a.eps_in, d0, d1, rstd);
+      *(f32x2*)&xs[buf][row][2 * lane] =
+          f32x2{d0 * rstd * lnw.x + lnb.x, d1 * rstd * lnw.y + lnb.y};
+    }
+    if (tid < kRows) ms[buf][tid] = st_mask;
+  };
+
+  auto epilogue = [&](int tile, int buf, const f32x16& acc_p, const f32x16& acc_g) {
+    const int r = tile / tiles_k;
+    const int k0 = (tile % tiles_k) * kRows;
+    float* dst = (side ? a.pb : a.pa) + ((int64_t)col * np + r) * np + k0 + 4 * half;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int kk = 8 * rr + 4 * half + e;
+        const float m = ms[buf][kk];
+        // native order: a = mask; a = a * sigmoid(g); a = a * p
+        const float val = (m * sigmoidf_(acc_g[4 * rr + e] + bq)) * (acc_p[4 * rr + e] + bp);
+        v[e] = k0 + kk < n ? val : 0.f;
+      }
+      *(f32x4*)(dst + 8 * rr) = f32x4{v[0], v[1], v[2], v[3]};
+    }
+  };
+
+  __builtin_amdgcn_s_waitcnt(0);
+  int tile = blockIdx.x;  // grid <= ntiles
+  fetch(tile);
+  stage(0);
+  int next = tile + (int)gridDim.x;
+  if (next < ntiles) fetch(next);
+  __syncthreads();
+  for (int buf = 0; tile < ntiles; buf ^= 1) {
+    f32x16 acc_p = {}, acc_g = {};
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const f32x4 av = *(const f32x4*)&xs[buf][l32][64 * half + 4 * t];
+      acc_p = mfma32(av.x, wp[4 * t + 0], acc_p);
+      acc_g = mfma32(av.x, wg[4 * t + 0], acc_g);
+      acc_p = mfma32(av.y, wp[4 * t + 1], acc_p);
+      acc_g = mfma32(av.y, wg[4 * t + 1], acc_g);
+      acc_p = mfma32(av.z, wp[4 * t + 2], acc_p);
+      acc_g = mfma32(av.z, wg[4 * t + 2], acc_g);
+      acc_p = mfma32(av.w, wp[4 * t + 3], acc_p);
+      acc_g = mfma32(av.w, wg[4 * t + 3], acc_g);
+    }
+    if (next < ntiles) {
+      stage(buf ^ 1);
+      if (next + (int)gridDim.x < ntiles) fetch(next + gridDim.x);
+    }
+    epilogue(tile, buf, acc_p, acc_g);
+    __syncthreads();
+    tile = next;
+    next += gridDim.x;
+  }
+}
+
+// ----------------------------------------------------------- contraction
+// One work-group = (channel c, 128 rows i, 128 columns j); four waves, each a
+// 64 x 64 quadrant as 2 x 2 blocks of v_mfma_f32_32x32x2_f32.  Per 32-key
+// stage a lane half h feeds keys 16h .. 16h + 15 (the sum over keys is
+// order-free, so both operands are read as contiguous row segments, four
+// b128 LDS reads per 32-row block).  Stages are double-buffered: the next
+// stage's global loads are in flight while this one is multiplied.
+// Work-groups of one channel are consecutive in the logical order, and
+// xcd_remap gives each XCD a contiguous range, so the A and B row panels a
+// range touches stay in that XCD's L2.
+__global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const float* __restrict__ pa,
+                                                                 const float* __restrict__ pb,
+                                                                 float* __restrict__ x, int n,
+                                                                 int np, int tiles,
+                                                                 uint32_t total) {
+  __shared__ __attribute__((aligned(16))) float As[2][kGemmTile][kKPad];
+  __shared__ __attribute__((aligned(16))) float Bs[2][kGemmTile][kKPad];
+
+  const uint32_t logical = xcd_remap(blockIdx.x, total);
+  const int per_channel = tiles * tiles;
+  const int c = (int)(logical / per_channel);
+  const int rem = (int)(logical % per_channel);
+  const int i0 = (rem / tiles) * kGemmTile;
+  const int j0 = (rem % tiles) * kGemmTile;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+  const int wi = (w >> 1) * 64;
+  const int wj = (w & 1) * 64;
+
+  const int64_t slice = (int64_t)np * np;
+  const __amdgpu_buffer_rsrc_t ra = buffer(pa + c * slice, slice * 4);
+  const __amdgpu_buffer_rsrc_t rb = buffer(pb + c * slice, slice * 4);
+  // Thread (row = tid / 8 + 32u, keys 4 * (tid % 8) .. +3) of each stage.
+  const int lrow = tid >> 3;
+  const int lc4 = (tid & 7) * 4;
+  const uint32_t va = (uint32_t)(((int64_t)(i0 + lrow) * np + lc4) * 4);
+  const uint32_t vb = (uint32_t)(((int64_t)(j0 + lrow) * np + lc4) * 4);
+  const uint32_t panel = (uint32_t)(32 * np * 4);  // 32 rows further down
+  const int nk = np / kKStage;
+
+  f32x4 ga[4], gb[4];
+  auto load = [&](int kt) {
+    const uint32_t s = (uint32_t)kt * (kKStage * 4);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      ga[u] = buffer_f4(ra, va + u * panel, s);
+      gb[u] = buffer_f4(rb, vb + u * panel, s);
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      *(f32x4*)&As[buf][lrow + 32 * u][lc4] = ga[u];
+      *(f32x4*)&Bs[buf][lrow + 32 * u][lc4] = gb[u];
+    }
+  };
+
+  f32x16 acc[2][2] = {};
+  load(0);
+  store(0);
+  if (nk > 1) load(1);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int kc = 16 * half + 4 * t;
+      const f32x4 a0 = *(const f32x4*)&As[buf][wi + l32][kc];
+      const f32x4 a1 = *(const f32x4*)&As[buf][wi + 32 + l32][kc];
+      const f32x4 b0 = *(const f32x4*)&Bs[buf][wj + l32][kc];
+      const f32x4 b1 = *(const f32x4*)&Bs[buf][wj + 32 + l32][kc];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[0][0] = mfma32(a0[e], b0[e], acc[0][0]);
+        acc[0][1] = mfma32(a0[e], b1[e], acc[0][1]);
+        acc[1][0] = mfma32(a1[e], b0[e], acc[1][0]);
+        acc[1][1] = mfma32(a1[e], b1[e], acc[1][1]);
+      }
+    }
+    if (kt + 1 < nk) {
+      store(buf ^ 1);
+      if (kt + 2 < nk) load(kt + 2);
+    }
+    __syncthreads();
+  }
+
+  // x is blocked [n][np / 32][128 channels][32 columns]: the finish kernel
+  // reads one contiguous 16 KB block per 32-pair tile.
+  const int64_t nb = np / 32;
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const int j = j0 + wj + 32 * cb + l32;
+    if (j >= n) continue;
+    float* col = x + ((int64_t)(j >> 5) * kChannels + c) * 32 + (j & 31);
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = i0 + wi + 32 * rb + mfma_row(r, half);
+        if (i < n) col[(int64_t)i * nb * kChannels * 32] = acc[rb][cb][r];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- finish
+// Persistent; 4 waves, each owning 32 output channels with the W_z and W_g
+// fragments resident.  Per tile of 32 pairs (i, j0 .. j0 + 31): the x block
+// is read (16 KB, contiguous) and transposed into LDS, z's rows are read in
+// the natural frame, both are normalised in place, then two 64-MFMA chains
+// per wave and the gated, optionally accumulated, store.
+__global__ __launch_bounds__(256, 2) void trimul_finish_kernel(TriMulArgs a, int tiles_j,
+                                                               int ntiles) {
+  __shared__ __attribute__((aligned(16))) float xs[kRows][kLds];
+  __shared__ __attribute__((aligned(16))) float zs[kRows][kLds];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+  const int col = 32 * w + l32;
+
+  float wz[64], wg[64];
+  load_fragment(a.w_z, col, half, wz);
+  load_fragment(a.w_g, col, half, wg);
+  const float bz = a.b_z ? a.b_z[col] : 0.f;
+  const float bg = a.b_g ? a.b_g[col] : 0.f;
+  f32x2 lnw_in = {1.f, 1.f}, lnb_in = {0.f, 0.f}, lnw_out = {1.f, 1.f}, lnb_out = {0.f, 0.f};
+  if (a.ln_in_w) lnw_in = *(const f32x2*)(a.ln_in_w + 2 * lane);
+  if (a.ln_in_b) lnb_in = *(const f32x2*)(a.ln_in_b + 2 * lane);
+  if (a.ln_out_w) lnw_out = *(const f32x2*)(a.ln_out_w + 2 * lane);
+  if (a.ln_out_b) lnb_out = *(const f32x2*)(a.ln_out_b + 2 * lane);
+  const int n = a.n;
+  const int64_t nb = a.np / 32;
+  const bool residual = a.accumulate != 0;
+
+  // Raw tile in registers: x (thread: channel tid/8 + 32u, columns
+  // 4*(tid%8)..+3) and z (thread: row tid/32 + 8u, channels 4*(tid%32)..+3).
+  f32x4 rx[4], rz[4];
+  auto fetch = [&](int tile) {
+    const int i = tile / tiles_j;
+    const int jb = tile % tiles_j;
+    const int j0 = jb * kRows;
+    const float* xb = a.x + ((int64_t)i * nb + jb) * kChannels * 32;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int idx = tid + 256 * u;
+      rx[u] = *(const f32x4*)(xb + (idx >> 3) * 32 + (idx & 7) * 4);
+      const int j = j0 + (idx >> 5);
+      rz[u] = j < n ? *(const f32x4*)(a.z + (int64_t)i * a.zs_i + (int64_t)j * a.zs_j +
+                                      (idx & 31) * 4)
+                    : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+
+  __builtin_amdgcn_s_waitcnt(0);
+  int tile = blockIdx.x;
+  fetch(tile);
+  for (; tile < ntiles; tile += gridDim.x) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int idx = tid + 256 * u;
+      const int c = idx >> 3;
+      const int j4 = (idx & 7) * 4;
+      xs[j4 + 0][c] = rx[u].x;
+      xs[j4 + 1][c] = rx[u].y;
+      xs[j4 + 2][c] = rx[u].z;
+      xs[j4 + 3][c] = rx[u].w;
+      *(f32x4*)&zs[idx >> 5][(idx & 31) * 4] = rz[u];
+    }
+    __syncthreads();
+    // Rows past n hold values K2 never wrote: they are normalised and
+    // multiplied like the others (rows are independent) and never stored.
+#pragma unroll
+    for (int rr = 0; rr < kRows / 4; ++rr) {
+      const int row = 8 * w + rr;
+      float d0, d1, rstd;
+      const f32x2 xv = *(const f32x2*)&xs[row][2 * lane];
+      ln_stats_c128(xv.x, xv.y, a.eps_out, d0, d1, rstd);
+      *(f32x2*)&xs[row][2 * lane] =
+          f32x2{d0 * rstd * lnw_out.x + lnb_out.x, d1 * rstd * lnw_out.y + lnb_out.y};
+      const f32x2 zv = *(const f32x2*)&zs[row][2 * lane];
+      ln_stats_c128(zv.x, zv.y, a.eps_in, d0, d1, rstd);
+      *(f32x2*)&zs[row][2 * lane] =
+          f32x2{d0 * rstd * lnw_in.x + lnb_in.x, d1 * rstd * lnw_in.y + lnb_in.y};
+    }
+    __syncthreads();
+    const int next = tile + (int)gridDim.x;
+    if (next < ntiles) fetch(next);
+    f32x16 acc_z = {}, acc_g = {};
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const f32x4 ax = *(const f32x4*)&xs[l32][64 * half + 4 * t];
+      const f32x4 az = *(const f32x4*)&zs[l32][64 * half + 4 * t];
+      acc_z = mfma32(ax.x, wz[4 * t + 0], acc_z);
+      acc_g = mfma32(az.x, wg[4 * t + 0], acc_g);
+      acc_z = mfma32(ax.y, wz[4 * t + 1], acc_z);
+      acc_g = mfma32(az.y, wg[4 * t + 1], acc_g);
+      acc_z = mfma32(ax.z, wz[4 * t + 2], acc_z);
+      acc_g = mfma32(az.z, wg[4 * t + 2], acc_g);
+      acc_z = mfma32(ax.w, wz[4 * t + 3], acc_z);
+      acc_g = mfma32(az.w, wg[4 * t + 3], acc_g);
+    }
+    const int i = tile / tiles_j;
+    const int j0 = (tile % tiles_j) * kRows;
+    float* dst = a.out + (int64_t)i * a.os_i + col;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int j = j0 + mfma_row(r, half);
+      if (j < n) {
+        float* d = dst + (int64_t)j * a.os_j;
+        // native: value = sigmoid(g) * x; z + value when adding
+        const float v = sigmoidf_(acc_g[r] + bg) * (acc_z[r] + bz);
+        *d = residual ? *d + v : v;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+int grid_for(int64_t ntiles, int per_cu) {
+  const int64_t cap = (int64_t)device_cu_count() * per_cu;
+  return (int)(ntiles < cap ? ntiles : cap);
+}
+
+}  // namespace
+
+hipError_t launch_trimul(const TriMulArgs& a, hipStream_t stream) {
+  if (a.n <= 0) return hipSuccess;
+  if (a.np % kGemmTile || a.np < a.n) return hipErrorInvalidValue;
+  const int tiles_k = a.np / kRows;
+  const int64_t proj_tiles = (int64_t)a.n * tiles_k;
+  const int tiles = a.np / kGemmTile;
+  const uint64_t gemm_total = (uint64_t)kChannels * tiles * tiles;
+  const int tiles_j = (a.n + kRows - 1) / kRows;
+  const int64_t fin_tiles = (int64_t)a.n * tiles_j;
+  if (proj_tiles > 0x7fffffff || gemm_total > 0x7fffffffu || fin_tiles > 0x7fffffff)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(trimul_project_kernel, dim3(grid_for(proj_tiles, 1)),
+                     dim3(kProjWaves * 64), 0, stream, a, tiles_k, (int)proj_tiles);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(trimul_contract_kernel, dim3((uint32_t)gemm_total), dim3(256), 0, stream,
+                     a.pa, a.pb, a.x, a.n, a.np, tiles, (uint32_t)gemm_total);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(trimul_finish_kernel, dim3(grid_for(fin_tiles, 2)), dim3(256), 0, stream,
+                     a, tiles_j, (int)fin_tiles);
+  return hipGetLastError();
+}
+
+}  // namespace fpx

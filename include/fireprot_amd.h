@@ -179,6 +179,42 @@ int fpx_attn_strided(const float* q, int64_t q_sb, int64_t q_sh, int64_t q_sn, c
                      float* out, int64_t o_sb, int64_t o_sh, int64_t o_sn, int batch, int n,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* Bytes of workspace fpx_tri_mul needs; 0 for unsupported sizes. */
+size_t fpx_tri_mul_workspace_bytes(int n, int c_z, int c_hidden);
+
+/* Triangle multiplicative update, outgoing or incoming, in one call:
+ *   zn = LayerNorm_in(z); a = mask * sigmoid(zn W_a_g^T + b) * (zn W_a_p^T + b);
+ *   b likewise; x[i,j] = sum_k a[i,k] * b[j,k] (outgoing) or
+ *   sum_k a[k,i] * b[k,j] (incoming), per channel;
+ *   u = sigmoid(zn W_g^T + b_g) * (LayerNorm_out(x) W_z^T + b_z);
+ *   out = u (accumulate = 0) or out + u (accumulate = 1, the native z += u).
+ * Replaces the Protenix module call TriangleMultiplicativeUpdate.forward(z,
+ * mask, inplace_safe, _add_with_inplace) as dispatched by
+ * patches/protenix/0001-*.patch:14-46 and python/fireprot/backends/amd/
+ * triangle_multiplication.py:294-345 (LN once, gated projections packed
+ * channel-first, BMM contraction, output LN, linear_z and the gated residual
+ * kernel of kernels/amd/fireprot_amd_ops.cu:590-602), for any N and with an
+ * explicit mask.
+ *   z        [n][n][128], strides (z_stride0, z_stride1, 1), multiples of 4
+ *   mask     nullable [n][n] multiplier of a and b (strides m_stride0/1)
+ *   ln_*     nullable LayerNorm affine [128]; eps as in the module (1e-5)
+ *   w_abpg   [4][128][128]: W_a_p, W_a_g, W_b_p, W_b_g stacked, torch [out, in]
+ *   b_abpg   nullable [4][128] biases of those four projections
+ *   w_z, w_g [128][128]; b_z, b_g nullable [128]
+ *   out      [n][n][128], strides (out_stride0, out_stride1, 1); may be z
+ *            itself with the same strides (the in-place update); any other
+ *            overlap with z is unsupported (status 2 when out == z with
+ *            different strides)
+ *   workspace at least fpx_tri_mul_workspace_bytes(n, 128, 128), 256-aligned
+ * Supported: c_z = c_hidden = 128, 1 <= n <= 4096. */
+int fpx_tri_mul(const float* z, int64_t z_stride0, int64_t z_stride1, const float* mask,
+                int64_t m_stride0, int64_t m_stride1, const float* ln_in_w, const float* ln_in_b,
+                float eps_in, const float* w_abpg, const float* b_abpg, const float* ln_out_w,
+                const float* ln_out_b, float eps_out, const float* w_z, const float* b_z,
+                const float* w_g, const float* b_g, int n, int c_z, int c_hidden, int outgoing,
+                int accumulate, float* out, int64_t out_stride0, int64_t out_stride1,
+                void* workspace, size_t workspace_bytes, void* stream);
+
 /* LayerNorm over 128 channels of rows x[i][j] read at x + i*stride_i + j*stride_j
  * (channel stride 1), written contiguously to y[rows_i][rows_j][128].  Covers
  * both the contiguous pair LN (kernels/amd/fireprot_amd_ops.cu:27-64,

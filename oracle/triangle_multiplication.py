@@ -112,10 +112,22 @@ def combine(a: torch.Tensor, b: torch.Tensor, *, outgoing: bool) -> torch.Tensor
 
 
 def update(z: torch.Tensor, mask: torch.Tensor | None, p: TriMulParams, *,
-           outgoing: bool) -> torch.Tensor:
-    """The module's update ``sigmoid(linear_g(LN_in z)) * linear_z(LN_out(x))``."""
+           outgoing: bool, rows: torch.Tensor | None = None) -> torch.Tensor:
+    """The module's update ``sigmoid(linear_g(LN_in z)) * linear_z(LN_out(x))``.
+
+    ``rows`` restricts the output to those first-index rows ``i`` (each output
+    row needs all of ``b`` and one row, or column, of ``a``); the result is then
+    ``[len(rows), N, 128]`` and equals ``update(...)[rows]``, which
+    tests/test_oracle_trimul.py checks.
+    """
     normalized, a, b = gated_projections(z, mask, p)
-    x = combine(a, b, outgoing=outgoing)
+    if rows is None:
+        x = combine(a, b, outgoing=outgoing)
+    else:
+        a_rows = a[rows] if outgoing else a[:, rows].transpose(0, 1)  # [R, k, c]
+        b_k = b if outgoing else b.transpose(0, 1)                      # [j, k, c]
+        x = torch.matmul(a_rows.permute(2, 0, 1), b_k.permute(2, 1, 0)).permute(1, 2, 0)
+        normalized = normalized[rows]
     del a, b
     x = linear(layer_norm(x, p.ln_out_w, p.ln_out_b, p.eps_out), p.w_z, p.b_z)
     return torch.sigmoid(linear(normalized, p.w_g, p.b_g)) * x

@@ -94,6 +94,48 @@ def test_strided_guards(lib):
     assert f(*_strided_args(ws_bytes=1)) == 4
 
 
+def test_tri_mul_workspace_sizes(lib):
+    seg = lambda b: -(-b // 256) * 256  # noqa: E731
+    for n in (1, 7, 129, 1000, 1536, 4096):
+        np_ = -(-n // 128) * 128
+        # a and b channel-major [128][np][np]; x blocked [n][np/32][128][32]
+        expected = 2 * seg(128 * np_ * np_ * 4) + seg(n * np_ * 128 * 4)
+        assert lib.fpx_tri_mul_workspace_bytes(n, 128, 128) == expected
+    for bad in ((0, 128, 128), (4097, 128, 128), (64, 64, 128), (64, 128, 32)):
+        assert lib.fpx_tri_mul_workspace_bytes(*bad) == 0
+
+
+def _tri_mul_args(**override):
+    args = dict(z=256, zs0=64 * 128, zs1=128, mask=None, ms0=0, ms1=0, ln_in_w=None,
+                ln_in_b=None, eps_in=1e-5, w=256, b=None, ln_out_w=None, ln_out_b=None,
+                eps_out=1e-5, w_z=256, b_z=None, w_g=256, b_g=None, n=64, c_z=128, c_h=128,
+                outgoing=1, accumulate=0, out=512, os0=64 * 128, os1=128, ws=256, ws_bytes=1,
+                stream=None)
+    args.update(override)
+    return list(args.values())
+
+
+def test_tri_mul_guards(lib):
+    f = lib.fpx_tri_mul
+    assert f(*_tri_mul_args()) == 4                                 # workspace too small
+    assert f(*_tri_mul_args(n=0)) == 2
+    assert f(*_tri_mul_args(n=4097)) == 2
+    assert f(*_tri_mul_args(c_h=64)) == 2
+    assert f(*_tri_mul_args(outgoing=2)) == 2
+    assert f(*_tri_mul_args(accumulate=-1)) == 2
+    assert f(*_tri_mul_args(zs1=130)) == 2                          # rows not 16-byte aligned
+    assert f(*_tri_mul_args(os0=-1)) == 2
+    assert f(*_tri_mul_args(mask=256, ms1=-1)) == 2
+    assert f(*_tri_mul_args(eps_out=-1.0)) == 2
+    assert f(*_tri_mul_args(out=256, os0=128, os1=64 * 128)) == 2   # z aliased, other strides
+    assert f(*_tri_mul_args(z=None)) == 3
+    assert f(*_tri_mul_args(z=260)) == 3
+    assert f(*_tri_mul_args(w_g=None)) == 3
+    assert f(*_tri_mul_args(mask=2)) == 3
+    assert f(*_tri_mul_args(ln_in_w=4)) == 3
+    assert f(*_tri_mul_args(ws=128)) == 3
+
+
 def _block_args(**override):
     args = dict(dtype=0, z=256, zs0=64 * 128, zs1=128, mask=None, ms0=0, ms1=0, ln_w=None,
                 ln_b=None, eps=1e-5, w_qkvg=256, b_g=None, w_bias=256, w_o=256, b_o=None,

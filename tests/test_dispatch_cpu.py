@@ -139,3 +139,47 @@ def test_registered_implementations():
     assert impl[ta.OPERATION][0]["name"] == ta.IMPLEMENTATION
     assert {c["name"] for c in impl[ta.BLOCK_OPERATION]} == {ta.BLOCK_IMPLEMENTATION,
                                                              ta.BLOCK_BF16_IMPLEMENTATION}
+
+
+def _trimul_signature(**change):
+    from fireprot_amd import triangle_multiplication as htm
+
+    base = dict(operation=htm.OPERATION, device_type="cuda", architecture="gfx950",
+                dtype="float32", shape=(1536, 1536, 128), layout="contiguous",
+                mode="inference", mask="dense", inplace=True,
+                attributes={"c_z": 128, "c_hidden": 128, "eligible": True, "reason": "",
+                            "direction": "incoming", "add_with_inplace": True})
+    base.update(change)
+    return OperationSignature.create(**base)
+
+
+def test_trimul_capability(monkeypatch):
+    from fireprot_amd import triangle_multiplication as htm
+
+    monkeypatch.setattr(_native, "available", lambda: True)
+    assert htm._supports(_trimul_signature()) is True
+    for change in (dict(device_type="cpu"), dict(architecture="gfx90a"), dict(dtype="bfloat16"),
+                   dict(mode="training"),
+                   dict(attributes={"c_z": 128, "c_hidden": 64, "eligible": True}),
+                   dict(attributes={"c_z": 128, "c_hidden": 128, "eligible": False,
+                                    "reason": "z rows are not 16-byte aligned"})):
+        assert htm._supports(_trimul_signature(**change))[0] is False
+    monkeypatch.setattr(_native, "available", lambda: False)
+    assert htm._supports(_trimul_signature()) == (False, "HIP extension unavailable")
+
+
+def test_trimul_dispatch_falls_back_for_cpu_tensors():
+    from fireprot_amd import triangle_multiplication as htm
+
+    module = SimpleNamespace(training=False, c_z=128, c_hidden=128, _outgoing=True)
+    registry.clear_runtime_state()
+    with torch.no_grad():
+        result = htm.dispatch_triangle_multiplication(
+            module=module, z=torch.zeros(4, 4, 128), mask=None, inplace_safe=True,
+            add_with_inplace=True, inplace_chunk_size=256, native=lambda **_: "native")
+    assert result == "native"
+    decision = registry.manifest()["decisions"][0]
+    assert decision["selected"] == "native"
+    assert decision["signature"]["attributes"]["direction"] == "outgoing"
+    ok, reason = htm.eligible(module, torch.zeros(4, 4, 128), None)
+    assert not ok and "HIP" in reason

@@ -103,6 +103,18 @@ def test_relabelling_equivariance():
         torch.testing.assert_close(moved, base[perm][:, perm], atol=1e-12, rtol=1e-12)
 
 
+def test_row_subset_matches_full_update():
+    n = 10
+    z = workloads.make_pair(n).double()
+    mask = (torch.rand(n, n, generator=torch.Generator().manual_seed(8)) < 0.8).double()
+    p = params_of(workloads.make_trimul_weights(biases=True), torch.float64)
+    rows = torch.tensor([0, 3, 9, 4])
+    for outgoing in (True, False):
+        full = tm.update(z, mask, p, outgoing=outgoing)
+        part = tm.update(z, mask, p, outgoing=outgoing, rows=rows)
+        torch.testing.assert_close(part, full[rows], atol=1e-12, rtol=1e-12)
+
+
 def test_forward_adds_or_overwrites():
     z, mask, params, u_out, _ = load_trimul_case("t7_tail")
     torch.testing.assert_close(tm.forward(z, mask, params, outgoing=True, add=True), z + u_out,
