@@ -360,16 +360,98 @@ def bench_trimul(args) -> dict:
     return result
 
 
+TRANSITION_METRIC = "pair transition ms + TFLOP/s (% MFMA peak) at N=1536 FP32, 1 GPU"
+
+
+def bench_transition(args) -> dict:
+    """Pair transition at N = 1536 (2.36 M pair rows, c = 128, n = 4), FP32:
+    one step = ``z += transition(z)`` in place (``fpx_transition``,
+    accumulate), as the Pairformer applies it.  Weights N(0, 0.05^2).
+    ``cpu_baseline`` times the oracle on 8192 rows and scales linearly.
+    """
+    import torch
+
+    from fireprot_amd import transition as htr
+    from fireprot_amd import workloads
+
+    n = 1536
+    dev = torch.device("cuda:0")
+    log(f"inputs transition n={n}")
+    z0 = workloads.make_pair(n)
+    w_cpu = workloads.make_transition_weights()
+    z = z0.to(dev)
+    weights = htr.TransitionWeights.from_tensors(**w_cpu).to(dev)
+    from fireprot_amd import _native
+
+    size = _native.library().fpx_transition_workspace_bytes(n, n, 128, 4)
+    ws = torch.empty(size, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        htr.pair_transition_residual(z, weights, workspace=ws)
+
+    with torch.inference_mode():
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        log(f"warmup {args.warmup} done")
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.steps):
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        log(f"timed {args.steps} steps: {ms:.3f} ms/step")
+    from oracle.transition import flops
+
+    flop = flops(n * n)
+    value = flop / (ms * 1e-3) / 1e12
+    result = {
+        "metric": TRANSITION_METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded z ~ N(0,1), N(0,0.05^2) weights)",
+        "config": {"workload": "transition-n1536-f32: z += transition(z), in place",
+                   "n": n, "rows": n * n, "c": 128, "expansion": 4, "step_flop": flop,
+                   "mfma_peak_frac": round(value / FP32_MFMA_PEAK_TFLOPS, 4)},
+        "roofline": None, "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        from oracle import transition as tr
+
+        threads = max(1, min(16, os.cpu_count() or 1))
+        torch.set_num_threads(threads)
+        sample = z0.reshape(-1, 128)[:8192]
+        with torch.inference_mode():
+            t0 = time.perf_counter()
+            tr.transition(sample, tr.TransitionParams(**w_cpu))
+            spent = time.perf_counter() - t0
+        total = spent * n * n / sample.shape[0]
+        result["cpu_baseline"] = {
+            "value": round(flop / total / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"oracle transition (native op order, {threads} threads) on the first "
+                       f"8192 pair rows ({spent:.2f} s), scaled to {n * n} rows: "
+                       f"{total:.1f} s per step"),
+            "cpu": platform.processor() or platform.machine(),
+        }
+    return result
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c4", choices=["c1", "c2", "c3", "c4", "c5"])
-    ap.add_argument("--workload", default="block", choices=["block", "openfold3", "trimul"],
+    ap.add_argument("--workload", default="block",
+                    choices=["block", "openfold3", "trimul", "transition"],
                     help="block: the triangle-attention block (default); openfold3: "
                          "OpenFold3's _attention through fpx_attn_strided; trimul: "
-                         "triangle multiplication (fpx_tri_mul)")
+                         "triangle multiplication (fpx_tri_mul); transition: the pair "
+                         "transition (fpx_transition)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 1 GiB device-to-device copy (the known-size "
@@ -395,6 +477,9 @@ def main() -> int:
         return 0
     if args.workload == "trimul":
         print(json.dumps(bench_trimul(args)), flush=True)
+        return 0
+    if args.workload == "transition":
+        print(json.dumps(bench_transition(args)), flush=True)
         return 0
     cfg = workloads.CONFIGS[args.config]
     n = cfg.n

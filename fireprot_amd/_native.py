@@ -85,6 +85,15 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         _p, _i64, _i64,              # out (may be z), strides
         _p, _sz, _p,                 # workspace, bytes, stream
     ]),
+    "fpx_transition_workspace_bytes": (_sz, [_i64, _i64, _i, _i]),
+    "fpx_transition": (_i, [
+        _p, _i64, _i64, _i64, _i64,  # x, rows_i, rows_j, strides
+        _p, _p, _f,                  # ln_w, ln_b, eps
+        _p, _p, _p,                  # w_a, w_b [512][128], w_o [128][512]
+        _i, _i, _i,                  # c, expansion, accumulate
+        _p, _i64, _i64,              # out (may be x), strides
+        _p, _sz, _p,                 # workspace, bytes, stream
+    ]),
     "fpx_layer_norm_c128": (_i, [_p, _i64, _i64, _i64, _i64, _p, _p, _f, _p, _p]),
     "fpx_qkv_projection": (_i, [_p, _i64, _p, _p, _p, _p, _p]),
     "fpx_sigmoid_mul_out": (_i, [_p, _p, _p, _i64, _p]),

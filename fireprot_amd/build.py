@@ -20,7 +20,7 @@ INCLUDE = ROOT / "include"
 LIB_DIR = PACKAGE / "_lib"
 LIB_PATH = LIB_DIR / "libfireprot_amd.so"
 SOURCES = ("attention.hip", "projection.hip", "bf16.hip", "elementwise.hip", "trimul.hip",
-           "capi.hip")
+           "transition.hip", "capi.hip")
 ARCH = "gfx950"
 
 HIPCC_FLAGS = (

@@ -206,6 +206,12 @@ TriMulWorkspace trimul_workspace(int n) {
   return w;
 }
 
+// Workspace of fpx_transition: h [round_up(rows, 128)][512] float.
+size_t transition_workspace(int64_t rows) {
+  return (size_t)round_up(round_up(rows, 128) * fpx::kTransitionHidden * (int64_t)sizeof(float),
+                          256);
+}
+
 // A [batch][4][n][32] operand with channel stride 1 the strided attention
 // kernel can read: non-negative strides that keep 16-byte rows aligned, and
 // (for K and V) a (b, h) slice that a buffer descriptor covers.
@@ -536,6 +542,52 @@ int fpx_tri_mul(const float* z, int64_t z_stride0, int64_t z_stride1, const floa
   a.outgoing = outgoing;
   a.accumulate = accumulate;
   return status(fpx::launch_trimul(a, static_cast<hipStream_t>(stream)));
+}
+
+size_t fpx_transition_workspace_bytes(int64_t rows_i, int64_t rows_j, int c, int expansion) {
+  if (rows_i < 0 || rows_j < 0 || rows_i > 0x7fffffff || rows_j > 0x7fffffff ||
+      c != fpx::kChannels || expansion * c != fpx::kTransitionHidden)
+    return 0;
+  const int64_t rows = rows_i * rows_j;
+  if (rows < 1 || (rows_j + 31) / 32 * rows_i > 0x7fffffffll) return 0;
+  return transition_workspace(rows);
+}
+
+int fpx_transition(const float* x, int64_t rows_i, int64_t rows_j, int64_t x_stride_i,
+                   int64_t x_stride_j, const float* ln_w, const float* ln_b, float eps,
+                   const float* w_a, const float* w_b, const float* w_o, int c, int expansion,
+                   int accumulate, float* out, int64_t out_stride_i, int64_t out_stride_j,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+  const size_t need = fpx_transition_workspace_bytes(rows_i, rows_j, c, expansion);
+  if (need == 0) return FPX_ERR_DIMS;
+  if (accumulate != 0 && accumulate != 1) return FPX_ERR_DIMS;
+  if (x_stride_i < 0 || x_stride_j < 0 || x_stride_i % 2 || x_stride_j % 2) return FPX_ERR_DIMS;
+  if (out_stride_i < 0 || out_stride_j < 0) return FPX_ERR_DIMS;
+  if (!(eps >= 0.0f)) return FPX_ERR_DIMS;
+  if (out == x && (out_stride_i != x_stride_i || out_stride_j != x_stride_j)) return FPX_ERR_DIMS;
+  if (!aligned(x, 8) || !aligned(w_a, 16) || !aligned(w_b, 16) || !aligned(w_o, 16) ||
+      !aligned(out, 4) || !aligned_or_null(ln_w, 8) || !aligned_or_null(ln_b, 8))
+    return FPX_ERR_POINTER;
+  if (!aligned(workspace, 256)) return FPX_ERR_POINTER;
+  if (workspace_bytes < need) return FPX_ERR_WORKSPACE;
+  fpx::TransitionArgs a{};
+  a.x = x;
+  a.xs_i = x_stride_i;
+  a.xs_j = x_stride_j;
+  a.rows_i = (int)rows_i;
+  a.rows_j = (int)rows_j;
+  a.ln_w = ln_w;
+  a.ln_b = ln_b;
+  a.eps = eps;
+  a.w_a = w_a;
+  a.w_b = w_b;
+  a.w_o = w_o;
+  a.h = static_cast<float*>(workspace);
+  a.out = out;
+  a.os_i = out_stride_i;
+  a.os_j = out_stride_j;
+  a.accumulate = accumulate;
+  return status(fpx::launch_transition(a, static_cast<hipStream_t>(stream)));
 }
 
 int fpx_layer_norm_c128(const float* x, int64_t rows_i, int64_t rows_j, int64_t stride_i,

@@ -104,6 +104,22 @@ __device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t total) {
                      : extra * (per + 1) + (xcd - extra) * per + slot;
 }
 
+// [128 x 32] weight fragment (B operand of v_mfma_f32_32x32x2_f32) of output
+// column col (this lane's l % 32) of a torch [out][in] weight with in
+// stride ld: lane half h holds input channels 64h .. 64h + 63.
+__device__ __forceinline__ void load_fragment(const float* w, int col, int half, float* wf,
+                                              int64_t ld = kChannels) {
+  const float* src = w + (int64_t)col * ld + 64 * half;
+#pragma unroll
+  for (int t = 0; t < 16; ++t) {
+    const f32x4 v = *(const f32x4*)(src + 4 * t);
+    wf[4 * t + 0] = v.x;
+    wf[4 * t + 1] = v.y;
+    wf[4 * t + 2] = v.z;
+    wf[4 * t + 3] = v.w;
+  }
+}
+
 __host__ __device__ __forceinline__ int64_t round_up(int64_t x, int64_t m) {
   return (x + m - 1) / m * m;
 }

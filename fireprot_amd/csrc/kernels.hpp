@@ -220,6 +220,33 @@ struct TriMulArgs {
 
 hipError_t launch_trimul(const TriMulArgs& args, hipStream_t stream);
 
+// ---------------------------------------------------------- pair transition
+// out = silu(LN(x) W_a^T) * (LN(x) W_b^T) W_o^T over rows x[i][j] at
+// x + i*xs_i + j*xs_j (transition.hip).  h is the workspace's [rows padded to
+// 128][512] intermediate.
+constexpr int kTransitionHidden = 512;
+
+struct TransitionArgs {
+  const float* x;
+  int64_t xs_i;
+  int64_t xs_j;
+  int rows_i;
+  int rows_j;
+  const float* ln_w;  // nullable
+  const float* ln_b;  // nullable
+  float eps;
+  const float* w_a;   // [512][128]
+  const float* w_b;   // [512][128]
+  const float* w_o;   // [128][512]
+  float* h;
+  float* out;
+  int64_t os_i;
+  int64_t os_j;
+  int accumulate;     // out = out + transition(x) instead of transition(x)
+};
+
+hipError_t launch_transition(const TransitionArgs& args, hipStream_t stream);
+
 int device_cu_count();
 
 }  // namespace fpx

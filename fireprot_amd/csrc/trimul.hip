@@ -22,6 +22,7 @@
 //   trimul_finish_kernel   LN_out(x) W_z^T and LN_in(z) W_g^T for 32 pairs
 //                          per tile, the sigmoid gate and the in-place write
 #include "common.hpp"
+#include "gemm.hpp"
 #include "kernels.hpp"
 
 namespace fpx {
@@ -29,33 +30,6 @@ namespace {
 
 constexpr int kRows = 32;                 // pair rows per projection tile
 constexpr int kLds = kChannels + 4;       // padded LDS row (floats)
-constexpr int kGemmTile = 128;            // contraction output tile (rows and columns)
-constexpr int kKStage = 32;               // contraction keys per LDS stage
-constexpr int kKPad = kKStage + 4;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer(const float* base, int64_t bytes) {
-  // dword 3 = 0x00020000: raw 32-bit buffer access on gfx9-family parts.
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, (int)bytes,
-                                           0x00020000);
-}
-
-__device__ __forceinline__ f32x4 buffer_f4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-}
-
-// [128 x 32] weight fragment of output columns col (lane l32) for the
-// B operand: lane half h holds input channels 64h .. 64h + 63.
-__device__ __forceinline__ void load_fragment(const float* w, int col, int half, float* wf) {
-  const float* src = w + (int64_t)col * kChannels + 64 * half;
-#pragma unroll
-  for (int t = 0; t < 16; ++t) {
-    const f32x4 v = *(const f32x4*)(src + 4 * t);
-    wf[4 * t + 0] = v.x;
-    wf[4 * t + 1] = v.y;
-    wf[4 * t + 2] = v.z;
-    wf[4 * t + 3] = v.w;
-  }
-}
 
 // ------------------------------------------------------------ projection
 // Persistent; 8 waves: waves 0-3 produce a, waves 4-7 produce b, each for 32
@@ -179,22 +153,17 @@ __global__ __launch_bounds__(kProjWaves * 64) void trimul_project_kernel(TriMulA
 }
 
 // ----------------------------------------------------------- contraction
-// One work-group = (channel c, 128 rows i, 128 columns j); four waves, each a
-// 64 x 64 quadrant as 2 x 2 blocks of v_mfma_f32_32x32x2_f32.  Per 32-key
-// stage a lane half h feeds keys 16h .. 16h + 15 (the sum over keys is
-// order-free, so both operands are read as contiguous row segments, four
-// b128 LDS reads per 32-row block).  Stages are double-buffered: the next
-// stage's global loads are in flight while this one is multiplied.
-// Work-groups of one channel are consecutive in the logical order, and
-// xcd_remap gives each XCD a contiguous range, so the A and B row panels a
-// range touches stay in that XCD's L2.
+// One work-group = (channel c, 128 rows i, 128 columns j) of x_c = A_c B_c^T
+// (gemm_nt_128 over the np keys).  Work-groups of one channel are consecutive
+// in the logical order, and xcd_remap gives each XCD a contiguous range, so
+// the A and B row panels a range touches stay in that XCD's L2.
 __global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const float* __restrict__ pa,
                                                                  const float* __restrict__ pb,
                                                                  float* __restrict__ x, int n,
                                                                  int np, int tiles,
                                                                  uint32_t total) {
-  __shared__ __attribute__((aligned(16))) float As[2][kGemmTile][kKPad];
-  __shared__ __attribute__((aligned(16))) float Bs[2][kGemmTile][kKPad];
+  __shared__ __attribute__((aligned(16))) GemmStage As[2];
+  __shared__ __attribute__((aligned(16))) GemmStage Bs[2];
 
   const uint32_t logical = xcd_remap(blockIdx.x, total);
   const int per_channel = tiles * tiles;
@@ -202,74 +171,21 @@ __global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const float* __
   const int rem = (int)(logical % per_channel);
   const int i0 = (rem / tiles) * kGemmTile;
   const int j0 = (rem % tiles) * kGemmTile;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int half = lane >> 5;
   const int l32 = lane & 31;
-  const int wi = (w >> 1) * 64;
-  const int wj = (w & 1) * 64;
 
   const int64_t slice = (int64_t)np * np;
-  const __amdgpu_buffer_rsrc_t ra = buffer(pa + c * slice, slice * 4);
-  const __amdgpu_buffer_rsrc_t rb = buffer(pb + c * slice, slice * 4);
-  // Thread (row = tid / 8 + 32u, keys 4 * (tid % 8) .. +3) of each stage.
-  const int lrow = tid >> 3;
-  const int lc4 = (tid & 7) * 4;
-  const uint32_t va = (uint32_t)(((int64_t)(i0 + lrow) * np + lc4) * 4);
-  const uint32_t vb = (uint32_t)(((int64_t)(j0 + lrow) * np + lc4) * 4);
-  const uint32_t panel = (uint32_t)(32 * np * 4);  // 32 rows further down
-  const int nk = np / kKStage;
-
-  f32x4 ga[4], gb[4];
-  auto load = [&](int kt) {
-    const uint32_t s = (uint32_t)kt * (kKStage * 4);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      ga[u] = buffer_f4(ra, va + u * panel, s);
-      gb[u] = buffer_f4(rb, vb + u * panel, s);
-    }
-  };
-  auto store = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      *(f32x4*)&As[buf][lrow + 32 * u][lc4] = ga[u];
-      *(f32x4*)&Bs[buf][lrow + 32 * u][lc4] = gb[u];
-    }
-  };
-
   f32x16 acc[2][2] = {};
-  load(0);
-  store(0);
-  if (nk > 1) load(1);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int kc = 16 * half + 4 * t;
-      const f32x4 a0 = *(const f32x4*)&As[buf][wi + l32][kc];
-      const f32x4 a1 = *(const f32x4*)&As[buf][wi + 32 + l32][kc];
-      const f32x4 b0 = *(const f32x4*)&Bs[buf][wj + l32][kc];
-      const f32x4 b1 = *(const f32x4*)&Bs[buf][wj + 32 + l32][kc];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        acc[0][0] = mfma32(a0[e], b0[e], acc[0][0]);
-        acc[0][1] = mfma32(a0[e], b1[e], acc[0][1]);
-        acc[1][0] = mfma32(a1[e], b0[e], acc[1][0]);
-        acc[1][1] = mfma32(a1[e], b1[e], acc[1][1]);
-      }
-    }
-    if (kt + 1 < nk) {
-      store(buf ^ 1);
-      if (kt + 2 < nk) load(kt + 2);
-    }
-    __syncthreads();
-  }
+  gemm_nt_128(pa + c * slice + (int64_t)i0 * np, np, pb + c * slice + (int64_t)j0 * np, np,
+              np / kKStage, As, Bs, acc);
 
   // x is blocked [n][np / 32][128 channels][32 columns]: the finish kernel
   // reads one contiguous 16 KB block per 32-pair tile.
   const int64_t nb = np / 32;
+  const int wi = (w >> 1) * 64;
+  const int wj = (w & 1) * 64;
 #pragma unroll
   for (int cb = 0; cb < 2; ++cb) {
     const int j = j0 + wj + 32 * cb + l32;

@@ -106,6 +106,33 @@ def make_trimul_weights(std: float = 0.1, *, biases: bool = False, affine: bool 
     return w
 
 
+TRANSITION_WEIGHT_SEED = 4343
+
+
+def make_transition_weights(std: float = 0.05, *, affine: bool = False,
+                            seed: int = TRANSITION_WEIGHT_SEED,
+                            channels: int = 128,
+                            expansion: int = 4) -> dict[str, torch.Tensor | None]:
+    """Random-init weights of a pair transition (Protenix ``Transition``,
+    n = 4): ``W_a``, ``W_b`` ``[512, 128]`` and ``W_o`` ``[128, 512]``, all
+    N(0, std^2); ``affine`` draws non-trivial LayerNorm scales and shifts."""
+    g = torch.Generator().manual_seed(seed)
+    hidden = expansion * channels
+
+    def normal(*shape, scale=std):
+        return torch.randn(*shape, generator=g, dtype=torch.float32) * scale
+
+    w: dict[str, torch.Tensor | None] = {
+        "ln_w": torch.ones(channels), "ln_b": torch.zeros(channels),
+        "w_a": normal(hidden, channels), "w_b": normal(hidden, channels),
+        "w_o": normal(channels, hidden),
+    }
+    if affine:
+        w["ln_w"] = 1.0 + normal(channels, scale=0.1)
+        w["ln_b"] = normal(channels, scale=0.1)
+    return w
+
+
 def make_pair(n: int, z_scale: float = 1.0, channels: int = 128) -> torch.Tensor:
     g = torch.Generator().manual_seed(Z_SEED_BASE + n)
     z = torch.randn(n, n, channels, generator=g, dtype=torch.float32)

@@ -215,6 +215,32 @@ int fpx_tri_mul(const float* z, int64_t z_stride0, int64_t z_stride1, const floa
                 int accumulate, float* out, int64_t out_stride0, int64_t out_stride1,
                 void* workspace, size_t workspace_bytes, void* stream);
 
+/* Bytes of workspace fpx_transition needs for rows_i x rows_j pair rows; 0
+ * for unsupported sizes. */
+size_t fpx_transition_workspace_bytes(int64_t rows_i, int64_t rows_j, int c, int expansion);
+
+/* Pair transition: out = W_o (silu(W_a LN(x)) * (W_b LN(x))) per 128-channel
+ * row, or out + that (accumulate = 1, the Pairformer's z += transition(z)).
+ * Replaces the Protenix module call Transition.forward (n = 4, c_in = 128) as
+ * hooked at python/fireprot/adapters/protenix/hooks.py:56-68 and dispatched
+ * by python/fireprot/backends/amd/recycle.py:360-390 / :203-227 (LayerNorm,
+ * transition_projection = silu(a) * b of kernels/amd/fireprot_amd_ops.cu:
+ * 1111-1165, then linear_no_bias), for any row count.
+ *   x        rows x[i][j] at x + i*x_stride_i + j*x_stride_j, 128 channels
+ *            with stride 1 (strides even, x 8-byte aligned); a flat
+ *            [rows][128] tensor is rows_i = 1, x_stride_j = 128
+ *   ln_w/b   nullable LayerNorm affine [128]; eps as in the module (1e-5)
+ *   w_a, w_b [512][128]; w_o [128][512] (torch [out, in], no biases)
+ *   out      same row addressing with out strides; may be x itself with the
+ *            same strides (in place); other overlaps unsupported
+ *   workspace fpx_transition_workspace_bytes(...) bytes, 256-aligned
+ * Supported: c = 128, expansion = 4. */
+int fpx_transition(const float* x, int64_t rows_i, int64_t rows_j, int64_t x_stride_i,
+                   int64_t x_stride_j, const float* ln_w, const float* ln_b, float eps,
+                   const float* w_a, const float* w_b, const float* w_o, int c, int expansion,
+                   int accumulate, float* out, int64_t out_stride_i, int64_t out_stride_j,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
 /* LayerNorm over 128 channels of rows x[i][j] read at x + i*stride_i + j*stride_j
  * (channel stride 1), written contiguously to y[rows_i][rows_j][128].  Covers
  * both the contiguous pair LN (kernels/amd/fireprot_amd_ops.cu:27-64,

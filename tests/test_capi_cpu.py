@@ -136,6 +136,36 @@ def test_tri_mul_guards(lib):
     assert f(*_tri_mul_args(ws=128)) == 3
 
 
+def test_transition_workspace_and_guards(lib):
+    seg = lambda b: -(-b // 256) * 256  # noqa: E731
+    for ri, rj in ((1, 1), (3, 5), (1536, 1536), (1, 1000000)):
+        rows = ri * rj
+        assert lib.fpx_transition_workspace_bytes(ri, rj, 128, 4) == seg(-(-rows // 128) * 128 * 512 * 4)
+    for bad in ((0, 5, 128, 4), (5, 0, 128, 4), (2, 2, 64, 4), (2, 2, 128, 2), (-1, 2, 128, 4)):
+        assert lib.fpx_transition_workspace_bytes(*bad) == 0
+    f = lib.fpx_transition
+
+    def args(**o):
+        a = dict(x=256, ri=4, rj=4, xsi=512, xsj=128, ln_w=None, ln_b=None, eps=1e-5, w_a=256,
+                 w_b=256, w_o=256, c=128, e=4, acc=0, out=512, osi=512, osj=128, ws=256,
+                 ws_bytes=1, stream=None)
+        a.update(o)
+        return list(a.values())
+
+    assert f(*args()) == 4
+    assert f(*args(ri=0)) == 2
+    assert f(*args(e=2)) == 2
+    assert f(*args(acc=3)) == 2
+    assert f(*args(xsj=127)) == 2
+    assert f(*args(osi=-1)) == 2
+    assert f(*args(eps=-1.0)) == 2
+    assert f(*args(out=256, osi=128, osj=512)) == 2     # x aliased with other strides
+    assert f(*args(x=None)) == 3
+    assert f(*args(w_o=8)) == 3
+    assert f(*args(ln_b=4)) == 3
+    assert f(*args(ws=128)) == 3
+
+
 def _block_args(**override):
     args = dict(dtype=0, z=256, zs0=64 * 128, zs1=128, mask=None, ms0=0, ms1=0, ln_w=None,
                 ln_b=None, eps=1e-5, w_qkvg=256, b_g=None, w_bias=256, w_o=256, b_o=None,

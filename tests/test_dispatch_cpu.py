@@ -183,3 +183,23 @@ def test_trimul_dispatch_falls_back_for_cpu_tensors():
     assert decision["signature"]["attributes"]["direction"] == "outgoing"
     ok, reason = htm.eligible(module, torch.zeros(4, 4, 128), None)
     assert not ok and "HIP" in reason
+
+
+def test_transition_capability_and_cpu_fallback(monkeypatch):
+    from fireprot_amd import transition as htr
+
+    monkeypatch.setattr(_native, "available", lambda: True)
+    base = dict(operation=htr.OPERATION, device_type="cuda", architecture="gfx950",
+                dtype="float32", shape=(1536, 1536, 128), layout="contiguous", mode="inference",
+                mask="none", inplace=False,
+                attributes={"expansion": 4, "c_in": 128, "eligible": True, "reason": ""})
+    assert htr._supports(OperationSignature.create(**base)) is True
+    for change in (dict(device_type="cpu"), dict(architecture="gfx942"), dict(dtype="float64"),
+                   dict(mode="training"),
+                   dict(attributes={"expansion": 2, "c_in": 128, "eligible": True})):
+        assert htr._supports(OperationSignature.create(**(base | change)))[0] is False
+    module = SimpleNamespace(training=False, n=4, c_in=128)
+    registry.clear_runtime_state()
+    with torch.inference_mode():
+        assert htr.dispatch_transition(module=module, x=torch.randn(5, 5, 128),
+                                       native=lambda **_: "native") == "native"
