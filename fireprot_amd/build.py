@@ -19,8 +19,8 @@ CSRC = PACKAGE / "csrc"
 INCLUDE = ROOT / "include"
 LIB_DIR = PACKAGE / "_lib"
 LIB_PATH = LIB_DIR / "libfireprot_amd.so"
-SOURCES = ("attention.hip", "projection.hip", "bf16.hip", "elementwise.hip", "trimul.hip",
-           "transition.hip", "capi.hip")
+SOURCES = ("attention.hip", "attention_split.hip", "projection.hip", "bf16.hip",
+           "elementwise.hip", "trimul.hip", "transition.hip", "capi.hip")
 ARCH = "gfx950"
 
 HIPCC_FLAGS = (

@@ -1,0 +1,409 @@
+// FP32-accurate triangle attention on the CDNA4 BF16 matrix cores.
+//
+// Reads the block's FP32 workspace exactly as attention_kernel<kAttnBlock>
+// does (q, k [B][H][np][32], v^T [B][H][32][np], the fragment-order bias
+// copies, tile flags, mask-bias rows, gate) and writes the same gated output.
+// Only the two products change: every FP32 operand is split exactly into
+// bfloat16 planes, x = x_hi + x_lo (+ x_rest), and the products run on
+// v_mfma_f32_32x32x16_bf16 with FP32 accumulation.  That instruction does 8x
+// the work of v_mfma_f32_32x32x2_f32 in half its cycles, and unlike the FP32
+// one it runs beside VALU work, so the softmax of one tile overlaps the
+// matrix work of the next.
+//
+//   S^T = K Q^T: three planes each; the six terms down to 2^-16 relative
+//     (hi hi, hi lo, lo hi, lo lo, hi rest, rest hi) leave an error of about
+//     3 * 2^-24 per product, FP32 rounding level.  Logit accuracy matters in
+//     absolute terms (a logit error d scales a weight by e^d), so large
+//     logits need all six.  12 MFMAs per 32-key tile.
+//   O^T += V^T P^T: two planes each, three terms (hi hi, hi lo, lo hi), a
+//     relative error below 2^-16 per weighted value.  6 MFMAs per tile.
+//
+// The split: hi = bf16(x) (round to nearest), lo = bf16(x - hi), rest =
+// bf16(x - hi - lo).  Each difference is exact (Sterbenz), and x - hi - lo
+// keeps at most 8 significant bits, so hi + lo + rest == x for normal x.
+//
+// Softmax, row classification, mask handling and the output are the FP32
+// kernel's (see attention.hip): log2-domain logits with the scaled bias as
+// the accumulator's start value and a snapped reference on rows with an
+// unmasked key; fl(fl(s + mask) + bias) in natural units with a lazy max on
+// fully masked rows.  The pipeline is the BF16 kernel's: K is staged one
+// tile ahead of V, and the S^T MFMAs of tile t + 1 are issued before the
+// softmax of tile t.
+#include "attn_common.hpp"
+#include "common.hpp"
+#include "kernels.hpp"
+
+#include <cmath>
+#include <type_traits>
+
+namespace fpx {
+namespace {
+
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kThreads = 256;
+constexpr int kRowB = kHeadDim + 8;  // bf16 per LDS row: 80 bytes, conflict-free b128 reads
+constexpr int kMaxKeys = kTileFlagWords * 32 * kBk;
+
+typedef __bf16 KPlane[kBk][kRowB];       // [key][channel]
+typedef __bf16 VPlane[kHeadDim][kRowB];  // [channel][key position], see v_position
+
+__device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ void split3(f32x4 x, bf16x4& hi, bf16x4& lo, bf16x4& rest) {
+  hi = __builtin_convertvector(x, bf16x4);
+  const f32x4 r1 = x - __builtin_convertvector(hi, f32x4);
+  lo = __builtin_convertvector(r1, bf16x4);
+  rest = __builtin_convertvector(r1 - __builtin_convertvector(lo, f32x4), bf16x4);
+}
+__device__ __forceinline__ void split3(f32x8 x, bf16x8& hi, bf16x8& lo, bf16x8& rest) {
+  hi = __builtin_convertvector(x, bf16x8);
+  const f32x8 r1 = x - __builtin_convertvector(hi, f32x8);
+  lo = __builtin_convertvector(r1, bf16x8);
+  rest = __builtin_convertvector(r1 - __builtin_convertvector(lo, f32x8), bf16x8);
+}
+__device__ __forceinline__ void split2(f32x4 x, bf16x4& hi, bf16x4& lo) {
+  hi = __builtin_convertvector(x, bf16x4);
+  lo = __builtin_convertvector(x - __builtin_convertvector(hi, f32x4), bf16x4);
+}
+__device__ __forceinline__ void split2(f32x8 x, bf16x8& hi, bf16x8& lo) {
+  hi = __builtin_convertvector(x, bf16x8);
+  lo = __builtin_convertvector(x - __builtin_convertvector(hi, f32x8), bf16x8);
+}
+
+// V^T keys are stored in the order in which the S^T accumulator registers
+// hold them: within each 16-key block, keys 0-3, 8-11, 4-7, 12-15.  Position
+// of the 4-key group g (keys 4g..4g+3) of a tile:
+__device__ __forceinline__ int v_position(int g) {
+  const int perm = (g & 1) * 2 + ((g >> 1) & 1);  // 0, 2, 1, 3
+  return (g >> 2) * 16 + perm * 4;
+}
+
+__global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a, int nqt, int nkt,
+                                                                      uint32_t total) {
+  __shared__ __attribute__((aligned(16))) KPlane Ks[2][3];
+  __shared__ __attribute__((aligned(16))) VPlane Vs[2][2];
+  __shared__ __attribute__((aligned(16))) float Ms[kMaxKeys];
+
+  const uint32_t logical = xcd_remap(blockIdx.x, total);
+  const int groups = (a.batch + kRowGroup - 1) / kRowGroup;
+  const int per_head = groups * kRowGroup * nqt;
+  const int h = (int)(logical / per_head);
+  const int rem = (int)(logical % per_head);
+  const int grp = rem / (kRowGroup * nqt);
+  const int in_grp = rem % (kRowGroup * nqt);
+  const int qt = in_grp / kRowGroup;
+  const int b = grp * kRowGroup + in_grp % kRowGroup;
+  if (b >= a.batch) return;  // padding of the last row group; uniform per work-group
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+  const int j0 = qt * kBq;
+  const int jq = j0 + 32 * w + l32;
+  const int qt32 = (j0 >> 5) + w;
+  const int row8 = tid >> 3;
+  const int col4 = (tid & 7) * 4;
+  const int vpos = v_position(col4 >> 2);
+  const int last = nkt - 1;
+
+  // Per-work-group buffer descriptors over the (b, h) slices and the wave's
+  // bias fragments (h, qt32, all key tiles), as in the FP32 kernel.
+  const int64_t bh = (int64_t)b * kHeads + h;
+  const int64_t nt = a.np >> 5;
+  const int64_t slice = (int64_t)a.np * kHeadDim;
+  const int64_t frag = ((int64_t)h * nt + qt32) * nt * 1024;
+  const __amdgpu_buffer_rsrc_t rk = buffer(a.k + bh * slice, slice * 4);
+  const __amdgpu_buffer_rsrc_t rv = buffer(a.v + bh * slice, slice * 4);
+  const __amdgpu_buffer_rsrc_t rb = buffer(a.bias + frag, nt * 4096);
+  const __amdgpu_buffer_rsrc_t rb2 = buffer(a.bias_l2 + frag, nt * 4096);
+  const uint32_t ok = (uint32_t)(row8 * kHeadDim + col4) * 4;
+  const uint32_t ov = (uint32_t)(row8 * a.np + col4) * 4;
+  const uint32_t ob = (uint32_t)lane * 16;
+  auto load_k = [&](int t) { return buffer_f4(rk, ok, (uint32_t)t * 4096); };
+  auto load_v = [&](int t) { return buffer_f4(rv, ov, (uint32_t)t * 128); };
+  auto load_frag = [&](__amdgpu_buffer_rsrc_t r, int t) -> f32x16 {
+    const uint32_t s = (uint32_t)t * 4096;
+    return cat4(buffer_f4(r, ob, s), buffer_f4(r, ob + 1024, s), buffer_f4(r, ob + 2048, s),
+                buffer_f4(r, ob + 3072, s));
+  };
+  // K(t) into the three K planes, V(t) into the two V planes (thread: key or
+  // channel row8, four consecutive columns).
+  auto store_k = [&](int buf, f32x4 kv) {
+    bf16x4 hi, lo, rest;
+    split3(kv, hi, lo, rest);
+    *(bf16x4*)&Ks[buf][0][row8][col4] = hi;
+    *(bf16x4*)&Ks[buf][1][row8][col4] = lo;
+    *(bf16x4*)&Ks[buf][2][row8][col4] = rest;
+  };
+  auto store_v = [&](int buf, f32x4 vv) {
+    bf16x4 hi, lo;
+    split2(vv, hi, lo);
+    *(bf16x4*)&Vs[buf][0][row8][vpos] = hi;
+    *(bf16x4*)&Vs[buf][1][row8][vpos] = lo;
+  };
+
+  // Row classification from the tile flags, as in the FP32 kernel.
+  uint32_t mw[kTileFlagWords];
+  uint32_t any = 0u, open = 0u;
+  {
+    const uint32_t* f = a.tile_flags + (int64_t)b * 2 * kTileFlagWords;
+#pragma unroll
+    for (int i = 0; i < kTileFlagWords; ++i) {
+      const int lo = 32 * i;
+      const uint32_t valid = nkt >= lo + 32 ? 0xffffffffu : nkt > lo ? (1u << (nkt - lo)) - 1u : 0u;
+      mw[i] = f[i];
+      any |= mw[i] & valid;
+      open |= ~f[kTileFlagWords + i] & valid;
+    }
+  }
+  const bool has_unmasked = open != 0u;
+  auto masked = [&](int t) -> bool {
+    const uint32_t word = t < 32 ? mw[0] : t < 64 ? mw[1] : t < 96 ? mw[2] : mw[3];
+    return (word >> (t & 31)) & 1u;
+  };
+  if (any != 0u) {
+    const float* src = a.mbias + (int64_t)b * a.mb_stride;
+    for (int k = 4 * tid; k < nkt * kBk; k += 4 * kThreads) *(f32x4*)&Ms[k] = *(const f32x4*)(src + k);
+  }
+  auto mask_vals = [&](int t) -> f32x16 {
+    const float* m = &Ms[t * kBk + 4 * half];
+    return cat4(*(const f32x4*)(m), *(const f32x4*)(m + 8), *(const f32x4*)(m + 16),
+                *(const f32x4*)(m + 24));
+  };
+
+  f32x16 o = {};
+  float l_run = 0.f;
+
+  auto run = [&](auto exact_tag) {
+    constexpr bool kExact = decltype(exact_tag)::value;
+    const f32x16 zero16 = {};
+
+    // Q planes, the B operand of S^T: lane holds Q[jq][16m + 8half + e],
+    // scaled by log2(e) on the fast path.
+    bf16x8 qh[2], ql[2], qr[2];
+    {
+      const float* src = a.q + (bh * a.np + jq) * kHeadDim + 8 * half;
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const f32x4 u = *(const f32x4*)(src + 16 * m);
+        const f32x4 v = *(const f32x4*)(src + 16 * m + 4);
+        f32x8 q = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+        if (!kExact) q *= kLog2e;
+        split3(q, qh[m], ql[m], qr[m]);
+      }
+    }
+
+    // S^T of the tile in Ks[buf], added to x (the scaled bias on the fast
+    // path, zero on the exact path); the smallest terms first.
+    auto scores = [&](int buf, f32x16 x) -> f32x16 {
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const bf16x8 kh = *(const bf16x8*)&Ks[buf][0][l32][16 * m + 8 * half];
+        const bf16x8 kl = *(const bf16x8*)&Ks[buf][1][l32][16 * m + 8 * half];
+        const bf16x8 kr = *(const bf16x8*)&Ks[buf][2][l32][16 * m + 8 * half];
+        x = mfma_bf16(kr, qh[m], x);
+        x = mfma_bf16(kh, qr[m], x);
+        x = mfma_bf16(kl, ql[m], x);
+        x = mfma_bf16(kl, qh[m], x);
+        x = mfma_bf16(kh, ql[m], x);
+        x = mfma_bf16(kh, qh[m], x);
+      }
+      return x;
+    };
+    // The rest of the logits of tile t: the mask bias on masked tiles (fast,
+    // in log2 units), or fl(fl(s + mask) + bias) in natural units (exact).
+    auto finish = [&](f32x16& x, int t) {
+      if (kExact) {
+        const f32x16 mb = mask_vals(t);
+        const f32x16 bias = load_frag(rb, t);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[r] = (x[r] + mb[r]) + bias[r];
+      } else if (masked(t)) {
+        const f32x16 mb = mask_vals(t);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[r] = __builtin_fmaf(mb[r], kLog2e, x[r]);
+      }
+    };
+    // Start value of a tile's S^T accumulator.
+    auto init = [&](int t) -> f32x16 { return kExact ? zero16 : load_frag(rb2, t); };
+
+    // Reference state of this lane's query (see attention.hip).
+    float m_ref = -INFINITY;
+    float m_thr = -INFINITY;
+    float c_ref = 0.f;
+    bool has_ref = false;
+    bool c_zero = true;
+
+    // Logits x of one tile -> the weights' hi and lo planes (P operand).
+    auto softmax = [&](const f32x16& x, bf16x8 (&ph)[2], bf16x8 (&pl)[2]) {
+      f32x16 p;
+      auto pack = [&]() {
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          const f32x8 v = {p[8 * m + 0], p[8 * m + 1], p[8 * m + 2], p[8 * m + 3],
+                           p[8 * m + 4], p[8 * m + 5], p[8 * m + 6], p[8 * m + 7]};
+          split2(v, ph[m], pl[m]);
+        }
+      };
+      if (kExact) {
+        const float mt = xor32_max(max16(x));
+        if (__any(mt > m_thr)) {
+          const float m_new = __builtin_elementwise_maximum(m_ref, mt);
+          const float c_new = m_new == -INFINITY ? 0.f : m_new * kLog2e;
+          const float alpha = m_ref == -INFINITY ? 0.f : exp2_fast(c_ref - c_new);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[r] *= alpha;
+          l_run *= alpha;
+          m_ref = m_new;
+          c_ref = c_new;
+          m_thr = m_new + kRescaleNat;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[r] = exp2_fast(__builtin_fmaf(x[r], kLog2e, -c_ref));
+        l_run += sum16(p);
+        pack();
+        return;
+      }
+      float ovf = 0.f;
+      if (has_ref) {
+        if (c_zero) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) p[r] = exp2_fast(x[r]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) p[r] = exp2_fast(x[r] - c_ref);
+        }
+        const float l_new = l_run + sum16(p);
+        const bool over = !(l_new <= kSumLimit);  // NaN or inf count as overflow
+        if (!__any(over)) {
+          l_run = l_new;
+          pack();
+          return;
+        }
+        ovf = over ? 1.f : 0.f;
+      }
+      // Rare path, taken by the whole wavefront (attention.hip).
+      const float mt = xor32_max(max16(x));
+      const bool fresh = m_ref == -INFINITY;
+      const bool need = fresh || xor32_max(ovf) > 0.f || mt > c_ref + kSnap;
+      m_ref = __builtin_elementwise_maximum(m_ref, mt);
+      const float snapped =
+          (m_ref == -INFINITY || (m_ref >= -kSnap && m_ref <= kSnap)) ? 0.f : m_ref;
+      const float c_new = fresh ? snapped
+                          : need ? __builtin_elementwise_maximum(snapped, c_ref + kLift)
+                                 : c_ref;
+      const float alpha = fresh ? 0.f : exp2_fast(c_ref - c_new);  // 1 when unchanged
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[r] *= alpha;
+      l_run *= alpha;
+      c_ref = c_new;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) p[r] = exp2_fast(x[r] - c_ref);
+      l_run += sum16(p);
+      has_ref = __all(m_ref != -INFINITY);
+      c_zero = __all(c_ref == 0.f);
+      pack();
+    };
+
+    // O^T += V^T P^T for the tile in Vs[buf].
+    auto pv = [&](int buf, const bf16x8 (&ph)[2], const bf16x8 (&pl)[2]) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const bf16x8 vh = *(const bf16x8*)&Vs[buf][0][l32][16 * m + 8 * half];
+        const bf16x8 vl = *(const bf16x8*)&Vs[buf][1][l32][16 * m + 8 * half];
+        o = mfma_bf16(vl, ph[m], o);
+        o = mfma_bf16(vh, pl[m], o);
+        o = mfma_bf16(vh, ph[m], o);
+      }
+    };
+
+    // Prologue: K(0), K(1), V(0) into LDS; S^T(0); K(2), V(1) in flight.
+    f32x16 x_a = init(0);
+    f32x16 x_b = init(last < 1 ? last : 1);
+    store_k(0, load_k(0));
+    store_v(0, load_v(0));
+    store_k(1, load_k(last < 1 ? last : 1));
+    f32x4 kreg = load_k(last < 2 ? last : 2);
+    f32x4 vreg = load_v(last < 1 ? last : 1);
+    __syncthreads();
+    x_a = scores(0, x_a);
+    finish(x_a, 0);
+    __syncthreads();  // every wave is done with K(0) before Ks[0] is refilled
+
+    // Iteration kt: Ks[(kt+1)&1] = K(kt+1), Vs[kt&1] = V(kt); cur = logits
+    // of tile kt; nxt = start value of tile kt+1; kreg = K(kt+2) and vreg =
+    // V(kt+1) in flight.  Indices past the last tile are clamped (in range,
+    // never used).
+    auto body = [&](int kt, f32x16& cur, f32x16& nxt) {
+      nxt = scores((kt + 1) & 1, nxt);
+      bf16x8 ph[2], pl[2];
+      softmax(cur, ph, pl);
+      pv(kt & 1, ph, pl);
+      finish(nxt, kt + 1);
+      cur = init(kt + 2 < last ? kt + 2 : last);
+      store_k(kt & 1, kreg);
+      store_v((kt + 1) & 1, vreg);
+      kreg = load_k(kt + 3 < last ? kt + 3 : last);
+      vreg = load_v(kt + 2 < last ? kt + 2 : last);
+      __syncthreads();
+    };
+    auto tail = [&](const f32x16& cur, int kt) {
+      bf16x8 ph[2], pl[2];
+      softmax(cur, ph, pl);
+      pv(kt & 1, ph, pl);
+    };
+    int kt = 0;
+    for (; kt + 2 < nkt; kt += 2) {
+      body(kt, x_a, x_b);
+      body(kt + 1, x_b, x_a);
+    }
+    if (kt + 1 < nkt) {
+      body(kt, x_a, x_b);
+      tail(x_b, kt + 1);
+    } else {
+      tail(x_a, kt);
+    }
+  };
+  if (has_unmasked) {
+    run(std::false_type{});
+  } else {
+    run(std::true_type{});
+  }
+
+  const float l_tot = xor32_sum(l_run);
+  if (jq < a.n) {
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int c = 8 * rr + 4 * half;  // channels c..c+3 of head h
+      f32x4 ov4 = {o[4 * rr + 0] / l_tot, o[4 * rr + 1] / l_tot, o[4 * rr + 2] / l_tot,
+                   o[4 * rr + 3] / l_tot};
+      const int64_t col = h * kHeadDim + c;
+      if (a.gate) ov4 = ov4 * *(const f32x4*)(a.gate + ((int64_t)b * a.np + jq) * kHidden + col);
+      *(f32x4*)(a.out + ((int64_t)b * a.n + jq) * kHidden + col) = ov4;
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_attention_split(const AttnArgs& a, hipStream_t stream) {
+  const int nqt = (int)(a.np / kBq);
+  const int nkt = (int)(round_up(a.n, kBk) / kBk);
+  const uint64_t groups = ((uint64_t)a.batch + kRowGroup - 1) / kRowGroup;
+  const uint64_t total = groups * kRowGroup * kHeads * nqt;
+  if (total == 0) return hipSuccess;
+  if (total > 0x7fffffffull) return hipErrorInvalidValue;
+  if (a.tile_flags == nullptr || a.bias_l2 == nullptr || nkt > kTileFlagWords * 32)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(attention_split_kernel, dim3((uint32_t)total), dim3(kThreads), 0, stream, a,
+                     nqt, nkt, (uint32_t)total);
+  return hipGetLastError();
+}
+
+}  // namespace fpx

@@ -1,0 +1,85 @@
+// Helpers shared by the FP32-accurate attention kernels (attention.hip on the
+// FP32 matrix cores, attention_split.hip on the BF16 matrix cores): buffer
+// loads, the lane-pair exchanges of the transposed S^T / O^T layout, row
+// reductions, and the softmax reference constants.
+#pragma once
+
+#include "common.hpp"
+
+namespace fpx {
+
+constexpr int kBq = 128;   // queries per work-group
+constexpr int kBk = 32;    // keys per tile
+constexpr int kRowGroup = 8;  // outer rows that share a bias slice in L2
+// Exact path: rescale when a tile max exceeds the reference by 8 binary
+// orders (in logit units).
+constexpr float kRescaleNat = 8.0f * 0.69314718055994531f;
+// Fast path (log2 units): the reference snaps to 0 while the row max lies in
+// [-kSnap, kSnap]; the running sum may grow to kSumLimit before a rescale; a
+// rescale forced by the sum moves the reference up by at least kLift.
+constexpr float kSnap = 56.0f;
+constexpr float kSumLimit = 18446744073709551616.0f;  // 2^64
+constexpr float kLift = 40.0f;
+
+__device__ __forceinline__ f32x16 cat4(f32x4 a, f32x4 b, f32x4 c, f32x4 d) {
+  f32x16 r;
+  r[0] = a.x; r[1] = a.y; r[2] = a.z; r[3] = a.w;
+  r[4] = b.x; r[5] = b.y; r[6] = b.z; r[7] = b.w;
+  r[8] = c.x; r[9] = c.y; r[10] = c.z; r[11] = c.w;
+  r[12] = d.x; r[13] = d.y; r[14] = d.z; r[15] = d.w;
+  return r;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer(const float* base, int64_t bytes) {
+  // dword 3 = 0x00020000: raw 32-bit buffer access on gfx9-family parts.
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+__device__ __forceinline__ f32x4 buffer_f4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+// max / sum of v over the lane pair (l, l ^ 32) with v_permlane32_swap
+// (no LDS round trip): after the swap one copy holds the low half in both
+// halves and the other the high half.
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v),
+                                                  __builtin_bit_cast(unsigned, v), false, false);
+  return __builtin_elementwise_maximum(__builtin_bit_cast(float, (unsigned)r[0]),
+                                       __builtin_bit_cast(float, (unsigned)r[1]));
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v),
+                                                  __builtin_bit_cast(unsigned, v), false, false);
+  return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+}
+
+// NaN-propagating max of 16 values (v_maximum3_f32): a NaN logit poisons its
+// row, as in the native softmax.
+__device__ __forceinline__ float max16(const f32x16& s) {
+  auto mx = [](float x, float y) { return __builtin_elementwise_maximum(x, y); };
+  float m0 = mx(mx(s[0], s[1]), s[2]);
+  float m1 = mx(mx(s[3], s[4]), s[5]);
+  float m2 = mx(mx(s[6], s[7]), s[8]);
+  float m3 = mx(mx(s[9], s[10]), s[11]);
+  float m4 = mx(mx(s[12], s[13]), s[14]);
+  m0 = mx(mx(m0, m1), s[15]);
+  m2 = mx(mx(m2, m3), m4);
+  return mx(m0, m2);
+}
+
+__device__ __forceinline__ float sum16(const f32x16& p) {
+  float a0 = p[0] + p[4], a1 = p[1] + p[5], a2 = p[2] + p[6], a3 = p[3] + p[7];
+  a0 += p[8];
+  a1 += p[9];
+  a2 += p[10];
+  a3 += p[11];
+  a0 += p[12];
+  a1 += p[13];
+  a2 += p[14];
+  a3 += p[15];
+  return (a0 + a1) + (a2 + a3);
+}
+
+}  // namespace fpx
