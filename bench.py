@@ -585,13 +585,48 @@ def main() -> int:
     flops = block.block_flops(n)
     step_flop = 2 * flops["block"]
     value = step_flop / (ms_per_step * 1e-3) / 1e12
-    attend_tflops = flops["core"] / (stages["attend"] * 1e-3) / 1e12
     traffic = None
     if TRAFFIC_FILE.exists():
         try:
-            traffic = json.loads(TRAFFIC_FILE.read_text()).get(cfg.name, {}).get("bytes_per_launch")
+            key = cfg.name if os.environ.get("FPX_ATTENTION_MFMA") != "f32" else f"{cfg.name}/fp32-mfma"
+            traffic = json.loads(TRAFFIC_FILE.read_text()).get(key, {}).get("bytes_per_launch")
         except (ValueError, AttributeError):
             traffic = None
+    attend_tflops = flops["core"] / (stages["attend"] * 1e-3) / 1e12
+    split = cfg.dtype != "bf16" and os.environ.get("FPX_ATTENTION_MFMA") != "f32"
+    if cfg.dtype == "bf16":
+        kernel_name = "attention_bf16_kernel (fpx_tri_attn_attend, BF16)"
+    elif split:
+        kernel_name = "attention_split_kernel (fpx_tri_attn_attend)"
+    else:
+        kernel_name = "attention_kernel<kAttnBlock> (fpx_tri_attn_attend)"
+    roofline = {
+        "kernel": kernel_name,
+        "bound": "mfma",
+        "achieved": round(attend_tflops, 3),
+        "peak": peak,
+        "unit": "TFLOP/s",
+        "frac": round(attend_tflops / peak, 4),
+        "traffic": traffic,
+        "flop_per_launch": flops["core"],
+        "avg_launch_ms": round(stages["attend"], 4),
+    }
+    if split:
+        # FP32-accurate products executed on the BF16 matrix cores: per 32 x 32
+        # (query x key) wave tile, 18 v_mfma_f32_32x32x16_bf16 (6 terms of
+        # S^T, 3 of O^T, two K-halves each) = 18 * 32768 flop, against
+        # 2 * 65536 algorithmic flop.
+        np_ = -(-n // 128) * 128
+        nkt = -(-n // 32)
+        executed = n * 4 * (np_ // 32) * nkt * 18 * 32768
+        executed_tflops = executed / (stages["attend"] * 1e-3) / 1e12
+        roofline.update({
+            "matrix_unit": "bf16 (exact 3-plane split of K and Q, 2-plane V and P)",
+            "executed_flop_per_launch": executed,
+            "executed_tflops": round(executed_tflops, 3),
+            "executed_peak": BF16_MFMA_PEAK_TFLOPS,
+            "executed_frac": round(executed_tflops / BF16_MFMA_PEAK_TFLOPS, 4),
+        })
     result = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -616,18 +651,7 @@ def main() -> int:
             "step_flop": step_flop,
             "stage_ms_start_node": {k: round(v, 4) for k, v in stages.items()},
         },
-        "roofline": {
-            "kernel": ("attention_bf16_kernel (fpx_tri_attn_attend, BF16)" if cfg.dtype == "bf16"
-                       else "attention_kernel<kAttnBlock> (fpx_tri_attn_attend)"),
-            "bound": "mfma",
-            "achieved": round(attend_tflops, 3),
-            "peak": peak,
-            "unit": "TFLOP/s",
-            "frac": round(attend_tflops / peak, 4),
-            "traffic": traffic,
-            "flop_per_launch": flops["core"],
-            "avg_launch_ms": round(stages["attend"], 4),
-        },
+        "roofline": roofline,
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
