@@ -538,7 +538,7 @@ bool block_on_fp32_mfma() {
 }  // namespace
 
 hipError_t launch_attention(int layout, const AttnArgs& a, hipStream_t stream) {
-  if (layout == kAttnBlock && !block_on_fp32_mfma()) return launch_attention_split(a, stream);
+  if (layout != kAttnHeadLast && !block_on_fp32_mfma()) return launch_attention_split(layout, a, stream);
   // Query tiles cover the padded extent; key tiles stop at the last real key
   // (tiles wholly past n hold only -inf mask bias and contribute nothing).
   const int nqt = (int)((layout != kAttnHeadLast ? a.np : round_up(a.n, kBq)) / kBq);

@@ -112,8 +112,16 @@ __device__ __forceinline__ int v_position(int g) {
   return (g >> 2) * 16 + perm * 4;
 }
 
+// LAYOUT kAttnBlock: the block's workspace (q, k [B][H][np][32], v^T
+// [B][H][32][np]).  kAttnStrided: a caller's q, k, v, out with (batch, head,
+// row) strides (fpx_attn_strided); K and V rows past n are clamped to row
+// n - 1 (finite values whose weights are exactly 0: their staged mask bias is
+// -inf), and V rows are transposed into the V^T planes on their way to LDS.
+// Both read the staged bias copies, mask rows and tile flags.
+template <int LAYOUT>
 __global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a, int nqt, int nkt,
                                                                       uint32_t total) {
+  constexpr bool kBlock = LAYOUT == kAttnBlock;
   __shared__ __attribute__((aligned(16))) KPlane Ks[2][3];
   __shared__ __attribute__((aligned(16))) VPlane Vs[2][2];
   __shared__ __attribute__((aligned(16))) float Ms[kMaxKeys];
@@ -147,15 +155,33 @@ __global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a
   const int64_t nt = a.np >> 5;
   const int64_t slice = (int64_t)a.np * kHeadDim;
   const int64_t frag = ((int64_t)h * nt + qt32) * nt * 1024;
-  const __amdgpu_buffer_rsrc_t rk = buffer(a.k + bh * slice, slice * 4);
-  const __amdgpu_buffer_rsrc_t rv = buffer(a.v + bh * slice, slice * 4);
+  const __amdgpu_buffer_rsrc_t rk =
+      kBlock ? buffer(a.k + bh * slice, slice * 4)
+             : buffer(a.k + b * a.ks[0] + h * a.ks[1], ((int64_t)(a.n - 1) * a.ks[2] + kHeadDim) * 4);
+  const __amdgpu_buffer_rsrc_t rv =
+      kBlock ? buffer(a.v + bh * slice, slice * 4)
+             : buffer(a.v + b * a.vs[0] + h * a.vs[1], ((int64_t)(a.n - 1) * a.vs[2] + kHeadDim) * 4);
   const __amdgpu_buffer_rsrc_t rb = buffer(a.bias + frag, nt * 4096);
   const __amdgpu_buffer_rsrc_t rb2 = buffer(a.bias_l2 + frag, nt * 4096);
   const uint32_t ok = (uint32_t)(row8 * kHeadDim + col4) * 4;
   const uint32_t ov = (uint32_t)(row8 * a.np + col4) * 4;
   const uint32_t ob = (uint32_t)lane * 16;
-  auto load_k = [&](int t) { return buffer_f4(rk, ok, (uint32_t)t * 4096); };
-  auto load_v = [&](int t) { return buffer_f4(rv, ov, (uint32_t)t * 128); };
+  // Strided rows: key t*32 + row8, clamped to n - 1; channels col4..+3.
+  auto row_of = [&](int t) -> uint32_t {
+    const int j = t * kBk + row8;
+    return (uint32_t)(j < a.n - 1 ? j : a.n - 1);
+  };
+  auto load_k = [&](int t) {
+    if constexpr (kBlock) return buffer_f4(rk, ok, (uint32_t)t * 4096);
+    else return buffer_f4(rk, row_of(t) * (uint32_t)a.ks[2] * 4 + (uint32_t)col4 * 4, 0);
+  };
+  auto load_v = [&](int t) {
+    if constexpr (kBlock) return buffer_f4(rv, ov, (uint32_t)t * 128);
+    else return buffer_f4(rv, row_of(t) * (uint32_t)a.vs[2] * 4 + (uint32_t)col4 * 4, 0);
+  };
+  // Strided V: thread holds key row8, channels col4..+3; its position in the
+  // V^T planes' key order:
+  const int kpos = v_position(row8 >> 2) + (row8 & 3);
   auto load_frag = [&](__amdgpu_buffer_rsrc_t r, int t) -> f32x16 {
     const uint32_t s = (uint32_t)t * 4096;
     return cat4(buffer_f4(r, ob, s), buffer_f4(r, ob + 1024, s), buffer_f4(r, ob + 2048, s),
@@ -173,8 +199,16 @@ __global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a
   auto store_v = [&](int buf, f32x4 vv) {
     bf16x4 hi, lo;
     split2(vv, hi, lo);
-    *(bf16x4*)&Vs[buf][0][row8][vpos] = hi;
-    *(bf16x4*)&Vs[buf][1][row8][vpos] = lo;
+    if constexpr (kBlock) {
+      *(bf16x4*)&Vs[buf][0][row8][vpos] = hi;
+      *(bf16x4*)&Vs[buf][1][row8][vpos] = lo;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        Vs[buf][0][col4 + e][kpos] = hi[e];
+        Vs[buf][1][col4 + e][kpos] = lo[e];
+      }
+    }
   };
 
   // Row classification from the tile flags, as in the FP32 kernel.
@@ -217,11 +251,15 @@ __global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a
     // scaled by log2(e) on the fast path.
     bf16x8 qh[2], ql[2], qr[2];
     {
-      const float* src = a.q + (bh * a.np + jq) * kHeadDim + 8 * half;
+      const bool ok_q = kBlock || jq < a.n;
+      const float* src = kBlock ? a.q + (bh * a.np + jq) * kHeadDim + 8 * half
+                                : a.q + b * a.qs[0] + h * a.qs[1] +
+                                      (int64_t)(ok_q ? jq : 0) * a.qs[2] + 8 * half;
+      const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
-        const f32x4 u = *(const f32x4*)(src + 16 * m);
-        const f32x4 v = *(const f32x4*)(src + 16 * m + 4);
+        const f32x4 u = ok_q ? *(const f32x4*)(src + 16 * m) : zero4;
+        const f32x4 v = ok_q ? *(const f32x4*)(src + 16 * m + 4) : zero4;
         f32x8 q = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
         if (!kExact) q *= kLog2e;
         split3(q, qh[m], ql[m], qr[m]);
@@ -412,16 +450,20 @@ __global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a
       const int c = 8 * rr + 4 * half;  // channels c..c+3 of head h
       f32x4 ov4 = {o[4 * rr + 0] / l_tot, o[4 * rr + 1] / l_tot, o[4 * rr + 2] / l_tot,
                    o[4 * rr + 3] / l_tot};
-      const int64_t col = h * kHeadDim + c;
-      if (a.gate) ov4 = ov4 * *(const f32x4*)(a.gate + ((int64_t)b * a.np + jq) * kHidden + col);
-      *(f32x4*)(a.out + ((int64_t)b * a.n + jq) * kHidden + col) = ov4;
+      if constexpr (kBlock) {
+        const int64_t col = h * kHeadDim + c;
+        if (a.gate) ov4 = ov4 * *(const f32x4*)(a.gate + ((int64_t)b * a.np + jq) * kHidden + col);
+        *(f32x4*)(a.out + ((int64_t)b * a.n + jq) * kHidden + col) = ov4;
+      } else {
+        *(f32x4*)(a.out + b * a.os[0] + h * a.os[1] + (int64_t)jq * a.os[2] + c) = ov4;
+      }
     }
   }
 }
 
 }  // namespace
 
-hipError_t launch_attention_split(const AttnArgs& a, hipStream_t stream) {
+hipError_t launch_attention_split(int layout, const AttnArgs& a, hipStream_t stream) {
   const int nqt = (int)(a.np / kBq);
   const int nkt = (int)(round_up(a.n, kBk) / kBk);
   const uint64_t groups = ((uint64_t)a.batch + kRowGroup - 1) / kRowGroup;
@@ -430,8 +472,15 @@ hipError_t launch_attention_split(const AttnArgs& a, hipStream_t stream) {
   if (total > 0x7fffffffull) return hipErrorInvalidValue;
   if (a.tile_flags == nullptr || a.bias_l2 == nullptr || nkt > kTileFlagWords * 32)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(attention_split_kernel, dim3((uint32_t)total), dim3(kThreads), 0, stream, a,
-                     nqt, nkt, (uint32_t)total);
+  if (layout == kAttnBlock) {
+    hipLaunchKernelGGL(attention_split_kernel<kAttnBlock>, dim3((uint32_t)total), dim3(kThreads), 0,
+                       stream, a, nqt, nkt, (uint32_t)total);
+  } else if (layout == kAttnStrided) {
+    hipLaunchKernelGGL(attention_split_kernel<kAttnStrided>, dim3((uint32_t)total), dim3(kThreads),
+                       0, stream, a, nqt, nkt, (uint32_t)total);
+  } else {
+    return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

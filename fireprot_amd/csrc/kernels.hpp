@@ -60,12 +60,12 @@ struct AttnArgs {
   int np;
 };
 
-// kAttnBlock runs attention_split_kernel (FP32-accurate products on the BF16
-// matrix cores) unless the environment sets FPX_ATTENTION_MFMA=f32, which
-// selects attention_kernel<kAttnBlock> on the FP32 matrix cores (read once
-// per process).
+// kAttnBlock and kAttnStrided run attention_split_kernel (FP32-accurate
+// products on the BF16 matrix cores) unless the environment sets
+// FPX_ATTENTION_MFMA=f32, which selects attention_kernel on the FP32 matrix
+// cores (read once per process); kAttnHeadLast always runs attention_kernel.
 hipError_t launch_attention(int layout, const AttnArgs& args, hipStream_t stream);
-hipError_t launch_attention_split(const AttnArgs& args, hipStream_t stream);
+hipError_t launch_attention_split(int layout, const AttnArgs& args, hipStream_t stream);
 
 // --------------------------------------------------------------- projection
 // Row tiles are 32 consecutive j of one outer row i; A rows are read at
