@@ -123,6 +123,36 @@ def cpu_baseline(cfg, z, mask, weights, budget_s: float = 40.0) -> dict:
 OF3_METRIC = "OpenFold3 _attention ms + TFLOP/s (% MFMA peak) at B=N=1536 FP32, 1 GPU"
 
 
+def split_executed(batch: int, n: int, ms: float) -> dict:
+    """BF16 matrix-core work the split attention kernel executes for its
+    FP32-accurate products: per 32 x 32 (query x key) wave tile, 18
+    v_mfma_f32_32x32x16_bf16 (6 terms of S^T, 3 of O^T, two K-halves each) =
+    18 * 32768 flop, against 2 * 65536 algorithmic flop.  Query rows are
+    padded to 128, keys to 32."""
+    np_ = -(-n // 128) * 128
+    nkt = -(-n // 32)
+    executed = batch * 4 * (np_ // 32) * nkt * 18 * 32768
+    executed_tflops = executed / (ms * 1e-3) / 1e12
+    return {
+        "matrix_unit": "bf16 (exact 3-plane split of K and Q, 2-plane V and P)",
+        "executed_flop_per_launch": executed,
+        "executed_tflops": round(executed_tflops, 3),
+        "executed_peak": BF16_MFMA_PEAK_TFLOPS,
+        "executed_frac": round(executed_tflops / BF16_MFMA_PEAK_TFLOPS, 4),
+    }
+
+
+def recorded_traffic(key: str) -> int | None:
+    """HBM bytes per launch recorded for ``key`` from the FETCH_SIZE and
+    WRITE_SIZE counter runs, or None."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    try:
+        return json.loads(TRAFFIC_FILE.read_text()).get(key, {}).get("bytes_per_launch")
+    except (ValueError, AttributeError):
+        return None
+
+
 def bench_openfold3(args) -> dict:
     """OpenFold3 ``_attention`` at B = N = 1536 (the pair stack's triangle
     attention as OpenFold3 calls it), ending-node wire layout: q/k/v
@@ -201,6 +231,7 @@ def bench_openfold3(args) -> dict:
 
     flop = block_flops(n)["core"]
     tflops = flop / (ms * 1e-3) / 1e12
+    fp32_mfma = os.environ.get("FPX_ATTENTION_MFMA") == "f32"
     result = {
         "metric": OF3_METRIC,
         "value": round(tflops, 3),
@@ -222,10 +253,13 @@ def bench_openfold3(args) -> dict:
             "max_abs_vs_native": diff,
         },
         "roofline": {
-            "kernel": "attention_kernel<kAttnStrided> + staging (fpx_attn_strided)",
+            "kernel": (f"attention_{'kernel' if fp32_mfma else 'split_kernel'}<kAttnStrided>"
+                       " + staging (fpx_attn_strided)"),
             "bound": "mfma", "achieved": round(tflops, 3), "peak": FP32_MFMA_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4),
-            "traffic": None, "flop_per_launch": flop, "avg_launch_ms": round(ms, 4),
+            "traffic": recorded_traffic("openfold3/fp32-mfma" if fp32_mfma else "openfold3"),
+            "flop_per_launch": flop, "avg_launch_ms": round(ms, 4),
+            **({} if fp32_mfma else split_executed(n, n, ms)),
         },
         "cpu_baseline": None,
     }
@@ -585,15 +619,10 @@ def main() -> int:
     flops = block.block_flops(n)
     step_flop = 2 * flops["block"]
     value = step_flop / (ms_per_step * 1e-3) / 1e12
-    traffic = None
-    if TRAFFIC_FILE.exists():
-        try:
-            key = cfg.name if os.environ.get("FPX_ATTENTION_MFMA") != "f32" else f"{cfg.name}/fp32-mfma"
-            traffic = json.loads(TRAFFIC_FILE.read_text()).get(key, {}).get("bytes_per_launch")
-        except (ValueError, AttributeError):
-            traffic = None
+    fp32_mfma = os.environ.get("FPX_ATTENTION_MFMA") == "f32"
+    traffic = recorded_traffic(f"{cfg.name}/fp32-mfma" if fp32_mfma else cfg.name)
     attend_tflops = flops["core"] / (stages["attend"] * 1e-3) / 1e12
-    split = cfg.dtype != "bf16" and os.environ.get("FPX_ATTENTION_MFMA") != "f32"
+    split = cfg.dtype != "bf16" and not fp32_mfma
     if cfg.dtype == "bf16":
         kernel_name = "attention_bf16_kernel (fpx_tri_attn_attend, BF16)"
     elif split:
@@ -612,21 +641,7 @@ def main() -> int:
         "avg_launch_ms": round(stages["attend"], 4),
     }
     if split:
-        # FP32-accurate products executed on the BF16 matrix cores: per 32 x 32
-        # (query x key) wave tile, 18 v_mfma_f32_32x32x16_bf16 (6 terms of
-        # S^T, 3 of O^T, two K-halves each) = 18 * 32768 flop, against
-        # 2 * 65536 algorithmic flop.
-        np_ = -(-n // 128) * 128
-        nkt = -(-n // 32)
-        executed = n * 4 * (np_ // 32) * nkt * 18 * 32768
-        executed_tflops = executed / (stages["attend"] * 1e-3) / 1e12
-        roofline.update({
-            "matrix_unit": "bf16 (exact 3-plane split of K and Q, 2-plane V and P)",
-            "executed_flop_per_launch": executed,
-            "executed_tflops": round(executed_tflops, 3),
-            "executed_peak": BF16_MFMA_PEAK_TFLOPS,
-            "executed_frac": round(executed_tflops / BF16_MFMA_PEAK_TFLOPS, 4),
-        })
+        roofline.update(split_executed(n, n, stages["attend"]))
     result = {
         "metric": METRIC,
         "value": round(value, 3),
