@@ -527,18 +527,16 @@ __global__ __launch_bounds__(kThreads, FPX_ATTN_WAVES_PER_SIMD) void attention_k
 
 }  // namespace
 
-namespace {
-bool block_on_fp32_mfma() {
+bool fp32_matrix_cores_selected() {
   static const bool fp32 = [] {
     const char* v = std::getenv("FPX_ATTENTION_MFMA");
     return v != nullptr && std::strcmp(v, "f32") == 0;
   }();
   return fp32;
 }
-}  // namespace
 
 hipError_t launch_attention(int layout, const AttnArgs& a, hipStream_t stream) {
-  if (layout != kAttnHeadLast && !block_on_fp32_mfma()) return launch_attention_split(layout, a, stream);
+  if (layout != kAttnHeadLast && !fp32_matrix_cores_selected()) return launch_attention_split(layout, a, stream);
   // Query tiles cover the padded extent; key tiles stop at the last real key
   // (tiles wholly past n hold only -inf mask bias and contribute nothing).
   const int nqt = (int)((layout != kAttnHeadLast ? a.np : round_up(a.n, kBq)) / kBq);

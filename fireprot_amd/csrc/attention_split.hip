@@ -32,6 +32,7 @@
 #include "attn_common.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
+#include "split.hpp"
 
 #include <cmath>
 #include <type_traits>
@@ -39,70 +40,12 @@
 namespace fpx {
 namespace {
 
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x8 __attribute__((ext_vector_type(8)));
-
 constexpr int kThreads = 256;
 constexpr int kRowB = kHeadDim + 8;  // bf16 per LDS row: 80 bytes, conflict-free b128 reads
 constexpr int kMaxKeys = kTileFlagWords * 32 * kBk;
 
 typedef __bf16 KPlane[kBk][kRowB];       // [key][channel]
 typedef __bf16 VPlane[kHeadDim][kRowB];  // [channel][key position], see v_position
-
-__device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-
-// One pair step of the splits below: the pair's bf16 roundings packed in one
-// word (v_cvt_pk_bf16_f32), and the residuals x - float(hi) with float(hi)
-// recovered from that word by a shift and a mask (the generic conversion
-// takes a third more instructions).
-__device__ __forceinline__ uint32_t split_pair(f32x2 x, f32x2& residual) {
-  const uint32_t hb = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, bf16x2));
-  const f32x2 back = {__builtin_bit_cast(float, hb << 16), __builtin_bit_cast(float, hb & 0xffff0000u)};
-  residual = x - back;
-  return hb;
-}
-
-__device__ __forceinline__ void split3(f32x4 x, bf16x4& hi, bf16x4& lo, bf16x4& rest) {
-  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-  f32x2 r1a, r1b, r2a, r2b;
-  const uint32_t ha = split_pair(f32x2{x.x, x.y}, r1a), hb = split_pair(f32x2{x.z, x.w}, r1b);
-  const uint32_t la = split_pair(r1a, r2a), lb = split_pair(r1b, r2b);
-  hi = __builtin_bit_cast(bf16x4, u32x2{ha, hb});
-  lo = __builtin_bit_cast(bf16x4, u32x2{la, lb});
-  rest = __builtin_bit_cast(bf16x4, u32x2{__builtin_bit_cast(uint32_t, __builtin_convertvector(r2a, bf16x2)),
-                                          __builtin_bit_cast(uint32_t, __builtin_convertvector(r2b, bf16x2))});
-}
-__device__ __forceinline__ void split3(f32x8 x, bf16x8& hi, bf16x8& lo, bf16x8& rest) {
-  hi = __builtin_convertvector(x, bf16x8);
-  const f32x8 r1 = x - __builtin_convertvector(hi, f32x8);
-  lo = __builtin_convertvector(r1, bf16x8);
-  rest = __builtin_convertvector(r1 - __builtin_convertvector(lo, f32x8), bf16x8);
-}
-__device__ __forceinline__ void split2(f32x4 x, bf16x4& hi, bf16x4& lo) {
-  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-  f32x2 ra, rb;
-  const uint32_t ha = split_pair(f32x2{x.x, x.y}, ra), hb = split_pair(f32x2{x.z, x.w}, rb);
-  hi = __builtin_bit_cast(bf16x4, u32x2{ha, hb});
-  lo = __builtin_bit_cast(bf16x4, u32x2{__builtin_bit_cast(uint32_t, __builtin_convertvector(ra, bf16x2)),
-                                        __builtin_bit_cast(uint32_t, __builtin_convertvector(rb, bf16x2))});
-}
-__device__ __forceinline__ void split2(f32x8 x, bf16x8& hi, bf16x8& lo) {
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  uint32_t h[4], l[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f32x2 r;
-    h[i] = split_pair(f32x2{x[2 * i], x[2 * i + 1]}, r);
-    l[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, bf16x2));
-  }
-  hi = __builtin_bit_cast(bf16x8, u32x4{h[0], h[1], h[2], h[3]});
-  lo = __builtin_bit_cast(bf16x8, u32x4{l[0], l[1], l[2], l[3]});
-}
 
 // V^T keys are stored in the order in which the S^T accumulator registers
 // hold them: within each 16-key block, keys 0-3, 8-11, 4-7, 12-15.  Position

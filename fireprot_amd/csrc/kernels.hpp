@@ -60,10 +60,14 @@ struct AttnArgs {
   int np;
 };
 
+// True when the environment sets FPX_ATTENTION_MFMA=f32 (read once per
+// process): the FP32 attention and projections then run on the FP32 matrix
+// cores (v_mfma_f32_32x32x2_f32) instead of their exact bf16 splits.
+bool fp32_matrix_cores_selected();
+
 // kAttnBlock and kAttnStrided run attention_split_kernel (FP32-accurate
-// products on the BF16 matrix cores) unless the environment sets
-// FPX_ATTENTION_MFMA=f32, which selects attention_kernel on the FP32 matrix
-// cores (read once per process); kAttnHeadLast always runs attention_kernel.
+// products on the BF16 matrix cores) unless fp32_matrix_cores_selected(),
+// which selects attention_kernel; kAttnHeadLast always runs attention_kernel.
 hipError_t launch_attention(int layout, const AttnArgs& args, hipStream_t stream);
 hipError_t launch_attention_split(int layout, const AttnArgs& args, hipStream_t stream);
 
@@ -106,6 +110,8 @@ struct ProjArgs {
   int accumulate;  // kProjOut: out = out + (x W_o^T + b_o), the residual update
 };
 
+// projection_split_kernel (exact three-plane bf16 splits on the BF16 matrix
+// cores) unless fp32_matrix_cores_selected(), which selects projection_kernel.
 hipError_t launch_projection(int mode, const ProjArgs& args, hipStream_t stream);
 
 // -------------------------------------------------------------- elementwise

@@ -16,6 +16,7 @@
 // x + i*xs_i + j*xs_j makes the ending-node read of z^T free of copies.
 #include "common.hpp"
 #include "kernels.hpp"
+#include "split.hpp"
 
 namespace fpx {
 namespace {
@@ -40,6 +41,75 @@ struct ProjTraits<kProjOut> {
   static constexpr int kWaves = 4;   // 128 output channels
   static constexpr bool kLn = false;
 };
+
+// Stores one wave's 32 x 32 result tile.  Lane holds rows 4*half +
+// 8*(r/4) + r%4 of the tile, column col_w of output group `group` (0 q, 1 k,
+// 2 v, 3 g; kProjOut: always 0), head or column block hw.  Row offsets are
+// compile-time constants once the lane's base includes its 4*half rows.
+template <int MODE>
+__device__ __forceinline__ void store_tile(const ProjArgs& a, int tile, int tiles_j, int group,
+                                           int hw, int col_w, float col_bias, int half, int l32,
+                                           const f32x16& acc) {
+  const int i = tile / tiles_j;
+  const int j0 = (tile % tiles_j) * kRows + 4 * half;
+  if (MODE == kProjBlock) {
+    const int64_t bh = (int64_t)i * kHeads + hw;
+    if (group == 0 || group == 1) {
+      float* dst = (group == 0 ? a.qh : a.kh) + (bh * a.np + j0) * kHeadDim + l32;
+      if (group == 0) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dst[(8 * (r >> 2) + (r & 3)) * kHeadDim] = acc[r] * a.q_scale;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dst[(8 * (r >> 2) + (r & 3)) * kHeadDim] = acc[r];
+      }
+    } else if (group == 2) {
+      float* dst = a.vt + (bh * kHeadDim + l32) * a.np + j0;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        *(f32x4*)(dst + 8 * rr) =
+            f32x4{acc[4 * rr + 0], acc[4 * rr + 1], acc[4 * rr + 2], acc[4 * rr + 3]};
+    } else {
+      // gate rows are padded to np: the tile is always stored whole
+      float* dst = a.gs + ((int64_t)i * a.np + j0) * kHidden + col_w;
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        dst[(8 * (r >> 2) + (r & 3)) * kHidden] = sigmoidf_(acc[r] + col_bias);
+    }
+  } else {
+    // Rows past rows_j exist only in the last tile of an outer row; the
+    // branch is uniform, so full tiles store with no per-element tests.
+    const bool full = (tile % tiles_j + 1) * kRows <= a.rows_j;
+    float* dst;
+    int64_t stride;
+    float scale = 1.0f, add = 0.0f;
+    if (MODE == kProjQkv) {
+      const int64_t rows = (int64_t)a.rows_i * a.rows_j;
+      dst = a.out + ((int64_t)group * rows + (int64_t)i * a.rows_j + j0) * kHidden + 32 * hw + l32;
+      stride = kHidden;
+      if (group == 0) scale = a.q_scale;
+    } else {
+      dst = a.out + (int64_t)i * a.os_i + (int64_t)j0 * a.os_j + col_w;
+      stride = a.os_j;
+      add = col_bias;
+    }
+    // The residual update adds the rounded update to the old value, as
+    // the native z += dz does.
+    const bool residual = MODE == kProjOut && a.accumulate != 0;
+    auto put = [&](float* d, float v) { *d = residual ? *d + v : v; };
+    if (full) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        put(dst + (int64_t)(8 * (r >> 2) + (r & 3)) * stride, acc[r] * scale + add);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int dj = 8 * (r >> 2) + (r & 3);
+        if (j0 + dj < a.rows_j) put(dst + (int64_t)dj * stride, acc[r] * scale + add);
+      }
+    }
+  }
+}
 
 template <int MODE>
 __global__ __launch_bounds__(ProjTraits<MODE>::kWaves * 64) void projection_kernel(ProjArgs a,
@@ -177,71 +247,8 @@ __global__ __launch_bounds__(ProjTraits<MODE>::kWaves * 64) void projection_kern
     return acc;
   };
 
-  // Lane holds rows 4*half + 8*(r/4) + r%4 of the tile, column 32*w + l32.
-  // Row offsets are compile-time constants once the lane's base includes
-  // its 4*half rows.
   auto epilogue = [&](int tile, const f32x16& acc) {
-    const int i = tile / tiles_j;
-    const int j0 = (tile % tiles_j) * kRows + 4 * half;
-    const int group = w >> 2;   // 0 q, 1 k, 2 v, 3 g (kProjOut: always 0)
-    const int hw = w & 3;       // head (q/k/v/g) or column block
-    if (MODE == kProjBlock) {
-      const int64_t bh = (int64_t)i * kHeads + hw;
-      if (group == 0 || group == 1) {
-        float* dst = (group == 0 ? a.qh : a.kh) + (bh * a.np + j0) * kHeadDim + l32;
-        if (group == 0) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) dst[(8 * (r >> 2) + (r & 3)) * kHeadDim] = acc[r] * a.q_scale;
-        } else {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) dst[(8 * (r >> 2) + (r & 3)) * kHeadDim] = acc[r];
-        }
-      } else if (group == 2) {
-        float* dst = a.vt + (bh * kHeadDim + l32) * a.np + j0;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          *(f32x4*)(dst + 8 * rr) =
-              f32x4{acc[4 * rr + 0], acc[4 * rr + 1], acc[4 * rr + 2], acc[4 * rr + 3]};
-      } else {
-        // gate rows are padded to np: the tile is always stored whole
-        float* dst = a.gs + ((int64_t)i * a.np + j0) * kHidden + col_w;
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          dst[(8 * (r >> 2) + (r & 3)) * kHidden] = sigmoidf_(acc[r] + col_bias);
-      }
-    } else {
-      // Rows past rows_j exist only in the last tile of an outer row; the
-      // branch is uniform, so full tiles store with no per-element tests.
-      const bool full = (tile % tiles_j + 1) * kRows <= a.rows_j;
-      float* dst;
-      int64_t stride;
-      float scale = 1.0f, add = 0.0f;
-      if (MODE == kProjQkv) {
-        const int64_t rows = (int64_t)a.rows_i * a.rows_j;
-        dst = a.out + ((int64_t)group * rows + (int64_t)i * a.rows_j + j0) * kHidden + 32 * hw + l32;
-        stride = kHidden;
-        if (group == 0) scale = a.q_scale;
-      } else {
-        dst = a.out + (int64_t)i * a.os_i + (int64_t)j0 * a.os_j + col_w;
-        stride = a.os_j;
-        add = col_bias;
-      }
-      // The residual update adds the rounded update to the old value, as
-      // the native z += dz does.
-      const bool residual = MODE == kProjOut && a.accumulate != 0;
-      auto put = [&](float* d, float v) { *d = residual ? *d + v : v; };
-      if (full) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          put(dst + (int64_t)(8 * (r >> 2) + (r & 3)) * stride, acc[r] * scale + add);
-      } else {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int dj = 8 * (r >> 2) + (r & 3);
-          if (j0 + dj < a.rows_j) put(dst + (int64_t)dj * stride, acc[r] * scale + add);
-        }
-      }
-    }
+    store_tile<MODE>(a, tile, tiles_j, w >> 2, w & 3, col_w, col_bias, half, l32, acc);
   };
 
   // Persistent loop: the tile after this one is fetched two tiles ahead and
@@ -268,6 +275,233 @@ __global__ __launch_bounds__(ProjTraits<MODE>::kWaves * 64) void projection_kern
   }
 }
 
+// ------------------------------------------------ FP32-accurate, BF16 cores
+//
+// The same projections with every FP32 operand split exactly into three
+// bfloat16 planes (split.hpp) and the six terms down to 2^-16 relative run on
+// v_mfma_f32_32x32x16_bf16: 48 of them per 32 x 32 tile over the 128 input
+// channels, against 64 v_mfma_f32_32x32x2_f32 of 8x less work each.  A
+// wave's three weight planes take 96 VGPRs, so a work-group covers only a
+// slice of the output columns: the block's 512 q/k/v/g columns (and the
+// 384 of kProjQkv) are cut into two slices of 8 (6) waves, one work-group
+// per CU, and the two work-groups of a slice pair run on the same XCD over
+// the same row tiles, so the second read of each row tile comes from L2.
+// Each slice normalises its rows itself (kProjBlock); slice s projects
+// triangle-bias heads 2s and 2s + 1.  Row tiles are split into the three
+// planes once, on their way into LDS.
+template <int MODE>
+struct SplitTraits;
+template <>
+struct SplitTraits<kProjBlock> {
+  static constexpr int kWaves = 8;  // 256 of q, k, v, g's 512 columns
+  static constexpr int kSlices = 2;
+  static constexpr int kMinBlocks = 1;
+};
+template <>
+struct SplitTraits<kProjQkv> {
+  static constexpr int kWaves = 6;  // 192 of q, k, v's 384 columns
+  static constexpr int kSlices = 2;
+  static constexpr int kMinBlocks = 2;
+};
+template <>
+struct SplitTraits<kProjOut> {
+  static constexpr int kWaves = 4;  // the 128 output channels
+  static constexpr int kSlices = 1;
+  static constexpr int kMinBlocks = 3;
+};
+
+constexpr int kPlaneRow = kChannels + 8;  // bf16 per LDS row: 272 bytes, conflict-free b128 reads
+typedef __bf16 XPlane[kRows][kPlaneRow];
+
+template <int MODE>
+__global__ __launch_bounds__(SplitTraits<MODE>::kWaves * 64, SplitTraits<MODE>::kMinBlocks) void
+projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
+  using T = SplitTraits<MODE>;
+  constexpr int NW = T::kWaves;
+  constexpr int kThreads = NW * 64;
+  constexpr bool kLn = MODE == kProjBlock;
+  constexpr int kRowsPerWave = kRows / NW;                  // kProjBlock: 4
+  constexpr int kVecs = kRows * kChannels / 4;              // float4 per tile
+  constexpr int kLoads = (kVecs + kThreads - 1) / kThreads; // kProjQkv, kProjOut
+  // Two row tiles of three planes: the MFMAs read one while the next is
+  // normalised and split into the other, so a tile needs one barrier.
+  __shared__ __attribute__((aligned(16))) XPlane xs[2][3];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+  // Consecutive logical indices share an XCD: the slices of a stream are
+  // neighbours (the grid is a multiple of 16 when the tiles allow it).
+  const uint32_t logical = xcd_remap(blockIdx.x, gridDim.x);
+  const int slice = (int)(logical % T::kSlices);
+  const int first = (int)(logical / T::kSlices);
+  const int cb = __builtin_amdgcn_readfirstlane(slice * NW + w);  // 32-column block
+  const int group = cb >> 2;
+  const int hw = cb & 3;
+
+  // Weight planes: B[k][col] for col = 32*hw + l32 of group `group`, lane
+  // holding channels 16s + 8*half + e of k step s.
+  bf16x8 wh[8], wl[8], wr[8];
+  {
+    const float* src = a.w[group] + (int64_t)(32 * hw + l32) * kChannels + 8 * half;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const f32x4 u = *(const f32x4*)(src + 16 * t);
+      const f32x4 v = *(const f32x4*)(src + 16 * t + 4);
+      split3(f32x8{u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w}, wh[t], wl[t], wr[t]);
+    }
+  }
+  const int col_w = MODE == kProjOut ? 32 * w + l32 : 32 * hw + l32;
+  const float col_bias = (MODE != kProjQkv && a.b_g != nullptr) ? a.b_g[col_w] : 0.f;
+
+  // LN constants (channels 2*lane, 2*lane+1) and this slice's two
+  // triangle-bias heads.
+  f32x2 lnw = {1.f, 1.f}, lnb = {0.f, 0.f};
+  f32x2 wb[2] = {};
+  if constexpr (kLn) {
+    if (a.ln_w) lnw = *(const f32x2*)(a.ln_w + 2 * lane);
+    if (a.ln_b) lnb = *(const f32x2*)(a.ln_b + 2 * lane);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+      wb[hh] = *(const f32x2*)(a.w_bias + (2 * slice + hh) * kChannels + 2 * lane);
+  }
+
+  f32x2 stage_ln[kLn ? kRowsPerWave : 1];
+  f32x4 stage_vec[kLn ? 1 : kLoads];
+
+  auto fetch = [&](int tile) {
+    const int i = tile / tiles_j;
+    const int j0 = (tile % tiles_j) * kRows;
+    if constexpr (kLn) {
+#pragma unroll
+      for (int rr = 0; rr < kRowsPerWave; ++rr) {
+        const int j = j0 + w * kRowsPerWave + rr;
+        stage_ln[rr] = j < a.rows_j
+                           ? *(const f32x2*)(a.x + (int64_t)i * a.xs_i + (int64_t)j * a.xs_j + 2 * lane)
+                           : f32x2{0.f, 0.f};
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < kLoads; ++t) {
+        const int idx = tid + t * kThreads;
+        const int j = j0 + (idx >> 5);
+        stage_vec[t] = (idx < kVecs && j < a.rows_j)
+                           ? *(const f32x4*)(a.x + (int64_t)i * a.xs_i + (int64_t)j * a.xs_j +
+                                             (idx & 31) * 4)
+                           : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  };
+
+  auto stage_rows = [&](int tile, int buf) {
+    const int i = tile / tiles_j;
+    const int j0 = (tile % tiles_j) * kRows;
+    if constexpr (kLn) {
+#pragma unroll
+      for (int rr = 0; rr < kRowsPerWave; ++rr) {
+        const int row = w * kRowsPerWave + rr;
+        const int j = j0 + row;
+        const bool valid = j < a.rows_j;
+        float d0, d1, rstd;
+        ln_stats_c128(stage_ln[rr].x, stage_ln[rr].y, a.eps, d0, d1, rstd);
+        float y0 = d0 * rstd * lnw.x + lnb.x;
+        float y1 = d1 * rstd * lnw.y + lnb.y;
+        if (!valid) y0 = y1 = 0.f;
+        f32x2 r1, r2;
+        const uint32_t hi = split_pair(f32x2{y0, y1}, r1);
+        const uint32_t lo = split_pair(r1, r2);
+        const uint32_t rest = __builtin_bit_cast(uint32_t, __builtin_convertvector(r2, bf16x2));
+        *(uint32_t*)&xs[buf][0][row][2 * lane] = hi;
+        *(uint32_t*)&xs[buf][1][row][2 * lane] = lo;
+        *(uint32_t*)&xs[buf][2][row][2 * lane] = rest;
+        if constexpr (MODE == kProjBlock) {
+          const float p0 = wave_sum(y0 * wb[0].x + y1 * wb[0].y);
+          const float p1 = wave_sum(y0 * wb[1].x + y1 * wb[1].y);
+          if (lane < 2) {
+            const float v = lane == 0 ? p0 : p1;
+            const int64_t at = bias_frag_index(2 * slice + lane, i, j, a.np);
+            a.tri_bias[at] = valid ? v : 0.f;
+            a.tri_bias_l2[at] = valid ? v * kLog2e : 0.f;
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < kLoads; ++t) {
+        const int idx = tid + t * kThreads;
+        if (idx < kVecs) {
+          bf16x4 hi, lo, rest;
+          split3(stage_vec[t], hi, lo, rest);
+          const int row = idx >> 5;
+          const int c4 = (idx & 31) * 4;
+          *(bf16x4*)&xs[buf][0][row][c4] = hi;
+          *(bf16x4*)&xs[buf][1][row][c4] = lo;
+          *(bf16x4*)&xs[buf][2][row][c4] = rest;
+        }
+      }
+    }
+  };
+
+  // 32 rows x 32 columns per wave, A[row][k] = the row planes, two
+  // accumulation chains so consecutive MFMAs do not wait on each other.
+  auto mfma_tile = [&](int buf) -> f32x16 {
+    f32x16 c0 = {}, c1 = {};
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int k = 16 * t + 8 * half;
+      const bf16x8 xh = *(const bf16x8*)&xs[buf][0][l32][k];
+      const bf16x8 xl = *(const bf16x8*)&xs[buf][1][l32][k];
+      const bf16x8 xr = *(const bf16x8*)&xs[buf][2][l32][k];
+      c0 = mfma_bf16(xh, wh[t], c0);
+      c1 = mfma_bf16(xh, wl[t], c1);
+      c0 = mfma_bf16(xl, wh[t], c0);
+      c1 = mfma_bf16(xl, wl[t], c1);
+      c0 = mfma_bf16(xr, wh[t], c0);
+      c1 = mfma_bf16(xh, wr[t], c1);
+    }
+    return c0 + c1;
+  };
+
+  __builtin_amdgcn_s_waitcnt(0);
+  int tile = first;  // first < streams <= ntiles: every work-group has a tile
+  fetch(tile);
+  stage_rows(tile, 0);
+  int next = tile + streams;
+  if (next < ntiles) fetch(next);
+  __syncthreads();
+  for (int buf = 0; tile < ntiles; buf ^= 1) {
+    const f32x16 acc = mfma_tile(buf);
+    if (next < ntiles) {
+      stage_rows(next, buf ^ 1);
+      if (next + streams < ntiles) fetch(next + streams);
+    }
+    store_tile<MODE>(a, tile, tiles_j, group, hw, col_w, col_bias, half, l32, acc);
+    __syncthreads();
+    tile = next;
+    next += streams;
+  }
+}
+
+template <int MODE>
+hipError_t launch_split(const ProjArgs& a, hipStream_t stream) {
+  using T = SplitTraits<MODE>;
+  const int tiles_j = (int)(round_up(a.span_j, kRows) / kRows);
+  const int64_t ntiles = (int64_t)a.rows_i * tiles_j;
+  if (ntiles == 0) return hipSuccess;
+  if (ntiles > 0x7fffffffll) return hipErrorInvalidValue;
+  // Streams of row tiles: one work-group per slice each, as many as fit
+  // (rounded down to a multiple of 8 so the grid spreads evenly over the
+  // XCDs and slice pairs never straddle two of them).
+  int64_t cap = (int64_t)device_cu_count() * T::kMinBlocks / T::kSlices;
+  if (cap >= 8) cap -= cap % 8;
+  const int streams = (int)(ntiles < cap ? ntiles : cap);
+  hipLaunchKernelGGL(projection_split_kernel<MODE>, dim3(streams * T::kSlices), dim3(T::kWaves * 64),
+                     0, stream, a, tiles_j, (int)ntiles, streams);
+  return hipGetLastError();
+}
+
 template <int MODE>
 hipError_t launch_mode(const ProjArgs& a, hipStream_t stream, int wgs_per_cu) {
   const int tiles_j = (int)(round_up(a.span_j, kRows) / kRows);
@@ -284,6 +518,18 @@ hipError_t launch_mode(const ProjArgs& a, hipStream_t stream, int wgs_per_cu) {
 }  // namespace
 
 hipError_t launch_projection(int mode, const ProjArgs& a, hipStream_t stream) {
+  if (!fp32_matrix_cores_selected()) {
+    switch (mode) {
+      case kProjBlock:
+        return launch_split<kProjBlock>(a, stream);
+      case kProjQkv:
+        return launch_split<kProjQkv>(a, stream);
+      case kProjOut:
+        return launch_split<kProjOut>(a, stream);
+      default:
+        return hipErrorInvalidValue;
+    }
+  }
   switch (mode) {
     case kProjBlock:
       return launch_mode<kProjBlock>(a, stream, 1);
