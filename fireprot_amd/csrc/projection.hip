@@ -18,6 +18,8 @@
 #include "kernels.hpp"
 #include "split.hpp"
 
+#include <type_traits>
+
 namespace fpx {
 namespace {
 
@@ -313,6 +315,21 @@ struct SplitTraits<kProjOut> {
 constexpr int kPlaneRow = kChannels + 8;  // bf16 per LDS row: 272 bytes, conflict-free b128 reads
 typedef __bf16 XPlane[kRows][kPlaneRow];
 
+// Sum over each 16-lane row of the wave (DPP quad_perm [1,0,3,2] and
+// [2,3,0,1], row_half_mirror, row_mirror), returned in all 16 lanes.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  v += dpp<0x140>(v);
+  return v;
+}
+
+// Lane 0 of each 16-lane row, broadcast to the row (DPP row_newbcast:0).
+__device__ __forceinline__ float row16_first(float v) {
+  return dpp<0x150>(v);
+}
+
 template <int MODE>
 __global__ __launch_bounds__(SplitTraits<MODE>::kWaves * 64, SplitTraits<MODE>::kMinBlocks) void
 projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
@@ -320,12 +337,15 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
   constexpr int NW = T::kWaves;
   constexpr int kThreads = NW * 64;
   constexpr bool kLn = MODE == kProjBlock;
-  constexpr int kRowsPerWave = kRows / NW;                  // kProjBlock: 4
+  static_assert(!kLn || NW * 4 == kRows, "LN mode: 4 rows per wave, 16 lanes per row");
   constexpr int kVecs = kRows * kChannels / 4;              // float4 per tile
   constexpr int kLoads = (kVecs + kThreads - 1) / kThreads; // kProjQkv, kProjOut
   // Two row tiles of three planes: the MFMAs read one while the next is
   // normalised and split into the other, so a tile needs one barrier.
   __shared__ __attribute__((aligned(16))) XPlane xs[2][3];
+  // LN mode: raw rows of the next tile.  Each wave reads and rewrites only
+  // its own rows, so the buffer needs no barrier of its own.
+  __shared__ __attribute__((aligned(16))) float raw[kLn ? kRows : 1][kChannels + 4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -342,7 +362,7 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
   const int hw = cb & 3;
 
   // Weight planes: B[k][col] for col = 32*hw + l32 of group `group`, lane
-  // holding channels 16s + 8*half + e of k step s.
+  // holding channels 16t + 8*half + e of k step t.
   bf16x8 wh[8], wl[8], wr[8];
   {
     const float* src = a.w[group] + (int64_t)(32 * hw + l32) * kChannels + 8 * half;
@@ -356,131 +376,231 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
   const int col_w = MODE == kProjOut ? 32 * w + l32 : 32 * hw + l32;
   const float col_bias = (MODE != kProjQkv && a.b_g != nullptr) ? a.b_g[col_w] : 0.f;
 
-  // LN constants (channels 2*lane, 2*lane+1) and this slice's two
-  // triangle-bias heads.
-  f32x2 lnw = {1.f, 1.f}, lnb = {0.f, 0.f};
-  f32x2 wb[2] = {};
+  // LN mode: 16 lanes per row, lane c16 = lane % 16 holding channels
+  // 8*c16 .. 8*c16 + 7 of row 4*w + lane/16; the LN affine and this slice's
+  // two triangle-bias heads for those channels.
+  const int c16 = lane & 15;
+  const int lrow = 4 * w + (lane >> 4);
+  f32x8 lnw, lnb, wb0, wb1;
   if constexpr (kLn) {
-    if (a.ln_w) lnw = *(const f32x2*)(a.ln_w + 2 * lane);
-    if (a.ln_b) lnb = *(const f32x2*)(a.ln_b + 2 * lane);
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh)
-      wb[hh] = *(const f32x2*)(a.w_bias + (2 * slice + hh) * kChannels + 2 * lane);
+    for (int e = 0; e < 8; ++e) {
+      lnw[e] = a.ln_w ? a.ln_w[8 * c16 + e] : 1.f;
+      lnb[e] = a.ln_b ? a.ln_b[8 * c16 + e] : 0.f;
+      wb0[e] = a.w_bias[(2 * slice) * kChannels + 8 * c16 + e];
+      wb1[e] = a.w_bias[(2 * slice + 1) * kChannels + 8 * c16 + e];
+    }
   }
 
-  f32x2 stage_ln[kLn ? kRowsPerWave : 1];
+  // Row loads in flight (LN mode: the tile after next).
+  f32x8 stage_ln;
   f32x4 stage_vec[kLn ? 1 : kLoads];
 
+  // Outer row i and first pair row j0 of a tile.
+  auto origin = [&](int tile, int& i, int& j0) {
+    i = tile / tiles_j;
+    j0 = (tile - i * tiles_j) * kRows;
+  };
+
+  // LN mode: loads with no branches (tile clamped to the last one, row to
+  // the last valid row; stage_split zeroes rows past rows_j), so every
+  // staged slot holds finished loads on every path.
+  auto fetch_ln = [&](f32x8& slot, int tile) {
+    int i, j0;
+    origin(tile < ntiles ? tile : ntiles - 1, i, j0);
+    const int j = min(j0 + lrow, a.rows_j - 1);
+    const float* src = a.x + (int64_t)i * a.xs_i + (int64_t)j * a.xs_j + 8 * c16;
+    const f32x4 u = *(const f32x4*)src;
+    const f32x4 v = *(const f32x4*)(src + 4);
+    slot = f32x8{u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+  };
+
   auto fetch = [&](int tile) {
-    const int i = tile / tiles_j;
-    const int j0 = (tile % tiles_j) * kRows;
-    if constexpr (kLn) {
+    int i, j0;
+    origin(tile, i, j0);
 #pragma unroll
-      for (int rr = 0; rr < kRowsPerWave; ++rr) {
-        const int j = j0 + w * kRowsPerWave + rr;
-        stage_ln[rr] = j < a.rows_j
-                           ? *(const f32x2*)(a.x + (int64_t)i * a.xs_i + (int64_t)j * a.xs_j + 2 * lane)
-                           : f32x2{0.f, 0.f};
-      }
-    } else {
+    for (int t = 0; t < kLoads; ++t) {
+      const int idx = tid + t * kThreads;
+      const int j = j0 + (idx >> 5);
+      stage_vec[t] = (idx < kVecs && j < a.rows_j)
+                         ? *(const f32x4*)(a.x + (int64_t)i * a.xs_i + (int64_t)j * a.xs_j +
+                                           (idx & 31) * 4)
+                         : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+
+  // LayerNorm statistics of the staged rows (two-pass on values shifted by
+  // the row's first channel, as ln_stats_c128), returning the centred values
+  // and 1/sqrt(biased var + eps).
+  auto ln_stats = [&](const f32x8& raw, f32x8& d, float& rstd) {
+    const float pivot = row16_first(raw[0]);
+    const f32x8 sh = raw - pivot;
+    float s = 0.f;
 #pragma unroll
-      for (int t = 0; t < kLoads; ++t) {
-        const int idx = tid + t * kThreads;
-        const int j = j0 + (idx >> 5);
-        stage_vec[t] = (idx < kVecs && j < a.rows_j)
-                           ? *(const f32x4*)(a.x + (int64_t)i * a.xs_i + (int64_t)j * a.xs_j +
-                                             (idx & 31) * 4)
-                           : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int e = 0; e < 8; ++e) s += sh[e];
+    const float mean = row16_sum(s) * (1.0f / kChannels);
+    d = sh - mean;
+    float q = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q += d[e] * d[e];
+    rstd = __builtin_amdgcn_rsqf(row16_sum(q) * (1.0f / kChannels) + a.eps);
+  };
+
+  // Normalises, splits and writes the staged rows into planes `buf`;
+  // returns this lane's triangle-bias value (head 2*slice + c16 for c16 < 2,
+  // 0 for rows past rows_j), stored later by store_bias.
+  auto stage_split = [&](int buf, const f32x8& d, float rstd, int j0) -> float {
+    const bool valid = j0 + lrow < a.rows_j;
+    f32x8 y = d * rstd * lnw + lnb;
+    if (!valid) y = f32x8{};
+    bf16x8 hi, lo, rest;
+    split3(y, hi, lo, rest);
+    *(bf16x8*)&xs[buf][0][lrow][8 * c16] = hi;
+    *(bf16x8*)&xs[buf][1][lrow][8 * c16] = lo;
+    *(bf16x8*)&xs[buf][2][lrow][8 * c16] = rest;
+    float p0 = 0.f, p1 = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      p0 += y[e] * wb0[e];
+      p1 += y[e] * wb1[e];
+    }
+    p0 = row16_sum(p0);
+    p1 = row16_sum(p1);
+    return c16 == 0 ? p0 : p1;
+  };
+
+  auto store_bias = [&](float v, int i, int j0) {
+    if (c16 < 2) {
+      const int j = j0 + lrow;
+      const int64_t at = bias_frag_index(2 * slice + c16, i, j, a.np);
+      a.tri_bias[at] = v;
+      a.tri_bias_l2[at] = v * kLog2e;
+    }
+  };
+
+  auto stage_vecs = [&](int buf) {
+#pragma unroll
+    for (int t = 0; t < kLoads; ++t) {
+      const int idx = tid + t * kThreads;
+      if (idx < kVecs) {
+        bf16x4 hi, lo, rest;
+        split3(stage_vec[t], hi, lo, rest);
+        const int row = idx >> 5;
+        const int c4 = (idx & 31) * 4;
+        *(bf16x4*)&xs[buf][0][row][c4] = hi;
+        *(bf16x4*)&xs[buf][1][row][c4] = lo;
+        *(bf16x4*)&xs[buf][2][row][c4] = rest;
       }
     }
   };
 
-  auto stage_rows = [&](int tile, int buf) {
-    const int i = tile / tiles_j;
-    const int j0 = (tile % tiles_j) * kRows;
-    if constexpr (kLn) {
-#pragma unroll
-      for (int rr = 0; rr < kRowsPerWave; ++rr) {
-        const int row = w * kRowsPerWave + rr;
-        const int j = j0 + row;
-        const bool valid = j < a.rows_j;
-        float d0, d1, rstd;
-        ln_stats_c128(stage_ln[rr].x, stage_ln[rr].y, a.eps, d0, d1, rstd);
-        float y0 = d0 * rstd * lnw.x + lnb.x;
-        float y1 = d1 * rstd * lnw.y + lnb.y;
-        if (!valid) y0 = y1 = 0.f;
-        f32x2 r1, r2;
-        const uint32_t hi = split_pair(f32x2{y0, y1}, r1);
-        const uint32_t lo = split_pair(r1, r2);
-        const uint32_t rest = __builtin_bit_cast(uint32_t, __builtin_convertvector(r2, bf16x2));
-        *(uint32_t*)&xs[buf][0][row][2 * lane] = hi;
-        *(uint32_t*)&xs[buf][1][row][2 * lane] = lo;
-        *(uint32_t*)&xs[buf][2][row][2 * lane] = rest;
-        if constexpr (MODE == kProjBlock) {
-          const float p0 = wave_sum(y0 * wb[0].x + y1 * wb[0].y);
-          const float p1 = wave_sum(y0 * wb[1].x + y1 * wb[1].y);
-          if (lane < 2) {
-            const float v = lane == 0 ? p0 : p1;
-            const int64_t at = bias_frag_index(2 * slice + lane, i, j, a.np);
-            a.tri_bias[at] = valid ? v : 0.f;
-            a.tri_bias_l2[at] = valid ? v * kLog2e : 0.f;
-          }
-        }
-      }
-    } else {
-#pragma unroll
-      for (int t = 0; t < kLoads; ++t) {
-        const int idx = tid + t * kThreads;
-        if (idx < kVecs) {
-          bf16x4 hi, lo, rest;
-          split3(stage_vec[t], hi, lo, rest);
-          const int row = idx >> 5;
-          const int c4 = (idx & 31) * 4;
-          *(bf16x4*)&xs[buf][0][row][c4] = hi;
-          *(bf16x4*)&xs[buf][1][row][c4] = lo;
-          *(bf16x4*)&xs[buf][2][row][c4] = rest;
-        }
-      }
-    }
-  };
-
-  // 32 rows x 32 columns per wave, A[row][k] = the row planes, two
+  // One 16-deep k step of the 32 x 32 tile, A[row][k] = the row planes; two
   // accumulation chains so consecutive MFMAs do not wait on each other.
-  auto mfma_tile = [&](int buf) -> f32x16 {
-    f32x16 c0 = {}, c1 = {};
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const int k = 16 * t + 8 * half;
-      const bf16x8 xh = *(const bf16x8*)&xs[buf][0][l32][k];
-      const bf16x8 xl = *(const bf16x8*)&xs[buf][1][l32][k];
-      const bf16x8 xr = *(const bf16x8*)&xs[buf][2][l32][k];
-      c0 = mfma_bf16(xh, wh[t], c0);
-      c1 = mfma_bf16(xh, wl[t], c1);
-      c0 = mfma_bf16(xl, wh[t], c0);
-      c1 = mfma_bf16(xl, wl[t], c1);
-      c0 = mfma_bf16(xr, wh[t], c0);
-      c1 = mfma_bf16(xh, wr[t], c1);
-    }
-    return c0 + c1;
+  auto mfma_step = [&](int buf, int t, f32x16& c0, f32x16& c1) {
+    const int k = 16 * t + 8 * half;
+    const bf16x8 xh = *(const bf16x8*)&xs[buf][0][l32][k];
+    const bf16x8 xl = *(const bf16x8*)&xs[buf][1][l32][k];
+    const bf16x8 xr = *(const bf16x8*)&xs[buf][2][l32][k];
+    c0 = mfma_bf16(xh, wh[t], c0);
+    c1 = mfma_bf16(xh, wl[t], c1);
+    c0 = mfma_bf16(xl, wh[t], c0);
+    c1 = mfma_bf16(xl, wl[t], c1);
+    c0 = mfma_bf16(xr, wh[t], c0);
+    c1 = mfma_bf16(xh, wr[t], c1);
   };
 
   __builtin_amdgcn_s_waitcnt(0);
   int tile = first;  // first < streams <= ntiles: every work-group has a tile
-  fetch(tile);
-  stage_rows(tile, 0);
   int next = tile + streams;
-  if (next < ntiles) fetch(next);
-  __syncthreads();
-  for (int buf = 0; tile < ntiles; buf ^= 1) {
-    const f32x16 acc = mfma_tile(buf);
-    if (next < ntiles) {
-      stage_rows(next, buf ^ 1);
-      if (next + streams < ntiles) fetch(next + streams);
+  if constexpr (kLn) {
+    // Iteration k computes tile T_k = first + k*streams from planes k&1 and
+    // normalises T_{k+1} from the raw LDS rows into the other planes.  The
+    // two waves sharing a SIMD run the iteration's halves in opposite
+    // orders, so one issues its k steps while the other normalises and
+    // stores: "lead" waves (0-3) run the k steps first; "trail" waves (4-7)
+    // normalise first, run their k steps last and store the result in the
+    // next iteration.  Per wave, the global accesses of an iteration are
+    // issued together, in this order: the registers holding T_{k+2}'s rows
+    // (loaded one iteration earlier) are copied to the raw rows, T_{k+3}'s
+    // rows are loaded, then the bias and results are stored.  The copy waits
+    // for all of the wave's earlier global accesses (loads and stores share
+    // one counter), which were issued an iteration ago.
+    const bool lead = w < NW / 2;
+    int i0, j00;
+    origin(tile, i0, j00);
+    fetch_ln(stage_ln, tile);
+    {
+      f32x8 d;
+      float rstd;
+      ln_stats(stage_ln, d, rstd);
+      store_bias(stage_split(0, d, rstd, j00), i0, j00);
     }
-    store_tile<MODE>(a, tile, tiles_j, group, hw, col_w, col_bias, half, l32, acc);
+    fetch_ln(stage_ln, next);
+    *(f32x8*)&raw[lrow][8 * c16] = stage_ln;
+    fetch_ln(stage_ln, next + streams);
     __syncthreads();
-    tile = next;
-    next += streams;
+
+    auto k_steps = [&](int buf) -> f32x16 {
+      f32x16 c0 = {}, c1 = {};
+#pragma unroll
+      for (int t = 0; t < 8; ++t) mfma_step(buf, t, c0, c1);
+      return c0 + c1;
+    };
+    // Normalises T_{k+1} (when it exists) into planes buf ^ 1, then issues
+    // the wave's global accesses; `result`/`result_tile` are stored last.
+    auto other_half = [&](int buf, const f32x16& result, int result_tile) {
+      const bool more = next < ntiles;
+      int ni, nj0;
+      origin(more ? next : tile, ni, nj0);
+      float bias = 0.f;
+      if (more) {
+        f32x8 d;
+        float rstd;
+        ln_stats(*(const f32x8*)&raw[lrow][8 * c16], d, rstd);
+        bias = stage_split(buf ^ 1, d, rstd, nj0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      *(f32x8*)&raw[lrow][8 * c16] = stage_ln;
+      fetch_ln(stage_ln, next + 2 * streams);
+      if (more) store_bias(bias, ni, nj0);
+      if (result_tile >= 0)
+        store_tile<MODE>(a, result_tile, tiles_j, group, hw, col_w, col_bias, half, l32, result);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // Only the k steps sit in wave-dependent branches, so the row staging
+    // keeps one register assignment on every path.  `res` is this tile's
+    // result on lead waves and the previous tile's on trail waves.
+    f32x16 res = {};
+    for (int buf = 0; tile < ntiles; buf ^= 1) {
+      if (lead) res = k_steps(buf);
+      const int result_tile = lead ? tile : tile - streams;
+      other_half(buf, res, result_tile >= first ? result_tile : -1);
+      if (!lead) res = k_steps(buf);
+      __syncthreads();
+      tile = next;
+      next += streams;
+    }
+    if (!lead && tile - streams >= first)
+      store_tile<MODE>(a, tile - streams, tiles_j, group, hw, col_w, col_bias, half, l32, res);
+  } else {
+    fetch(tile);
+    stage_vecs(0);
+    if (next < ntiles) fetch(next);
+    __syncthreads();
+    for (int buf = 0; tile < ntiles; buf ^= 1) {
+      f32x16 c0 = {}, c1 = {};
+#pragma unroll
+      for (int t = 0; t < 8; ++t) mfma_step(buf, t, c0, c1);
+      if (next < ntiles) {
+        stage_vecs(buf ^ 1);
+        if (next + streams < ntiles) fetch(next + streams);
+      }
+      store_tile<MODE>(a, tile, tiles_j, group, hw, col_w, col_bias, half, l32, c0 + c1);
+      __syncthreads();
+      tile = next;
+      next += streams;
+    }
   }
 }
 
