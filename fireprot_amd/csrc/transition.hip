@@ -108,14 +108,21 @@ __global__ __launch_bounds__(256, 2) void transition_up_kernel(TransitionArgs a,
   }
 }
 
+// kSplit: gemm_nt_128_split (BF16 matrix cores, exact three-plane splits).
+template <bool kSplit>
 __global__ __launch_bounds__(256, 2) void transition_down_kernel(TransitionArgs a,
                                                                  int64_t rows) {
+  static_assert(sizeof(GemmStage) == sizeof(SplitStage), "both mainloops share the LDS stages");
   __shared__ __attribute__((aligned(16))) GemmStage As[2];
   __shared__ __attribute__((aligned(16))) GemmStage Bs[2];
   const int64_t r0 = (int64_t)blockIdx.x * kGemmTile;
   f32x16 acc[2][2] = {};
   // W_o is [128 out][512 in]: the B operand rows are output channels.
-  gemm_nt_128(a.h + r0 * kHid, kHid, a.w_o, kHid, kHid / kKStage, As, Bs, acc);
+  if constexpr (kSplit)
+    gemm_nt_128_split(a.h + r0 * kHid, kHid, a.w_o, kHid, kHid / kSplitK,
+                      reinterpret_cast<SplitStage*>(As), reinterpret_cast<SplitStage*>(Bs), acc);
+  else
+    gemm_nt_128(a.h + r0 * kHid, kHid, a.w_o, kHid, kHid / kKStage, As, Bs, acc);
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
@@ -161,8 +168,12 @@ hipError_t launch_transition(const TransitionArgs& a, hipStream_t stream) {
                      stream, a, tiles_j, (int)up_tiles, (int)slots);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(transition_down_kernel, dim3((uint32_t)down_tiles), dim3(256), 0, stream, a,
-                     rows);
+  if (fp32_matrix_cores_selected())
+    hipLaunchKernelGGL(transition_down_kernel<false>, dim3((uint32_t)down_tiles), dim3(256), 0,
+                       stream, a, rows);
+  else
+    hipLaunchKernelGGL(transition_down_kernel<true>, dim3((uint32_t)down_tiles), dim3(256), 0,
+                       stream, a, rows);
   return hipGetLastError();
 }
 

@@ -157,11 +157,14 @@ __global__ __launch_bounds__(kProjWaves * 64) void trimul_project_kernel(TriMulA
 // (gemm_nt_128 over the np keys).  Work-groups of one channel are consecutive
 // in the logical order, and xcd_remap gives each XCD a contiguous range, so
 // the A and B row panels a range touches stay in that XCD's L2.
+// kSplit: gemm_nt_128_split (BF16 matrix cores, exact three-plane splits).
+template <bool kSplit>
 __global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const float* __restrict__ pa,
                                                                  const float* __restrict__ pb,
                                                                  float* __restrict__ x, int n,
                                                                  int np, int tiles,
                                                                  uint32_t total) {
+  static_assert(sizeof(GemmStage) == sizeof(SplitStage), "both mainloops share the LDS stages");
   __shared__ __attribute__((aligned(16))) GemmStage As[2];
   __shared__ __attribute__((aligned(16))) GemmStage Bs[2];
 
@@ -178,8 +181,13 @@ __global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const float* __
 
   const int64_t slice = (int64_t)np * np;
   f32x16 acc[2][2] = {};
-  gemm_nt_128(pa + c * slice + (int64_t)i0 * np, np, pb + c * slice + (int64_t)j0 * np, np,
-              np / kKStage, As, Bs, acc);
+  if constexpr (kSplit)
+    gemm_nt_128_split(pa + c * slice + (int64_t)i0 * np, np, pb + c * slice + (int64_t)j0 * np,
+                      np, np / kSplitK, reinterpret_cast<SplitStage*>(As),
+                      reinterpret_cast<SplitStage*>(Bs), acc);
+  else
+    gemm_nt_128(pa + c * slice + (int64_t)i0 * np, np, pb + c * slice + (int64_t)j0 * np, np,
+                np / kKStage, As, Bs, acc);
 
   // x is blocked [n][np / 32][128 channels][32 columns]: the finish kernel
   // reads one contiguous 16 KB block per 32-pair tile.
@@ -340,8 +348,12 @@ hipError_t launch_trimul(const TriMulArgs& a, hipStream_t stream) {
                      dim3(kProjWaves * 64), 0, stream, a, tiles_k, (int)proj_tiles);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(trimul_contract_kernel, dim3((uint32_t)gemm_total), dim3(256), 0, stream,
-                     a.pa, a.pb, a.x, a.n, a.np, tiles, (uint32_t)gemm_total);
+  if (fp32_matrix_cores_selected())
+    hipLaunchKernelGGL(trimul_contract_kernel<false>, dim3((uint32_t)gemm_total), dim3(256), 0,
+                       stream, a.pa, a.pb, a.x, a.n, a.np, tiles, (uint32_t)gemm_total);
+  else
+    hipLaunchKernelGGL(trimul_contract_kernel<true>, dim3((uint32_t)gemm_total), dim3(256), 0,
+                       stream, a.pa, a.pb, a.x, a.n, a.np, tiles, (uint32_t)gemm_total);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(trimul_finish_kernel, dim3(grid_for(fin_tiles, 2)), dim3(256), 0, stream,
