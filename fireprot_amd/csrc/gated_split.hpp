@@ -1,0 +1,312 @@
+// Gated pair-row projections on the CDNA4 BF16 matrix cores, FP32-accurate.
+//
+// Both the triangle multiplication's input projections and the pair
+// transition's hidden layer produce, per channel c of a pair row x,
+//
+//   value_c = LN(x) . Wv[c] + bv[c]    gate_c = LN(x) . Wg[c] + bg[c]
+//
+// and combine the two:  (mask * sigmoid(gate)) * value  (kGatedTriMul) or
+// silu(gate) * value  (kGatedTransition).  Rows are split exactly into three
+// bfloat16 planes as they are staged to LDS, weights once per launch
+// (split.hpp), and each 32 x 32 block sums the six terms down to 2^-16
+// relative on v_mfma_f32_32x32x16_bf16.
+//
+// A wave's 32 B-operand columns are 16 value channels followed by the gate
+// channels of the same 16 channels, so its three weight planes fit in 96
+// VGPRs and the result of lane l (value) and lane l + 16 (gate) belong to one
+// channel: one v_permlane16_swap per register pair hands each lane both.  A
+// work-group (8 waves) covers 128 channels, one slice; the slices of a row
+// tile are neighbouring work-groups in the XCD-aware order.
+//
+// The pipeline is that of projection_split_kernel<kProjBlock>: LayerNorm 16
+// lanes per row, raw rows staged through LDS so that a row load is waited
+// an iteration after its issue, and lead / trail waves running the k steps
+// and the normalise-and-store half in opposite orders.
+#pragma once
+
+#include "common.hpp"
+#include "kernels.hpp"
+#include "split.hpp"
+
+namespace fpx {
+
+enum GatedMode { kGatedTriMul = 0, kGatedTransition = 1 };
+
+struct GatedArgs {
+  const float* x;        // pair row (r, k) at x + r * xs_r + k * xs_k
+  int64_t xs_r;
+  int64_t xs_k;
+  int rows_r;            // outer rows
+  int rows_k;            // valid k extent
+  int span_k;            // k extent covered by tiles (a multiple of 32, >= rows_k)
+  const float* ln_w;     // nullable
+  const float* ln_b;     // nullable
+  float eps;
+  const float* w_value[4];  // per slice: [128 out][128 in]
+  const float* w_gate[4];
+  const float* b_value[4];  // nullable
+  const float* b_gate[4];   // nullable
+  const float* mask;     // kGatedTriMul: nullable multiplier of row (r, k)
+  int64_t ms_r;
+  int64_t ms_k;
+  float* out[4];         // per slice, see gated_split_kernel
+  int np;                // kGatedTriMul: packed extent of the output
+};
+
+template <int MODE>
+struct GatedTraits;
+template <>
+struct GatedTraits<kGatedTriMul> {
+  static constexpr int kSlices = 2;  // a, b
+};
+template <>
+struct GatedTraits<kGatedTransition> {
+  static constexpr int kSlices = 4;  // hidden quarters
+};
+
+constexpr int kGatedWaves = 8;
+constexpr int kGatedRows = 32;
+constexpr int kGatedPlaneRow = kChannels + 8;  // bf16 per LDS row: 272 bytes
+
+// Outputs: kGatedTriMul writes out[slice][(c * np + r) * np + k] for all
+// k < span_k (0 past rows_k), channel-major with keys contiguous, the
+// contraction's operand layout.  kGatedTransition writes
+// out[slice][(r * rows_k + k) * 512 + c] for k < rows_k (h rows, the slice's
+// 128 columns of the 512).
+template <int MODE>
+__global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedArgs a, int tiles_k,
+                                                                          int ntiles,
+                                                                          int streams) {
+  constexpr int kSlices = GatedTraits<MODE>::kSlices;
+  __shared__ __attribute__((aligned(16))) __bf16 xs[2][3][kGatedRows][kGatedPlaneRow];
+  __shared__ __attribute__((aligned(16))) float raw[kGatedRows][kChannels + 4];
+  __shared__ float ms[4][kGatedRows];  // mask of tile T_k's rows at [k & 3]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+  const uint32_t logical = xcd_remap(blockIdx.x, gridDim.x);
+  const int slice = (int)(logical % kSlices);
+  const int first = (int)(logical / kSlices);
+  const bool odd = l32 >= 16;           // gate column (B operand) / odd 16-lane row
+  const int ch = 16 * w + (l32 & 15);   // channel of this lane's column, within the slice
+
+  bf16x8 wh[8], wl[8], wr[8];
+  {
+    const float* src = (odd ? a.w_gate[slice] : a.w_value[slice]) + (int64_t)ch * kChannels +
+                       8 * half;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const f32x4 u = *(const f32x4*)(src + 16 * t);
+      const f32x4 v = *(const f32x4*)(src + 16 * t + 4);
+      split3(f32x8{u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w}, wh[t], wl[t], wr[t]);
+    }
+  }
+  const float bv = a.b_value[slice] ? a.b_value[slice][ch] : 0.f;
+  const float bg = a.b_gate[slice] ? a.b_gate[slice][ch] : 0.f;
+
+  // LN: 16 lanes per row, lane c16 holding channels 8*c16 .. 8*c16 + 7 of
+  // tile row lrow.
+  const int c16 = lane & 15;
+  const int lrow = 4 * w + (lane >> 4);
+  f32x8 lnw, lnb;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    lnw[e] = a.ln_w ? a.ln_w[8 * c16 + e] : 1.f;
+    lnb[e] = a.ln_b ? a.ln_b[8 * c16 + e] : 0.f;
+  }
+
+  auto origin = [&](int tile, int& r, int& k0) {
+    r = tile / tiles_k;
+    k0 = (tile - r * tiles_k) * kGatedRows;
+  };
+
+  // Row loads with no branches on the data path (tile clamped to the last
+  // one, row to the last valid row); the mask is 0 past rows_k.
+  f32x8 stage_ln;
+  float stage_m = 0.f;
+  auto fetch = [&](int tile) {
+    int r, k0;
+    origin(tile < ntiles ? tile : ntiles - 1, r, k0);
+    const int kk = k0 + lrow;
+    const int k = min(kk, a.rows_k - 1);
+    const float* src = a.x + (int64_t)r * a.xs_r + (int64_t)k * a.xs_k + 8 * c16;
+    const f32x4 u = *(const f32x4*)src;
+    const f32x4 v = *(const f32x4*)(src + 4);
+    stage_ln = f32x8{u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+    if constexpr (MODE == kGatedTriMul) {
+      const float m = a.mask ? a.mask[(int64_t)r * a.ms_r + (int64_t)k * a.ms_k] : 1.f;
+      stage_m = kk < a.rows_k ? m : 0.f;
+    }
+  };
+
+  auto ln_stats = [&](const f32x8& rawv, f32x8& d, float& rstd) {
+    const float pivot = row16_first(rawv[0]);
+    const f32x8 sh = rawv - pivot;
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += sh[e];
+    const float mean = row16_sum(s) * (1.0f / kChannels);
+    d = sh - mean;
+    float q = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q += d[e] * d[e];
+    rstd = __builtin_amdgcn_rsqf(row16_sum(q) * (1.0f / kChannels) + a.eps);
+  };
+
+  auto stage_split = [&](int buf, const f32x8& d, float rstd, int k0) {
+    f32x8 y = d * rstd * lnw + lnb;
+    if (k0 + lrow >= a.rows_k) y = f32x8{};
+    bf16x8 hi, lo, rest;
+    split3(y, hi, lo, rest);
+    *(bf16x8*)&xs[buf][0][lrow][8 * c16] = hi;
+    *(bf16x8*)&xs[buf][1][lrow][8 * c16] = lo;
+    *(bf16x8*)&xs[buf][2][lrow][8 * c16] = rest;
+  };
+
+  auto consume = [&](int tile_index) {  // tile_index: k of the staged tile T_k
+    *(f32x8*)&raw[lrow][8 * c16] = stage_ln;
+    if constexpr (MODE == kGatedTriMul) {
+      if (c16 == 0) ms[tile_index & 3][lrow] = stage_m;
+    }
+  };
+
+  auto mfma_step = [&](int buf, int t, f32x16& c0, f32x16& c1) {
+    const int k = 16 * t + 8 * half;
+    const bf16x8 xh = *(const bf16x8*)&xs[buf][0][l32][k];
+    const bf16x8 xl = *(const bf16x8*)&xs[buf][1][l32][k];
+    const bf16x8 xr = *(const bf16x8*)&xs[buf][2][l32][k];
+    c0 = mfma_bf16(xh, wh[t], c0);
+    c1 = mfma_bf16(xh, wl[t], c1);
+    c0 = mfma_bf16(xl, wh[t], c0);
+    c1 = mfma_bf16(xl, wl[t], c1);
+    c0 = mfma_bf16(xr, wh[t], c0);
+    c1 = mfma_bf16(xh, wr[t], c1);
+  };
+  auto k_steps = [&](int buf) -> f32x16 {
+    f32x16 c0 = {}, c1 = {};
+#pragma unroll
+    for (int t = 0; t < 8; ++t) mfma_step(buf, t, c0, c1);
+    return c0 + c1;
+  };
+
+  // Result of tile `tile` (the k-th of this stream): lanes of even 16-lane
+  // rows hold the value channel, odd rows the gate channel.  Swapping
+  // register r with r + 8 across the row pair leaves every lane the value
+  // and gate of its channel for registers r + (odd ? 8 : 0), r < 8, i.e.
+  // tile rows 8 rr + 4 half + e for rr = (odd ? 2 : 0) + r / 4, e = r % 4.
+  auto store = [&](const f32x16& res, int tile, int k) {
+    f32x8 val;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      // Elements are copied out first: __builtin_bit_cast of a vector
+      // element reads element 0 with this compiler.
+      const float lo_reg = res[r];
+      const float hi_reg = res[r + 8];
+      const auto s = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, lo_reg),
+                                                      __builtin_bit_cast(unsigned, hi_reg),
+                                                      false, false);
+      const float p = __builtin_bit_cast(float, (unsigned)s[0]) + bv;
+      const float g = __builtin_bit_cast(float, (unsigned)s[1]);
+      if constexpr (MODE == kGatedTriMul) {
+        const int row = 8 * ((odd ? 2 : 0) + (r >> 2)) + 4 * half + (r & 3);
+        // native order: a = mask; a = a * sigmoid(g); a = a * p
+        val[r] = (ms[k & 3][row] * sigmoidf_(g + bg)) * p;
+      } else {
+        val[r] = g * sigmoidf_(g) * p;  // silu(a) * b
+      }
+    }
+    int r_out, k0;
+    origin(tile, r_out, k0);
+    const int rr0 = odd ? 2 : 0;
+    if constexpr (MODE == kGatedTriMul) {
+      float* dst = a.out[slice] + ((int64_t)ch * a.np + r_out) * a.np + k0 + 4 * half;
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+        *(f32x4*)(dst + 8 * (rr0 + q)) =
+            f32x4{val[4 * q + 0], val[4 * q + 1], val[4 * q + 2], val[4 * q + 3]};
+    } else {
+      float* dst = a.out[slice] + (int64_t)r_out * a.rows_k * 512 + ch;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const int kk = k0 + 8 * (rr0 + (r >> 2)) + 4 * half + (r & 3);
+        if (kk < a.rows_k) dst[(int64_t)kk * 512] = val[r];
+      }
+    }
+  };
+
+  const bool lead = w < kGatedWaves / 2;
+  int tile = first;  // first < streams <= ntiles: every work-group has a tile
+  int next = tile + streams;
+  int kidx = 0;      // k of tile T_k
+  fetch(tile);
+  {
+    int r0, k00;
+    origin(tile, r0, k00);
+    f32x8 d;
+    float rstd;
+    ln_stats(stage_ln, d, rstd);
+    stage_split(0, d, rstd, k00);
+    if constexpr (MODE == kGatedTriMul) {
+      if (c16 == 0) ms[0][lrow] = stage_m;
+    }
+  }
+  fetch(next);
+  consume(1);
+  fetch(next + streams);
+  __syncthreads();
+
+  f32x16 res = {};
+  for (int buf = 0; tile < ntiles; buf ^= 1) {
+    if (lead) res = k_steps(buf);
+    {
+      // The other half: normalise T_{k+1} into the other planes, then the
+      // iteration's global accesses (see projection_split_kernel).
+      const bool more = next < ntiles;
+      if (more) {
+        int rn, kn0;
+        origin(next, rn, kn0);
+        f32x8 d;
+        float rstd;
+        ln_stats(*(const f32x8*)&raw[lrow][8 * c16], d, rstd);
+        stage_split(buf ^ 1, d, rstd, kn0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      consume(kidx + 2);
+      fetch(next + 2 * streams);
+      if (lead)
+        store(res, tile, kidx);
+      else if (kidx > 0)
+        store(res, tile - streams, kidx - 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (!lead) res = k_steps(buf);
+    __syncthreads();
+    tile = next;
+    next += streams;
+    ++kidx;
+  }
+  if (!lead && kidx > 0) store(res, tile - streams, kidx - 1);
+}
+
+// Launches gated_split_kernel<MODE> over rows_r x span_k / 32 row tiles.
+template <int MODE>
+hipError_t launch_gated_split(const GatedArgs& a, hipStream_t stream) {
+  constexpr int kSlices = GatedTraits<MODE>::kSlices;
+  const int tiles_k = a.span_k / kGatedRows;
+  const int64_t ntiles = (int64_t)a.rows_r * tiles_k;
+  if (ntiles == 0) return hipSuccess;
+  if (a.span_k % kGatedRows || a.span_k < a.rows_k || a.rows_k < 1 || ntiles > 0x7fffffffll)
+    return hipErrorInvalidValue;
+  int64_t cap = (int64_t)device_cu_count() / kSlices;
+  if (cap >= 8) cap -= cap % 8;
+  if (cap < 1) cap = 1;
+  const int streams = (int)(ntiles < cap ? ntiles : cap);
+  hipLaunchKernelGGL(gated_split_kernel<MODE>, dim3(streams * kSlices), dim3(kGatedWaves * 64), 0,
+                     stream, a, tiles_k, (int)ntiles, streams);
+  return hipGetLastError();
+}
+
+}  // namespace fpx

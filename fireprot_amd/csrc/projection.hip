@@ -315,21 +315,6 @@ struct SplitTraits<kProjOut> {
 constexpr int kPlaneRow = kChannels + 8;  // bf16 per LDS row: 272 bytes, conflict-free b128 reads
 typedef __bf16 XPlane[kRows][kPlaneRow];
 
-// Sum over each 16-lane row of the wave (DPP quad_perm [1,0,3,2] and
-// [2,3,0,1], row_half_mirror, row_mirror), returned in all 16 lanes.
-__device__ __forceinline__ float row16_sum(float v) {
-  v += dpp<0xB1>(v);
-  v += dpp<0x4E>(v);
-  v += dpp<0x141>(v);
-  v += dpp<0x140>(v);
-  return v;
-}
-
-// Lane 0 of each 16-lane row, broadcast to the row (DPP row_newbcast:0).
-__device__ __forceinline__ float row16_first(float v) {
-  return dpp<0x150>(v);
-}
-
 template <int MODE>
 __global__ __launch_bounds__(SplitTraits<MODE>::kWaves * 64, SplitTraits<MODE>::kMinBlocks) void
 projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {

@@ -76,4 +76,19 @@ __device__ __forceinline__ void split2(f32x8 x, bf16x8& hi, bf16x8& lo) {
   lo = __builtin_bit_cast(bf16x8, u32x4{l[0], l[1], l[2], l[3]});
 }
 
+// Sum over each 16-lane row of the wave (DPP quad_perm [1,0,3,2] and
+// [2,3,0,1], row_half_mirror, row_mirror), returned in all 16 lanes.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  v += dpp<0x140>(v);
+  return v;
+}
+
+// Lane 0 of each 16-lane row, broadcast to the row (DPP row_newbcast:0).
+__device__ __forceinline__ float row16_first(float v) {
+  return dpp<0x150>(v);
+}
+
 }  // namespace fpx

@@ -13,6 +13,7 @@
 //   shared gemm_nt_128 mainloop (K = 512), with the strided, optionally
 //   accumulated store.
 #include "common.hpp"
+#include "gated_split.hpp"
 #include "gemm.hpp"
 #include "kernels.hpp"
 
@@ -164,9 +165,30 @@ hipError_t launch_transition(const TransitionArgs& a, hipStream_t stream) {
   int64_t slots = grid_cap(2) / kQuarters;
   if (slots > up_tiles) slots = up_tiles;
   if (slots < 1) slots = 1;
-  hipLaunchKernelGGL(transition_up_kernel, dim3((uint32_t)(slots * kQuarters)), dim3(256), 0,
-                     stream, a, tiles_j, (int)up_tiles, (int)slots);
-  hipError_t e = hipGetLastError();
+  hipError_t e;
+  if (fp32_matrix_cores_selected()) {
+    hipLaunchKernelGGL(transition_up_kernel, dim3((uint32_t)(slots * kQuarters)), dim3(256), 0,
+                       stream, a, tiles_j, (int)up_tiles, (int)slots);
+    e = hipGetLastError();
+  } else {
+    GatedArgs g{};
+    g.x = a.x;
+    g.xs_r = a.xs_i;
+    g.xs_k = a.xs_j;
+    g.rows_r = a.rows_i;
+    g.rows_k = a.rows_j;
+    g.span_k = tiles_j * kRows;
+    g.ln_w = a.ln_w;
+    g.ln_b = a.ln_b;
+    g.eps = a.eps;
+    // h = silu(x W_a^T) * (x W_b^T): W_a rows are the gates, W_b rows the values.
+    for (int q = 0; q < kQuarters; ++q) {
+      g.w_value[q] = a.w_b + (int64_t)q * kChannels * kChannels;
+      g.w_gate[q] = a.w_a + (int64_t)q * kChannels * kChannels;
+      g.out[q] = a.h + q * kChannels;
+    }
+    e = launch_gated_split<kGatedTransition>(g, stream);
+  }
   if (e != hipSuccess) return e;
   if (fp32_matrix_cores_selected())
     hipLaunchKernelGGL(transition_down_kernel<false>, dim3((uint32_t)down_tiles), dim3(256), 0,

@@ -22,6 +22,7 @@
 //   trimul_finish_kernel   LN_out(x) W_z^T and LN_in(z) W_g^T for 32 pairs
 //                          per tile, the sigmoid gate and the in-place write
 #include "common.hpp"
+#include "gated_split.hpp"
 #include "gemm.hpp"
 #include "kernels.hpp"
 
@@ -41,7 +42,6 @@ constexpr int kProjWaves = 8;
 
 __global__ __launch_bounds__(kProjWaves * 64) void trimul_project_kernel(TriMulArgs a, int tiles_k,
                                                                          int ntiles) {
-  constexpr int kThreads = kProjWaves * 64;
   constexpr int kRowsPerWave = kRows / kProjWaves;
   __shared__ __attribute__((aligned(16))) float xs[2][kRows][kLds];
   __shared__ float ms[2][kRows];
@@ -344,9 +344,36 @@ hipError_t launch_trimul(const TriMulArgs& a, hipStream_t stream) {
   const int64_t fin_tiles = (int64_t)a.n * tiles_j;
   if (proj_tiles > 0x7fffffff || gemm_total > 0x7fffffffu || fin_tiles > 0x7fffffff)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(trimul_project_kernel, dim3(grid_for(proj_tiles, 1)),
-                     dim3(kProjWaves * 64), 0, stream, a, tiles_k, (int)proj_tiles);
-  hipError_t e = hipGetLastError();
+  hipError_t e;
+  if (fp32_matrix_cores_selected()) {
+    hipLaunchKernelGGL(trimul_project_kernel, dim3(grid_for(proj_tiles, 1)),
+                       dim3(kProjWaves * 64), 0, stream, a, tiles_k, (int)proj_tiles);
+    e = hipGetLastError();
+  } else {
+    GatedArgs g{};
+    g.x = a.z;
+    g.xs_r = a.outgoing ? a.zs_i : a.zs_j;
+    g.xs_k = a.outgoing ? a.zs_j : a.zs_i;
+    g.rows_r = a.n;
+    g.rows_k = a.n;
+    g.span_k = a.np;
+    g.ln_w = a.ln_in_w;
+    g.ln_b = a.ln_in_b;
+    g.eps = a.eps_in;
+    for (int side = 0; side < 2; ++side) {
+      g.w_value[side] = a.w_ab[2 * side];
+      g.w_gate[side] = a.w_ab[2 * side + 1];
+      g.b_value[side] = a.b_ab[2 * side];
+      g.b_gate[side] = a.b_ab[2 * side + 1];
+    }
+    g.mask = a.mask;
+    g.ms_r = a.outgoing ? a.ms_i : a.ms_j;
+    g.ms_k = a.outgoing ? a.ms_j : a.ms_i;
+    g.out[0] = a.pa;
+    g.out[1] = a.pb;
+    g.np = a.np;
+    e = launch_gated_split<kGatedTriMul>(g, stream);
+  }
   if (e != hipSuccess) return e;
   if (fp32_matrix_cores_selected())
     hipLaunchKernelGGL(trimul_contract_kernel<false>, dim3((uint32_t)gemm_total), dim3(256), 0,
