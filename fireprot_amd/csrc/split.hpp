@@ -26,6 +26,14 @@ __device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// v_mfma_f32_16x16x32_bf16: lane l holds A[l % 16][8 (l / 16) + e] and
+// B[8 (l / 16) + e][l % 16], e = 0..7, of one 32-deep k step, and result
+// register r holds D[4 (l / 16) + r][l % 16] (checked on the device against a
+// host product of small integers).
+__device__ __forceinline__ f32x4 mfma16_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 // One pair step of the splits below: the pair's bf16 roundings packed in one

@@ -326,6 +326,230 @@ __global__ __launch_bounds__(256, 2) void trimul_finish_kernel(TriMulArgs a, int
   }
 }
 
+// ------------------------------------------------- finish, BF16 cores
+// The finish on v_mfma_f32_16x16x32_bf16 with exact three-plane splits of
+// both normalised inputs and both weights (six terms, FP32 rounding level).
+// The 16 x 16 shape lets a wave hold W_z and W_g planes for 16 output
+// channels in 96 VGPRs while the value (LN_out(x) W_z^T) and gate
+// (LN_in(z) W_g^T) results of one channel land in the same lane, so a
+// work-group of 8 waves covers all 128 channels of a 32-pair tile.
+// Persistent, one work-group per CU, with the pipeline of the split
+// projections: raw x (transposed on its way in) and z rows are staged
+// through per-wave LDS rows and waited an iteration after their loads;
+// waves 0-3 run their k steps first, waves 4-7 last.  With accumulate, the
+// residual values are loaded an iteration ahead of their stores.
+constexpr int kFinPlaneRow = kChannels + 8;  // bf16 per LDS row: 272 bytes
+
+__global__ __launch_bounds__(512, 1) void trimul_finish_split_kernel(TriMulArgs a, int tiles_j,
+                                                                     int ntiles) {
+  __shared__ __attribute__((aligned(16))) __bf16 px[2][3][kRows][kFinPlaneRow];
+  __shared__ __attribute__((aligned(16))) __bf16 pz[2][3][kRows][kFinPlaneRow];
+  __shared__ __attribute__((aligned(16))) float raw_x[kRows][kChannels + 4];
+  __shared__ __attribute__((aligned(16))) float raw_z[kRows][kChannels + 4];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15;
+  const int g4 = lane >> 4;          // 16-lane group: k group of the operands, row group of D
+  const int ch = 16 * w + l16;       // output channel of this lane
+  const int n = a.n;
+  const int64_t nb = a.np / 32;
+  const bool residual = a.accumulate != 0;
+
+  // Weight planes: B[k][c] = W[c][k], lane holding keys 32t + 8 g4 + e.
+  bf16x8 wz[3][4], wg[3][4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const float* sz = a.w_z + (int64_t)ch * kChannels + 32 * t + 8 * g4;
+    const float* sg = a.w_g + (int64_t)ch * kChannels + 32 * t + 8 * g4;
+    const f32x4 z0 = *(const f32x4*)sz, z1 = *(const f32x4*)(sz + 4);
+    const f32x4 g0 = *(const f32x4*)sg, g1 = *(const f32x4*)(sg + 4);
+    split3(f32x8{z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w}, wz[0][t], wz[1][t], wz[2][t]);
+    split3(f32x8{g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w}, wg[0][t], wg[1][t], wg[2][t]);
+  }
+  const float bz = a.b_z ? a.b_z[ch] : 0.f;
+  const float bg = a.b_g ? a.b_g[ch] : 0.f;
+
+  // LN lanes: 16 per row, lane c16 = l16 holding channels 8 c16 .. +7 of
+  // tile row lrow.
+  const int lrow = 4 * w + g4;
+  f32x8 lnw_in, lnb_in, lnw_out, lnb_out;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int c = 8 * l16 + e;
+    lnw_in[e] = a.ln_in_w ? a.ln_in_w[c] : 1.f;
+    lnb_in[e] = a.ln_in_b ? a.ln_in_b[c] : 0.f;
+    lnw_out[e] = a.ln_out_w ? a.ln_out_w[c] : 1.f;
+    lnb_out[e] = a.ln_out_b ? a.ln_out_b[c] : 0.f;
+  }
+
+  auto origin = [&](int tile, int& i, int& jb) {
+    i = tile / tiles_j;
+    jb = tile - i * tiles_j;
+  };
+
+  // Loads of one tile: x chunks x[c][4w .. 4w+3] for c = lane, lane + 64 of
+  // the tile's contiguous 16 KB block (this wave's 4 rows, transposed at
+  // the copy), and z row lrow (clamped to n - 1), channels 8 l16 .. +7.
+  f32x4 sx[2];
+  f32x8 sz_raw;
+  auto fetch = [&](int tile) {
+    int i, jb;
+    origin(tile < ntiles ? tile : ntiles - 1, i, jb);
+    const float* xb = a.x + ((int64_t)i * nb + jb) * kChannels * 32 + 4 * w;
+    sx[0] = *(const f32x4*)(xb + (int64_t)lane * 32);
+    sx[1] = *(const f32x4*)(xb + (int64_t)(lane + 64) * 32);
+    const int j = min(jb * kRows + lrow, n - 1);
+    const float* zr = a.z + (int64_t)i * a.zs_i + (int64_t)j * a.zs_j + 8 * l16;
+    const f32x4 u = *(const f32x4*)zr;
+    const f32x4 v = *(const f32x4*)(zr + 4);
+    sz_raw = f32x8{u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+  };
+  auto copy_raw = [&]() {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) raw_x[4 * w + e][lane + 64 * q] = sx[q][e];
+    }
+    *(f32x8*)&raw_z[lrow][8 * l16] = sz_raw;
+  };
+
+  auto ln_split = [&](const f32x8& rawv, float eps, const f32x8& gw, const f32x8& gb, bool valid,
+                      __bf16 (*planes)[kRows][kFinPlaneRow]) {
+    const float pivot = row16_first(rawv[0]);
+    const f32x8 sh = rawv - pivot;
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += sh[e];
+    const f32x8 d = sh - row16_sum(s) * (1.0f / kChannels);
+    float q = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q += d[e] * d[e];
+    const float rstd = __builtin_amdgcn_rsqf(row16_sum(q) * (1.0f / kChannels) + eps);
+    f32x8 y = d * rstd * gw + gb;
+    if (!valid) y = f32x8{};
+    bf16x8 hi, lo, rest;
+    split3(y, hi, lo, rest);
+    *(bf16x8*)&planes[0][lrow][8 * l16] = hi;
+    *(bf16x8*)&planes[1][lrow][8 * l16] = lo;
+    *(bf16x8*)&planes[2][lrow][8 * l16] = rest;
+  };
+  // Normalises the raw rows of the tile whose first pair row is j0 into
+  // planes buf.  Rows past n (never stored) are zeroed.
+  auto normalise = [&](int buf, int j0) {
+    const bool valid = j0 + lrow < n;
+    ln_split(*(const f32x8*)&raw_x[lrow][8 * l16], a.eps_out, lnw_out, lnb_out, valid, px[buf]);
+    ln_split(*(const f32x8*)&raw_z[lrow][8 * l16], a.eps_in, lnw_in, lnb_in, valid, pz[buf]);
+  };
+
+  // acc[rb][0]: value, acc[rb][1]: gate, rows 16 rb + 4 g4 + r, channel ch.
+  auto k_steps = [&](int buf, f32x4 (&acc)[2][2]) {
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) acc[rb][0] = acc[rb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    constexpr int kTerms[6][2] = {{0, 0}, {0, 1}, {1, 0}, {1, 1}, {0, 2}, {2, 0}};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      bf16x8 ax[2][3], az[2][3];
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl) {
+          ax[rb][pl] = *(const bf16x8*)&px[buf][pl][16 * rb + l16][32 * t + 8 * g4];
+          az[rb][pl] = *(const bf16x8*)&pz[buf][pl][16 * rb + l16][32 * t + 8 * g4];
+        }
+      }
+#pragma unroll
+      for (int tm = 0; tm < 6; ++tm) {
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+          acc[rb][0] = mfma16_bf16(ax[rb][kTerms[tm][0]], wz[kTerms[tm][1]][t], acc[rb][0]);
+          acc[rb][1] = mfma16_bf16(az[rb][kTerms[tm][0]], wg[kTerms[tm][1]][t], acc[rb][1]);
+        }
+      }
+    }
+  };
+
+  // Residual values of a tile (accumulate), loaded an iteration ahead.
+  f32x4 resid[2] = {};
+  auto load_resid = [&](int tile) {
+    if (!residual || tile >= ntiles) return;
+    int i, jb;
+    origin(tile, i, jb);
+    const float* o = a.out + (int64_t)i * a.os_i + ch;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = min(jb * kRows + 16 * rb + 4 * g4 + r, n - 1);
+        resid[rb][r] = o[(int64_t)j * a.os_j];
+      }
+    }
+  };
+  auto store = [&](int tile, const f32x4 (&acc)[2][2]) {
+    int i, jb;
+    origin(tile, i, jb);
+    float* o = a.out + (int64_t)i * a.os_i + ch;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = jb * kRows + 16 * rb + 4 * g4 + r;
+        // native: value = sigmoid(g) * x; z + value when adding
+        const float v = sigmoidf_(acc[rb][1][r] + bg) * (acc[rb][0][r] + bz);
+        if (j < n) o[(int64_t)j * a.os_j] = residual ? resid[rb][r] + v : v;
+      }
+    }
+  };
+
+  const bool lead = w < 4;
+  const int stride = (int)gridDim.x;
+  int tile = blockIdx.x;  // grid <= ntiles: every work-group has a tile
+  int next = tile + stride;
+  {
+    int i0, jb0;
+    origin(tile, i0, jb0);
+    fetch(tile);
+    copy_raw();
+    normalise(0, jb0 * kRows);
+  }
+  fetch(next);
+  copy_raw();
+  fetch(next + stride);
+  if (lead) load_resid(tile);
+  __syncthreads();
+
+  f32x4 res[2][2] = {};
+  int done = -1;  // trail waves: the tile whose result `res` holds
+  for (int buf = 0; tile < ntiles; buf ^= 1) {
+    if (lead) k_steps(buf, res);
+    if (next < ntiles) {
+      int i1, jb1;
+      origin(next, i1, jb1);
+      normalise(buf ^ 1, jb1 * kRows);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    copy_raw();
+    fetch(next + 2 * stride);
+    if (lead) {
+      store(tile, res);
+      load_resid(next);
+    } else {
+      if (done >= 0) store(done, res);
+      load_resid(tile);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (!lead) {
+      k_steps(buf, res);
+      done = tile;
+    }
+    __syncthreads();
+    tile = next;
+    next += stride;
+  }
+  if (!lead && done >= 0) store(done, res);
+}
+
 int grid_for(int64_t ntiles, int per_cu) {
   const int64_t cap = (int64_t)device_cu_count() * per_cu;
   return (int)(ntiles < cap ? ntiles : cap);
@@ -383,8 +607,12 @@ hipError_t launch_trimul(const TriMulArgs& a, hipStream_t stream) {
                        stream, a.pa, a.pb, a.x, a.n, a.np, tiles, (uint32_t)gemm_total);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(trimul_finish_kernel, dim3(grid_for(fin_tiles, 2)), dim3(256), 0, stream,
-                     a, tiles_j, (int)fin_tiles);
+  if (fp32_matrix_cores_selected())
+    hipLaunchKernelGGL(trimul_finish_kernel, dim3(grid_for(fin_tiles, 2)), dim3(256), 0, stream,
+                       a, tiles_j, (int)fin_tiles);
+  else
+    hipLaunchKernelGGL(trimul_finish_split_kernel, dim3(grid_for(fin_tiles, 1)), dim3(512), 0,
+                       stream, a, tiles_j, (int)fin_tiles);
   return hipGetLastError();
 }
 
