@@ -488,6 +488,101 @@ def bench_transition(args) -> dict:
     return result
 
 
+OPS_METRIC = "pair LayerNorm and sigmoid gate HBM GB/s (% of 8 TB/s) at N=1536 FP32, 1 GPU"
+
+
+def bench_ops(args) -> dict:
+    """The memory-bound stage kernels at N = 1536, FP32, each on its own:
+
+    - pair LayerNorm of z [1536, 1536, 128] (``fpx_layer_norm_c128``), read
+      contiguously (starting node) and through the transposed view with
+      strides (128, N*128) (ending node, no transposed copy): reads and
+      writes 512 N^2 bytes each, 2.42 GB per launch;
+    - the sigmoid output gate ``out = value * sigmoid(gate)``
+      (``fpx_sigmoid_mul_out``) over N^2 * 128 floats: two reads and one
+      write, 3.62 GB per launch.
+
+    The block fuses both (LN into the projection prologue, the gate into the
+    attention epilogue); these standalone entries serve the reference's
+    per-op hooks.  torch's own ops on the same GPU are timed beside them.
+    ``value`` is the transposed-view LayerNorm's GB/s (the reference's
+    transposed-norm benchmark); the line carries all six rates.
+    """
+    import torch
+    import torch.nn.functional as F
+
+    from fireprot_amd import _native, workloads
+
+    n = 1536
+    dev = torch.device("cuda:0")
+    lib = _native.library()
+    log(f"inputs ops n={n}")
+    z = workloads.make_pair(n).to(dev)
+    g = torch.Generator().manual_seed(733)
+    w = torch.randn(128, generator=g).to(dev)
+    b = torch.randn(128, generator=g).to(dev)
+    gate = torch.randn(n, n, 128, generator=g).to(dev)
+    y = torch.empty_like(z)
+    stream = torch.cuda.current_stream(dev)
+    count = n * n * 128
+    ln_bytes = 2 * 4 * count
+    gate_bytes = 3 * 4 * count
+
+    def ln(transposed):
+        si, sj = (128, n * 128) if transposed else (n * 128, 128)
+        _native.check(lib.fpx_layer_norm_c128(z.data_ptr(), n, n, si, sj, w.data_ptr(), b.data_ptr(),
+                                               1e-5, y.data_ptr(), stream.cuda_stream),
+                      "fpx_layer_norm_c128")
+
+    def sig():
+        _native.check(lib.fpx_sigmoid_mul_out(gate.data_ptr(), z.data_ptr(), y.data_ptr(), count,
+                                              stream.cuda_stream), "fpx_sigmoid_mul_out")
+
+    cases = {
+        "layer_norm": (lambda: ln(False), ln_bytes),
+        "layer_norm_transposed": (lambda: ln(True), ln_bytes),
+        "sigmoid_gate": (sig, gate_bytes),
+        "torch_layer_norm": (lambda: F.layer_norm(z, (128,), w, b, 1e-5), ln_bytes),
+        "torch_layer_norm_transposed":
+            (lambda: F.layer_norm(z.transpose(0, 1), (128,), w, b, 1e-5), ln_bytes),
+        "torch_sigmoid_gate": (lambda: torch.sigmoid(gate) * z, gate_bytes),
+    }
+    out = {}
+    with torch.inference_mode():
+        for name, (fn, nbytes) in cases.items():
+            for _ in range(args.warmup):
+                fn()
+            torch.cuda.synchronize()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(args.steps):
+                fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / args.steps
+            out[name] = {"ms": round(ms, 4), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                         "hbm_peak_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+            log(f"{name}: {ms:.3f} ms, {out[name]['gbps']} GB/s")
+    head = out["layer_norm_transposed"]
+    traffic = recorded_traffic("ops-layer-norm-transposed")
+    return {
+        "metric": OPS_METRIC, "value": head["gbps"], "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": head["ms"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded z ~ N(0,1), gate ~ N(0,1), random LN affine)",
+        "config": {"workload": "ops-n1536-f32: standalone pair LayerNorm (contiguous and "
+                               "transposed view) and sigmoid gate", "n": n,
+                   "bytes_per_launch": {"layer_norm": ln_bytes, "sigmoid_gate": gate_bytes},
+                   "kernels": out},
+        "roofline": {"kernel": "layer_norm32_kernel (fpx_layer_norm_c128, transposed view)",
+                     "bound": "hbm", "achieved": head["gbps"], "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": head["hbm_peak_frac"], "traffic": traffic,
+                     "avg_launch_ms": head["ms"]},
+        "cpu_baseline": None,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -495,11 +590,12 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c4", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--workload", default="block",
-                    choices=["block", "openfold3", "trimul", "transition"],
+                    choices=["block", "openfold3", "trimul", "transition", "ops"],
                     help="block: the triangle-attention block (default); openfold3: "
                          "OpenFold3's _attention through fpx_attn_strided; trimul: "
                          "triangle multiplication (fpx_tri_mul); transition: the pair "
-                         "transition (fpx_transition)")
+                         "transition (fpx_transition); ops: the standalone pair "
+                         "LayerNorm and sigmoid gate (HBM-bound)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 1 GiB device-to-device copy (the known-size "
@@ -528,6 +624,12 @@ def main() -> int:
         return 0
     if args.workload == "trimul":
         result = bench_trimul(args)
+        if args.calibrate_copy:
+            calibrate_copy(torch.device("cuda:0"))
+        print(json.dumps(result), flush=True)
+        return 0
+    if args.workload == "ops":
+        result = bench_ops(args)
         if args.calibrate_copy:
             calibrate_copy(torch.device("cuda:0"))
         print(json.dumps(result), flush=True)

@@ -97,6 +97,7 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "fpx_layer_norm_c128": (_i, [_p, _i64, _i64, _i64, _i64, _p, _p, _f, _p, _p]),
     "fpx_qkv_projection": (_i, [_p, _i64, _p, _p, _p, _p, _p]),
     "fpx_sigmoid_mul_out": (_i, [_p, _p, _p, _i64, _p]),
+    "fpx_split_planes": (_i, [_p, _i64, _p, _p]),
 }
 
 _lock = threading.RLock()

@@ -631,4 +631,10 @@ int fpx_sigmoid_mul_out(const float* gate, const float* value, float* out, int64
                                         static_cast<hipStream_t>(stream)));
 }
 
+int fpx_split_planes(const float* x, int64_t count, uint16_t* planes, void* stream) {
+  if (count < 0 || count % 8 != 0) return FPX_ERR_DIMS;
+  if (!aligned(x, 16) || !aligned(planes, 16)) return FPX_ERR_POINTER;
+  return status(fpx::launch_split_planes(x, planes, count / 8, static_cast<hipStream_t>(stream)));
+}
+
 }  // extern "C"

@@ -2,6 +2,7 @@
 // bias, the standalone C128 pair LayerNorm and the sigmoid output gate.
 #include "common.hpp"
 #include "kernels.hpp"
+#include "split.hpp"
 
 #include <atomic>
 #include <cmath>
@@ -133,6 +134,48 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const float* __restrict
       f32x2{d0 * rstd * gw.x + gb.x, d1 * rstd * gw.y + gb.y};
 }
 
+// Thirty-two lanes per 128-channel row, one 16-byte vector per lane (the
+// 32 lanes read the row's 512 contiguous bytes); a wave covers 2 rows and a
+// work-group 8 rows that are consecutive along axis b, the axis whose rows
+// are adjacent in memory (j for the contiguous pair, i for the transposed
+// view), so each work-group reads 4 KB contiguously.  Row (a, r) is read at
+// x + a*xs_a + r*xs_b and written at y + a*ys_a + r*ys_b.  Statistics as
+// ln_stats_c128: values shifted by the row's first channel, their mean, then
+// the biased variance of the centred values; row16_sum plus one xor-16
+// exchange per reduction.
+__global__ __launch_bounds__(256) void layer_norm32_kernel(const float* __restrict__ x,
+                                                           int64_t rows_b, int64_t xs_a,
+                                                           int64_t xs_b, int64_t ys_a,
+                                                           int64_t ys_b,
+                                                           const float* __restrict__ w,
+                                                           const float* __restrict__ b, float eps,
+                                                           float* __restrict__ y, int groups_b) {
+  const int c32 = threadIdx.x & 31;
+  const int r8 = threadIdx.x >> 5;
+  const int g = blockIdx.x;
+  const int64_t ra = g / groups_b;
+  const int64_t rb = (int64_t)(g - (int)ra * groups_b) * 8 + r8;
+  const bool valid = rb < rows_b;
+  f32x4 v = {0.f, 0.f, 0.f, 0.f};
+  if (valid) v = *(const f32x4*)(x + ra * xs_a + rb * xs_b + 4 * c32);
+  const float pivot = __shfl(v.x, 0, 32);
+  const f32x4 sh = v - pivot;
+  float s = row16_sum((sh.x + sh.y) + (sh.z + sh.w));
+  s += __shfl_xor(s, 16, 32);
+  const float mean = s * (1.0f / kChannels);
+  const f32x4 d = sh - mean;
+  float q = row16_sum((d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w));
+  q += __shfl_xor(q, 16, 32);
+  const float rstd = __builtin_amdgcn_rsqf(q * (1.0f / kChannels) + eps);
+  f32x4 gw = {1.f, 1.f, 1.f, 1.f}, gb = {0.f, 0.f, 0.f, 0.f};
+  if (w) gw = *(const f32x4*)(w + 4 * c32);
+  if (b) gb = *(const f32x4*)(b + 4 * c32);
+  if (valid) *(f32x4*)(y + ra * ys_a + rb * ys_b + 4 * c32) = d * rstd * gw + gb;
+}
+
+// out = value * sigmoid(gate), one 16-byte vector per thread (a plain copy
+// kernel of this shape streams fastest on this part: more vectors per thread
+// measured slower).
 __global__ __launch_bounds__(256) void sigmoid_mul_kernel(const f32x4* __restrict__ gate,
                                                           const f32x4* __restrict__ value,
                                                           f32x4* __restrict__ out,
@@ -202,6 +245,25 @@ hipError_t launch_layer_norm(const float* x, int64_t rows_i, int64_t rows_j, int
                              hipStream_t stream) {
   const int64_t rows = rows_i * rows_j;
   if (rows == 0) return hipSuccess;
+  auto a16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  if (a16(x) && a16(y) && (w == nullptr || a16(w)) && (b == nullptr || a16(b)) && xs_i % 4 == 0 &&
+      xs_j % 4 == 0) {
+    // Group rows along the axis with the smaller input stride (b); a is the other.
+    const bool along_i = rows_i > 1 && xs_i < xs_j;
+    const int64_t rows_a = along_i ? rows_j : rows_i;
+    const int64_t rows_b = along_i ? rows_i : rows_j;
+    const int64_t groups_b = (rows_b + 7) / 8;
+    const int64_t blocks = rows_a * groups_b;
+    if (groups_b <= 0x7fffffffll && blocks <= 0x7fffffffll) {
+      const int64_t ys_i = rows_j * kChannels, ys_j = kChannels;
+      hipLaunchKernelGGL(layer_norm32_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream, x,
+                         rows_b, along_i ? xs_j : xs_i, along_i ? xs_i : xs_j,
+                         along_i ? ys_j : ys_i, along_i ? ys_i : ys_j, w, b, eps, y,
+                         (int)groups_b);
+      return hipGetLastError();
+    }
+  }
+  // Rows only 8-byte aligned: one wavefront per row.
   const int64_t blocks = (rows + 3) / 4;
   if (blocks > 0x7fffffffll) return hipErrorInvalidValue;
   hipLaunchKernelGGL(layer_norm_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream, x, rows_i,
@@ -216,6 +278,43 @@ hipError_t launch_sigmoid_mul(const float* gate, const float* value, float* out,
   if (blocks > 0x7fffffffll) return hipErrorInvalidValue;
   hipLaunchKernelGGL(sigmoid_mul_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream,
                      (const f32x4*)gate, (const f32x4*)value, (f32x4*)out, count4);
+  return hipGetLastError();
+}
+
+// The exact bf16 plane split every FP32-accurate kernel uses, run on count8
+// groups of 8 floats: planes[0..2] from split3 (f32x8), planes[3..4] from
+// split2 on the two f32x4 halves, each plane [count8 * 8] bf16.
+__global__ __launch_bounds__(256) void split_planes_kernel(const f32x4* __restrict__ x,
+                                                           uint32_t* __restrict__ planes,
+                                                           int64_t count8) {
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (g >= count8) return;
+  const f32x4 u = x[2 * g], v = x[2 * g + 1];
+  bf16x8 hi, lo, rest;
+  split3(f32x8{u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w}, hi, lo, rest);
+  bf16x4 h0, l0, h1, l1;
+  split2(u, h0, l0);
+  split2(v, h1, l1);
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  const int64_t words = count8 * 4;  // one plane, in 32-bit words
+  u32x4* out = reinterpret_cast<u32x4*>(planes);
+  out[g] = __builtin_bit_cast(u32x4, hi);
+  out[words / 4 + g] = __builtin_bit_cast(u32x4, lo);
+  out[2 * words / 4 + g] = __builtin_bit_cast(u32x4, rest);
+  const u32x2 a = __builtin_bit_cast(u32x2, h0), b = __builtin_bit_cast(u32x2, h1);
+  const u32x2 c = __builtin_bit_cast(u32x2, l0), d = __builtin_bit_cast(u32x2, l1);
+  out[3 * words / 4 + g] = u32x4{a.x, a.y, b.x, b.y};
+  out[4 * words / 4 + g] = u32x4{c.x, c.y, d.x, d.y};
+}
+
+hipError_t launch_split_planes(const float* x, uint16_t* planes, int64_t count8,
+                               hipStream_t stream) {
+  if (count8 == 0) return hipSuccess;
+  const int64_t blocks = (count8 + 255) / 256;
+  if (blocks > 0x7fffffffll) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(split_planes_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream,
+                     (const f32x4*)x, reinterpret_cast<uint32_t*>(planes), count8);
   return hipGetLastError();
 }
 

@@ -144,6 +144,10 @@ hipError_t launch_layer_norm(const float* x, int64_t rows_i, int64_t rows_j, int
 hipError_t launch_sigmoid_mul(const float* gate, const float* value, float* out, int64_t count4,
                               hipStream_t stream);
 
+// Exact bf16 plane split self-check (split.hpp) over count8 groups of 8 floats.
+hipError_t launch_split_planes(const float* x, uint16_t* planes, int64_t count8,
+                               hipStream_t stream);
+
 // ------------------------------------------------------------ BF16 block
 // BF16 storage / FP32 accumulation variant of the block (gfx950
 // v_mfma_f32_32x32x16_bf16).  Same workspace roles and strides as the FP32

@@ -36,50 +36,85 @@ __device__ __forceinline__ f32x4 mfma16_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-// One pair step of the splits below: the pair's bf16 roundings packed in one
-// word (v_cvt_pk_bf16_f32), and the residuals x - float(hi) with float(hi)
-// recovered from that word by a shift and a mask (the generic conversion
-// takes a third more instructions).
-__device__ __forceinline__ uint32_t split_pair(f32x2 x, f32x2& residual) {
-  const uint32_t hb = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, bf16x2));
+// The pair steps of the splits below: the pair's bf16 roundings packed in
+// one word (v_cvt_pk_bf16_f32, round to nearest even), and the residuals
+// x - float(hi), with float(hi) recovered from that word by a shift and a
+// mask (the generic conversion takes a third more instructions).  Each
+// residual is exact (Sterbenz).  The shift, the mask and the subtraction run
+// at the double FP32/integer VALU rate once two waves share a SIMD, so they
+// cost as much as one v_dot2c_f32_bf16 against (-1, 0) would (measured).
+__device__ __forceinline__ uint32_t round_pair(f32x2 x) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, bf16x2));
+}
+__device__ __forceinline__ f32x2 residual_pair(uint32_t hb, f32x2 x) {
   const f32x2 back = {__builtin_bit_cast(float, hb << 16), __builtin_bit_cast(float, hb & 0xffff0000u)};
-  residual = x - back;
+  return x - back;
+}
+__device__ __forceinline__ uint32_t split_pair(f32x2 x, f32x2& residual) {
+  const uint32_t hb = round_pair(x);
+  residual = residual_pair(hb, x);
   return hb;
+}
+
+// N values (N even) -> hi, lo (and rest) planes, packed two per word.  Each
+// phase runs over all pairs before the next reads its results.
+template <int N>
+__device__ __forceinline__ void split2_words(const float* x, uint32_t* hi, uint32_t* lo) {
+  f32x2 r[N / 2];
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) hi[i] = round_pair(f32x2{x[2 * i], x[2 * i + 1]});
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) r[i] = residual_pair(hi[i], f32x2{x[2 * i], x[2 * i + 1]});
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) lo[i] = round_pair(r[i]);
+}
+template <int N>
+__device__ __forceinline__ void split3_words(const float* x, uint32_t* hi, uint32_t* lo,
+                                             uint32_t* rest) {
+  f32x2 r1[N / 2], r2[N / 2];
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) hi[i] = round_pair(f32x2{x[2 * i], x[2 * i + 1]});
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) r1[i] = residual_pair(hi[i], f32x2{x[2 * i], x[2 * i + 1]});
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) lo[i] = round_pair(r1[i]);
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) r2[i] = residual_pair(lo[i], r1[i]);
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) rest[i] = round_pair(r2[i]);
 }
 
 __device__ __forceinline__ void split3(f32x4 x, bf16x4& hi, bf16x4& lo, bf16x4& rest) {
   typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-  f32x2 r1a, r1b, r2a, r2b;
-  const uint32_t ha = split_pair(f32x2{x.x, x.y}, r1a), hb = split_pair(f32x2{x.z, x.w}, r1b);
-  const uint32_t la = split_pair(r1a, r2a), lb = split_pair(r1b, r2b);
-  hi = __builtin_bit_cast(bf16x4, u32x2{ha, hb});
-  lo = __builtin_bit_cast(bf16x4, u32x2{la, lb});
-  rest = __builtin_bit_cast(bf16x4, u32x2{__builtin_bit_cast(uint32_t, __builtin_convertvector(r2a, bf16x2)),
-                                          __builtin_bit_cast(uint32_t, __builtin_convertvector(r2b, bf16x2))});
+  const float v[4] = {x.x, x.y, x.z, x.w};
+  uint32_t h[2], l[2], r[2];
+  split3_words<4>(v, h, l, r);
+  hi = __builtin_bit_cast(bf16x4, u32x2{h[0], h[1]});
+  lo = __builtin_bit_cast(bf16x4, u32x2{l[0], l[1]});
+  rest = __builtin_bit_cast(bf16x4, u32x2{r[0], r[1]});
 }
 __device__ __forceinline__ void split3(f32x8 x, bf16x8& hi, bf16x8& lo, bf16x8& rest) {
-  hi = __builtin_convertvector(x, bf16x8);
-  const f32x8 r1 = x - __builtin_convertvector(hi, f32x8);
-  lo = __builtin_convertvector(r1, bf16x8);
-  rest = __builtin_convertvector(r1 - __builtin_convertvector(lo, f32x8), bf16x8);
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const float v[8] = {x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]};
+  uint32_t h[4], l[4], r[4];
+  split3_words<8>(v, h, l, r);
+  hi = __builtin_bit_cast(bf16x8, u32x4{h[0], h[1], h[2], h[3]});
+  lo = __builtin_bit_cast(bf16x8, u32x4{l[0], l[1], l[2], l[3]});
+  rest = __builtin_bit_cast(bf16x8, u32x4{r[0], r[1], r[2], r[3]});
 }
 __device__ __forceinline__ void split2(f32x4 x, bf16x4& hi, bf16x4& lo) {
   typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-  f32x2 ra, rb;
-  const uint32_t ha = split_pair(f32x2{x.x, x.y}, ra), hb = split_pair(f32x2{x.z, x.w}, rb);
-  hi = __builtin_bit_cast(bf16x4, u32x2{ha, hb});
-  lo = __builtin_bit_cast(bf16x4, u32x2{__builtin_bit_cast(uint32_t, __builtin_convertvector(ra, bf16x2)),
-                                        __builtin_bit_cast(uint32_t, __builtin_convertvector(rb, bf16x2))});
+  const float v[4] = {x.x, x.y, x.z, x.w};
+  uint32_t h[2], l[2];
+  split2_words<4>(v, h, l);
+  hi = __builtin_bit_cast(bf16x4, u32x2{h[0], h[1]});
+  lo = __builtin_bit_cast(bf16x4, u32x2{l[0], l[1]});
 }
 __device__ __forceinline__ void split2(f32x8 x, bf16x8& hi, bf16x8& lo) {
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const float v[8] = {x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]};
   uint32_t h[4], l[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f32x2 r;
-    h[i] = split_pair(f32x2{x[2 * i], x[2 * i + 1]}, r);
-    l[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, bf16x2));
-  }
+  split2_words<8>(v, h, l);
   hi = __builtin_bit_cast(bf16x8, u32x4{h[0], h[1], h[2], h[3]});
   lo = __builtin_bit_cast(bf16x8, u32x4{l[0], l[1], l[2], l[3]});
 }

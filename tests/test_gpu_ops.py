@@ -98,3 +98,43 @@ def test_sigmoid_gate_extremes_and_inputs_unchanged():
     assert result.data_ptr() != vc.data_ptr()
     with pytest.raises(ValueError):
         attention_gate.sigmoid_mul_out(gc[:, 1:], vc[:, 1:])
+
+
+@pytest.mark.parametrize("layout", ["offset8", "stride130", "rows2d"])
+def test_layer_norm_other_layouts(layout):
+    """Rows only 8-byte aligned (the one-wave-per-row kernel), rows whose
+    stride is not a multiple of 4 floats, and a 2-D [R, 128] input with a
+    ragged last row group (16 rows per group in the 16-byte-aligned kernel)."""
+    g = torch.Generator().manual_seed(1063)
+    n = 150
+    w = torch.randn(128, generator=g)
+    b = torch.randn(128, generator=g)
+    if layout == "offset8":
+        flat = torch.randn(n * n * 128 + 2, generator=g).cuda()
+        view = flat[2:].view(n, n, 128)
+        assert view.data_ptr() % 16 == 8
+    elif layout == "stride130":
+        view = torch.randn(n, n, 130, generator=g).cuda()[..., :128]
+    else:
+        view = torch.randn(n * n + 5, 128, generator=g).cuda()
+    expected = oracle.layer_norm(view.cpu(), w, b, 1e-5)
+    with torch.inference_mode():
+        actual = layer_norm.layer_norm_c128(view, w.cuda(), b.cuda(), 1e-5)
+        torch.cuda.synchronize()
+    assert_f32_parity(f"ln {layout}", actual.cpu(), expected)
+
+
+def test_sigmoid_gate_ragged_count():
+    g = torch.Generator().manual_seed(1069)
+    gate = torch.randn(37, 3, 128, generator=g) * 20
+    value = torch.randn(37, 3, 128, generator=g)
+    out = torch.full((37, 3, 128), float("nan")).cuda()
+    from fireprot_amd import _native
+
+    lib = _native.library()
+    gc, vc = gate.cuda(), value.cuda()
+    code = lib.fpx_sigmoid_mul_out(gc.data_ptr(), vc.data_ptr(), out.data_ptr(), gate.numel(),
+                                   torch.cuda.current_stream().cuda_stream)
+    _native.check(code, "fpx_sigmoid_mul_out")
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.cpu(), torch.sigmoid(gate) * value, atol=2e-6, rtol=2e-6)
