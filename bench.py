@@ -123,18 +123,33 @@ def cpu_baseline(cfg, z, mask, weights, budget_s: float = 40.0) -> dict:
 OF3_METRIC = "OpenFold3 _attention ms + TFLOP/s (% MFMA peak) at B=N=1536 FP32, 1 GPU"
 
 
-def split_executed(batch: int, n: int, ms: float) -> dict:
+def visited_key_tiles(n: int, valid: int | None, skip: bool) -> int:
+    """32-key tiles the block's attention visits per (outer row, head, query
+    tile), summed over outer rows.  With a tail mask (the first ``valid``
+    residues unmasked on both axes) and ``skip``, an outer row with an
+    unmasked key leaves out the trailing tiles whose keys are all masked
+    (their weights are exactly 0); fully masked rows visit every tile."""
+    nkt = -(-n // 32)
+    if valid is None or not skip or valid >= n:
+        return n * nkt
+    return valid * (-(-valid // 32)) + (n - valid) * nkt
+
+
+def split_executed(batch: int, n: int, ms: float, tiles: int | None = None) -> dict:
     """BF16 matrix-core work the split attention kernel executes for its
     FP32-accurate products: per 32 x 32 (query x key) wave tile, 18
     v_mfma_f32_32x32x16_bf16 (6 terms of S^T, 3 of O^T, two K-halves each) =
     18 * 32768 flop, against 2 * 65536 algorithmic flop.  Query rows are
-    padded to 128, keys to 32."""
+    padded to 128, keys to 32.  ``tiles``: key tiles visited summed over the
+    outer rows (default: every tile of every row)."""
     np_ = -(-n // 128) * 128
     nkt = -(-n // 32)
-    executed = batch * 4 * (np_ // 32) * nkt * 18 * 32768
+    visited = batch * nkt if tiles is None else tiles
+    executed = visited * 4 * (np_ // 32) * 18 * 32768
     executed_tflops = executed / (ms * 1e-3) / 1e12
     return {
         "matrix_unit": "bf16 (exact 3-plane split of K and Q, 2-plane V and P)",
+        "visited_key_tile_frac": round(visited / (batch * nkt), 4),
         "executed_flop_per_launch": executed,
         "executed_tflops": round(executed_tflops, 3),
         "executed_peak": BF16_MFMA_PEAK_TFLOPS,
@@ -743,7 +758,8 @@ def main() -> int:
         "avg_launch_ms": round(stages["attend"], 4),
     }
     if split:
-        roofline.update(split_executed(n, n, stages["attend"]))
+        roofline.update(split_executed(n, n, stages["attend"],
+                                       visited_key_tiles(n, cfg.valid, skip=True)))
     result = {
         "metric": METRIC,
         "value": round(value, 3),

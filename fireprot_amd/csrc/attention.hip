@@ -273,7 +273,7 @@ __global__ __launch_bounds__(kThreads, FPX_ATTN_WAVES_PER_SIMD) void attention_k
   uint32_t mw[kTileFlagWords] = {0u, 0u, 0u, 0u};
   bool any_masked, has_unmasked;
   if (kStaged) {
-    const uint32_t* f = a.tile_flags + (int64_t)b * 2 * kTileFlagWords;
+    const uint32_t* f = a.tile_flags + (int64_t)b * kTileFlagParts * kTileFlagWords;
     uint32_t any = 0u, open = 0u;
 #pragma unroll
     for (int i = 0; i < kTileFlagWords; ++i) {

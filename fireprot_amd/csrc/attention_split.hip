@@ -62,7 +62,7 @@ __device__ __forceinline__ int v_position(int g) {
 // -inf), and V rows are transposed into the V^T planes on their way to LDS.
 // Both read the staged bias copies, mask rows and tile flags.
 template <int LAYOUT>
-__global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a, int nqt, int nkt,
+__global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a, int nqt, int nkt_all,
                                                                       uint32_t total) {
   constexpr bool kBlock = LAYOUT == kAttnBlock;
   __shared__ __attribute__((aligned(16))) KPlane Ks[2][3];
@@ -90,7 +90,6 @@ __global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a
   const int row8 = tid >> 3;
   const int col4 = (tid & 7) * 4;
   const int vpos = v_position(col4 >> 2);
-  const int last = nkt - 1;
 
   // Per-work-group buffer descriptors over the (b, h) slices and the wave's
   // bias fragments (h, qt32, all key tiles), as in the FP32 kernel.
@@ -158,17 +157,41 @@ __global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a
   uint32_t mw[kTileFlagWords];
   uint32_t any = 0u, open = 0u;
   {
-    const uint32_t* f = a.tile_flags + (int64_t)b * 2 * kTileFlagWords;
+    const uint32_t* f = a.tile_flags + (int64_t)b * kTileFlagParts * kTileFlagWords;
 #pragma unroll
     for (int i = 0; i < kTileFlagWords; ++i) {
       const int lo = 32 * i;
-      const uint32_t valid = nkt >= lo + 32 ? 0xffffffffu : nkt > lo ? (1u << (nkt - lo)) - 1u : 0u;
+      const uint32_t valid =
+          nkt_all >= lo + 32 ? 0xffffffffu : nkt_all > lo ? (1u << (nkt_all - lo)) - 1u : 0u;
       mw[i] = f[i];
       any |= mw[i] & valid;
       open |= ~f[kTileFlagWords + i] & valid;
     }
   }
   const bool has_unmasked = open != 0u;
+  // Key tiles visited.  On rows with an unmasked key, the trailing tiles
+  // whose every mask bias is <= -kSkipMask carry weights that are exactly 0
+  // when the prepare projection's magnitude record bounds the logits
+  // (kernels.hpp), so they are left out; the result is bit-identical.
+  int nkt = nkt_all;
+  if constexpr (kBlock) {
+    if (has_unmasked && a.magnitudes != nullptr && a.magnitudes[4] == 1u) {
+      const float mq = __builtin_bit_cast(float, a.magnitudes[0]);
+      const float mk = __builtin_bit_cast(float, a.magnitudes[1]);
+      const float mv = __builtin_bit_cast(float, a.magnitudes[2]);
+      const float mb = __builtin_bit_cast(float, a.magnitudes[3]);
+      if (32.0f * mq * mk + mb < kSkipBound && mv < INFINITY) {  // false for NaN
+        const uint32_t* far = a.tile_flags + (int64_t)b * kTileFlagParts * kTileFlagWords +
+                              2 * kTileFlagWords;
+        while (nkt > 1) {
+          const int t = nkt - 1;
+          if (!((far[t >> 5] >> (t & 31)) & 1u)) break;
+          nkt = t;
+        }
+      }
+    }
+  }
+  const int last = nkt - 1;
   auto masked = [&](int t) -> bool {
     const uint32_t word = t < 32 ? mw[0] : t < 64 ? mw[1] : t < 96 ? mw[2] : mw[3];
     return (word >> (t & 31)) & 1u;

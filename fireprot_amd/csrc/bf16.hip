@@ -398,7 +398,7 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
   uint32_t mw[kTileFlagWords];
   uint32_t any = 0u, open = 0u;
   {
-    const uint32_t* f = a.tile_flags + (int64_t)b * 2 * kTileFlagWords;
+    const uint32_t* f = a.tile_flags + (int64_t)b * kTileFlagParts * kTileFlagWords;
 #pragma unroll
     for (int i = 0; i < kTileFlagWords; ++i) {
       const int lo = 32 * i;

@@ -32,7 +32,8 @@ size_t elem_bytes(int dtype) { return dtype == FPX_BF16 ? 2 : 4; }
 //   qh, kh [n][4][np][32]; vt [n][4][32][np]; gs [n][np][128]; og [n][n][128];
 //   tri_bias [4][np][np] (FP32: fragment order, twice: as is and scaled by
 //   log2(e)); mbias [n][np] float;
-//   tile flags [n][2 * kTileFlagWords] uint32
+//   tile flags [n][kTileFlagParts * kTileFlagWords] uint32, then the
+//   kMagnitudeWords words of the magnitude record
 struct BlockWorkspace {
   size_t qh, kh, vt, gs, og, bias, mbias, flags, total;
 };
@@ -46,7 +47,8 @@ BlockWorkspace block_workspace(int n, int dtype) {
   const size_t gate = seg((size_t)n * np * fpx::kHidden * e);
   const size_t bias = seg((size_t)fpx::kHeads * np * np * e * (dtype == FPX_F32 ? 2 : 1));
   const size_t mb = seg((size_t)n * np * sizeof(float));
-  const size_t fl = seg((size_t)n * 2 * fpx::kTileFlagWords * sizeof(uint32_t));
+  const size_t fl = seg(((size_t)n * fpx::kTileFlagParts * fpx::kTileFlagWords +
+                        fpx::kMagnitudeWords) * sizeof(uint32_t));
   BlockWorkspace w{};
   w.qh = 0;
   w.kh = w.qh + qkv;
@@ -71,6 +73,7 @@ struct BlockPointers {
   char *qh, *kh, *vt, *gs, *og, *tri;
   float* mbias;
   uint32_t* flags;
+  uint32_t* magnitudes;
   int np;
 };
 
@@ -86,6 +89,7 @@ BlockPointers block_pointers(void* workspace, int n, int dtype) {
   p.tri = base + ws.bias;
   p.mbias = reinterpret_cast<float*>(base + ws.mbias);
   p.flags = reinterpret_cast<uint32_t*>(base + ws.flags);
+  p.magnitudes = p.flags + (size_t)n * fpx::kTileFlagParts * fpx::kTileFlagWords;
   p.np = (int)round_up(n, kQueryTile);
   return p;
 }
@@ -172,7 +176,7 @@ int block_impl(int dtype, const void* z, int64_t z_stride0, int64_t z_stride1, c
 
 // Workspace of fpx_attn_strided, 256-byte aligned segments:
 //   bias [4][np][np] float in fragment order, twice (as is, scaled by log2(e));
-//   mbias [batch][np] float; tile flags [batch][2 * kTileFlagWords] uint32.
+//   mbias [batch][np] float; tile flags [batch][kTileFlagParts * kTileFlagWords] uint32.
 struct StridedWorkspace {
   size_t bias, bias_l2, mbias, flags, total;
 };
@@ -185,7 +189,8 @@ StridedWorkspace strided_workspace(int batch, int n) {
   w.bias_l2 = seg((size_t)fpx::kHeads * np * np * sizeof(float));
   w.mbias = 2 * w.bias_l2;
   w.flags = w.mbias + seg((size_t)batch * np * sizeof(float));
-  w.total = w.flags + seg((size_t)batch * 2 * fpx::kTileFlagWords * sizeof(uint32_t));
+  w.total = w.flags + seg((size_t)batch * fpx::kTileFlagParts * fpx::kTileFlagWords *
+                           sizeof(uint32_t));
   return w;
 }
 
@@ -260,7 +265,7 @@ int fpx_tri_attn_prepare(int dtype, const void* z, int64_t z_stride0, int64_t z_
   const int64_t ms_j = ending ? m_stride0 : m_stride1;
 
   hipError_t e = fpx::launch_mask_bias(mask, ms_i, ms_j, n, w.np, mask_inf, w.mbias, w.flags,
-                                       w.tri, dtype == FPX_BF16, s);
+                                       w.tri, dtype == FPX_BF16, w.magnitudes, s);
   if (e != hipSuccess) return status(e);
 
   const float q_scale = 1.0f / std::sqrt((float)fpx::kHeadDim);
@@ -310,6 +315,7 @@ int fpx_tri_attn_prepare(int dtype, const void* z, int64_t z_stride0, int64_t z_
   p.gs = as<float>(w.gs);
   p.tri_bias = as<float>(w.tri);
   p.tri_bias_l2 = as<float>(w.tri) + (size_t)fpx::kHeads * w.np * w.np;
+  p.magnitudes = w.magnitudes;
   p.np = w.np;
   return status(fpx::launch_projection(fpx::kProjBlock, p, s));
 }
@@ -347,6 +353,7 @@ int fpx_tri_attn_attend(int dtype, int n, void* workspace, size_t workspace_byte
   a.gate = as<float>(w.gs);
   a.out = as<float>(w.og);
   a.tile_flags = w.flags;
+  a.magnitudes = w.magnitudes;
   a.batch = n;
   a.n = n;
   a.np = w.np;

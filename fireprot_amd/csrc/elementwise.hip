@@ -11,25 +11,29 @@ namespace fpx {
 namespace {
 
 // One wavefront per row i < rows: mbias[i][k] for k < np and the row's tile
-// flags.  Word w of the first kTileFlagWords has bit t % 32 of tile t = 32w +
-// t % 32 set when some key of that 32-key tile has a nonzero mask bias (-0
-// counts as zero, since s + -0 == s); the next kTileFlagWords words do the
-// same for "every key of the tile has a nonzero mask bias".  Padded keys
-// (k >= n, -inf) count as masked.  kFromMask: the source is a {0, 1} mask and
+// flags.  Word w of part 0 (the first kTileFlagWords words) has bit t % 32 of
+// tile t = 32w + t % 32 set when some key of that 32-key tile has a nonzero
+// mask bias (-0 counts as zero, since s + -0 == s); part 1 does the same for
+// "every key of the tile has a nonzero mask bias", part 2 for "every key of
+// the tile has a mask bias <= -kSkipMask".  Padded keys (k >= n, -inf) count
+// as masked in all three.  kFromMask: the source is a {0, 1} mask and
 // inf * (mask - 1) is evaluated as two rounded fp32 ops, as the native
 // expression is (patches/protenix/0005-*.patch:36-39); otherwise the source
 // already holds mask-bias values and is copied.  np is a multiple of 64.
+// Work-group 0 also zeroes the magnitude record (nullable).
 template <bool kFromMask>
 __global__ __launch_bounds__(256) void mask_rows_kernel(const float* __restrict__ mask,
                                                         int64_t ms_i, int64_t ms_j, int rows,
                                                         int n, int np, float inf,
                                                         float* __restrict__ mbias,
-                                                        uint32_t* __restrict__ flags) {
+                                                        uint32_t* __restrict__ flags,
+                                                        uint32_t* __restrict__ magnitudes) {
+  if (magnitudes != nullptr && blockIdx.x == 0 && threadIdx.x < kMagnitudeWords)
+    magnitudes[threadIdx.x] = 0u;
   const int lane = threadIdx.x & 63;
   const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (i >= rows) return;
-  uint32_t any[kTileFlagWords] = {};
-  uint32_t all[kTileFlagWords] = {};
+  uint32_t part[kTileFlagParts][kTileFlagWords] = {};
   for (int k0 = 0; k0 < np; k0 += 64) {
     const int k = k0 + lane;
     float v = -INFINITY;
@@ -39,25 +43,26 @@ __global__ __launch_bounds__(256) void mask_rows_kernel(const float* __restrict_
     }
     mbias[(int64_t)i * np + k] = v;
     const uint64_t nz = __ballot(v != 0.0f);
-    const uint32_t lo = (uint32_t)nz;
-    const uint32_t hi = (uint32_t)(nz >> 32);
+    const uint64_t far = __ballot(v <= -kSkipMask);
     const int t = k0 >> 5;  // tiles t and t + 1 (t even)
-    const uint32_t any_bits = (uint32_t)(lo != 0u) | ((uint32_t)(hi != 0u) << 1);
-    const uint32_t all_bits = (uint32_t)(lo == ~0u) | ((uint32_t)(hi == ~0u) << 1);
+    const uint32_t bits[kTileFlagParts] = {
+        (uint32_t)((uint32_t)nz != 0u) | ((uint32_t)((nz >> 32) != 0u) << 1),
+        (uint32_t)((uint32_t)nz == ~0u) | ((uint32_t)((nz >> 32) == ~0u) << 1),
+        (uint32_t)((uint32_t)far == ~0u) | ((uint32_t)((far >> 32) == ~0u) << 1)};
 #pragma unroll
     for (int wd = 0; wd < kTileFlagWords; ++wd) {
       if (wd == (t >> 5)) {
-        any[wd] |= any_bits << (t & 31);
-        all[wd] |= all_bits << (t & 31);
+#pragma unroll
+        for (int pt = 0; pt < kTileFlagParts; ++pt) part[pt][wd] |= bits[pt] << (t & 31);
       }
     }
   }
-  uint32_t* dst = flags + (int64_t)i * 2 * kTileFlagWords;
+  uint32_t* dst = flags + (int64_t)i * kTileFlagParts * kTileFlagWords;
 #pragma unroll
-  for (int wd = 0; wd < kTileFlagWords; ++wd) {
-    if (lane == wd) dst[wd] = any[wd];
-    if (lane == kTileFlagWords + wd) dst[kTileFlagWords + wd] = all[wd];
-  }
+  for (int pt = 0; pt < kTileFlagParts; ++pt)
+#pragma unroll
+    for (int wd = 0; wd < kTileFlagWords; ++wd)
+      if (lane == pt * kTileFlagWords + wd) dst[pt * kTileFlagWords + wd] = part[pt][wd];
 }
 
 // Zero rows [n, np) of every head of the triangle bias (padded queries), in
@@ -192,11 +197,11 @@ __global__ __launch_bounds__(256) void sigmoid_mul_kernel(const f32x4* __restric
 
 hipError_t launch_mask_bias(const float* mask, int64_t ms_i, int64_t ms_j, int n, int np,
                             float inf, float* mbias, uint32_t* tile_flags, void* tri_bias,
-                            bool bias_bf16, hipStream_t stream) {
+                            bool bias_bf16, uint32_t* magnitudes, hipStream_t stream) {
   if (n <= 0) return hipSuccess;
   if (np % 64 || np > kTileFlagWords * 32 * 32) return hipErrorInvalidValue;
   hipLaunchKernelGGL(mask_rows_kernel<true>, dim3((uint32_t)((n + 3) / 4)), dim3(256), 0, stream,
-                     mask, ms_i, ms_j, n, n, np, inf, mbias, tile_flags);
+                     mask, ms_i, ms_j, n, n, np, inf, mbias, tile_flags, magnitudes);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || np == n) return e;
   const int64_t total = (int64_t)kHeads * (np - n) * np;
@@ -223,7 +228,7 @@ hipError_t launch_mask_rows(const float* values, int64_t vs_i, int64_t vs_k, int
   if (rows <= 0 || n <= 0) return hipSuccess;
   if (np % 64 || np < n || np > kTileFlagWords * 32 * 32) return hipErrorInvalidValue;
   hipLaunchKernelGGL(mask_rows_kernel<false>, dim3((uint32_t)((rows + 3) / 4)), dim3(256), 0,
-                     stream, values, vs_i, vs_k, rows, n, np, 0.0f, mbias, tile_flags);
+                     stream, values, vs_i, vs_k, rows, n, np, 0.0f, mbias, tile_flags, nullptr);
   return hipGetLastError();
 }
 

@@ -16,9 +16,13 @@ namespace fpx {
 //                q, k : [B][H][np][32]   (q pre-scaled by 1/sqrt(32))
 //                v    : [B][H][32][np]   (transposed per head)
 //                mbias: [B][np]          (required)
-//                tile_flags: [B][2][kTileFlagWords] bit t of part 0 = some
-//                        key of 32-key tile t has a nonzero mask bias; of
-//                        part 1 = every key of tile t has one
+//                tile_flags: [B][kTileFlagParts][kTileFlagWords] bit t of
+//                        part 0 = some key of 32-key tile t has a nonzero
+//                        mask bias; of part 1 = every key of tile t has one;
+//                        of part 2 = every key of tile t has a mask bias at
+//                        or below -kSkipMask
+//                magnitudes: nullable, kMagnitudeWords written by the
+//                        prepare projection (see ProjArgs::magnitudes)
 //                bias : [H][np][np] in fragment order (bias_frag_index)
 //                bias_l2: the same scaled by log2(e)
 //                gate : [B][np][128] sigmoid(g), multiplied in the epilogue
@@ -37,6 +41,22 @@ enum AttnLayout { kAttnBlock = 0, kAttnHeadLast = 1, kAttnStrided = 2 };
 
 // Words of per-row tile flags: 32-key tiles of np <= 4096 keys.
 constexpr int kTileFlagWords = 4;
+constexpr int kTileFlagParts = 3;
+
+// Trailing key tiles whose every mask bias is <= -kSkipMask are not visited
+// on rows that have an unmasked key, when the logit magnitude bound
+// B = 32 max|q| max|k| + max|bias| (q as stored, natural units) is below
+// kSkipBound and max|v| is finite.  Their weights are then exactly 0: a skipped key's log2-domain
+// logit lies at least (kSkipMask - 2 B) log2(e) - 56 > 7e8 below the row's
+// softmax reference, so exp2 underflows to 0 (bit-identical results).
+constexpr float kSkipMask = 536870912.0f;  // 2^29
+constexpr float kSkipBound = 67108864.0f;  // 2^26
+// Words of the magnitude record: max|q|, max|k|, max|v|, max|bias| as float
+// bits (atomicMax on non-negative floats; a NaN sorts above inf, so any
+// non-finite value disables the skip), then 1 once the projection wrote them.
+// A skipped key with a non-finite v would have made the native row NaN
+// (0 * inf), hence max|v| must be finite too.
+constexpr int kMagnitudeWords = 5;
 
 struct AttnArgs {
   const float* q;
@@ -51,6 +71,7 @@ struct AttnArgs {
   const float* gate;
   float* out;
   const uint32_t* tile_flags;
+  const uint32_t* magnitudes;  // kAttnBlock: nullable; enables the trailing-tile skip
   int64_t qs[3];  // kAttnStrided: (batch, head, row) element strides
   int64_t ks[3];
   int64_t vs[3];
@@ -102,6 +123,7 @@ struct ProjArgs {
   float* gs;
   float* tri_bias;     // fragment order (bias_frag_index)
   float* tri_bias_l2;  // the same scaled by log2(e)
+  uint32_t* magnitudes;  // nullable: max|q|, max|k|, max|v|, max|bias| (kMagnitudeWords)
   int np;
   // kProjQkv / kProjOut outputs
   float* out;
@@ -116,13 +138,14 @@ hipError_t launch_projection(int mode, const ProjArgs& args, hipStream_t stream)
 
 // -------------------------------------------------------------- elementwise
 // mbias[i][k] = k < n ? inf * (mask_x[i][k] - 1) : -inf  (0 for k < n when
-// mask is null), the per-row tile flags of the attention kernel, and zero
-// rows [n, np) of every head of the triangle bias: both float copies in
-// fragment order (bias_frag_index, unscaled then log2(e)-scaled, contiguous),
-// or the one bf16 copy (bias_frag_index_bf16) when bias_bf16.
+// mask is null), the per-row tile flags of the attention kernel, zero rows
+// [n, np) of every head of the triangle bias: both float copies in fragment
+// order (bias_frag_index, unscaled then log2(e)-scaled, contiguous), or the
+// one bf16 copy (bias_frag_index_bf16) when bias_bf16, and zero the
+// magnitude record (nullable) that the projection then fills.
 hipError_t launch_mask_bias(const float* mask, int64_t ms_i, int64_t ms_j, int n, int np,
                             float inf, float* mbias, uint32_t* tile_flags, void* tri_bias,
-                            bool bias_bf16, hipStream_t stream);
+                            bool bias_bf16, uint32_t* magnitudes, hipStream_t stream);
 
 // Staging for kAttnStrided.  launch_mask_rows: mbias[i][k] = values[i*vs_i +
 // k*vs_k] for k < n (0 when values is null), -inf for n <= k < np, and the

@@ -377,6 +377,16 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
     }
   }
 
+  // kProjBlock: running max |result| of this wave's group (q unscaled, k, v)
+  // and max |bias| of the values this lane stores, for the magnitude record.
+  float out_max = 0.f, bias_max = 0.f;
+  auto note = [&](const f32x16& r) {
+    if (MODE == kProjBlock && group < 3 && a.magnitudes != nullptr) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) out_max = __builtin_elementwise_maximum(out_max, __builtin_fabsf(r[e]));
+    }
+  };
+
   // Row loads in flight (LN mode: the tile after next).
   f32x8 stage_ln;
   f32x4 stage_vec[kLn ? 1 : kLoads];
@@ -456,6 +466,7 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
 
   auto store_bias = [&](float v, int i, int j0) {
     if (c16 < 2) {
+      bias_max = __builtin_elementwise_maximum(bias_max, __builtin_fabsf(v));
       const int j = j0 + lrow;
       const int64_t at = bias_frag_index(2 * slice + c16, i, j, a.np);
       a.tri_bias[at] = v;
@@ -548,8 +559,10 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
       *(f32x8*)&raw[lrow][8 * c16] = stage_ln;
       fetch_ln(stage_ln, next + 2 * streams);
       if (more) store_bias(bias, ni, nj0);
-      if (result_tile >= 0)
+      if (result_tile >= 0) {
+        note(result);
         store_tile<MODE>(a, result_tile, tiles_j, group, hw, col_w, col_bias, half, l32, result);
+      }
       __builtin_amdgcn_sched_barrier(0);
     };
 
@@ -566,8 +579,26 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
       tile = next;
       next += streams;
     }
-    if (!lead && tile - streams >= first)
+    if (!lead && tile - streams >= first) {
+      note(res);
       store_tile<MODE>(a, tile - streams, tiles_j, group, hw, col_w, col_bias, half, l32, res);
+    }
+    if (a.magnitudes != nullptr) {
+      // Wave maxima (NaN-propagating), one atomic per wave and record word.
+      float om = out_max, bm = bias_max;
+#pragma unroll
+      for (int d = 32; d >= 1; d >>= 1) {
+        om = __builtin_elementwise_maximum(om, __shfl_xor(om, d));
+        bm = __builtin_elementwise_maximum(bm, __shfl_xor(bm, d));
+      }
+      if (lane == 0) {
+        if (group < 3)
+          atomicMax(&a.magnitudes[group],
+                    __builtin_bit_cast(uint32_t, group == 0 ? om * a.q_scale : om));
+        atomicMax(&a.magnitudes[3], __builtin_bit_cast(uint32_t, bm));
+        if (blockIdx.x == 0 && w == 0) a.magnitudes[4] = 1u;
+      }
+    }
   } else {
     fetch(tile);
     stage_vecs(0);
