@@ -15,6 +15,7 @@
 // P operand is taken straight from the S^T registers: element e of MFMA m in
 // lane half hb is register 8m + e, i.e. key 16m + 8(e/4) + 4hb + e%4 of the
 // tile, and V^T is read with that same key order.
+#include "attn_common.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -264,35 +265,35 @@ hipError_t launch_proj_mode(const Bf16ProjArgs& a, hipStream_t stream, int wgs_p
 
 // ------------------------------------------------------------------- attention
 //
-// Same work-group shape and order as the FP32 kernel: (outer row b, head h,
-// 128 queries), four waves of 32 queries, 32-key tiles, K and V^T
-// double-buffered in LDS, one barrier per tile.  BF16 matrix instructions run
-// beside VALU work on gfx950, so the S^T MFMAs of the next tile are issued
-// before the softmax of this one, and the kernel is bound by its VALU work,
-// which v_exp_f32 (quarter rate, about 8 cycles per wave) dominates.  Per tile
-// a wave issues 6 MFMAs and about 67 VALU instructions:
-//   - The triangle bias (bf16, fragment-major) enters the S^T accumulator
-//     through two MFMAs with an identity A operand: I * Bias^T adds each bf16
-//     bias value exactly, with no conversion instructions.
-//   - Softmax: lazy running max (a rescale when a tile max exceeds it by
-//     2^8), p = exp2(fma(x, log2 e, -c)) with one rounded c per query, P
-//     packed to bf16 with v_cvt_pk_bf16_f32.  The row sum l adds the FP32
-//     weights (their bf16 roundings are unbiased, so O / l stays a weighted
-//     mean to well within the bf16 bar).
-// Rows whose keys are all masked form fl(fl(s + mask_bias) + bias) in FP32
-// in that order (the identity MFMAs add the bias last); other rows start the
-// accumulator from the bias and add the mask bias only on masked tiles.
+// Same work-group shape, order and pipeline as the FP32-accurate split kernel
+// (attention_split.hip): (outer row b, head h, 128 queries), four waves of 32
+// queries, 32-key tiles, K staged one tile ahead of V^T in LDS (both
+// double-buffered), the S^T MFMAs of tile t + 1 issued before the softmax of
+// tile t, one barrier per tile.  Per tile a wave issues 4 MFMAs (S^T and O^T,
+// two K-halves each) and about 60 VALU instructions.
+//   - The triangle bias enters as the start value of the S^T accumulator:
+//     its bf16 copy is held in the accumulator's lane and register order
+//     (bias_frag_index_bf16), loaded two tiles ahead with two 1 KB reads and
+//     widened to FP32 with one shift or mask per value (an FP32 copy doubles
+//     the bytes per tile, and the kernel then waits on its loads).
+//   - Rows with an unmasked key: p = exp2(fma(x, log2 e, -c)) with the FP32
+//     kernels' snapped reference c (0 while the row max lies within
+//     kSnap of it; rescaled only when a running sum passes kSumLimit), so a
+//     tile needs no max, no cross-lane exchange and no branch.  The mask
+//     bias is added on masked tiles only.  P is packed to bf16 with
+//     v_cvt_pk_bf16_f32; the row sum l adds the FP32 weights (their bf16
+//     roundings are unbiased, so O / l stays a weighted mean well within the
+//     bf16 bar).
+//   - Rows whose keys are all masked form fl(fl(s + mask_bias) + bias) in
+//     FP32 in that order, with a lazy running max (rescale when a tile max
+//     exceeds it by 2^8) and one rounded c per query.
 
-constexpr int kBq = 128;
-constexpr int kBk = 32;
 constexpr int kRowB = kHeadDim + 8;  // bf16 per LDS row: 80 bytes, conflict-free b128 reads
 constexpr int kThreads = 256;
-constexpr int kRowGroup = 8;
 constexpr int kMaxKeysB = kTileFlagWords * 32 * kBk;
-constexpr float kRescaleNatB = 8.0f * 0.69314718055994531f;
 
 typedef __bf16 KTileB[kBk][kRowB];      // [key][channel]
-typedef __bf16 VTileB[kHeadDim][kRowB];  // [channel][key position], see kVPos
+typedef __bf16 VTileB[kHeadDim][kRowB];  // [channel][key position], see v_position
 
 // V^T keys are stored in the order in which the S^T accumulator registers
 // hold them: within each 16-key block, keys 0-3, 8-11, 4-7, 12-15.  Position
@@ -308,29 +309,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_b(const __bf16* base, i
 }
 __device__ __forceinline__ bf16x4 buffer_b64(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
-}
-__device__ __forceinline__ bf16x8 buffer_b128(__amdgpu_buffer_rsrc_t r, uint32_t voff,
-                                              uint32_t soff) {
-  return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-}
-
-__device__ __forceinline__ float xor32_max_bf(float v) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v),
-                                                  __builtin_bit_cast(unsigned, v), false, false);
-  return __builtin_elementwise_maximum(__builtin_bit_cast(float, (unsigned)r[0]),
-                                       __builtin_bit_cast(float, (unsigned)r[1]));
-}
-
-__device__ __forceinline__ float max16_bf(const f32x16& s) {
-  auto mx = [](float x, float y) { return __builtin_elementwise_maximum(x, y); };
-  float m0 = mx(mx(s[0], s[1]), s[2]);
-  float m1 = mx(mx(s[3], s[4]), s[5]);
-  float m2 = mx(mx(s[6], s[7]), s[8]);
-  float m3 = mx(mx(s[9], s[10]), s[11]);
-  float m4 = mx(mx(s[12], s[13]), s[14]);
-  m0 = mx(mx(m0, m1), s[15]);
-  m2 = mx(mx(m2, m3), m4);
-  return mx(m0, m2);
 }
 
 __device__ __forceinline__ bf16x8 pack8(const f32x16& p, int m) {
@@ -381,20 +359,30 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
   const uint32_t ob = (uint32_t)lane * 16;
   auto load_k = [&](int t) { return buffer_b64(rk, ok, (uint32_t)t * 2048); };
   auto load_v = [&](int t) { return buffer_b64(rv, ov, (uint32_t)t * 64); };
-  struct BiasFrag {
-    bf16x8 m0, m1;
+  // Registers 0-7 and 8-15 of the lane's bias fragment as packed bf16 pairs.
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  struct BiasWords {
+    u32x4 lo, hi;
   };
-  auto load_bias = [&](int t) {
-    return BiasFrag{buffer_b128(rb, ob, (uint32_t)t * 2048),
-                    buffer_b128(rb, ob + 1024, (uint32_t)t * 2048)};
+  auto load_frag = [&](int t) -> BiasWords {
+    const uint32_t so = (uint32_t)t * 2048;
+    return BiasWords{__builtin_amdgcn_raw_buffer_load_b128(rb, ob, so, 0),
+                     __builtin_amdgcn_raw_buffer_load_b128(rb, ob + 1024, so, 0)};
+  };
+  auto widen = [](const BiasWords& bw) -> f32x16 {
+    f32x16 x;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = __builtin_bit_cast(float, bw.lo[i] << 16);
+      x[2 * i + 1] = __builtin_bit_cast(float, bw.lo[i] & 0xffff0000u);
+      x[8 + 2 * i] = __builtin_bit_cast(float, bw.hi[i] << 16);
+      x[8 + 2 * i + 1] = __builtin_bit_cast(float, bw.hi[i] & 0xffff0000u);
+    }
+    return x;
   };
   const int vpos = v_position(col4 >> 2);
-  auto store_kv = [&](int buf, bf16x4 k, bf16x4 v) {
-    *(bf16x4*)&Ks[buf][row8][col4] = k;
-    *(bf16x4*)&Vs[buf][row8][vpos] = v;
-  };
 
-  // Row classification, as in the FP32 kernel.
+  // Row classification, as in the FP32 kernels.
   uint32_t mw[kTileFlagWords];
   uint32_t any = 0u, open = 0u;
   {
@@ -417,89 +405,115 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
     const float* src = a.mbias + (int64_t)b * a.np;
     for (int k = 4 * tid; k < nkt * kBk; k += 4 * kThreads) *(f32x4*)&Ms[k] = *(const f32x4*)(src + k);
   }
-  auto add_mask = [&](f32x16& x, int t) {
+  auto mask_vals = [&](int t) -> f32x16 {
     const float* m = &Ms[t * kBk + 4 * half];
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const f32x4 mb = *(const f32x4*)(m + 8 * rr);
-      x[4 * rr + 0] += mb.x;
-      x[4 * rr + 1] += mb.y;
-      x[4 * rr + 2] += mb.z;
-      x[4 * rr + 3] += mb.w;
-    }
+    return cat4(*(const f32x4*)(m), *(const f32x4*)(m + 8), *(const f32x4*)(m + 16),
+                *(const f32x4*)(m + 24));
   };
 
-  // Constant operands: Q (B of S^T, lane holds Q[jq][16m + 8half + e]) and the
-  // identity (A of the bias MFMAs: key l32 against key 16m + 8half + e).
+  // Q, the B operand of S^T: lane holds Q[jq][16m + 8half + e].
   bf16x8 qf[2];
   {
     const __bf16* src = a.q + (bh * a.np + jq) * kHeadDim + 8 * half;
     qf[0] = *(const bf16x8*)(src);
     qf[1] = *(const bf16x8*)(src + 16);
   }
-  bf16x8 eye[2];
-#pragma unroll
-  for (int m = 0; m < 2; ++m)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) eye[m][e] = (__bf16)(l32 == 16 * m + 8 * half + e ? 1.0f : 0.0f);
 
   f32x16 o = {};
   float l_run = 0.f;
-  float m_ref = -INFINITY, m_thr = -INFINITY, c_ref = 0.f;
 
-  auto softmax = [&](const f32x16& x, bf16x8& p0, bf16x8& p1) {
-    const float mt = xor32_max_bf(max16_bf(x));
-    if (__any(mt > m_thr)) {
-      const float m_new = __builtin_elementwise_maximum(m_ref, mt);
-      const float c_new = m_new == -INFINITY ? 0.f : m_new * kLog2e;
-      const float alpha = m_ref == -INFINITY ? 0.f : exp2_fast(c_ref - c_new);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[r] *= alpha;
-      l_run *= alpha;
-      m_ref = m_new;
-      c_ref = c_new;
-      m_thr = m_new + kRescaleNatB;
-    }
-    f32x16 p;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) p[r] = exp2_fast(__builtin_fmaf(x[r], kLog2e, -c_ref));
-    float s4[4] = {p[0], p[1], p[2], p[3]};
-#pragma unroll
-    for (int r = 4; r < 16; ++r) s4[r & 3] += p[r];
-    l_run += (s4[0] + s4[1]) + (s4[2] + s4[3]);
-    p0 = pack8(p, 0);
-    p1 = pack8(p, 1);
-  };
-
-  // Software pipeline (BF16 MFMAs run beside VALU work): the S^T MFMAs of
-  // tile kt+1 are issued before the softmax of tile kt.  LDS holds K of tile
-  // kt+1 and V of tile kt during iteration kt; two bias sets alternate
-  // between even and odd tiles and are loaded two tiles ahead.
   auto run = [&](auto exact_tag) {
     constexpr bool kExact = decltype(exact_tag)::value;
     const f32x16 zero16 = {};
-    // S^T of tile t from Ks[buf]: fast rows start from the bias; exact rows
-    // get K Q^T only (the mask and then the bias follow in finish()).
-    auto scores = [&](int buf, const BiasFrag& bias) -> f32x16 {
+    // S^T of the tile in Ks[buf] added to x (the bias on the fast path).
+    auto scores = [&](int buf, f32x16 x) -> f32x16 {
       const bf16x8 k0 = *(const bf16x8*)&Ks[buf][l32][8 * half];
       const bf16x8 k1 = *(const bf16x8*)&Ks[buf][l32][16 + 8 * half];
-      f32x16 x = zero16;
-      if (!kExact) {
-        x = mfma_bf16(eye[0], bias.m0, x);
-        x = mfma_bf16(eye[1], bias.m1, x);
-      }
       x = mfma_bf16(k0, qf[0], x);
       return mfma_bf16(k1, qf[1], x);
     };
-    auto finish = [&](f32x16& x, const BiasFrag& bias, int t) {
+    // The rest of the logits of tile t (natural units): the mask bias on
+    // masked tiles (fast), or fl(fl(s + mask) + bias) (exact).
+    auto finish = [&](f32x16& x, int t) {
       if (kExact) {
-        add_mask(x, t);
-        x = mfma_bf16(eye[0], bias.m0, x);
-        x = mfma_bf16(eye[1], bias.m1, x);
+        const f32x16 mb = mask_vals(t);
+        const f32x16 bias = widen(load_frag(t));
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[r] = (x[r] + mb[r]) + bias[r];
       } else if (masked(t)) {
-        add_mask(x, t);
+        const f32x16 mb = mask_vals(t);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[r] += mb[r];
       }
     };
+
+    // Reference state of this lane's query (log2 units; see attention.hip).
+    float m_ref = -INFINITY;
+    float m_thr = -INFINITY;
+    float c_ref = 0.f;
+    bool has_ref = false;
+
+    auto softmax = [&](const f32x16& x, bf16x8& p0, bf16x8& p1) {
+      f32x16 p;
+      if (kExact) {
+        const float mt = xor32_max(max16(x));
+        if (__any(mt > m_thr)) {
+          const float m_new = __builtin_elementwise_maximum(m_ref, mt);
+          const float c_new = m_new == -INFINITY ? 0.f : m_new * kLog2e;
+          const float alpha = m_ref == -INFINITY ? 0.f : exp2_fast(c_ref - c_new);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[r] *= alpha;
+          l_run *= alpha;
+          m_ref = m_new;
+          c_ref = c_new;
+          m_thr = m_new + kRescaleNat;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[r] = exp2_fast(__builtin_fmaf(x[r], kLog2e, -c_ref));
+        l_run += sum16(p);
+        p0 = pack8(p, 0);
+        p1 = pack8(p, 1);
+        return;
+      }
+      float ovf = 0.f;
+      if (has_ref) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[r] = exp2_fast(__builtin_fmaf(x[r], kLog2e, -c_ref));
+        const float l_new = l_run + sum16(p);
+        const bool over = !(l_new <= kSumLimit);  // NaN or inf count as overflow
+        if (!__any(over)) {
+          l_run = l_new;
+          p0 = pack8(p, 0);
+          p1 = pack8(p, 1);
+          return;
+        }
+        ovf = over ? 1.f : 0.f;
+      }
+      // Rare path, taken by the whole wavefront (attention.hip), in log2 units.
+      const float mt = xor32_max(max16(x)) * kLog2e;
+      const bool fresh = m_ref == -INFINITY;
+      const bool need = fresh || xor32_max(ovf) > 0.f || mt > c_ref + kSnap;
+      m_ref = __builtin_elementwise_maximum(m_ref, mt);
+      const float snapped =
+          (m_ref == -INFINITY || (m_ref >= -kSnap && m_ref <= kSnap)) ? 0.f : m_ref;
+      const float c_new = fresh ? snapped
+                          : need ? __builtin_elementwise_maximum(snapped, c_ref + kLift)
+                                 : c_ref;
+      const float alpha = fresh ? 0.f : exp2_fast(c_ref - c_new);  // 1 when unchanged
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[r] *= alpha;
+      l_run *= alpha;
+      c_ref = c_new;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) p[r] = exp2_fast(__builtin_fmaf(x[r], kLog2e, -c_ref));
+      l_run += sum16(p);
+      has_ref = __all(m_ref != -INFINITY);
+      p0 = pack8(p, 0);
+      p1 = pack8(p, 1);
+    };
+
+    // O^T += V^T P^T for the tile in Vs[buf]; P comes straight from the
+    // S^T register order, which V^T's key positions follow.
     auto pv = [&](int buf, const bf16x8& p0, const bf16x8& p1) {
       const bf16x8 v0 = *(const bf16x8*)&Vs[buf][l32][8 * half];
       const bf16x8 v1 = *(const bf16x8*)&Vs[buf][l32][16 + 8 * half];
@@ -508,28 +522,36 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
     };
 
     // Prologue: K(0), K(1), V(0) into LDS; S^T(0); K(2), V(1) in flight.
-    BiasFrag bias_e = load_bias(0);
-    BiasFrag bias_o = load_bias(last < 1 ? last : 1);
-    store_kv(0, load_k(0), load_v(0));
+    // The fast path's bias words of tile t are loaded at iteration t - 3
+    // (two slots alternate) and widened when S^T(t) starts.
+    BiasWords bw_e{}, bw_o{};
+    if (!kExact) {
+      bw_e = load_frag(0);
+      bw_o = load_frag(last < 1 ? last : 1);
+    }
+    *(bf16x4*)&Ks[0][row8][col4] = load_k(0);
+    *(bf16x4*)&Vs[0][row8][vpos] = load_v(0);
     *(bf16x4*)&Ks[1][row8][col4] = load_k(last < 1 ? last : 1);
     bf16x4 kreg = load_k(last < 2 ? last : 2);
     bf16x4 vreg = load_v(last < 1 ? last : 1);
     __syncthreads();
-    f32x16 x_a = scores(0, bias_e);
-    finish(x_a, bias_e, 0);
-    bias_e = load_bias(last < 2 ? last : 2);
+    f32x16 x_a = scores(0, kExact ? zero16 : widen(bw_e));
+    if (!kExact) bw_e = load_frag(last < 2 ? last : 2);
+    finish(x_a, 0);
     __syncthreads();  // every wave is done with K(0) before Ks[0] is refilled
     f32x16 x_b;
 
-    // Iteration kt: Ks[(kt+1)&1] = K(kt+1), Vs[kt&1] = V(kt), cur = S^T(kt),
-    // bias_n = bias(kt+1); kreg = K(kt+2), vreg = V(kt+1) in flight.
-    auto body = [&](int kt, f32x16& cur, f32x16& nxt, BiasFrag& bias_n) {
-      nxt = scores((kt + 1) & 1, bias_n);
+    // Iteration kt: Ks[(kt+1)&1] = K(kt+1), Vs[kt&1] = V(kt); cur = logits
+    // of tile kt; bw = bias words of tile kt+1, refilled with tile kt+3;
+    // kreg = K(kt+2) and vreg = V(kt+1) in flight.  Indices past the last
+    // tile are clamped (in range, never used).
+    auto body = [&](int kt, f32x16& cur, f32x16& nxt, BiasWords& bw) {
+      nxt = scores((kt + 1) & 1, kExact ? zero16 : widen(bw));
+      if (!kExact) bw = load_frag(kt + 3 < last ? kt + 3 : last);
       bf16x8 p0, p1;
       softmax(cur, p0, p1);
       pv(kt & 1, p0, p1);
-      finish(nxt, bias_n, kt + 1);
-      bias_n = load_bias(kt + 3 < last ? kt + 3 : last);
+      finish(nxt, kt + 1);
       *(bf16x4*)&Ks[kt & 1][row8][col4] = kreg;
       *(bf16x4*)&Vs[(kt + 1) & 1][row8][vpos] = vreg;
       kreg = load_k(kt + 3 < last ? kt + 3 : last);
@@ -543,11 +565,11 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
     };
     int kt = 0;
     for (; kt + 2 < nkt; kt += 2) {
-      body(kt, x_a, x_b, bias_o);
-      body(kt + 1, x_b, x_a, bias_e);
+      body(kt, x_a, x_b, bw_o);
+      body(kt + 1, x_b, x_a, bw_e);
     }
     if (kt + 1 < nkt) {
-      body(kt, x_a, x_b, bias_o);
+      body(kt, x_a, x_b, bw_o);
       tail(x_b, kt + 1);
     } else {
       tail(x_a, kt);
@@ -559,12 +581,7 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
     run(std::true_type{});
   }
 
-  const float l_tot = __builtin_bit_cast(float, (unsigned)__builtin_amdgcn_permlane32_swap(
-                          __builtin_bit_cast(unsigned, l_run), __builtin_bit_cast(unsigned, l_run),
-                          false, false)[0]) +
-                      __builtin_bit_cast(float, (unsigned)__builtin_amdgcn_permlane32_swap(
-                          __builtin_bit_cast(unsigned, l_run), __builtin_bit_cast(unsigned, l_run),
-                          false, false)[1]);
+  const float l_tot = xor32_sum(l_run);
   if (jq < a.n) {
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {

@@ -31,7 +31,7 @@ size_t elem_bytes(int dtype) { return dtype == FPX_BF16 ? 2 : 4; }
 // (4 for FPX_F32, 2 for FPX_BF16; the mask bias is always float):
 //   qh, kh [n][4][np][32]; vt [n][4][32][np]; gs [n][np][128]; og [n][n][128];
 //   tri_bias [4][np][np] (FP32: fragment order, twice: as is and scaled by
-//   log2(e)); mbias [n][np] float;
+//   log2(e); BF16: bias_frag_index_bf16, once); mbias [n][np] float;
 //   tile flags [n][kTileFlagParts * kTileFlagWords] uint32, then the
 //   kMagnitudeWords words of the magnitude record
 struct BlockWorkspace {

@@ -130,16 +130,18 @@ __host__ __device__ __forceinline__ int64_t round_up(int64_t x, int64_t m) {
 // v_mfma_f32_32x32x2_f32 (lane = q%32 + 32*((k%32/4)%2), register
 // r = 4*(k%32/8) + k%4), so a wave loads its fragment with four coalesced
 // 1 KB reads.  np is the padded extent (a multiple of 32).
-// The BF16 block's bias copy: for every (head, 32-query tile, 32-key tile)
-// one contiguous 2 KB block holding, for MFMA m = (k%32)/16 and lane
-// q%32 + 32*((k%16)/8), the 8 consecutive keys 16m + 8*half .. +7 -- the B
-// operand of v_mfma_f32_32x32x16_bf16 -- so a wave loads it with two
-// coalesced 1 KB reads.
+// The BF16 block's bias copy (bf16-rounded values): for every (head, 32-query
+// tile, 32-key tile) one contiguous 2 KB block in the same lane and register
+// order as bias_frag_index, register r of lane l at (r / 8) * 512 + l * 8 +
+// r % 8, so a wave loads its fragment with two coalesced 1 KB reads and widens
+// each value to FP32 with one shift or mask.
 __host__ __device__ __forceinline__ int64_t bias_frag_index_bf16(int h, int q, int k, int np) {
   const int64_t nt = np >> 5;
   const int t = k & 31;
-  return (((int64_t)h * nt + (q >> 5)) * nt + (k >> 5)) * 1024 + (t >> 4) * 512 +
-         ((q & 31) + 32 * ((t >> 3) & 1)) * 8 + (t & 7);
+  const int lane = (q & 31) + 32 * ((t >> 2) & 1);
+  const int r = 4 * (t >> 3) + (t & 3);
+  return (((int64_t)h * nt + (q >> 5)) * nt + (k >> 5)) * 1024 + (r >> 3) * 512 + lane * 8 +
+         (r & 7);
 }
 
 __host__ __device__ __forceinline__ int64_t bias_frag_index(int h, int q, int k, int np) {

@@ -67,7 +67,7 @@ __global__ __launch_bounds__(256) void mask_rows_kernel(const float* __restrict_
 
 // Zero rows [n, np) of every head of the triangle bias (padded queries), in
 // the FP32 or the BF16 fragment order.
-template <typename BiasT, bool kFrag>
+template <typename BiasT>
 __global__ void bias_pad_kernel(int n, int np, BiasT* __restrict__ tri_bias) {
   const int64_t per_head = (int64_t)(np - n) * np;
   const int64_t total = kHeads * per_head;
@@ -77,8 +77,8 @@ __global__ void bias_pad_kernel(int n, int np, BiasT* __restrict__ tri_bias) {
     const int64_t r = idx % per_head;
     const int q = n + (int)(r / np);
     const int k = (int)(r % np);
-    tri_bias[kFrag ? bias_frag_index(h, q, k, np) : bias_frag_index_bf16(h, q, k, np)] =
-        (BiasT)0.0f;
+    tri_bias[sizeof(BiasT) == 4 ? bias_frag_index(h, q, k, np)
+                                : bias_frag_index_bf16(h, q, k, np)] = (BiasT)0.0f;
   }
 }
 
@@ -209,14 +209,14 @@ hipError_t launch_mask_bias(const float* mask, int64_t ms_i, int64_t ms_j, int n
   const int64_t cap = (int64_t)device_cu_count() * 16;
   if (blocks > cap) blocks = cap;
   if (bias_bf16) {
-    hipLaunchKernelGGL((bias_pad_kernel<__bf16, false>), dim3((uint32_t)blocks), dim3(256), 0,
-                       stream, n, np, static_cast<__bf16*>(tri_bias));
+    hipLaunchKernelGGL(bias_pad_kernel<__bf16>, dim3((uint32_t)blocks), dim3(256), 0, stream, n,
+                       np, static_cast<__bf16*>(tri_bias));
     return hipGetLastError();
   }
   float* copy = static_cast<float*>(tri_bias);
   for (int c = 0; c < 2; ++c) {
-    hipLaunchKernelGGL((bias_pad_kernel<float, true>), dim3((uint32_t)blocks), dim3(256), 0,
-                       stream, n, np, copy + (int64_t)c * kHeads * np * np);
+    hipLaunchKernelGGL(bias_pad_kernel<float>, dim3((uint32_t)blocks), dim3(256), 0, stream, n,
+                       np, copy + (int64_t)c * kHeads * np * np);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

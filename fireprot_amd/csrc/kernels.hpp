@@ -195,7 +195,7 @@ struct Bf16ProjArgs {
   __bf16* kh;
   __bf16* vt;
   __bf16* gs;
-  __bf16* tri_bias;
+  __bf16* tri_bias;  // fragment order (bias_frag_index_bf16)
   int np;
   __bf16* out;
   int64_t os_i;
