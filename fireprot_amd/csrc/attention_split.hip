@@ -18,6 +18,16 @@
 //   O^T += V^T P^T: two planes each, three terms (hi hi, hi lo, lo hi), a
 //     relative error below 2^-16 per weighted value.  6 MFMAs per tile.
 //
+// The block layout (kAttnBlock) takes q and k already split by the prepare
+// projection into fp16 (hi, lo) pairs, scaled per 32 x 32 tile by a power
+// of two so that the tile's max lies in [2^14, 2^15) (ProjArgs::planes):
+// 22 significant bits per value, so S^T = K Q^T needs only three terms
+// (hi hi, hi lo, lo hi) on v_mfma_f32_32x32x16_f16, 6 MFMAs per tile, with
+// an error at the level of an FP32 dot product.  The logit is then
+// fma(acc, log2(e) 2^-(e_q + e_k), bias) (exact scaling, one rounding).  V^T
+// arrives as bf16 (hi, lo) pairs.  The pairs are de-interleaved with v_perm
+// on their way into LDS, so no split happens in this kernel.
+//
 // The split: hi = bf16(x) (round to nearest), lo = bf16(x - hi), rest =
 // bf16(x - hi - lo).  Each difference is exact (Sterbenz), and x - hi - lo
 // keeps at most 8 significant bits, so hi + lo + rest == x for normal x.
@@ -44,7 +54,22 @@ constexpr int kThreads = 256;
 constexpr int kRowB = kHeadDim + 8;  // bf16 per LDS row: 80 bytes, conflict-free b128 reads
 constexpr int kMaxKeys = kTileFlagWords * 32 * kBk;
 
-typedef __bf16 KPlane[kBk][kRowB];       // [key][channel]
+typedef __bf16 KPlane[kBk][kRowB];       // [key][channel] (fp16 bits in the block layout)
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x16 mfma_f16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// Four (hi, lo) pair words -> the four hi and the four lo 16-bit values.
+__device__ __forceinline__ void unpair4(f32x4 words, bf16x4& hi, bf16x4& lo) {
+  const u32x4 w = __builtin_bit_cast(u32x4, words);
+  const u32x2 a = deinterleave_pairs(w.x, w.y), b = deinterleave_pairs(w.z, w.w);
+  hi = __builtin_bit_cast(bf16x4, u32x2{a.x, b.x});
+  lo = __builtin_bit_cast(bf16x4, u32x2{a.y, b.y});
+}
 typedef __bf16 VPlane[kHeadDim][kRowB];  // [channel][key position], see v_position
 
 // V^T keys are stored in the order in which the S^T accumulator registers
@@ -68,6 +93,7 @@ __global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a
   __shared__ __attribute__((aligned(16))) KPlane Ks[2][3];
   __shared__ __attribute__((aligned(16))) VPlane Vs[2][2];
   __shared__ __attribute__((aligned(16))) float Ms[kMaxKeys];
+  __shared__ float Sk[kTileFlagWords * 32];  // block layout: 2^-e_k of each key tile
 
   const uint32_t logical = xcd_remap(blockIdx.x, total);
   const int groups = (a.batch + kRowGroup - 1) / kRowGroup;
@@ -133,18 +159,23 @@ __global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a
   // channel row8, four consecutive columns).
   auto store_k = [&](int buf, f32x4 kv) {
     bf16x4 hi, lo, rest;
-    split3(kv, hi, lo, rest);
+    if constexpr (kBlock) {
+      unpair4(kv, hi, lo);  // fp16 pairs
+    } else {
+      split3(kv, hi, lo, rest);
+      *(bf16x4*)&Ks[buf][2][row8][col4] = rest;
+    }
     *(bf16x4*)&Ks[buf][0][row8][col4] = hi;
     *(bf16x4*)&Ks[buf][1][row8][col4] = lo;
-    *(bf16x4*)&Ks[buf][2][row8][col4] = rest;
   };
   auto store_v = [&](int buf, f32x4 vv) {
     bf16x4 hi, lo;
-    split2(vv, hi, lo);
     if constexpr (kBlock) {
+      unpair4(vv, hi, lo);  // bf16 pairs
       *(bf16x4*)&Vs[buf][0][row8][vpos] = hi;
       *(bf16x4*)&Vs[buf][1][row8][vpos] = lo;
     } else {
+      split2(vv, hi, lo);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         Vs[buf][0][col4 + e][kpos] = hi[e];
@@ -200,6 +231,15 @@ __global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a
     const float* src = a.mbias + (int64_t)b * a.mb_stride;
     for (int k = 4 * tid; k < nkt * kBk; k += 4 * kThreads) *(f32x4*)&Ms[k] = *(const f32x4*)(src + k);
   }
+  // Block layout: the product scale 2^-(e_q + e_k) of this wave's queries
+  // and each key tile (read after the prologue's first barrier).
+  float sq = 1.0f;
+  if constexpr (kBlock) {
+    const int64_t per = (int64_t)kHeads * nt;
+    const float* sc = a.scales + (int64_t)b * per + (int64_t)h * nt;
+    sq = sc[qt32];
+    for (int t = tid; t < nkt; t += kThreads) Sk[t] = sc[(int64_t)a.batch * per + t];
+  }
   auto mask_vals = [&](int t) -> f32x16 {
     const float* m = &Ms[t * kBk + 4 * half];
     return cat4(*(const f32x4*)(m), *(const f32x4*)(m + 8), *(const f32x4*)(m + 16),
@@ -213,14 +253,24 @@ __global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a
     constexpr bool kExact = decltype(exact_tag)::value;
     const f32x16 zero16 = {};
 
-    // Q planes, the B operand of S^T: lane holds Q[jq][16m + 8half + e],
+    // Q planes, the B operand of S^T: lane holds Q[jq][16m + 8half + e].
+    // Block layout: the fp16 (hi, lo) pairs of the prepare stage (the log2(e)
+    // of the fast path enters with the product scale); strided: split here,
     // scaled by log2(e) on the fast path.
     bf16x8 qh[2], ql[2], qr[2];
-    {
-      const bool ok_q = kBlock || jq < a.n;
-      const float* src = kBlock ? a.q + (bh * a.np + jq) * kHeadDim + 8 * half
-                                : a.q + b * a.qs[0] + h * a.qs[1] +
-                                      (int64_t)(ok_q ? jq : 0) * a.qs[2] + 8 * half;
+    if constexpr (kBlock) {
+      const f32x4* src = (const f32x4*)(a.q + (bh * a.np + jq) * kHeadDim + 8 * half);
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        bf16x4 h0, l0, h1, l1;
+        unpair4(src[4 * m], h0, l0);
+        unpair4(src[4 * m + 1], h1, l1);
+        qh[m] = bf16x8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+        ql[m] = bf16x8{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+      }
+    } else {
+      const bool ok_q = jq < a.n;
+      const float* src = a.q + b * a.qs[0] + h * a.qs[1] + (int64_t)(ok_q ? jq : 0) * a.qs[2] + 8 * half;
       const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
@@ -232,32 +282,52 @@ __global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a
       }
     }
 
-    // S^T of the tile in Ks[buf], added to x (the scaled bias on the fast
-    // path, zero on the exact path); the smallest terms first.
+    // S^T of the tile in Ks[buf], added to x (strided: the scaled bias on the
+    // fast path, zero on the exact path; block: zero); the smallest terms first.
     auto scores = [&](int buf, f32x16 x) -> f32x16 {
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
         const bf16x8 kh = *(const bf16x8*)&Ks[buf][0][l32][16 * m + 8 * half];
         const bf16x8 kl = *(const bf16x8*)&Ks[buf][1][l32][16 * m + 8 * half];
-        const bf16x8 kr = *(const bf16x8*)&Ks[buf][2][l32][16 * m + 8 * half];
-        x = mfma_bf16(kr, qh[m], x);
-        x = mfma_bf16(kh, qr[m], x);
-        x = mfma_bf16(kl, ql[m], x);
-        x = mfma_bf16(kl, qh[m], x);
-        x = mfma_bf16(kh, ql[m], x);
-        x = mfma_bf16(kh, qh[m], x);
+        if constexpr (kBlock) {
+          x = mfma_f16(kl, qh[m], x);
+          x = mfma_f16(kh, ql[m], x);
+          x = mfma_f16(kh, qh[m], x);
+        } else {
+          const bf16x8 kr = *(const bf16x8*)&Ks[buf][2][l32][16 * m + 8 * half];
+          x = mfma_bf16(kr, qh[m], x);
+          x = mfma_bf16(kh, qr[m], x);
+          x = mfma_bf16(kl, ql[m], x);
+          x = mfma_bf16(kl, qh[m], x);
+          x = mfma_bf16(kh, ql[m], x);
+          x = mfma_bf16(kh, qh[m], x);
+        }
       }
       return x;
     };
-    // The rest of the logits of tile t: the mask bias on masked tiles (fast,
-    // in log2 units), or fl(fl(s + mask) + bias) in natural units (exact).
-    auto finish = [&](f32x16& x, int t) {
+    // The logits of tile t from its product acc: the mask bias on masked
+    // tiles (fast, in log2 units), or fl(fl(s + mask) + bias) in natural
+    // units (exact).  Strided: acc already holds the fast path's bias; block:
+    // x holds the bias (fast) and acc the scaled product (s = acc 2^-(e_q + e_k),
+    // an exact scaling).
+    auto finish = [&](f32x16& x, const f32x16& acc, int t) {
+      float st = 1.0f;
+      if constexpr (kBlock) st = sq * Sk[t];
       if (kExact) {
         const f32x16 mb = mask_vals(t);
         const f32x16 bias = load_frag(rb, t);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) x[r] = (x[r] + mb[r]) + bias[r];
-      } else if (masked(t)) {
+        for (int r = 0; r < 16; ++r) x[r] = ((kBlock ? acc[r] * st : acc[r]) + mb[r]) + bias[r];
+        return;
+      }
+      if constexpr (kBlock) {
+        const float sl = st * kLog2e;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[r] = __builtin_fmaf(acc[r], sl, x[r]);
+      } else {
+        x = acc;
+      }
+      if (masked(t)) {
         const f32x16 mb = mask_vals(t);
 #pragma unroll
         for (int r = 0; r < 16; ++r) x[r] = __builtin_fmaf(mb[r], kLog2e, x[r]);
@@ -365,8 +435,7 @@ __global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a
     f32x4 kreg = load_k(last < 2 ? last : 2);
     f32x4 vreg = load_v(last < 1 ? last : 1);
     __syncthreads();
-    x_a = scores(0, x_a);
-    finish(x_a, 0);
+    finish(x_a, scores(0, kBlock || kExact ? zero16 : x_a), 0);
     __syncthreads();  // every wave is done with K(0) before Ks[0] is refilled
 
     // Iteration kt: Ks[(kt+1)&1] = K(kt+1), Vs[kt&1] = V(kt); cur = logits
@@ -374,11 +443,11 @@ __global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a
     // V(kt+1) in flight.  Indices past the last tile are clamped (in range,
     // never used).
     auto body = [&](int kt, f32x16& cur, f32x16& nxt) {
-      nxt = scores((kt + 1) & 1, nxt);
+      const f32x16 acc = scores((kt + 1) & 1, kBlock || kExact ? zero16 : nxt);
       bf16x8 ph[2], pl[2];
       softmax(cur, ph, pl);
       pv(kt & 1, ph, pl);
-      finish(nxt, kt + 1);
+      finish(nxt, acc, kt + 1);
       cur = init(kt + 2 < last ? kt + 2 : last);
       store_k(kt & 1, kreg);
       store_v((kt + 1) & 1, vreg);
@@ -438,6 +507,7 @@ hipError_t launch_attention_split(int layout, const AttnArgs& a, hipStream_t str
   if (total > 0x7fffffffull) return hipErrorInvalidValue;
   if (a.tile_flags == nullptr || a.bias_l2 == nullptr || nkt > kTileFlagWords * 32)
     return hipErrorInvalidValue;
+  if (layout == kAttnBlock && a.scales == nullptr) return hipErrorInvalidValue;
   if (layout == kAttnBlock) {
     hipLaunchKernelGGL(attention_split_kernel<kAttnBlock>, dim3((uint32_t)total), dim3(kThreads), 0,
                        stream, a, nqt, nkt, (uint32_t)total);

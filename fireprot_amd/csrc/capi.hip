@@ -33,9 +33,12 @@ size_t elem_bytes(int dtype) { return dtype == FPX_BF16 ? 2 : 4; }
 //   tri_bias [4][np][np] (FP32: fragment order, twice: as is and scaled by
 //   log2(e); BF16: bias_frag_index_bf16, once); mbias [n][np] float;
 //   tile flags [n][kTileFlagParts * kTileFlagWords] uint32, then the
-//   kMagnitudeWords words of the magnitude record
+//   kMagnitudeWords words of the magnitude record; scales [2][n][4][np / 32]
+//   float (the plane layout's per-tile inverse scales of q and k).
+// FP32 blocks on the BF16 matrix cores hold q, k and v^T in the plane layout
+// (ProjArgs::planes), in the same bytes as FP32 values.
 struct BlockWorkspace {
-  size_t qh, kh, vt, gs, og, bias, mbias, flags, total;
+  size_t qh, kh, vt, gs, og, bias, mbias, flags, scales, total;
 };
 
 BlockWorkspace block_workspace(int n, int dtype) {
@@ -58,7 +61,8 @@ BlockWorkspace block_workspace(int n, int dtype) {
   w.bias = w.og + g;
   w.mbias = w.bias + bias;
   w.flags = w.mbias + mb;
-  w.total = w.flags + fl;
+  w.scales = w.flags + fl;
+  w.total = w.scales + seg((size_t)2 * n * fpx::kHeads * (np / 32) * sizeof(float));
   return w;
 }
 
@@ -74,6 +78,7 @@ struct BlockPointers {
   float* mbias;
   uint32_t* flags;
   uint32_t* magnitudes;
+  float* scales;
   int np;
 };
 
@@ -90,6 +95,7 @@ BlockPointers block_pointers(void* workspace, int n, int dtype) {
   p.mbias = reinterpret_cast<float*>(base + ws.mbias);
   p.flags = reinterpret_cast<uint32_t*>(base + ws.flags);
   p.magnitudes = p.flags + (size_t)n * fpx::kTileFlagParts * fpx::kTileFlagWords;
+  p.scales = reinterpret_cast<float*>(base + ws.scales);
   p.np = (int)round_up(n, kQueryTile);
   return p;
 }
@@ -316,6 +322,7 @@ int fpx_tri_attn_prepare(int dtype, const void* z, int64_t z_stride0, int64_t z_
   p.tri_bias = as<float>(w.tri);
   p.tri_bias_l2 = as<float>(w.tri) + (size_t)fpx::kHeads * w.np * w.np;
   p.magnitudes = w.magnitudes;
+  p.scales = w.scales;
   p.np = w.np;
   return status(fpx::launch_projection(fpx::kProjBlock, p, s));
 }
@@ -354,6 +361,7 @@ int fpx_tri_attn_attend(int dtype, int n, void* workspace, size_t workspace_byte
   a.out = as<float>(w.og);
   a.tile_flags = w.flags;
   a.magnitudes = w.magnitudes;
+  a.scales = w.scales;
   a.batch = n;
   a.n = n;
   a.np = w.np;

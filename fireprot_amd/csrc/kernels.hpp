@@ -43,6 +43,10 @@ enum AttnLayout { kAttnBlock = 0, kAttnHeadLast = 1, kAttnStrided = 2 };
 constexpr int kTileFlagWords = 4;
 constexpr int kTileFlagParts = 3;
 
+// Per-tile exponent range of the fp16 planes: |e| <= kPlaneExpMax, so the
+// product scale 2^-(e_q + e_k) times log2(e) stays a normal float.
+constexpr int kPlaneExpMax = 63;
+
 // Trailing key tiles whose every mask bias is <= -kSkipMask are not visited
 // on rows that have an unmasked key, when the logit magnitude bound
 // B = 32 max|q| max|k| + max|bias| (q as stored, natural units) is below
@@ -72,6 +76,7 @@ struct AttnArgs {
   float* out;
   const uint32_t* tile_flags;
   const uint32_t* magnitudes;  // kAttnBlock: nullable; enables the trailing-tile skip
+  const float* scales;  // kAttnBlock: q, k, v in the plane layout (ProjArgs::planes), or null
   int64_t qs[3];  // kAttnStrided: (batch, head, row) element strides
   int64_t ks[3];
   int64_t vs[3];
@@ -124,6 +129,16 @@ struct ProjArgs {
   float* tri_bias;     // fragment order (bias_frag_index)
   float* tri_bias_l2;  // the same scaled by log2(e)
   uint32_t* magnitudes;  // nullable: max|q|, max|k|, max|v|, max|bias| (kMagnitudeWords)
+  // Plane layout of q, k, v^T (set by launch_projection for the split
+  // kernel; the FP32-matrix-core kernels keep plain FP32):
+  //   q, k: 32-bit word (j, c) of (i, h) holds the fp16 pair (hi, lo) of the
+  //         value times 2^e, e chosen per 32 x 32 (rows j, head channels)
+  //         tile so that the tile's max |value| 2^e lies in [2^14, 2^15);
+  //         hi = fp16(x 2^e) and lo = fp16(x 2^e - hi) carry 22 bits;
+  //   v^T:  word (c, j) holds the bf16 pair (hi, lo) of the value;
+  //   scales[(t * rows_i + i) * 4 + h][j / 32] = 2^-e for t = 0 (q), 1 (k).
+  int planes;
+  float* scales;
   int np;
   // kProjQkv / kProjOut outputs
   float* out;

@@ -54,7 +54,59 @@ __device__ __forceinline__ void store_tile(const ProjArgs& a, int tile, int tile
                                            const f32x16& acc) {
   const int i = tile / tiles_j;
   const int j0 = (tile % tiles_j) * kRows + 4 * half;
-  if (MODE == kProjBlock) {
+  if (MODE == kProjBlock && a.planes) {
+    // Plane layout (ProjArgs::planes): q, k as scaled fp16 (hi, lo) pairs
+    // with the tile's inverse scale, v^T as bf16 (hi, lo) pairs.
+    const int64_t bh = (int64_t)i * kHeads + hw;
+    uint32_t* words;
+    if (group == 0 || group == 1) {
+      const float scale = group == 0 ? a.q_scale : 1.0f;
+      // NaN-propagating max |value| of the 32 x 32 tile (scaling by a
+      // positive constant keeps the maximum)
+      float m = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) m = __builtin_elementwise_maximum(m, __builtin_fabsf(acc[r]));
+      m = wave_max(m) * scale;
+      // m 2^e in [2^14, 2^15); e = 0 for a zero or non-finite tile
+      int e = 0;
+      if (m > 0.f && m < INFINITY) {
+        e = 15 - __builtin_amdgcn_frexp_expf(m);
+        e = e < -kPlaneExpMax ? -kPlaneExpMax : e > kPlaneExpMax ? kPlaneExpMax : e;
+      }
+      // (acc * scale) 2^e == acc * (scale 2^e): one rounding either way
+      const float f = __builtin_ldexpf(scale, e);
+      words = reinterpret_cast<uint32_t*>(group == 0 ? a.qh : a.kh) + (bh * a.np + j0) * kHeadDim + l32;
+      typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const f32x2 x = {acc[r] * f, acc[r + 1] * f};
+        const f16x2 hi = __builtin_convertvector(x, f16x2);
+        const f16x2 lo = __builtin_convertvector(x - __builtin_convertvector(hi, f32x2), f16x2);
+        const u32x2 w = interleave_pairs(__builtin_bit_cast(uint32_t, hi), __builtin_bit_cast(uint32_t, lo));
+        words[(8 * (r >> 2) + (r & 3)) * kHeadDim] = w.x;
+        words[(8 * (r >> 2) + (r & 3) + 1) * kHeadDim] = w.y;
+      }
+      if (half == 0 && l32 == 0)
+        a.scales[(((int64_t)group * a.rows_i + i) * kHeads + hw) * (a.np >> 5) + tile % tiles_j] =
+            __builtin_ldexpf(1.0f, -e);
+    } else if (group == 2) {
+      words = reinterpret_cast<uint32_t*>(a.vt) + (bh * kHeadDim + l32) * a.np + j0;
+      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        bf16x4 hi, lo;
+        split2(f32x4{acc[4 * rr + 0], acc[4 * rr + 1], acc[4 * rr + 2], acc[4 * rr + 3]}, hi, lo);
+        const u32x2 h = __builtin_bit_cast(u32x2, hi), l = __builtin_bit_cast(u32x2, lo);
+        const u32x2 w0 = interleave_pairs(h.x, l.x), w1 = interleave_pairs(h.y, l.y);
+        *(u32x4*)(words + 8 * rr) = u32x4{w0.x, w0.y, w1.x, w1.y};
+      }
+    } else {
+      float* dst = a.gs + ((int64_t)i * a.np + j0) * kHidden + col_w;
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        dst[(8 * (r >> 2) + (r & 3)) * kHidden] = sigmoidf_(acc[r] + col_bias);
+    }
+  } else if (MODE == kProjBlock) {
     const int64_t bh = (int64_t)i * kHeads + hw;
     if (group == 0 || group == 1) {
       float* dst = (group == 0 ? a.qh : a.kh) + (bh * a.np + j0) * kHeadDim + l32;
@@ -585,12 +637,7 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
     }
     if (a.magnitudes != nullptr) {
       // Wave maxima (NaN-propagating), one atomic per wave and record word.
-      float om = out_max, bm = bias_max;
-#pragma unroll
-      for (int d = 32; d >= 1; d >>= 1) {
-        om = __builtin_elementwise_maximum(om, __shfl_xor(om, d));
-        bm = __builtin_elementwise_maximum(bm, __shfl_xor(bm, d));
-      }
+      const float om = wave_max(out_max), bm = wave_max(bias_max);
       if (lane == 0) {
         if (group < 3)
           atomicMax(&a.magnitudes[group],
@@ -653,10 +700,14 @@ hipError_t launch_mode(const ProjArgs& a, hipStream_t stream, int wgs_per_cu) {
 
 }  // namespace
 
-hipError_t launch_projection(int mode, const ProjArgs& a, hipStream_t stream) {
+hipError_t launch_projection(int mode, const ProjArgs& args, hipStream_t stream) {
+  ProjArgs a = args;
+  a.planes = 0;
   if (!fp32_matrix_cores_selected()) {
     switch (mode) {
       case kProjBlock:
+        if (a.scales == nullptr) return hipErrorInvalidValue;
+        a.planes = 1;
         return launch_split<kProjBlock>(a, stream);
       case kProjQkv:
         return launch_split<kProjQkv>(a, stream);

@@ -119,6 +119,30 @@ __device__ __forceinline__ void split2(f32x8 x, bf16x8& hi, bf16x8& lo) {
   lo = __builtin_bit_cast(bf16x8, u32x4{l[0], l[1], l[2], l[3]});
 }
 
+// (hi, lo) pair words of the plane layout: word = hi | lo << 16.  From the
+// packed pairs hi2 = (hi0, hi1) and lo2 = (lo0, lo1) to the words (w0, w1),
+// and back (v_perm_b32: selector byte k picks byte k of {src0, src1} with
+// src1 in bytes 0-3).
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u32x2 interleave_pairs(uint32_t hi2, uint32_t lo2) {
+  return u32x2{__builtin_amdgcn_perm(lo2, hi2, 0x05040100u),
+               __builtin_amdgcn_perm(lo2, hi2, 0x07060302u)};
+}
+// Returns (hi2, lo2).
+__device__ __forceinline__ u32x2 deinterleave_pairs(uint32_t w0, uint32_t w1) {
+  return u32x2{__builtin_amdgcn_perm(w1, w0, 0x05040100u),
+               __builtin_amdgcn_perm(w1, w0, 0x07060302u)};
+}
+
+// fp16 (hi, lo) pair word of x (|x| below 2^15 for full precision): hi =
+// fp16(x) (round to nearest), lo = fp16(x - hi); x - hi is exact.
+__device__ __forceinline__ uint32_t f16_pair_word(float x) {
+  const _Float16 hi = (_Float16)x;
+  const _Float16 lo = (_Float16)(x - (float)hi);
+  return (uint32_t)__builtin_bit_cast(uint16_t, hi) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
+}
+
 // Sum over each 16-lane row of the wave (DPP quad_perm [1,0,3,2] and
 // [2,3,0,1], row_half_mirror, row_mirror), returned in all 16 lanes.
 __device__ __forceinline__ float row16_sum(float v) {

@@ -48,11 +48,12 @@ def test_abi_version_and_workspace_sizes(lib):
         for dtype, e in ((0, 4), (1, 2)):
             copies = 2 if dtype == 0 else 1  # FP32: unscaled and log2(e)-scaled bias
             # q, k, v^T; gate (rows padded to np); gated output; bias; mask bias;
-            # tile flags (3 parts of 4 words per row) plus the 5-word magnitude record
+            # tile flags (3 parts of 4 words per row) plus the 5-word magnitude record;
+            # the q and k tiles' inverse scales of the plane layout
             expected = (3 * seg(n * 4 * np_ * 32 * e) + seg(n * np_ * 128 * e)
                         + seg(n * n * 128 * e)
                         + seg(4 * np_ * np_ * e * copies) + seg(n * np_ * 4)
-                        + seg((n * 12 + 5) * 4))
+                        + seg((n * 12 + 5) * 4) + seg(2 * n * 4 * (np_ // 32) * 4))
             assert lib.fpx_tri_attn_workspace_bytes(n, 128, 4, 32, dtype) == expected
     for bad in ((0, 128, 4, 32, 0), (4097, 128, 4, 32, 0), (64, 64, 4, 32, 0),
                 (64, 128, 8, 32, 0), (64, 128, 4, 16, 0), (64, 128, 4, 32, 7)):
