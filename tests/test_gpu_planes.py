@@ -1,0 +1,111 @@
+"""The plane layout the FP32 block's prepare stage writes for its attention.
+
+q and k are held as fp16 (hi, lo) pairs scaled by a power of two per 32 x 32
+tile (rows j, the head's 32 channels), so that the tile's max |value| times
+the scale lies in [2^14, 2^15); the workspace keeps the inverse scales.  v^T
+is held as bf16 (hi, lo) pairs.  Decoding the pairs must give the FP32
+projections back to 22 (q, k) and 16 (v) significant bits, and the scales
+must be the promised powers of two.  The layout is internal to the block's
+workspace; the offsets below restate the workspace segments (capi.hip).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from fireprot_amd import _native
+from fireprot_amd import block as hip_block
+from fireprot_amd import workloads
+from oracle import triangle_attention as oracle
+from tests.helpers import oracle_params
+
+pytestmark = pytest.mark.gpu
+
+
+def _seg(b: int) -> int:
+    return -(-b // 256) * 256
+
+
+def _offsets(n: int) -> dict:
+    np_ = -(-n // 128) * 128
+    qkv = _seg(n * 4 * np_ * 32 * 4)
+    o = {"np": np_, "qh": 0, "kh": qkv, "vt": 2 * qkv, "gs": 3 * qkv}
+    o["og"] = o["gs"] + _seg(n * np_ * 128 * 4)
+    o["bias"] = o["og"] + _seg(n * n * 128 * 4)
+    o["mbias"] = o["bias"] + _seg(4 * np_ * np_ * 4 * 2)
+    o["flags"] = o["mbias"] + _seg(n * np_ * 4)
+    o["scales"] = o["flags"] + _seg((n * 12 + 5) * 4)
+    return o
+
+
+def _f16_pairs(words: np.ndarray) -> np.ndarray:
+    hi = (words & 0xFFFF).astype(np.uint16).view(np.float16).astype(np.float64)
+    lo = (words >> 16).astype(np.uint16).view(np.float16).astype(np.float64)
+    return hi + lo
+
+
+def _bf16_pairs(words: np.ndarray) -> np.ndarray:
+    hi = ((words & 0xFFFF) << 16).astype(np.uint32).view(np.float32).astype(np.float64)
+    lo = (words & 0xFFFF0000).astype(np.uint32).view(np.float32).astype(np.float64)
+    return hi + lo
+
+
+@pytest.mark.parametrize("ending", [False, True])
+@pytest.mark.parametrize("scale", [1.0, 300.0, 1e-3])
+def test_prepare_planes_decode_to_the_projections(ending, scale):
+    n = 100
+    z = workloads.make_pair(n)
+    w = workloads.make_weights()
+    for key in ("w_q", "w_k", "w_v"):
+        w[key] = w[key] * scale
+    # a constant pair row: its normalised row is the LN bias, far smaller
+    # than the other rows of its tile (exercises the per-tile scale)
+    z[3, 7] = 5.0
+    weights = hip_block.BlockWeights.from_tensors(**w).to("cuda")
+    lib = _native.library()
+    ws_bytes = hip_block.workspace_bytes(n, torch.float32)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device="cuda")
+    zc = z.cuda()
+    code = lib.fpx_tri_attn_prepare(
+        0, zc.data_ptr(), zc.stride(0), zc.stride(1), None, 0, 0,
+        weights.ln_w.data_ptr() if weights.ln_w is not None else None,
+        weights.ln_b.data_ptr() if weights.ln_b is not None else None, weights.eps,
+        weights.w_qkvg.data_ptr(), None, weights.w_bias.data_ptr(), weights.inf, n, int(ending),
+        ws.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream)
+    _native.check(code, "fpx_tri_attn_prepare")
+    torch.cuda.synchronize()
+    raw = ws.cpu().numpy()
+    o = _offsets(n)
+    np_, nt = o["np"], o["np"] // 32
+
+    def words(start, count):
+        return raw[start:start + 4 * count].view(np.uint32)
+
+    scales = raw[o["scales"]:o["scales"] + 4 * 2 * n * 4 * nt].view(np.float32).reshape(2, n, 4, nt)
+    mant, _ = np.frexp(scales)
+    assert np.all(mant == 0.5), "scales must be powers of two"
+
+    params = oracle_params(w).to(torch.float64)
+    x = z.transpose(0, 1) if ending else z
+    xl = oracle.layer_norm(x.double(), params.ln_w, params.ln_b, params.eps)
+    eq, ek, ev = oracle.prep_qkv(xl, params, apply_scale=True)
+
+    for t, (seg, ref) in enumerate((("qh", eq), ("kh", ek))):
+        dec = _f16_pairs(words(o[seg], n * 4 * np_ * 32).reshape(n, 4, np_, 32))
+        tile_max = np.abs(dec).reshape(n, 4, nt, 32 * 32).max(axis=-1)
+        live = tile_max > 0
+        assert np.all((tile_max[live] >= 2.0 ** 14) & (tile_max[live] < 2.0 ** 15))
+        val = dec * np.repeat(scales[t], 32, axis=-1)[..., None]
+        refn = ref.numpy()
+        err = np.abs(val[:, :, :n] - refn).max()
+        bound = 2e-6 * np.abs(refn).max()
+        print(f"{seg} ending={ending} scale={scale}: max|err|={err:.3e} bound={bound:.3e}", flush=True)
+        assert err <= bound
+        assert np.all(val[:, :, n:] == 0), "padded rows must be zero"
+    vt = _bf16_pairs(words(o["vt"], n * 4 * 32 * np_).reshape(n, 4, 32, np_))
+    refv = ev.numpy().transpose(0, 1, 3, 2)
+    err = np.abs(vt[..., :n] - refv).max()
+    bound = 2e-5 * np.abs(refv).max()
+    print(f"v ending={ending} scale={scale}: max|err|={err:.3e} bound={bound:.3e}", flush=True)
+    assert err <= bound
