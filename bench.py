@@ -135,20 +135,28 @@ def visited_key_tiles(n: int, valid: int | None, skip: bool) -> int:
     return valid * (-(-valid // 32)) + (n - valid) * nkt
 
 
-def split_executed(batch: int, n: int, ms: float, tiles: int | None = None) -> dict:
-    """BF16 matrix-core work the split attention kernel executes for its
-    FP32-accurate products: per 32 x 32 (query x key) wave tile, 18
-    v_mfma_f32_32x32x16_bf16 (6 terms of S^T, 3 of O^T, two K-halves each) =
-    18 * 32768 flop, against 2 * 65536 algorithmic flop.  Query rows are
-    padded to 128, keys to 32.  ``tiles``: key tiles visited summed over the
-    outer rows (default: every tile of every row)."""
+def split_executed(batch: int, n: int, ms: float, tiles: int | None = None,
+                   fp16_planes: bool = False) -> dict:
+    """16-bit matrix-core work the split attention kernel executes for its
+    FP32-accurate products, per 32 x 32 (query x key) wave tile, counted in
+    32x32x16 MFMAs of 32768 flop each (two K-halves per product term)
+    against 2 * 65536 algorithmic flop:
+      - caller-supplied q/k/v (strided layout): 6 bf16 terms of S^T and 3 of
+        O^T = 18 MFMAs;
+      - the block's fp16 planes: 3 fp16 terms of S^T and 3 bf16 of O^T = 12.
+    fp16 and bf16 MFMAs share one dense peak.  Query rows are padded to 128,
+    keys to 32.  ``tiles``: key tiles visited summed over the outer rows
+    (default: every tile of every row)."""
     np_ = -(-n // 128) * 128
     nkt = -(-n // 32)
     visited = batch * nkt if tiles is None else tiles
-    executed = visited * 4 * (np_ // 32) * 18 * 32768
+    per_tile = 12 if fp16_planes else 18
+    executed = visited * 4 * (np_ // 32) * per_tile * 32768
     executed_tflops = executed / (ms * 1e-3) / 1e12
+    unit = ("fp16 (2-plane q, k scaled per tile) for S^T, bf16 (2-plane v, p) for O^T"
+            if fp16_planes else "bf16 (exact 3-plane split of K and Q, 2-plane V and P)")
     return {
-        "matrix_unit": "bf16 (exact 3-plane split of K and Q, 2-plane V and P)",
+        "matrix_unit": unit,
         "visited_key_tile_frac": round(visited / (batch * nkt), 4),
         "executed_flop_per_launch": executed,
         "executed_tflops": round(executed_tflops, 3),
@@ -759,7 +767,8 @@ def main() -> int:
     }
     if split:
         roofline.update(split_executed(n, n, stages["attend"],
-                                       visited_key_tiles(n, cfg.valid, skip=True)))
+                                       visited_key_tiles(n, cfg.valid, skip=True),
+                                       fp16_planes=True))
     result = {
         "metric": METRIC,
         "value": round(value, 3),
