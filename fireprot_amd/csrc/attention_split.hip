@@ -55,13 +55,7 @@ constexpr int kRowB = kHeadDim + 8;  // bf16 per LDS row: 80 bytes, conflict-fre
 constexpr int kMaxKeys = kTileFlagWords * 32 * kBk;
 
 typedef __bf16 KPlane[kBk][kRowB];       // [key][channel] (fp16 bits in the block layout)
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ f32x16 mfma_f16(bf16x8 a, bf16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
-                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-}
 
 // Four (hi, lo) pair words -> the four hi and the four lo 16-bit values.
 __device__ __forceinline__ void unpair4(f32x4 words, bf16x4& hi, bf16x4& lo) {

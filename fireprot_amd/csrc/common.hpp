@@ -79,6 +79,19 @@ __device__ __forceinline__ float wave_max(float v) {
   return mx(__builtin_bit_cast(float, (unsigned)s[0]), __builtin_bit_cast(float, (unsigned)s[1]));
 }
 
+// NaN-propagating maximum over each 32-lane half of the wave (lanes 0-31 and
+// 32-63 separately), returned in every lane of the half.
+__device__ __forceinline__ float half_max(float v) {
+  auto mx = [](float x, float y) { return __builtin_elementwise_maximum(x, y); };
+  v = mx(v, dpp<0xB1>(v));
+  v = mx(v, dpp<0x4E>(v));
+  v = mx(v, dpp<0x141>(v));
+  v = mx(v, dpp<0x140>(v));
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v),
+                                                  __builtin_bit_cast(unsigned, v), false, false);
+  return mx(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+}
+
 // Two-pass LayerNorm statistics of a 128-channel row held as two values per
 // lane.  Values are shifted by lane 0's first value before summing, so rows
 // with |mean| >> std (e.g. 1000 + 0.001*c) keep their digits: the centred

@@ -329,20 +329,27 @@ __global__ __launch_bounds__(ProjTraits<MODE>::kWaves * 64) void projection_kern
   }
 }
 
-// ------------------------------------------------ FP32-accurate, BF16 cores
+// ------------------------------------------------ FP32-accurate, fp16 cores
 //
-// The same projections with every FP32 operand split exactly into three
-// bfloat16 planes (split.hpp) and the six terms down to 2^-16 relative run on
-// v_mfma_f32_32x32x16_bf16: 48 of them per 32 x 32 tile over the 128 input
-// channels, against 64 v_mfma_f32_32x32x2_f32 of 8x less work each.  A
-// wave's three weight planes take 96 VGPRs, so a work-group covers only a
-// slice of the output columns: the block's 512 q/k/v/g columns (and the
-// 384 of kProjQkv) are cut into two slices of 8 (6) waves, one work-group
-// per CU, and the two work-groups of a slice pair run on the same XCD over
-// the same row tiles, so the second read of each row tile comes from L2.
-// Each slice normalises its rows itself (kProjBlock); slice s projects
-// triangle-bias heads 2s and 2s + 1.  Row tiles are split into the three
-// planes once, on their way into LDS.
+// The same projections on v_mfma_f32_32x32x16_f16 with every FP32 operand
+// held as scaled fp16 (hi, lo) planes (split.hpp): the three terms hi hi,
+// hi lo, lo hi take 24 MFMAs per 32 x 32 tile over the 128 input channels,
+// against 64 v_mfma_f32_32x32x2_f32 of 8x less work each, with an error per
+// product below an FP32 dot product's.  Scales are powers of two:
+//   - each weight column by 2^ew, its max |w| in [2^14, 2^15);
+//   - LN rows (kProjBlock) by one 2^ex per launch from the LN affine: the
+//     centred, normalised row has 2-norm sqrt(128), so |y_c| <= sqrt(128)
+//     |ln_w_c| + |ln_b_c|; ln_w and ln_b are pre-scaled, so the scaled row
+//     costs nothing;
+//   - other rows (kProjQkv, kProjOut) each by their own 2^er.
+// Results are scaled back with ldexp, exactly.  A wave's two weight planes
+// take 64 VGPRs and a work-group covers a slice of the output columns: the
+// block's 512 q/k/v/g columns (and the 384 of kProjQkv) are cut into two
+// slices of 8 (6) waves, one work-group per CU, and the two work-groups of a
+// slice pair run on the same XCD over the same row tiles, so the second read
+// of each row tile comes from L2.  Each slice normalises its rows itself
+// (kProjBlock); slice s projects triangle-bias heads 2s and 2s + 1.  Row
+// tiles are split into the planes once, on their way into LDS.
 template <int MODE>
 struct SplitTraits;
 template <>
@@ -377,9 +384,11 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
   static_assert(!kLn || NW * 4 == kRows, "LN mode: 4 rows per wave, 16 lanes per row");
   constexpr int kVecs = kRows * kChannels / 4;              // float4 per tile
   constexpr int kLoads = (kVecs + kThreads - 1) / kThreads; // kProjQkv, kProjOut
-  // Two row tiles of three planes: the MFMAs read one while the next is
+  // Two row tiles of two planes: the MFMAs read one while the next is
   // normalised and split into the other, so a tile needs one barrier.
-  __shared__ __attribute__((aligned(16))) XPlane xs[2][3];
+  __shared__ __attribute__((aligned(16))) XPlane xs[2][2];
+  // kProjQkv, kProjOut: each staged row's plane exponent er.
+  __shared__ __attribute__((aligned(16))) int rexp[2][kRows];
   // LN mode: raw rows of the next tile.  Each wave reads and rewrites only
   // its own rows, so the buffer needs no barrier of its own.
   __shared__ __attribute__((aligned(16))) float raw[kLn ? kRows : 1][kChannels + 4];
@@ -399,16 +408,29 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
   const int hw = cb & 3;
 
   // Weight planes: B[k][col] for col = 32*hw + l32 of group `group`, lane
-  // holding channels 16t + 8*half + e of k step t.
-  bf16x8 wh[8], wl[8], wr[8];
+  // holding channels 16t + 8*half + e of k step t, scaled by 2^ew (the
+  // column's max |w| over both halves of the wave).
+  bf16x8 wh[8], wl[8];
+  int ew;
   {
     const float* src = a.w[group] + (int64_t)(32 * hw + l32) * kChannels + 8 * half;
+    f32x8 wv[8];
+    float m = 0.f;
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       const f32x4 u = *(const f32x4*)(src + 16 * t);
       const f32x4 v = *(const f32x4*)(src + 16 * t + 4);
-      split3(f32x8{u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w}, wh[t], wl[t], wr[t]);
+      wv[t] = f32x8{u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) m = __builtin_elementwise_maximum(m, __builtin_fabsf(wv[t][e]));
     }
+    const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, m),
+                                                     __builtin_bit_cast(unsigned, m), false, false);
+    m = __builtin_elementwise_maximum(__builtin_bit_cast(float, (unsigned)sw[0]),
+                                      __builtin_bit_cast(float, (unsigned)sw[1]));
+    ew = plane_exp(m);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) split_f16(ldexp8(wv[t], ew), wh[t], wl[t]);
   }
   const int col_w = MODE == kProjOut ? 32 * w + l32 : 32 * hw + l32;
   const float col_bias = (MODE != kProjQkv && a.b_g != nullptr) ? a.b_g[col_w] : 0.f;
@@ -419,14 +441,23 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
   const int c16 = lane & 15;
   const int lrow = 4 * w + (lane >> 4);
   f32x8 lnw, lnb, wb0, wb1;
+  int ex = 0;  // LN mode: plane exponent of every row
   if constexpr (kLn) {
+    float bound = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       lnw[e] = a.ln_w ? a.ln_w[8 * c16 + e] : 1.f;
       lnb[e] = a.ln_b ? a.ln_b[8 * c16 + e] : 0.f;
       wb0[e] = a.w_bias[(2 * slice) * kChannels + 8 * c16 + e];
       wb1[e] = a.w_bias[(2 * slice + 1) * kChannels + 8 * c16 + e];
+      bound = __builtin_elementwise_maximum(
+          bound, 11.3137085f * __builtin_fabsf(lnw[e]) + __builtin_fabsf(lnb[e]));
     }
+    // |y_c| <= sqrt(128) |ln_w_c| + |ln_b_c| up to FP32 rounding (< 1e-5
+    // relative); the margin keeps |y| 2^ex below 2^15.
+    ex = plane_exp(wave_max(bound) * (1.0f + 0x1p-10f));
+    lnw = ldexp8(lnw, ex);
+    lnb = ldexp8(lnb, ex);
   }
 
   // kProjBlock: running max |result| of this wave's group (q unscaled, k, v)
@@ -496,15 +527,16 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
   // Normalises, splits and writes the staged rows into planes `buf`;
   // returns this lane's triangle-bias value (head 2*slice + c16 for c16 < 2,
   // 0 for rows past rows_j), stored later by store_bias.
+  // The normalised row comes out scaled by 2^ex (ln_w, ln_b pre-scaled):
+  // every rounding of y and of the bias sum scales with it exactly.
   auto stage_split = [&](int buf, const f32x8& d, float rstd, int j0) -> float {
     const bool valid = j0 + lrow < a.rows_j;
     f32x8 y = d * rstd * lnw + lnb;
     if (!valid) y = f32x8{};
-    bf16x8 hi, lo, rest;
-    split3(y, hi, lo, rest);
+    bf16x8 hi, lo;
+    split_f16(y, hi, lo);
     *(bf16x8*)&xs[buf][0][lrow][8 * c16] = hi;
     *(bf16x8*)&xs[buf][1][lrow][8 * c16] = lo;
-    *(bf16x8*)&xs[buf][2][lrow][8 * c16] = rest;
     float p0 = 0.f, p1 = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -513,7 +545,7 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
     }
     p0 = row16_sum(p0);
     p1 = row16_sum(p1);
-    return c16 == 0 ? p0 : p1;
+    return __builtin_ldexpf(c16 == 0 ? p0 : p1, -ex);
   };
 
   auto store_bias = [&](float v, int i, int j0) {
@@ -526,35 +558,62 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
     }
   };
 
+  // A row's 32 float4 sit in one 32-lane half of a wave (whole waves skip
+  // the idx >= kVecs slots), so the row max is a half-wave reduction.
   auto stage_vecs = [&](int buf) {
 #pragma unroll
     for (int t = 0; t < kLoads; ++t) {
       const int idx = tid + t * kThreads;
       if (idx < kVecs) {
-        bf16x4 hi, lo, rest;
-        split3(stage_vec[t], hi, lo, rest);
+        const f32x4 x = stage_vec[t];
+        const float m = half_max(__builtin_elementwise_maximum(
+            __builtin_elementwise_maximum(__builtin_fabsf(x.x), __builtin_fabsf(x.y)),
+            __builtin_elementwise_maximum(__builtin_fabsf(x.z), __builtin_fabsf(x.w))));
+        const int er = plane_exp(m);
+        bf16x4 hi, lo;
+        split_f16(ldexp4(x, er), hi, lo);
         const int row = idx >> 5;
         const int c4 = (idx & 31) * 4;
         *(bf16x4*)&xs[buf][0][row][c4] = hi;
         *(bf16x4*)&xs[buf][1][row][c4] = lo;
-        *(bf16x4*)&xs[buf][2][row][c4] = rest;
+        if ((idx & 31) == 0) rexp[buf][row] = er;
       }
     }
   };
 
+  // Scales a wave's 32 x 32 result back: ldexp by -(row exponent + ew).
+  auto unscale = [&](f32x16 r, int buf) -> f32x16 {
+    if constexpr (kLn) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) r[e] = __builtin_ldexpf(r[e], -(ex + ew));
+    } else {
+      typedef int i32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const i32x4 er = *(const i32x4*)&rexp[buf][8 * rr + 4 * half];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[4 * rr + e] = __builtin_ldexpf(r[4 * rr + e], -(er[e] + ew));
+      }
+    }
+    return r;
+  };
+
   // One 16-deep k step of the 32 x 32 tile, A[row][k] = the row planes; two
-  // accumulation chains so consecutive MFMAs do not wait on each other.
+  // accumulation chains, swapped every step, so consecutive MFMAs do not
+  // wait on each other.
   auto mfma_step = [&](int buf, int t, f32x16& c0, f32x16& c1) {
     const int k = 16 * t + 8 * half;
     const bf16x8 xh = *(const bf16x8*)&xs[buf][0][l32][k];
     const bf16x8 xl = *(const bf16x8*)&xs[buf][1][l32][k];
-    const bf16x8 xr = *(const bf16x8*)&xs[buf][2][l32][k];
-    c0 = mfma_bf16(xh, wh[t], c0);
-    c1 = mfma_bf16(xh, wl[t], c1);
-    c0 = mfma_bf16(xl, wh[t], c0);
-    c1 = mfma_bf16(xl, wl[t], c1);
-    c0 = mfma_bf16(xr, wh[t], c0);
-    c1 = mfma_bf16(xh, wr[t], c1);
+    if (t & 1) {
+      c1 = mfma_f16(xh, wh[t], c1);
+      c0 = mfma_f16(xh, wl[t], c0);
+      c1 = mfma_f16(xl, wh[t], c1);
+    } else {
+      c0 = mfma_f16(xh, wh[t], c0);
+      c1 = mfma_f16(xh, wl[t], c1);
+      c0 = mfma_f16(xl, wh[t], c0);
+    }
   };
 
   __builtin_amdgcn_s_waitcnt(0);
@@ -592,7 +651,7 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
       f32x16 c0 = {}, c1 = {};
 #pragma unroll
       for (int t = 0; t < 8; ++t) mfma_step(buf, t, c0, c1);
-      return c0 + c1;
+      return unscale(c0 + c1, buf);
     };
     // Normalises T_{k+1} (when it exists) into planes buf ^ 1, then issues
     // the wave's global accesses; `result`/`result_tile` are stored last.
@@ -659,7 +718,7 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
         stage_vecs(buf ^ 1);
         if (next + streams < ntiles) fetch(next + streams);
       }
-      store_tile<MODE>(a, tile, tiles_j, group, hw, col_w, col_bias, half, l32, c0 + c1);
+      store_tile<MODE>(a, tile, tiles_j, group, hw, col_w, col_bias, half, l32, unscale(c0 + c1, buf));
       __syncthreads();
       tile = next;
       next += streams;

@@ -143,6 +143,67 @@ __device__ __forceinline__ uint32_t f16_pair_word(float x) {
          ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
 }
 
+// v_mfma_f32_32x32x16_f16 on fp16 bit patterns held in bf16x8 vectors (the
+// planes share one storage type); the operand and result layouts are those
+// of the bf16 instruction.
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ f32x16 mfma_f16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// Scaled fp16 planes.  A block of values whose max |x| is m is scaled by
+// 2^e, e = plane_exp(m), so that m 2^e lies in [2^14, 2^15), and split into
+// hi = fp16(x 2^e) and lo = fp16(x 2^e - hi) (round to nearest even; the
+// difference is exact).  hi + lo keeps about 22 significant bits, and the
+// three terms hi hi, hi lo, lo hi of a product leave a relative error of
+// about 2^-22 per product term; values far below the block's max keep an
+// absolute error below 2^-25 of the scaled unit.  The scaling is a power of
+// two (ldexp), so it and its inverse are exact.  e = 0 for a zero or
+// non-finite m (NaN and infinities then reach the products unscaled).
+__device__ __forceinline__ int plane_exp(float m) {
+  return (m > 0.f && m < INFINITY) ? 15 - __builtin_amdgcn_frexp_expf(m) : 0;
+}
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+template <int N>
+__device__ __forceinline__ void split_f16_words(const float* x, uint32_t* hi, uint32_t* lo) {
+  f32x2 r[N / 2];
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+    const f32x2 v = {x[2 * i], x[2 * i + 1]};
+    const f16x2 h = __builtin_convertvector(v, f16x2);
+    hi[i] = __builtin_bit_cast(uint32_t, h);
+    r[i] = v - __builtin_convertvector(h, f32x2);
+  }
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) lo[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(r[i], f16x2));
+}
+// Already scaled values -> fp16 hi and lo planes (bit patterns in bf16x8/x4).
+__device__ __forceinline__ void split_f16(f32x8 x, bf16x8& hi, bf16x8& lo) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const float v[8] = {x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]};
+  uint32_t h[4], l[4];
+  split_f16_words<8>(v, h, l);
+  hi = __builtin_bit_cast(bf16x8, u32x4{h[0], h[1], h[2], h[3]});
+  lo = __builtin_bit_cast(bf16x8, u32x4{l[0], l[1], l[2], l[3]});
+}
+__device__ __forceinline__ void split_f16(f32x4 x, bf16x4& hi, bf16x4& lo) {
+  const float v[4] = {x.x, x.y, x.z, x.w};
+  uint32_t h[2], l[2];
+  split_f16_words<4>(v, h, l);
+  hi = __builtin_bit_cast(bf16x4, u32x2{h[0], h[1]});
+  lo = __builtin_bit_cast(bf16x4, u32x2{l[0], l[1]});
+}
+__device__ __forceinline__ f32x8 ldexp8(f32x8 x, int e) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = __builtin_ldexpf(x[i], e);
+  return x;
+}
+__device__ __forceinline__ f32x4 ldexp4(f32x4 x, int e) {
+  return f32x4{__builtin_ldexpf(x.x, e), __builtin_ldexpf(x.y, e), __builtin_ldexpf(x.z, e),
+               __builtin_ldexpf(x.w, e)};
+}
+
 // Sum over each 16-lane row of the wave (DPP quad_perm [1,0,3,2] and
 // [2,3,0,1], row_half_mirror, row_mirror), returned in all 16 lanes.
 __device__ __forceinline__ float row16_sum(float v) {
