@@ -19,14 +19,17 @@
 //     relative error below 2^-16 per weighted value.  6 MFMAs per tile.
 //
 // The block layout (kAttnBlock) takes q and k already split by the prepare
-// projection into fp16 (hi, lo) pairs, scaled per 32 x 32 tile by a power
+// projection into fp16 hi and lo planes, scaled per 32 x 32 tile by a power
 // of two so that the tile's max lies in [2^14, 2^15) (ProjArgs::planes):
 // 22 significant bits per value, so S^T = K Q^T needs only three terms
 // (hi hi, hi lo, lo hi) on v_mfma_f32_32x32x16_f16, 6 MFMAs per tile, with
 // an error at the level of an FP32 dot product.  The logit is then
 // fma(acc, log2(e) 2^-(e_q + e_k), bias) (exact scaling, one rounding).  V^T
-// arrives as bf16 (hi, lo) pairs.  The pairs are de-interleaved with v_perm
-// on their way into LDS, so no split happens in this kernel.
+// arrives as bf16 hi and lo planes with its keys already in accumulator
+// order.  Each key tile's four 2 KB planes go straight from global memory
+// into a ring of LDS stages (global_load_lds_dwordx4, no registers), two
+// tiles ahead of use, with 16-byte chunks swizzled so the operand reads are
+// free of bank conflicts; no split happens in this kernel.
 //
 // The split: hi = bf16(x) (round to nearest), lo = bf16(x - hi), rest =
 // bf16(x - hi - lo).  Each difference is exact (Sterbenz), and x - hi - lo
@@ -52,18 +55,49 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kRowB = kHeadDim + 8;  // bf16 per LDS row: 80 bytes, conflict-free b128 reads
-constexpr int kMaxKeys = kTileFlagWords * 32 * kBk;
+
+// Block layout ring: stage s holds one key tile as four 2 KB planes (K hi,
+// K lo, V^T hi, V^T lo), each 32 rows of 64 bytes.  Tile t sits in stage
+// t % kStages and is loaded two iterations before its S^T.
+constexpr int kStages = 4;
+constexpr int kPlaneBytes = 2048;
+constexpr int kStageBytes = 4 * kPlaneBytes;
+// 16-byte chunk c of plane row r sits at chunk c ^ swz(r).  The operand
+// reads (rows 0-31, one chunk per instruction and half-wave) then hit
+// distinct banks in every group of 8 rows at 128 bytes per cycle and of 16
+// rows at 256 bytes per cycle.
+__device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
+// Waves per SIMD: the block layout fits four work-groups per CU (ring and
+// mask row within 40 KB of LDS at N <= 1536).
+template <int LAYOUT>
+constexpr int kWavesPerEu = LAYOUT == kAttnBlock ? 4 : 3;
+
+// One global_load_lds_dwordx4: lane l copies 16 bytes from src into the LDS
+// at dst + 16 l (dst uniform across the wave).  Written as inline assembly
+// so the compiler does not see an LDS write it cannot tell apart from the
+// stages being read, which would make it wait for every copy before the next
+// LDS read; the kernel waits for the copies itself (wait_vmcnt).  Loads the
+// compiler issues before or after stay correctly waited for, since vector
+// memory loads retire in issue order.
+__device__ __forceinline__ void lds_dma16(const void* src, const uint8_t* dst) {
+  const uint32_t lds_addr =
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)dst;
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(lds_addr)
+               : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 
 typedef __bf16 KPlane[kBk][kRowB];       // [key][channel] (fp16 bits in the block layout)
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// Four (hi, lo) pair words -> the four hi and the four lo 16-bit values.
-__device__ __forceinline__ void unpair4(f32x4 words, bf16x4& hi, bf16x4& lo) {
-  const u32x4 w = __builtin_bit_cast(u32x4, words);
-  const u32x2 a = deinterleave_pairs(w.x, w.y), b = deinterleave_pairs(w.z, w.w);
-  hi = __builtin_bit_cast(bf16x4, u32x2{a.x, b.x});
-  lo = __builtin_bit_cast(bf16x4, u32x2{a.y, b.y});
-}
 typedef __bf16 VPlane[kHeadDim][kRowB];  // [channel][key position], see v_position
 
 // V^T keys are stored in the order in which the S^T accumulator registers
@@ -81,12 +115,17 @@ __device__ __forceinline__ int v_position(int g) {
 // -inf), and V rows are transposed into the V^T planes on their way to LDS.
 // Both read the staged bias copies, mask rows and tile flags.
 template <int LAYOUT>
-__global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a, int nqt, int nkt_all,
-                                                                      uint32_t total) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kWavesPerEu<LAYOUT>, 4)))
+void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
   constexpr bool kBlock = LAYOUT == kAttnBlock;
-  __shared__ __attribute__((aligned(16))) KPlane Ks[2][3];
-  __shared__ __attribute__((aligned(16))) VPlane Vs[2][2];
-  __shared__ __attribute__((aligned(16))) float Ms[kMaxKeys];
+  // Block layout: the ring of key tiles (kStages x kStageBytes).  Strided
+  // layout: two register-staged tiles, K in three planes and V^T in two.
+  constexpr int kLdsBytes = kBlock ? kStages * kStageBytes : (int)(6 * sizeof(KPlane) + 4 * sizeof(VPlane));
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
+  auto& Ks = *reinterpret_cast<KPlane(*)[2][3]>(lds);
+  auto& Vs = *reinterpret_cast<VPlane(*)[2][2]>(lds + 6 * sizeof(KPlane));
+  // Mask-bias row of this outer row, nkt_all * kBk floats (dynamic).
+  extern __shared__ __attribute__((aligned(16))) float Ms[];
   __shared__ float Sk[kTileFlagWords * 32];  // block layout: 2^-e_k of each key tile
 
   const uint32_t logical = xcd_remap(blockIdx.x, total);
@@ -109,7 +148,6 @@ __global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a
   const int qt32 = (j0 >> 5) + w;
   const int row8 = tid >> 3;
   const int col4 = (tid & 7) * 4;
-  const int vpos = v_position(col4 >> 2);
 
   // Per-work-group buffer descriptors over the (b, h) slices and the wave's
   // bias fragments (h, qt32, all key tiles), as in the FP32 kernel.
@@ -117,29 +155,49 @@ __global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a
   const int64_t nt = a.np >> 5;
   const int64_t slice = (int64_t)a.np * kHeadDim;
   const int64_t frag = ((int64_t)h * nt + qt32) * nt * 1024;
-  const __amdgpu_buffer_rsrc_t rk =
-      kBlock ? buffer(a.k + bh * slice, slice * 4)
-             : buffer(a.k + b * a.ks[0] + h * a.ks[1], ((int64_t)(a.n - 1) * a.ks[2] + kHeadDim) * 4);
-  const __amdgpu_buffer_rsrc_t rv =
-      kBlock ? buffer(a.v + bh * slice, slice * 4)
-             : buffer(a.v + b * a.vs[0] + h * a.vs[1], ((int64_t)(a.n - 1) * a.vs[2] + kHeadDim) * 4);
   const __amdgpu_buffer_rsrc_t rb = buffer(a.bias + frag, nt * 4096);
   const __amdgpu_buffer_rsrc_t rb2 = buffer(a.bias_l2 + frag, nt * 4096);
-  const uint32_t ok = (uint32_t)(row8 * kHeadDim + col4) * 4;
-  const uint32_t ov = (uint32_t)(row8 * a.np + col4) * 4;
   const uint32_t ob = (uint32_t)lane * 16;
-  // Strided rows: key t*32 + row8, clamped to n - 1; channels col4..+3.
+  (void)slice;
+
+  // Block layout: per (b, h) a slice of np * 128 bytes, the hi plane and
+  // then the lo plane of 16-bit values: q, k [np rows][32 channels], v^T
+  // [np / 32 tiles][32 channels][32 key positions].  A tile's plane is 2 KB
+  // contiguous.  Wave w fills plane w of a stage (K hi, K lo, V^T hi,
+  // V^T lo): lane l writes chunk l % 4 of rows l / 4 and 16 + l / 4, read
+  // from that row's chunk (l % 4) ^ swz(row).
+  const int64_t slice_bytes = (int64_t)a.np * 128;
+  const uint8_t* dma_src = reinterpret_cast<const uint8_t*>(w < 2 ? a.k : a.v) + bh * slice_bytes +
+                           (w & 1) * (slice_bytes >> 1) + (lane >> 2) * 64 +
+                           16 * ((lane & 3) ^ swz(lane >> 2));
+  auto dma = [&](int t, int stage) {
+    const uint8_t* src = dma_src + (int64_t)t * kPlaneBytes;
+    const uint8_t* dst = lds + stage * kStageBytes + w * kPlaneBytes;
+    lds_dma16(src, dst);
+    lds_dma16(src + 1024, dst + 1024);
+  };
+  // Operand reads: lane (l32, half) reads chunk 2m + half of row l32.
+  const uint32_t rd0 = l32 * 64 + 16 * (half ^ swz(l32));
+  const uint32_t rd1 = l32 * 64 + 16 * ((2 + half) ^ swz(l32));
+  auto plane_rd = [&](int stage, int plane, int m) -> bf16x8 {
+    return *(const bf16x8*)(lds + stage * kStageBytes + plane * kPlaneBytes + (m ? rd1 : rd0));
+  };
+
+  // Strided layout: register staging.  Rows: key t*32 + row8, clamped to
+  // n - 1; channels col4..+3.
+  const __amdgpu_buffer_rsrc_t rk =
+      buffer(a.k + b * a.ks[0] + h * a.ks[1], ((int64_t)(a.n - 1) * a.ks[2] + kHeadDim) * 4);
+  const __amdgpu_buffer_rsrc_t rv =
+      buffer(a.v + b * a.vs[0] + h * a.vs[1], ((int64_t)(a.n - 1) * a.vs[2] + kHeadDim) * 4);
   auto row_of = [&](int t) -> uint32_t {
     const int j = t * kBk + row8;
     return (uint32_t)(j < a.n - 1 ? j : a.n - 1);
   };
   auto load_k = [&](int t) {
-    if constexpr (kBlock) return buffer_f4(rk, ok, (uint32_t)t * 4096);
-    else return buffer_f4(rk, row_of(t) * (uint32_t)a.ks[2] * 4 + (uint32_t)col4 * 4, 0);
+    return buffer_f4(rk, row_of(t) * (uint32_t)a.ks[2] * 4 + (uint32_t)col4 * 4, 0);
   };
   auto load_v = [&](int t) {
-    if constexpr (kBlock) return buffer_f4(rv, ov, (uint32_t)t * 128);
-    else return buffer_f4(rv, row_of(t) * (uint32_t)a.vs[2] * 4 + (uint32_t)col4 * 4, 0);
+    return buffer_f4(rv, row_of(t) * (uint32_t)a.vs[2] * 4 + (uint32_t)col4 * 4, 0);
   };
   // Strided V: thread holds key row8, channels col4..+3; its position in the
   // V^T planes' key order:
@@ -149,32 +207,22 @@ __global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a
     return cat4(buffer_f4(r, ob, s), buffer_f4(r, ob + 1024, s), buffer_f4(r, ob + 2048, s),
                 buffer_f4(r, ob + 3072, s));
   };
-  // K(t) into the three K planes, V(t) into the two V planes (thread: key or
-  // channel row8, four consecutive columns).
+  // Strided layout: K(t) into the three K planes, V(t) into the two V planes
+  // (thread: key row8, four consecutive channels).
   auto store_k = [&](int buf, f32x4 kv) {
     bf16x4 hi, lo, rest;
-    if constexpr (kBlock) {
-      unpair4(kv, hi, lo);  // fp16 pairs
-    } else {
-      split3(kv, hi, lo, rest);
-      *(bf16x4*)&Ks[buf][2][row8][col4] = rest;
-    }
+    split3(kv, hi, lo, rest);
     *(bf16x4*)&Ks[buf][0][row8][col4] = hi;
     *(bf16x4*)&Ks[buf][1][row8][col4] = lo;
+    *(bf16x4*)&Ks[buf][2][row8][col4] = rest;
   };
   auto store_v = [&](int buf, f32x4 vv) {
     bf16x4 hi, lo;
-    if constexpr (kBlock) {
-      unpair4(vv, hi, lo);  // bf16 pairs
-      *(bf16x4*)&Vs[buf][0][row8][vpos] = hi;
-      *(bf16x4*)&Vs[buf][1][row8][vpos] = lo;
-    } else {
-      split2(vv, hi, lo);
+    split2(vv, hi, lo);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        Vs[buf][0][col4 + e][kpos] = hi[e];
-        Vs[buf][1][col4 + e][kpos] = lo[e];
-      }
+    for (int e = 0; e < 4; ++e) {
+      Vs[buf][0][col4 + e][kpos] = hi[e];
+      Vs[buf][1][col4 + e][kpos] = lo[e];
     }
   };
 
@@ -253,14 +301,11 @@ __global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a
     // scaled by log2(e) on the fast path.
     bf16x8 qh[2], ql[2], qr[2];
     if constexpr (kBlock) {
-      const f32x4* src = (const f32x4*)(a.q + (bh * a.np + jq) * kHeadDim + 8 * half);
+      const uint8_t* src = reinterpret_cast<const uint8_t*>(a.q) + bh * slice_bytes + (int64_t)jq * 64;
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
-        bf16x4 h0, l0, h1, l1;
-        unpair4(src[4 * m], h0, l0);
-        unpair4(src[4 * m + 1], h1, l1);
-        qh[m] = bf16x8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
-        ql[m] = bf16x8{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+        qh[m] = *(const bf16x8*)(src + 16 * (2 * m + half));
+        ql[m] = *(const bf16x8*)(src + (slice_bytes >> 1) + 16 * (2 * m + half));
       }
     } else {
       const bool ok_q = jq < a.n;
@@ -276,18 +321,21 @@ __global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a
       }
     }
 
-    // S^T of the tile in Ks[buf], added to x (strided: the scaled bias on the
-    // fast path, zero on the exact path; block: zero); the smallest terms first.
+    // S^T of the tile in LDS buffer/stage buf, added to x (strided: the
+    // scaled bias on the fast path, zero on the exact path; block: zero); the
+    // smallest terms first.
     auto scores = [&](int buf, f32x16 x) -> f32x16 {
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
-        const bf16x8 kh = *(const bf16x8*)&Ks[buf][0][l32][16 * m + 8 * half];
-        const bf16x8 kl = *(const bf16x8*)&Ks[buf][1][l32][16 * m + 8 * half];
         if constexpr (kBlock) {
+          const bf16x8 kh = plane_rd(buf, 0, m);
+          const bf16x8 kl = plane_rd(buf, 1, m);
           x = mfma_f16(kl, qh[m], x);
           x = mfma_f16(kh, ql[m], x);
           x = mfma_f16(kh, qh[m], x);
         } else {
+          const bf16x8 kh = *(const bf16x8*)&Ks[buf][0][l32][16 * m + 8 * half];
+          const bf16x8 kl = *(const bf16x8*)&Ks[buf][1][l32][16 * m + 8 * half];
           const bf16x8 kr = *(const bf16x8*)&Ks[buf][2][l32][16 * m + 8 * half];
           x = mfma_bf16(kr, qh[m], x);
           x = mfma_bf16(kh, qr[m], x);
@@ -408,62 +456,112 @@ __global__ __launch_bounds__(kThreads, 3) void attention_split_kernel(AttnArgs a
       pack();
     };
 
-    // O^T += V^T P^T for the tile in Vs[buf].
+    // O^T += V^T P^T for the tile in LDS buffer/stage buf.
     auto pv = [&](int buf, const bf16x8 (&ph)[2], const bf16x8 (&pl)[2]) {
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
-        const bf16x8 vh = *(const bf16x8*)&Vs[buf][0][l32][16 * m + 8 * half];
-        const bf16x8 vl = *(const bf16x8*)&Vs[buf][1][l32][16 * m + 8 * half];
+        const bf16x8 vh = kBlock ? plane_rd(buf, 2, m) : *(const bf16x8*)&Vs[buf][0][l32][16 * m + 8 * half];
+        const bf16x8 vl = kBlock ? plane_rd(buf, 3, m) : *(const bf16x8*)&Vs[buf][1][l32][16 * m + 8 * half];
         o = mfma_bf16(vl, ph[m], o);
         o = mfma_bf16(vh, pl[m], o);
         o = mfma_bf16(vh, ph[m], o);
       }
     };
 
-    // Prologue: K(0), K(1), V(0) into LDS; S^T(0); K(2), V(1) in flight.
-    f32x16 x_a = init(0);
-    f32x16 x_b = init(last < 1 ? last : 1);
-    store_k(0, load_k(0));
-    store_v(0, load_v(0));
-    store_k(1, load_k(last < 1 ? last : 1));
-    f32x4 kreg = load_k(last < 2 ? last : 2);
-    f32x4 vreg = load_v(last < 1 ? last : 1);
-    __syncthreads();
-    finish(x_a, scores(0, kBlock || kExact ? zero16 : x_a), 0);
-    __syncthreads();  // every wave is done with K(0) before Ks[0] is refilled
-
-    // Iteration kt: Ks[(kt+1)&1] = K(kt+1), Vs[kt&1] = V(kt); cur = logits
-    // of tile kt; nxt = start value of tile kt+1; kreg = K(kt+2) and vreg =
-    // V(kt+1) in flight.  Indices past the last tile are clamped (in range,
-    // never used).
-    auto body = [&](int kt, f32x16& cur, f32x16& nxt) {
-      const f32x16 acc = scores((kt + 1) & 1, kBlock || kExact ? zero16 : nxt);
-      bf16x8 ph[2], pl[2];
-      softmax(cur, ph, pl);
-      pv(kt & 1, ph, pl);
-      finish(nxt, acc, kt + 1);
-      cur = init(kt + 2 < last ? kt + 2 : last);
-      store_k(kt & 1, kreg);
-      store_v((kt + 1) & 1, vreg);
-      kreg = load_k(kt + 3 < last ? kt + 3 : last);
-      vreg = load_v(kt + 2 < last ? kt + 2 : last);
-      __syncthreads();
-    };
-    auto tail = [&](const f32x16& cur, int kt) {
-      bf16x8 ph[2], pl[2];
-      softmax(cur, ph, pl);
-      pv(kt & 1, ph, pl);
-    };
+    auto clamp = [&](int t) { return t < last ? t : last; };
     int kt = 0;
-    for (; kt + 2 < nkt; kt += 2) {
-      body(kt, x_a, x_b);
-      body(kt + 1, x_b, x_a);
-    }
-    if (kt + 1 < nkt) {
-      body(kt, x_a, x_b);
-      tail(x_b, kt + 1);
+    if constexpr (kBlock) {
+      // Prologue: tiles 0-2 on their way into stages 0-2; S^T(0) once tiles
+      // 0 and 1 have landed.  Iteration t reads K(t+1) and V(t) and starts
+      // tile t+3 into the stage that held tile t-1, which every wave left
+      // behind at the previous barrier.  The copy is issued after the
+      // logits, whose bias-fragment loads the compiler waits for with a
+      // count that also covers any later load.  Tiles past the last are
+      // clamped (in range, never used).
+      auto stage = [](int t) { return t & (kStages - 1); };
+      f32x16 x_a = init(0);
+      f32x16 x_b = init(clamp(1));
+      dma(0, 0);
+      dma(clamp(1), 1);
+      dma(clamp(2), 2);
+      wait_vmcnt<2>();
+      __syncthreads();
+      finish(x_a, scores(0, zero16), 0);
+      auto body = [&](int t, f32x16& cur, f32x16& nxt) {
+        const f32x16 acc = scores(stage(t + 1), zero16);
+        bf16x8 ph[2], pl[2];
+        softmax(cur, ph, pl);
+        pv(stage(t), ph, pl);
+        finish(nxt, acc, t + 1);
+        dma(clamp(t + 3), stage(t + 3));
+        cur = init(clamp(t + 2));
+        // Tile t+2 has landed once at most this iteration's two tile loads
+        // and (fast path) four bias-fragment loads are outstanding: vector
+        // memory loads retire in issue order.
+        wait_vmcnt<kExact ? 2 : 6>();
+        __syncthreads();
+      };
+      auto tail = [&](const f32x16& cur, int t) {
+        bf16x8 ph[2], pl[2];
+        softmax(cur, ph, pl);
+        pv(stage(t), ph, pl);
+      };
+      for (; kt + 2 < nkt; kt += 2) {
+        body(kt, x_a, x_b);
+        body(kt + 1, x_b, x_a);
+      }
+      if (kt + 1 < nkt) {
+        body(kt, x_a, x_b);
+        tail(x_b, kt + 1);
+      } else {
+        tail(x_a, kt);
+      }
+      wait_vmcnt<0>();  // the clamped tail loads land before the LDS is released
     } else {
-      tail(x_a, kt);
+      // Prologue: K(0), K(1), V(0) into LDS; S^T(0); K(2), V(1) in flight.
+      f32x16 x_a = init(0);
+      f32x16 x_b = init(clamp(1));
+      store_k(0, load_k(0));
+      store_v(0, load_v(0));
+      store_k(1, load_k(clamp(1)));
+      f32x4 kreg = load_k(clamp(2));
+      f32x4 vreg = load_v(clamp(1));
+      __syncthreads();
+      finish(x_a, scores(0, kExact ? zero16 : x_a), 0);
+      __syncthreads();  // every wave is done with K(0) before Ks[0] is refilled
+
+      // Iteration t: Ks[(t+1)&1] = K(t+1), Vs[t&1] = V(t); cur = logits of
+      // tile t; nxt = start value of tile t+1; kreg = K(t+2) and vreg =
+      // V(t+1) in flight.  Indices past the last tile are clamped (in range,
+      // never used).
+      auto body = [&](int t, f32x16& cur, f32x16& nxt) {
+        const f32x16 acc = scores((t + 1) & 1, kExact ? zero16 : nxt);
+        bf16x8 ph[2], pl[2];
+        softmax(cur, ph, pl);
+        pv(t & 1, ph, pl);
+        finish(nxt, acc, t + 1);
+        cur = init(clamp(t + 2));
+        store_k(t & 1, kreg);
+        store_v((t + 1) & 1, vreg);
+        kreg = load_k(clamp(t + 3));
+        vreg = load_v(clamp(t + 2));
+        __syncthreads();
+      };
+      auto tail = [&](const f32x16& cur, int t) {
+        bf16x8 ph[2], pl[2];
+        softmax(cur, ph, pl);
+        pv(t & 1, ph, pl);
+      };
+      for (; kt + 2 < nkt; kt += 2) {
+        body(kt, x_a, x_b);
+        body(kt + 1, x_b, x_a);
+      }
+      if (kt + 1 < nkt) {
+        body(kt, x_a, x_b);
+        tail(x_b, kt + 1);
+      } else {
+        tail(x_a, kt);
+      }
     }
   };
   if (has_unmasked) {
@@ -502,12 +600,13 @@ hipError_t launch_attention_split(int layout, const AttnArgs& a, hipStream_t str
   if (a.tile_flags == nullptr || a.bias_l2 == nullptr || nkt > kTileFlagWords * 32)
     return hipErrorInvalidValue;
   if (layout == kAttnBlock && a.scales == nullptr) return hipErrorInvalidValue;
+  const size_t mask_row_bytes = (size_t)nkt * kBk * sizeof(float);
   if (layout == kAttnBlock) {
-    hipLaunchKernelGGL(attention_split_kernel<kAttnBlock>, dim3((uint32_t)total), dim3(kThreads), 0,
-                       stream, a, nqt, nkt, (uint32_t)total);
+    hipLaunchKernelGGL(attention_split_kernel<kAttnBlock>, dim3((uint32_t)total), dim3(kThreads),
+                       mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total);
   } else if (layout == kAttnStrided) {
     hipLaunchKernelGGL(attention_split_kernel<kAttnStrided>, dim3((uint32_t)total), dim3(kThreads),
-                       0, stream, a, nqt, nkt, (uint32_t)total);
+                       mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total);
   } else {
     return hipErrorInvalidValue;
   }

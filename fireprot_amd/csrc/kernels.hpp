@@ -130,12 +130,16 @@ struct ProjArgs {
   float* tri_bias_l2;  // the same scaled by log2(e)
   uint32_t* magnitudes;  // nullable: max|q|, max|k|, max|v|, max|bias| (kMagnitudeWords)
   // Plane layout of q, k, v^T (set by launch_projection for the split
-  // kernel; the FP32-matrix-core kernels keep plain FP32):
-  //   q, k: 32-bit word (j, c) of (i, h) holds the fp16 pair (hi, lo) of the
-  //         value times 2^e, e chosen per 32 x 32 (rows j, head channels)
-  //         tile so that the tile's max |value| 2^e lies in [2^14, 2^15);
-  //         hi = fp16(x 2^e) and lo = fp16(x 2^e - hi) carry 22 bits;
-  //   v^T:  word (c, j) holds the bf16 pair (hi, lo) of the value;
+  // kernel; the FP32-matrix-core kernels keep plain FP32).  The (i, h) slice
+  // of np * 128 bytes holds a hi plane and then a lo plane of 16-bit values:
+  //   q, k: [np rows j][32 channels] fp16 of the value times 2^e, e chosen
+  //         per 32 x 32 (rows j, head channels) tile so that the tile's max
+  //         |value| 2^e lies in [2^14, 2^15); hi = fp16(x 2^e) and lo =
+  //         fp16(x 2^e - hi) carry 22 bits;
+  //   v^T:  [np / 32 key tiles][32 channels][32 key positions] bf16 hi =
+  //         bf16(x), lo = bf16(x - hi); key 4g + e of a tile at position
+  //         16 (g / 4) + 4 (0, 2, 1, 3)[g % 4] + e (the S^T accumulator's
+  //         register order);
   //   scales[(t * rows_i + i) * 4 + h][j / 32] = 2^-e for t = 0 (q), 1 (k).
   int planes;
   float* scales;

@@ -55,11 +55,13 @@ __device__ __forceinline__ void store_tile(const ProjArgs& a, int tile, int tile
   const int i = tile / tiles_j;
   const int j0 = (tile % tiles_j) * kRows + 4 * half;
   if (MODE == kProjBlock && a.planes) {
-    // Plane layout (ProjArgs::planes): q, k as scaled fp16 (hi, lo) pairs
-    // with the tile's inverse scale, v^T as bf16 (hi, lo) pairs.
+    // Plane layout (ProjArgs::planes): per (i, head) a slice of np * 128
+    // bytes, the hi plane and then the lo plane of 16-bit values.
     const int64_t bh = (int64_t)i * kHeads + hw;
-    uint32_t* words;
+    const int64_t slice_bytes = (int64_t)a.np * 128;
     if (group == 0 || group == 1) {
+      // q, k: scaled fp16 planes [np rows][32 channels] with the tile's
+      // inverse scale.
       const float scale = group == 0 ? a.q_scale : 1.0f;
       // NaN-propagating max |value| of the 32 x 32 tile (scaling by a
       // positive constant keeps the maximum)
@@ -75,30 +77,46 @@ __device__ __forceinline__ void store_tile(const ProjArgs& a, int tile, int tile
       }
       // (acc * scale) 2^e == acc * (scale 2^e): one rounding either way
       const float f = __builtin_ldexpf(scale, e);
-      words = reinterpret_cast<uint32_t*>(group == 0 ? a.qh : a.kh) + (bh * a.np + j0) * kHeadDim + l32;
+      // Lane pairs (l32, l32 ^ 1) swap halves so that each lane stores one
+      // 32-bit word per plane and row pair: the even lane channels l32 and
+      // l32 + 1 of the pair's first row, the odd lane channels l32 - 1 and
+      // l32 of its second row.
+      const bool odd = l32 & 1;
+      const uint32_t sel = odd ? 0x03020706u : 0x05040100u;
+      uint8_t* base = reinterpret_cast<uint8_t*>(group == 0 ? a.qh : a.kh) + bh * slice_bytes +
+                      (int64_t)(j0 + odd) * 64 + (l32 - odd) * 2;
       typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
         const f32x2 x = {acc[r] * f, acc[r + 1] * f};
         const f16x2 hi = __builtin_convertvector(x, f16x2);
         const f16x2 lo = __builtin_convertvector(x - __builtin_convertvector(hi, f32x2), f16x2);
-        const u32x2 w = interleave_pairs(__builtin_bit_cast(uint32_t, hi), __builtin_bit_cast(uint32_t, lo));
-        words[(8 * (r >> 2) + (r & 3)) * kHeadDim] = w.x;
-        words[(8 * (r >> 2) + (r & 3) + 1) * kHeadDim] = w.y;
+        const uint32_t hw_ = __builtin_bit_cast(uint32_t, hi), lw = __builtin_bit_cast(uint32_t, lo);
+        const uint32_t ho = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hw_, 0xB1, 0xF, 0xF, false);
+        const uint32_t lo_ = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lw, 0xB1, 0xF, 0xF, false);
+        const int64_t row = 8 * (r >> 2) + (r & 3);
+        *(uint32_t*)(base + row * 64) = __builtin_amdgcn_perm(ho, hw_, sel);
+        *(uint32_t*)(base + (slice_bytes >> 1) + row * 64) = __builtin_amdgcn_perm(lo_, lw, sel);
       }
       if (half == 0 && l32 == 0)
         a.scales[(((int64_t)group * a.rows_i + i) * kHeads + hw) * (a.np >> 5) + tile % tiles_j] =
             __builtin_ldexpf(1.0f, -e);
     } else if (group == 2) {
-      words = reinterpret_cast<uint32_t*>(a.vt) + (bh * kHeadDim + l32) * a.np + j0;
-      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+      // v^T: bf16 planes [np / 32 tiles][32 channels][32 key positions],
+      // keys of a tile in the order of the S^T accumulator registers (key
+      // group g of four at position 16 (g / 4) + 4 (0, 2, 1, 3)[g % 4]).
+      // This lane's keys 8 rr + e + 4 half sit at positions 8 half + 4 rr + e
+      // (rr < 2) and 16 + 8 half + 4 (rr - 2) + e.
+      uint8_t* base = reinterpret_cast<uint8_t*>(a.vt) + bh * slice_bytes +
+                      (int64_t)(tile % tiles_j) * 2048 + l32 * 64 + 16 * half;
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        bf16x4 hi, lo;
-        split2(f32x4{acc[4 * rr + 0], acc[4 * rr + 1], acc[4 * rr + 2], acc[4 * rr + 3]}, hi, lo);
-        const u32x2 h = __builtin_bit_cast(u32x2, hi), l = __builtin_bit_cast(u32x2, lo);
-        const u32x2 w0 = interleave_pairs(h.x, l.x), w1 = interleave_pairs(h.y, l.y);
-        *(u32x4*)(words + 8 * rr) = u32x4{w0.x, w0.y, w1.x, w1.y};
+      for (int q = 0; q < 2; ++q) {
+        bf16x8 hi, lo;
+        split2(f32x8{acc[8 * q + 0], acc[8 * q + 1], acc[8 * q + 2], acc[8 * q + 3], acc[8 * q + 4],
+                     acc[8 * q + 5], acc[8 * q + 6], acc[8 * q + 7]},
+               hi, lo);
+        *(bf16x8*)(base + 32 * q) = hi;
+        *(bf16x8*)(base + (slice_bytes >> 1) + 32 * q) = lo;
       }
     } else {
       float* dst = a.gs + ((int64_t)i * a.np + j0) * kHidden + col_w;

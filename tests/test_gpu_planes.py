@@ -1,12 +1,15 @@
 """The plane layout the FP32 block's prepare stage writes for its attention.
 
-q and k are held as fp16 (hi, lo) pairs scaled by a power of two per 32 x 32
-tile (rows j, the head's 32 channels), so that the tile's max |value| times
-the scale lies in [2^14, 2^15); the workspace keeps the inverse scales.  v^T
-is held as bf16 (hi, lo) pairs.  Decoding the pairs must give the FP32
-projections back to 22 (q, k) and 16 (v) significant bits, and the scales
-must be the promised powers of two.  The layout is internal to the block's
-workspace; the offsets below restate the workspace segments (capi.hip).
+Per (outer row, head) the workspace holds a hi plane and then a lo plane of
+16-bit values.  q and k are [np rows][32 channels] fp16 planes of the value
+scaled by a power of two per 32 x 32 tile (rows j, the head's 32 channels), so
+that the tile's max |value| times the scale lies in [2^14, 2^15); the
+workspace keeps the inverse scales.  v^T is held as bf16 planes [key tile][32
+channels][32 key positions] with a tile's keys in the S^T accumulator's
+register order.  Decoding the planes must give the FP32 projections back to
+22 (q, k) and 16 (v) significant bits, and the scales must be the promised
+powers of two.  The layout is internal to the block's workspace; the offsets
+below restate the workspace segments (capi.hip).
 """
 from __future__ import annotations
 
@@ -39,16 +42,18 @@ def _offsets(n: int) -> dict:
     return o
 
 
-def _f16_pairs(words: np.ndarray) -> np.ndarray:
-    hi = (words & 0xFFFF).astype(np.uint16).view(np.float16).astype(np.float64)
-    lo = (words >> 16).astype(np.uint16).view(np.float16).astype(np.float64)
-    return hi + lo
+def _f16(bits: np.ndarray) -> np.ndarray:
+    return bits.view(np.float16).astype(np.float64)
 
 
-def _bf16_pairs(words: np.ndarray) -> np.ndarray:
-    hi = ((words & 0xFFFF) << 16).astype(np.uint32).view(np.float32).astype(np.float64)
-    lo = (words & 0xFFFF0000).astype(np.uint32).view(np.float32).astype(np.float64)
-    return hi + lo
+def _bf16(bits: np.ndarray) -> np.ndarray:
+    return (bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def _key_positions() -> np.ndarray:
+    """Position of each key of a 32-key tile in the v^T planes."""
+    perm = (0, 2, 1, 3)
+    return np.array([16 * (k // 16) + 4 * perm[(k // 4) % 4] + k % 4 for k in range(32)])
 
 
 @pytest.mark.parametrize("ending", [False, True])
@@ -79,8 +84,8 @@ def test_prepare_planes_decode_to_the_projections(ending, scale):
     o = _offsets(n)
     np_, nt = o["np"], o["np"] // 32
 
-    def words(start, count):
-        return raw[start:start + 4 * count].view(np.uint32)
+    def halves(start, count):
+        return raw[start:start + 2 * count].view(np.uint16)
 
     scales = raw[o["scales"]:o["scales"] + 4 * 2 * n * 4 * nt].view(np.float32).reshape(2, n, 4, nt)
     mant, _ = np.frexp(scales)
@@ -92,7 +97,8 @@ def test_prepare_planes_decode_to_the_projections(ending, scale):
     eq, ek, ev = oracle.prep_qkv(xl, params, apply_scale=True)
 
     for t, (seg, ref) in enumerate((("qh", eq), ("kh", ek))):
-        dec = _f16_pairs(words(o[seg], n * 4 * np_ * 32).reshape(n, 4, np_, 32))
+        planes = halves(o[seg], n * 4 * 2 * np_ * 32).reshape(n, 4, 2, np_, 32)
+        dec = _f16(planes[:, :, 0]) + _f16(planes[:, :, 1])
         tile_max = np.abs(dec).reshape(n, 4, nt, 32 * 32).max(axis=-1)
         live = tile_max > 0
         assert np.all((tile_max[live] >= 2.0 ** 14) & (tile_max[live] < 2.0 ** 15))
@@ -103,7 +109,10 @@ def test_prepare_planes_decode_to_the_projections(ending, scale):
         print(f"{seg} ending={ending} scale={scale}: max|err|={err:.3e} bound={bound:.3e}", flush=True)
         assert err <= bound
         assert np.all(val[:, :, n:] == 0), "padded rows must be zero"
-    vt = _bf16_pairs(words(o["vt"], n * 4 * 32 * np_).reshape(n, 4, 32, np_))
+    planes = halves(o["vt"], n * 4 * 2 * np_ * 32).reshape(n, 4, 2, nt, 32, 32)
+    vt_pos = _bf16(planes[:, :, 0]) + _bf16(planes[:, :, 1])  # [n, 4, tile, channel, position]
+    vt = vt_pos[..., _key_positions()]                        # key order within each tile
+    vt = vt.transpose(0, 1, 3, 2, 4).reshape(n, 4, 32, np_)   # [n, 4, channel, key]
     refv = ev.numpy().transpose(0, 1, 3, 2)
     err = np.abs(vt[..., :n] - refv).max()
     bound = 2e-5 * np.abs(refv).max()
