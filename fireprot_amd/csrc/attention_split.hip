@@ -78,7 +78,9 @@ constexpr int kWavesPerEu = LAYOUT == kAttnBlock ? 4 : 3;
 // stages being read, which would make it wait for every copy before the next
 // LDS read; the kernel waits for the copies itself (wait_vmcnt).  Loads the
 // compiler issues before or after stay correctly waited for, since vector
-// memory loads retire in issue order.
+// memory loads retire in issue order.  M0 is clobbered: the kernel makes no
+// other use of it (no LDS DMA, message or indexed-register instruction of
+// the compiler's own).
 __device__ __forceinline__ void lds_dma16(const void* src, const uint8_t* dst) {
   const uint32_t lds_addr =
       (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)dst;
