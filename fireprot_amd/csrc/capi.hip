@@ -201,9 +201,10 @@ StridedWorkspace strided_workspace(int batch, int n) {
 }
 
 // Workspace of fpx_tri_mul, 256-byte aligned segments: a and b channel-major
-// [128][np][np] float; x blocked [n][np / 32][128][32] float.
+// [128][np][np] float; x blocked [n][np / 32][128][32] float; the row maxima
+// of a and b [2][128][np] uint32.
 struct TriMulWorkspace {
-  size_t pa, pb, x, total;
+  size_t pa, pb, x, rowmax, total;
 };
 
 TriMulWorkspace trimul_workspace(int n) {
@@ -213,14 +214,19 @@ TriMulWorkspace trimul_workspace(int n) {
   w.pa = 0;
   w.pb = seg((size_t)fpx::kChannels * np * np * sizeof(float));
   w.x = 2 * w.pb;
-  w.total = w.x + seg((size_t)n * np * fpx::kChannels * sizeof(float));
+  w.rowmax = w.x + seg((size_t)n * np * fpx::kChannels * sizeof(float));
+  w.total = w.rowmax + seg(2 * (size_t)fpx::kChannels * np * sizeof(uint32_t));
   return w;
 }
 
-// Workspace of fpx_transition: h [round_up(rows, 128)][512] float.
-size_t transition_workspace(int64_t rows) {
+// Workspace of fpx_transition: h [round_up(rows, 128)][512] float, then the
+// 129 maxima words of the fp16-plane path.
+size_t transition_h_bytes(int64_t rows) {
   return (size_t)round_up(round_up(rows, 128) * fpx::kTransitionHidden * (int64_t)sizeof(float),
                           256);
+}
+size_t transition_workspace(int64_t rows) {
+  return transition_h_bytes(rows) + (size_t)round_up(129 * (int64_t)sizeof(uint32_t), 256);
 }
 
 // A [batch][4][n][32] operand with channel stride 1 the strided attention
@@ -549,6 +555,7 @@ int fpx_tri_mul(const float* z, int64_t z_stride0, int64_t z_stride1, const floa
   a.pa = as<float>(base + ws.pa);
   a.pb = as<float>(base + ws.pb);
   a.x = as<float>(base + ws.x);
+  a.rowmax = as<uint32_t>(base + ws.rowmax);
   a.out = out;
   a.os_i = out_stride0;
   a.os_j = out_stride1;
@@ -598,6 +605,7 @@ int fpx_transition(const float* x, int64_t rows_i, int64_t rows_j, int64_t x_str
   a.w_b = w_b;
   a.w_o = w_o;
   a.h = static_cast<float*>(workspace);
+  a.maxima = as<uint32_t>(static_cast<char*>(workspace) + transition_h_bytes((int64_t)rows_i * rows_j));
   a.out = out;
   a.os_i = out_stride_i;
   a.os_j = out_stride_j;

@@ -1,4 +1,4 @@
-// Gated pair-row projections on the CDNA4 BF16 matrix cores, FP32-accurate.
+// Gated pair-row projections on the CDNA4 16-bit matrix cores, FP32-accurate.
 //
 // Both the triangle multiplication's input projections and the pair
 // transition's hidden layer produce, per channel c of a pair row x,
@@ -6,13 +6,15 @@
 //   value_c = LN(x) . Wv[c] + bv[c]    gate_c = LN(x) . Wg[c] + bg[c]
 //
 // and combine the two:  (mask * sigmoid(gate)) * value  (kGatedTriMul) or
-// silu(gate) * value  (kGatedTransition).  Rows are split exactly into three
-// bfloat16 planes as they are staged to LDS, weights once per launch
-// (split.hpp), and each 32 x 32 block sums the six terms down to 2^-16
-// relative on v_mfma_f32_32x32x16_bf16.
+// silu(gate) * value  (kGatedTransition).  Rows and weights are held as
+// power-of-two scaled fp16 (hi, lo) planes (split.hpp): the LN rows by one
+// 2^ex per launch from the LN affine (|y_c| <= sqrt(128) |ln_w_c| + |ln_b_c|,
+// applied by pre-scaling ln_w and ln_b), each weight column by its own 2^ew;
+// each 32 x 32 block sums the three terms hi hi, hi lo, lo hi on
+// v_mfma_f32_32x32x16_f16 and is scaled back with ldexp, exactly.
 //
 // A wave's 32 B-operand columns are 16 value channels followed by the gate
-// channels of the same 16 channels, so its three weight planes fit in 96
+// channels of the same 16 channels, so its two weight planes fit in 64
 // VGPRs and the result of lane l (value) and lane l + 16 (gate) belong to one
 // channel: one v_permlane16_swap per register pair hands each lane both.  A
 // work-group (8 waves) covers 128 channels, one slice; the slices of a row
@@ -51,6 +53,10 @@ struct GatedArgs {
   int64_t ms_k;
   float* out[4];         // per slice, see gated_split_kernel
   int np;                // kGatedTriMul: packed extent of the output
+  uint32_t* rowmax;      // kGatedTriMul: [slice][128][np] max |out| over k per (channel, row),
+                         // float bits by atomic max (zeroed before the launch); null: none
+  uint32_t* out_max;     // kGatedTransition: max |out| of the launch, float bits by atomic
+                         // max (zeroed before the launch); null: none
 };
 
 template <int MODE>
@@ -78,7 +84,7 @@ __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedA
                                                                           int ntiles,
                                                                           int streams) {
   constexpr int kSlices = GatedTraits<MODE>::kSlices;
-  __shared__ __attribute__((aligned(16))) __bf16 xs[2][3][kGatedRows][kGatedPlaneRow];
+  __shared__ __attribute__((aligned(16))) __bf16 xs[2][2][kGatedRows][kGatedPlaneRow];
   __shared__ __attribute__((aligned(16))) float raw[kGatedRows][kChannels + 4];
   __shared__ float ms[4][kGatedRows];  // mask of tile T_k's rows at [k & 3]
 
@@ -93,16 +99,30 @@ __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedA
   const bool odd = l32 >= 16;           // gate column (B operand) / odd 16-lane row
   const int ch = 16 * w + (l32 & 15);   // channel of this lane's column, within the slice
 
-  bf16x8 wh[8], wl[8], wr[8];
+  // Weight planes of this lane's column, scaled by 2^ew (the column's max
+  // |w| over both halves of the wave).
+  bf16x8 wh[8], wl[8];
+  int ew;
   {
     const float* src = (odd ? a.w_gate[slice] : a.w_value[slice]) + (int64_t)ch * kChannels +
                        8 * half;
+    f32x8 wv[8];
+    float m = 0.f;
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       const f32x4 u = *(const f32x4*)(src + 16 * t);
       const f32x4 v = *(const f32x4*)(src + 16 * t + 4);
-      split3(f32x8{u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w}, wh[t], wl[t], wr[t]);
+      wv[t] = f32x8{u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) m = __builtin_elementwise_maximum(m, __builtin_fabsf(wv[t][e]));
     }
+    const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, m),
+                                                     __builtin_bit_cast(unsigned, m), false, false);
+    m = __builtin_elementwise_maximum(__builtin_bit_cast(float, (unsigned)sw[0]),
+                                      __builtin_bit_cast(float, (unsigned)sw[1]));
+    ew = plane_exp(m);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) split_f16(ldexp8(wv[t], ew), wh[t], wl[t]);
   }
   const float bv = a.b_value[slice] ? a.b_value[slice][ch] : 0.f;
   const float bg = a.b_gate[slice] ? a.b_gate[slice][ch] : 0.f;
@@ -112,11 +132,19 @@ __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedA
   const int c16 = lane & 15;
   const int lrow = 4 * w + (lane >> 4);
   f32x8 lnw, lnb;
+  float bound = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     lnw[e] = a.ln_w ? a.ln_w[8 * c16 + e] : 1.f;
     lnb[e] = a.ln_b ? a.ln_b[8 * c16 + e] : 0.f;
+    bound = __builtin_elementwise_maximum(
+        bound, 11.3137085f * __builtin_fabsf(lnw[e]) + __builtin_fabsf(lnb[e]));
   }
+  // |y_c| <= sqrt(128) |ln_w_c| + |ln_b_c| up to FP32 rounding; the margin
+  // keeps |y| 2^ex below 2^15.
+  const int ex = plane_exp(wave_max(bound) * (1.0f + 0x1p-10f));
+  lnw = ldexp8(lnw, ex);
+  lnb = ldexp8(lnb, ex);
 
   auto origin = [&](int tile, int& r, int& k0) {
     r = tile / tiles_k;
@@ -157,13 +185,12 @@ __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedA
   };
 
   auto stage_split = [&](int buf, const f32x8& d, float rstd, int k0) {
-    f32x8 y = d * rstd * lnw + lnb;
+    f32x8 y = d * rstd * lnw + lnb;  // scaled by 2^ex
     if (k0 + lrow >= a.rows_k) y = f32x8{};
-    bf16x8 hi, lo, rest;
-    split3(y, hi, lo, rest);
+    bf16x8 hi, lo;
+    split_f16(y, hi, lo);
     *(bf16x8*)&xs[buf][0][lrow][8 * c16] = hi;
     *(bf16x8*)&xs[buf][1][lrow][8 * c16] = lo;
-    *(bf16x8*)&xs[buf][2][lrow][8 * c16] = rest;
   };
 
   auto consume = [&](int tile_index) {  // tile_index: k of the staged tile T_k
@@ -173,23 +200,29 @@ __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedA
     }
   };
 
+  // Two accumulation chains, swapped every k step.
   auto mfma_step = [&](int buf, int t, f32x16& c0, f32x16& c1) {
     const int k = 16 * t + 8 * half;
     const bf16x8 xh = *(const bf16x8*)&xs[buf][0][l32][k];
     const bf16x8 xl = *(const bf16x8*)&xs[buf][1][l32][k];
-    const bf16x8 xr = *(const bf16x8*)&xs[buf][2][l32][k];
-    c0 = mfma_bf16(xh, wh[t], c0);
-    c1 = mfma_bf16(xh, wl[t], c1);
-    c0 = mfma_bf16(xl, wh[t], c0);
-    c1 = mfma_bf16(xl, wl[t], c1);
-    c0 = mfma_bf16(xr, wh[t], c0);
-    c1 = mfma_bf16(xh, wr[t], c1);
+    if (t & 1) {
+      c1 = mfma_f16(xh, wh[t], c1);
+      c0 = mfma_f16(xh, wl[t], c0);
+      c1 = mfma_f16(xl, wh[t], c1);
+    } else {
+      c0 = mfma_f16(xh, wh[t], c0);
+      c1 = mfma_f16(xh, wl[t], c1);
+      c0 = mfma_f16(xl, wh[t], c0);
+    }
   };
   auto k_steps = [&](int buf) -> f32x16 {
     f32x16 c0 = {}, c1 = {};
 #pragma unroll
     for (int t = 0; t < 8; ++t) mfma_step(buf, t, c0, c1);
-    return c0 + c1;
+    f32x16 r = c0 + c1;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) r[e] = __builtin_ldexpf(r[e], -(ex + ew));
+    return r;
   };
 
   // Result of tile `tile` (the k-th of this stream): lanes of even 16-lane
@@ -197,6 +230,7 @@ __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedA
   // register r with r + 8 across the row pair leaves every lane the value
   // and gate of its channel for registers r + (odd ? 8 : 0), r < 8, i.e.
   // tile rows 8 rr + 4 half + e for rr = (odd ? 2 : 0) + r / 4, e = r % 4.
+  float out_max = 0.f;  // kGatedTransition: running max |value| stored
   auto store = [&](const f32x16& res, int tile, int k) {
     f32x8 val;
 #pragma unroll
@@ -222,6 +256,24 @@ __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedA
     origin(tile, r_out, k0);
     const int rr0 = odd ? 2 : 0;
     if constexpr (MODE == kGatedTriMul) {
+      if (a.rowmax != nullptr) {
+        // max |value| of the channel over the tile's 32 keys: this lane's 8,
+        // then lanes l ^ 16 (other register half) and l ^ 32 (other rows)
+        float m = 0.f;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) m = __builtin_elementwise_maximum(m, __builtin_fabsf(val[r]));
+        const auto s16 = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, m),
+                                                          __builtin_bit_cast(unsigned, m), false, false);
+        m = __builtin_elementwise_maximum(__builtin_bit_cast(float, (unsigned)s16[0]),
+                                          __builtin_bit_cast(float, (unsigned)s16[1]));
+        const auto s32 = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, m),
+                                                          __builtin_bit_cast(unsigned, m), false, false);
+        m = __builtin_elementwise_maximum(__builtin_bit_cast(float, (unsigned)s32[0]),
+                                          __builtin_bit_cast(float, (unsigned)s32[1]));
+        if (!odd && half == 0)
+          atomicMax(&a.rowmax[((int64_t)slice * kChannels + ch) * a.np + r_out],
+                    __builtin_bit_cast(uint32_t, m));
+      }
       float* dst = a.out[slice] + ((int64_t)ch * a.np + r_out) * a.np + k0 + 4 * half;
 #pragma unroll
       for (int q = 0; q < 2; ++q)
@@ -232,7 +284,10 @@ __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedA
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
         const int kk = k0 + 8 * (rr0 + (r >> 2)) + 4 * half + (r & 3);
-        if (kk < a.rows_k) dst[(int64_t)kk * 512] = val[r];
+        if (kk < a.rows_k) {
+          dst[(int64_t)kk * 512] = val[r];
+          out_max = __builtin_elementwise_maximum(out_max, __builtin_fabsf(val[r]));
+        }
       }
     }
   };
@@ -289,6 +344,11 @@ __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedA
     ++kidx;
   }
   if (!lead && kidx > 0) store(res, tile - streams, kidx - 1);
+  if (MODE == kGatedTransition && a.out_max != nullptr) {
+    // one atomic per wave: the NaN-propagating max of the values it stored
+    const float m = wave_max(out_max);
+    if (lane == 0) atomicMax(a.out_max, __builtin_bit_cast(uint32_t, m));
+  }
 }
 
 // Launches gated_split_kernel<MODE> over rows_r x span_k / 32 row tiles.

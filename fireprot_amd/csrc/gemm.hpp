@@ -206,4 +206,91 @@ __device__ __forceinline__ void gemm_nt_128_split(const float* a, int64_t lda, c
   }
 }
 
+// The same product on v_mfma_f32_32x32x16_f16 with power-of-two scaled fp16
+// (hi, lo) planes (split.hpp): row r of A is scaled by 2^ea[r] and row r of
+// B by 2^eb[r] (ea, eb: 128 per-row exponents, plane_exp of each row's max
+// |value| over all keys, in LDS), so acc[rb][cb] comes out scaled by
+// 2^(ea[row] + eb[col]) for the caller to undo with ldexp.  Three terms (hi
+// hi, hi lo, lo hi) per 16-key stage: 12 MFMAs per wave and stage.
+typedef __bf16 F16Stage[2][kGemmTile][kSplitRow];  // planes hi, lo (fp16 bits)
+
+__device__ __forceinline__ void gemm_nt_128_f16(const float* a, int64_t lda, const float* b,
+                                                int64_t ldb, int nk, F16Stage* As, F16Stage* Bs,
+                                                const int* ea, const int* eb,
+                                                f32x16 (&acc)[2][2]) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+  const int wi = (w >> 1) * 64;
+  const int wj = (w & 1) * 64;
+
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a, (127 * lda + kSplitK * nk) * 4);
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(b, (127 * ldb + kSplitK * nk) * 4);
+  // Thread (row = tid / 4 + 64 u, keys 4 (tid % 4) .. +3) of each stage.
+  const int lrow = tid >> 2;
+  const int lc4 = (tid & 3) * 4;
+  const uint32_t va = (uint32_t)((lrow * lda + lc4) * 4);
+  const uint32_t vb = (uint32_t)((lrow * ldb + lc4) * 4);
+  const uint32_t pa = (uint32_t)(64 * lda * 4);  // 64 rows further down
+  const uint32_t pb = (uint32_t)(64 * ldb * 4);
+  const int xa[2] = {ea[lrow], ea[lrow + 64]};
+  const int xb[2] = {eb[lrow], eb[lrow + 64]};
+
+  f32x4 ga[2], gb[2];
+  auto load = [&](int kt) {
+    const uint32_t s = (uint32_t)kt * (kSplitK * 4);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      ga[u] = buffer_load_f4(ra, va + u * pa, s);
+      gb[u] = buffer_load_f4(rb, vb + u * pb, s);
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      bf16x4 h, l;
+      split_f16(ldexp4(ga[u], xa[u]), h, l);
+      *(bf16x4*)&As[buf][0][lrow + 64 * u][lc4] = h;
+      *(bf16x4*)&As[buf][1][lrow + 64 * u][lc4] = l;
+      split_f16(ldexp4(gb[u], xb[u]), h, l);
+      *(bf16x4*)&Bs[buf][0][lrow + 64 * u][lc4] = h;
+      *(bf16x4*)&Bs[buf][1][lrow + 64 * u][lc4] = l;
+    }
+  };
+
+  load(0);
+  store(0);
+  if (nk > 1) load(1);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    bf16x8 ap[2][2], bp[2][2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+#pragma unroll
+      for (int pl = 0; pl < 2; ++pl) {
+        ap[q][pl] = *(const bf16x8*)&As[buf][pl][wi + 32 * q + l32][8 * half];
+        bp[q][pl] = *(const bf16x8*)&Bs[buf][pl][wj + 32 * q + l32][8 * half];
+      }
+    }
+    constexpr int kTerms[3][2] = {{0, 0}, {0, 1}, {1, 0}};
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+#pragma unroll
+      for (int rb2 = 0; rb2 < 2; ++rb2) {
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+          acc[rb2][cb] = mfma_f16(ap[rb2][kTerms[t][0]], bp[cb][kTerms[t][1]], acc[rb2][cb]);
+      }
+    }
+    if (kt + 1 < nk) {
+      store(buf ^ 1);
+      if (kt + 2 < nk) load(kt + 2);
+    }
+    __syncthreads();
+  }
+}
+
 }  // namespace fpx

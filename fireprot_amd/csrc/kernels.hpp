@@ -266,6 +266,9 @@ struct TriMulArgs {
   float* pa;
   float* pb;
   float* x;
+  // fp16-plane path: [2 (a, b)][128 channels][np rows] running max |a|, |b|
+  // over the keys of each (channel, row), as float bits (atomic max)
+  uint32_t* rowmax;
   float* out;
   int64_t os_i;
   int64_t os_j;
@@ -296,6 +299,9 @@ struct TransitionArgs {
   const float* w_b;   // [512][128]
   const float* w_o;   // [128][512]
   float* h;
+  // fp16-plane path: [0] max |h| of the launch, [1 + c] max |W_o[c]|, as
+  // float bits (129 words)
+  uint32_t* maxima;
   float* out;
   int64_t os_i;
   int64_t os_j;

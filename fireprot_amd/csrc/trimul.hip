@@ -152,21 +152,31 @@ __global__ __launch_bounds__(kProjWaves * 64) void trimul_project_kernel(TriMulA
   }
 }
 
+// Clears `words` 32-bit words (a multiple of 4) with vector stores.
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int64_t words) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  if (4 * i < words) reinterpret_cast<u32x4*>(p)[i] = u32x4{0u, 0u, 0u, 0u};
+}
+
 // ----------------------------------------------------------- contraction
 // One work-group = (channel c, 128 rows i, 128 columns j) of x_c = A_c B_c^T
 // (gemm_nt_128 over the np keys).  Work-groups of one channel are consecutive
 // in the logical order, and xcd_remap gives each XCD a contiguous range, so
 // the A and B row panels a range touches stay in that XCD's L2.
-// kSplit: gemm_nt_128_split (BF16 matrix cores, exact three-plane splits).
+// kSplit: gemm_nt_128_f16 (16-bit matrix cores, scaled fp16 planes), with
+// each row's exponent from the row maxima the projection recorded.
 template <bool kSplit>
 __global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const float* __restrict__ pa,
                                                                  const float* __restrict__ pb,
+                                                                 const uint32_t* __restrict__ rowmax,
                                                                  float* __restrict__ x, int n,
                                                                  int np, int tiles,
                                                                  uint32_t total) {
-  static_assert(sizeof(GemmStage) == sizeof(SplitStage), "both mainloops share the LDS stages");
+  static_assert(sizeof(F16Stage) <= sizeof(GemmStage), "both mainloops share the LDS stages");
   __shared__ __attribute__((aligned(16))) GemmStage As[2];
   __shared__ __attribute__((aligned(16))) GemmStage Bs[2];
+  __shared__ int ea[kSplit ? kGemmTile : 1], eb[kSplit ? kGemmTile : 1];
 
   const uint32_t logical = xcd_remap(blockIdx.x, total);
   const int per_channel = tiles * tiles;
@@ -181,11 +191,25 @@ __global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const float* __
 
   const int64_t slice = (int64_t)np * np;
   f32x16 acc[2][2] = {};
-  if constexpr (kSplit)
-    gemm_nt_128_split(pa + c * slice + (int64_t)i0 * np, np, pb + c * slice + (int64_t)j0 * np,
-                      np, np / kSplitK, reinterpret_cast<SplitStage*>(As),
-                      reinterpret_cast<SplitStage*>(Bs), acc);
-  else
+  if constexpr (kSplit) {
+    const int t = threadIdx.x;
+    const uint32_t* rm = rowmax + ((int64_t)(t >> 7) * kChannels + c) * np + ((t >> 7) ? j0 : i0);
+    (t >> 7 ? eb : ea)[t & 127] = plane_exp(__builtin_bit_cast(float, rm[t & 127]));
+    __syncthreads();
+    gemm_nt_128_f16(pa + c * slice + (int64_t)i0 * np, np, pb + c * slice + (int64_t)j0 * np,
+                    np, np / kSplitK, reinterpret_cast<F16Stage*>(As),
+                    reinterpret_cast<F16Stage*>(Bs), ea, eb, acc);
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) {
+        const int ej = eb[(w & 1) * 64 + 32 * cb + l32];
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          acc[rb][cb][r] = __builtin_ldexpf(acc[rb][cb][r], -(ea[(w >> 1) * 64 + 32 * rb + mfma_row(r, half)] + ej));
+      }
+    }
+  } else
     gemm_nt_128(pa + c * slice + (int64_t)i0 * np, np, pb + c * slice + (int64_t)j0 * np, np,
                 np / kKStage, As, Bs, acc);
 
@@ -596,15 +620,22 @@ hipError_t launch_trimul(const TriMulArgs& a, hipStream_t stream) {
     g.out[0] = a.pa;
     g.out[1] = a.pb;
     g.np = a.np;
+    g.rowmax = a.rowmax;
+    if (a.rowmax == nullptr) return hipErrorInvalidValue;
+    const int64_t words = 2 * (int64_t)kChannels * a.np;
+    hipLaunchKernelGGL(zero_words_kernel, dim3((uint32_t)((words / 4 + 255) / 256)), dim3(256), 0,
+                       stream, a.rowmax, words);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
     e = launch_gated_split<kGatedTriMul>(g, stream);
   }
   if (e != hipSuccess) return e;
   if (fp32_matrix_cores_selected())
     hipLaunchKernelGGL(trimul_contract_kernel<false>, dim3((uint32_t)gemm_total), dim3(256), 0,
-                       stream, a.pa, a.pb, a.x, a.n, a.np, tiles, (uint32_t)gemm_total);
+                       stream, a.pa, a.pb, a.rowmax, a.x, a.n, a.np, tiles, (uint32_t)gemm_total);
   else
     hipLaunchKernelGGL(trimul_contract_kernel<true>, dim3((uint32_t)gemm_total), dim3(256), 0,
-                       stream, a.pa, a.pb, a.x, a.n, a.np, tiles, (uint32_t)gemm_total);
+                       stream, a.pa, a.pb, a.rowmax, a.x, a.n, a.np, tiles, (uint32_t)gemm_total);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (fp32_matrix_cores_selected())

@@ -101,8 +101,9 @@ def test_tri_mul_workspace_sizes(lib):
     seg = lambda b: -(-b // 256) * 256  # noqa: E731
     for n in (1, 7, 129, 1000, 1536, 4096):
         np_ = -(-n // 128) * 128
-        # a and b channel-major [128][np][np]; x blocked [n][np/32][128][32]
-        expected = 2 * seg(128 * np_ * np_ * 4) + seg(n * np_ * 128 * 4)
+        # a and b channel-major [128][np][np]; x blocked [n][np/32][128][32];
+        # the row maxima of a and b [2][128][np] uint32
+        expected = 2 * seg(128 * np_ * np_ * 4) + seg(n * np_ * 128 * 4) + seg(2 * 128 * np_ * 4)
         assert lib.fpx_tri_mul_workspace_bytes(n, 128, 128) == expected
     for bad in ((0, 128, 128), (4097, 128, 128), (64, 64, 128), (64, 128, 32)):
         assert lib.fpx_tri_mul_workspace_bytes(*bad) == 0
@@ -143,7 +144,8 @@ def test_transition_workspace_and_guards(lib):
     seg = lambda b: -(-b // 256) * 256  # noqa: E731
     for ri, rj in ((1, 1), (3, 5), (1536, 1536), (1, 1000000)):
         rows = ri * rj
-        assert lib.fpx_transition_workspace_bytes(ri, rj, 128, 4) == seg(-(-rows // 128) * 128 * 512 * 4)
+        # h [round_up(rows, 128)][512] float, then 129 maxima words
+        assert lib.fpx_transition_workspace_bytes(ri, rj, 128, 4) == seg(-(-rows // 128) * 128 * 512 * 4) + seg(129 * 4)
     for bad in ((0, 5, 128, 4), (5, 0, 128, 4), (2, 2, 64, 4), (2, 2, 128, 2), (-1, 2, 128, 4)):
         assert lib.fpx_transition_workspace_bytes(*bad) == 0
     f = lib.fpx_transition
