@@ -152,6 +152,12 @@ __device__ __forceinline__ f32x16 mfma_f16(bf16x8 a, bf16x8 b, f32x16 c) {
                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
+// v_mfma_f32_16x16x32_f16 on fp16 bit patterns (layouts of mfma16_bf16).
+__device__ __forceinline__ f32x4 mfma16_f16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
 // Scaled fp16 planes.  A block of values whose max |x| is m is scaled by
 // 2^e, e = plane_exp(m), so that m 2^e lies in [2^14, 2^15), and split into
 // hi = fp16(x 2^e) and lo = fp16(x 2^e - hi) (round to nearest even; the

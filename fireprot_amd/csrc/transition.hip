@@ -17,6 +17,8 @@
 #include "gemm.hpp"
 #include "kernels.hpp"
 
+#include <type_traits>
+
 namespace fpx {
 namespace {
 
@@ -136,9 +138,9 @@ __global__ __launch_bounds__(256) void transition_maxima_kernel(const float* __r
 template <bool kSplit>
 __global__ __launch_bounds__(256, 2) void transition_down_kernel(TransitionArgs a,
                                                                  int64_t rows) {
-  static_assert(sizeof(F16Stage) <= sizeof(GemmStage), "both mainloops share the LDS stages");
-  __shared__ __attribute__((aligned(16))) GemmStage As[2];
-  __shared__ __attribute__((aligned(16))) GemmStage Bs[2];
+  using Stage = std::conditional_t<kSplit, F16Stage, GemmStage>;
+  __shared__ __attribute__((aligned(16))) Stage As[2];
+  __shared__ __attribute__((aligned(16))) Stage Bs[2];
   __shared__ int ea[kSplit ? kGemmTile : 1], eb[kSplit ? kGemmTile : 1];
   const int64_t r0 = (int64_t)blockIdx.x * kGemmTile;
   f32x16 acc[2][2] = {};
@@ -155,8 +157,7 @@ __global__ __launch_bounds__(256, 2) void transition_down_kernel(TransitionArgs 
     if (t < kGemmTile) ea[t] = ex;
     else eb[t - kGemmTile] = plane_exp(__builtin_bit_cast(float, a.maxima[1 + t - kGemmTile]));
     __syncthreads();
-    gemm_nt_128_f16(a.h + r0 * kHid, kHid, a.w_o, kHid, kHid / kSplitK,
-                    reinterpret_cast<F16Stage*>(As), reinterpret_cast<F16Stage*>(Bs), ea, eb, acc);
+    gemm_nt_128_f16(a.h + r0 * kHid, kHid, a.w_o, kHid, kHid / kSplitK, As, Bs, ea, eb, acc);
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll

@@ -23,6 +23,8 @@
 //                          per tile, the sigmoid gate and the in-place write
 #include "common.hpp"
 #include "gated_split.hpp"
+
+#include <type_traits>
 #include "gemm.hpp"
 #include "kernels.hpp"
 
@@ -173,9 +175,10 @@ __global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const float* __
                                                                  float* __restrict__ x, int n,
                                                                  int np, int tiles,
                                                                  uint32_t total) {
-  static_assert(sizeof(F16Stage) <= sizeof(GemmStage), "both mainloops share the LDS stages");
-  __shared__ __attribute__((aligned(16))) GemmStage As[2];
-  __shared__ __attribute__((aligned(16))) GemmStage Bs[2];
+  // fp16 planes take two thirds of the FP32 stages' LDS: three work-groups per CU.
+  using Stage = std::conditional_t<kSplit, F16Stage, GemmStage>;
+  __shared__ __attribute__((aligned(16))) Stage As[2];
+  __shared__ __attribute__((aligned(16))) Stage Bs[2];
   __shared__ int ea[kSplit ? kGemmTile : 1], eb[kSplit ? kGemmTile : 1];
 
   const uint32_t logical = xcd_remap(blockIdx.x, total);
@@ -197,8 +200,7 @@ __global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const float* __
     (t >> 7 ? eb : ea)[t & 127] = plane_exp(__builtin_bit_cast(float, rm[t & 127]));
     __syncthreads();
     gemm_nt_128_f16(pa + c * slice + (int64_t)i0 * np, np, pb + c * slice + (int64_t)j0 * np,
-                    np, np / kSplitK, reinterpret_cast<F16Stage*>(As),
-                    reinterpret_cast<F16Stage*>(Bs), ea, eb, acc);
+                    np, np / kSplitK, As, Bs, ea, eb, acc);
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
@@ -366,8 +368,8 @@ constexpr int kFinPlaneRow = kChannels + 8;  // bf16 per LDS row: 272 bytes
 
 __global__ __launch_bounds__(512, 1) void trimul_finish_split_kernel(TriMulArgs a, int tiles_j,
                                                                      int ntiles) {
-  __shared__ __attribute__((aligned(16))) __bf16 px[2][3][kRows][kFinPlaneRow];
-  __shared__ __attribute__((aligned(16))) __bf16 pz[2][3][kRows][kFinPlaneRow];
+  __shared__ __attribute__((aligned(16))) __bf16 px[2][2][kRows][kFinPlaneRow];
+  __shared__ __attribute__((aligned(16))) __bf16 pz[2][2][kRows][kFinPlaneRow];
   __shared__ __attribute__((aligned(16))) float raw_x[kRows][kChannels + 4];
   __shared__ __attribute__((aligned(16))) float raw_z[kRows][kChannels + 4];
 
@@ -381,16 +383,45 @@ __global__ __launch_bounds__(512, 1) void trimul_finish_split_kernel(TriMulArgs 
   const int64_t nb = a.np / 32;
   const bool residual = a.accumulate != 0;
 
-  // Weight planes: B[k][c] = W[c][k], lane holding keys 32t + 8 g4 + e.
-  bf16x8 wz[3][4], wg[3][4];
+  // Weight planes: B[k][c] = W[c][k], lane holding keys 32t + 8 g4 + e, as
+  // fp16 (hi, lo) of W[c] 2^ew (each channel row's max |w| over the four
+  // lanes l16 + 16 g4 that hold it).
+  bf16x8 wz[2][4], wg[2][4];
+  int ewz, ewg;
+  {
+    f32x8 vz[4], vg[4];
+    float mz = 0.f, mg = 0.f;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const float* sz = a.w_z + (int64_t)ch * kChannels + 32 * t + 8 * g4;
-    const float* sg = a.w_g + (int64_t)ch * kChannels + 32 * t + 8 * g4;
-    const f32x4 z0 = *(const f32x4*)sz, z1 = *(const f32x4*)(sz + 4);
-    const f32x4 g0 = *(const f32x4*)sg, g1 = *(const f32x4*)(sg + 4);
-    split3(f32x8{z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w}, wz[0][t], wz[1][t], wz[2][t]);
-    split3(f32x8{g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w}, wg[0][t], wg[1][t], wg[2][t]);
+    for (int t = 0; t < 4; ++t) {
+      const float* sz = a.w_z + (int64_t)ch * kChannels + 32 * t + 8 * g4;
+      const float* sg = a.w_g + (int64_t)ch * kChannels + 32 * t + 8 * g4;
+      const f32x4 z0 = *(const f32x4*)sz, z1 = *(const f32x4*)(sz + 4);
+      const f32x4 g0 = *(const f32x4*)sg, g1 = *(const f32x4*)(sg + 4);
+      vz[t] = f32x8{z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
+      vg[t] = f32x8{g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        mz = __builtin_elementwise_maximum(mz, __builtin_fabsf(vz[t][e]));
+        mg = __builtin_elementwise_maximum(mg, __builtin_fabsf(vg[t][e]));
+      }
+    }
+    auto rows4_max = [](float v) {  // lanes l, l ^ 16, l ^ 32, l ^ 48
+      const auto s = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v),
+                                                      __builtin_bit_cast(unsigned, v), false, false);
+      v = __builtin_elementwise_maximum(__builtin_bit_cast(float, (unsigned)s[0]),
+                                        __builtin_bit_cast(float, (unsigned)s[1]));
+      const auto u = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v),
+                                                      __builtin_bit_cast(unsigned, v), false, false);
+      return __builtin_elementwise_maximum(__builtin_bit_cast(float, (unsigned)u[0]),
+                                           __builtin_bit_cast(float, (unsigned)u[1]));
+    };
+    ewz = plane_exp(rows4_max(mz));
+    ewg = plane_exp(rows4_max(mg));
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      split_f16(ldexp8(vz[t], ewz), wz[0][t], wz[1][t]);
+      split_f16(ldexp8(vg[t], ewg), wg[0][t], wg[1][t]);
+    }
   }
   const float bz = a.b_z ? a.b_z[ch] : 0.f;
   const float bg = a.b_g ? a.b_g[ch] : 0.f;
@@ -399,6 +430,7 @@ __global__ __launch_bounds__(512, 1) void trimul_finish_split_kernel(TriMulArgs 
   // tile row lrow.
   const int lrow = 4 * w + g4;
   f32x8 lnw_in, lnb_in, lnw_out, lnb_out;
+  float bound_in = 0.f, bound_out = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int c = 8 * l16 + e;
@@ -406,7 +438,19 @@ __global__ __launch_bounds__(512, 1) void trimul_finish_split_kernel(TriMulArgs 
     lnb_in[e] = a.ln_in_b ? a.ln_in_b[c] : 0.f;
     lnw_out[e] = a.ln_out_w ? a.ln_out_w[c] : 1.f;
     lnb_out[e] = a.ln_out_b ? a.ln_out_b[c] : 0.f;
+    bound_in = __builtin_elementwise_maximum(
+        bound_in, 11.3137085f * __builtin_fabsf(lnw_in[e]) + __builtin_fabsf(lnb_in[e]));
+    bound_out = __builtin_elementwise_maximum(
+        bound_out, 11.3137085f * __builtin_fabsf(lnw_out[e]) + __builtin_fabsf(lnb_out[e]));
   }
+  // LN rows as fp16 planes scaled by one power of two per input: |y_c| <=
+  // sqrt(128) |ln_w_c| + |ln_b_c| up to FP32 rounding (pre-scaled affines).
+  const int ex_in = plane_exp(wave_max(bound_in) * (1.0f + 0x1p-10f));
+  const int ex_out = plane_exp(wave_max(bound_out) * (1.0f + 0x1p-10f));
+  lnw_in = ldexp8(lnw_in, ex_in);
+  lnb_in = ldexp8(lnb_in, ex_in);
+  lnw_out = ldexp8(lnw_out, ex_out);
+  lnb_out = ldexp8(lnb_out, ex_out);
 
   auto origin = [&](int tile, int& i, int& jb) {
     i = tile / tiles_j;
@@ -453,11 +497,10 @@ __global__ __launch_bounds__(512, 1) void trimul_finish_split_kernel(TriMulArgs 
     const float rstd = __builtin_amdgcn_rsqf(row16_sum(q) * (1.0f / kChannels) + eps);
     f32x8 y = d * rstd * gw + gb;
     if (!valid) y = f32x8{};
-    bf16x8 hi, lo, rest;
-    split3(y, hi, lo, rest);
+    bf16x8 hi, lo;
+    split_f16(y, hi, lo);
     *(bf16x8*)&planes[0][lrow][8 * l16] = hi;
     *(bf16x8*)&planes[1][lrow][8 * l16] = lo;
-    *(bf16x8*)&planes[2][lrow][8 * l16] = rest;
   };
   // Normalises the raw rows of the tile whose first pair row is j0 into
   // planes buf.  Rows past n (never stored) are zeroed.
@@ -471,25 +514,33 @@ __global__ __launch_bounds__(512, 1) void trimul_finish_split_kernel(TriMulArgs 
   auto k_steps = [&](int buf, f32x4 (&acc)[2][2]) {
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) acc[rb][0] = acc[rb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    constexpr int kTerms[6][2] = {{0, 0}, {0, 1}, {1, 0}, {1, 1}, {0, 2}, {2, 0}};
+    constexpr int kTerms[3][2] = {{0, 0}, {0, 1}, {1, 0}};
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      bf16x8 ax[2][3], az[2][3];
+      bf16x8 ax[2][2], az[2][2];
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
-        for (int pl = 0; pl < 3; ++pl) {
+        for (int pl = 0; pl < 2; ++pl) {
           ax[rb][pl] = *(const bf16x8*)&px[buf][pl][16 * rb + l16][32 * t + 8 * g4];
           az[rb][pl] = *(const bf16x8*)&pz[buf][pl][16 * rb + l16][32 * t + 8 * g4];
         }
       }
 #pragma unroll
-      for (int tm = 0; tm < 6; ++tm) {
+      for (int tm = 0; tm < 3; ++tm) {
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb) {
-          acc[rb][0] = mfma16_bf16(ax[rb][kTerms[tm][0]], wz[kTerms[tm][1]][t], acc[rb][0]);
-          acc[rb][1] = mfma16_bf16(az[rb][kTerms[tm][0]], wg[kTerms[tm][1]][t], acc[rb][1]);
+          acc[rb][0] = mfma16_f16(ax[rb][kTerms[tm][0]], wz[kTerms[tm][1]][t], acc[rb][0]);
+          acc[rb][1] = mfma16_f16(az[rb][kTerms[tm][0]], wg[kTerms[tm][1]][t], acc[rb][1]);
         }
+      }
+    }
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        acc[rb][0][r] = __builtin_ldexpf(acc[rb][0][r], -(ex_out + ewz));
+        acc[rb][1][r] = __builtin_ldexpf(acc[rb][1][r], -(ex_in + ewg));
       }
     }
   };
