@@ -1,5 +1,6 @@
-// FP32 matrix-core GEMM mainloop shared by the triangle-multiplication
-// contraction and the pair transition's output projection.
+// GEMM mainloops shared by the triangle-multiplication contraction and the
+// pair transition's output projection: FP32 matrix cores (gemm_nt_128) and
+// FP32-accurate fp16 planes (gemm_nt_128_f16).
 //
 // One work-group (256 threads, four waves) accumulates a 128 x 128 tile
 //   C[i][j] = sum_k A[i][k] B[j][k]
@@ -109,102 +110,12 @@ __device__ __forceinline__ void gemm_nt_128(const float* a, int64_t lda, const f
   }
 }
 
-// ------------------------------------------------ FP32-accurate, BF16 cores
+// ------------------------------------------------ FP32-accurate, fp16 cores
 //
-// The same 128 x 128 tile on v_mfma_f32_32x32x16_bf16: every FP32 element of
-// A and B is split exactly into three bfloat16 planes (split.hpp) as its
-// stage is written to LDS, and each 32 x 32 block sums the six terms down to
-// 2^-16 relative (hi hi, hi lo, lo hi, lo lo, hi rest, rest hi), FP32
-// rounding level.  Stages are 16 keys (one k step), double-buffered, so the
-// 2 x 2 x 3 planes fit the FP32 routine's 72 KB of LDS: 24 MFMAs per wave
-// per stage, each of the four blocks' six terms interleaved with the
-// other blocks'.
+// Stages of 16 keys (one k step), double-buffered; rows padded to 24 16-bit
+// values (48 B), conflict-free b128 reads.
 constexpr int kSplitK = 16;
-constexpr int kSplitRow = kSplitK + 8;  // bf16 per LDS row (48 B): conflict-free b128 reads
-
-typedef __bf16 SplitStage[3][kGemmTile][kSplitRow];  // planes hi, lo, rest
-
-// acc as gemm_nt_128, over keys 0 .. 16 nk - 1 (nk stages of 16 keys); the
-// same readability and 2 GiB conditions with 16 nk in place of 32 nk.
-__device__ __forceinline__ void gemm_nt_128_split(const float* a, int64_t lda, const float* b,
-                                                  int64_t ldb, int nk, SplitStage* As,
-                                                  SplitStage* Bs, f32x16 (&acc)[2][2]) {
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int half = lane >> 5;
-  const int l32 = lane & 31;
-  const int wi = (w >> 1) * 64;
-  const int wj = (w & 1) * 64;
-
-  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a, (127 * lda + kSplitK * nk) * 4);
-  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(b, (127 * ldb + kSplitK * nk) * 4);
-  // Thread (row = tid / 4 + 64 u, keys 4 (tid % 4) .. +3) of each stage.
-  const int lrow = tid >> 2;
-  const int lc4 = (tid & 3) * 4;
-  const uint32_t va = (uint32_t)((lrow * lda + lc4) * 4);
-  const uint32_t vb = (uint32_t)((lrow * ldb + lc4) * 4);
-  const uint32_t pa = (uint32_t)(64 * lda * 4);  // 64 rows further down
-  const uint32_t pb = (uint32_t)(64 * ldb * 4);
-
-  f32x4 ga[2], gb[2];
-  auto load = [&](int kt) {
-    const uint32_t s = (uint32_t)kt * (kSplitK * 4);
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      ga[u] = buffer_load_f4(ra, va + u * pa, s);
-      gb[u] = buffer_load_f4(rb, vb + u * pb, s);
-    }
-  };
-  auto store = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      bf16x4 h, l, r;
-      split3(ga[u], h, l, r);
-      *(bf16x4*)&As[buf][0][lrow + 64 * u][lc4] = h;
-      *(bf16x4*)&As[buf][1][lrow + 64 * u][lc4] = l;
-      *(bf16x4*)&As[buf][2][lrow + 64 * u][lc4] = r;
-      split3(gb[u], h, l, r);
-      *(bf16x4*)&Bs[buf][0][lrow + 64 * u][lc4] = h;
-      *(bf16x4*)&Bs[buf][1][lrow + 64 * u][lc4] = l;
-      *(bf16x4*)&Bs[buf][2][lrow + 64 * u][lc4] = r;
-    }
-  };
-
-  load(0);
-  store(0);
-  if (nk > 1) load(1);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    // Lane: rows wi + 32 rb + l32 of A and wj + 32 cb + l32 of B, keys
-    // 8 half .. 8 half + 7 of the stage, three planes each.
-    bf16x8 ap[2][3], bp[2][3];
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-#pragma unroll
-      for (int pl = 0; pl < 3; ++pl) {
-        ap[q][pl] = *(const bf16x8*)&As[buf][pl][wi + 32 * q + l32][8 * half];
-        bp[q][pl] = *(const bf16x8*)&Bs[buf][pl][wj + 32 * q + l32][8 * half];
-      }
-    }
-    constexpr int kTerms[6][2] = {{0, 0}, {0, 1}, {1, 0}, {1, 1}, {0, 2}, {2, 0}};
-#pragma unroll
-    for (int t = 0; t < 6; ++t) {
-#pragma unroll
-      for (int rb2 = 0; rb2 < 2; ++rb2) {
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
-          acc[rb2][cb] = mfma_bf16(ap[rb2][kTerms[t][0]], bp[cb][kTerms[t][1]], acc[rb2][cb]);
-      }
-    }
-    if (kt + 1 < nk) {
-      store(buf ^ 1);
-      if (kt + 2 < nk) load(kt + 2);
-    }
-    __syncthreads();
-  }
-}
+constexpr int kSplitRow = kSplitK + 8;
 
 // The same product on v_mfma_f32_32x32x16_f16 with power-of-two scaled fp16
 // (hi, lo) planes (split.hpp): row r of A is scaled by 2^ea[r] and row r of
