@@ -276,13 +276,14 @@ def bench_openfold3(args) -> dict:
             "max_abs_vs_native": diff,
         },
         "roofline": {
-            "kernel": (f"attention_{'kernel' if fp32_mfma else 'split_kernel'}<kAttnStrided>"
-                       " + staging (fpx_attn_strided)"),
+            "kernel": ("attention_kernel<kAttnStrided> + staging (fpx_attn_strided)" if fp32_mfma
+                       else "attention_split_kernel<kAttnStaged> + plane, mask and bias staging"
+                            " (fpx_attn_strided)"),
             "bound": "mfma", "achieved": round(tflops, 3), "peak": FP32_MFMA_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4),
             "traffic": recorded_traffic("openfold3/fp32-mfma" if fp32_mfma else "openfold3"),
             "flop_per_launch": flop, "avg_launch_ms": round(ms, 4),
-            **({} if fp32_mfma else split_executed(n, n, ms)),
+            **({} if fp32_mfma else split_executed(n, n, ms, fp16_planes=True)),
         },
         "cpu_baseline": None,
     }

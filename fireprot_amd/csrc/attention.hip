@@ -536,7 +536,7 @@ bool fp32_matrix_cores_selected() {
 }
 
 hipError_t launch_attention(int layout, const AttnArgs& a, hipStream_t stream) {
-  if (layout != kAttnHeadLast && !fp32_matrix_cores_selected()) return launch_attention_split(layout, a, stream);
+  if (layout == kAttnBlock && !fp32_matrix_cores_selected()) return launch_attention_split(layout, a, stream);
   // Query tiles cover the padded extent; key tiles stop at the last real key
   // (tiles wholly past n hold only -inf mask bias and contribute nothing).
   const int nqt = (int)((layout != kAttnHeadLast ? a.np : round_up(a.n, kBq)) / kBq);

@@ -54,7 +54,6 @@ namespace fpx {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kRowB = kHeadDim + 8;  // bf16 per LDS row: 80 bytes, conflict-free b128 reads
 
 // Block layout ring: stage s holds one key tile as four 2 KB planes (K hi,
 // K lo, V^T hi, V^T lo), each 32 rows of 64 bytes.  Tile t sits in stage
@@ -67,10 +66,8 @@ constexpr int kStageBytes = 4 * kPlaneBytes;
 // distinct banks in every group of 8 rows at 128 bytes per cycle and of 16
 // rows at 256 bytes per cycle.
 __device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
-// Waves per SIMD: the block layout fits four work-groups per CU (ring and
-// mask row within 40 KB of LDS at N <= 1536).
-template <int LAYOUT>
-constexpr int kWavesPerEu = LAYOUT == kAttnBlock ? 4 : 3;
+// Four waves per SIMD: four work-groups per CU (ring and mask row within
+// 40 KB of LDS at N <= 1536).
 
 // One global_load_lds_dwordx4: lane l copies 16 bytes from src into the LDS
 // at dst + 16 l (dst uniform across the wave).  Written as inline assembly
@@ -97,10 +94,7 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-typedef __bf16 KPlane[kBk][kRowB];       // [key][channel] (fp16 bits in the block layout)
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-typedef __bf16 VPlane[kHeadDim][kRowB];  // [channel][key position], see v_position
 
 // V^T keys are stored in the order in which the S^T accumulator registers
 // hold them: within each 16-key block, keys 0-3, 8-11, 4-7, 12-15.  Position
@@ -110,25 +104,21 @@ __device__ __forceinline__ int v_position(int g) {
   return (g >> 2) * 16 + perm * 4;
 }
 
-// LAYOUT kAttnBlock: the block's workspace (q, k [B][H][np][32], v^T
-// [B][H][32][np]).  kAttnStrided: a caller's q, k, v, out with (batch, head,
-// row) strides (fpx_attn_strided); K and V rows past n are clamped to row
-// n - 1 (finite values whose weights are exactly 0: their staged mask bias is
-// -inf), and V rows are transposed into the V^T planes on their way to LDS.
-// Both read the staged bias copies, mask rows and tile flags.
+// Both layouts read q, k and v^T in the plane layout (ProjArgs::planes) with
+// their per-tile scales, and the staged bias copies, mask rows and tile
+// flags.  LAYOUT kAttnBlock: the block's workspace, gated head-last output;
+// kAttnStaged: planes staged from a caller's strided q, k, v
+// (launch_stage_planes), output through the caller's strides, no gate.
 template <int LAYOUT>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kWavesPerEu<LAYOUT>, 4)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
   constexpr bool kBlock = LAYOUT == kAttnBlock;
-  // Block layout: the ring of key tiles (kStages x kStageBytes).  Strided
-  // layout: two register-staged tiles, K in three planes and V^T in two.
-  constexpr int kLdsBytes = kBlock ? kStages * kStageBytes : (int)(6 * sizeof(KPlane) + 4 * sizeof(VPlane));
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
-  auto& Ks = *reinterpret_cast<KPlane(*)[2][3]>(lds);
-  auto& Vs = *reinterpret_cast<VPlane(*)[2][2]>(lds + 6 * sizeof(KPlane));
+  static_assert(LAYOUT == kAttnBlock || LAYOUT == kAttnStaged, "plane layouts only");
+  // The ring of key tiles (kStages x kStageBytes).
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kStages * kStageBytes];
   // Mask-bias row of this outer row, nkt_all * kBk floats (dynamic).
   extern __shared__ __attribute__((aligned(16))) float Ms[];
-  __shared__ float Sk[kTileFlagWords * 32];  // block layout: 2^-e_k of each key tile
+  __shared__ float Sk[kTileFlagWords * 32];  // 2^-e_k of each key tile
 
   const uint32_t logical = xcd_remap(blockIdx.x, total);
   const int groups = (a.batch + kRowGroup - 1) / kRowGroup;
@@ -148,21 +138,17 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
   const int j0 = qt * kBq;
   const int jq = j0 + 32 * w + l32;
   const int qt32 = (j0 >> 5) + w;
-  const int row8 = tid >> 3;
-  const int col4 = (tid & 7) * 4;
 
   // Per-work-group buffer descriptors over the (b, h) slices and the wave's
   // bias fragments (h, qt32, all key tiles), as in the FP32 kernel.
   const int64_t bh = (int64_t)b * kHeads + h;
   const int64_t nt = a.np >> 5;
-  const int64_t slice = (int64_t)a.np * kHeadDim;
   const int64_t frag = ((int64_t)h * nt + qt32) * nt * 1024;
   const __amdgpu_buffer_rsrc_t rb = buffer(a.bias + frag, nt * 4096);
   const __amdgpu_buffer_rsrc_t rb2 = buffer(a.bias_l2 + frag, nt * 4096);
   const uint32_t ob = (uint32_t)lane * 16;
-  (void)slice;
 
-  // Block layout: per (b, h) a slice of np * 128 bytes, the hi plane and
+  // Per (b, h) a slice of np * 128 bytes, the hi plane and
   // then the lo plane of 16-bit values: q, k [np rows][32 channels], v^T
   // [np / 32 tiles][32 channels][32 key positions].  A tile's plane is 2 KB
   // contiguous.  Wave w fills plane w of a stage (K hi, K lo, V^T hi,
@@ -185,49 +171,11 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
     return *(const bf16x8*)(lds + stage * kStageBytes + plane * kPlaneBytes + (m ? rd1 : rd0));
   };
 
-  // Strided layout: register staging.  Rows: key t*32 + row8, clamped to
-  // n - 1; channels col4..+3.
-  const __amdgpu_buffer_rsrc_t rk =
-      buffer(a.k + b * a.ks[0] + h * a.ks[1], ((int64_t)(a.n - 1) * a.ks[2] + kHeadDim) * 4);
-  const __amdgpu_buffer_rsrc_t rv =
-      buffer(a.v + b * a.vs[0] + h * a.vs[1], ((int64_t)(a.n - 1) * a.vs[2] + kHeadDim) * 4);
-  auto row_of = [&](int t) -> uint32_t {
-    const int j = t * kBk + row8;
-    return (uint32_t)(j < a.n - 1 ? j : a.n - 1);
-  };
-  auto load_k = [&](int t) {
-    return buffer_f4(rk, row_of(t) * (uint32_t)a.ks[2] * 4 + (uint32_t)col4 * 4, 0);
-  };
-  auto load_v = [&](int t) {
-    return buffer_f4(rv, row_of(t) * (uint32_t)a.vs[2] * 4 + (uint32_t)col4 * 4, 0);
-  };
-  // Strided V: thread holds key row8, channels col4..+3; its position in the
-  // V^T planes' key order:
-  const int kpos = v_position(row8 >> 2) + (row8 & 3);
   auto load_frag = [&](__amdgpu_buffer_rsrc_t r, int t) -> f32x16 {
     const uint32_t s = (uint32_t)t * 4096;
     return cat4(buffer_f4(r, ob, s), buffer_f4(r, ob + 1024, s), buffer_f4(r, ob + 2048, s),
                 buffer_f4(r, ob + 3072, s));
   };
-  // Strided layout: K(t) into the three K planes, V(t) into the two V planes
-  // (thread: key row8, four consecutive channels).
-  auto store_k = [&](int buf, f32x4 kv) {
-    bf16x4 hi, lo, rest;
-    split3(kv, hi, lo, rest);
-    *(bf16x4*)&Ks[buf][0][row8][col4] = hi;
-    *(bf16x4*)&Ks[buf][1][row8][col4] = lo;
-    *(bf16x4*)&Ks[buf][2][row8][col4] = rest;
-  };
-  auto store_v = [&](int buf, f32x4 vv) {
-    bf16x4 hi, lo;
-    split2(vv, hi, lo);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      Vs[buf][0][col4 + e][kpos] = hi[e];
-      Vs[buf][1][col4 + e][kpos] = lo[e];
-    }
-  };
-
   // Row classification from the tile flags, as in the FP32 kernel.
   uint32_t mw[kTileFlagWords];
   uint32_t any = 0u, open = 0u;
@@ -249,7 +197,7 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
   // when the prepare projection's magnitude record bounds the logits
   // (kernels.hpp), so they are left out; the result is bit-identical.
   int nkt = nkt_all;
-  if constexpr (kBlock) {
+  {
     if (has_unmasked && a.magnitudes != nullptr && a.magnitudes[4] == 1u) {
       const float mq = __builtin_bit_cast(float, a.magnitudes[0]);
       const float mk = __builtin_bit_cast(float, a.magnitudes[1]);
@@ -275,10 +223,10 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
     const float* src = a.mbias + (int64_t)b * a.mb_stride;
     for (int k = 4 * tid; k < nkt * kBk; k += 4 * kThreads) *(f32x4*)&Ms[k] = *(const f32x4*)(src + k);
   }
-  // Block layout: the product scale 2^-(e_q + e_k) of this wave's queries
-  // and each key tile (read after the prologue's first barrier).
+  // The product scale 2^-(e_q + e_k) of this wave's queries and each key
+  // tile (read after the prologue's first barrier).
   float sq = 1.0f;
-  if constexpr (kBlock) {
+  {
     const int64_t per = (int64_t)kHeads * nt;
     const float* sc = a.scales + (int64_t)b * per + (int64_t)h * nt;
     sq = sc[qt32];
@@ -297,79 +245,50 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
     constexpr bool kExact = decltype(exact_tag)::value;
     const f32x16 zero16 = {};
 
-    // Q planes, the B operand of S^T: lane holds Q[jq][16m + 8half + e].
-    // Block layout: the fp16 (hi, lo) pairs of the prepare stage (the log2(e)
-    // of the fast path enters with the product scale); strided: split here,
-    // scaled by log2(e) on the fast path.
-    bf16x8 qh[2], ql[2], qr[2];
-    if constexpr (kBlock) {
+    // Q planes, the B operand of S^T: lane holds Q[jq][16m + 8half + e], the
+    // fp16 hi and lo planes (the log2(e) of the fast path enters with the
+    // product scale).
+    bf16x8 qh[2], ql[2];
+    {
       const uint8_t* src = reinterpret_cast<const uint8_t*>(a.q) + bh * slice_bytes + (int64_t)jq * 64;
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
         qh[m] = *(const bf16x8*)(src + 16 * (2 * m + half));
         ql[m] = *(const bf16x8*)(src + (slice_bytes >> 1) + 16 * (2 * m + half));
       }
-    } else {
-      const bool ok_q = jq < a.n;
-      const float* src = a.q + b * a.qs[0] + h * a.qs[1] + (int64_t)(ok_q ? jq : 0) * a.qs[2] + 8 * half;
-      const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const f32x4 u = ok_q ? *(const f32x4*)(src + 16 * m) : zero4;
-        const f32x4 v = ok_q ? *(const f32x4*)(src + 16 * m + 4) : zero4;
-        f32x8 q = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
-        if (!kExact) q *= kLog2e;
-        split3(q, qh[m], ql[m], qr[m]);
-      }
     }
 
-    // S^T of the tile in LDS buffer/stage buf, added to x (strided: the
-    // scaled bias on the fast path, zero on the exact path; block: zero); the
+    // S^T of the tile in ring stage buf (scaled by 2^(e_q + e_k)); the
     // smallest terms first.
-    auto scores = [&](int buf, f32x16 x) -> f32x16 {
+    auto scores = [&](int buf) -> f32x16 {
+      f32x16 x = zero16;
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
-        if constexpr (kBlock) {
-          const bf16x8 kh = plane_rd(buf, 0, m);
-          const bf16x8 kl = plane_rd(buf, 1, m);
-          x = mfma_f16(kl, qh[m], x);
-          x = mfma_f16(kh, ql[m], x);
-          x = mfma_f16(kh, qh[m], x);
-        } else {
-          const bf16x8 kh = *(const bf16x8*)&Ks[buf][0][l32][16 * m + 8 * half];
-          const bf16x8 kl = *(const bf16x8*)&Ks[buf][1][l32][16 * m + 8 * half];
-          const bf16x8 kr = *(const bf16x8*)&Ks[buf][2][l32][16 * m + 8 * half];
-          x = mfma_bf16(kr, qh[m], x);
-          x = mfma_bf16(kh, qr[m], x);
-          x = mfma_bf16(kl, ql[m], x);
-          x = mfma_bf16(kl, qh[m], x);
-          x = mfma_bf16(kh, ql[m], x);
-          x = mfma_bf16(kh, qh[m], x);
-        }
+        const bf16x8 kh = plane_rd(buf, 0, m);
+        const bf16x8 kl = plane_rd(buf, 1, m);
+        x = mfma_f16(kl, qh[m], x);
+        x = mfma_f16(kh, ql[m], x);
+        x = mfma_f16(kh, qh[m], x);
       }
       return x;
     };
-    // The logits of tile t from its product acc: the mask bias on masked
-    // tiles (fast, in log2 units), or fl(fl(s + mask) + bias) in natural
-    // units (exact).  Strided: acc already holds the fast path's bias; block:
-    // x holds the bias (fast) and acc the scaled product (s = acc 2^-(e_q + e_k),
-    // an exact scaling).
+    // The logits of tile t from its product acc (s = acc 2^-(e_q + e_k), an
+    // exact scaling): with x holding the bias in log2 units, plus the mask
+    // bias on masked tiles (fast), or fl(fl(s + mask) + bias) in natural
+    // units (exact).
     auto finish = [&](f32x16& x, const f32x16& acc, int t) {
-      float st = 1.0f;
-      if constexpr (kBlock) st = sq * Sk[t];
+      const float st = sq * Sk[t];
       if (kExact) {
         const f32x16 mb = mask_vals(t);
         const f32x16 bias = load_frag(rb, t);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) x[r] = ((kBlock ? acc[r] * st : acc[r]) + mb[r]) + bias[r];
+        for (int r = 0; r < 16; ++r) x[r] = ((acc[r] * st) + mb[r]) + bias[r];
         return;
       }
-      if constexpr (kBlock) {
+      {
         const float sl = st * kLog2e;
 #pragma unroll
         for (int r = 0; r < 16; ++r) x[r] = __builtin_fmaf(acc[r], sl, x[r]);
-      } else {
-        x = acc;
       }
       if (masked(t)) {
         const f32x16 mb = mask_vals(t);
@@ -462,8 +381,8 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
     auto pv = [&](int buf, const bf16x8 (&ph)[2], const bf16x8 (&pl)[2]) {
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
-        const bf16x8 vh = kBlock ? plane_rd(buf, 2, m) : *(const bf16x8*)&Vs[buf][0][l32][16 * m + 8 * half];
-        const bf16x8 vl = kBlock ? plane_rd(buf, 3, m) : *(const bf16x8*)&Vs[buf][1][l32][16 * m + 8 * half];
+        const bf16x8 vh = plane_rd(buf, 2, m);
+        const bf16x8 vl = plane_rd(buf, 3, m);
         o = mfma_bf16(vl, ph[m], o);
         o = mfma_bf16(vh, pl[m], o);
         o = mfma_bf16(vh, ph[m], o);
@@ -472,99 +391,52 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
 
     auto clamp = [&](int t) { return t < last ? t : last; };
     int kt = 0;
-    if constexpr (kBlock) {
-      // Prologue: tiles 0-2 on their way into stages 0-2; S^T(0) once tiles
-      // 0 and 1 have landed.  Iteration t reads K(t+1) and V(t) and starts
-      // tile t+3 into the stage that held tile t-1, which every wave left
-      // behind at the previous barrier.  The copy is issued after the
-      // logits, whose bias-fragment loads the compiler waits for with a
-      // count that also covers any later load.  Tiles past the last are
-      // clamped (in range, never used).
-      auto stage = [](int t) { return t & (kStages - 1); };
-      f32x16 x_a = init(0);
-      f32x16 x_b = init(clamp(1));
-      dma(0, 0);
-      dma(clamp(1), 1);
-      dma(clamp(2), 2);
-      wait_vmcnt<2>();
+    // Prologue: tiles 0-2 on their way into stages 0-2; S^T(0) once tiles
+    // 0 and 1 have landed.  Iteration t reads K(t+1) and V(t) and starts
+    // tile t+3 into the stage that held tile t-1, which every wave left
+    // behind at the previous barrier.  The copy is issued after the
+    // logits, whose bias-fragment loads the compiler waits for with a
+    // count that also covers any later load.  Tiles past the last are
+    // clamped (in range, never used).
+    auto stage = [](int t) { return t & (kStages - 1); };
+    f32x16 x_a = init(0);
+    f32x16 x_b = init(clamp(1));
+    dma(0, 0);
+    dma(clamp(1), 1);
+    dma(clamp(2), 2);
+    wait_vmcnt<2>();
+    __syncthreads();
+    finish(x_a, scores(0), 0);
+    auto body = [&](int t, f32x16& cur, f32x16& nxt) {
+      const f32x16 acc = scores(stage(t + 1));
+      bf16x8 ph[2], pl[2];
+      softmax(cur, ph, pl);
+      pv(stage(t), ph, pl);
+      finish(nxt, acc, t + 1);
+      dma(clamp(t + 3), stage(t + 3));
+      cur = init(clamp(t + 2));
+      // Tile t+2 has landed once at most this iteration's two tile loads
+      // and (fast path) four bias-fragment loads are outstanding: vector
+      // memory loads retire in issue order.
+      wait_vmcnt<kExact ? 2 : 6>();
       __syncthreads();
-      finish(x_a, scores(0, zero16), 0);
-      auto body = [&](int t, f32x16& cur, f32x16& nxt) {
-        const f32x16 acc = scores(stage(t + 1), zero16);
-        bf16x8 ph[2], pl[2];
-        softmax(cur, ph, pl);
-        pv(stage(t), ph, pl);
-        finish(nxt, acc, t + 1);
-        dma(clamp(t + 3), stage(t + 3));
-        cur = init(clamp(t + 2));
-        // Tile t+2 has landed once at most this iteration's two tile loads
-        // and (fast path) four bias-fragment loads are outstanding: vector
-        // memory loads retire in issue order.
-        wait_vmcnt<kExact ? 2 : 6>();
-        __syncthreads();
-      };
-      auto tail = [&](const f32x16& cur, int t) {
-        bf16x8 ph[2], pl[2];
-        softmax(cur, ph, pl);
-        pv(stage(t), ph, pl);
-      };
-      for (; kt + 2 < nkt; kt += 2) {
-        body(kt, x_a, x_b);
-        body(kt + 1, x_b, x_a);
-      }
-      if (kt + 1 < nkt) {
-        body(kt, x_a, x_b);
-        tail(x_b, kt + 1);
-      } else {
-        tail(x_a, kt);
-      }
-      wait_vmcnt<0>();  // the clamped tail loads land before the LDS is released
-    } else {
-      // Prologue: K(0), K(1), V(0) into LDS; S^T(0); K(2), V(1) in flight.
-      f32x16 x_a = init(0);
-      f32x16 x_b = init(clamp(1));
-      store_k(0, load_k(0));
-      store_v(0, load_v(0));
-      store_k(1, load_k(clamp(1)));
-      f32x4 kreg = load_k(clamp(2));
-      f32x4 vreg = load_v(clamp(1));
-      __syncthreads();
-      finish(x_a, scores(0, kExact ? zero16 : x_a), 0);
-      __syncthreads();  // every wave is done with K(0) before Ks[0] is refilled
-
-      // Iteration t: Ks[(t+1)&1] = K(t+1), Vs[t&1] = V(t); cur = logits of
-      // tile t; nxt = start value of tile t+1; kreg = K(t+2) and vreg =
-      // V(t+1) in flight.  Indices past the last tile are clamped (in range,
-      // never used).
-      auto body = [&](int t, f32x16& cur, f32x16& nxt) {
-        const f32x16 acc = scores((t + 1) & 1, kExact ? zero16 : nxt);
-        bf16x8 ph[2], pl[2];
-        softmax(cur, ph, pl);
-        pv(t & 1, ph, pl);
-        finish(nxt, acc, t + 1);
-        cur = init(clamp(t + 2));
-        store_k(t & 1, kreg);
-        store_v((t + 1) & 1, vreg);
-        kreg = load_k(clamp(t + 3));
-        vreg = load_v(clamp(t + 2));
-        __syncthreads();
-      };
-      auto tail = [&](const f32x16& cur, int t) {
-        bf16x8 ph[2], pl[2];
-        softmax(cur, ph, pl);
-        pv(t & 1, ph, pl);
-      };
-      for (; kt + 2 < nkt; kt += 2) {
-        body(kt, x_a, x_b);
-        body(kt + 1, x_b, x_a);
-      }
-      if (kt + 1 < nkt) {
-        body(kt, x_a, x_b);
-        tail(x_b, kt + 1);
-      } else {
-        tail(x_a, kt);
-      }
+    };
+    auto tail = [&](const f32x16& cur, int t) {
+      bf16x8 ph[2], pl[2];
+      softmax(cur, ph, pl);
+      pv(stage(t), ph, pl);
+    };
+    for (; kt + 2 < nkt; kt += 2) {
+      body(kt, x_a, x_b);
+      body(kt + 1, x_b, x_a);
     }
+    if (kt + 1 < nkt) {
+      body(kt, x_a, x_b);
+      tail(x_b, kt + 1);
+    } else {
+      tail(x_a, kt);
+    }
+    wait_vmcnt<0>();  // the clamped tail loads land before the LDS is released
   };
   if (has_unmasked) {
     run(std::false_type{});
@@ -599,19 +471,130 @@ hipError_t launch_attention_split(int layout, const AttnArgs& a, hipStream_t str
   const uint64_t total = groups * kRowGroup * kHeads * nqt;
   if (total == 0) return hipSuccess;
   if (total > 0x7fffffffull) return hipErrorInvalidValue;
-  if (a.tile_flags == nullptr || a.bias_l2 == nullptr || nkt > kTileFlagWords * 32)
+  if (a.tile_flags == nullptr || a.bias_l2 == nullptr || a.scales == nullptr ||
+      nkt > kTileFlagWords * 32)
     return hipErrorInvalidValue;
-  if (layout == kAttnBlock && a.scales == nullptr) return hipErrorInvalidValue;
   const size_t mask_row_bytes = (size_t)nkt * kBk * sizeof(float);
   if (layout == kAttnBlock) {
     hipLaunchKernelGGL(attention_split_kernel<kAttnBlock>, dim3((uint32_t)total), dim3(kThreads),
                        mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total);
-  } else if (layout == kAttnStrided) {
-    hipLaunchKernelGGL(attention_split_kernel<kAttnStrided>, dim3((uint32_t)total), dim3(kThreads),
+  } else if (layout == kAttnStaged) {
+    hipLaunchKernelGGL(attention_split_kernel<kAttnStaged>, dim3((uint32_t)total), dim3(kThreads),
                        mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total);
   } else {
     return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------- staging
+// A caller's strided q, k, v (element (b, h, j, c) at b s[0] + h s[1] +
+// j s[2] + c) into the plane layout for kAttnStaged, one wave per (outer row
+// b, head h, 32-row tile t, operand):
+//   q, k: rows 32t .. 32t + 31 (zero past n) times 2^e, e chosen so that
+//         the tile's max |value| 2^e lies in [2^14, 2^15) (|e| <=
+//         kPlaneExpMax; 0 for a zero or non-finite tile), as fp16 hi and lo
+//         planes [np][32] of the (b, h) slice, and 2^-e at
+//         scales[((op batch + b) 4 + h) (np / 32) + t] (op 0: q, 1: k);
+//   v:    the tile transposed to [32 channels][32 key positions] (a tile's
+//         keys in v_position order) as bf16 hi and lo planes.
+// Each wave transposes v through its own LDS tile; no work-group barrier.
+__global__ __launch_bounds__(256) void stage_planes_kernel(AttnArgs a, uint8_t* qp, uint8_t* kp,
+                                                           uint8_t* vp, float* scales,
+                                                           int64_t waves) {
+  __shared__ float tv[4][32][33];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int64_t gw = (int64_t)blockIdx.x * 4 + w;
+  if (gw >= waves) return;  // whole waves
+  const int nt = a.np >> 5;
+  const int op = (int)(gw % 3);
+  const int64_t rest = gw / 3;
+  const int t = (int)(rest % nt);
+  const int64_t bh = rest / nt;
+  const int h = (int)(bh & 3);
+  const int64_t b = bh >> 2;
+  const int r = lane >> 1;
+  const int c0 = (lane & 1) * 16;
+  const int j = 32 * t + r;
+  const float* src = op == 0 ? a.q : op == 1 ? a.k : a.v;
+  const int64_t* st = op == 0 ? a.qs : op == 1 ? a.ks : a.vs;
+  f32x4 x[4] = {};
+  if (j < a.n) {
+    const float* row = src + b * st[0] + h * st[1] + (int64_t)j * st[2] + c0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = *(const f32x4*)(row + 4 * i);
+  }
+  const int64_t slice_bytes = (int64_t)a.np * 128;
+  uint8_t* dst = (op == 0 ? qp : op == 1 ? kp : vp) + bh * slice_bytes;
+  if (op < 2) {
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      m = __builtin_elementwise_maximum(
+          m, __builtin_elementwise_maximum(
+                 __builtin_elementwise_maximum(__builtin_fabsf(x[i].x), __builtin_fabsf(x[i].y)),
+                 __builtin_elementwise_maximum(__builtin_fabsf(x[i].z), __builtin_fabsf(x[i].w))));
+    m = wave_max(m);
+    int e = plane_exp(m);
+    e = e < -kPlaneExpMax ? -kPlaneExpMax : e > kPlaneExpMax ? kPlaneExpMax : e;
+    const float f = __builtin_ldexpf(1.0f, e);
+    bf16x8 hi[2], lo[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const f32x4 u = x[2 * i] * f, v = x[2 * i + 1] * f;
+      split_f16(f32x8{u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w}, hi[i], lo[i]);
+    }
+    uint8_t* o = dst + (int64_t)j * 64 + c0 * 2;
+    *(bf16x8*)o = hi[0];
+    *(bf16x8*)(o + 16) = hi[1];
+    *(bf16x8*)(o + (slice_bytes >> 1)) = lo[0];
+    *(bf16x8*)(o + (slice_bytes >> 1) + 16) = lo[1];
+    if (lane == 0) scales[(((int64_t)op * a.batch + b) * kHeads + h) * nt + t] = __builtin_ldexpf(1.0f, -e);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      tv[w][r][c0 + 4 * i + 0] = x[i].x;
+      tv[w][r][c0 + 4 * i + 1] = x[i].y;
+      tv[w][r][c0 + 4 * i + 2] = x[i].z;
+      tv[w][r][c0 + 4 * i + 3] = x[i].w;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // lane: channel c = lane / 2, key positions p0 .. p0 + 15
+    const int c = lane >> 1;
+    const int p0 = (lane & 1) * 16;
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int p = p0 + i;
+      const int g = 4 * (p >> 4) + v_position(((p >> 2) & 3)) / 4;  // (0, 2, 1, 3) is its own inverse
+      v[i] = tv[w][4 * g + (p & 3)][c];
+    }
+    bf16x8 hi[2], lo[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      split2(f32x8{v[8 * i], v[8 * i + 1], v[8 * i + 2], v[8 * i + 3], v[8 * i + 4], v[8 * i + 5],
+                   v[8 * i + 6], v[8 * i + 7]},
+             hi[i], lo[i]);
+    uint8_t* o = dst + (int64_t)t * kPlaneBytes + c * 64 + p0 * 2;
+    *(bf16x8*)o = hi[0];
+    *(bf16x8*)(o + 16) = hi[1];
+    *(bf16x8*)(o + (slice_bytes >> 1)) = lo[0];
+    *(bf16x8*)(o + (slice_bytes >> 1) + 16) = lo[1];
+  }
+}
+
+hipError_t launch_stage_planes(const AttnArgs& a, void* q_planes, void* k_planes, void* v_planes,
+                               float* scales, hipStream_t stream) {
+  const int64_t waves = 3 * (int64_t)a.batch * kHeads * (a.np / 32);
+  if (waves == 0) return hipSuccess;
+  const int64_t blocks = (waves + 3) / 4;
+  if (blocks > 0x7fffffffll || a.np % kBq) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(stage_planes_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream, a,
+                     static_cast<uint8_t*>(q_planes), static_cast<uint8_t*>(k_planes),
+                     static_cast<uint8_t*>(v_planes), scales, waves);
   return hipGetLastError();
 }
 

@@ -182,9 +182,11 @@ int block_impl(int dtype, const void* z, int64_t z_stride0, int64_t z_stride1, c
 
 // Workspace of fpx_attn_strided, 256-byte aligned segments:
 //   bias [4][np][np] float in fragment order, twice (as is, scaled by log2(e));
-//   mbias [batch][np] float; tile flags [batch][kTileFlagParts * kTileFlagWords] uint32.
+//   mbias [batch][np] float; tile flags [batch][kTileFlagParts * kTileFlagWords] uint32;
+//   q, k and v planes [batch][4] slices of np * 128 bytes each; their scales
+//   [2][batch][4][np / 32] float.
 struct StridedWorkspace {
-  size_t bias, bias_l2, mbias, flags, total;
+  size_t bias, bias_l2, mbias, flags, qp, kp, vp, scales, total;
 };
 
 StridedWorkspace strided_workspace(int batch, int n) {
@@ -195,8 +197,13 @@ StridedWorkspace strided_workspace(int batch, int n) {
   w.bias_l2 = seg((size_t)fpx::kHeads * np * np * sizeof(float));
   w.mbias = 2 * w.bias_l2;
   w.flags = w.mbias + seg((size_t)batch * np * sizeof(float));
-  w.total = w.flags + seg((size_t)batch * fpx::kTileFlagParts * fpx::kTileFlagWords *
-                           sizeof(uint32_t));
+  w.qp = w.flags + seg((size_t)batch * fpx::kTileFlagParts * fpx::kTileFlagWords *
+                        sizeof(uint32_t));
+  const size_t planes = seg((size_t)batch * fpx::kHeads * np * 128);
+  w.kp = w.qp + planes;
+  w.vp = w.kp + planes;
+  w.scales = w.vp + planes;
+  w.total = w.scales + seg(2 * (size_t)batch * fpx::kHeads * (np / 32) * sizeof(float));
   return w;
 }
 
@@ -496,7 +503,19 @@ int fpx_attn_strided(const float* q, int64_t q_sb, int64_t q_sh, int64_t q_sn, c
   a.batch = batch;
   a.n = n;
   a.np = np;
-  return status(fpx::launch_attention(fpx::kAttnStrided, a, st));
+  if (fpx::fp32_matrix_cores_selected()) return status(fpx::launch_attention(fpx::kAttnStrided, a, st));
+  // q, k, v into the plane layout, then the block attention's kernel on it
+  void* qp = base + ws.qp;
+  void* kp = base + ws.kp;
+  void* vp = base + ws.vp;
+  float* scales = as<float>(base + ws.scales);
+  e = fpx::launch_stage_planes(a, qp, kp, vp, scales, st);
+  if (e != hipSuccess) return status(e);
+  a.q = static_cast<const float*>(qp);
+  a.k = static_cast<const float*>(kp);
+  a.v = static_cast<const float*>(vp);
+  a.scales = scales;
+  return status(fpx::launch_attention_split(fpx::kAttnStaged, a, st));
 }
 
 size_t fpx_tri_mul_workspace_bytes(int n, int c_z, int c_hidden) {

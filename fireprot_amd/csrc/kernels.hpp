@@ -37,7 +37,10 @@ namespace fpx {
 //                mbias, tile_flags, bias, bias_l2 : staged as for kAttnBlock
 //                               (launch_mask_rows, launch_stage_bias), np a
 //                               multiple of 128
-enum AttnLayout { kAttnBlock = 0, kAttnHeadLast = 1, kAttnStrided = 2 };
+// kAttnStaged:  kAttnStrided's operands after launch_stage_planes: q, k, v
+//                in the plane layout with their scales (as kAttnBlock
+//                reads them), out through the os strides, no gate
+enum AttnLayout { kAttnBlock = 0, kAttnHeadLast = 1, kAttnStrided = 2, kAttnStaged = 3 };
 
 // Words of per-row tile flags: 32-key tiles of np <= 4096 keys.
 constexpr int kTileFlagWords = 4;
@@ -91,11 +94,18 @@ struct AttnArgs {
 // cores (v_mfma_f32_32x32x2_f32) instead of their exact bf16 splits.
 bool fp32_matrix_cores_selected();
 
-// kAttnBlock and kAttnStrided run attention_split_kernel (FP32-accurate
-// products on the BF16 matrix cores) unless fp32_matrix_cores_selected(),
-// which selects attention_kernel; kAttnHeadLast always runs attention_kernel.
+// launch_attention: kAttnBlock runs attention_split_kernel (FP32-accurate
+// products on the 16-bit matrix cores) unless fp32_matrix_cores_selected(),
+// which selects attention_kernel; kAttnStrided and kAttnHeadLast run
+// attention_kernel.  launch_attention_split runs attention_split_kernel for
+// kAttnBlock or kAttnStaged.
 hipError_t launch_attention(int layout, const AttnArgs& args, hipStream_t stream);
 hipError_t launch_attention_split(int layout, const AttnArgs& args, hipStream_t stream);
+// kAttnStrided q, k, v of args -> the plane layout of kAttnStaged: q_planes,
+// k_planes, v_planes each [batch][4] slices of np * 128 bytes, scales
+// [2][batch][4][np / 32] floats.
+hipError_t launch_stage_planes(const AttnArgs& args, void* q_planes, void* k_planes,
+                               void* v_planes, float* scales, hipStream_t stream);
 
 // --------------------------------------------------------------- projection
 // Row tiles are 32 consecutive j of one outer row i; A rows are read at
