@@ -498,36 +498,38 @@ hipError_t launch_attention_split(int layout, const AttnArgs& a, hipStream_t str
 //         scales[((op batch + b) 4 + h) (np / 32) + t] (op 0: q, 1: k);
 //   v:    the tile transposed to [32 channels][32 key positions] (a tile's
 //         keys in v_position order) as bf16 hi and lo planes.
-// Each wave transposes v through its own LDS tile; no work-group barrier.
+// partial (nullable): each work-group's NaN-propagating max |q|, |k|, |v| at
+// partial[3 blockIdx.x + op] (0 for operands it did not stage), reduced by
+// reduce_magnitudes_kernel.  Each wave transposes v through its own LDS
+// tile.
 __global__ __launch_bounds__(256) void stage_planes_kernel(AttnArgs a, uint8_t* qp, uint8_t* kp,
                                                            uint8_t* vp, float* scales,
-                                                           int64_t waves) {
+                                                           float* partial, int64_t waves) {
   __shared__ float tv[4][32][33];
+  __shared__ float wmax[4][3];
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int64_t gw = (int64_t)blockIdx.x * 4 + w;
-  if (gw >= waves) return;  // whole waves
   const int nt = a.np >> 5;
-  const int op = (int)(gw % 3);
-  const int64_t rest = gw / 3;
-  const int t = (int)(rest % nt);
-  const int64_t bh = rest / nt;
-  const int h = (int)(bh & 3);
-  const int64_t b = bh >> 2;
-  const int r = lane >> 1;
-  const int c0 = (lane & 1) * 16;
-  const int j = 32 * t + r;
-  const float* src = op == 0 ? a.q : op == 1 ? a.k : a.v;
-  const int64_t* st = op == 0 ? a.qs : op == 1 ? a.ks : a.vs;
-  f32x4 x[4] = {};
-  if (j < a.n) {
-    const float* row = src + b * st[0] + h * st[1] + (int64_t)j * st[2] + c0;
+  float mq = 0.f, mk = 0.f, mv = 0.f;  // this wave's maxima (NaN-propagating)
+  if (gw < waves) {  // whole waves
+    const int op = (int)(gw % 3);
+    const int64_t rest = gw / 3;
+    const int t = (int)(rest % nt);
+    const int64_t bh = rest / nt;
+    const int h = (int)(bh & 3);
+    const int64_t b = bh >> 2;
+    const int r = lane >> 1;
+    const int c0 = (lane & 1) * 16;
+    const int j = 32 * t + r;
+    const float* src = op == 0 ? a.q : op == 1 ? a.k : a.v;
+    const int64_t* st = op == 0 ? a.qs : op == 1 ? a.ks : a.vs;
+    f32x4 x[4] = {};
+    if (j < a.n) {
+      const float* row = src + b * st[0] + h * st[1] + (int64_t)j * st[2] + c0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = *(const f32x4*)(row + 4 * i);
-  }
-  const int64_t slice_bytes = (int64_t)a.np * 128;
-  uint8_t* dst = (op == 0 ? qp : op == 1 ? kp : vp) + bh * slice_bytes;
-  if (op < 2) {
+      for (int i = 0; i < 4; ++i) x[i] = *(const f32x4*)(row + 4 * i);
+    }
     float m = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -536,65 +538,126 @@ __global__ __launch_bounds__(256) void stage_planes_kernel(AttnArgs a, uint8_t* 
                  __builtin_elementwise_maximum(__builtin_fabsf(x[i].x), __builtin_fabsf(x[i].y)),
                  __builtin_elementwise_maximum(__builtin_fabsf(x[i].z), __builtin_fabsf(x[i].w))));
     m = wave_max(m);
-    int e = plane_exp(m);
-    e = e < -kPlaneExpMax ? -kPlaneExpMax : e > kPlaneExpMax ? kPlaneExpMax : e;
-    const float f = __builtin_ldexpf(1.0f, e);
-    bf16x8 hi[2], lo[2];
+    const int64_t slice_bytes = (int64_t)a.np * 128;
+    uint8_t* dst = (op == 0 ? qp : op == 1 ? kp : vp) + bh * slice_bytes;
+    if (op < 2) {
+      if (op == 0) mq = m;
+      else mk = m;
+      int e = plane_exp(m);
+      e = e < -kPlaneExpMax ? -kPlaneExpMax : e > kPlaneExpMax ? kPlaneExpMax : e;
+      const float f = __builtin_ldexpf(1.0f, e);
+      bf16x8 hi[2], lo[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const f32x4 u = x[2 * i] * f, v = x[2 * i + 1] * f;
-      split_f16(f32x8{u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w}, hi[i], lo[i]);
+      for (int i = 0; i < 2; ++i) {
+        const f32x4 u = x[2 * i] * f, v = x[2 * i + 1] * f;
+        split_f16(f32x8{u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w}, hi[i], lo[i]);
+      }
+      uint8_t* o = dst + (int64_t)j * 64 + c0 * 2;
+      *(bf16x8*)o = hi[0];
+      *(bf16x8*)(o + 16) = hi[1];
+      *(bf16x8*)(o + (slice_bytes >> 1)) = lo[0];
+      *(bf16x8*)(o + (slice_bytes >> 1) + 16) = lo[1];
+      if (lane == 0)
+        scales[(((int64_t)op * a.batch + b) * kHeads + h) * nt + t] = __builtin_ldexpf(1.0f, -e);
+    } else {
+      mv = m;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        tv[w][r][c0 + 4 * i + 0] = x[i].x;
+        tv[w][r][c0 + 4 * i + 1] = x[i].y;
+        tv[w][r][c0 + 4 * i + 2] = x[i].z;
+        tv[w][r][c0 + 4 * i + 3] = x[i].w;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // lane: channel c = lane / 2, key positions p0 .. p0 + 15
+      const int c = lane >> 1;
+      const int p0 = (lane & 1) * 16;
+      float v[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int p = p0 + i;
+        const int g = 4 * (p >> 4) + v_position((p >> 2) & 3) / 4;  // (0, 2, 1, 3) is its own inverse
+        v[i] = tv[w][4 * g + (p & 3)][c];
+      }
+      bf16x8 hi[2], lo[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        split2(f32x8{v[8 * i], v[8 * i + 1], v[8 * i + 2], v[8 * i + 3], v[8 * i + 4],
+                     v[8 * i + 5], v[8 * i + 6], v[8 * i + 7]},
+               hi[i], lo[i]);
+      uint8_t* o = dst + (int64_t)t * kPlaneBytes + c * 64 + p0 * 2;
+      *(bf16x8*)o = hi[0];
+      *(bf16x8*)(o + 16) = hi[1];
+      *(bf16x8*)(o + (slice_bytes >> 1)) = lo[0];
+      *(bf16x8*)(o + (slice_bytes >> 1) + 16) = lo[1];
     }
-    uint8_t* o = dst + (int64_t)j * 64 + c0 * 2;
-    *(bf16x8*)o = hi[0];
-    *(bf16x8*)(o + 16) = hi[1];
-    *(bf16x8*)(o + (slice_bytes >> 1)) = lo[0];
-    *(bf16x8*)(o + (slice_bytes >> 1) + 16) = lo[1];
-    if (lane == 0) scales[(((int64_t)op * a.batch + b) * kHeads + h) * nt + t] = __builtin_ldexpf(1.0f, -e);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      tv[w][r][c0 + 4 * i + 0] = x[i].x;
-      tv[w][r][c0 + 4 * i + 1] = x[i].y;
-      tv[w][r][c0 + 4 * i + 2] = x[i].z;
-      tv[w][r][c0 + 4 * i + 3] = x[i].w;
+  }
+  if (partial != nullptr) {
+    if (lane == 0) {
+      wmax[w][0] = mq;
+      wmax[w][1] = mk;
+      wmax[w][2] = mv;
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // lane: channel c = lane / 2, key positions p0 .. p0 + 15
-    const int c = lane >> 1;
-    const int p0 = (lane & 1) * 16;
-    float v[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int p = p0 + i;
-      const int g = 4 * (p >> 4) + v_position(((p >> 2) & 3)) / 4;  // (0, 2, 1, 3) is its own inverse
-      v[i] = tv[w][4 * g + (p & 3)][c];
+    __syncthreads();
+    if (threadIdx.x < 3) {
+      const int op = threadIdx.x;
+      partial[3 * (int64_t)blockIdx.x + op] = __builtin_elementwise_maximum(
+          __builtin_elementwise_maximum(wmax[0][op], wmax[1][op]),
+          __builtin_elementwise_maximum(wmax[2][op], wmax[3][op]));
     }
-    bf16x8 hi[2], lo[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-      split2(f32x8{v[8 * i], v[8 * i + 1], v[8 * i + 2], v[8 * i + 3], v[8 * i + 4], v[8 * i + 5],
-                   v[8 * i + 6], v[8 * i + 7]},
-             hi[i], lo[i]);
-    uint8_t* o = dst + (int64_t)t * kPlaneBytes + c * 64 + p0 * 2;
-    *(bf16x8*)o = hi[0];
-    *(bf16x8*)(o + 16) = hi[1];
-    *(bf16x8*)(o + (slice_bytes >> 1)) = lo[0];
-    *(bf16x8*)(o + (slice_bytes >> 1) + 16) = lo[1];
   }
 }
 
+// magnitudes[op] = max(magnitudes[op], partial[3 i + op]) over the count
+// work-groups (op < 3; the record starts zeroed), one atomic per word and
+// work-group; work-group 0 sets magnitudes[4] = 1.
+__global__ __launch_bounds__(256) void reduce_magnitudes_kernel(const float* __restrict__ partial,
+                                                                int64_t count,
+                                                                uint32_t* __restrict__ magnitudes) {
+  __shared__ float part[4][3];
+  float m[3] = {0.f, 0.f, 0.f};
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (int64_t)gridDim.x * 256) {
+#pragma unroll
+    for (int op = 0; op < 3; ++op) m[op] = __builtin_elementwise_maximum(m[op], partial[3 * i + op]);
+  }
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int op = 0; op < 3; ++op) {
+    const float wm = wave_max(m[op]);
+    if (lane == 0) part[w][op] = wm;
+  }
+  __syncthreads();
+  if (threadIdx.x < 3) {
+    const int op = threadIdx.x;
+    const float r = __builtin_elementwise_maximum(__builtin_elementwise_maximum(part[0][op], part[1][op]),
+                                                  __builtin_elementwise_maximum(part[2][op], part[3][op]));
+    atomicMax(&magnitudes[op], __builtin_bit_cast(uint32_t, r));
+    if (blockIdx.x == 0 && op == 0) magnitudes[4] = 1u;
+  }
+}
+
+int64_t stage_planes_groups(const AttnArgs& a) {
+  return (3 * (int64_t)a.batch * kHeads * (a.np / 32) + 3) / 4;
+}
+
 hipError_t launch_stage_planes(const AttnArgs& a, void* q_planes, void* k_planes, void* v_planes,
-                               float* scales, hipStream_t stream) {
+                               float* scales, float* partial, uint32_t* magnitudes,
+                               hipStream_t stream) {
   const int64_t waves = 3 * (int64_t)a.batch * kHeads * (a.np / 32);
   if (waves == 0) return hipSuccess;
-  const int64_t blocks = (waves + 3) / 4;
+  const int64_t blocks = stage_planes_groups(a);
   if (blocks > 0x7fffffffll || a.np % kBq) return hipErrorInvalidValue;
+  if ((partial == nullptr) != (magnitudes == nullptr)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(stage_planes_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream, a,
                      static_cast<uint8_t*>(q_planes), static_cast<uint8_t*>(k_planes),
-                     static_cast<uint8_t*>(v_planes), scales, waves);
+                     static_cast<uint8_t*>(v_planes), scales, partial, waves);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || magnitudes == nullptr) return e;
+  const int64_t rgroups = (blocks + 255) / 256 < 256 ? (blocks + 255) / 256 : 256;
+  hipLaunchKernelGGL(reduce_magnitudes_kernel, dim3((uint32_t)rgroups), dim3(256), 0, stream,
+                     partial, blocks, magnitudes);
   return hipGetLastError();
 }
 

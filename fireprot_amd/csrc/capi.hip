@@ -184,9 +184,10 @@ int block_impl(int dtype, const void* z, int64_t z_stride0, int64_t z_stride1, c
 //   bias [4][np][np] float in fragment order, twice (as is, scaled by log2(e));
 //   mbias [batch][np] float; tile flags [batch][kTileFlagParts * kTileFlagWords] uint32;
 //   q, k and v planes [batch][4] slices of np * 128 bytes each; their scales
-//   [2][batch][4][np / 32] float.
+//   [2][batch][4][np / 32] float; the magnitude record (kMagnitudeWords) and
+//   the staging's per-work-group maxima (3 floats per group of 4 tiles).
 struct StridedWorkspace {
-  size_t bias, bias_l2, mbias, flags, qp, kp, vp, scales, total;
+  size_t bias, bias_l2, mbias, flags, qp, kp, vp, scales, magnitudes, partial, total;
 };
 
 StridedWorkspace strided_workspace(int batch, int n) {
@@ -203,7 +204,10 @@ StridedWorkspace strided_workspace(int batch, int n) {
   w.kp = w.qp + planes;
   w.vp = w.kp + planes;
   w.scales = w.vp + planes;
-  w.total = w.scales + seg(2 * (size_t)batch * fpx::kHeads * (np / 32) * sizeof(float));
+  w.magnitudes = w.scales + seg(2 * (size_t)batch * fpx::kHeads * (np / 32) * sizeof(float));
+  w.partial = w.magnitudes + seg(fpx::kMagnitudeWords * sizeof(uint32_t));
+  const size_t groups = (3 * (size_t)batch * fpx::kHeads * (np / 32) + 3) / 4;
+  w.total = w.partial + seg(3 * groups * sizeof(float));
   return w;
 }
 
@@ -481,9 +485,12 @@ int fpx_attn_strided(const float* q, int64_t q_sb, int64_t q_sh, int64_t q_sn, c
   float* mbias = as<float>(base + ws.mbias);
   uint32_t* flags = as<uint32_t>(base + ws.flags);
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  hipError_t e = fpx::launch_mask_rows(mask_bias, m_sb, m_sk, batch, n, np, mbias, flags, st);
+  const bool planes = !fpx::fp32_matrix_cores_selected();
+  uint32_t* mag = planes ? as<uint32_t>(base + ws.magnitudes) : nullptr;
+  hipError_t e =
+      fpx::launch_mask_rows(mask_bias, m_sb, m_sk, batch, n, np, mbias, flags, mag, st);
   if (e != hipSuccess) return status(e);
-  e = fpx::launch_stage_bias(bias, b_sh, b_sq, b_sk, n, np, frag, frag_l2, st);
+  e = fpx::launch_stage_bias(bias, b_sh, b_sq, b_sk, n, np, frag, frag_l2, mag, st);
   if (e != hipSuccess) return status(e);
   a.q = q;
   a.k = k;
@@ -503,18 +510,20 @@ int fpx_attn_strided(const float* q, int64_t q_sb, int64_t q_sh, int64_t q_sn, c
   a.batch = batch;
   a.n = n;
   a.np = np;
-  if (fpx::fp32_matrix_cores_selected()) return status(fpx::launch_attention(fpx::kAttnStrided, a, st));
-  // q, k, v into the plane layout, then the block attention's kernel on it
+  if (!planes) return status(fpx::launch_attention(fpx::kAttnStrided, a, st));
+  // q, k, v into the plane layout, then the block attention's kernel on it;
+  // the magnitude record enables its trailing masked-tile skip
   void* qp = base + ws.qp;
   void* kp = base + ws.kp;
   void* vp = base + ws.vp;
   float* scales = as<float>(base + ws.scales);
-  e = fpx::launch_stage_planes(a, qp, kp, vp, scales, st);
+  e = fpx::launch_stage_planes(a, qp, kp, vp, scales, as<float>(base + ws.partial), mag, st);
   if (e != hipSuccess) return status(e);
   a.q = static_cast<const float*>(qp);
   a.k = static_cast<const float*>(kp);
   a.v = static_cast<const float*>(vp);
   a.scales = scales;
+  a.magnitudes = mag;
   return status(fpx::launch_attention_split(fpx::kAttnStaged, a, st));
 }
 

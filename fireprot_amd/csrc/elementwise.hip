@@ -89,9 +89,11 @@ __global__ void bias_pad_kernel(int n, int np, BiasT* __restrict__ tri_bias) {
 __global__ __launch_bounds__(256) void stage_bias_kernel(const float* __restrict__ bias,
                                                          int64_t sh, int64_t sq, int64_t sk,
                                                          int n, int np, float* __restrict__ frag,
-                                                         float* __restrict__ frag_l2) {
+                                                         float* __restrict__ frag_l2,
+                                                         uint32_t* __restrict__ magnitudes) {
   const int64_t nt = np >> 5;
   const int64_t total4 = (int64_t)kHeads * np * np / 4;
+  float vmax = 0.f;  // NaN-propagating max |bias| staged by this lane
   for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total4;
        idx += (int64_t)gridDim.x * blockDim.x) {
     const int64_t f = idx * 4;
@@ -111,6 +113,22 @@ __global__ __launch_bounds__(256) void stage_bias_kernel(const float* __restrict
     }
     *(f32x4*)(frag + f) = v;
     *(f32x4*)(frag_l2 + f) = v * kLog2e;
+    vmax = __builtin_elementwise_maximum(
+        vmax, __builtin_elementwise_maximum(
+                  __builtin_elementwise_maximum(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
+                  __builtin_elementwise_maximum(__builtin_fabsf(v.z), __builtin_fabsf(v.w))));
+  }
+  if (magnitudes != nullptr) {
+    // one atomic per work-group: atomics on one word serialise
+    __shared__ float wmax[4];
+    const float m = wave_max(vmax);
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const float bm = __builtin_elementwise_maximum(__builtin_elementwise_maximum(wmax[0], wmax[1]),
+                                                     __builtin_elementwise_maximum(wmax[2], wmax[3]));
+      atomicMax(&magnitudes[3], __builtin_bit_cast(uint32_t, bm));
+    }
   }
 }
 
@@ -224,24 +242,27 @@ hipError_t launch_mask_bias(const float* mask, int64_t ms_i, int64_t ms_j, int n
 }
 
 hipError_t launch_mask_rows(const float* values, int64_t vs_i, int64_t vs_k, int rows, int n,
-                            int np, float* mbias, uint32_t* tile_flags, hipStream_t stream) {
+                            int np, float* mbias, uint32_t* tile_flags, uint32_t* magnitudes,
+                            hipStream_t stream) {
   if (rows <= 0 || n <= 0) return hipSuccess;
   if (np % 64 || np < n || np > kTileFlagWords * 32 * 32) return hipErrorInvalidValue;
   hipLaunchKernelGGL(mask_rows_kernel<false>, dim3((uint32_t)((rows + 3) / 4)), dim3(256), 0,
-                     stream, values, vs_i, vs_k, rows, n, np, 0.0f, mbias, tile_flags, nullptr);
+                     stream, values, vs_i, vs_k, rows, n, np, 0.0f, mbias, tile_flags, magnitudes);
   return hipGetLastError();
 }
 
 hipError_t launch_stage_bias(const float* bias, int64_t sh, int64_t sq, int64_t sk, int n, int np,
-                             float* frag, float* frag_l2, hipStream_t stream) {
+                             float* frag, float* frag_l2, uint32_t* magnitudes,
+                             hipStream_t stream) {
   if (n <= 0) return hipSuccess;
   if (np % 32 || np < n) return hipErrorInvalidValue;
   const int64_t total4 = (int64_t)kHeads * np * np / 4;
   int64_t blocks = (total4 + 255) / 256;
-  const int64_t cap = (int64_t)device_cu_count() * 32;
+  // a few work-groups per CU stream the copy; fewer keep the record's atomics few
+  const int64_t cap = (int64_t)device_cu_count() * (magnitudes != nullptr ? 4 : 32);
   if (blocks > cap) blocks = cap;
   hipLaunchKernelGGL(stage_bias_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream, bias, sh, sq,
-                     sk, n, np, frag, frag_l2);
+                     sk, n, np, frag, frag_l2, magnitudes);
   return hipGetLastError();
 }
 

@@ -104,8 +104,12 @@ hipError_t launch_attention_split(int layout, const AttnArgs& args, hipStream_t 
 // kAttnStrided q, k, v of args -> the plane layout of kAttnStaged: q_planes,
 // k_planes, v_planes each [batch][4] slices of np * 128 bytes, scales
 // [2][batch][4][np / 32] floats.
+// magnitudes (nullable, with partial of 3 stage_planes_groups floats):
+// words 0-2 of the record (max |q|, |k|, |v|) and word 4.
+int64_t stage_planes_groups(const AttnArgs& args);
 hipError_t launch_stage_planes(const AttnArgs& args, void* q_planes, void* k_planes,
-                               void* v_planes, float* scales, hipStream_t stream);
+                               void* v_planes, float* scales, float* partial,
+                               uint32_t* magnitudes, hipStream_t stream);
 
 // --------------------------------------------------------------- projection
 // Row tiles are 32 consecutive j of one outer row i; A rows are read at
@@ -176,15 +180,19 @@ hipError_t launch_mask_bias(const float* mask, int64_t ms_i, int64_t ms_j, int n
                             float inf, float* mbias, uint32_t* tile_flags, void* tri_bias,
                             bool bias_bf16, uint32_t* magnitudes, hipStream_t stream);
 
-// Staging for kAttnStrided.  launch_mask_rows: mbias[i][k] = values[i*vs_i +
-// k*vs_k] for k < n (0 when values is null), -inf for n <= k < np, and the
-// tile flags, for rows i < rows.  launch_stage_bias: both fragment-order
-// copies (as is, and scaled by log2(e)) of bias[h][q][k] read at h*sh + q*sq +
-// k*sk, 0 for q or k >= n (and everywhere when bias is null).
+// Staging for kAttnStrided / kAttnStaged.  launch_mask_rows: mbias[i][k] =
+// values[i*vs_i + k*vs_k] for k < n (0 when values is null), -inf for n <= k
+// < np, and the tile flags, for rows i < rows; it zeroes the magnitude record
+// (nullable).  launch_stage_bias: both fragment-order copies (as is, and
+// scaled by log2(e)) of bias[h][q][k] read at h*sh + q*sq + k*sk, 0 for q or
+// k >= n (and everywhere when bias is null); max |bias| into the record's
+// word 3 (nullable).  launch_stage_planes fills words 0-2 and sets word 4.
 hipError_t launch_mask_rows(const float* values, int64_t vs_i, int64_t vs_k, int rows, int n,
-                            int np, float* mbias, uint32_t* tile_flags, hipStream_t stream);
+                            int np, float* mbias, uint32_t* tile_flags, uint32_t* magnitudes,
+                            hipStream_t stream);
 hipError_t launch_stage_bias(const float* bias, int64_t sh, int64_t sq, int64_t sk, int n, int np,
-                             float* frag, float* frag_l2, hipStream_t stream);
+                             float* frag, float* frag_l2, uint32_t* magnitudes,
+                             hipStream_t stream);
 
 // LayerNorm over 128 channels of rows x[i][j] at x + i*xs_i + j*xs_j,
 // written contiguously to y[(i*rows_j + j)*128 + c].

@@ -65,9 +65,11 @@ def test_strided_workspace_sizes(lib):
     for batch, n in ((1, 1), (7, 96), (1536, 1000), (1536, 1536), (3, 4096)):
         np_ = -(-n // 128) * 128
         # two fragment-order bias copies; mask-bias rows; tile flags (3 x 4 words);
-        # q, k, v planes (np * 128 bytes per row and head); their scales
+        # q, k, v planes (np * 128 bytes per row and head); their scales; the
+        # magnitude record (5 words); the staging's per-group maxima
         expected = (2 * seg(4 * np_ * np_ * 4) + seg(batch * np_ * 4) + seg(batch * 12 * 4)
-                    + 3 * seg(batch * 4 * np_ * 128) + seg(2 * batch * 4 * (np_ // 32) * 4))
+                    + 3 * seg(batch * 4 * np_ * 128) + seg(2 * batch * 4 * (np_ // 32) * 4)
+                    + seg(5 * 4) + seg(3 * ((3 * batch * 4 * (np_ // 32) + 3) // 4) * 4))
         assert lib.fpx_attn_strided_workspace_bytes(batch, n) == expected
     for bad in ((0, 8), (2, 0), (2, 4097)):
         assert lib.fpx_attn_strided_workspace_bytes(*bad) == 0

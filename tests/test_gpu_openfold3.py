@@ -247,3 +247,32 @@ def test_n1536_full_batch_layout_invariance_and_sampled_rows():
     assert torch.isfinite(got).all()  # row n // 2 is fully masked: -1e9-quantised, finite
     exp = expected(*parts, b_cpu)
     assert_f32_parity("of3 n1536 rows", got, exp)
+
+
+@pytest.mark.parametrize("n,valid", [(300, 200), (640, 520)])
+def test_masked_tail_skip_is_bit_identical(n, valid):
+    """Keys past `valid` masked with -1e9 (at or below -2^29: their trailing
+    tiles are skipped once the staged magnitudes bound the logits) or with
+    -1e8 (visited, weights still exactly 0): outputs bit-identical, and both
+    match the oracle."""
+    print(f"case of3 skip n={n} valid={valid}", flush=True)
+    q, k, v, _, bias = make_case(3, n, 41, mask="none")
+    keep = (torch.arange(n) < valid).float().expand(3, 1, 1, n).contiguous()
+    skipped = run(q, k, v, 1e9 * (keep - 1.0), bias)
+    visited = run(q, k, v, 1e8 * (keep - 1.0), bias)
+    assert torch.equal(skipped, visited)
+    assert_f32_parity(f"of3 skip n={n}", skipped, expected(q, k, v, 1e9 * (keep - 1.0), bias))
+
+
+def test_non_finite_masked_value_keeps_every_tile():
+    """An infinite v at a masked key: the magnitude record sees it, no tile is
+    skipped, and the 0 * inf of the native softmax reaches the output."""
+    n, valid = 200, 100
+    q, k, v, _, bias = make_case(2, n, 43, mask="none")
+    v[1, 2, 150, 5] = float("inf")
+    keep = (torch.arange(n) < valid).float().expand(2, 1, 1, n).contiguous()
+    mb = 1e9 * (keep - 1.0)
+    actual = run(q, k, v, mb, bias)
+    ref = expected(q, k, v, mb, bias)
+    assert torch.equal(torch.isnan(actual), torch.isnan(ref))
+    assert_f32_parity("of3 inf at masked key", actual, ref)
