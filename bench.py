@@ -283,7 +283,8 @@ def bench_openfold3(args) -> dict:
             "unit": "TFLOP/s", "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4),
             "traffic": recorded_traffic("openfold3/fp32-mfma" if fp32_mfma else "openfold3"),
             "flop_per_launch": flop, "avg_launch_ms": round(ms, 4),
-            **({} if fp32_mfma else split_executed(n, n, ms, fp16_planes=True)),
+            **({} if fp32_mfma else split_executed(n, n, ms, visited_key_tiles(n, n - 184, skip=True),
+                                                   fp16_planes=True)),
         },
         "cpu_baseline": None,
     }
