@@ -61,38 +61,9 @@ constexpr int kThreads = 256;
 constexpr int kStages = 4;
 constexpr int kPlaneBytes = 2048;
 constexpr int kStageBytes = 4 * kPlaneBytes;
-// 16-byte chunk c of plane row r sits at chunk c ^ swz(r).  The operand
-// reads (rows 0-31, one chunk per instruction and half-wave) then hit
-// distinct banks in every group of 8 rows at 128 bytes per cycle and of 16
-// rows at 256 bytes per cycle.
-__device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
 // Four waves per SIMD: four work-groups per CU (ring and mask row within
 // 40 KB of LDS at N <= 1536).
 
-// One global_load_lds_dwordx4: lane l copies 16 bytes from src into the LDS
-// at dst + 16 l (dst uniform across the wave).  Written as inline assembly
-// so the compiler does not see an LDS write it cannot tell apart from the
-// stages being read, which would make it wait for every copy before the next
-// LDS read; the kernel waits for the copies itself (wait_vmcnt).  Loads the
-// compiler issues before or after stay correctly waited for, since vector
-// memory loads retire in issue order.  M0 is clobbered: the kernel makes no
-// other use of it (no LDS DMA, message or indexed-register instruction of
-// the compiler's own).
-__device__ __forceinline__ void lds_dma16(const void* src, const uint8_t* dst) {
-  const uint32_t lds_addr =
-      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)dst;
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :
-               : "v"(src), "s"(lds_addr)
-               : "memory", "m0");
-}
-
-// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 

@@ -192,11 +192,17 @@ __global__ __launch_bounds__(Bf16ProjTraits<MODE>::kWaves * 64) void projection_
         for (int r = 0; r < 16; ++r)
           dst[(8 * (r >> 2) + (r & 3)) * kHeadDim] = (__bf16)(acc[r] * scale);
       } else if (group == 2) {
-        __bf16* dst = a.vt + (bh * kHeadDim + l32) * a.np + j0;
+        // V^T keys of a 32-key tile in the S^T accumulator's register order
+        // (within each 16-key block: keys 0-3, 8-11, 4-7, 12-15): this lane's
+        // 4-key group g = 2 rr + half (keys 4 g + e) goes to position pos + e.
+        __bf16* dst = a.vt + (bh * kHeadDim + l32) * a.np + (tile % tiles_j) * kRows;
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          *(bf16x4*)(dst + 8 * rr) = bf16x4{(__bf16)acc[4 * rr + 0], (__bf16)acc[4 * rr + 1],
-                                            (__bf16)acc[4 * rr + 2], (__bf16)acc[4 * rr + 3]};
+        for (int rr = 0; rr < 4; ++rr) {
+          const int g = 2 * rr + half;
+          const int pos = (g >> 2) * 16 + ((g & 1) * 2 + ((g >> 1) & 1)) * 4;
+          *(bf16x4*)(dst + pos) = bf16x4{(__bf16)acc[4 * rr + 0], (__bf16)acc[4 * rr + 1],
+                                         (__bf16)acc[4 * rr + 2], (__bf16)acc[4 * rr + 3]};
+        }
       } else {
         // gate rows are padded to np: the tile is always stored whole
         __bf16* dst = a.gs + ((int64_t)i * a.np + j0) * kHidden + col_w;
@@ -288,20 +294,17 @@ hipError_t launch_proj_mode(const Bf16ProjArgs& a, hipStream_t stream, int wgs_p
 //     FP32 in that order, with a lazy running max (rescale when a tile max
 //     exceeds it by 2^8) and one rounded c per query.
 
-constexpr int kRowB = kHeadDim + 8;  // bf16 per LDS row: 80 bytes, conflict-free b128 reads
 constexpr int kThreads = 256;
 constexpr int kMaxKeysB = kTileFlagWords * 32 * kBk;
-
-typedef __bf16 KTileB[kBk][kRowB];      // [key][channel]
-typedef __bf16 VTileB[kHeadDim][kRowB];  // [channel][key position], see v_position
-
-// V^T keys are stored in the order in which the S^T accumulator registers
-// hold them: within each 16-key block, keys 0-3, 8-11, 4-7, 12-15.  Position
-// of the 4-key group g (keys 4g..4g+3) of a tile:
-__device__ __forceinline__ int v_position(int g) {
-  const int perm = (g & 1) * 2 + ((g >> 1) & 1);  // 0, 2, 1, 3
-  return (g >> 2) * 16 + perm * 4;
-}
+// LDS ring: stage s holds key tile t (t % kStagesB == s) as the K tile [32
+// keys][32 channels] and the V^T tile [32 channels][32 key positions], 2 KB
+// each, 16-byte chunks swizzled (swz); tile t is copied in two tiles ahead
+// of its S^T.  The projection stores V^T with a tile's keys already in the
+// order in which the S^T accumulator registers hold them (within each
+// 16-key block, keys 0-3, 8-11, 4-7, 12-15).
+constexpr int kStagesB = 4;
+constexpr int kTileBytesB = 2048;
+constexpr int kStageBytesB = 2 * kTileBytesB;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_b(const __bf16* base, int64_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<__bf16*>(base), (short)0, (int)bytes,
@@ -320,8 +323,7 @@ __device__ __forceinline__ bf16x8 pack8(const f32x16& p, int m) {
 
 __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArgs a, int nqt,
                                                                      int nkt, uint32_t total) {
-  __shared__ __attribute__((aligned(16))) KTileB Ks[2];
-  __shared__ __attribute__((aligned(16))) VTileB Vs[2];
+  __shared__ __attribute__((aligned(16))) uint8_t ring[kStagesB * kStageBytesB];
   __shared__ __attribute__((aligned(16))) float Ms[kMaxKeysB];
 
   const uint32_t logical = xcd_remap(blockIdx.x, total);
@@ -342,8 +344,6 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
   const int j0 = qt * kBq;
   const int jq = j0 + 32 * w + l32;
   const int qt32 = (j0 >> 5) + w;
-  const int row8 = tid >> 3;
-  const int col4 = (tid & 7) * 4;
   const int last = nkt - 1;
 
   // Per-work-group buffer descriptors: K [np][32], V^T [32][np] of (b, h);
@@ -351,14 +351,25 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
   const int64_t bh = (int64_t)b * kHeads + h;
   const int64_t slice = (int64_t)a.np * kHeadDim;
   const int64_t nt = a.np >> 5;
-  const __amdgpu_buffer_rsrc_t rk = buffer_b(a.k + bh * slice, slice * 2);
-  const __amdgpu_buffer_rsrc_t rv = buffer_b(a.v + bh * slice, slice * 2);
   const __amdgpu_buffer_rsrc_t rb = buffer_b(a.bias + ((int64_t)h * nt + qt32) * nt * 1024, nt * 2048);
-  const uint32_t ok = (uint32_t)(row8 * kHeadDim + col4) * 2;
-  const uint32_t ov = (uint32_t)(row8 * a.np + col4) * 2;
   const uint32_t ob = (uint32_t)lane * 16;
-  auto load_k = [&](int t) { return buffer_b64(rk, ok, (uint32_t)t * 2048); };
-  auto load_v = [&](int t) { return buffer_b64(rv, ov, (uint32_t)t * 64); };
+  // Tile copies: wave w fills rows 16 (w % 2) .. + 15 of the K tile (w < 2)
+  // or of the V^T tile; lane l writes chunk l % 4 of row l / 4 of them, read
+  // from that row's chunk (l % 4) ^ swz(row) (swz(r + 16) == swz(r)).
+  const int crow = 16 * (w & 1) + (lane >> 2);
+  const int cchunk = (lane & 3) ^ swz(lane >> 2);
+  const __bf16* csrc = w < 2 ? a.k + bh * slice + crow * kHeadDim + 8 * cchunk
+                             : a.v + bh * slice + (int64_t)crow * a.np + 8 * cchunk;
+  const int64_t ctile = w < 2 ? kBk * kHeadDim : kBk;  // elements from tile t to t + 1
+  auto dma = [&](int t, int stage) {
+    lds_dma16(csrc + t * ctile, ring + stage * kStageBytesB + (w >> 1) * kTileBytesB + (w & 1) * 1024);
+  };
+  // Operand reads: lane (l32, half) reads chunks half and 2 + half of row l32.
+  const uint32_t rd0 = l32 * 64 + 16 * (half ^ swz(l32));
+  const uint32_t rd1 = l32 * 64 + 16 * ((2 + half) ^ swz(l32));
+  auto tile_rd = [&](int stage, int which, int m) -> bf16x8 {
+    return *(const bf16x8*)(ring + stage * kStageBytesB + which * kTileBytesB + (m ? rd1 : rd0));
+  };
   // Registers 0-7 and 8-15 of the lane's bias fragment as packed bf16 pairs.
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   struct BiasWords {
@@ -380,7 +391,6 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
     }
     return x;
   };
-  const int vpos = v_position(col4 >> 2);
 
   // Row classification, as in the FP32 kernels.
   uint32_t mw[kTileFlagWords];
@@ -427,8 +437,8 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
     const f32x16 zero16 = {};
     // S^T of the tile in Ks[buf] added to x (the bias on the fast path).
     auto scores = [&](int buf, f32x16 x) -> f32x16 {
-      const bf16x8 k0 = *(const bf16x8*)&Ks[buf][l32][8 * half];
-      const bf16x8 k1 = *(const bf16x8*)&Ks[buf][l32][16 + 8 * half];
+      const bf16x8 k0 = tile_rd(buf, 0, 0);
+      const bf16x8 k1 = tile_rd(buf, 0, 1);
       x = mfma_bf16(k0, qf[0], x);
       return mfma_bf16(k1, qf[1], x);
     };
@@ -515,53 +525,55 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
     // O^T += V^T P^T for the tile in Vs[buf]; P comes straight from the
     // S^T register order, which V^T's key positions follow.
     auto pv = [&](int buf, const bf16x8& p0, const bf16x8& p1) {
-      const bf16x8 v0 = *(const bf16x8*)&Vs[buf][l32][8 * half];
-      const bf16x8 v1 = *(const bf16x8*)&Vs[buf][l32][16 + 8 * half];
+      const bf16x8 v0 = tile_rd(buf, 1, 0);
+      const bf16x8 v1 = tile_rd(buf, 1, 1);
       o = mfma_bf16(v0, p0, o);
       o = mfma_bf16(v1, p1, o);
     };
 
-    // Prologue: K(0), K(1), V(0) into LDS; S^T(0); K(2), V(1) in flight.
-    // The fast path's bias words of tile t are loaded at iteration t - 3
-    // (two slots alternate) and widened when S^T(t) starts.
+    // Prologue: tiles 0-2 on their way into stages 0-2; S^T(0) once tiles 0
+    // and 1 have landed.  The fast path's bias words of tile t are loaded at
+    // iteration t - 3 (two slots alternate) and widened when S^T(t) starts.
+    auto clamp = [&](int t) { return t < last ? t : last; };
+    auto stage = [](int t) { return t & (kStagesB - 1); };
     BiasWords bw_e{}, bw_o{};
     if (!kExact) {
       bw_e = load_frag(0);
-      bw_o = load_frag(last < 1 ? last : 1);
+      bw_o = load_frag(clamp(1));
     }
-    *(bf16x4*)&Ks[0][row8][col4] = load_k(0);
-    *(bf16x4*)&Vs[0][row8][vpos] = load_v(0);
-    *(bf16x4*)&Ks[1][row8][col4] = load_k(last < 1 ? last : 1);
-    bf16x4 kreg = load_k(last < 2 ? last : 2);
-    bf16x4 vreg = load_v(last < 1 ? last : 1);
+    dma(0, 0);
+    dma(clamp(1), 1);
+    dma(clamp(2), 2);
+    wait_vmcnt<1>();
     __syncthreads();
     f32x16 x_a = scores(0, kExact ? zero16 : widen(bw_e));
-    if (!kExact) bw_e = load_frag(last < 2 ? last : 2);
+    if (!kExact) bw_e = load_frag(clamp(2));
     finish(x_a, 0);
-    __syncthreads();  // every wave is done with K(0) before Ks[0] is refilled
     f32x16 x_b;
 
-    // Iteration kt: Ks[(kt+1)&1] = K(kt+1), Vs[kt&1] = V(kt); cur = logits
-    // of tile kt; bw = bias words of tile kt+1, refilled with tile kt+3;
-    // kreg = K(kt+2) and vreg = V(kt+1) in flight.  Indices past the last
-    // tile are clamped (in range, never used).
+    // Iteration kt reads K(kt+1) and V(kt) and copies tile kt+3 into the
+    // stage that held tile kt-1, which every wave left behind at the previous
+    // barrier; cur = logits of tile kt; bw = bias words of tile kt+1,
+    // refilled with tile kt+3.  Tiles past the last are clamped (in range,
+    // never used).
     auto body = [&](int kt, f32x16& cur, f32x16& nxt, BiasWords& bw) {
-      nxt = scores((kt + 1) & 1, kExact ? zero16 : widen(bw));
-      if (!kExact) bw = load_frag(kt + 3 < last ? kt + 3 : last);
+      nxt = scores(stage(kt + 1), kExact ? zero16 : widen(bw));
+      if (!kExact) bw = load_frag(clamp(kt + 3));
       bf16x8 p0, p1;
       softmax(cur, p0, p1);
-      pv(kt & 1, p0, p1);
+      pv(stage(kt), p0, p1);
       finish(nxt, kt + 1);
-      *(bf16x4*)&Ks[kt & 1][row8][col4] = kreg;
-      *(bf16x4*)&Vs[(kt + 1) & 1][row8][vpos] = vreg;
-      kreg = load_k(kt + 3 < last ? kt + 3 : last);
-      vreg = load_v(kt + 2 < last ? kt + 2 : last);
+      dma(clamp(kt + 3), stage(kt + 3));
+      // Tile kt+2 has landed once at most this iteration's copy and (fast
+      // path) its two bias-word loads are outstanding: vector memory loads
+      // retire in issue order.
+      wait_vmcnt<kExact ? 1 : 3>();
       __syncthreads();
     };
     auto tail = [&](const f32x16& cur, int kt) {
       bf16x8 p0, p1;
       softmax(cur, p0, p1);
-      pv(kt & 1, p0, p1);
+      pv(stage(kt), p0, p1);
     };
     int kt = 0;
     for (; kt + 2 < nkt; kt += 2) {
@@ -574,6 +586,7 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
     } else {
       tail(x_a, kt);
     }
+    wait_vmcnt<0>();  // the clamped tail copies land before the LDS is released
   };
   if (has_unmasked) {
     run(std::false_type{});
