@@ -1,47 +1,45 @@
-// FP32-accurate triangle attention on the CDNA4 BF16 matrix cores.
+// FP32-accurate triangle attention on the CDNA4 16-bit matrix cores.
 //
-// Reads the block's FP32 workspace exactly as attention_kernel<kAttnBlock>
-// does (q, k [B][H][np][32], v^T [B][H][32][np], the fragment-order bias
-// copies, tile flags, mask-bias rows, gate) and writes the same gated output.
-// Only the two products change: every FP32 operand is split exactly into
-// bfloat16 planes, x = x_hi + x_lo (+ x_rest), and the products run on
-// v_mfma_f32_32x32x16_bf16 with FP32 accumulation.  That instruction does 8x
-// the work of v_mfma_f32_32x32x2_f32 in half its cycles, and unlike the FP32
-// one it runs beside VALU work, so the softmax of one tile overlaps the
-// matrix work of the next.
+// Every FP32 operand of the two products is held as power-of-two scaled fp16
+// (hi, lo) planes: x 2^e = hi + lo with hi = fp16(x 2^e), lo = fp16(x 2^e -
+// hi), 22 significant bits, e chosen per tile so the tile's max |value| 2^e
+// lies in [2^14, 2^15).  A product then takes three terms (hi hi, hi lo,
+// lo hi) on v_mfma_f32_32x32x16_f16 with FP32 accumulation, an error per
+// product of about 2^-22, at the level of an FP32 dot product.  That
+// instruction does 8x the work of v_mfma_f32_32x32x2_f32 in half its cycles,
+// and unlike the FP32 one it runs beside VALU work, so the softmax of one
+// tile overlaps the matrix work of the next.
 //
-//   S^T = K Q^T: three planes each; the six terms down to 2^-16 relative
-//     (hi hi, hi lo, lo hi, lo lo, hi rest, rest hi) leave an error of about
-//     3 * 2^-24 per product, FP32 rounding level.  Logit accuracy matters in
-//     absolute terms (a logit error d scales a weight by e^d), so large
-//     logits need all six.  12 MFMAs per 32-key tile.
-//   O^T += V^T P^T: two planes each, three terms (hi hi, hi lo, lo hi), a
-//     relative error below 2^-16 per weighted value.  6 MFMAs per tile.
+//   S^T = K Q^T: q and k arrive as planes scaled per 32 x 32 tile (prepare
+//     projection or stage_planes_kernel); the logit is fma(acc, log2(e)
+//     2^-(e_q + e_k), bias log2(e)) (exact scaling, one rounding).  6 MFMAs
+//     per 32-key tile.
+//   O^T += V^T P^T: v^T arrives as planes scaled per key tile t (2^e_t), its
+//     keys in the S^T accumulator's register order; the weights P of tile t
+//     are split per tile into fp16 planes as P 2^(kVShift - (e_t - e_min))
+//     (at most 2^15), so every product carries the same 2^(e_min + kVShift),
+//     removed in the epilogue.  6 MFMAs per tile.
 //
-// The block layout (kAttnBlock) takes q and k already split by the prepare
-// projection into fp16 hi and lo planes, scaled per 32 x 32 tile by a power
-// of two so that the tile's max lies in [2^14, 2^15) (ProjArgs::planes):
-// 22 significant bits per value, so S^T = K Q^T needs only three terms
-// (hi hi, hi lo, lo hi) on v_mfma_f32_32x32x16_f16, 6 MFMAs per tile, with
-// an error at the level of an FP32 dot product.  The logit is then
-// fma(acc, log2(e) 2^-(e_q + e_k), bias) (exact scaling, one rounding).  V^T
-// arrives as bf16 hi and lo planes with its keys already in accumulator
-// order.  Each key tile's four 2 KB planes go straight from global memory
-// into a ring of LDS stages (global_load_lds_dwordx4, no registers), two
-// tiles ahead of use, with 16-byte chunks swizzled so the operand reads are
-// free of bank conflicts; no split happens in this kernel.
+// Each key tile's four 2 KB planes (K hi, K lo, V^T hi, V^T lo) go straight
+// from global memory into a ring of LDS stages (global_load_lds_dwordx4, no
+// registers), two tiles ahead of use, with 16-byte chunks swizzled so the
+// operand reads are free of bank conflicts.
 //
-// The split: hi = bf16(x) (round to nearest), lo = bf16(x - hi), rest =
-// bf16(x - hi - lo).  Each difference is exact (Sterbenz), and x - hi - lo
-// keeps at most 8 significant bits, so hi + lo + rest == x for normal x.
-//
-// Softmax, row classification, mask handling and the output are the FP32
-// kernel's (see attention.hip): log2-domain logits with the scaled bias as
-// the accumulator's start value and a snapped reference on rows with an
-// unmasked key; fl(fl(s + mask) + bias) in natural units with a lazy max on
-// fully masked rows.  The pipeline is the BF16 kernel's: K is staged one
-// tile ahead of V, and the S^T MFMAs of tile t + 1 are issued before the
-// softmax of tile t.
+// Softmax, two paths, each its own launch over the same grid (a work-group
+// of the other path exits at once), so each gets its own register budget:
+//   fast (rows with an unmasked key whose logits the magnitude record bounds
+//     below kFastBound): log2-domain logits with the scaled bias as the
+//     S^T accumulator's start value; an integer reference c per query, moved
+//     up to the tile's max when a lane's weights of a tile would pass 2^15;
+//     P' = exp2(x - (c + g_t)) with the tile's exponent shift g_t folded into
+//     the exact integer c + g_t;
+//   exact (fully masked rows, and rows whose logits are not bounded):
+//     fl(fl(s + mask) + bias) in natural units, as the native path rounds
+//     them, with a lazy max and one rounded reference, so equal quantised
+//     logits get equal weights (the -1e9 of a padding row has an FP32
+//     spacing of 64).
+// K is staged one tile ahead of V, and the S^T MFMAs of tile t + 1 are issued
+// before the softmax of tile t.
 #include "attn_common.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
@@ -61,6 +59,11 @@ constexpr int kThreads = 256;
 constexpr int kStages = 4;
 constexpr int kPlaneBytes = 2048;
 constexpr int kStageBytes = 4 * kPlaneBytes;
+// Weights enter P.V as fp16 planes scaled by 2^(kVShift - d_t) (at most
+// 2^15), d_t = e_t - e_min >= 0 the v^T tile's exponent above the row's
+// smallest; kPlaneMax bounds a lane's 16 scaled weights of one tile.
+constexpr int kVShift = 7;
+constexpr float kPlaneMax = 32768.0f;
 // Four waves per SIMD: four work-groups per CU (ring and mask row within
 // 40 KB of LDS at N <= 1536).
 
@@ -80,8 +83,11 @@ __device__ __forceinline__ int v_position(int g) {
 // flags.  LAYOUT kAttnBlock: the block's workspace, gated head-last output;
 // kAttnStaged: planes staged from a caller's strided q, k, v
 // (launch_stage_planes), output through the caller's strides, no gate.
-template <int LAYOUT>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
+// EXACT selects the softmax path the launch serves (see launch_attention_split);
+// the exact path holds a few more values and runs at three waves per SIMD.
+template <int LAYOUT, bool EXACT>
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(EXACT ? 3 : 4, EXACT ? 3 : 4)))
 void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
   constexpr bool kBlock = LAYOUT == kAttnBlock;
   static_assert(LAYOUT == kAttnBlock || LAYOUT == kAttnStaged, "plane layouts only");
@@ -90,6 +96,8 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
   // Mask-bias row of this outer row, nkt_all * kBk floats (dynamic).
   extern __shared__ __attribute__((aligned(16))) float Ms[];
   __shared__ float Sk[kTileFlagWords * 32];  // 2^-e_k of each key tile
+  __shared__ int Ev[kTileFlagWords * 32];    // e_v of each key tile's v^T planes
+  __shared__ float Wv[kThreads / 64];        // per wave: max 2^-e_v over its tiles
 
   const uint32_t logical = xcd_remap(blockIdx.x, total);
   const int groups = (a.batch + kRowGroup - 1) / kRowGroup;
@@ -99,7 +107,13 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
   const int grp = rem / (kRowGroup * nqt);
   const int in_grp = rem % (kRowGroup * nqt);
   const int qt = in_grp / kRowGroup;
-  const int b = grp * kRowGroup + in_grp % kRowGroup;
+  // Logical row lr = u groups + v runs outer row 8 v + u: each XCD's
+  // contiguous range of logical rows takes every 8th outer row, so rows that
+  // leave the launch early (the other softmax path, padding) spread evenly
+  // over the XCDs.  The bias a work-group reads depends on (h, qt) only, so
+  // work-groups that run together still share it in L2.
+  const int lr = grp * kRowGroup + in_grp % kRowGroup;
+  const int b = kRowGroup * (lr % groups) + lr / groups;
   if (b >= a.batch) return;  // padding of the last row group; uniform per work-group
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -167,14 +181,20 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
   // whose every mask bias is <= -kSkipMask carry weights that are exactly 0
   // when the prepare projection's magnitude record bounds the logits
   // (kernels.hpp), so they are left out; the result is bit-identical.
+  // The fast softmax needs the same record to bound the logits below
+  // kFastBound (its integer reference then stays exact when shifted by a
+  // tile's plane exponent); other rows take the exact path.
   int nkt = nkt_all;
+  bool fast = false;
   {
     if (has_unmasked && a.magnitudes != nullptr && a.magnitudes[4] == 1u) {
       const float mq = __builtin_bit_cast(float, a.magnitudes[0]);
       const float mk = __builtin_bit_cast(float, a.magnitudes[1]);
       const float mv = __builtin_bit_cast(float, a.magnitudes[2]);
       const float mb = __builtin_bit_cast(float, a.magnitudes[3]);
-      if (32.0f * mq * mk + mb < kSkipBound && mv < INFINITY) {  // false for NaN
+      const float bound = 32.0f * mq * mk + mb;
+      fast = bound < kFastBound && mv < INFINITY;  // false for NaN
+      if (bound < kSkipBound && mv < INFINITY) {  // false for NaN
         const uint32_t* far = a.tile_flags + (int64_t)b * kTileFlagParts * kTileFlagWords +
                               2 * kTileFlagWords;
         while (nkt > 1) {
@@ -185,6 +205,8 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
       }
     }
   }
+  // Each row runs in the launch of its softmax path (uniform per work-group).
+  if (fast == EXACT) return;
   const int last = nkt - 1;
   auto masked = [&](int t) -> bool {
     const uint32_t word = t < 32 ? mw[0] : t < 64 ? mw[1] : t < 96 ? mw[2] : mw[3];
@@ -195,13 +217,23 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
     for (int k = 4 * tid; k < nkt * kBk; k += 4 * kThreads) *(f32x4*)&Ms[k] = *(const f32x4*)(src + k);
   }
   // The product scale 2^-(e_q + e_k) of this wave's queries and each key
-  // tile (read after the prologue's first barrier).
+  // tile, and each key tile's v^T exponent e_t with their maximum 2^-e_min
+  // (read after the prologue's first barrier).  e_min runs over every key
+  // tile, visited or not, so leaving out trailing tiles changes no bit.
   float sq = 1.0f;
   {
     const int64_t per = (int64_t)kHeads * nt;
     const float* sc = a.scales + (int64_t)b * per + (int64_t)h * nt;
     sq = sc[qt32];
-    for (int t = tid; t < nkt; t += kThreads) Sk[t] = sc[(int64_t)a.batch * per + t];
+    float vmax = 0.f;
+    for (int t = tid; t < nkt_all; t += kThreads) {
+      if (t < nkt) Sk[t] = sc[(int64_t)a.batch * per + t];
+      const float sv = sc[2 * (int64_t)a.batch * per + t];
+      Ev[t] = inv_scale_exp(sv);
+      vmax = __builtin_elementwise_maximum(vmax, sv);
+    }
+    vmax = wave_max(vmax);
+    if (lane == 0) Wv[w] = vmax;
   }
   auto mask_vals = [&](int t) -> f32x16 {
     const float* m = &Ms[t * kBk + 4 * half];
@@ -211,6 +243,7 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
 
   f32x16 o = {};
   float l_run = 0.f;
+  int e_min = 0;  // smallest v^T plane exponent over the visited tiles
 
   auto run = [&](auto exact_tag) {
     constexpr bool kExact = decltype(exact_tag)::value;
@@ -244,16 +277,21 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
       return x;
     };
     // The logits of tile t from its product acc (s = acc 2^-(e_q + e_k), an
-    // exact scaling): with x holding the bias in log2 units, plus the mask
-    // bias on masked tiles (fast), or fl(fl(s + mask) + bias) in natural
-    // units (exact).
+    // exact scaling), x holding the tile's bias fragment: the bias in log2
+    // units plus the mask bias on masked tiles (fast), or fl(fl(s + mask) +
+    // bias) in natural units (exact).
     auto finish = [&](f32x16& x, const f32x16& acc, int t) {
       const float st = sq * Sk[t];
       if (kExact) {
-        const f32x16 mb = mask_vals(t);
-        const f32x16 bias = load_frag(rb, t);
+        if (masked(t)) {
+          const f32x16 mb = mask_vals(t);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) x[r] = ((acc[r] * st) + mb[r]) + bias[r];
+          for (int r = 0; r < 16; ++r) x[r] = ((acc[r] * st) + mb[r]) + x[r];
+        } else {
+          // every mask bias of the tile is 0: fl(s + 0) = s
+#pragma unroll
+          for (int r = 0; r < 16; ++r) x[r] = (acc[r] * st) + x[r];
+        }
         return;
       }
       {
@@ -267,85 +305,108 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
         for (int r = 0; r < 16; ++r) x[r] = __builtin_fmaf(mb[r], kLog2e, x[r]);
       }
     };
-    // Start value of a tile's S^T accumulator.
-    auto init = [&](int t) -> f32x16 { return kExact ? zero16 : load_frag(rb2, t); };
+    // A tile's bias fragment, loaded two tiles ahead of its logits: scaled
+    // by log2(e) (fast) or as is (exact).
+    auto init = [&](int t) -> f32x16 { return load_frag(kExact ? rb : rb2, t); };
 
-    // Reference state of this lane's query (see attention.hip).
+    // Reference state of this lane's query: the weights are exp2(x - c_ref)
+    // (x in log2 units on the fast path) or exp2(x log2(e) - c_ref) (natural
+    // units on the exact path); m_ref is the running max (-inf: none yet).
     float m_ref = -INFINITY;
-    float m_thr = -INFINITY;
     float c_ref = 0.f;
+    float w_ref = 1.f;  // exact path: 2^-(m_ref log2(e) - c_ref)
     bool has_ref = false;
-    bool c_zero = true;
 
-    // Logits x of one tile -> the weights' hi and lo planes (P operand).
-    auto softmax = [&](const f32x16& x, bf16x8 (&ph)[2], bf16x8 (&pl)[2]) {
-      f32x16 p;
-      auto pack = [&]() {
-#pragma unroll
-        for (int m = 0; m < 2; ++m) {
-          const f32x8 v = {p[8 * m + 0], p[8 * m + 1], p[8 * m + 2], p[8 * m + 3],
-                           p[8 * m + 4], p[8 * m + 5], p[8 * m + 6], p[8 * m + 7]};
-          split2(v, ph[m], pl[m]);
-        }
+    // Logits x of tile t -> the weights' fp16 hi and lo planes (P operand).
+    // Tile t's v^T planes carry 2^e_t, so its weights P enter as
+    // P' = P 2^-g, g = e_t - e_min - kVShift: every product then carries the
+    // same 2^(e_min + kVShift), removed in the epilogue.  P <= 2^8 keeps
+    // P' <= 2^15, within fp16; the largest weight of the row sits at or
+    // above 2^(kVShift - 1) in the tiles of exponent e_min, far above the
+    // fp16 planes' absolute resolution (2^-25).  The row sum adds the
+    // unscaled P.
+    auto softmax = [&](const f32x16& x, int t, bf16x8 (&ph)[2], bf16x8 (&pl)[2]) {
+      const int g = __builtin_amdgcn_readfirstlane(Ev[t]) - e_min - kVShift;  // uniform
+      // The weights are formed, summed and split eight at a time (8 keys per
+      // operand half m), so only half of them are live at once.
+      auto sum8 = [](const f32x8& v) {
+        return ((v[0] + v[4]) + (v[1] + v[5])) + ((v[2] + v[6]) + (v[3] + v[7]));
       };
       if (kExact) {
+        // Lazy max: the reference moves when a tile's max exceeds the last
+        // one by 8 binary orders; equal quantised logits get equal weights
+        // (one rounded c_ref per reference).  c_ref = fl(m log2(e)) is off
+        // by r0 = m log2(e) - c_ref (up to half its spacing: 64 at the
+        // -1e9 of a padding row), so the weights p = exp2(x log2(e) - c_ref)
+        // carry 2^r0: P = p w_r with w_r = 2^-r0 is at most 2^8, and the
+        // sums hold P, in units of exp(x - m_ref).
         const float mt = xor32_max(max16(x));
-        if (__any(mt > m_thr)) {
+        if (__any(mt > m_ref + kRescaleNat)) {
           const float m_new = __builtin_elementwise_maximum(m_ref, mt);
           const float c_new = m_new == -INFINITY ? 0.f : m_new * kLog2e;
-          const float alpha = m_ref == -INFINITY ? 0.f : exp2_fast(c_ref - c_new);
+          const float alpha = m_ref == -INFINITY ? 0.f : exp2_fast((m_ref - m_new) * kLog2e);
 #pragma unroll
           for (int r = 0; r < 16; ++r) o[r] *= alpha;
           l_run *= alpha;
           m_ref = m_new;
           c_ref = c_new;
-          m_thr = m_new + kRescaleNat;
+          w_ref = m_new == -INFINITY ? 1.f : exp2_fast(-__builtin_fmaf(m_new, kLog2e, -c_new));
         }
+        const float f = w_ref * __builtin_ldexpf(1.0f, -g);  // exact: a power of two times w_ref
+        float ps = 0.f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) p[r] = exp2_fast(__builtin_fmaf(x[r], kLog2e, -c_ref));
-        l_run += sum16(p);
-        pack();
+        for (int m = 0; m < 2; ++m) {
+          f32x8 v;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = exp2_fast(__builtin_fmaf(x[8 * m + e], kLog2e, -c_ref));
+          ps += sum8(v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] *= f;
+          split_f16(v, ph[m], pl[m]);
+        }
+        l_run = __builtin_fmaf(ps, w_ref, l_run);
         return;
       }
-      float ovf = 0.f;
-      if (has_ref) {
-        if (c_zero) {
+      // Fast path: c_ref is an integer of magnitude below 2^22 once a tile
+      // with an unmasked key has set it (kFastBound), so c_ref + g is exact
+      // and P' = exp2(x - (c_ref + g)) costs no multiply.  A lane pair holds
+      // one query's 32 keys and keeps one reference.
+      const float gf = (float)g;
+      f32x16 p;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) p[r] = exp2_fast(x[r]);
-        } else {
+      for (int r = 0; r < 16; ++r) p[r] = exp2_fast(x[r] - (c_ref + gf));
+      float ps = sum16(p);
+      // ps <= 2^15 bounds every P' of the lane; NaN or inf counts as over.
+      if (!has_ref || __any(!(ps <= kPlaneMax))) {
+        // Rare, taken by the whole wavefront: the first tile, or a tile
+        // whose weights would leave the fp16 range.  The reference moves up
+        // to the tile's max rounded up to an integer, so every weight of the
+        // tile is at most 1; the previous sums scale by the exact power of
+        // two alpha.  A query whose logits are all -inf so far keeps no
+        // reference (its weights are 0).
+        const float mt = xor32_max(max16(x));
+        const bool fresh = m_ref == -INFINITY;
+        m_ref = __builtin_elementwise_maximum(m_ref, mt);
+        const float top = __builtin_ceilf(mt);
+        const float c_new = fresh ? (m_ref == -INFINITY ? 0.f : top)
+                                  : __builtin_elementwise_maximum(c_ref, top);
+        const float alpha = fresh ? 0.f : exp2_fast(c_ref - c_new);  // 1 when unchanged
 #pragma unroll
-          for (int r = 0; r < 16; ++r) p[r] = exp2_fast(x[r] - c_ref);
-        }
-        const float l_new = l_run + sum16(p);
-        const bool over = !(l_new <= kSumLimit);  // NaN or inf count as overflow
-        if (!__any(over)) {
-          l_run = l_new;
-          pack();
-          return;
-        }
-        ovf = over ? 1.f : 0.f;
+        for (int r = 0; r < 16; ++r) o[r] *= alpha;
+        l_run *= alpha;
+        c_ref = c_new;
+        has_ref = __all(m_ref != -INFINITY);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[r] = exp2_fast(x[r] - (c_ref + gf));
+        ps = sum16(p);
       }
-      // Rare path, taken by the whole wavefront (attention.hip).
-      const float mt = xor32_max(max16(x));
-      const bool fresh = m_ref == -INFINITY;
-      const bool need = fresh || xor32_max(ovf) > 0.f || mt > c_ref + kSnap;
-      m_ref = __builtin_elementwise_maximum(m_ref, mt);
-      const float snapped =
-          (m_ref == -INFINITY || (m_ref >= -kSnap && m_ref <= kSnap)) ? 0.f : m_ref;
-      const float c_new = fresh ? snapped
-                          : need ? __builtin_elementwise_maximum(snapped, c_ref + kLift)
-                                 : c_ref;
-      const float alpha = fresh ? 0.f : exp2_fast(c_ref - c_new);  // 1 when unchanged
+      l_run = __builtin_fmaf(ps, __builtin_ldexpf(1.0f, g), l_run);  // P = P' 2^g
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[r] *= alpha;
-      l_run *= alpha;
-      c_ref = c_new;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) p[r] = exp2_fast(x[r] - c_ref);
-      l_run += sum16(p);
-      has_ref = __all(m_ref != -INFINITY);
-      c_zero = __all(c_ref == 0.f);
-      pack();
+      for (int m = 0; m < 2; ++m) {
+        const f32x8 v = {p[8 * m + 0], p[8 * m + 1], p[8 * m + 2], p[8 * m + 3],
+                         p[8 * m + 4], p[8 * m + 5], p[8 * m + 6], p[8 * m + 7]};
+        split_f16(v, ph[m], pl[m]);
+      }
     };
 
     // O^T += V^T P^T for the tile in LDS buffer/stage buf.
@@ -354,9 +415,9 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
       for (int m = 0; m < 2; ++m) {
         const bf16x8 vh = plane_rd(buf, 2, m);
         const bf16x8 vl = plane_rd(buf, 3, m);
-        o = mfma_bf16(vl, ph[m], o);
-        o = mfma_bf16(vh, pl[m], o);
-        o = mfma_bf16(vh, ph[m], o);
+        o = mfma_f16(vl, ph[m], o);
+        o = mfma_f16(vh, pl[m], o);
+        o = mfma_f16(vh, ph[m], o);
       }
     };
 
@@ -377,24 +438,27 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
     dma(clamp(2), 2);
     wait_vmcnt<2>();
     __syncthreads();
+    e_min = __builtin_amdgcn_readfirstlane(
+        inv_scale_exp(__builtin_elementwise_maximum(__builtin_elementwise_maximum(Wv[0], Wv[1]),
+                                                    __builtin_elementwise_maximum(Wv[2], Wv[3]))));
     finish(x_a, scores(0), 0);
     auto body = [&](int t, f32x16& cur, f32x16& nxt) {
       const f32x16 acc = scores(stage(t + 1));
       bf16x8 ph[2], pl[2];
-      softmax(cur, ph, pl);
+      softmax(cur, t, ph, pl);
       pv(stage(t), ph, pl);
       finish(nxt, acc, t + 1);
       dma(clamp(t + 3), stage(t + 3));
       cur = init(clamp(t + 2));
       // Tile t+2 has landed once at most this iteration's two tile loads
-      // and (fast path) four bias-fragment loads are outstanding: vector
-      // memory loads retire in issue order.
-      wait_vmcnt<kExact ? 2 : 6>();
+      // and four bias-fragment loads are outstanding: vector memory loads
+      // retire in issue order.
+      wait_vmcnt<6>();
       __syncthreads();
     };
     auto tail = [&](const f32x16& cur, int t) {
       bf16x8 ph[2], pl[2];
-      softmax(cur, ph, pl);
+      softmax(cur, t, ph, pl);
       pv(stage(t), ph, pl);
     };
     for (; kt + 2 < nkt; kt += 2) {
@@ -409,19 +473,19 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
     }
     wait_vmcnt<0>();  // the clamped tail loads land before the LDS is released
   };
-  if (has_unmasked) {
-    run(std::false_type{});
-  } else {
-    run(std::true_type{});
-  }
+  run(std::integral_constant<bool, EXACT>{});
 
   const float l_tot = xor32_sum(l_run);
   if (jq < a.n) {
+    // o carries 2^(e_min + kVShift) (exact powers of two)
+    const int ue = -(e_min + kVShift);
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int c = 8 * rr + 4 * half;  // channels c..c+3 of head h
-      f32x4 ov4 = {o[4 * rr + 0] / l_tot, o[4 * rr + 1] / l_tot, o[4 * rr + 2] / l_tot,
-                   o[4 * rr + 3] / l_tot};
+      f32x4 ov4 = {__builtin_ldexpf(o[4 * rr + 0], ue) / l_tot,
+                   __builtin_ldexpf(o[4 * rr + 1], ue) / l_tot,
+                   __builtin_ldexpf(o[4 * rr + 2], ue) / l_tot,
+                   __builtin_ldexpf(o[4 * rr + 3], ue) / l_tot};
       if constexpr (kBlock) {
         const int64_t col = h * kHeadDim + c;
         if (a.gate) ov4 = ov4 * *(const f32x4*)(a.gate + ((int64_t)b * a.np + jq) * kHidden + col);
@@ -446,12 +510,21 @@ hipError_t launch_attention_split(int layout, const AttnArgs& a, hipStream_t str
       nkt > kTileFlagWords * 32)
     return hipErrorInvalidValue;
   const size_t mask_row_bytes = (size_t)nkt * kBk * sizeof(float);
+  // Two launches over the same grid: rows on the fast softmax path, then
+  // the others (fully masked rows, rows whose logits are not bounded); each
+  // work-group of the wrong path exits after reading its row's flags.
   if (layout == kAttnBlock) {
-    hipLaunchKernelGGL(attention_split_kernel<kAttnBlock>, dim3((uint32_t)total), dim3(kThreads),
-                       mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total);
+    hipLaunchKernelGGL((attention_split_kernel<kAttnBlock, false>), dim3((uint32_t)total),
+                       dim3(kThreads), mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    hipLaunchKernelGGL((attention_split_kernel<kAttnBlock, true>), dim3((uint32_t)total),
+                       dim3(kThreads), mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total);
   } else if (layout == kAttnStaged) {
-    hipLaunchKernelGGL(attention_split_kernel<kAttnStaged>, dim3((uint32_t)total), dim3(kThreads),
-                       mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total);
+    hipLaunchKernelGGL((attention_split_kernel<kAttnStaged, false>), dim3((uint32_t)total),
+                       dim3(kThreads), mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    hipLaunchKernelGGL((attention_split_kernel<kAttnStaged, true>), dim3((uint32_t)total),
+                       dim3(kThreads), mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total);
   } else {
     return hipErrorInvalidValue;
   }
@@ -468,7 +541,9 @@ hipError_t launch_attention_split(int layout, const AttnArgs& a, hipStream_t str
 //         planes [np][32] of the (b, h) slice, and 2^-e at
 //         scales[((op batch + b) 4 + h) (np / 32) + t] (op 0: q, 1: k);
 //   v:    the tile transposed to [32 channels][32 key positions] (a tile's
-//         keys in v_position order) as bf16 hi and lo planes.
+//         keys in v_position order) times 2^e (e = value_plane_exp of the
+//         tile's max |value|) as fp16 hi and lo planes, and 2^-e at
+//         scales[((2 batch + b) 4 + h) (np / 32) + t].
 // partial (nullable): each work-group's NaN-propagating max |q|, |k|, |v| at
 // partial[3 blockIdx.x + op] (0 for operands it did not stage), reduced by
 // reduce_magnitudes_kernel.  Each wave transposes v through its own LDS
@@ -552,17 +627,21 @@ __global__ __launch_bounds__(256) void stage_planes_kernel(AttnArgs a, uint8_t* 
         const int g = 4 * (p >> 4) + v_position((p >> 2) & 3) / 4;  // (0, 2, 1, 3) is its own inverse
         v[i] = tv[w][4 * g + (p & 3)][c];
       }
+      const int e = value_plane_exp(m);
+      const float f = __builtin_ldexpf(1.0f, e);
       bf16x8 hi[2], lo[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        split2(f32x8{v[8 * i], v[8 * i + 1], v[8 * i + 2], v[8 * i + 3], v[8 * i + 4],
-                     v[8 * i + 5], v[8 * i + 6], v[8 * i + 7]},
-               hi[i], lo[i]);
+        split_f16(f32x8{v[8 * i] * f, v[8 * i + 1] * f, v[8 * i + 2] * f, v[8 * i + 3] * f,
+                        v[8 * i + 4] * f, v[8 * i + 5] * f, v[8 * i + 6] * f, v[8 * i + 7] * f},
+                  hi[i], lo[i]);
       uint8_t* o = dst + (int64_t)t * kPlaneBytes + c * 64 + p0 * 2;
       *(bf16x8*)o = hi[0];
       *(bf16x8*)(o + 16) = hi[1];
       *(bf16x8*)(o + (slice_bytes >> 1)) = lo[0];
       *(bf16x8*)(o + (slice_bytes >> 1) + 16) = lo[1];
+      if (lane == 0)
+        scales[(((int64_t)2 * a.batch + b) * kHeads + h) * nt + t] = __builtin_ldexpf(1.0f, -e);
     }
   }
   if (partial != nullptr) {

@@ -33,8 +33,8 @@ size_t elem_bytes(int dtype) { return dtype == FPX_BF16 ? 2 : 4; }
 //   tri_bias [4][np][np] (FP32: fragment order, twice: as is and scaled by
 //   log2(e); BF16: bias_frag_index_bf16, once); mbias [n][np] float;
 //   tile flags [n][kTileFlagParts * kTileFlagWords] uint32, then the
-//   kMagnitudeWords words of the magnitude record; scales [2][n][4][np / 32]
-//   float (the plane layout's per-tile inverse scales of q and k).
+//   kMagnitudeWords words of the magnitude record; scales [3][n][4][np / 32]
+//   float (the plane layout's per-tile inverse scales of q, k and v^T).
 // FP32 blocks on the BF16 matrix cores hold q, k and v^T in the plane layout
 // (ProjArgs::planes), in the same bytes as FP32 values.
 struct BlockWorkspace {
@@ -62,7 +62,7 @@ BlockWorkspace block_workspace(int n, int dtype) {
   w.mbias = w.bias + bias;
   w.flags = w.mbias + mb;
   w.scales = w.flags + fl;
-  w.total = w.scales + seg((size_t)2 * n * fpx::kHeads * (np / 32) * sizeof(float));
+  w.total = w.scales + seg((size_t)3 * n * fpx::kHeads * (np / 32) * sizeof(float));
   return w;
 }
 
@@ -184,7 +184,7 @@ int block_impl(int dtype, const void* z, int64_t z_stride0, int64_t z_stride1, c
 //   bias [4][np][np] float in fragment order, twice (as is, scaled by log2(e));
 //   mbias [batch][np] float; tile flags [batch][kTileFlagParts * kTileFlagWords] uint32;
 //   q, k and v planes [batch][4] slices of np * 128 bytes each; their scales
-//   [2][batch][4][np / 32] float; the magnitude record (kMagnitudeWords) and
+//   [3][batch][4][np / 32] float; the magnitude record (kMagnitudeWords) and
 //   the staging's per-work-group maxima (3 floats per group of 4 tiles).
 struct StridedWorkspace {
   size_t bias, bias_l2, mbias, flags, qp, kp, vp, scales, magnitudes, partial, total;
@@ -204,7 +204,7 @@ StridedWorkspace strided_workspace(int batch, int n) {
   w.kp = w.qp + planes;
   w.vp = w.kp + planes;
   w.scales = w.vp + planes;
-  w.magnitudes = w.scales + seg(2 * (size_t)batch * fpx::kHeads * (np / 32) * sizeof(float));
+  w.magnitudes = w.scales + seg(3 * (size_t)batch * fpx::kHeads * (np / 32) * sizeof(float));
   w.partial = w.magnitudes + seg(fpx::kMagnitudeWords * sizeof(uint32_t));
   const size_t groups = (3 * (size_t)batch * fpx::kHeads * (np / 32) + 3) / 4;
   w.total = w.partial + seg(3 * groups * sizeof(float));

@@ -34,6 +34,7 @@ __global__ __launch_bounds__(256) void mask_rows_kernel(const float* __restrict_
   const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (i >= rows) return;
   uint32_t part[kTileFlagParts][kTileFlagWords] = {};
+  float vmax = -INFINITY;  // NaN-propagating max of the row's mask biases
   for (int k0 = 0; k0 < np; k0 += 64) {
     const int k = k0 + lane;
     float v = -INFINITY;
@@ -41,6 +42,7 @@ __global__ __launch_bounds__(256) void mask_rows_kernel(const float* __restrict_
       const float m = mask ? mask[i * ms_i + k * ms_j] : 0.0f;
       v = !mask ? 0.0f : kFromMask ? inf * (m - 1.0f) : m;
     }
+    vmax = __builtin_elementwise_maximum(vmax, v);
     mbias[(int64_t)i * np + k] = v;
     const uint64_t nz = __ballot(v != 0.0f);
     const uint64_t far = __ballot(v <= -kSkipMask);
@@ -57,6 +59,7 @@ __global__ __launch_bounds__(256) void mask_rows_kernel(const float* __restrict_
       }
     }
   }
+  part[kTileFlagMaxPart][0] = __builtin_bit_cast(uint32_t, wave_max(vmax));
   uint32_t* dst = flags + (int64_t)i * kTileFlagParts * kTileFlagWords;
 #pragma unroll
   for (int pt = 0; pt < kTileFlagParts; ++pt)

@@ -20,7 +20,8 @@ namespace fpx {
 //                        part 0 = some key of 32-key tile t has a nonzero
 //                        mask bias; of part 1 = every key of tile t has one;
 //                        of part 2 = every key of tile t has a mask bias at
-//                        or below -kSkipMask
+//                        or below -kSkipMask; word 0 of part 3 = the row's
+//                        largest mask bias as float bits (NaN-propagating)
 //                magnitudes: nullable, kMagnitudeWords written by the
 //                        prepare projection (see ProjArgs::magnitudes)
 //                bias : [H][np][np] in fragment order (bias_frag_index)
@@ -44,7 +45,8 @@ enum AttnLayout { kAttnBlock = 0, kAttnHeadLast = 1, kAttnStrided = 2, kAttnStag
 
 // Words of per-row tile flags: 32-key tiles of np <= 4096 keys.
 constexpr int kTileFlagWords = 4;
-constexpr int kTileFlagParts = 3;
+constexpr int kTileFlagParts = 4;
+constexpr int kTileFlagMaxPart = 3;
 
 // Per-tile exponent range of the fp16 planes: |e| <= kPlaneExpMax, so the
 // product scale 2^-(e_q + e_k) times log2(e) stays a normal float.
@@ -53,11 +55,18 @@ constexpr int kPlaneExpMax = 63;
 // Trailing key tiles whose every mask bias is <= -kSkipMask are not visited
 // on rows that have an unmasked key, when the logit magnitude bound
 // B = 32 max|q| max|k| + max|bias| (q as stored, natural units) is below
-// kSkipBound and max|v| is finite.  Their weights are then exactly 0: a skipped key's log2-domain
-// logit lies at least (kSkipMask - 2 B) log2(e) - 56 > 7e8 below the row's
-// softmax reference, so exp2 underflows to 0 (bit-identical results).
+// kSkipBound and max|v| is finite.  Their weights are then exactly 0: a
+// skipped key's log2-domain logit lies at least (kSkipMask - 2 B) log2(e)
+// > 5e8 below the row's softmax reference (which is at least the logit of
+// the row's unmasked key), so exp2 underflows to 0 (bit-identical results).
 constexpr float kSkipMask = 536870912.0f;  // 2^29
 constexpr float kSkipBound = 67108864.0f;  // 2^26
+// The FP32 block attention's fast softmax (attention_split.hip) runs on rows
+// with an unmasked key when B plus the row's largest mask bias (if positive)
+// is below kFastBound: every logit of an unmasked key then lies within 2^22
+// of 0 in log2 units, so the integer softmax reference stays exact when a
+// tile's plane exponent is added to it.
+constexpr float kFastBound = 2097152.0f;  // 2^21
 // Words of the magnitude record: max|q|, max|k|, max|v|, max|bias| as float
 // bits (atomicMax on non-negative floats; a NaN sorts above inf, so any
 // non-finite value disables the skip), then 1 once the projection wrote them.
@@ -103,7 +112,7 @@ hipError_t launch_attention(int layout, const AttnArgs& args, hipStream_t stream
 hipError_t launch_attention_split(int layout, const AttnArgs& args, hipStream_t stream);
 // kAttnStrided q, k, v of args -> the plane layout of kAttnStaged: q_planes,
 // k_planes, v_planes each [batch][4] slices of np * 128 bytes, scales
-// [2][batch][4][np / 32] floats.
+// [3][batch][4][np / 32] floats.
 // magnitudes (nullable, with partial of 3 stage_planes_groups floats):
 // words 0-2 of the record (max |q|, |k|, |v|) and word 4.
 int64_t stage_planes_groups(const AttnArgs& args);
@@ -150,11 +159,14 @@ struct ProjArgs {
   //         per 32 x 32 (rows j, head channels) tile so that the tile's max
   //         |value| 2^e lies in [2^14, 2^15); hi = fp16(x 2^e) and lo =
   //         fp16(x 2^e - hi) carry 22 bits;
-  //   v^T:  [np / 32 key tiles][32 channels][32 key positions] bf16 hi =
-  //         bf16(x), lo = bf16(x - hi); key 4g + e of a tile at position
+  //   v^T:  [np / 32 key tiles][32 channels][32 key positions] fp16 of the
+  //         value times 2^e, e per key tile (value_plane_exp of its max
+  //         |value|: [2^14, 2^15) as above, kPlaneExpMax for a zero tile),
+  //         hi and lo as for q, k; key 4g + e of a tile at position
   //         16 (g / 4) + 4 (0, 2, 1, 3)[g % 4] + e (the S^T accumulator's
   //         register order);
-  //   scales[(t * rows_i + i) * 4 + h][j / 32] = 2^-e for t = 0 (q), 1 (k).
+  //   scales[(t * rows_i + i) * 4 + h][j / 32] = 2^-e for t = 0 (q), 1 (k),
+  //         2 (v^T).
   int planes;
   float* scales;
   int np;

@@ -102,22 +102,32 @@ __device__ __forceinline__ void store_tile(const ProjArgs& a, int tile, int tile
         a.scales[(((int64_t)group * a.rows_i + i) * kHeads + hw) * (a.np >> 5) + tile % tiles_j] =
             __builtin_ldexpf(1.0f, -e);
     } else if (group == 2) {
-      // v^T: bf16 planes [np / 32 tiles][32 channels][32 key positions],
-      // keys of a tile in the order of the S^T accumulator registers (key
-      // group g of four at position 16 (g / 4) + 4 (0, 2, 1, 3)[g % 4]).
-      // This lane's keys 8 rr + e + 4 half sit at positions 8 half + 4 rr + e
-      // (rr < 2) and 16 + 8 half + 4 (rr - 2) + e.
+      // v^T: fp16 planes [np / 32 tiles][32 channels][32 key positions],
+      // the tile scaled by 2^e (its max |value| in [2^14, 2^15), as q and k;
+      // value_plane_exp), keys of a tile in the order of the S^T accumulator
+      // registers (key group g of four at position 16 (g / 4) + 4 (0, 2, 1,
+      // 3)[g % 4]).  This lane's keys 8 rr + e + 4 half sit at positions
+      // 8 half + 4 rr + e (rr < 2) and 16 + 8 half + 4 (rr - 2) + e.
+      float m = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) m = __builtin_elementwise_maximum(m, __builtin_fabsf(acc[r]));
+      const int e = value_plane_exp(wave_max(m));
+      const float f = __builtin_ldexpf(1.0f, e);
       uint8_t* base = reinterpret_cast<uint8_t*>(a.vt) + bh * slice_bytes +
                       (int64_t)(tile % tiles_j) * 2048 + l32 * 64 + 16 * half;
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         bf16x8 hi, lo;
-        split2(f32x8{acc[8 * q + 0], acc[8 * q + 1], acc[8 * q + 2], acc[8 * q + 3], acc[8 * q + 4],
-                     acc[8 * q + 5], acc[8 * q + 6], acc[8 * q + 7]},
-               hi, lo);
+        split_f16(f32x8{acc[8 * q + 0] * f, acc[8 * q + 1] * f, acc[8 * q + 2] * f,
+                        acc[8 * q + 3] * f, acc[8 * q + 4] * f, acc[8 * q + 5] * f,
+                        acc[8 * q + 6] * f, acc[8 * q + 7] * f},
+                  hi, lo);
         *(bf16x8*)(base + 32 * q) = hi;
         *(bf16x8*)(base + (slice_bytes >> 1) + 32 * q) = lo;
       }
+      if (half == 0 && l32 == 0)
+        a.scales[(((int64_t)2 * a.rows_i + i) * kHeads + hw) * (a.np >> 5) + tile % tiles_j] =
+            __builtin_ldexpf(1.0f, -e);
     } else {
       float* dst = a.gs + ((int64_t)i * a.np + j0) * kHidden + col_w;
 #pragma unroll

@@ -15,6 +15,7 @@
 #pragma once
 
 #include "common.hpp"
+#include "kernels.hpp"
 
 namespace fpx {
 
@@ -170,16 +171,38 @@ __device__ __forceinline__ f32x4 mfma16_f16(bf16x8 a, bf16x8 b, f32x4 c) {
 __device__ __forceinline__ int plane_exp(float m) {
   return (m > 0.f && m < INFINITY) ? 15 - __builtin_amdgcn_frexp_expf(m) : 0;
 }
+// Plane exponent of a v^T tile: plane_exp clamped to |e| <= kPlaneExpMax,
+// and kPlaneExpMax for a zero tile, so that it never lowers the smallest
+// exponent of a row (the attention scales each tile's weights by
+// 2^(e_min - e_t) before the product: see attention_split.hip).
+__device__ __forceinline__ int value_plane_exp(float m) {
+  if (m == 0.f) return kPlaneExpMax;
+  const int e = plane_exp(m);
+  return e < -kPlaneExpMax ? -kPlaneExpMax : e > kPlaneExpMax ? kPlaneExpMax : e;
+}
+// e of a power-of-two inverse plane scale s = 2^-e (a normal float).
+__device__ __forceinline__ int inv_scale_exp(float s) {
+  return 1 - __builtin_amdgcn_frexp_expf(s);
+}
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+// -1.0f in an SGPR the optimiser cannot fold, so that the residual
+// fma(float(hi), -1, x) = x - hi stays one v_fma_mix_f32 (the fp16 operand
+// converted in the instruction) instead of a conversion and a subtraction.
+__device__ __forceinline__ float opaque_minus_one() {
+  float m;
+  asm("s_mov_b32 %0, 0xbf800000" : "=s"(m));
+  return m;
+}
 template <int N>
 __device__ __forceinline__ void split_f16_words(const float* x, uint32_t* hi, uint32_t* lo) {
   f32x2 r[N / 2];
+  const float m1 = opaque_minus_one();
 #pragma unroll
   for (int i = 0; i < N / 2; ++i) {
     const f32x2 v = {x[2 * i], x[2 * i + 1]};
     const f16x2 h = __builtin_convertvector(v, f16x2);
     hi[i] = __builtin_bit_cast(uint32_t, h);
-    r[i] = v - __builtin_convertvector(h, f32x2);
+    r[i] = f32x2{__builtin_fmaf((float)h.x, m1, v.x), __builtin_fmaf((float)h.y, m1, v.y)};
   }
 #pragma unroll
   for (int i = 0; i < N / 2; ++i) lo[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(r[i], f16x2));

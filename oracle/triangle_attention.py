@@ -105,7 +105,7 @@ def permute_final_dims(t: torch.Tensor, inds: Sequence[int]) -> torch.Tensor:
 
 
 def attention_core(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                   biases: Sequence[torch.Tensor]) -> torch.Tensor:
+                   biases: Sequence[torch.Tensor], *, logits_f32: bool = False) -> torch.Tensor:
     """Native ``_attention(q, k, v, biases)``: returns ``[*, H, Q, C]``.
 
     ``a = q @ k^T``; ``a += b`` for each bias in list order (mask bias first,
@@ -115,10 +115,23 @@ def attention_core(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     tests/operators/test_direct_attention.py:44-47.  Pinned by brute-force
     loops and by closed forms (N=1 gives v; zero logits give mean_k v; a +80
     bias selects one key; an all -inf row gives NaN) in tests/test_oracle.py.
+
+    ``logits_f32`` (float64 inputs): round the logits to float32 at the
+    native add points, ``fl32(fl32(fl32(s) + fl32(mb)) + fl32(bias))``, and
+    keep everything else in float64 -- the ``logits="f32"`` evaluation of
+    oracle/brute.py.  It reproduces what the FP32 native path does to fully
+    masked rows (-1e9 has a float32 spacing of 64, so their logits tie).
     """
     a = torch.matmul(q, permute_final_dims(k, (1, 0)))
-    for bias in biases:
-        a += bias
+    if logits_f32:
+        def fl32(t):
+            return t.to(torch.float32).to(a.dtype)
+        a = fl32(a)
+        for bias in biases:
+            a = fl32(a + fl32(bias))
+    else:
+        for bias in biases:
+            a += bias
     a = torch.softmax(a, dim=-1)
     return torch.matmul(a, v)
 
@@ -168,7 +181,7 @@ def triangle_bias(x_ln: torch.Tensor, p: BlockParams) -> torch.Tensor:
 
 def block(z: torch.Tensor, mask: torch.Tensor | None, p: BlockParams, *,
           ending: bool = False, outer_rows: torch.Tensor | None = None,
-          chunk: int = 64) -> torch.Tensor:
+          chunk: int = 64, logits_f32: bool = False) -> torch.Tensor:
     """Triangle-attention block ``(z[N,N,C], mask[N,N]) -> dz[N,N,C]``.
 
     Restates ``TriangleAttention.forward`` (patch 0005:14-48) with
@@ -184,6 +197,8 @@ def block(z: torch.Tensor, mask: torch.Tensor | None, p: BlockParams, *,
     (chunk invariance: docs/protenix-long1536.md:889-901).  The result then has
     shape ``[len(outer_rows), N, C]`` in the (possibly transposed) x frame.
     ``chunk`` bounds the materialised score tensor to ``chunk * H * N * N``.
+    ``logits_f32`` rounds the logits to float32 at the native add points
+    (see ``attention_core``); meant for float64 inputs.
     """
     x = z
     if ending:
@@ -203,7 +218,7 @@ def block(z: torch.Tensor, mask: torch.Tensor | None, p: BlockParams, *,
             biases.append(mask_bias(mask[sel], p.inf))
         biases.append(tri)
         q, k, v = prep_qkv(xs, p, apply_scale=True)
-        o = attention_core(q, k, v, biases).transpose(-2, -3)
+        o = attention_core(q, k, v, biases, logits_f32=logits_f32).transpose(-2, -3)
         out.append(wrap_up(o, xs, p))
     dz = torch.cat(out, dim=0) if out else x.new_empty((0, n, x.shape[-1]))
     if ending and outer_rows is None:

@@ -48,12 +48,12 @@ def test_abi_version_and_workspace_sizes(lib):
         for dtype, e in ((0, 4), (1, 2)):
             copies = 2 if dtype == 0 else 1  # FP32: unscaled and log2(e)-scaled bias
             # q, k, v^T; gate (rows padded to np); gated output; bias; mask bias;
-            # tile flags (3 parts of 4 words per row) plus the 5-word magnitude record;
-            # the q and k tiles' inverse scales of the plane layout
+            # tile flags (4 parts of 4 words per row) plus the 5-word magnitude record;
+            # the q, k and v^T tiles' inverse scales of the plane layout
             expected = (3 * seg(n * 4 * np_ * 32 * e) + seg(n * np_ * 128 * e)
                         + seg(n * n * 128 * e)
                         + seg(4 * np_ * np_ * e * copies) + seg(n * np_ * 4)
-                        + seg((n * 12 + 5) * 4) + seg(2 * n * 4 * (np_ // 32) * 4))
+                        + seg((n * 16 + 5) * 4) + seg(3 * n * 4 * (np_ // 32) * 4))
             assert lib.fpx_tri_attn_workspace_bytes(n, 128, 4, 32, dtype) == expected
     for bad in ((0, 128, 4, 32, 0), (4097, 128, 4, 32, 0), (64, 64, 4, 32, 0),
                 (64, 128, 8, 32, 0), (64, 128, 4, 16, 0), (64, 128, 4, 32, 7)):
@@ -64,11 +64,11 @@ def test_strided_workspace_sizes(lib):
     seg = lambda b: -(-b // 256) * 256  # noqa: E731
     for batch, n in ((1, 1), (7, 96), (1536, 1000), (1536, 1536), (3, 4096)):
         np_ = -(-n // 128) * 128
-        # two fragment-order bias copies; mask-bias rows; tile flags (3 x 4 words);
+        # two fragment-order bias copies; mask-bias rows; tile flags (4 x 4 words);
         # q, k, v planes (np * 128 bytes per row and head); their scales; the
         # magnitude record (5 words); the staging's per-group maxima
-        expected = (2 * seg(4 * np_ * np_ * 4) + seg(batch * np_ * 4) + seg(batch * 12 * 4)
-                    + 3 * seg(batch * 4 * np_ * 128) + seg(2 * batch * 4 * (np_ // 32) * 4)
+        expected = (2 * seg(4 * np_ * np_ * 4) + seg(batch * np_ * 4) + seg(batch * 16 * 4)
+                    + 3 * seg(batch * 4 * np_ * 128) + seg(3 * batch * 4 * (np_ // 32) * 4)
                     + seg(5 * 4) + seg(3 * ((3 * batch * 4 * (np_ // 32) + 3) // 4) * 4))
         assert lib.fpx_attn_strided_workspace_bytes(batch, n) == expected
     for bad in ((0, 8), (2, 0), (2, 4097)):

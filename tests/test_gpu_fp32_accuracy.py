@@ -1,0 +1,129 @@
+"""The FP32 block computes at FP32 accuracy, held to the float64 oracle.
+
+The reference's FP32 path is plain FP32 arithmetic (TF32 off:
+python/fireprot_workers/protenix.py:113-114), and its operator tests hold the
+FP32 attention core to 2e-5 against native at full N=1536
+(tests/operators/test_long1536_attention.py:71).  The HIP block runs its
+products on the 16-bit matrix cores through power-of-two scaled fp16 (hi, lo)
+planes; these tests show that this costs no accuracy against FP32 itself.
+
+Bar, per configuration, node and region: the HIP result's max error against
+the float64 oracle must stay within max(2e-6 * max|ref|, twice the error of
+the same oracle evaluated in FP32 (the native path)).  A scheme with 16-bit
+significands anywhere in P.V fails it (about 6x over at C4).
+
+Rows whose keys are all masked follow the FP32 native path's logit ties (the
+-1e9 mask bias has a float32 spacing of 64), which plain float64 does not
+show; their float64 reference rounds the logits to float32 at the native add
+points (``logits_f32``), pinned by the brute-force fixtures.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from fireprot_amd import block as hip_block
+from fireprot_amd import workloads
+from oracle import triangle_attention as oracle
+from tests.helpers import hip_weights, oracle_params
+from tests.test_gpu_block import _sample_rows
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-6
+
+
+def strict_close(name: str, actual: torch.Tensor, ref64: torch.Tensor, ref32: torch.Tensor,
+                 tol: float = TOL) -> None:
+    """max|actual - ref64| <= max(tol * max|ref64|, 2 max|ref32 - ref64|); NaN where ref64 is."""
+    actual = actual.double()
+    nan = torch.isnan(ref64)
+    assert torch.equal(torch.isnan(actual), nan), f"{name}: NaN positions differ"
+    keep = ~nan
+    err = (actual - ref64)[keep].abs().max().item() if keep.any() else 0.0
+    err32 = (ref32.double() - ref64)[keep].abs().max().item() if keep.any() else 0.0
+    ref = ref64[keep].abs().max().item() if keep.any() else 0.0
+    bar = max(tol * ref, 2.0 * err32)
+    print(f"{name}: max|err|={err:.3e} fp32 oracle {err32:.3e} max|ref|={ref:.3e} "
+          f"bar={bar:.3e} ratio={err / max(err32, 1e-30):.2f}", flush=True)
+    assert err <= bar, f"{name}: {err:.3e} > {bar:.3e}"
+
+
+def _check_regions(name, actual, z, mask, w, ending, rows, valid):
+    """actual: rows ``rows`` of the block output in the x frame."""
+    p32 = oracle_params(w)
+    p64 = p32.to(torch.float64)
+    z64 = z.double()
+    m64 = None if mask is None else mask.double()
+    valid = z.shape[0] if valid is None else valid
+    for region, sel in (("valid", rows < valid), ("padded", rows >= valid)):
+        if not sel.any():
+            continue
+        sub = rows[sel]
+        ref32 = oracle.block(z, mask, p32, ending=ending, outer_rows=sub)
+        ref64 = oracle.block(z64, m64, p64, ending=ending, outer_rows=sub,
+                             logits_f32=(region == "padded"))
+        strict_close(f"{name} {region}", actual[sel], ref64, ref32)
+
+
+def _run_rows(z, mask, w, ending, rows):
+    with torch.inference_mode():
+        out = hip_block.triangle_attention_block(
+            z.cuda(), None if mask is None else mask.cuda(), hip_weights(w), ending=ending)
+        x_frame = out.transpose(0, 1) if ending else out
+        picked = x_frame[rows.cuda()].cpu()
+        torch.cuda.synchronize()
+    del out, x_frame
+    torch.cuda.empty_cache()
+    return picked
+
+
+@pytest.mark.parametrize("ending", [False, True])
+def test_c2_full_at_fp32_accuracy(ending):
+    cfg = workloads.CONFIGS["c2"]
+    print(f"case {cfg.name} ending={ending} (all rows)", flush=True)
+    z, mask, w = workloads.make_inputs(cfg)
+    rows = torch.arange(cfg.n)
+    actual = _run_rows(z, mask, w, ending, rows)
+    _check_regions(f"{cfg.name} ending={ending}", actual, z, mask, w, ending, rows, cfg.valid)
+
+
+@pytest.mark.parametrize("key", ["c3", "c4"])
+@pytest.mark.parametrize("ending", [False, True])
+def test_long_configs_sampled_rows_at_fp32_accuracy(key, ending):
+    cfg = workloads.CONFIGS[key]
+    rows = _sample_rows(cfg.n, cfg.valid)
+    print(f"case {cfg.name} ending={ending} rows={rows.tolist()}", flush=True)
+    z, mask, w = workloads.make_inputs(cfg)
+    actual = _run_rows(z, mask, w, ending, rows)
+    _check_regions(f"{cfg.name} ending={ending}", actual, z, mask, w, ending, rows, cfg.valid)
+
+
+@pytest.mark.parametrize("bias_scale,z_scale", [(60.0, 1.0), (1e-3, 1.0), (1.0, 1e-3), (8.0, 1e3)])
+def test_extreme_scales_at_fp32_accuracy(bias_scale, z_scale):
+    """Logits of a few hundred, a near-zero bias, and tiny or huge z (LN
+    removes the z scale up to eps): the softmax reference and the per-tile
+    plane scales must keep FP32 accuracy across all of them."""
+    n = 200
+    z = workloads.make_pair(n, z_scale)
+    mask = workloads.make_mask(n, 170)
+    w = workloads.make_weights(bias_scale=bias_scale)
+    rows = torch.arange(n)
+    for ending in (False, True):
+        actual = _run_rows(z, mask, w, ending, rows)
+        _check_regions(f"bias x{bias_scale} z x{z_scale} ending={ending}", actual, z, mask, w,
+                       ending, rows, 170)
+
+
+@pytest.mark.parametrize("v_scale", [1e-6, 1e4])
+def test_value_weight_scales_at_fp32_accuracy(v_scale):
+    """W_v scaled far from 1: v^T planes are scaled per tile, so the products
+    keep their accuracy relative to the values."""
+    n = 160
+    z = workloads.make_pair(n)
+    mask = workloads.make_mask(n, 150)
+    w = workloads.make_weights(bias_scale=4.0)
+    w["w_v"] = w["w_v"] * v_scale
+    rows = torch.arange(n)
+    actual = _run_rows(z, mask, w, False, rows)
+    _check_regions(f"w_v x{v_scale}", actual, z, mask, w, False, rows, 150)

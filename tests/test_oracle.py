@@ -54,6 +54,21 @@ def test_float64_oracle_matches_brute_force(name, ending):
 
 @pytest.mark.parametrize("name", CASES)
 @pytest.mark.parametrize("ending", [False, True])
+def test_float64_oracle_with_float32_logits_matches_brute_force(name, ending):
+    """The float64 evaluation with logits rounded to float32 at the native add
+    points (the GPU parity bar for fully masked rows) against the brute
+    force's ``logits="f32"`` expectation, to float64 rounding."""
+    z, mask, params, expected = load_case(name)
+    dz = oracle.block(z, mask, params, ending=ending, logits_f32=True)
+    tag = "end" if ending else "start"
+    torch.testing.assert_close(dz, expected[f"dz_{tag}_f32l"], atol=1e-12, rtol=1e-10)
+    if name in ("n7_tail", "n6_order"):
+        # fully masked rows: the float32 logits tie where float64 does not
+        assert (dz - expected[f"dz_{tag}_f64"]).abs().max() > 1e-4
+
+
+@pytest.mark.parametrize("name", CASES)
+@pytest.mark.parametrize("ending", [False, True])
 def test_float32_oracle_matches_float32_logit_brute_force(name, ending):
     z, mask, params, expected = load_case(name, torch.float32)
     dz = oracle.block(z, mask, params, ending=ending)
@@ -200,7 +215,8 @@ def _mutated_block(monkeypatch, kind):
     elif kind == "bias_before_mask":
         orig = oracle.attention_core
         monkeypatch.setattr(oracle, "attention_core",
-                            lambda q, k, v, biases: orig(q, k, v, list(reversed(biases))))
+                            lambda q, k, v, biases, **kw: orig(q, k, v, list(reversed(biases)),
+                                                               **kw))
     else:
         raise ValueError(kind)
 
