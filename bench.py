@@ -10,12 +10,20 @@ Inputs, weights, outputs and workspace are resident in HBM before timing.
 
 Output: one JSON line.  ``value`` is the step's algorithmic TFLOP/s
 (2 x (512 N^3 + 164864 N^2) flop per step); ``ms_per_step`` covers both
-blocks.  ``roofline`` is the attention kernel alone (``fpx_tri_attn_attend``,
-512 N^3 flop per launch) timed with HIP events on the launch stream, against
-the 157.3 TFLOP/s FP32 matrix peak.  ``cpu_baseline`` times the CPU oracle
-(native PyTorch op order, FP32) on the host cores on the same step (about 16 s
-on a 16-core share).  ``roofline.traffic`` is the attention kernel's HBM bytes
-per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary.
+blocks.  ``roofline`` is the attention kernel alone (``fpx_tri_attn_attend``)
+timed with HIP events on the launch stream.  Its ``peak`` is that of the
+matrix unit the kernel issues: the FP32 block computes its products on the
+16-bit matrix cores (power-of-two scaled fp16 hi/lo planes, FP32-accurate),
+so the peak is the 2.5 PFLOP/s dense fp16/bf16 figure; ``achieved`` counts
+the algorithmic FP32 flop of the key tiles the kernel visits (trailing
+masked tiles whose weights are exactly 0 are left out), and
+``executed_frac`` the 16-bit matrix work it actually issues.  Under
+``FPX_ATTENTION_MFMA=f32`` the peak is the 157.3 TFLOP/s FP32 matrix peak.
+``roofline.traffic`` is the attention kernel's HBM bytes per launch from the
+committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary.  ``cpu_baseline`` times
+the CPU oracle (native PyTorch op order, FP32) on the lease's host cores on
+the same step, and ``parity`` compares the timed GPU outputs of that step with
+the oracle's, every element of both nodes (valid and padded rows apart).
 """
 from __future__ import annotations
 
@@ -55,21 +63,52 @@ def calibrate_copy(dev) -> None:
     del src, dst
 
 
-def cpu_baseline(cfg, z, mask, weights, budget_s: float = 40.0) -> dict:
-    """Time the CPU oracle (native op order) on the host cores.
+def host_cores() -> int:
+    """Cores this process may run on: the lease's CPU share (OMP_NUM_THREADS
+    when the host sets it, else the affinity mask)."""
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(int(env), affinity) if env.isdigit() and int(env) > 0 else affinity)
+
+
+def cpu_model() -> str:
+    try:
+        for line in pathlib.Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def host_record(threads: int) -> dict:
+    return {"cores": threads, "os_cpu_count": os.cpu_count(),
+            "affinity_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity")
+            else None, "cpu": cpu_model()}
+
+
+def cpu_baseline(cfg, z, mask, weights, budget_s: float = 40.0):
+    """Time the CPU oracle (native op order) on the lease's host cores.
 
     FP32 configurations run both directions in full (the starting node alone
     when it exceeds ``budget_s``, the ending node then taken as equal).  The
     BF16 configuration runs the native path on bfloat16 tensors for 8 and 24
     evenly spaced outer rows per direction and extrapolates linearly in rows
     (rows are independent), since the full N=2048 BF16 CPU run takes minutes.
+    Returns the record and the oracle outputs it computed: ``{"start": dz,
+    "end": dz}`` in z's frame (full), or ``{"start_rows": (rows, dz_x), ...}``
+    for the sampled BF16 rows (x frame).
     """
     import torch
 
     from oracle import triangle_attention as oracle
 
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = host_cores()
     torch.set_num_threads(threads)
+    outputs = {}
     params = oracle.BlockParams(**weights)
     times = {}
     both = True
@@ -83,8 +122,9 @@ def cpu_baseline(cfg, z, mask, weights, budget_s: float = 40.0) -> dict:
                 for rows in (8, 24):
                     sel = torch.linspace(0, cfg.n - 1, rows).round().long()
                     t0 = time.perf_counter()
-                    run(z, mask, params, ending=ending, outer_rows=sel)
+                    res = run(z, mask, params, ending=ending, outer_rows=sel)
                     spent.append(time.perf_counter() - t0)
+                outputs[f"{key}_rows"] = (sel, res)
                 per_row = max((spent[1] - spent[0]) / 16, 0.0)
                 times[key] = max(spent[0] - 8 * per_row, 0.0) + per_row * cfg.n
                 log(f"cpu oracle ending={ending}: 8 rows {spent[0]:.2f} s, 24 rows {spent[1]:.2f} s")
@@ -94,7 +134,7 @@ def cpu_baseline(cfg, z, mask, weights, budget_s: float = 40.0) -> dict:
                 both = False
                 break
             t0 = time.perf_counter()
-            run(z, mask, params, ending=ending)
+            outputs[key] = run(z, mask, params, ending=ending)
             times[key] = time.perf_counter() - t0
             log(f"cpu oracle ending={ending}: {times[key]:.2f} s")
     from oracle.triangle_attention import block_flops
@@ -107,17 +147,53 @@ def cpu_baseline(cfg, z, mask, weights, budget_s: float = 40.0) -> dict:
     else:
         measured = ("both directions in full" if both
                     else "the starting node in full (ending node taken as equal)")
-    return {
+    record = {
         "value": round(flop / total / 1e12, 5),
         "unit": "TFLOP/s",
-        "cores": threads,
         "kind": "port",
         "sample": (f"CPU oracle (native PyTorch op order, {threads} threads, outer rows in "
                    f"chunks) on the same {cfg.name} inputs, {measured}: "
                    f"start {times['start']:.1f} s + end {times['end']:.1f} s per step"),
         "step_s": round(total, 2),
-        "cpu": platform.processor() or platform.machine(),
+        **host_record(threads),
     }
+    return record, outputs
+
+
+def parity_report(cfg, gpu: dict, oracle_out: dict) -> dict:
+    """Max |GPU - CPU oracle| over the step's outputs, valid and padded outer
+    rows apart (x frame), with the largest |oracle| value beside it."""
+    import torch
+
+    valid = cfg.valid if cfg.valid is not None else cfg.n
+    report = {}
+    for key in ("start", "end"):
+        if key in oracle_out:
+            ref = oracle_out[key].double()
+            got = gpu[key].double()
+            if key == "end":
+                ref, got = ref.transpose(0, 1), got.transpose(0, 1)
+            rows = torch.arange(cfg.n)
+        elif f"{key}_rows" in oracle_out:
+            rows, ref = oracle_out[f"{key}_rows"]
+            ref = ref.double()
+            full = gpu[key].transpose(0, 1) if key == "end" else gpu[key]
+            got = full[rows].double()
+        else:
+            continue
+        entry = {"rows_compared": int(len(rows))}
+        for region, sel in (("valid", rows < valid), ("padded", rows >= valid)):
+            if bool(sel.any()):
+                diff = (got[sel] - ref[sel]).abs()
+                nan_same = bool(torch.equal(torch.isnan(got[sel]), torch.isnan(ref[sel])))
+                finite = torch.isfinite(ref[sel])
+                entry[region] = {"max_abs": float(diff[finite].max()) if bool(finite.any())
+                                 else 0.0,
+                                 "max_ref": float(ref[sel][finite].abs().max())
+                                 if bool(finite.any()) else 0.0,
+                                 "nan_positions_equal": nan_same}
+        report[key] = entry
+    return report
 
 
 OF3_METRIC = "OpenFold3 _attention ms + TFLOP/s (% MFMA peak) at B=N=1536 FP32, 1 GPU"
@@ -143,7 +219,8 @@ def split_executed(batch: int, n: int, ms: float, tiles: int | None = None,
     against 2 * 65536 algorithmic flop:
       - caller-supplied q/k/v (strided layout): 6 bf16 terms of S^T and 3 of
         O^T = 18 MFMAs;
-      - the block's fp16 planes: 3 fp16 terms of S^T and 3 bf16 of O^T = 12.
+      - fp16 planes (the block's, and the staged strided operands): 3 fp16
+        terms of S^T and 3 of O^T = 12.
     fp16 and bf16 MFMAs share one dense peak.  Query rows are padded to 128,
     keys to 32.  ``tiles``: key tiles visited summed over the outer rows
     (default: every tile of every row)."""
@@ -153,8 +230,9 @@ def split_executed(batch: int, n: int, ms: float, tiles: int | None = None,
     per_tile = 12 if fp16_planes else 18
     executed = visited * 4 * (np_ // 32) * per_tile * 32768
     executed_tflops = executed / (ms * 1e-3) / 1e12
-    unit = ("fp16 (2-plane q, k scaled per tile) for S^T, bf16 (2-plane v, p) for O^T"
-            if fp16_planes else "bf16 (exact 3-plane split of K and Q, 2-plane V and P)")
+    unit = ("fp16 hi/lo planes scaled by powers of two (q, k per 32x32 tile; v^T per key "
+            "tile; p per tile), three terms per product" if fp16_planes
+            else "bf16 (exact 3-plane split of K and Q, 2-plane V and P)")
     return {
         "matrix_unit": unit,
         "visited_key_tile_frac": round(visited / (batch * nkt), 4),
@@ -255,6 +333,10 @@ def bench_openfold3(args) -> dict:
     flop = block_flops(n)["core"]
     tflops = flop / (ms * 1e-3) / 1e12
     fp32_mfma = os.environ.get("FPX_ATTENTION_MFMA") == "f32"
+    of3_visited = visited_key_tiles(n, n - 184, skip=not fp32_mfma)
+    of3_flop = flop * of3_visited // (n * -(-n // 32))
+    of3_peak = FP32_MFMA_PEAK_TFLOPS if fp32_mfma else BF16_MFMA_PEAK_TFLOPS
+    of3_achieved = of3_flop / (ms * 1e-3) / 1e12
     result = {
         "metric": OF3_METRIC,
         "value": round(tflops, 3),
@@ -279,19 +361,20 @@ def bench_openfold3(args) -> dict:
             "kernel": ("attention_kernel<kAttnStrided> + staging (fpx_attn_strided)" if fp32_mfma
                        else "attention_split_kernel<kAttnStaged> + plane, mask and bias staging"
                             " (fpx_attn_strided)"),
-            "bound": "mfma", "achieved": round(tflops, 3), "peak": FP32_MFMA_PEAK_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4),
+            "bound": "mfma", "achieved": round(of3_achieved, 3), "peak": of3_peak,
+            "unit": "TFLOP/s", "frac": round(of3_achieved / of3_peak, 4),
             "traffic": recorded_traffic("openfold3/fp32-mfma" if fp32_mfma else "openfold3"),
-            "flop_per_launch": flop, "avg_launch_ms": round(ms, 4),
-            **({} if fp32_mfma else split_executed(n, n, ms, visited_key_tiles(n, n - 184, skip=True),
-                                                   fp16_planes=True)),
+            "flop_per_launch": of3_flop, "flop_all_tiles": flop,
+            "fp32_algorithmic_tflops_all_tiles": round(tflops, 3),
+            "avg_launch_ms": round(ms, 4),
+            **({} if fp32_mfma else split_executed(n, n, ms, of3_visited, fp16_planes=True)),
         },
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
         from oracle import triangle_attention as oracle
 
-        threads = max(1, min(16, os.cpu_count() or 1))
+        threads = host_cores()
         torch.set_num_threads(threads)
         rows = torch.linspace(0, n - 1, 16).round().long().to(dev)
         parts = [t[rows].cpu() for t in (q, k, v, mask)]
@@ -302,12 +385,11 @@ def bench_openfold3(args) -> dict:
             spent = time.perf_counter() - t0
         total = spent * n / 16
         result["cpu_baseline"] = {
-            "value": round(flop / total / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
-            "kind": "port",
+            "value": round(flop / total / 1e12, 5), "unit": "TFLOP/s", "kind": "port",
             "sample": (f"oracle attention_core (native op order, {threads} threads) on 16 "
                        f"evenly spaced rows of the same inputs, {spent:.1f} s, scaled to "
                        f"{n} rows: {total:.0f} s per step"),
-            "cpu": platform.processor() or platform.machine(),
+            **host_record(threads),
         }
     return result
 
@@ -405,7 +487,7 @@ def bench_trimul(args) -> dict:
     if not args.no_cpu_baseline:
         from oracle import triangle_multiplication as tm
 
-        threads = max(1, min(16, os.cpu_count() or 1))
+        threads = host_cores()
         torch.set_num_threads(threads)
         params = tm.TriMulParams(**w_cpu)
         rows = torch.linspace(0, n - 1, 8).round().long()
@@ -423,12 +505,12 @@ def bench_trimul(args) -> dict:
         total = sum(proj_s + (spent[d] - proj_s) * n / len(rows) for d in (True, False))
         result["cpu_baseline"] = {
             "value": round(2 * f["total"] / total / 1e12, 5), "unit": "TFLOP/s",
-            "cores": threads, "kind": "port",
+            "kind": "port",
             "sample": (f"oracle update (native op order, {threads} threads) on 8 evenly spaced "
                        f"rows per direction ({spent[True]:.1f} s and {spent[False]:.1f} s, "
                        f"full-size projections {proj_s:.1f} s included), row part scaled to "
                        f"{n} rows: {total:.0f} s per step"),
-            "cpu": platform.processor() or platform.machine(),
+            **host_record(threads),
         }
     return result
 
@@ -481,6 +563,9 @@ def bench_transition(args) -> dict:
 
     flop = flops(n * n)
     value = flop / (ms * 1e-3) / 1e12
+    # fp16 planes on the 16-bit matrix cores unless the FP32 ones are selected
+    tr_peak = (FP32_MFMA_PEAK_TFLOPS if os.environ.get("FPX_ATTENTION_MFMA") == "f32"
+               else BF16_MFMA_PEAK_TFLOPS)
     result = {
         "metric": TRANSITION_METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
@@ -488,13 +573,13 @@ def bench_transition(args) -> dict:
         "data": "synthetic (seeded z ~ N(0,1), N(0,0.05^2) weights)",
         "config": {"workload": "transition-n1536-f32: z += transition(z), in place",
                    "n": n, "rows": n * n, "c": 128, "expansion": 4, "step_flop": flop,
-                   "mfma_peak_frac": round(value / FP32_MFMA_PEAK_TFLOPS, 4)},
+                   "peak": tr_peak, "peak_frac": round(value / tr_peak, 4)},
         "roofline": None, "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
         from oracle import transition as tr
 
-        threads = max(1, min(16, os.cpu_count() or 1))
+        threads = host_cores()
         torch.set_num_threads(threads)
         sample = z0.reshape(-1, 128)[:8192]
         with torch.inference_mode():
@@ -503,12 +588,11 @@ def bench_transition(args) -> dict:
             spent = time.perf_counter() - t0
         total = spent * n * n / sample.shape[0]
         result["cpu_baseline"] = {
-            "value": round(flop / total / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
-            "kind": "port",
+            "value": round(flop / total / 1e12, 5), "unit": "TFLOP/s", "kind": "port",
             "sample": (f"oracle transition (native op order, {threads} threads) on the first "
                        f"8192 pair rows ({spent:.2f} s), scaled to {n * n} rows: "
                        f"{total:.1f} s per step"),
-            "cpu": platform.processor() or platform.machine(),
+            **host_record(threads),
         }
     return result
 
@@ -672,7 +756,6 @@ def main() -> int:
     dev = torch.device("cuda:0")
     dtype = torch.bfloat16 if cfg.dtype == "bf16" else torch.float32
     dtype_code = block.DTYPES[dtype]
-    peak = BF16_MFMA_PEAK_TFLOPS if cfg.dtype == "bf16" else FP32_MFMA_PEAK_TFLOPS
     z = z_cpu.to(dtype).to(dev)
     mask = None if mask_cpu is None else mask_cpu.to(dev)
     weights = block.BlockWeights.from_tensors(**w, dtype=dtype).to(dev)
@@ -748,14 +831,21 @@ def main() -> int:
     value = step_flop / (ms_per_step * 1e-3) / 1e12
     fp32_mfma = os.environ.get("FPX_ATTENTION_MFMA") == "f32"
     traffic = recorded_traffic(f"{cfg.name}/fp32-mfma" if fp32_mfma else cfg.name)
-    attend_tflops = flops["core"] / (stages["attend"] * 1e-3) / 1e12
     split = cfg.dtype != "bf16" and not fp32_mfma
     if cfg.dtype == "bf16":
         kernel_name = "attention_bf16_kernel (fpx_tri_attn_attend, BF16)"
     elif split:
-        kernel_name = "attention_split_kernel (fpx_tri_attn_attend)"
+        kernel_name = ("attention_split_kernel<kAttnBlock, fast | exact> "
+                       "(fpx_tri_attn_attend, fp16 planes)")
     else:
-        kernel_name = "attention_kernel<kAttnBlock> (fpx_tri_attn_attend)"
+        kernel_name = "attention_kernel<kAttnBlock> (fpx_tri_attn_attend, FP32 matrix cores)"
+    # The peak of the matrix unit the kernel issues: fp16/bf16 unless the FP32
+    # matrix cores are selected.
+    peak = FP32_MFMA_PEAK_TFLOPS if fp32_mfma and cfg.dtype != "bf16" else BF16_MFMA_PEAK_TFLOPS
+    nkt = -(-n // 32)
+    visited = visited_key_tiles(n, cfg.valid, skip=cfg.dtype != "bf16")
+    visited_flop = flops["core"] * visited // (n * nkt)
+    attend_tflops = visited_flop / (stages["attend"] * 1e-3) / 1e12
     roofline = {
         "kernel": kernel_name,
         "bound": "mfma",
@@ -764,13 +854,15 @@ def main() -> int:
         "unit": "TFLOP/s",
         "frac": round(attend_tflops / peak, 4),
         "traffic": traffic,
-        "flop_per_launch": flops["core"],
+        "flop_per_launch": visited_flop,
+        "flop_all_tiles": flops["core"],
+        "visited_key_tile_frac": round(visited / (n * nkt), 4),
         "avg_launch_ms": round(stages["attend"], 4),
+        "fp32_algorithmic_tflops_all_tiles": round(
+            flops["core"] / (stages["attend"] * 1e-3) / 1e12, 3),
     }
     if split:
-        roofline.update(split_executed(n, n, stages["attend"],
-                                       visited_key_tiles(n, cfg.valid, skip=True),
-                                       fp16_planes=True))
+        roofline.update(split_executed(n, n, stages["attend"], visited, fp16_planes=True))
     result = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -791,7 +883,7 @@ def main() -> int:
             "bias_scale": cfg.bias_scale,
             "block_ms": round(ms_per_step / 2, 4),
             "block_tflops": round(value, 3),
-            "block_mfma_peak_frac": round(value / peak, 4),
+            "block_peak_frac": round(value / peak, 4),
             "step_flop": step_flop,
             "stage_ms_start_node": {k: round(v, 4) for k, v in stages.items()},
         },
@@ -799,9 +891,13 @@ def main() -> int:
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
+        gpu_out = {"start": out_s.float().cpu(), "end": out_e.float().cpu()}
         del out_s, out_e, ws
         torch.cuda.empty_cache()
-        result["cpu_baseline"] = cpu_baseline(cfg, z_cpu, mask_cpu, w)
+        record, oracle_out = cpu_baseline(cfg, z_cpu, mask_cpu, w)
+        result["cpu_baseline"] = record
+        result["parity"] = parity_report(cfg, gpu_out, oracle_out)
+        log(f"parity vs CPU oracle: {json.dumps(result['parity'])}")
     print(json.dumps(result), flush=True)
     return 0
 

@@ -62,6 +62,9 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "fpx_tri_attn_attend": (_i, [_i, _i, _p, _sz, _p]),
     "fpx_tri_attn_finish": (_i, [_i, _p, _p, _i, _i, _p, _i64, _i64, _p, _sz, _p]),
     "fpx_attn_core": (_i, [_p, _p, _p, _p, _p, _i, _i, _p]),
+    "ck_attention": (_i, [_p, _p, _p, _p, _p, _i, _i, _p]),
+    "ck_attention_exact1536": (_i, [_p, _p, _p, _p, _p, _i, _i, _p]),
+    "ck_attention_vector_bias1000": (_i, [_p, _p, _p, _p, _p, _i, _i, _p]),
     "fpx_attn_core_masked": (_i, [_p, _p, _p, _p, _i64, _p, _i64, _p, _i, _i, _p]),
     "fpx_attn_strided_workspace_bytes": (_sz, [_i, _i]),
     "fpx_attn_strided": (_i, [

@@ -449,7 +449,27 @@ int fpx_attn_core_masked(const float* q, const float* k, const float* v, const f
 
 int fpx_attn_core(float* q, float* k, float* v, float* bias, float* out, int batch, int n,
                   void* stream) {
-  return fpx_attn_core_masked(q, k, v, nullptr, 0, bias, n, out, batch, n, stream);
+  // the reference's physical bias row stride (fireprot_ck_attention.cpp:37)
+  return fpx_attn_core_masked(q, k, v, nullptr, 0, bias, n == 1536 ? n + 16 : n, out, batch, n,
+                              stream);
+}
+
+int ck_attention(float* q, float* k, float* v, float* bias, float* out, int batch, int n,
+                 void* stream) {
+  if (!((batch == 1000 && n == 1000) || (batch == 512 && n == 1536))) return FPX_ERR_DIMS;
+  return fpx_attn_core(q, k, v, bias, out, batch, n, stream);
+}
+
+int ck_attention_exact1536(float* q, float* k, float* v, float* bias, float* out, int batch,
+                           int n, void* stream) {
+  if (batch != 512 || n != 1536) return FPX_ERR_DIMS;
+  return fpx_attn_core_masked(q, k, v, nullptr, 0, bias, 1552, out, batch, n, stream);
+}
+
+int ck_attention_vector_bias1000(float* q, float* k, float* v, float* bias, float* out,
+                                 int batch, int n, void* stream) {
+  if (batch != 1000 || n != 1000) return FPX_ERR_DIMS;
+  return fpx_attn_core_masked(q, k, v, nullptr, 0, bias, 1000, out, batch, n, stream);
 }
 
 size_t fpx_attn_strided_workspace_bytes(int batch, int n) {

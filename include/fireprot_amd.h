@@ -128,13 +128,39 @@ int fpx_tri_attn_finish(int dtype, const void* w_o, const void* b_o, int n, int 
  *   int ck_attention(float* q, float* k, float* v, float* bias, float* out,
  *                    int batch, int n, void* stream)
  * (kernels/amd/fireprot_ck_attention.cpp:34, 66, 102; ctypes binding at
- * python/fireprot/backends/amd/ck_attention.py:65-73).
+ * python/fireprot/backends/amd/ck_attention.py:65-73), for any batch >= 1 and
+ * n % 4 == 0 (the reference entries accept two shapes only).
  * q, k, v, out: [batch][heads=4][n][32] viewed with strides (n*128, 32, 128, 1),
  * i.e. memory [batch][n][4][32]; q already scaled by 1/sqrt(32).
- * bias: [1][4][n][n] contiguous, shared by every batch row.
- * Requires n % 4 == 0 and 16-byte aligned pointers. */
+ * bias: [1][4][n][S] shared by every batch row, with the reference's physical
+ * row stride S = n + 16 at n == 1536 (ck_attention.py:126-130,
+ * fireprot_ck_attention.cpp:37) and S = n otherwise.  Head stride n * S.
+ * Requires 16-byte aligned pointers (status 3 otherwise). */
 int fpx_attn_core(float* q, float* k, float* v, float* bias, float* out, int batch, int n,
                   void* stream);
+
+/* The reference's three exported entries, by name and behaviour, so that its
+ * ctypes loader (python/fireprot/backends/amd/ck_attention.py:65-73) binds
+ * this library unchanged and its attention() body (ck_attention.py:115-141)
+ * runs as written.  Same arguments and layout as fpx_attn_core; each accepts
+ * only the shapes of its reference counterpart and returns 2 for any other:
+ *   ck_attention                 (batch, n) = (1000, 1000) or (512, 1536);
+ *                                bias row stride 1552 at n = 1536
+ *                                (fireprot_ck_attention.cpp:34-37)
+ *   ck_attention_exact1536       (512, 1536), bias row stride 1552
+ *                                (fireprot_ck_attention.cpp:66-72)
+ *   ck_attention_vector_bias1000 (1000, 1000), bias row stride 1000
+ *                                (fireprot_ck_attention.cpp:102-107)
+ * A null or misaligned (16-byte) pointer returns 3 before any launch, as the
+ * reference's vector_bias1000 entry does (fireprot_ck_attention.cpp:106-107);
+ * the computation is FP32 on the FP32 matrix cores, asynchronous on the
+ * caller's stream, with no allocation. */
+int ck_attention(float* q, float* k, float* v, float* bias, float* out, int batch, int n,
+                 void* stream);
+int ck_attention_exact1536(float* q, float* k, float* v, float* bias, float* out, int batch,
+                           int n, void* stream);
+int ck_attention_vector_bias1000(float* q, float* k, float* v, float* bias, float* out,
+                                 int batch, int n, void* stream);
 
 /* Attention core with the additive mask bias of the two-bias form
  * biases = [mask_bias[batch,1,1,n], tri_bias[1,4,n,n]]

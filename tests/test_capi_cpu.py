@@ -20,7 +20,7 @@ HEADER = pathlib.Path(__file__).resolve().parents[1] / "include" / "fireprot_amd
 
 def _declared():
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return sorted(set(re.findall(r"\b(fpx_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b((?:fpx|ck)_\w+)\s*\(", text)))
 
 
 @pytest.fixture(scope="module")
@@ -234,3 +234,19 @@ def test_status_errors_raise():
     for code, word in ((2, "unsupported"), (3, "pointer"), (4, "workspace"), (98, "HIP")):
         with pytest.raises(RuntimeError, match=word):
             _native.check(code, "call")
+
+
+def test_reference_named_entries_reject_other_shapes_before_touching_memory(lib):
+    """ck_attention, ck_attention_exact1536 and ck_attention_vector_bias1000
+    accept only their reference shapes (fireprot_ck_attention.cpp:35, 68,
+    106) and check pointers before any launch."""
+    for name, good in (("ck_attention", ((1000, 1000), (512, 1536))),
+                       ("ck_attention_exact1536", ((512, 1536),)),
+                       ("ck_attention_vector_bias1000", ((1000, 1000),))):
+        fn = getattr(lib, name)
+        for batch, n in ((1, 1536), (512, 1000), (1000, 1536), (511, 1536), (1000, 999)):
+            if (batch, n) not in good:
+                assert fn(None, None, None, None, None, batch, n, None) == 2, (name, batch, n)
+        for batch, n in good:
+            assert fn(None, None, None, None, None, batch, n, None) == 3, (name, batch, n)
+            assert fn(16, 16, 16, 4, 16, batch, n, None) == 3, (name, batch, n)
