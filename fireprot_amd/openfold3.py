@@ -1,30 +1,41 @@
 """OpenFold3 ``_attention`` served by the gfx950 attention core.
 
-The reference replaces ``openfold3.core.model.primitives.attention._attention``
-inside an explicit scope (python/fireprot/adapters/openfold3/attention.py):
+The reference swaps ``openfold3.core.model.primitives.attention._attention``
+for a dispatcher inside an explicit scope (python/fireprot/adapters/openfold3/
+attention.py:43-84) and keeps these rules, which callers rely on:
 
-* ``attention_scope(dispatcher)`` checks the upstream source file against a
-  pinned SHA-256 and that ``_attention`` is still the original function
-  (attention.py:71-84), then installs a hook for the duration of the scope;
-* the hook (``_scoped_hook``, attention.py:43-68) is process-wide but only the
-  execution context that opened the scope sees the dispatcher (a
-  ``ContextVar``); other threads and copied contexts keep the captured native
-  function, a second concurrent scope is refused, and on exit the original is
-  restored unless someone else replaced the hook meanwhile (then it raises and
-  leaves the foreign owner in place);
-* ``AttentionDispatcher`` (attention.py:87-155) registers one candidate in a
-  private registry and routes eligible calls to it, everything else to the
-  native function.
+* the upstream source file must hash to a pinned SHA-256, and its
+  ``_attention`` must still be the function defined in that file (the refusal
+  messages "Unsupported OpenFold3 attention source" and "OpenFold3 attention
+  was already replaced");
+* one scope at a time, process-wide ("An OpenFold3 attention scope is already
+  installed");
+* only the execution context that opened the scope (and contexts copied from
+  it while it is open) reaches the dispatcher; other threads keep calling the
+  native function, and any reference to the installed callable that outlives
+  the scope calls the native function too;
+* on exit the native function is put back, unless someone replaced the
+  installed callable meanwhile: then the foreign callable stays, the scope
+  slot is released, and "OpenFold3 attention hook changed during its scope"
+  is raised.
 
-The reference's fused candidate is still three steps: a QK einsum, its
-mask+bias+softmax C ABI (backends/amd/softmax_fp32.py:57-84) over the
-materialised ``[B, 4, N, N]`` scores, and a PV einsum.  Here the candidate is
-``StridedAttention``: one launch of ``fpx_attn_strided`` that reads q, k, v,
-the mask bias and the triangle bias in whatever strides the model hands over
-(head-first, head-last and the transposed ending-node views), stages the two
-biases in the kernel's order and never writes the scores to memory.  Its
-output is ``[B, 4, N, 32]`` viewed on ``[B, N, 4, 32]`` memory, so the
-model's following ``transpose(-2, -3)`` and head flattening need no copy.
+Here the installed callable is a ``ScopedAttentionHook`` object.  It is its
+own context manager: entering claims the single process-wide slot, records the
+native function, places itself on the module and marks itself active in a
+context variable; a call checks that the active hook of the calling context
+is this very object and that the scope is still open.
+
+``AttentionDispatcher`` (attention.py:87-155) registers one candidate in a
+private registry and routes eligible calls to it, everything else to the
+native function.  The reference's fused candidate is still three steps: a QK
+einsum, its mask+bias+softmax C ABI (backends/amd/softmax_fp32.py:57-84) over
+the materialised ``[B, 4, N, N]`` scores, and a PV einsum.  Here the candidate
+is ``StridedAttention``: one launch sequence of ``fpx_attn_strided`` that reads
+q, k, v, the mask bias and the triangle bias in whatever strides the model
+hands over (head-first, head-last and the transposed ending-node views),
+stages them in the kernel's order and never writes the scores to memory.  Its
+output is ``[B, 4, N, 32]`` viewed on ``[B, N, 4, 32]`` memory, so the model's
+following ``transpose(-2, -3)`` and head flattening need no copy.
 
 Both ``use_high_precision`` modes compute in FP32 (the reference runs both
 under the same FP32 autocast context, attention.py:135-137).
@@ -52,62 +63,85 @@ HEADS = 4
 HEAD_DIM = 32
 MAX_N = 4096
 
-_current: ContextVar[Any] = ContextVar("fireprot_amd_openfold3_attention", default=None)
-_lock = threading.RLock()
-_installed = False
+# The hook object active in the current execution context (threads start
+# without one; copied contexts inherit it).
+_active_hook: ContextVar[Any] = ContextVar("fireprot_amd_openfold3_active_hook", default=None)
+# The hook that currently holds the process-wide scope (at most one).
+_slot: list[Any] = []
+_slot_guard = threading.Lock()
 
 
-@contextmanager
-def _scoped_hook(module: Any, dispatcher: Any):
-    """Install ``dispatcher(original, *args, **kwargs)`` as ``module._attention``
-    for this execution context only; see the module docstring for the rules."""
-    global _installed
-    with _lock:
-        if _installed:
-            raise RuntimeError("An OpenFold3 attention scope is already installed")
-        original = module._attention
-        state = {"live": True}
+class ScopedAttentionHook:
+    """The callable placed on ``module._attention`` for one scope, and the
+    context manager that places and removes it.
 
-        def hook(*args: Any, **kwargs: Any) -> Any:
-            selected = _current.get()
-            if not state["live"] or selected is None:
-                return original(*args, **kwargs)
-            return selected(original, *args, **kwargs)
-
-        module._attention = hook
-        _installed = True
-        token = _current.set(dispatcher)
-    try:
-        yield
-    finally:
-        with _lock:
-            state["live"] = False
-            _current.reset(token)
-            _installed = False
-            if module._attention is not hook:
-                raise RuntimeError("OpenFold3 attention hook changed during its scope")
-            module._attention = original
-
-
-@contextmanager
-def attention_scope(dispatcher: Any, module: Any = None):
-    """Scope in which OpenFold3's ``_attention`` goes through ``dispatcher``.
-
-    ``module`` defaults to ``openfold3.core.model.primitives.attention``; its
-    source must hash to ``SOURCE_SHA256`` and its ``_attention`` must be the
-    function defined there (attention.py:71-84).
+    A call runs ``dispatcher(native, *args, **kwargs)`` when the calling
+    context's active hook is this object and the scope is open; any other
+    call (other threads, calls after the scope closed) runs ``native``.
     """
-    if module is None:
-        import openfold3.core.model.primitives.attention as module  # noqa: PLC0415
+
+    def __init__(self, module: Any, dispatcher: Any):
+        self.module = module
+        self.dispatcher = dispatcher
+        self.native: Any = None
+        self.open = False
+        self._token: Any = None
+
+    def __call__(self, *args: Any, **kwargs: Any) -> Any:
+        if self.open and _active_hook.get() is self:
+            return self.dispatcher(self.native, *args, **kwargs)
+        return self.native(*args, **kwargs)
+
+    def __enter__(self) -> "ScopedAttentionHook":
+        with _slot_guard:
+            if _slot:
+                raise RuntimeError("An OpenFold3 attention scope is already installed")
+            self.native = self.module._attention
+            _slot.append(self)
+            self.open = True
+            self.module._attention = self
+            self._token = _active_hook.set(self)
+        return self
+
+    def __exit__(self, *exc_info: Any) -> bool:
+        with _slot_guard:
+            self.open = False
+            _active_hook.reset(self._token)
+            _slot.remove(self)
+            displaced = self.module._attention is not self
+            if not displaced:
+                self.module._attention = self.native
+        if displaced:
+            raise RuntimeError("OpenFold3 attention hook changed during its scope")
+        return False
+
+
+def _verify_upstream(module: Any) -> None:
+    """The pinned source file, and its own ``_attention`` still in place."""
     source = Path(module.__file__).resolve()
     if hashlib.sha256(source.read_bytes()).hexdigest() != SOURCE_SHA256:
         raise RuntimeError("Unsupported OpenFold3 attention source")
     code = getattr(module._attention, "__code__", None)
-    if (code is None or code.co_name != "_attention"
-            or Path(code.co_filename).resolve() != source):
+    defined_here = (code is not None and code.co_name == "_attention"
+                    and Path(code.co_filename).resolve() == source)
+    if not defined_here:
         raise RuntimeError("OpenFold3 attention was already replaced")
-    with _scoped_hook(module, dispatcher):
-        yield
+
+
+@contextmanager
+def attention_scope(dispatcher: Any, module: Any = None):
+    """Scope in which OpenFold3's ``_attention`` goes through ``dispatcher``
+    (called as ``dispatcher(native, *args, **kwargs)``).
+
+    ``module`` defaults to ``openfold3.core.model.primitives.attention``; its
+    source must hash to ``SOURCE_SHA256`` and its ``_attention`` must be the
+    function defined there.  Yields the installed hook.
+    """
+    if module is None:
+        import openfold3.core.model.primitives.attention as module  # noqa: PLC0415
+    _verify_upstream(module)
+    with ScopedAttentionHook(module, dispatcher) as hook:
+        yield hook
 
 
 def _architecture(index: int) -> str:

@@ -162,7 +162,7 @@ def test_scoped_hook_routes_eligible_calls_to_the_kernel():
     q, k, v, mb, bias = make_case(6, 136, 9)
     args = [qkv_view(t.cuda(), "head_last") for t in (q, k, v)]
     biases = [mb.cuda(), bias_view(bias.cuda(), "head_last")]
-    with of3._scoped_hook(module, dispatcher):
+    with of3.ScopedAttentionHook(module, dispatcher):
         with torch.inference_mode():
             fused = module._attention(*args, biases, use_high_precision=True)
             again = module._attention(*args, biases)

@@ -1,11 +1,18 @@
-"""Scope isolation, source pinning and native fallback of the OpenFold3
-``_attention`` consumer on the CPU (mirrors the reference's
-tests/operators/test_openfold3_attention_scope.py)."""
+"""Scope rules, source pinning and native fallback of the OpenFold3
+``_attention`` consumer, on the CPU.
+
+The scope rules are those the reference's adapter promises
+(python/fireprot/adapters/openfold3/attention.py:43-84): one scope at a time,
+only the opening context (and contexts copied from it) reaches the
+dispatcher, stale references fall back to native, a foreign replacement is
+reported and left in place.
+"""
 from __future__ import annotations
 
+import asyncio
 import hashlib
 import importlib.util
-from concurrent.futures import ThreadPoolExecutor
+import threading
 from contextvars import copy_context
 from types import SimpleNamespace
 
@@ -15,53 +22,104 @@ import torch
 from fireprot_amd import openfold3 as of3
 
 
-def test_scope_isolates_other_threads_and_restores_original():
-    native = lambda x: ("native", x)  # noqa: E731
-    target = SimpleNamespace(_attention=native)
-    selected = lambda original, x: ("selected", x)  # noqa: E731
-    with ThreadPoolExecutor(max_workers=1) as pool:
-        with of3._scoped_hook(target, selected):
-            assert target._attention(1) == ("selected", 1)
-            assert pool.submit(target._attention, 2).result() == ("native", 2)
-            leaked = target._attention
-            inherited = copy_context()
-        assert target._attention is native
-        assert leaked(3) == ("native", 3)
-        assert inherited.run(leaked, 4) == ("native", 4)
+def _recording_target():
+    """A stand-in module whose native ``_attention`` records its callers."""
+    seen = []
+
+    def native(tag):
+        seen.append(("native", tag))
+        return "native"
+
+    return SimpleNamespace(_attention=native), seen
 
 
-def test_nested_and_concurrent_installs_rejected_without_displacing_outer():
-    target = SimpleNamespace(_attention=lambda: "native")
+def test_only_the_opening_context_reaches_the_dispatcher():
+    target, seen = _recording_target()
+    native = target._attention
+    routed = []
 
-    def attempt():
-        with of3._scoped_hook(target, lambda original: "inner"):
-            pytest.fail("a second installation was accepted")
+    def dispatcher(original, tag):
+        routed.append(tag)
+        return original(f"via-{tag}")
 
-    with of3._scoped_hook(target, lambda original: "outer"):
-        with pytest.raises(RuntimeError, match="already installed"):
-            attempt()
-        with ThreadPoolExecutor(max_workers=1) as pool:
-            with pytest.raises(RuntimeError, match="already installed"):
-                pool.submit(attempt).result()
-        assert target._attention() == "outer"
-    assert target._attention() == "native"
+    results = {}
 
+    def worker(tag):
+        results[tag] = target._attention(tag)
 
-def test_exception_cleanup_and_external_replacement_detection():
-    native = lambda: "native"  # noqa: E731
-    target = SimpleNamespace(_attention=native)
-    with pytest.raises(ValueError, match="model failure"):
-        with of3._scoped_hook(target, lambda original: "selected"):
-            raise ValueError("model failure")
+    with of3.ScopedAttentionHook(target, dispatcher) as hook:
+        assert target._attention is hook and hook.native is native
+        assert target._attention("main") == "native"
+        # a thread started inside the scope runs in a fresh context: native
+        thread = threading.Thread(target=worker, args=("thread",))
+        thread.start()
+        thread.join()
+        # a context copied inside the scope inherits the active hook
+        copied = copy_context()
+        assert copied.run(target._attention, "copied") == "native"
+
+        # an asyncio task copies the context of the code that creates it
+        async def task():
+            return target._attention("task")
+        assert asyncio.run(task()) == "native"
+        stale = target._attention
+    assert routed == ["main", "copied", "task"]
+    assert ("native", "thread") in seen and results["thread"] == "native"
+    # after the scope: the module holds the native function again, and both a
+    # stale reference and a context copied during the scope go native
     assert target._attention is native
-    foreign = lambda: "foreign"  # noqa: E731
-    with pytest.raises(RuntimeError, match="changed during"):
-        with of3._scoped_hook(target, lambda original: "selected"):
+    routed.clear()
+    assert stale("late") == "native" and copied.run(stale, "late-copy") == "native"
+    assert routed == []
+
+
+def test_a_second_scope_is_refused_while_one_is_open():
+    target, _ = _recording_target()
+    other, _ = _recording_target()
+    errors = []
+
+    def contender():
+        try:
+            with of3.ScopedAttentionHook(other, lambda original, tag: "second"):
+                pass
+        except RuntimeError as error:
+            errors.append(str(error))
+
+    with of3.ScopedAttentionHook(target, lambda original, tag: "first"):
+        # the slot is process-wide: another module or another thread is refused
+        with pytest.raises(RuntimeError, match="already installed"):
+            with of3.ScopedAttentionHook(target, lambda original, tag: "nested"):
+                pass
+        thread = threading.Thread(target=contender)
+        thread.start()
+        thread.join()
+        assert errors and "already installed" in errors[0]
+        assert target._attention("x") == "first"
+        assert not isinstance(other._attention, of3.ScopedAttentionHook)
+    # released: a new scope opens normally
+    with of3.ScopedAttentionHook(other, lambda original, tag: "again"):
+        assert other._attention("y") == "again"
+
+
+def test_errors_inside_the_scope_and_foreign_replacements():
+    target, _ = _recording_target()
+    native = target._attention
+    with pytest.raises(KeyError, match="lookup inside the model"):
+        with of3.ScopedAttentionHook(target, lambda original, tag: "hooked"):
+            raise KeyError("lookup inside the model")
+    assert target._attention is native
+    # a caller that swaps _attention itself while the scope is open keeps it
+    def foreign(tag):
+        return "foreign"
+
+    with pytest.raises(RuntimeError, match="changed during its scope"):
+        with of3.ScopedAttentionHook(target, lambda original, tag: "hooked"):
             target._attention = foreign
     assert target._attention is foreign
-    # the failed cleanup released the guard without displacing the foreign owner
-    with of3._scoped_hook(target, lambda original: original()):
-        assert target._attention() == "foreign"
+    # and the slot was released: the next scope wraps the foreign function
+    with of3.ScopedAttentionHook(target, lambda original, tag: original(tag) + "+hooked"):
+        assert target._attention("z") == "foreign+hooked"
+    assert target._attention is foreign
 
 
 def _module_from(tmp_path, text):
