@@ -224,7 +224,11 @@ class StridedAttention:
         ok, _ = tensor_contract(query, key, value, biases)
         return ok and query.device.index == self.device
 
-    def __call__(self, query: Any, key: Any, value: Any, biases: Any) -> Any:
+    def __call__(self, query: Any, key: Any, value: Any, biases: Any,
+                 workspace: Any = None) -> Any:
+        """``workspace``: an optional uint8 device tensor of at least
+        ``fpx_attn_strided_workspace_bytes(B, N)`` bytes (any contents; a
+        fresh one is allocated when omitted)."""
         import torch
 
         if not self.supports(query, key, value, biases):
@@ -236,7 +240,11 @@ class StridedAttention:
             out = torch.empty((batch, n, HEADS, HEAD_DIM), device=query.device,
                               dtype=torch.float32).transpose(1, 2)
             size = self.library.fpx_attn_strided_workspace_bytes(batch, n)
-            workspace = torch.empty(size, dtype=torch.uint8, device=query.device)
+            if workspace is None:
+                workspace = torch.empty(size, dtype=torch.uint8, device=query.device)
+            elif (workspace.dtype != torch.uint8 or workspace.device != query.device
+                  or workspace.numel() < size):
+                raise ValueError(f"workspace needs {size} bytes on {query.device}")
             code = self.library.fpx_attn_strided(
                 q.data_ptr(), *q.stride()[:3], k.data_ptr(), *k.stride()[:3],
                 v.data_ptr(), *v.stride()[:3],

@@ -25,6 +25,7 @@ path of this package.
 from __future__ import annotations
 
 import functools
+import weakref
 from collections.abc import Callable, Sequence
 from typing import Any
 
@@ -157,12 +158,50 @@ def dispatch_triangle_attention(*, module: Any, q: Any, k: Any, v: Any, biases: 
 
 # ----------------------------------------------------------------- block
 
+MAX_N = 4096  # the largest pair size the block's C ABI accepts
+
+# Packed weights per module, rebuilt only when one of the module's parameter
+# tensors changes (identity, storage or in-place version) or the device does.
+_packed: "weakref.WeakKeyDictionary[Any, tuple[tuple, BlockWeights]]" = weakref.WeakKeyDictionary()
+
+
+def _parameter_key(module: Any) -> tuple:
+    """Identity, storage and version of every tensor _weights_of reads."""
+    owners = ((module.layer_norm, module.linear, module.mha.linear_q, module.mha.linear_k,
+               module.mha.linear_v, module.mha.linear_g, module.mha.linear_o)
+              if hasattr(module, "mha") else
+              (module.layernorm, module.linear_qkv, module.linear_bias, module.linear_g,
+               module.linear_out))
+    key = []
+    for owner in owners:
+        for name in ("weight", "bias"):
+            t = getattr(owner, name, None)
+            key.append(None if t is None else
+                       (id(t), t.data_ptr(), t._version, t.dtype, str(t.device)))
+    key.append((float(getattr(module, "inf", 1e9)),))
+    return tuple(key)
+
+
 def _weights_of(module: Any) -> BlockWeights:
-    if hasattr(module, "mha"):
-        return BlockWeights.from_protenix(module)
-    if hasattr(module, "linear_qkv"):
-        return BlockWeights.from_atlasfold(module)
-    raise TypeError(f"unrecognised triangle-attention module {type(module).__name__}")
+    """The module's weights packed for the block (w_qkvg concatenated), cached
+    per module while its parameters are unchanged."""
+    if not (hasattr(module, "mha") or hasattr(module, "linear_qkv")):
+        raise TypeError(f"unrecognised triangle-attention module {type(module).__name__}")
+    try:
+        key = _parameter_key(module)
+        hit = _packed.get(module)
+    except TypeError:  # not weak-referenceable: no cache
+        key, hit = None, None
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    weights = (BlockWeights.from_protenix(module) if hasattr(module, "mha")
+               else BlockWeights.from_atlasfold(module))
+    if key is not None:
+        try:
+            _packed[module] = (key, weights)
+        except TypeError:
+            pass
+    return weights
 
 
 def block_eligible(module: Any, z: Any, mask: Any) -> tuple[bool, str]:
@@ -173,6 +212,8 @@ def block_eligible(module: Any, z: Any, mask: Any) -> tuple[bool, str]:
         return False, "z is not a float32 or bfloat16 HIP tensor"
     if z.dim() != 3 or z.shape[0] != z.shape[1] or z.shape[2] != 128 or z.stride(2) != 1:
         return False, "z must be [N, N, 128] with unit channel stride"
+    if not 1 <= z.shape[0] <= MAX_N:
+        return False, f"N must lie in 1..{MAX_N}"
     align = 16 // z.element_size()
     if z.stride(0) % align or z.stride(1) % align or z.data_ptr() % 16:
         return False, "z rows are not 16-byte aligned"

@@ -203,3 +203,65 @@ def test_transition_capability_and_cpu_fallback(monkeypatch):
     with torch.inference_mode():
         assert htr.dispatch_transition(module=module, x=torch.randn(5, 5, 128),
                                        native=lambda **_: "native") == "native"
+
+
+class _FakeHipTensor:
+    """Just enough of a HIP tensor for block_eligible's shape checks."""
+
+    def __init__(self, n):
+        self.is_cuda = True
+        self.dtype = torch.float32
+        self.shape = (n, n, 128)
+        self.device = torch.device("cpu")
+
+    def dim(self):
+        return 3
+
+    def stride(self, d=None):
+        s = (self.shape[1] * 128, 128, 1)
+        return s if d is None else s[d]
+
+    def element_size(self):
+        return 4
+
+    def data_ptr(self):
+        return 0
+
+
+def test_block_eligibility_bounds_the_pair_size():
+    """N outside 1..4096 is rejected with a reason (the C ABI would return 2),
+    so the registry falls back to native instead of raising."""
+    m = _protenix_like()
+    for n in (0, 4097, 5000):
+        ok, reason = ta.block_eligible(m, _FakeHipTensor(n), None)
+        assert not ok and reason == "N must lie in 1..4096", (n, reason)
+
+
+class _TriangleAttentionModule(torch.nn.Module):
+    """A Protenix-shaped module (weak-referenceable, like the real one)."""
+
+    def __init__(self):
+        super().__init__()
+        self.layer_norm = torch.nn.LayerNorm(128)
+        self.linear = torch.nn.Linear(128, 4, bias=False)
+        self.mha = torch.nn.Module()
+        for name in ("linear_q", "linear_k", "linear_v"):
+            setattr(self.mha, name, torch.nn.Linear(128, 128, bias=False))
+        self.mha.linear_g = torch.nn.Linear(128, 128)
+        self.mha.linear_o = torch.nn.Linear(128, 128)
+        self.mha.no_heads, self.mha.c_hidden, self.inf = 4, 32, 1e9
+
+
+def test_packed_block_weights_are_cached_until_a_parameter_changes():
+    m = _TriangleAttentionModule()
+    first = ta._weights_of(m)
+    assert ta._weights_of(m) is first  # no re-concatenation per call
+    with torch.no_grad():
+        m.mha.linear_k.weight.mul_(2.0)  # in place: the version counter moves
+    second = ta._weights_of(m)
+    assert second is not first
+    assert torch.equal(second.w_qkvg[128:256], m.mha.linear_k.weight)
+    m.mha.linear_o = torch.nn.Linear(128, 128)  # a new parameter object
+    third = ta._weights_of(m)
+    assert third is not second and torch.equal(third.w_o, m.mha.linear_o.weight)
+    assert ta._weights_of(m) is third
