@@ -54,6 +54,15 @@ SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         _p, _i64, _i64,              # z_out (may be z), strides
         _p, _sz, _p,                 # workspace, bytes, stream
     ]),
+    "fpx_tri_attn_block_noalloc": (_i, [
+        _i, _p, _i64, _i64,          # dtype, z, z strides
+        _p, _i64, _i64,              # mask, mask strides
+        _p, _p, _f,                  # ln_w, ln_b, eps
+        _p, _p, _p, _p, _p,          # w_qkvg, b_g, w_bias, w_o, b_o
+        _f, _i, _i, _i, _i, _i,      # mask_inf, n, c, heads, head_dim, ending
+        _p, _i64, _i64,              # dz, dz strides
+        _p,                          # stream (no workspace)
+    ]),
     "fpx_tri_attn_prepare": (_i, [
         _i, _p, _i64, _i64, _p, _i64, _i64,   # dtype, z, strides, mask, strides
         _p, _p, _f, _p, _p, _p,               # ln_w, ln_b, eps, w_qkvg, b_g, w_bias

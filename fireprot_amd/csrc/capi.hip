@@ -10,6 +10,7 @@
 #include "kernels.hpp"
 
 #include <cmath>
+#include <mutex>
 
 namespace {
 
@@ -249,6 +250,40 @@ bool strided_operand_ok(const int64_t s[3], int n, bool slice) {
   return !slice || ((int64_t)(n - 1) * s[2] + fpx::kHeadDim) * 4 < 0x7fffffffll;
 }
 
+// Scratch of fpx_tri_attn_block_noalloc: the block workspace of N <= 128
+// (block_workspace(128, FPX_F32).total = 42565888 bytes, every smaller N and
+// the BF16 block need less), held by each GPU the library runs on until the
+// process ends.  Host code never passes `scratch` itself (its host-side name
+// is no device address): it uses the per-device address that
+// hipGetSymbolAddress returns.
+constexpr int kNoAllocMaxN = 128;
+constexpr size_t kNoAllocScratchBytes = 41u << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mutex;
+void* scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up once per device with
+// that device current; nullptr (and the HIP status in *err) on failure.
+void* device_scratch(hipError_t* err) {
+  int device = 0;
+  *err = hipGetDevice(&device);
+  if (*err != hipSuccess) return nullptr;
+  if (device < 0 || device >= kMaxDevices) {
+    *err = hipErrorInvalidDevice;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (scratch_ptr[device] == nullptr) {
+    void* ptr = nullptr;
+    *err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (*err != hipSuccess) return nullptr;
+    scratch_ptr[device] = ptr;
+  }
+  return scratch_ptr[device];
+}
+
 }  // namespace
 
 extern "C" {
@@ -402,6 +437,23 @@ int fpx_tri_attn_block(int dtype, const void* z, int64_t z_stride0, int64_t z_st
   return block_impl(dtype, z, z_stride0, z_stride1, mask, m_stride0, m_stride1, ln_w, ln_b, eps,
                     w_qkvg, b_g, w_bias, w_o, b_o, mask_inf, n, c, heads, head_dim, ending, dz,
                     dz_stride0, dz_stride1, workspace, workspace_bytes, stream, 0);
+}
+
+int fpx_tri_attn_block_noalloc(int dtype, const void* z, int64_t z_stride0, int64_t z_stride1,
+                               const float* mask, int64_t m_stride0, int64_t m_stride1,
+                               const void* ln_w, const void* ln_b, float eps, const void* w_qkvg,
+                               const void* b_g, const void* w_bias, const void* w_o,
+                               const void* b_o, float mask_inf, int n, int c, int heads,
+                               int head_dim, int ending, void* dz, int64_t dz_stride0,
+                               int64_t dz_stride1, void* stream) {
+  if (!block_dims_ok(n, c, heads, head_dim, dtype) || n > kNoAllocMaxN) return FPX_ERR_DIMS;
+  if (block_workspace(n, dtype).total > kNoAllocScratchBytes) return FPX_ERR_DIMS;
+  hipError_t err = hipSuccess;
+  void* ws = device_scratch(&err);
+  if (ws == nullptr) return status(err);
+  return block_impl(dtype, z, z_stride0, z_stride1, mask, m_stride0, m_stride1, ln_w, ln_b, eps,
+                    w_qkvg, b_g, w_bias, w_o, b_o, mask_inf, n, c, heads, head_dim, ending, dz,
+                    dz_stride0, dz_stride1, ws, kNoAllocScratchBytes, stream, 0);
 }
 
 int fpx_tri_attn_block_residual(int dtype, const void* z, int64_t z_stride0, int64_t z_stride1,

@@ -103,6 +103,24 @@ int fpx_tri_attn_block_residual(int dtype, const void* z, int64_t z_stride0, int
                                 int64_t out_stride0, int64_t out_stride1, void* workspace,
                                 size_t workspace_bytes, void* stream);
 
+/* fpx_tri_attn_block without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * workspace is a fixed device array inside the library (41 MiB per GPU the
+ * library runs on, held until the process ends), so it serves n <= 128 only
+ * (status 2 above); everything else is as fpx_tri_attn_block, and the result
+ * is bit-identical to it.  It allocates nothing and calls no allocating
+ * library routine.  Every call on one GPU uses that GPU's one array: calls
+ * that overlap on one GPU (two streams, or two host threads) race and must
+ * be serialised by the caller. */
+int fpx_tri_attn_block_noalloc(int dtype, const void* z, int64_t z_stride0, int64_t z_stride1,
+                               const float* mask, int64_t m_stride0, int64_t m_stride1,
+                               const void* ln_w, const void* ln_b, float eps, const void* w_qkvg,
+                               const void* b_g, const void* w_bias, const void* w_o,
+                               const void* b_o, float mask_inf, int n, int c, int heads,
+                               int head_dim, int ending, void* dz, int64_t dz_stride0,
+                               int64_t dz_stride1, void* stream);
+
 /* The block's three stages, run in this order on one workspace;
  * fpx_tri_attn_block is exactly prepare + attend + finish.  Split so a caller
  * (or a profiler) can time or overlap the stages; the workspace carries the
