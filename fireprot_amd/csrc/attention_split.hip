@@ -446,10 +446,10 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
       const f32x16 acc = scores(stage(t + 1));
       bf16x8 ph[2], pl[2];
       softmax(cur, t, ph, pl);
+      cur = init(clamp(t + 2));
       pv(stage(t), ph, pl);
       finish(nxt, acc, t + 1);
       dma(clamp(t + 3), stage(t + 3));
-      cur = init(clamp(t + 2));
       // Tile t+2 has landed once at most this iteration's two tile loads
       // and four bias-fragment loads are outstanding: vector memory loads
       // retire in issue order.

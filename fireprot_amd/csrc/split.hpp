@@ -185,27 +185,36 @@ __device__ __forceinline__ int inv_scale_exp(float s) {
   return 1 - __builtin_amdgcn_frexp_expf(s);
 }
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-// -1.0f in an SGPR the optimiser cannot fold, so that the residual
-// fma(float(hi), -1, x) = x - hi stays one v_fma_mix_f32 (the fp16 operand
-// converted in the instruction) instead of a conversion and a subtraction.
+// -1.0f in an SGPR the optimiser cannot fold, for the residual fma(float(hi),
+// -1, x) = x - hi of the fp16 splits below.
 __device__ __forceinline__ float opaque_minus_one() {
   float m;
   asm("s_mov_b32 %0, 0xbf800000" : "=s"(m));
   return m;
 }
+// N values (N even) -> fp16 hi and lo planes, packed two per word.  hi is one
+// v_cvt_pk_f16_f32 per pair; each lo is one v_fma_mixlo_f16 / v_fma_mixhi_f16:
+// fma(float(hi half), -1, x) rounded to fp16 into the low / high half of the
+// word.  x - hi is exact in FP32, so lo = fp16(x - hi) with one rounding, the
+// same bits as a conversion of the FP32 residual (the compiler would spend a
+// v_fma_mix_f32 per value and a v_cvt_pk_f16_f32 per pair on it).
 template <int N>
 __device__ __forceinline__ void split_f16_words(const float* x, uint32_t* hi, uint32_t* lo) {
-  f32x2 r[N / 2];
   const float m1 = opaque_minus_one();
 #pragma unroll
-  for (int i = 0; i < N / 2; ++i) {
-    const f32x2 v = {x[2 * i], x[2 * i + 1]};
-    const f16x2 h = __builtin_convertvector(v, f16x2);
-    hi[i] = __builtin_bit_cast(uint32_t, h);
-    r[i] = f32x2{__builtin_fmaf((float)h.x, m1, v.x), __builtin_fmaf((float)h.y, m1, v.y)};
-  }
+  for (int i = 0; i < N / 2; ++i)
+    hi[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x[2 * i], x[2 * i + 1]}, f16x2));
 #pragma unroll
-  for (int i = 0; i < N / 2; ++i) lo[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(r[i], f16x2));
+  for (int i = 0; i < N / 2; ++i) {
+    uint32_t l;
+    asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[1,0,0]"
+        : "=&v"(l)
+        : "v"(hi[i]), "s"(m1), "v"(x[2 * i]));
+    asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+        : "+v"(l)
+        : "v"(hi[i]), "s"(m1), "v"(x[2 * i + 1]));
+    lo[i] = l;
+  }
 }
 // Already scaled values -> fp16 hi and lo planes (bit patterns in bf16x8/x4).
 __device__ __forceinline__ void split_f16(f32x8 x, bf16x8& hi, bf16x8& lo) {
