@@ -27,10 +27,11 @@
 //
 // Softmax, two paths, each its own launch over the same grid (a work-group
 // of the other path exits at once), so each gets its own register budget:
-//   fast (rows with an unmasked key whose logits the magnitude record bounds
-//     below kFastBound): log2-domain logits with the scaled bias as the
-//     S^T accumulator's start value; an integer reference c per query, moved
-//     up to the tile's max when a lane's weights of a tile would pass 2^15;
+//   fast (rows with an unmasked key whose logits the magnitude record and
+//     the row's largest mask bias bound below kFastBound): log2-domain
+//     logits fma(acc, scale, bias log2(e)); an integer reference c per
+//     query, moved up to the tile's max when a lane's weights of a tile
+//     would pass 2^15;
 //     P' = exp2(x - (c + g_t)) with the tile's exponent shift g_t folded into
 //     the exact integer c + g_t;
 //   exact (fully masked rows, and rows whose logits are not bounded):
@@ -182,7 +183,8 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
   // when the prepare projection's magnitude record bounds the logits
   // (kernels.hpp), so they are left out; the result is bit-identical.
   // The fast softmax needs the same record to bound the logits below
-  // kFastBound (its integer reference then stays exact when shifted by a
+  // kFastBound, together with the row's largest mask bias when that is
+  // positive (its integer reference then stays exact when shifted by a
   // tile's plane exponent); other rows take the exact path.
   int nkt = nkt_all;
   bool fast = false;
@@ -192,8 +194,12 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
       const float mk = __builtin_bit_cast(float, a.magnitudes[1]);
       const float mv = __builtin_bit_cast(float, a.magnitudes[2]);
       const float mb = __builtin_bit_cast(float, a.magnitudes[3]);
+      const float mm = __builtin_bit_cast(
+          float, a.tile_flags[((int64_t)b * kTileFlagParts + kTileFlagMaxPart) * kTileFlagWords]);
       const float bound = 32.0f * mq * mk + mb;
-      fast = bound < kFastBound && mv < INFINITY;  // false for NaN
+      const float lift = mm > 0.0f ? mm : 0.0f;
+      // false for NaN anywhere (the comparison with mm rejects a NaN mask bias)
+      fast = bound + lift < kFastBound && (mm <= 0.0f || mm < kFastBound) && mv < INFINITY;
       if (bound < kSkipBound && mv < INFINITY) {  // false for NaN
         const uint32_t* far = a.tile_flags + (int64_t)b * kTileFlagParts * kTileFlagWords +
                               2 * kTileFlagWords;

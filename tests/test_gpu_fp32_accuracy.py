@@ -127,3 +127,32 @@ def test_value_weight_scales_at_fp32_accuracy(v_scale):
     rows = torch.arange(n)
     actual = _run_rows(z, mask, w, False, rows)
     _check_regions(f"w_v x{v_scale}", actual, z, mask, w, False, rows, 150)
+
+
+def test_positive_mask_bias_rows_take_the_exact_path():
+    """A mask entry of 2 gives inf * (mask - 1) = +1e9 on its key.  Such
+    logits are far beyond what the fast softmax's integer reference holds
+    exactly, so their rows must reproduce the native FP32 ties of
+    fl(fl(s + mask) + bias) (float32 spacing 64 near 1e9), as fully masked
+    rows do; the other rows keep the plain FP32 bar."""
+    n = 160
+    z = workloads.make_pair(n)
+    mask = workloads.make_mask(n, 150)
+    for i in range(0, 40):
+        mask[i, (7 * i + torch.tensor([0, 11, 22])) % 30] = 2.0  # keys 0-29 only
+    w = workloads.make_weights(bias_scale=4.0)
+    p32 = oracle_params(w)
+    p64 = p32.to(torch.float64)
+    rows = torch.arange(n)
+    for ending in (False, True):
+        print(f"case positive mask bias ending={ending}", flush=True)
+        actual = _run_rows(z, mask, w, ending, rows)
+        m_x = mask.t() if ending else mask
+        tied = (m_x > 1).any(1) | ~(m_x > 0).any(1)  # +1e9 keys, or every key masked
+        assert tied.any() and (~tied).any()
+        for region, sel in (("tied", tied), ("plain", ~tied)):
+            sub = rows[sel]
+            ref32 = oracle.block(z, mask, p32, ending=ending, outer_rows=sub)
+            ref64 = oracle.block(z.double(), mask.double(), p64, ending=ending, outer_rows=sub,
+                                 logits_f32=(region == "tied"))
+            strict_close(f"positive mask ending={ending} {region}", actual[sel], ref64, ref32)
