@@ -310,31 +310,22 @@ hipError_t launch_sigmoid_mul(const float* gate, const float* value, float* out,
   return hipGetLastError();
 }
 
-// The exact bf16 plane split every FP32-accurate kernel uses, run on count8
-// groups of 8 floats: planes[0..2] from split3 (f32x8), planes[3..4] from
-// split2 on the two f32x4 halves, each plane [count8 * 8] bf16.
+// The fp16 (hi, lo) split behind every FP32-accurate product (split_f16),
+// on count8 groups of 8 floats taken as given (the kernels scale each block
+// by a power of two first): plane 0 = hi, plane 1 = lo, each [count8 * 8]
+// fp16 bit patterns.
 __global__ __launch_bounds__(256) void split_planes_kernel(const f32x4* __restrict__ x,
                                                            uint32_t* __restrict__ planes,
                                                            int64_t count8) {
   const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (g >= count8) return;
   const f32x4 u = x[2 * g], v = x[2 * g + 1];
-  bf16x8 hi, lo, rest;
-  split3(f32x8{u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w}, hi, lo, rest);
-  bf16x4 h0, l0, h1, l1;
-  split2(u, h0, l0);
-  split2(v, h1, l1);
+  bf16x8 hi, lo;
+  split_f16(f32x8{u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w}, hi, lo);
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-  const int64_t words = count8 * 4;  // one plane, in 32-bit words
   u32x4* out = reinterpret_cast<u32x4*>(planes);
   out[g] = __builtin_bit_cast(u32x4, hi);
-  out[words / 4 + g] = __builtin_bit_cast(u32x4, lo);
-  out[2 * words / 4 + g] = __builtin_bit_cast(u32x4, rest);
-  const u32x2 a = __builtin_bit_cast(u32x2, h0), b = __builtin_bit_cast(u32x2, h1);
-  const u32x2 c = __builtin_bit_cast(u32x2, l0), d = __builtin_bit_cast(u32x2, l1);
-  out[3 * words / 4 + g] = u32x4{a.x, a.y, b.x, b.y};
-  out[4 * words / 4 + g] = u32x4{c.x, c.y, d.x, d.y};
+  out[count8 + g] = __builtin_bit_cast(u32x4, lo);
 }
 
 hipError_t launch_split_planes(const float* x, uint16_t* planes, int64_t count8,

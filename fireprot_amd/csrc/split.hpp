@@ -1,17 +1,18 @@
-// Exact splits of FP32 values into bfloat16 planes for the CDNA4 BF16
-// matrix cores, and the v_mfma_f32_32x32x16_bf16 step.
+// FP32 values as power-of-two scaled fp16 (hi, lo) planes for the CDNA4
+// 16-bit matrix cores, and the 32x32x16 / 16x16x32 MFMA steps on them.
 //
-// hi = bf16(x) (round to nearest), lo = bf16(x - hi), rest = bf16(x - hi -
-// lo).  Each difference is exact (Sterbenz), and x - hi - lo keeps at most 8
-// significant bits, so hi + lo + rest == x for normal x.  A product of two
-// three-plane operands summed over the six terms down to 2^-16 relative
-// (hi hi, hi lo, lo hi, lo lo, hi rest, rest hi) leaves an error of about
-// 3 * 2^-24 per product, FP32 rounding level; two-plane operands and three
-// terms (hi hi, hi lo, lo hi) leave a relative error below 2^-16.
+// A block of values is scaled by one power of two 2^e so that its max |x|
+// lies in [2^14, 2^15), then split: hi = fp16(x 2^e) (round to nearest even)
+// and lo = fp16(x 2^e - hi), where the difference is exact in FP32.  hi + lo
+// keeps about 22 significant bits; a product of two such operands over the
+// three terms hi hi, hi lo, lo hi leaves a relative error of about 2^-22 per
+// product, the level of an FP32 dot product.  Scaling by a power of two (and
+// back) is exact.
 //
-// Operand lane layout of v_mfma_f32_32x32x16_bf16 (one block): lane l holds
-// A[l % 32][8 * (l / 32) + e] and B[8 * (l / 32) + e][l % 32], e = 0..7, of
-// one 16-deep k step; the FP32 result has the 32x32x2 f32 layout (common.hpp).
+// Operand lane layout of v_mfma_f32_32x32x16_{f16,bf16} (one block): lane l
+// holds A[l % 32][8 * (l / 32) + e] and B[8 * (l / 32) + e][l % 32],
+// e = 0..7, of one 16-deep k step; the FP32 result has the 32x32x2 f32 layout
+// (common.hpp).
 #pragma once
 
 #include "common.hpp"
@@ -22,6 +23,7 @@ namespace fpx {
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -33,115 +35,6 @@ __device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
 // host product of small integers).
 __device__ __forceinline__ f32x4 mfma16_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-
-// The pair steps of the splits below: the pair's bf16 roundings packed in
-// one word (v_cvt_pk_bf16_f32, round to nearest even), and the residuals
-// x - float(hi), with float(hi) recovered from that word by a shift and a
-// mask (the generic conversion takes a third more instructions).  Each
-// residual is exact (Sterbenz).  The shift, the mask and the subtraction run
-// at the double FP32/integer VALU rate once two waves share a SIMD, so they
-// cost as much as one v_dot2c_f32_bf16 against (-1, 0) would (measured).
-__device__ __forceinline__ uint32_t round_pair(f32x2 x) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, bf16x2));
-}
-__device__ __forceinline__ f32x2 residual_pair(uint32_t hb, f32x2 x) {
-  const f32x2 back = {__builtin_bit_cast(float, hb << 16), __builtin_bit_cast(float, hb & 0xffff0000u)};
-  return x - back;
-}
-__device__ __forceinline__ uint32_t split_pair(f32x2 x, f32x2& residual) {
-  const uint32_t hb = round_pair(x);
-  residual = residual_pair(hb, x);
-  return hb;
-}
-
-// N values (N even) -> hi, lo (and rest) planes, packed two per word.  Each
-// phase runs over all pairs before the next reads its results.
-template <int N>
-__device__ __forceinline__ void split2_words(const float* x, uint32_t* hi, uint32_t* lo) {
-  f32x2 r[N / 2];
-#pragma unroll
-  for (int i = 0; i < N / 2; ++i) hi[i] = round_pair(f32x2{x[2 * i], x[2 * i + 1]});
-#pragma unroll
-  for (int i = 0; i < N / 2; ++i) r[i] = residual_pair(hi[i], f32x2{x[2 * i], x[2 * i + 1]});
-#pragma unroll
-  for (int i = 0; i < N / 2; ++i) lo[i] = round_pair(r[i]);
-}
-template <int N>
-__device__ __forceinline__ void split3_words(const float* x, uint32_t* hi, uint32_t* lo,
-                                             uint32_t* rest) {
-  f32x2 r1[N / 2], r2[N / 2];
-#pragma unroll
-  for (int i = 0; i < N / 2; ++i) hi[i] = round_pair(f32x2{x[2 * i], x[2 * i + 1]});
-#pragma unroll
-  for (int i = 0; i < N / 2; ++i) r1[i] = residual_pair(hi[i], f32x2{x[2 * i], x[2 * i + 1]});
-#pragma unroll
-  for (int i = 0; i < N / 2; ++i) lo[i] = round_pair(r1[i]);
-#pragma unroll
-  for (int i = 0; i < N / 2; ++i) r2[i] = residual_pair(lo[i], r1[i]);
-#pragma unroll
-  for (int i = 0; i < N / 2; ++i) rest[i] = round_pair(r2[i]);
-}
-
-__device__ __forceinline__ void split3(f32x4 x, bf16x4& hi, bf16x4& lo, bf16x4& rest) {
-  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-  const float v[4] = {x.x, x.y, x.z, x.w};
-  uint32_t h[2], l[2], r[2];
-  split3_words<4>(v, h, l, r);
-  hi = __builtin_bit_cast(bf16x4, u32x2{h[0], h[1]});
-  lo = __builtin_bit_cast(bf16x4, u32x2{l[0], l[1]});
-  rest = __builtin_bit_cast(bf16x4, u32x2{r[0], r[1]});
-}
-__device__ __forceinline__ void split3(f32x8 x, bf16x8& hi, bf16x8& lo, bf16x8& rest) {
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  const float v[8] = {x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]};
-  uint32_t h[4], l[4], r[4];
-  split3_words<8>(v, h, l, r);
-  hi = __builtin_bit_cast(bf16x8, u32x4{h[0], h[1], h[2], h[3]});
-  lo = __builtin_bit_cast(bf16x8, u32x4{l[0], l[1], l[2], l[3]});
-  rest = __builtin_bit_cast(bf16x8, u32x4{r[0], r[1], r[2], r[3]});
-}
-__device__ __forceinline__ void split2(f32x4 x, bf16x4& hi, bf16x4& lo) {
-  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-  const float v[4] = {x.x, x.y, x.z, x.w};
-  uint32_t h[2], l[2];
-  split2_words<4>(v, h, l);
-  hi = __builtin_bit_cast(bf16x4, u32x2{h[0], h[1]});
-  lo = __builtin_bit_cast(bf16x4, u32x2{l[0], l[1]});
-}
-__device__ __forceinline__ void split2(f32x8 x, bf16x8& hi, bf16x8& lo) {
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  const float v[8] = {x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]};
-  uint32_t h[4], l[4];
-  split2_words<8>(v, h, l);
-  hi = __builtin_bit_cast(bf16x8, u32x4{h[0], h[1], h[2], h[3]});
-  lo = __builtin_bit_cast(bf16x8, u32x4{l[0], l[1], l[2], l[3]});
-}
-
-// (hi, lo) pair words of the plane layout: word = hi | lo << 16.  From the
-// packed pairs hi2 = (hi0, hi1) and lo2 = (lo0, lo1) to the words (w0, w1),
-// and back (v_perm_b32: selector byte k picks byte k of {src0, src1} with
-// src1 in bytes 0-3).
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ u32x2 interleave_pairs(uint32_t hi2, uint32_t lo2) {
-  return u32x2{__builtin_amdgcn_perm(lo2, hi2, 0x05040100u),
-               __builtin_amdgcn_perm(lo2, hi2, 0x07060302u)};
-}
-// Returns (hi2, lo2).
-__device__ __forceinline__ u32x2 deinterleave_pairs(uint32_t w0, uint32_t w1) {
-  return u32x2{__builtin_amdgcn_perm(w1, w0, 0x05040100u),
-               __builtin_amdgcn_perm(w1, w0, 0x07060302u)};
-}
-
-// fp16 (hi, lo) pair word of x (|x| below 2^15 for full precision): hi =
-// fp16(x) (round to nearest), lo = fp16(x - hi); x - hi is exact.
-__device__ __forceinline__ uint32_t f16_pair_word(float x) {
-  const _Float16 hi = (_Float16)x;
-  const _Float16 lo = (_Float16)(x - (float)hi);
-  return (uint32_t)__builtin_bit_cast(uint16_t, hi) |
-         ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
 }
 
 // v_mfma_f32_32x32x16_f16 on fp16 bit patterns held in bf16x8 vectors (the

@@ -308,13 +308,15 @@ int fpx_qkv_projection(const float* x, int64_t rows, const float* wq, const floa
 int fpx_sigmoid_mul_out(const float* gate, const float* value, float* out, int64_t count,
                         void* stream);
 
-/* The exact bfloat16 plane split behind every FP32-accurate kernel of this
- * library, exposed so its exactness can be checked: count floats (count % 8
- * == 0) into five [count] bf16 planes: hi, lo, rest of the three-plane split
- * (hi = bf16(x), lo = bf16(x - hi), rest = bf16(x - hi - lo), round to nearest
- * even; hi + lo + rest == x for normal x), then hi, lo of the two-plane
- * split.  No counterpart in the reference (its kernels compute in FP32 or
- * round once); used by this library's own parity tests. */
+/* The fp16 (hi, lo) split behind every FP32-accurate product of this
+ * library, exposed so its bits can be checked on a new driver or compiler:
+ * count floats (count % 8 == 0), taken as given, into two [count] planes of
+ * fp16 bit patterns, hi = fp16(x) and lo = fp16(x - hi) (round to nearest
+ * even; x - hi is exact, so hi + lo holds 22 significant bits of x for
+ * |x| in [2^-3, 65504]).  The kernels first scale each block of values by a
+ * power of two so its max lies in [2^14, 2^15).  No counterpart in the
+ * reference (its kernels compute in FP32 or round once); used by this
+ * library's own parity tests. */
 int fpx_split_planes(const float* x, int64_t count, uint16_t* planes, void* stream);
 
 #ifdef __cplusplus
