@@ -1,5 +1,5 @@
 // Helpers shared by the FP32-accurate attention kernels (attention.hip on the
-// FP32 matrix cores, attention_split.hip on the BF16 matrix cores): buffer
+// FP32 matrix cores, attention_split.hip on the 16-bit matrix cores, bf16.hip): buffer
 // loads, the lane-pair exchanges of the transposed S^T / O^T layout, row
 // reductions, and the softmax reference constants.
 #pragma once
@@ -14,6 +14,7 @@ constexpr int kRowGroup = 8;  // outer rows that share a bias slice in L2
 // Exact path: rescale when a tile max exceeds the reference by 8 binary
 // orders (in logit units).
 constexpr float kRescaleNat = 8.0f * 0.69314718055994531f;
+constexpr float kRescaleLog2 = 8.0f;  // the same in log2 units
 // Fast path (log2 units): the reference snaps to 0 while the row max lies in
 // [-kSnap, kSnap]; the running sum may grow to kSumLimit before a rescale; a
 // rescale forced by the sum moves the reference up by at least kLift.

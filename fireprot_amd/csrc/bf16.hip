@@ -156,7 +156,7 @@ __global__ __launch_bounds__(Bf16ProjTraits<MODE>::kWaves * 64) void projection_
           for (int h = 0; h < kHeads; ++h) p[h] = wave_sum(r0 * wb[h][0] + r1 * wb[h][1]);
           if (lane < kHeads) {
             const float v = lane == 0 ? p[0] : lane == 1 ? p[1] : lane == 2 ? p[2] : p[3];
-            a.tri_bias[bias_frag_index_bf16(lane, i, j, a.np)] = (__bf16)(valid ? v : 0.f);
+            a.tri_bias[bias_frag_index_bf16(lane, i, j, a.np)] = (__bf16)(valid ? v * kLog2e : 0.f);
           }
         }
       }
@@ -282,17 +282,21 @@ hipError_t launch_proj_mode(const Bf16ProjArgs& a, hipStream_t stream, int wgs_p
 //     (bias_frag_index_bf16), loaded two tiles ahead with two 1 KB reads and
 //     widened to FP32 with one shift or mask per value (an FP32 copy doubles
 //     the bytes per tile, and the kernel then waits on its loads).
-//   - Rows with an unmasked key: p = exp2(fma(x, log2 e, -c)) with the FP32
-//     kernels' snapped reference c (0 while the row max lies within
-//     kSnap of it; rescaled only when a running sum passes kSumLimit), so a
-//     tile needs no max, no cross-lane exchange and no branch.  The mask
-//     bias is added on masked tiles only.  P is packed to bf16 with
+//   - q and the bias copy are stored scaled by log2(e), so the logits leave
+//     the matrix cores in log2 units.
+//   - Rows with an unmasked key: p = exp2(x - c) with the FP32 kernels'
+//     snapped reference c (0 while the row max lies within kSnap of it;
+//     rescaled only when a running sum passes kSumLimit), so a tile needs no
+//     max, no cross-lane exchange and no branch, and while every reference
+//     of the wave is 0 no subtraction either: p = exp2(x).  The mask bias is
+//     added (times log2(e)) on masked tiles only.  P is packed to bf16 with
 //     v_cvt_pk_bf16_f32; the row sum l adds the FP32 weights (their bf16
 //     roundings are unbiased, so O / l stays a weighted mean well within the
 //     bf16 bar).
 //   - Rows whose keys are all masked form fl(fl(s + mask_bias) + bias) in
-//     FP32 in that order, with a lazy running max (rescale when a tile max
-//     exceeds it by 2^8) and one rounded c per query.
+//     FP32 in that order (log2 units), with a lazy running max (rescale when
+//     a tile max exceeds it by 2^8) and the max itself as the reference, so
+//     equal quantised logits get equal weights.
 
 constexpr int kThreads = 256;
 constexpr int kMaxKeysB = kTileFlagWords * 32 * kBk;
@@ -442,18 +446,19 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
       x = mfma_bf16(k0, qf[0], x);
       return mfma_bf16(k1, qf[1], x);
     };
-    // The rest of the logits of tile t (natural units): the mask bias on
-    // masked tiles (fast), or fl(fl(s + mask) + bias) (exact).
+    // The rest of the logits of tile t (log2 units: q and the bias copy
+    // carry log2(e)): the mask bias on masked tiles (fast), or
+    // fl(fl(s + mask) + bias) (exact).
     auto finish = [&](f32x16& x, int t) {
       if (kExact) {
         const f32x16 mb = mask_vals(t);
         const f32x16 bias = widen(load_frag(t));
 #pragma unroll
-        for (int r = 0; r < 16; ++r) x[r] = (x[r] + mb[r]) + bias[r];
+        for (int r = 0; r < 16; ++r) x[r] = __builtin_fmaf(mb[r], kLog2e, x[r]) + bias[r];
       } else if (masked(t)) {
         const f32x16 mb = mask_vals(t);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) x[r] += mb[r];
+        for (int r = 0; r < 16; ++r) x[r] = __builtin_fmaf(mb[r], kLog2e, x[r]);
       }
     };
 
@@ -462,6 +467,7 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
     float m_thr = -INFINITY;
     float c_ref = 0.f;
     bool has_ref = false;
+    bool zero_ref = true;  // every query of the wave has c_ref == 0 (uniform)
 
     auto softmax = [&](const f32x16& x, bf16x8& p0, bf16x8& p1) {
       f32x16 p;
@@ -469,17 +475,17 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
         const float mt = xor32_max(max16(x));
         if (__any(mt > m_thr)) {
           const float m_new = __builtin_elementwise_maximum(m_ref, mt);
-          const float c_new = m_new == -INFINITY ? 0.f : m_new * kLog2e;
+          const float c_new = m_new == -INFINITY ? 0.f : m_new;
           const float alpha = m_ref == -INFINITY ? 0.f : exp2_fast(c_ref - c_new);
 #pragma unroll
           for (int r = 0; r < 16; ++r) o[r] *= alpha;
           l_run *= alpha;
           m_ref = m_new;
           c_ref = c_new;
-          m_thr = m_new + kRescaleNat;
+          m_thr = m_new + kRescaleLog2;
         }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) p[r] = exp2_fast(__builtin_fmaf(x[r], kLog2e, -c_ref));
+        for (int r = 0; r < 16; ++r) p[r] = exp2_fast(x[r] - c_ref);
         l_run += sum16(p);
         p0 = pack8(p, 0);
         p1 = pack8(p, 1);
@@ -487,8 +493,13 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
       }
       float ovf = 0.f;
       if (has_ref) {
+        if (zero_ref) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) p[r] = exp2_fast(__builtin_fmaf(x[r], kLog2e, -c_ref));
+          for (int r = 0; r < 16; ++r) p[r] = exp2_fast(x[r]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) p[r] = exp2_fast(x[r] - c_ref);
+        }
         const float l_new = l_run + sum16(p);
         const bool over = !(l_new <= kSumLimit);  // NaN or inf count as overflow
         if (!__any(over)) {
@@ -500,7 +511,7 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
         ovf = over ? 1.f : 0.f;
       }
       // Rare path, taken by the whole wavefront (attention.hip), in log2 units.
-      const float mt = xor32_max(max16(x)) * kLog2e;
+      const float mt = xor32_max(max16(x));
       const bool fresh = m_ref == -INFINITY;
       const bool need = fresh || xor32_max(ovf) > 0.f || mt > c_ref + kSnap;
       m_ref = __builtin_elementwise_maximum(m_ref, mt);
@@ -514,8 +525,9 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
       for (int r = 0; r < 16; ++r) o[r] *= alpha;
       l_run *= alpha;
       c_ref = c_new;
+      zero_ref = __all(c_ref == 0.f);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) p[r] = exp2_fast(__builtin_fmaf(x[r], kLog2e, -c_ref));
+      for (int r = 0; r < 16; ++r) p[r] = exp2_fast(x[r] - c_ref);
       l_run += sum16(p);
       has_ref = __all(m_ref != -INFINITY);
       p0 = pack8(p, 0);

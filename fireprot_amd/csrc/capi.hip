@@ -343,7 +343,9 @@ int fpx_tri_attn_prepare(int dtype, const void* z, int64_t z_stride0, int64_t z_
     for (int g = 0; g < 4; ++g) p.w[g] = wq + g * wstride;
     p.bias_vec = static_cast<const __bf16*>(b_g);
     p.w_bias = static_cast<const __bf16*>(w_bias);
-    p.q_scale = q_scale;
+    // BF16 attention logits come out of the matrix cores in log2 units: q
+    // and the triangle bias are stored scaled by log2(e).
+    p.q_scale = q_scale * fpx::kLog2e;
     p.qh = as<__bf16>(w.qh);
     p.kh = as<__bf16>(w.kh);
     p.vt = as<__bf16>(w.vt);

@@ -239,12 +239,12 @@ struct Bf16ProjArgs {
   const __bf16* w[4];
   const __bf16* bias_vec;   // gate bias (prepare) or output bias (finish), nullable
   const __bf16* w_bias;
-  float q_scale;
+  float q_scale;      // log2(e) / sqrt(32): the attention's logits are in log2 units
   __bf16* qh;
   __bf16* kh;
   __bf16* vt;
   __bf16* gs;
-  __bf16* tri_bias;  // fragment order (bias_frag_index_bf16)
+  __bf16* tri_bias;  // fragment order (bias_frag_index_bf16), scaled by log2(e)
   int np;
   __bf16* out;
   int64_t os_i;
@@ -258,7 +258,7 @@ struct Bf16AttnArgs {
   const __bf16* v;
   const float* mbias;
   const uint32_t* tile_flags;
-  const __bf16* bias;  // fragment order (bias_frag_index_bf16)
+  const __bf16* bias;  // fragment order (bias_frag_index_bf16), scaled by log2(e)
   const __bf16* gate;
   __bf16* out;
   int batch;
