@@ -213,7 +213,30 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
   }
   // Each row runs in the launch of its softmax path (uniform per work-group).
   if (fast == EXACT) return;
+  // Exact rows whose mask bias is one finite nonzero value m on every key
+  // < n (padding rows: inf (mask - 1) = -1e9) and whose products are bounded
+  // below half a unit in the last place of m: then fl(s + m) = m for every
+  // key (|s| <= 32 max|q| max|k|, with a margin for the native rounding of
+  // s), so the native logit fl(fl(s + m) + bias) is fl(m + bias) and S^T
+  // need not be formed (no K tiles, no S^T MFMAs).
+  bool constant_mask = false;
+  float m_row = 0.f;
+  if (EXACT && a.magnitudes != nullptr && a.magnitudes[4] == 1u) {
+    const uint32_t* f3 = a.tile_flags + ((int64_t)b * kTileFlagParts + kTileFlagMaxPart) * kTileFlagWords;
+    const float hi = __builtin_bit_cast(float, f3[0]);
+    const float lo = __builtin_bit_cast(float, f3[1]);
+    const float mq = __builtin_bit_cast(float, a.magnitudes[0]);
+    const float mk = __builtin_bit_cast(float, a.magnitudes[1]);
+    // false for NaN anywhere, for infinite m and for m = 0
+    if (hi == lo && __builtin_fabsf(hi) < INFINITY && hi != 0.f) {
+      const float s_bound = 32.0f * mq * mk * (1.0f + 0x1p-10f);
+      const float half_ulp = __builtin_ldexpf(1.0f, __builtin_amdgcn_frexp_expf(hi) - 25);
+      constant_mask = s_bound < half_ulp;
+      m_row = hi;
+    }
+  }
   const int last = nkt - 1;
+  const int full_tiles = a.n / kBk;  // key tiles wholly below n
   auto masked = [&](int t) -> bool {
     const uint32_t word = t < 32 ? mw[0] : t < 64 ? mw[1] : t < 96 ? mw[2] : mw[3];
     return (word >> (t & 31)) & 1u;
@@ -251,15 +274,23 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
   float l_run = 0.f;
   int e_min = 0;  // smallest v^T plane exponent over the visited tiles
 
-  auto run = [&](auto exact_tag) {
+  auto run = [&](auto exact_tag, auto constant_tag) {
     constexpr bool kExact = decltype(exact_tag)::value;
+    // exact rows with a constant mask bias: logits fl(m_row + bias), V only
+    constexpr bool kConst = decltype(constant_tag)::value;
+    static_assert(kExact || !kConst, "the constant-mask shortcut serves exact rows");
     const f32x16 zero16 = {};
+    // Tile copies into the ring; the constant-mask shortcut needs no K tiles
+    // (waves 0 and 1 copy K hi and K lo).
+    auto copy = [&](int t, int st) {
+      if (!kConst || w >= 2) dma(t, st);
+    };
 
     // Q planes, the B operand of S^T: lane holds Q[jq][16m + 8half + e], the
     // fp16 hi and lo planes (the log2(e) of the fast path enters with the
     // product scale).
     bf16x8 qh[2], ql[2];
-    {
+    if (!kConst) {
       const uint8_t* src = reinterpret_cast<const uint8_t*>(a.q) + bh * slice_bytes + (int64_t)jq * 64;
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
@@ -272,6 +303,7 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
     // smallest terms first.
     auto scores = [&](int buf) -> f32x16 {
       f32x16 x = zero16;
+      if (kConst) return x;
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
         const bf16x8 kh = plane_rd(buf, 0, m);
@@ -287,6 +319,18 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
     // units plus the mask bias on masked tiles (fast), or fl(fl(s + mask) +
     // bias) in natural units (exact).
     auto finish = [&](f32x16& x, const f32x16& acc, int t) {
+      if (kConst) {
+        if (t < full_tiles) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) x[r] = m_row + x[r];
+        } else {
+          // the tile holding key n - 1: -inf mask bias on the keys >= n
+          const f32x16 mb = mask_vals(t);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) x[r] = mb[r] + x[r];
+        }
+        return;
+      }
       const float st = sq * Sk[t];
       if (kExact) {
         if (masked(t)) {
@@ -439,9 +483,9 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
     auto stage = [](int t) { return t & (kStages - 1); };
     f32x16 x_a = init(0);
     f32x16 x_b = init(clamp(1));
-    dma(0, 0);
-    dma(clamp(1), 1);
-    dma(clamp(2), 2);
+    copy(0, 0);
+    copy(clamp(1), 1);
+    copy(clamp(2), 2);
     wait_vmcnt<2>();
     __syncthreads();
     e_min = __builtin_amdgcn_readfirstlane(
@@ -455,7 +499,7 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
       cur = init(clamp(t + 2));
       pv(stage(t), ph, pl);
       finish(nxt, acc, t + 1);
-      dma(clamp(t + 3), stage(t + 3));
+      copy(clamp(t + 3), stage(t + 3));
       // Tile t+2 has landed once at most this iteration's two tile loads
       // and four bias-fragment loads are outstanding: vector memory loads
       // retire in issue order.
@@ -479,7 +523,14 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
     }
     wait_vmcnt<0>();  // the clamped tail loads land before the LDS is released
   };
-  run(std::integral_constant<bool, EXACT>{});
+  if constexpr (EXACT) {
+    if (constant_mask)
+      run(std::true_type{}, std::true_type{});
+    else
+      run(std::true_type{}, std::false_type{});
+  } else {
+    run(std::false_type{}, std::false_type{});
+  }
 
   const float l_tot = xor32_sum(l_run);
   if (jq < a.n) {

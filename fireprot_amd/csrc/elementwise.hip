@@ -16,7 +16,8 @@ namespace {
 // mask bias (-0 counts as zero, since s + -0 == s); part 1 does the same for
 // "every key of the tile has a nonzero mask bias", part 2 for "every key of
 // the tile has a mask bias <= -kSkipMask".  Padded keys (k >= n, -inf) count
-// as masked in all three.  kFromMask: the source is a {0, 1} mask and
+// as masked in all three.  Part 3 holds the row's largest mask bias (word 0)
+// and its smallest over the keys < n (word 1), as float bits, NaN-propagating.  kFromMask: the source is a {0, 1} mask and
 // inf * (mask - 1) is evaluated as two rounded fp32 ops, as the native
 // expression is (patches/protenix/0005-*.patch:36-39); otherwise the source
 // already holds mask-bias values and is copied.  np is a multiple of 64.
@@ -35,12 +36,14 @@ __global__ __launch_bounds__(256) void mask_rows_kernel(const float* __restrict_
   if (i >= rows) return;
   uint32_t part[kTileFlagParts][kTileFlagWords] = {};
   float vmax = -INFINITY;  // NaN-propagating max of the row's mask biases
+  float vneg = -INFINITY;  // NaN-propagating max of -bias over the keys < n
   for (int k0 = 0; k0 < np; k0 += 64) {
     const int k = k0 + lane;
     float v = -INFINITY;
     if (k < n) {
       const float m = mask ? mask[i * ms_i + k * ms_j] : 0.0f;
       v = !mask ? 0.0f : kFromMask ? inf * (m - 1.0f) : m;
+      vneg = __builtin_elementwise_maximum(vneg, -v);
     }
     vmax = __builtin_elementwise_maximum(vmax, v);
     mbias[(int64_t)i * np + k] = v;
@@ -60,6 +63,7 @@ __global__ __launch_bounds__(256) void mask_rows_kernel(const float* __restrict_
     }
   }
   part[kTileFlagMaxPart][0] = __builtin_bit_cast(uint32_t, wave_max(vmax));
+  part[kTileFlagMaxPart][1] = __builtin_bit_cast(uint32_t, -wave_max(vneg));
   uint32_t* dst = flags + (int64_t)i * kTileFlagParts * kTileFlagWords;
 #pragma unroll
   for (int pt = 0; pt < kTileFlagParts; ++pt)

@@ -20,8 +20,9 @@ namespace fpx {
 //                        part 0 = some key of 32-key tile t has a nonzero
 //                        mask bias; of part 1 = every key of tile t has one;
 //                        of part 2 = every key of tile t has a mask bias at
-//                        or below -kSkipMask; word 0 of part 3 = the row's
-//                        largest mask bias as float bits (NaN-propagating)
+//                        or below -kSkipMask; words 0 and 1 of part 3 =
+//                        the row's largest mask bias and its smallest over
+//                        the keys < n, as float bits (NaN-propagating)
 //                magnitudes: nullable, kMagnitudeWords written by the
 //                        prepare projection (see ProjArgs::magnitudes)
 //                bias : [H][np][np] in fragment order (bias_frag_index)

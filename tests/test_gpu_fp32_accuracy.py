@@ -156,3 +156,25 @@ def test_positive_mask_bias_rows_take_the_exact_path():
             ref64 = oracle.block(z.double(), mask.double(), p64, ending=ending, outer_rows=sub,
                                  logits_f32=(region == "tied"))
             strict_close(f"positive mask ending={ending} {region}", actual[sel], ref64, ref32)
+
+
+@pytest.mark.parametrize("qk_scale", [1.0, 8.0])
+def test_padding_rows_with_and_without_the_constant_mask_shortcut(qk_scale):
+    """Padding rows carry one mask bias (-1e9) on every key.  While
+    32 max|q| max|k| stays below half its float32 spacing (32), fl(s + m) = m
+    and the attention skips S^T for them (qk_scale 1); scaling W_q and W_k by
+    8 lifts |s| past that bound, so the same rows take the full exact path
+    with logits spread over several float32 buckets of -1e9.  Both must meet
+    the FP32 bar against float64 with float32-rounded logits."""
+    n, valid = 160, 130
+    z = workloads.make_pair(n)
+    mask = workloads.make_mask(n, valid)
+    w = workloads.make_weights(bias_scale=4.0)
+    w["w_q"] = w["w_q"] * qk_scale
+    w["w_k"] = w["w_k"] * qk_scale
+    rows = torch.arange(n)
+    for ending in (False, True):
+        print(f"case padding rows qk x{qk_scale} ending={ending}", flush=True)
+        actual = _run_rows(z, mask, w, ending, rows)
+        _check_regions(f"padding qk x{qk_scale} ending={ending}", actual, z, mask, w, ending, rows,
+                       valid)

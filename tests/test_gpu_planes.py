@@ -122,3 +122,63 @@ def test_prepare_planes_decode_to_the_projections(ending, scale):
     print(f"v ending={ending} scale={scale}: max|err|={err:.3e} bound={bound:.3e}", flush=True)
     assert err <= bound
     assert np.all(vt[..., n:] == 0), "padded keys must be zero"
+
+
+def test_mask_rows_flags_and_row_extremes():
+    """The mask stage's bias rows and per-row tile flags, against numpy:
+    part 0 / 1 / 2 bit t = some key / every key / every key at or below
+    -2^29 of 32-key tile t has a nonzero mask bias, keys past n counting as
+    -inf; part 3 = the row's largest mask bias and its smallest over the keys
+    < n (NaN-propagating).  The attention classifies rows from these words."""
+    n = 100
+    np_ = 128
+    gen = torch.Generator().manual_seed(5)
+    mask = (torch.rand(n, n, generator=gen) > 0.3).float()
+    mask[5] = 0.0                 # fully masked: -1e9 on every key
+    mask[6, :40] = 2.0            # +1e9 on some keys
+    mask[7, 33] = float("nan")
+    mask[8] = 1.0                 # no mask bias at all
+    z = workloads.make_pair(n)
+    weights = hip_block.BlockWeights.from_tensors(**workloads.make_weights()).to("cuda")
+    lib = _native.library()
+    ws_bytes = hip_block.workspace_bytes(n, torch.float32)
+    ws = torch.full((ws_bytes,), 0xFF, dtype=torch.uint8, device="cuda")
+    zc, mc = z.cuda(), mask.cuda()
+    code = lib.fpx_tri_attn_prepare(
+        0, zc.data_ptr(), zc.stride(0), zc.stride(1), mc.data_ptr(), mc.stride(0), mc.stride(1),
+        weights.ln_w.data_ptr() if weights.ln_w is not None else None,
+        weights.ln_b.data_ptr() if weights.ln_b is not None else None, weights.eps,
+        weights.w_qkvg.data_ptr(), None, weights.w_bias.data_ptr(), weights.inf, n, 0,
+        ws.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream)
+    _native.check(code, "fpx_tri_attn_prepare")
+    torch.cuda.synchronize()
+    o = _offsets(n)
+    raw = ws.cpu().numpy()
+    mbias = raw[o["mbias"]:o["mbias"] + n * np_ * 4].view(np.float32).reshape(n, np_)
+    flags = raw[o["flags"]:o["flags"] + n * 16 * 4].view(np.uint32).reshape(n, 4, 4)
+
+    m = mask.numpy().astype(np.float32)
+    with np.errstate(invalid="ignore"):
+        want = np.float32(weights.inf) * (m - np.float32(1.0))
+    full = np.full((n, np_), -np.inf, dtype=np.float32)
+    full[:, :n] = want
+    nan = np.isnan(full)
+    np.testing.assert_array_equal(np.isnan(mbias), nan)
+    np.testing.assert_array_equal(mbias[~nan], full[~nan])
+    tiles = full.reshape(n, np_ // 32, 32)
+    with np.errstate(invalid="ignore"):
+        parts = [(tiles != 0).any(2), (tiles != 0).all(2), (tiles <= -2.0 ** 29).all(2)]
+    for p, bits in enumerate(parts):
+        words = np.zeros((n, 4), dtype=np.uint64)
+        for t in range(np_ // 32):
+            words[:, t // 32] |= bits[:, t].astype(np.uint64) << np.uint64(t % 32)
+        np.testing.assert_array_equal(flags[:, p, :].astype(np.uint64), words, err_msg=f"part {p}")
+    hi = flags[:, 3, 0].view(np.float32)
+    lo = flags[:, 3, 1].view(np.float32)
+    want_hi = full.max(1)
+    want_lo = full[:, :n].min(1)
+    for got, exp, name in ((hi, want_hi, "max"), (lo, want_lo, "min")):
+        np.testing.assert_array_equal(np.isnan(got), np.isnan(exp), err_msg=name)
+        keep = ~np.isnan(exp)
+        np.testing.assert_array_equal(got[keep], exp[keep], err_msg=name)
+    assert hi[5] == lo[5] == np.float32(-1e9) and hi[8] == lo[8] == 0.0 and np.isnan(hi[7])
