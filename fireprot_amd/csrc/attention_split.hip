@@ -79,6 +79,42 @@ __device__ __forceinline__ int v_position(int g) {
   return (g >> 2) * 16 + perm * 4;
 }
 
+// Rows whose mask bias is one finite nonzero value m on every key < n
+// (padding rows: inf (mask - 1) = -1e9), when the products are bounded below
+// half a unit in the last place of m: then fl(s + m) = m for every key
+// (|s| <= 32 max|q| max|k|, with a margin for the native rounding of s), so
+// the native logit fl(fl(s + m) + bias) is fl(m + bias), the same for every
+// such row.
+__device__ __forceinline__ bool constant_mask_row(const AttnArgs& a, int b, float& m) {
+  if (a.magnitudes == nullptr || a.magnitudes[4] != 1u) return false;
+  const uint32_t* f3 =
+      a.tile_flags + ((int64_t)b * kTileFlagParts + kTileFlagMaxPart) * kTileFlagWords;
+  const float hi = __builtin_bit_cast(float, f3[0]);
+  const float lo = __builtin_bit_cast(float, f3[1]);
+  // false for NaN anywhere, for an infinite m and for m = 0
+  if (!(hi == lo && __builtin_fabsf(hi) < INFINITY && hi != 0.f)) return false;
+  const float mq = __builtin_bit_cast(float, a.magnitudes[0]);
+  const float mk = __builtin_bit_cast(float, a.magnitudes[1]);
+  const float s_bound = 32.0f * mq * mk * (1.0f + 0x1p-10f);
+  const float half_ulp = __builtin_ldexpf(1.0f, __builtin_amdgcn_frexp_expf(hi) - 25);
+  m = hi;
+  return s_bound < half_ulp;
+}
+
+// The constant-row kernel serves chunks of kConstRows consecutive outer
+// rows: the rows of a chunk that satisfy constant_mask_row with the m of
+// the chunk's first such row.  The exact launch leaves exactly those out.
+constexpr int kConstRows = 4;
+__device__ __forceinline__ bool const_chunk_member(const AttnArgs& a, int b) {
+  float m;
+  if (!constant_mask_row(a, b, m)) return false;
+  for (int r = b - b % kConstRows; r < b; ++r) {
+    float mr;
+    if (constant_mask_row(a, r, mr)) return mr == m;
+  }
+  return true;  // the chunk's first constant-mask row
+}
+
 // Both layouts read q, k and v^T in the plane layout (ProjArgs::planes) with
 // their per-tile scales, and the staged bias copies, mask rows and tile
 // flags.  LAYOUT kAttnBlock: the block's workspace, gated head-last output;
@@ -213,28 +249,11 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
   }
   // Each row runs in the launch of its softmax path (uniform per work-group).
   if (fast == EXACT) return;
-  // Exact rows whose mask bias is one finite nonzero value m on every key
-  // < n (padding rows: inf (mask - 1) = -1e9) and whose products are bounded
-  // below half a unit in the last place of m: then fl(s + m) = m for every
-  // key (|s| <= 32 max|q| max|k|, with a margin for the native rounding of
-  // s), so the native logit fl(fl(s + m) + bias) is fl(m + bias) and S^T
-  // need not be formed (no K tiles, no S^T MFMAs).
-  bool constant_mask = false;
+  // Exact rows that the constant-row kernel serves are left out; other
+  // constant-mask rows (another m than their chunk's) still skip S^T here.
+  if (EXACT && const_chunk_member(a, b)) return;
   float m_row = 0.f;
-  if (EXACT && a.magnitudes != nullptr && a.magnitudes[4] == 1u) {
-    const uint32_t* f3 = a.tile_flags + ((int64_t)b * kTileFlagParts + kTileFlagMaxPart) * kTileFlagWords;
-    const float hi = __builtin_bit_cast(float, f3[0]);
-    const float lo = __builtin_bit_cast(float, f3[1]);
-    const float mq = __builtin_bit_cast(float, a.magnitudes[0]);
-    const float mk = __builtin_bit_cast(float, a.magnitudes[1]);
-    // false for NaN anywhere, for infinite m and for m = 0
-    if (hi == lo && __builtin_fabsf(hi) < INFINITY && hi != 0.f) {
-      const float s_bound = 32.0f * mq * mk * (1.0f + 0x1p-10f);
-      const float half_ulp = __builtin_ldexpf(1.0f, __builtin_amdgcn_frexp_expf(hi) - 25);
-      constant_mask = s_bound < half_ulp;
-      m_row = hi;
-    }
-  }
+  const bool constant_mask = EXACT && constant_mask_row(a, b, m_row);
   const int last = nkt - 1;
   const int full_tiles = a.n / kBk;  // key tiles wholly below n
   auto masked = [&](int t) -> bool {
@@ -554,6 +573,279 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
   }
 }
 
+// Constant-mask rows (const_chunk_member): their logits fl(m + bias) and
+// therefore their weights do not depend on the row, so a work-group forms
+// the weights of its (head, 128 queries) once per key tile and applies them
+// to the V of the up to kConstRows rows of its chunk.  No K tiles, no S^T;
+// per row and tile 6 MFMAs (O^T += V^T P^T, three fp16 terms) and one fma
+// per value.  The softmax is the exact path's (natural units, lazy max, one
+// rounded reference), so equal quantised logits get equal weights.  The
+// weights' planes P' = P 2^kVShift are shared by the rows; each row's v^T
+// tile carries its own 2^e_t, so every tile's product starts from zero and
+// is added to the row's O with the exact factor 2^-(e_t + kVShift).
+// XCD x serves the (head, query tile) pairs [x H nqt / 8, (x + 1) H nqt / 8)
+// of every chunk, chunk-major: a chunk's V slices meet in that XCD's L2
+// across its query tiles, and every XCD holds the same share of the chunks
+// that have work.
+constexpr int kConstStages = 3;
+
+// The per-row accumulators of the constant-row kernel as named members, and
+// a loop over the rows with a compile-time index, so the rows' registers
+// are never indexed at run time (which would move them to scratch memory).
+struct ConstRowsO {
+  f32x16 r0, r1, r2, r3;
+};
+static_assert(kConstRows == 4, "ConstRowsO holds four rows");
+template <int R>
+__device__ __forceinline__ f32x16& const_row(ConstRowsO& o) {
+  if constexpr (R == 0) return o.r0;
+  else if constexpr (R == 1) return o.r1;
+  else if constexpr (R == 2) return o.r2;
+  else return o.r3;
+}
+template <typename F>
+__device__ __forceinline__ void for_const_rows(F&& f) {
+  f(std::integral_constant<int, 0>{});
+  f(std::integral_constant<int, 1>{});
+  f(std::integral_constant<int, 2>{});
+  f(std::integral_constant<int, 3>{});
+}
+
+template <int LAYOUT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attention_const_kernel(AttnArgs a, int nqt, int nkt, int nchunks) {
+  constexpr bool kBlock = LAYOUT == kAttnBlock;
+  static_assert(LAYOUT == kAttnBlock || LAYOUT == kAttnStaged, "plane layouts only");
+  // Stage s: V^T hi and lo planes of each chunk row, (row, plane) at
+  // (2 row + plane) kPlaneBytes.
+  constexpr int kStageBytesC = kConstRows * 2 * kPlaneBytes;
+  __shared__ __attribute__((aligned(16))) uint8_t ring[kConstStages * kStageBytesC];
+  __shared__ float Sv[kConstRows][kTileFlagWords * 32];  // 2^-(e_t + kVShift) per row and tile
+
+  const int nhq = kHeads * nqt;
+  const int xcd = (int)(blockIdx.x % kXcds);
+  const int slot = (int)(blockIdx.x / kXcds);
+  const int hq0 = xcd * nhq / kXcds;
+  const int nh = (xcd + 1) * nhq / kXcds - hq0;
+  if (nh == 0 || slot >= nh * nchunks) return;
+  const int chunk = slot / nh;
+  const int hq = hq0 + slot % nh;
+  const int h = hq / nqt;
+  const int qt = hq % nqt;
+
+  // The chunk's rows served here, bit r for row chunk kConstRows + r
+  // (uniform across the work-group).
+  uint32_t live = 0u;
+  float m_row = 0.f;
+  for (int r = 0; r < kConstRows; ++r) {
+    const int b = chunk * kConstRows + r;
+    float m = 0.f;
+    if (b < a.batch && constant_mask_row(a, b, m) && (live == 0u || m == m_row)) {
+      if (live == 0u) m_row = m;
+      live |= 1u << r;
+    }
+  }
+  live = __builtin_amdgcn_readfirstlane(live);
+  if (live == 0u) return;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+  const int j0 = qt * kBq;
+  const int jq = j0 + 32 * w + l32;
+  const int qt32 = (j0 >> 5) + w;
+  const int64_t nt = a.np >> 5;
+  const int64_t frag = ((int64_t)h * nt + qt32) * nt * 1024;
+  const __amdgpu_buffer_rsrc_t rb = buffer(a.bias + frag, nt * 4096);
+  const uint32_t ob = (uint32_t)lane * 16;
+  const int64_t slice_bytes = (int64_t)a.np * 128;
+
+  // Wave w copies the V^T planes of chunk row w (if live): lane l writes
+  // chunk l % 4 of plane rows l / 4 and 16 + l / 4, as in the block kernel.
+  const bool copies = (live >> w) & 1u;
+  const uint8_t* vsrc = reinterpret_cast<const uint8_t*>(a.v) +
+                        ((int64_t)(chunk * kConstRows + w) * kHeads + h) * slice_bytes +
+                        (lane >> 2) * 64 + 16 * ((lane & 3) ^ swz(lane >> 2));
+  auto copy = [&](int t, int stage) {
+    if (!copies) return;
+    const uint8_t* src = vsrc + (int64_t)t * kPlaneBytes;
+    uint8_t* dst = ring + stage * kStageBytesC + 2 * w * kPlaneBytes;
+    lds_dma16(src, dst);
+    lds_dma16(src + 1024, dst + 1024);
+    lds_dma16(src + (slice_bytes >> 1), dst + kPlaneBytes);
+    lds_dma16(src + (slice_bytes >> 1) + 1024, dst + kPlaneBytes + 1024);
+  };
+  const uint32_t rd0 = l32 * 64 + 16 * (half ^ swz(l32));
+  const uint32_t rd1 = l32 * 64 + 16 * ((2 + half) ^ swz(l32));
+  auto plane_rd = [&](int stage, int r, int plane, int m) -> bf16x8 {
+    return *(const bf16x8*)(ring + stage * kStageBytesC + (2 * r + plane) * kPlaneBytes + (m ? rd1 : rd0));
+  };
+  auto load_frag = [&](int t) -> f32x16 {
+    const uint32_t so = (uint32_t)t * 4096;
+    return cat4(buffer_f4(rb, ob, so), buffer_f4(rb, ob + 1024, so), buffer_f4(rb, ob + 2048, so),
+                buffer_f4(rb, ob + 3072, so));
+  };
+
+  // Each live row's v^T tile factors 2^-(e_t + kVShift), exact powers of two.
+  {
+    const int64_t per = (int64_t)kHeads * nt;
+    for (int i = tid; i < kConstRows * nkt; i += kThreads) {
+      const int r = i / nkt, t = i % nkt;
+      const int b = chunk * kConstRows + r;
+      Sv[r][t] = b < a.batch
+                     ? __builtin_ldexpf(a.scales[2 * (int64_t)a.batch * per + (int64_t)b * per +
+                                                 (int64_t)h * nt + t],
+                                        -kVShift)
+                     : 0.f;
+    }
+  }
+
+  // Logits of tile t from its bias fragment: fl(m + bias), -inf past key n.
+  const int full_tiles = a.n / kBk;
+  auto finish = [&](f32x16& x, int t) {
+    if (t < full_tiles) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[r] = m_row + x[r];
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = t * kBk + 8 * (r >> 2) + 4 * half + (r & 3);
+        x[r] = key < a.n ? m_row + x[r] : -INFINITY;
+      }
+    }
+  };
+
+  ConstRowsO o = {};
+  float l_run = 0.f;
+  float m_ref = -INFINITY;
+  float c_ref = 0.f;
+  float w_ref = 1.f;
+  const f32x16 zero16 = {};
+
+  // The exact path's softmax of one tile, shared by the rows: weights
+  // P = exp2(x log2(e) - c_ref) w_ref (at most 2^8 by the lazy max), into
+  // fp16 planes as P 2^kVShift.
+  auto softmax = [&](const f32x16& x, bf16x8 (&ph)[2], bf16x8 (&pl)[2]) {
+    const float mt = xor32_max(max16(x));
+    if (__any(mt > m_ref + kRescaleNat)) {
+      const float m_new = __builtin_elementwise_maximum(m_ref, mt);
+      const float c_new = m_new == -INFINITY ? 0.f : m_new * kLog2e;
+      const float alpha = m_ref == -INFINITY ? 0.f : exp2_fast((m_ref - m_new) * kLog2e);
+      for_const_rows([&](auto r) {
+        f32x16& acc = const_row<decltype(r)::value>(o);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] *= alpha;
+      });
+      l_run *= alpha;
+      m_ref = m_new;
+      c_ref = c_new;
+      w_ref = m_new == -INFINITY ? 1.f : exp2_fast(-__builtin_fmaf(m_new, kLog2e, -c_new));
+    }
+    const float f = w_ref * (float)(1 << kVShift);
+    float ps = 0.f;
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      f32x8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = exp2_fast(__builtin_fmaf(x[8 * m + e], kLog2e, -c_ref));
+      ps += ((v[0] + v[4]) + (v[1] + v[5])) + ((v[2] + v[6]) + (v[3] + v[7]));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] *= f;
+      split_f16(v, ph[m], pl[m]);
+    }
+    l_run = __builtin_fmaf(ps, w_ref, l_run);
+  };
+  // O_r += 2^-(e_t + kVShift) V'^T P'^T for every live row.
+  auto pv = [&](int stage, int t, const bf16x8 (&ph)[2], const bf16x8 (&pl)[2]) {
+    for_const_rows([&](auto rc) {
+      constexpr int r = decltype(rc)::value;
+      if (!((live >> r) & 1u)) return;
+      f32x16 acc = zero16;
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const bf16x8 vh = plane_rd(stage, r, 0, m);
+        const bf16x8 vl = plane_rd(stage, r, 1, m);
+        acc = mfma_f16(vl, ph[m], acc);
+        acc = mfma_f16(vh, pl[m], acc);
+        acc = mfma_f16(vh, ph[m], acc);
+      }
+      const float sc = Sv[r][t];
+      f32x16& orow = const_row<r>(o);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) orow[e] = __builtin_fmaf(acc[e], sc, orow[e]);
+    });
+  };
+
+  const int last = nkt - 1;
+  auto clamp = [&](int t) { return t < last ? t : last; };
+  auto stage = [](int t) { return t % kConstStages; };
+  // Prologue: tiles 0 and 1 on their way; tile t + 2 is copied at iteration
+  // t into the stage that held tile t - 1, which every wave left behind at
+  // the previous barrier.  Tiles past the last are clamped (in range, never
+  // used).
+  f32x16 x_a = load_frag(0);
+  f32x16 x_b = load_frag(clamp(1));
+  copy(0, 0);
+  copy(clamp(1), 1);
+  wait_vmcnt<4>();  // tile 0 and both bias fragments have landed
+  __syncthreads();
+  finish(x_a, 0);
+  auto body = [&](int t, f32x16& cur, f32x16& nxt) {
+    bf16x8 ph[2], pl[2];
+    softmax(cur, ph, pl);
+    cur = load_frag(clamp(t + 2));
+    pv(stage(t), t, ph, pl);
+    finish(nxt, t + 1);
+    copy(clamp(t + 2), stage(t + 2));
+    // Tile t + 1 has landed once at most this iteration's four bias-fragment
+    // loads and four tile copies are outstanding (loads retire in order).
+    wait_vmcnt<8>();
+    __syncthreads();
+  };
+  auto tail = [&](const f32x16& cur, int t) {
+    bf16x8 ph[2], pl[2];
+    softmax(cur, ph, pl);
+    pv(stage(t), t, ph, pl);
+  };
+  int kt = 0;
+  for (; kt + 2 < nkt; kt += 2) {
+    body(kt, x_a, x_b);
+    body(kt + 1, x_b, x_a);
+  }
+  if (kt + 1 < nkt) {
+    body(kt, x_a, x_b);
+    tail(x_b, kt + 1);
+  } else {
+    tail(x_a, kt);
+  }
+  wait_vmcnt<0>();  // the clamped tail loads land before the LDS is released
+
+  const float l_tot = xor32_sum(l_run);
+  if (jq < a.n) {
+    for_const_rows([&](auto rc) {
+      constexpr int r = decltype(rc)::value;
+      if (!((live >> r) & 1u)) return;
+      const int b = chunk * kConstRows + r;
+      const f32x16& orow = const_row<r>(o);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int c = 8 * rr + 4 * half;  // channels c..c+3 of head h
+        f32x4 ov4 = {orow[4 * rr + 0] / l_tot, orow[4 * rr + 1] / l_tot, orow[4 * rr + 2] / l_tot,
+                     orow[4 * rr + 3] / l_tot};
+        if constexpr (kBlock) {
+          const int64_t col = h * kHeadDim + c;
+          if (a.gate) ov4 = ov4 * *(const f32x4*)(a.gate + ((int64_t)b * a.np + jq) * kHidden + col);
+          *(f32x4*)(a.out + ((int64_t)b * a.n + jq) * kHidden + col) = ov4;
+        } else {
+          *(f32x4*)(a.out + b * a.os[0] + h * a.os[1] + (int64_t)jq * a.os[2] + c) = ov4;
+        }
+      }
+    });
+  }
+}
+
 }  // namespace
 
 hipError_t launch_attention_split(int layout, const AttnArgs& a, hipStream_t stream) {
@@ -569,19 +861,31 @@ hipError_t launch_attention_split(int layout, const AttnArgs& a, hipStream_t str
   const size_t mask_row_bytes = (size_t)nkt * kBk * sizeof(float);
   // Two launches over the same grid: rows on the fast softmax path, then
   // the others (fully masked rows, rows whose logits are not bounded); each
-  // work-group of the wrong path exits after reading its row's flags.
+  // work-group of the wrong path exits after reading its row's flags.  A
+  // third launch serves the constant-mask rows (padding rows) a chunk of
+  // kConstRows at a time; its work-groups without such rows exit at once.
+  const int nchunks = (a.batch + kConstRows - 1) / kConstRows;
+  const uint64_t const_grid =
+      (uint64_t)kXcds * ((kHeads * nqt + kXcds - 1) / kXcds) * (uint64_t)nchunks;
+  if (const_grid > 0x7fffffffull) return hipErrorInvalidValue;
   if (layout == kAttnBlock) {
     hipLaunchKernelGGL((attention_split_kernel<kAttnBlock, false>), dim3((uint32_t)total),
                        dim3(kThreads), mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     hipLaunchKernelGGL((attention_split_kernel<kAttnBlock, true>), dim3((uint32_t)total),
                        dim3(kThreads), mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    hipLaunchKernelGGL((attention_const_kernel<kAttnBlock>), dim3(const_grid), dim3(kThreads), 0,
+                       stream, a, nqt, nkt, nchunks);
   } else if (layout == kAttnStaged) {
     hipLaunchKernelGGL((attention_split_kernel<kAttnStaged, false>), dim3((uint32_t)total),
                        dim3(kThreads), mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     hipLaunchKernelGGL((attention_split_kernel<kAttnStaged, true>), dim3((uint32_t)total),
                        dim3(kThreads), mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    hipLaunchKernelGGL((attention_const_kernel<kAttnStaged>), dim3(const_grid), dim3(kThreads), 0,
+                       stream, a, nqt, nkt, nchunks);
   } else {
     return hipErrorInvalidValue;
   }
