@@ -46,6 +46,7 @@
 #include "kernels.hpp"
 #include "split.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <type_traits>
 
@@ -115,42 +116,137 @@ __device__ __forceinline__ bool const_chunk_member(const AttnArgs& a, int b) {
   return true;  // the chunk's first constant-mask row
 }
 
+// Work item -> (outer row b, head h, query tile qt).  Items are dispatched
+// round-robin over the XCDs (item % kXcds), each XCD with its own 4 MB L2.
+// Item counts are rows8 * kHeads * nqt, rows8 = batch rounded up to
+// kRowGroup.
+//   pair groups (ppg > 0): the kHeads * nqt (head, query tile) pairs form
+//     groups of ppg pairs; XCD x serves groups x, x + kXcds, ... one after
+//     the other, each for every outer row, row-major (the ppg pairs of a row
+//     are consecutive items, so they share the row's K/V slices in L2).  The
+//     host picks ppg so that a group's bias slices (ppg x 128 queries x np
+//     keys x 4 bytes) stay within about 2.5 MB of the L2.
+//   row groups (ppg = 0): head, group of kRowGroup outer rows, query tile,
+//     row in group, each XCD a contiguous range; logical row lr = u groups
+//     + v runs outer row 8 v + u, so each XCD takes every 8th outer row and
+//     rows that leave a launch early spread evenly over the XCDs.
+__device__ __forceinline__ void attn_item(uint32_t item, uint32_t total, int batch, int nqt, int ppg,
+                                          int& b, int& h, int& qt) {
+  if (ppg > 0) {
+    const int xcd = (int)(item % kXcds);
+    const int slot = (int)(item / kXcds);
+    const int rows8 = (int)(total / (uint32_t)(kHeads * nqt));
+    const int pass = slot / (rows8 * ppg);
+    const int within = slot - pass * rows8 * ppg;
+    b = within / ppg;
+    const int pair = (xcd + kXcds * pass) * ppg + within % ppg;
+    h = pair / nqt;
+    qt = pair % nqt;
+    return;
+  }
+  const uint32_t logical = xcd_remap(item, total);
+  const int groups = (batch + kRowGroup - 1) / kRowGroup;
+  const int per_head = groups * kRowGroup * nqt;
+  h = (int)(logical / per_head);
+  const int rem = (int)(logical % per_head);
+  const int grp = rem / (kRowGroup * nqt);
+  const int in_grp = rem % (kRowGroup * nqt);
+  qt = in_grp / kRowGroup;
+  const int lr = grp * kRowGroup + in_grp % kRowGroup;
+  b = kRowGroup * (lr % groups) + lr / groups;
+}
+
+// LDS of the attention work-group: the ring of key tiles, the per-tile
+// scales, and the mask-bias row (dynamic, after the static arrays).
+struct AttnLds {
+  uint8_t* ring;  // kStages x kStageBytes
+  float* Ms;      // mask-bias row of this outer row, nkt_all * kBk floats
+  float* Sk;      // 2^-e_k of each key tile
+  int* Ev;        // e_v of each key tile's v^T planes
+  float* Wv;      // per wave: max 2^-e_v over its tiles
+};
+
+// Row classification from the tile flags and the magnitude record: returns
+// whether row b takes the fast softmax path, with the key tiles it visits
+// (nkt), the tile words of part 0 (mw: a tile holds a nonzero mask bias) and
+// whether any visited tile does (any).
+// On rows with an unmasked key, the trailing tiles whose every mask bias is
+// <= -kSkipMask carry weights that are exactly 0 when the prepare
+// projection's magnitude record bounds the logits (kernels.hpp), so they are
+// left out; the result is bit-identical.  The fast softmax needs the same
+// record to bound the logits below kFastBound, together with the row's
+// largest mask bias when that is positive (its integer reference then stays
+// exact when shifted by a tile's plane exponent); other rows take the exact
+// path.
+__device__ __forceinline__ bool row_is_fast(const AttnArgs& a, int b, int nkt_all, int& nkt,
+                                            uint32_t (&mw)[kTileFlagWords], uint32_t& any) {
+  uint32_t open = 0u;
+  any = 0u;
+  {
+    const uint32_t* f = a.tile_flags + (int64_t)b * kTileFlagParts * kTileFlagWords;
+#pragma unroll
+    for (int i = 0; i < kTileFlagWords; ++i) {
+      const int lo = 32 * i;
+      const uint32_t valid =
+          nkt_all >= lo + 32 ? 0xffffffffu : nkt_all > lo ? (1u << (nkt_all - lo)) - 1u : 0u;
+      mw[i] = f[i];
+      any |= mw[i] & valid;
+      open |= ~f[kTileFlagWords + i] & valid;
+    }
+  }
+  const bool has_unmasked = open != 0u;
+  nkt = nkt_all;
+  bool fast = false;
+  if (has_unmasked && a.magnitudes != nullptr && a.magnitudes[4] == 1u) {
+    const float mq = __builtin_bit_cast(float, a.magnitudes[0]);
+    const float mk = __builtin_bit_cast(float, a.magnitudes[1]);
+    const float mv = __builtin_bit_cast(float, a.magnitudes[2]);
+    const float mb = __builtin_bit_cast(float, a.magnitudes[3]);
+    const float mm = __builtin_bit_cast(
+        float, a.tile_flags[((int64_t)b * kTileFlagParts + kTileFlagMaxPart) * kTileFlagWords]);
+    const float bound = 32.0f * mq * mk + mb;
+    const float lift = mm > 0.0f ? mm : 0.0f;
+    // false for NaN anywhere (the comparison with mm rejects a NaN mask bias)
+    fast = bound + lift < kFastBound && (mm <= 0.0f || mm < kFastBound) && mv < INFINITY;
+    if (bound < kSkipBound && mv < INFINITY) {  // false for NaN
+      const uint32_t* far =
+          a.tile_flags + (int64_t)b * kTileFlagParts * kTileFlagWords + 2 * kTileFlagWords;
+      while (nkt > 1) {
+        const int t = nkt - 1;
+        if (!((far[t >> 5] >> (t & 31)) & 1u)) break;
+        nkt = t;
+      }
+    }
+  }
+  return fast;
+}
+
+// Rows served by the exact launch: neither fast nor taken by the
+// constant-row kernel.
+__device__ __forceinline__ bool row_is_exact(const AttnArgs& a, int b, int nkt_all) {
+  int nkt;
+  uint32_t mw[kTileFlagWords], any;
+  return !row_is_fast(a, b, nkt_all, nkt, mw, any) && !const_chunk_member(a, b);
+}
+
 // Both layouts read q, k and v^T in the plane layout (ProjArgs::planes) with
 // their per-tile scales, and the staged bias copies, mask rows and tile
 // flags.  LAYOUT kAttnBlock: the block's workspace, gated head-last output;
 // kAttnStaged: planes staged from a caller's strided q, k, v
 // (launch_stage_planes), output through the caller's strides, no gate.
-// EXACT selects the softmax path the launch serves (see launch_attention_split);
-// the exact path holds a few more values and runs at three waves per SIMD.
+// One work item (b, h, qt) of the split attention.  Uniform per work-group;
+// returns at once (before any LDS access) when the row belongs to the other
+// softmax path or to the constant-row kernel.
 template <int LAYOUT, bool EXACT>
-__global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(EXACT ? 3 : 4, EXACT ? 3 : 4)))
-void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
+__device__ __forceinline__ void attend_item(const AttnArgs& a, int nqt, int nkt_all, int b, int h,
+                                            int qt, const AttnLds& L) {
   constexpr bool kBlock = LAYOUT == kAttnBlock;
   static_assert(LAYOUT == kAttnBlock || LAYOUT == kAttnStaged, "plane layouts only");
-  // The ring of key tiles (kStages x kStageBytes).
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kStages * kStageBytes];
-  // Mask-bias row of this outer row, nkt_all * kBk floats (dynamic).
-  extern __shared__ __attribute__((aligned(16))) float Ms[];
-  __shared__ float Sk[kTileFlagWords * 32];  // 2^-e_k of each key tile
-  __shared__ int Ev[kTileFlagWords * 32];    // e_v of each key tile's v^T planes
-  __shared__ float Wv[kThreads / 64];        // per wave: max 2^-e_v over its tiles
-
-  const uint32_t logical = xcd_remap(blockIdx.x, total);
-  const int groups = (a.batch + kRowGroup - 1) / kRowGroup;
-  const int per_head = groups * kRowGroup * nqt;
-  const int h = (int)(logical / per_head);
-  const int rem = (int)(logical % per_head);
-  const int grp = rem / (kRowGroup * nqt);
-  const int in_grp = rem % (kRowGroup * nqt);
-  const int qt = in_grp / kRowGroup;
-  // Logical row lr = u groups + v runs outer row 8 v + u: each XCD's
-  // contiguous range of logical rows takes every 8th outer row, so rows that
-  // leave the launch early (the other softmax path, padding) spread evenly
-  // over the XCDs.  The bias a work-group reads depends on (h, qt) only, so
-  // work-groups that run together still share it in L2.
-  const int lr = grp * kRowGroup + in_grp % kRowGroup;
-  const int b = kRowGroup * (lr % groups) + lr / groups;
+  uint8_t* const lds = L.ring;
+  float* const Ms = L.Ms;
+  float* const Sk = L.Sk;
+  int* const Ev = L.Ev;
+  float* const Wv = L.Wv;
   if (b >= a.batch) return;  // padding of the last row group; uniform per work-group
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -198,55 +294,10 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
     return cat4(buffer_f4(r, ob, s), buffer_f4(r, ob + 1024, s), buffer_f4(r, ob + 2048, s),
                 buffer_f4(r, ob + 3072, s));
   };
-  // Row classification from the tile flags, as in the FP32 kernel.
   uint32_t mw[kTileFlagWords];
-  uint32_t any = 0u, open = 0u;
-  {
-    const uint32_t* f = a.tile_flags + (int64_t)b * kTileFlagParts * kTileFlagWords;
-#pragma unroll
-    for (int i = 0; i < kTileFlagWords; ++i) {
-      const int lo = 32 * i;
-      const uint32_t valid =
-          nkt_all >= lo + 32 ? 0xffffffffu : nkt_all > lo ? (1u << (nkt_all - lo)) - 1u : 0u;
-      mw[i] = f[i];
-      any |= mw[i] & valid;
-      open |= ~f[kTileFlagWords + i] & valid;
-    }
-  }
-  const bool has_unmasked = open != 0u;
-  // Key tiles visited.  On rows with an unmasked key, the trailing tiles
-  // whose every mask bias is <= -kSkipMask carry weights that are exactly 0
-  // when the prepare projection's magnitude record bounds the logits
-  // (kernels.hpp), so they are left out; the result is bit-identical.
-  // The fast softmax needs the same record to bound the logits below
-  // kFastBound, together with the row's largest mask bias when that is
-  // positive (its integer reference then stays exact when shifted by a
-  // tile's plane exponent); other rows take the exact path.
-  int nkt = nkt_all;
-  bool fast = false;
-  {
-    if (has_unmasked && a.magnitudes != nullptr && a.magnitudes[4] == 1u) {
-      const float mq = __builtin_bit_cast(float, a.magnitudes[0]);
-      const float mk = __builtin_bit_cast(float, a.magnitudes[1]);
-      const float mv = __builtin_bit_cast(float, a.magnitudes[2]);
-      const float mb = __builtin_bit_cast(float, a.magnitudes[3]);
-      const float mm = __builtin_bit_cast(
-          float, a.tile_flags[((int64_t)b * kTileFlagParts + kTileFlagMaxPart) * kTileFlagWords]);
-      const float bound = 32.0f * mq * mk + mb;
-      const float lift = mm > 0.0f ? mm : 0.0f;
-      // false for NaN anywhere (the comparison with mm rejects a NaN mask bias)
-      fast = bound + lift < kFastBound && (mm <= 0.0f || mm < kFastBound) && mv < INFINITY;
-      if (bound < kSkipBound && mv < INFINITY) {  // false for NaN
-        const uint32_t* far = a.tile_flags + (int64_t)b * kTileFlagParts * kTileFlagWords +
-                              2 * kTileFlagWords;
-        while (nkt > 1) {
-          const int t = nkt - 1;
-          if (!((far[t >> 5] >> (t & 31)) & 1u)) break;
-          nkt = t;
-        }
-      }
-    }
-  }
+  uint32_t any;
+  int nkt;
+  const bool fast = row_is_fast(a, b, nkt_all, nkt, mw, any);
   // Each row runs in the launch of its softmax path (uniform per work-group).
   if (fast == EXACT) return;
   // Exact rows that the constant-row kernel serves are left out; other
@@ -573,6 +624,45 @@ void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total) {
   }
 }
 
+// The fast launch runs one work item per work-group (total work-groups,
+// attn_item order).  The exact launch is persistent: at most kExactGroups
+// work-groups walk units u = blockIdx.x + k gridDim.x, unit u = pairs
+// u % kExactChunks, u % kExactChunks + kExactChunks, ... of outer row
+// u / kExactChunks; a row that is not exact costs one check, and an exact
+// row's pairs spread over kExactChunks work-groups.  The barrier after an
+// item releases the LDS for the next.  EXACT selects the softmax path the
+// launch serves; the exact path holds a few more values and runs at three
+// waves per SIMD.
+constexpr int kExactGroups = 768;  // three work-groups of four waves per CU
+constexpr int kExactChunks = 4;
+template <int LAYOUT, bool EXACT>
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(EXACT ? 3 : 4, EXACT ? 3 : 4)))
+void attention_split_kernel(AttnArgs a, int nqt, int nkt_all, uint32_t total, int ppg) {
+  __shared__ __attribute__((aligned(16))) uint8_t ring[kStages * kStageBytes];
+  extern __shared__ __attribute__((aligned(16))) float Ms[];
+  __shared__ float Sk[kTileFlagWords * 32];
+  __shared__ int Ev[kTileFlagWords * 32];
+  __shared__ float Wv[kThreads / 64];
+  const AttnLds L{ring, Ms, Sk, Ev, Wv};
+  if constexpr (!EXACT) {
+    int b, h, qt;
+    attn_item(blockIdx.x, total, a.batch, nqt, ppg, b, h, qt);
+    attend_item<LAYOUT, EXACT>(a, nqt, nkt_all, b, h, qt, L);
+  } else {
+    const int npairs = kHeads * nqt;
+    const uint32_t units = (uint32_t)a.batch * kExactChunks;
+    for (uint32_t u = blockIdx.x; u < units; u += gridDim.x) {
+      const int b = (int)(u / kExactChunks);
+      if (!row_is_exact(a, b, nkt_all)) continue;  // uniform per work-group
+      for (int pair = (int)(u % kExactChunks); pair < npairs; pair += kExactChunks) {
+        attend_item<LAYOUT, EXACT>(a, nqt, nkt_all, b, pair / nqt, pair % nqt, L);
+        __syncthreads();
+      }
+    }
+  }
+}
+
 // Constant-mask rows (const_chunk_member): their logits fl(m + bias) and
 // therefore their weights do not depend on the row, so a work-group forms
 // the weights of its (head, 128 queries) once per key tile and applies them
@@ -611,20 +701,21 @@ __device__ __forceinline__ void for_const_rows(F&& f) {
   f(std::integral_constant<int, 3>{});
 }
 
+// Stage s: V^T hi and lo planes of each chunk row, (row, plane) at
+// (2 row + plane) kPlaneBytes.
+constexpr int kStageBytesC = kConstRows * 2 * kPlaneBytes;
+typedef float ConstScales[kTileFlagWords * 32];  // 2^-(e_t + kVShift) per tile of a row
+
+// One work item of the constant-row kernel; uniform per work-group, returns
+// at once (before any LDS access) when the item has no constant-mask rows.
 template <int LAYOUT>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void attention_const_kernel(AttnArgs a, int nqt, int nkt, int nchunks) {
+__device__ __forceinline__ void const_item(const AttnArgs& a, int nqt, int nkt, int nchunks,
+                                           uint32_t item, uint8_t* ring, ConstScales* Sv) {
   constexpr bool kBlock = LAYOUT == kAttnBlock;
   static_assert(LAYOUT == kAttnBlock || LAYOUT == kAttnStaged, "plane layouts only");
-  // Stage s: V^T hi and lo planes of each chunk row, (row, plane) at
-  // (2 row + plane) kPlaneBytes.
-  constexpr int kStageBytesC = kConstRows * 2 * kPlaneBytes;
-  __shared__ __attribute__((aligned(16))) uint8_t ring[kConstStages * kStageBytesC];
-  __shared__ float Sv[kConstRows][kTileFlagWords * 32];  // 2^-(e_t + kVShift) per row and tile
-
   const int nhq = kHeads * nqt;
-  const int xcd = (int)(blockIdx.x % kXcds);
-  const int slot = (int)(blockIdx.x / kXcds);
+  const int xcd = (int)(item % kXcds);
+  const int slot = (int)(item / kXcds);
   const int hq0 = xcd * nhq / kXcds;
   const int nh = (xcd + 1) * nhq / kXcds - hq0;
   if (nh == 0 || slot >= nh * nchunks) return;
@@ -846,6 +937,20 @@ void attention_const_kernel(AttnArgs a, int nqt, int nkt, int nchunks) {
   }
 }
 
+// A work-group per item: the few items with work spread over the whole
+// chip as the empty ones leave (a grid that walks the items would give some
+// work-groups one item more than others).  The loop serves any grid.
+template <int LAYOUT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attention_const_kernel(AttnArgs a, int nqt, int nkt, int nchunks, uint32_t items) {
+  __shared__ __attribute__((aligned(16))) uint8_t ring[kConstStages * kStageBytesC];
+  __shared__ ConstScales Sv[kConstRows];
+  for (uint32_t item = blockIdx.x; item < items; item += gridDim.x) {
+    const_item<LAYOUT>(a, nqt, nkt, nchunks, item, ring, Sv);
+    __syncthreads();
+  }
+}
+
 }  // namespace
 
 hipError_t launch_attention_split(int layout, const AttnArgs& a, hipStream_t stream) {
@@ -859,33 +964,51 @@ hipError_t launch_attention_split(int layout, const AttnArgs& a, hipStream_t str
       nkt > kTileFlagWords * 32)
     return hipErrorInvalidValue;
   const size_t mask_row_bytes = (size_t)nkt * kBk * sizeof(float);
-  // Two launches over the same grid: rows on the fast softmax path, then
-  // the others (fully masked rows, rows whose logits are not bounded); each
-  // work-group of the wrong path exits after reading its row's flags.  A
-  // third launch serves the constant-mask rows (padding rows) a chunk of
-  // kConstRows at a time; its work-groups without such rows exit at once.
+  // Pair groups (attn_item): the largest ppg dividing nqt / 2 (so the
+  // kHeads * nqt pairs form a multiple of kXcds groups) whose bias slices
+  // fit kGroupBiasBytes; ppg = 1 would fetch every K/V slice once per pair,
+  // so that case keeps the row-group order.
+  constexpr uint64_t kGroupBiasBytes = 2560ull << 10;
+  const uint64_t slice_bytes = (uint64_t)kBq * (uint64_t)a.np * sizeof(float);
+  int ppg = 0;
+  if (nqt % 2 == 0) {
+    for (int g = nqt / 2; g >= 2; --g) {
+      if ((nqt / 2) % g == 0 && (uint64_t)g * slice_bytes <= kGroupBiasBytes) {
+        ppg = g;
+        break;
+      }
+    }
+  }
+  // Three launches: rows on the fast softmax path (one work-group per work
+  // item; the others leave after reading their row's flags), then the other
+  // rows (fully masked rows, rows whose logits are not bounded) on a
+  // persistent grid, then the constant-mask rows (padding rows), a chunk of
+  // kConstRows at a time, one work-group per item.
+  const uint32_t exact_grid =
+      (uint32_t)std::min<uint64_t>((uint64_t)a.batch * kExactChunks, kExactGroups);
   const int nchunks = (a.batch + kConstRows - 1) / kConstRows;
-  const uint64_t const_grid =
+  const uint64_t const_items =
       (uint64_t)kXcds * ((kHeads * nqt + kXcds - 1) / kXcds) * (uint64_t)nchunks;
-  if (const_grid > 0x7fffffffull) return hipErrorInvalidValue;
+  if (const_items > 0x7fffffffull) return hipErrorInvalidValue;
+  const uint32_t const_grid = (uint32_t)const_items;
   if (layout == kAttnBlock) {
     hipLaunchKernelGGL((attention_split_kernel<kAttnBlock, false>), dim3((uint32_t)total),
-                       dim3(kThreads), mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total);
+                       dim3(kThreads), mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total, ppg);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-    hipLaunchKernelGGL((attention_split_kernel<kAttnBlock, true>), dim3((uint32_t)total),
-                       dim3(kThreads), mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total);
+    hipLaunchKernelGGL((attention_split_kernel<kAttnBlock, true>), dim3(exact_grid),
+                       dim3(kThreads), mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total, ppg);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     hipLaunchKernelGGL((attention_const_kernel<kAttnBlock>), dim3(const_grid), dim3(kThreads), 0,
-                       stream, a, nqt, nkt, nchunks);
+                       stream, a, nqt, nkt, nchunks, (uint32_t)const_items);
   } else if (layout == kAttnStaged) {
     hipLaunchKernelGGL((attention_split_kernel<kAttnStaged, false>), dim3((uint32_t)total),
-                       dim3(kThreads), mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total);
+                       dim3(kThreads), mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total, ppg);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-    hipLaunchKernelGGL((attention_split_kernel<kAttnStaged, true>), dim3((uint32_t)total),
-                       dim3(kThreads), mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total);
+    hipLaunchKernelGGL((attention_split_kernel<kAttnStaged, true>), dim3(exact_grid),
+                       dim3(kThreads), mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total, ppg);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     hipLaunchKernelGGL((attention_const_kernel<kAttnStaged>), dim3(const_grid), dim3(kThreads), 0,
-                       stream, a, nqt, nkt, nchunks);
+                       stream, a, nqt, nkt, nchunks, (uint32_t)const_items);
   } else {
     return hipErrorInvalidValue;
   }
