@@ -116,46 +116,6 @@ __device__ __forceinline__ bool const_chunk_member(const AttnArgs& a, int b) {
   return true;  // the chunk's first constant-mask row
 }
 
-// Work item -> (outer row b, head h, query tile qt).  Items are dispatched
-// round-robin over the XCDs (item % kXcds), each XCD with its own 4 MB L2.
-// Item counts are rows8 * kHeads * nqt, rows8 = batch rounded up to
-// kRowGroup.
-//   pair groups (ppg > 0): the kHeads * nqt (head, query tile) pairs form
-//     groups of ppg pairs; XCD x serves groups x, x + kXcds, ... one after
-//     the other, each for every outer row, row-major (the ppg pairs of a row
-//     are consecutive items, so they share the row's K/V slices in L2).  The
-//     host picks ppg so that a group's bias slices (ppg x 128 queries x np
-//     keys x 4 bytes) stay within about 2.5 MB of the L2.
-//   row groups (ppg = 0): head, group of kRowGroup outer rows, query tile,
-//     row in group, each XCD a contiguous range; logical row lr = u groups
-//     + v runs outer row 8 v + u, so each XCD takes every 8th outer row and
-//     rows that leave a launch early spread evenly over the XCDs.
-__device__ __forceinline__ void attn_item(uint32_t item, uint32_t total, int batch, int nqt, int ppg,
-                                          int& b, int& h, int& qt) {
-  if (ppg > 0) {
-    const int xcd = (int)(item % kXcds);
-    const int slot = (int)(item / kXcds);
-    const int rows8 = (int)(total / (uint32_t)(kHeads * nqt));
-    const int pass = slot / (rows8 * ppg);
-    const int within = slot - pass * rows8 * ppg;
-    b = within / ppg;
-    const int pair = (xcd + kXcds * pass) * ppg + within % ppg;
-    h = pair / nqt;
-    qt = pair % nqt;
-    return;
-  }
-  const uint32_t logical = xcd_remap(item, total);
-  const int groups = (batch + kRowGroup - 1) / kRowGroup;
-  const int per_head = groups * kRowGroup * nqt;
-  h = (int)(logical / per_head);
-  const int rem = (int)(logical % per_head);
-  const int grp = rem / (kRowGroup * nqt);
-  const int in_grp = rem % (kRowGroup * nqt);
-  qt = in_grp / kRowGroup;
-  const int lr = grp * kRowGroup + in_grp % kRowGroup;
-  b = kRowGroup * (lr % groups) + lr / groups;
-}
-
 // LDS of the attention work-group: the ring of key tiles, the per-tile
 // scales, and the mask-bias row (dynamic, after the static arrays).
 struct AttnLds {
@@ -964,21 +924,7 @@ hipError_t launch_attention_split(int layout, const AttnArgs& a, hipStream_t str
       nkt > kTileFlagWords * 32)
     return hipErrorInvalidValue;
   const size_t mask_row_bytes = (size_t)nkt * kBk * sizeof(float);
-  // Pair groups (attn_item): the largest ppg dividing nqt / 2 (so the
-  // kHeads * nqt pairs form a multiple of kXcds groups) whose bias slices
-  // fit kGroupBiasBytes; ppg = 1 would fetch every K/V slice once per pair,
-  // so that case keeps the row-group order.
-  constexpr uint64_t kGroupBiasBytes = 2560ull << 10;
-  const uint64_t slice_bytes = (uint64_t)kBq * (uint64_t)a.np * sizeof(float);
-  int ppg = 0;
-  if (nqt % 2 == 0) {
-    for (int g = nqt / 2; g >= 2; --g) {
-      if ((nqt / 2) % g == 0 && (uint64_t)g * slice_bytes <= kGroupBiasBytes) {
-        ppg = g;
-        break;
-      }
-    }
-  }
+  const int ppg = pair_group_size(nqt, (uint64_t)kBq * (uint64_t)a.np * sizeof(float));
   // Three launches: rows on the fast softmax path (one work-group per work
   // item; the others leave after reading their row's flags), then the other
   // rows (fully masked rows, rows whose logits are not bounded) on a

@@ -326,19 +326,13 @@ __device__ __forceinline__ bf16x8 pack8(const f32x16& p, int m) {
 }
 
 __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArgs a, int nqt,
-                                                                     int nkt, uint32_t total) {
+                                                                     int nkt, uint32_t total,
+                                                                     int ppg) {
   __shared__ __attribute__((aligned(16))) uint8_t ring[kStagesB * kStageBytesB];
   __shared__ __attribute__((aligned(16))) float Ms[kMaxKeysB];
 
-  const uint32_t logical = xcd_remap(blockIdx.x, total);
-  const int groups = (a.batch + kRowGroup - 1) / kRowGroup;
-  const int per_head = groups * kRowGroup * nqt;
-  const int h = (int)(logical / per_head);
-  const int rem = (int)(logical % per_head);
-  const int grp = rem / (kRowGroup * nqt);
-  const int in_grp = rem % (kRowGroup * nqt);
-  const int qt = in_grp / kRowGroup;
-  const int b = grp * kRowGroup + in_grp % kRowGroup;
+  int b, h, qt;
+  attn_item(blockIdx.x, total, a.batch, nqt, ppg, b, h, qt);
   if (b >= a.batch) return;  // padding of the last row group; uniform per work-group
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -642,8 +636,9 @@ hipError_t launch_attention_bf16(const Bf16AttnArgs& a, hipStream_t stream) {
   const uint64_t total = groups * kRowGroup * kHeads * nqt;
   if (total == 0) return hipSuccess;
   if (total > 0x7fffffffull) return hipErrorInvalidValue;
+  const int ppg = pair_group_size(nqt, (uint64_t)kBq * (uint64_t)a.np * sizeof(__bf16));
   hipLaunchKernelGGL(attention_bf16_kernel, dim3((uint32_t)total), dim3(kThreads), 0, stream, a, nqt,
-                     nkt, (uint32_t)total);
+                     nkt, (uint32_t)total, ppg);
   return hipGetLastError();
 }
 
