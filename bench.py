@@ -212,7 +212,7 @@ def visited_key_tiles(n: int, valid: int | None, skip: bool) -> int:
 
 
 def split_executed(batch: int, n: int, ms: float, tiles: int | None = None,
-                   fp16_planes: bool = False) -> dict:
+                   fp16_planes: bool = False, const_tiles: int = 0) -> dict:
     """16-bit matrix-core work the split attention kernel executes for its
     FP32-accurate products, per 32 x 32 (query x key) wave tile, counted in
     32x32x16 MFMAs of 32768 flop each (two K-halves per product term)
@@ -223,12 +223,14 @@ def split_executed(batch: int, n: int, ms: float, tiles: int | None = None,
         terms of S^T and 3 of O^T = 12.
     fp16 and bf16 MFMAs share one dense peak.  Query rows are padded to 128,
     keys to 32.  ``tiles``: key tiles visited summed over the outer rows
-    (default: every tile of every row)."""
+    (default: every tile of every row).  ``const_tiles``: the part of
+    ``tiles`` on constant-mask rows (padding rows, fl(s + m) = m for every
+    key), whose S^T the kernel leaves out: 6 MFMAs per wave tile (O^T only)."""
     np_ = -(-n // 128) * 128
     nkt = -(-n // 32)
     visited = batch * nkt if tiles is None else tiles
     per_tile = 12 if fp16_planes else 18
-    executed = visited * 4 * (np_ // 32) * per_tile * 32768
+    executed = ((visited - const_tiles) * per_tile + const_tiles * 6) * 4 * (np_ // 32) * 32768
     executed_tflops = executed / (ms * 1e-3) / 1e12
     unit = ("fp16 hi/lo planes scaled by powers of two (q, k per 32x32 tile; v^T per key "
             "tile; p per tile), three terms per product" if fp16_planes
@@ -835,8 +837,8 @@ def main() -> int:
     if cfg.dtype == "bf16":
         kernel_name = "attention_bf16_kernel (fpx_tri_attn_attend, BF16)"
     elif split:
-        kernel_name = ("attention_split_kernel<kAttnBlock, fast | exact> "
-                       "(fpx_tri_attn_attend, fp16 planes)")
+        kernel_name = ("attention_split_kernel<kAttnBlock, fast | exact> + "
+                       "attention_const_kernel<kAttnBlock> (fpx_tri_attn_attend, fp16 planes)")
     else:
         kernel_name = "attention_kernel<kAttnBlock> (fpx_tri_attn_attend, FP32 matrix cores)"
     # The peak of the matrix unit the kernel issues: fp16/bf16 unless the FP32
@@ -862,7 +864,10 @@ def main() -> int:
             flops["core"] / (stages["attend"] * 1e-3) / 1e12, 3),
     }
     if split:
-        roofline.update(split_executed(n, n, stages["attend"], visited, fp16_planes=True))
+        # padding rows of a tail mask take the constant-mask kernel (no S^T)
+        const_tiles = 0 if cfg.valid is None or cfg.valid >= n else (n - cfg.valid) * nkt
+        roofline.update(split_executed(n, n, stages["attend"], visited, fp16_planes=True,
+                                       const_tiles=const_tiles))
     result = {
         "metric": METRIC,
         "value": round(value, 3),
