@@ -177,6 +177,25 @@ __global__ __launch_bounds__(Bf16ProjTraits<MODE>::kWaves * 64) void projection_
     return acc;
   };
 
+  // Stores rows r and r + 1 (r even) of a column-per-lane tile as 32-bit
+  // words: lane pairs (l32, l32 ^ 1) exchange their bf16 pairs, so the even
+  // lane stores columns l32, l32 + 1 of row r and the odd lane columns
+  // l32 - 1, l32 of row r + 1.  dst addresses (row 0, column l32) of the
+  // tile in a row-major bf16 array with `stride` elements per row.
+  auto store_pairs = [&](__bf16* dst, int64_t stride, const f32x16& v) {
+    const bool odd = l32 & 1;
+    const uint32_t sel = odd ? 0x03020706u : 0x05040100u;
+    __bf16* base = dst + (odd ? stride - 1 : 0);
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) {
+      const bf16x2 w2 = {(__bf16)v[r], (__bf16)v[r + 1]};
+      const uint32_t mine = __builtin_bit_cast(uint32_t, w2);
+      const uint32_t other = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mine, 0xB1, 0xF, 0xF, false);
+      *(uint32_t*)(base + (int64_t)(8 * (r >> 2) + (r & 3)) * stride) =
+          __builtin_amdgcn_perm(other, mine, sel);
+    }
+  };
+
   // Lane holds rows 4*half + 8*(r/4) + r%4 of the tile, column col_w.
   auto epilogue = [&](int tile, const f32x16& acc) {
     const int i = tile / tiles_j;
@@ -188,9 +207,10 @@ __global__ __launch_bounds__(Bf16ProjTraits<MODE>::kWaves * 64) void projection_
       if (group == 0 || group == 1) {
         __bf16* dst = (group == 0 ? a.qh : a.kh) + (bh * a.np + j0) * kHeadDim + l32;
         const float scale = group == 0 ? a.q_scale : 1.0f;
+        f32x16 v;
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          dst[(8 * (r >> 2) + (r & 3)) * kHeadDim] = (__bf16)(acc[r] * scale);
+        for (int r = 0; r < 16; ++r) v[r] = acc[r] * scale;
+        store_pairs(dst, kHeadDim, v);
       } else if (group == 2) {
         // V^T keys of a 32-key tile in the S^T accumulator's register order
         // (within each 16-key block: keys 0-3, 8-11, 4-7, 12-15): this lane's
@@ -206,9 +226,10 @@ __global__ __launch_bounds__(Bf16ProjTraits<MODE>::kWaves * 64) void projection_
       } else {
         // gate rows are padded to np: the tile is always stored whole
         __bf16* dst = a.gs + ((int64_t)i * a.np + j0) * kHidden + col_w;
+        f32x16 v;
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          dst[(8 * (r >> 2) + (r & 3)) * kHidden] = (__bf16)sigmoidf_(acc[r] + col_bias);
+        for (int r = 0; r < 16; ++r) v[r] = sigmoidf_(acc[r] + col_bias);
+        store_pairs(dst, kHidden, v);
       }
     } else {
       const bool full = (tile % tiles_j + 1) * kRows <= a.rows_j;
