@@ -264,17 +264,24 @@ __global__ __launch_bounds__(Bf16ProjTraits<MODE>::kWaves * 64) void projection_
   int next = tile + (int)gridDim.x;
   if (next < ntiles) fetch(next);
   __syncthreads();
+  // A tile's results are stored one iteration late, right after the next
+  // tile's rows are staged: loads and stores share one counter, and the
+  // wait for the staged rows' loads then finds the stores a full iteration
+  // old instead of waiting for their completion.
+  f32x16 acc_prev = {};
+  int prev_tile = -1;
   for (int buf = 0; tile < ntiles; buf ^= 1) {
     const f32x16 acc = mfma_tile(buf);
-    if (next < ntiles) {
-      stage_rows(next, buf ^ 1);
-      if (next + (int)gridDim.x < ntiles) fetch(next + gridDim.x);
-    }
-    epilogue(tile, acc);
+    if (next < ntiles) stage_rows(next, buf ^ 1);
+    if (prev_tile >= 0) epilogue(prev_tile, acc_prev);
+    if (next < ntiles && next + (int)gridDim.x < ntiles) fetch(next + gridDim.x);
+    acc_prev = acc;
+    prev_tile = tile;
     __syncthreads();
     tile = next;
     next += gridDim.x;
   }
+  if (prev_tile >= 0) epilogue(prev_tile, acc_prev);
 }
 
 template <int MODE>
