@@ -212,10 +212,14 @@ __global__ __launch_bounds__(Bf16ProjTraits<MODE>::kWaves * 64) void projection_
         for (int r = 0; r < 16; ++r) v[r] = acc[r] * scale;
         store_pairs(dst, kHeadDim, v);
       } else if (group == 2) {
-        // V^T keys of a 32-key tile in the S^T accumulator's register order
-        // (within each 16-key block: keys 0-3, 8-11, 4-7, 12-15): this lane's
-        // 4-key group g = 2 rr + half (keys 4 g + e) goes to position pos + e.
-        __bf16* dst = a.vt + (bh * kHeadDim + l32) * a.np + (tile % tiles_j) * kRows;
+        // V^T tile-major, [np / 32 key tiles][32 channels][32 key positions]
+        // per (i, head), so a tile's 2 KB are contiguous and its stores fill
+        // whole cache lines.  Keys of a tile in the S^T accumulator's
+        // register order (within each 16-key block: keys 0-3, 8-11, 4-7,
+        // 12-15): this lane's 4-key group g = 2 rr + half (keys 4 g + e) goes
+        // to position pos + e.
+        __bf16* dst = a.vt + bh * a.np * kHeadDim + (int64_t)(tile % tiles_j) * (kRows * kHeadDim) +
+                      l32 * kRows;
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int g = 2 * rr + half;
@@ -372,7 +376,7 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
   const int qt32 = (j0 >> 5) + w;
   const int last = nkt - 1;
 
-  // Per-work-group buffer descriptors: K [np][32], V^T [32][np] of (b, h);
+  // Per-work-group buffer descriptors: K [np][32], V^T [np / 32][32][32] of (b, h);
   // the wave's bias fragments (h, qt32, all key tiles), 2 KB each.
   const int64_t bh = (int64_t)b * kHeads + h;
   const int64_t slice = (int64_t)a.np * kHeadDim;
@@ -384,9 +388,9 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
   // from that row's chunk (l % 4) ^ swz(row) (swz(r + 16) == swz(r)).
   const int crow = 16 * (w & 1) + (lane >> 2);
   const int cchunk = (lane & 3) ^ swz(lane >> 2);
-  const __bf16* csrc = w < 2 ? a.k + bh * slice + crow * kHeadDim + 8 * cchunk
-                             : a.v + bh * slice + (int64_t)crow * a.np + 8 * cchunk;
-  const int64_t ctile = w < 2 ? kBk * kHeadDim : kBk;  // elements from tile t to t + 1
+  // K rows and V^T tiles are both 2 KB blocks per 32-key tile, rows of 64 bytes.
+  const __bf16* csrc = (w < 2 ? a.k : a.v) + bh * slice + crow * kHeadDim + 8 * cchunk;
+  const int64_t ctile = kBk * kHeadDim;  // elements from tile t to t + 1
   auto dma = [&](int t, int stage) {
     lds_dma16(csrc + t * ctile, ring + stage * kStageBytesB + (w >> 1) * kTileBytesB + (w & 1) * 1024);
   };
