@@ -125,8 +125,9 @@ __global__ __launch_bounds__(Bf16ProjTraits<MODE>::kWaves * 64) void projection_
         const int row = idx >> 4;
         const int c8 = (idx & 15) * 8;
         const int j = j0 + row;
+        const int64_t c = a.xs_h != 0 ? (c8 >> 5) * a.xs_h + (c8 & 31) : c8;
         stage_vec[t] = (idx < kVecs && j < a.rows_j)
-                           ? *(const bf16x8*)(a.x + (int64_t)i * a.xs_i + (int64_t)j * a.xs_j + c8)
+                           ? *(const bf16x8*)(a.x + (int64_t)i * a.xs_i + (int64_t)j * a.xs_j + c)
                            : zero8;
       }
     }
@@ -639,7 +640,9 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
       const int c = 8 * rr + 4 * half;
       const int64_t col = h * kHeadDim + c;
       const bf16x4 g = *(const bf16x4*)(a.gate + ((int64_t)b * a.np + jq) * kHidden + col);
-      *(bf16x4*)(a.out + ((int64_t)b * a.n + jq) * kHidden + col) = bf16x4{(__bf16)(o[4 * rr + 0] / l_tot * (float)g.x),
+      // head-major gated output [4][batch][n][32]: a work-group's 128 queries
+      // of one head are 8 KB contiguous, so its stores fill whole cache lines
+      *(bf16x4*)(a.out + (((int64_t)h * a.batch + b) * a.n + jq) * kHeadDim + c) = bf16x4{(__bf16)(o[4 * rr + 0] / l_tot * (float)g.x),
                                        (__bf16)(o[4 * rr + 1] / l_tot * (float)g.y),
                                        (__bf16)(o[4 * rr + 2] / l_tot * (float)g.z),
                                        (__bf16)(o[4 * rr + 3] / l_tot * (float)g.w)};

@@ -30,7 +30,8 @@ size_t elem_bytes(int dtype) { return dtype == FPX_BF16 ? 2 : 4; }
 
 // Workspace segments of the block, all 256-byte aligned, element size e
 // (4 for FPX_F32, 2 for FPX_BF16; the mask bias is always float):
-//   qh, kh [n][4][np][32]; vt [n][4][32][np]; gs [n][np][128]; og [n][n][128];
+//   qh, kh [n][4][np][32]; vt [n][4][32][np] (BF16: [n][4][np / 32][32][32],
+//   tile-major); gs [n][np][128]; og [n][n][128] (BF16: head-major [4][n][n][32]);
 //   tri_bias [4][np][np] (FP32: fragment order, twice: as is and scaled by
 //   log2(e); BF16: bias_frag_index_bf16, once); mbias [n][np] float;
 //   tile flags [n][kTileFlagParts * kTileFlagWords] uint32, then the
@@ -128,9 +129,10 @@ int finish_stage(int dtype, const void* w_o, const void* b_o, int n, int ending,
   const int64_t os_j = ending ? dz_stride0 : dz_stride1;
   if (dtype == FPX_BF16) {
     fpx::Bf16ProjArgs o{};
-    o.x = as<__bf16>(w.og);
-    o.xs_i = (int64_t)n * fpx::kHidden;
-    o.xs_j = fpx::kHidden;
+    o.x = as<__bf16>(w.og);  // head-major [4][n][n][32]
+    o.xs_i = (int64_t)n * fpx::kHeadDim;
+    o.xs_j = fpx::kHeadDim;
+    o.xs_h = (int64_t)n * n * fpx::kHeadDim;
     o.rows_i = n;
     o.rows_j = n;
     o.span_j = n;

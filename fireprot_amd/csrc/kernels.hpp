@@ -231,6 +231,7 @@ struct Bf16ProjArgs {
   const __bf16* x;
   int64_t xs_i;
   int64_t xs_j;
+  int64_t xs_h;  // finish: elements between the heads' 32-channel parts of a row (0: adjacent)
   int rows_i;
   int rows_j;
   int span_j;
