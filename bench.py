@@ -810,6 +810,29 @@ def main() -> int:
                                                   out_s.stride(1), ws.data_ptr(), ws_bytes,
                                                   sptr), "finish")
 
+        # One block call at a time (starting node, the module's entry with
+        # its output and workspace passed in), each bracketed by its own HIP
+        # events: median and p95 over 20 calls, the reference benchmark's
+        # per-call statistics.
+        def one_block():
+            block.triangle_attention_block(z, mask, weights, ending=False, out=out_s, workspace=ws)
+
+        per_call = []
+        for _ in range(20):
+            c0 = torch.cuda.Event(enable_timing=True)
+            c1 = torch.cuda.Event(enable_timing=True)
+            c0.record(stream)
+            one_block()
+            c1.record(stream)
+            c1.synchronize()
+            per_call.append(c0.elapsed_time(c1))
+        per_call.sort()
+        block_call = {"calls": len(per_call), "median_ms": round(per_call[len(per_call) // 2], 4),
+                      "p95_ms": round(per_call[int(0.95 * (len(per_call) - 1) + 0.5)], 4),
+                      "min_ms": round(per_call[0], 4)}
+        log(f"single block call (start): median {block_call['median_ms']:.3f} ms, "
+            f"p95 {block_call['p95_ms']:.3f} ms")
+
         stages = {}
         for name, fn in (("prepare", prepare), ("attend", attend), ("finish", finish)):
             fn()
@@ -891,6 +914,7 @@ def main() -> int:
             "block_peak_frac": round(value / peak, 4),
             "step_flop": step_flop,
             "stage_ms_start_node": {k: round(v, 4) for k, v in stages.items()},
+            "block_call_start_node": block_call,
         },
         "roofline": roofline,
         "cpu_baseline": None,

@@ -214,9 +214,10 @@ StridedWorkspace strided_workspace(int batch, int n) {
   return w;
 }
 
-// Workspace of fpx_tri_mul, 256-byte aligned segments: a and b channel-major
-// [128][np][np] float; x blocked [n][np / 32][128][32] float; the row maxima
-// of a and b [2][128][np] uint32.
+// Workspace of fpx_tri_mul, 256-byte aligned segments: a and b, 128 np^2
+// floats each (channel-blocked [8][np / 32][np][16][32] on the fp16-plane
+// path, channel-major [128][np][np] on the FP32 one); x blocked
+// [n][np / 32][128][32] float; the row maxima of a and b [2][128][np] uint32.
 struct TriMulWorkspace {
   size_t pa, pb, x, rowmax, total;
 };

@@ -54,7 +54,7 @@ struct GatedArgs {
   float* out[4];         // per slice, see gated_split_kernel
   int np;                // kGatedTriMul: packed extent of the output
   uint32_t* rowmax;      // kGatedTriMul: [slice][128][np] max |out| over k per (channel, row),
-                         // float bits by atomic max (zeroed before the launch); null: none
+                         // float bits; null: none
   uint32_t* out_max;     // kGatedTransition: max |out| of the launch, float bits by atomic
                          // max (zeroed before the launch); null: none
 };
@@ -74,11 +74,18 @@ constexpr int kGatedWaves = 8;
 constexpr int kGatedRows = 32;
 constexpr int kGatedPlaneRow = kChannels + 8;  // bf16 per LDS row: 272 bytes
 
-// Outputs: kGatedTriMul writes out[slice][(c * np + r) * np + k] for all
-// k < span_k (0 past rows_k), channel-major with keys contiguous, the
-// contraction's operand layout.  kGatedTransition writes
-// out[slice][(r * rows_k + k) * 512 + c] for k < rows_k (h rows, the slice's
-// 128 columns of the 512).
+// Outputs: kGatedTriMul writes, for all k < span_k (0 past rows_k), the
+// channel-blocked layout
+//   out[slice][(((c / 16) * (span_k / 32) + k / 32) * np + r) * 512 + (c % 16) * 32 + k % 32]
+// (np = a.np >= rows_r): a wave's 16 channels x 32 keys of a tile are one
+// contiguous 2 KB block, the blocks of consecutive rows r are adjacent, and
+// channel c's row r is 32-key runs np * 512 floats apart, the contraction's
+// operand layout.  Each work-group owns whole rows r (first, first +
+// streams, ...), so the row maxima are plain stores, and the work-groups
+// in flight write one run of adjacent blocks per channel group.
+// kGatedTransition writes out[slice][(r * rows_k + k) * 512 + c] for
+// k < rows_k (h rows, the slice's 128 columns of the 512); its work-groups
+// take tiles first, first + streams, ... of the row-major tile order.
 template <int MODE>
 __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedArgs a, int tiles_k,
                                                                           int ntiles,
@@ -146,18 +153,31 @@ __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedA
   lnw = ldexp8(lnw, ex);
   lnb = ldexp8(lnb, ex);
 
-  auto origin = [&](int tile, int& r, int& k0) {
-    r = tile / tiles_k;
-    k0 = (tile - r * tiles_k) * kGatedRows;
+  // This work-group's tiles, local index i < count (at least one).
+  int count;
+  if constexpr (MODE == kGatedTriMul)
+    count = tiles_k * ((a.rows_r - first + streams - 1) / streams);
+  else
+    count = (ntiles - first + streams - 1) / streams;
+  auto origin = [&](int i, int& r, int& k0) {
+    if constexpr (MODE == kGatedTriMul) {
+      const int q = i / tiles_k;
+      r = first + streams * q;
+      k0 = (i - q * tiles_k) * kGatedRows;
+    } else {
+      const int tile = first + streams * i;
+      r = tile / tiles_k;
+      k0 = (tile - r * tiles_k) * kGatedRows;
+    }
   };
 
   // Row loads with no branches on the data path (tile clamped to the last
   // one, row to the last valid row); the mask is 0 past rows_k.
   f32x8 stage_ln;
   float stage_m = 0.f;
-  auto fetch = [&](int tile) {
+  auto fetch = [&](int i) {
     int r, k0;
-    origin(tile < ntiles ? tile : ntiles - 1, r, k0);
+    origin(i < count ? i : count - 1, r, k0);
     const int kk = k0 + lrow;
     const int k = min(kk, a.rows_k - 1);
     const float* src = a.x + (int64_t)r * a.xs_r + (int64_t)k * a.xs_k + 8 * c16;
@@ -193,10 +213,10 @@ __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedA
     *(bf16x8*)&xs[buf][1][lrow][8 * c16] = lo;
   };
 
-  auto consume = [&](int tile_index) {  // tile_index: k of the staged tile T_k
+  auto consume = [&](int i) {  // i: local index of the staged tile
     *(f32x8*)&raw[lrow][8 * c16] = stage_ln;
     if constexpr (MODE == kGatedTriMul) {
-      if (c16 == 0) ms[tile_index & 3][lrow] = stage_m;
+      if (c16 == 0) ms[i & 3][lrow] = stage_m;
     }
   };
 
@@ -225,13 +245,14 @@ __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedA
     return r;
   };
 
-  // Result of tile `tile` (the k-th of this stream): lanes of even 16-lane
+  // Result of local tile i: lanes of even 16-lane
   // rows hold the value channel, odd rows the gate channel.  Swapping
   // register r with r + 8 across the row pair leaves every lane the value
   // and gate of its channel for registers r + (odd ? 8 : 0), r < 8, i.e.
   // tile rows 8 rr + 4 half + e for rr = (odd ? 2 : 0) + r / 4, e = r % 4.
   float out_max = 0.f;  // kGatedTransition: running max |value| stored
-  auto store = [&](const f32x16& res, int tile, int k) {
+  float row_max = 0.f;  // kGatedTriMul: max |value| of this lane's channel over the row so far
+  auto store = [&](const f32x16& res, int i) {
     f32x8 val;
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
@@ -247,21 +268,24 @@ __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedA
       if constexpr (MODE == kGatedTriMul) {
         const int row = 8 * ((odd ? 2 : 0) + (r >> 2)) + 4 * half + (r & 3);
         // native order: a = mask; a = a * sigmoid(g); a = a * p
-        val[r] = (ms[k & 3][row] * sigmoidf_(g + bg)) * p;
+        val[r] = (ms[i & 3][row] * sigmoidf_(g + bg)) * p;
       } else {
         val[r] = g * sigmoidf_(g) * p;  // silu(a) * b
       }
     }
     int r_out, k0;
-    origin(tile, r_out, k0);
+    origin(i, r_out, k0);
     const int rr0 = odd ? 2 : 0;
     if constexpr (MODE == kGatedTriMul) {
-      if (a.rowmax != nullptr) {
-        // max |value| of the channel over the tile's 32 keys: this lane's 8,
-        // then lanes l ^ 16 (other register half) and l ^ 32 (other rows)
-        float m = 0.f;
 #pragma unroll
-        for (int r = 0; r < 8; ++r) m = __builtin_elementwise_maximum(m, __builtin_fabsf(val[r]));
+      for (int r = 0; r < 8; ++r)
+        row_max = __builtin_elementwise_maximum(row_max, __builtin_fabsf(val[r]));
+      if (k0 + kGatedRows == a.span_k) {
+        // the row's last tile: the channel's max over the row is the max of
+        // this lane's, lane l ^ 16's (other register half) and lane l ^ 32's
+        // (other tile rows)
+        float m = row_max;
+        row_max = 0.f;
         const auto s16 = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, m),
                                                           __builtin_bit_cast(unsigned, m), false, false);
         m = __builtin_elementwise_maximum(__builtin_bit_cast(float, (unsigned)s16[0]),
@@ -270,11 +294,14 @@ __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedA
                                                           __builtin_bit_cast(unsigned, m), false, false);
         m = __builtin_elementwise_maximum(__builtin_bit_cast(float, (unsigned)s32[0]),
                                           __builtin_bit_cast(float, (unsigned)s32[1]));
-        if (!odd && half == 0)
-          atomicMax(&a.rowmax[((int64_t)slice * kChannels + ch) * a.np + r_out],
-                    __builtin_bit_cast(uint32_t, m));
+        if (!odd && half == 0 && a.rowmax != nullptr)
+          a.rowmax[((int64_t)slice * kChannels + ch) * a.np + r_out] =
+              __builtin_bit_cast(uint32_t, m);
       }
-      float* dst = a.out[slice] + ((int64_t)ch * a.np + r_out) * a.np + k0 + 4 * half;
+      // the wave's 2 KB block of the channel-blocked layout
+      float* dst = a.out[slice] +
+                   (((int64_t)w * tiles_k + k0 / kGatedRows) * a.np + r_out) * 512 +
+                   (l32 & 15) * 32 + 4 * half;
 #pragma unroll
       for (int q = 0; q < 2; ++q)
         *(f32x4*)(dst + 8 * (rr0 + q)) =
@@ -293,13 +320,10 @@ __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedA
   };
 
   const bool lead = w < kGatedWaves / 2;
-  int tile = first;  // first < streams <= ntiles: every work-group has a tile
-  int next = tile + streams;
-  int kidx = 0;      // k of tile T_k
-  fetch(tile);
+  fetch(0);
   {
     int r0, k00;
-    origin(tile, r0, k00);
+    origin(0, r0, k00);
     f32x8 d;
     float rstd;
     ln_stats(stage_ln, d, rstd);
@@ -308,42 +332,41 @@ __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedA
       if (c16 == 0) ms[0][lrow] = stage_m;
     }
   }
-  fetch(next);
+  fetch(1);
   consume(1);
-  fetch(next + streams);
+  fetch(2);
   __syncthreads();
 
   f32x16 res = {};
-  for (int buf = 0; tile < ntiles; buf ^= 1) {
+  int i = 0;
+  for (int buf = 0; i < count; buf ^= 1) {
     if (lead) res = k_steps(buf);
     {
       // The other half: normalise T_{k+1} into the other planes, then the
       // iteration's global accesses (see projection_split_kernel).
-      const bool more = next < ntiles;
+      const bool more = i + 1 < count;
       if (more) {
         int rn, kn0;
-        origin(next, rn, kn0);
+        origin(i + 1, rn, kn0);
         f32x8 d;
         float rstd;
         ln_stats(*(const f32x8*)&raw[lrow][8 * c16], d, rstd);
         stage_split(buf ^ 1, d, rstd, kn0);
       }
       __builtin_amdgcn_sched_barrier(0);
-      consume(kidx + 2);
-      fetch(next + 2 * streams);
+      consume(i + 2);
+      fetch(i + 3);
       if (lead)
-        store(res, tile, kidx);
-      else if (kidx > 0)
-        store(res, tile - streams, kidx - 1);
+        store(res, i);
+      else if (i > 0)
+        store(res, i - 1);
       __builtin_amdgcn_sched_barrier(0);
     }
     if (!lead) res = k_steps(buf);
     __syncthreads();
-    tile = next;
-    next += streams;
-    ++kidx;
+    ++i;
   }
-  if (!lead && kidx > 0) store(res, tile - streams, kidx - 1);
+  if (!lead) store(res, i - 1);
   if (MODE == kGatedTransition && a.out_max != nullptr) {
     // one atomic per wave: the NaN-propagating max of the values it stored
     const float m = wave_max(out_max);
@@ -360,10 +383,13 @@ hipError_t launch_gated_split(const GatedArgs& a, hipStream_t stream) {
   if (ntiles == 0) return hipSuccess;
   if (a.span_k % kGatedRows || a.span_k < a.rows_k || a.rows_k < 1 || ntiles > 0x7fffffffll)
     return hipErrorInvalidValue;
+  if (MODE == kGatedTriMul && a.rows_r > a.np) return hipErrorInvalidValue;
   int64_t cap = (int64_t)device_cu_count() / kSlices;
   if (cap >= 8) cap -= cap % 8;
   if (cap < 1) cap = 1;
-  const int streams = (int)(ntiles < cap ? ntiles : cap);
+  // kGatedTriMul: whole rows per work-group
+  const int64_t units = MODE == kGatedTriMul ? (int64_t)a.rows_r : ntiles;
+  const int streams = (int)(units < cap ? units : cap);
   hipLaunchKernelGGL(gated_split_kernel<MODE>, dim3(streams * kSlices), dim3(kGatedWaves * 64), 0,
                      stream, a, tiles_k, (int)ntiles, streams);
   return hipGetLastError();

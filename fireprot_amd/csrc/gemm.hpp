@@ -122,11 +122,14 @@ constexpr int kSplitRow = kSplitK + 8;
 // B by 2^eb[r] (ea, eb: 128 per-row exponents, plane_exp of each row's max
 // |value| over all keys, in LDS), so acc[rb][cb] comes out scaled by
 // 2^(ea[row] + eb[col]) for the caller to undo with ldexp.  Three terms (hi
-// hi, hi lo, lo hi) per 16-key stage: 12 MFMAs per wave and stage.
+// hi, hi lo, lo hi) per 16-key stage: 12 MFMAs per wave and stage.  A row's
+// keys are runs of 32 contiguous values, kblock floats apart (32: the whole
+// row contiguous); nk (16-key stages) is even when kblock != 32.
 typedef __bf16 F16Stage[2][kGemmTile][kSplitRow];  // planes hi, lo (fp16 bits)
 
 __device__ __forceinline__ void gemm_nt_128_f16(const float* a, int64_t lda, const float* b,
-                                                int64_t ldb, int nk, F16Stage* As, F16Stage* Bs,
+                                                int64_t ldb, int64_t kblock, int nk,
+                                                F16Stage* As, F16Stage* Bs,
                                                 const int* ea, const int* eb,
                                                 f32x16 (&acc)[2][2]) {
   const int tid = threadIdx.x;
@@ -137,8 +140,6 @@ __device__ __forceinline__ void gemm_nt_128_f16(const float* a, int64_t lda, con
   const int wi = (w >> 1) * 64;
   const int wj = (w & 1) * 64;
 
-  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a, (127 * lda + kSplitK * nk) * 4);
-  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(b, (127 * ldb + kSplitK * nk) * 4);
   // Thread (row = tid / 4 + 64 u, keys 4 (tid % 4) .. +3) of each stage.
   const int lrow = tid >> 2;
   const int lc4 = (tid & 3) * 4;
@@ -151,7 +152,11 @@ __device__ __forceinline__ void gemm_nt_128_f16(const float* a, int64_t lda, con
 
   f32x4 ga[2], gb[2];
   auto load = [&](int kt) {
-    const uint32_t s = (uint32_t)kt * (kSplitK * 4);
+    // one buffer resource per 32-key run: the 32-bit offsets span 128 rows
+    const int64_t run = (int64_t)(kt >> 1) * kblock;
+    const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a + run, (127 * lda + 2 * kSplitK) * 4);
+    const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(b + run, (127 * ldb + 2 * kSplitK) * 4);
+    const uint32_t s = (uint32_t)((kt & 1) * kSplitK * 4);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       ga[u] = buffer_load_f4(ra, va + u * pa, s);

@@ -273,9 +273,11 @@ hipError_t launch_attention_bf16(const Bf16AttnArgs& args, hipStream_t stream);
 
 // -------------------------------------------------- triangle multiplication
 // Outgoing / incoming triangle multiplicative update, c_z = c_hidden = 128
-// (trimul.hip).  Workspace roles: a and b channel-major [128][np][np] (rows
-// of the contraction frame, keys contiguous; rows >= n unused, keys >= n
-// zero), x blocked [n][np / 32][128][32].  np is a multiple of 128.
+// (trimul.hip).  Workspace roles: a and b, 128 np^2 floats each (rows of the
+// contraction frame; rows >= n unused, keys >= n zero): channel-blocked
+// [8][np / 32][np][16][32] on the fp16-plane path, channel-major
+// [128][np][np] on the FP32 one; x blocked [n][np / 32][128][32].  np is a
+// multiple of 128.
 struct TriMulArgs {
   const float* z;
   int64_t zs_i;

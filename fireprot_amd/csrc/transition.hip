@@ -157,7 +157,8 @@ __global__ __launch_bounds__(256, 2) void transition_down_kernel(TransitionArgs 
     if (t < kGemmTile) ea[t] = ex;
     else eb[t - kGemmTile] = plane_exp(__builtin_bit_cast(float, a.maxima[1 + t - kGemmTile]));
     __syncthreads();
-    gemm_nt_128_f16(a.h + r0 * kHid, kHid, a.w_o, kHid, kHid / kSplitK, As, Bs, ea, eb, acc);
+    gemm_nt_128_f16(a.h + r0 * kHid, kHid, a.w_o, kHid, 32, kHid / kSplitK, As, Bs, ea, eb,
+                    acc);
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll

@@ -11,15 +11,19 @@
 // z[k, r] for the incoming one, so both directions are one kernel chain; the
 // incoming read of z^T goes through strides, with no transposed copy.
 //
-// Three launches:
-//   trimul_project_kernel  LN_in, the four 128x128 projections, sigmoid gates
-//                          and the mask; writes a and b channel-major
-//                          ([128][np rows][np keys], keys contiguous), the
-//                          operand layout of the contraction
+// Three launches (the default fp16-plane kernels; the FP32-matrix-core
+// ones in brackets):
+//   gated_split_kernel<kGatedTriMul> [trimul_project_kernel]
+//                          LN_in, the four 128x128 projections, sigmoid gates
+//                          and the mask; writes a and b channel-blocked (each
+//                          channel's rows as 32-key runs, gated_split.hpp)
+//                          with each (channel, row)'s max |value| [channel-
+//                          major [128][np rows][np keys], keys contiguous]
 //   trimul_contract_kernel x_c = A_c B_c^T for the 128 channels: a batched
-//                          GEMM on 128 x 128 output tiles, 32-key stages
+//                          GEMM on 128 x 128 output tiles, key stages
 //                          double-buffered in LDS, XCD-aware tile order
-//   trimul_finish_kernel   LN_out(x) W_z^T and LN_in(z) W_g^T for 32 pairs
+//   trimul_finish_split_kernel [trimul_finish_kernel]
+//                          LN_out(x) W_z^T and LN_in(z) W_g^T for 32 pairs
 //                          per tile, the sigmoid gate and the in-place write
 #include "common.hpp"
 #include "gated_split.hpp"
@@ -154,20 +158,17 @@ __global__ __launch_bounds__(kProjWaves * 64) void trimul_project_kernel(TriMulA
   }
 }
 
-// Clears `words` 32-bit words (a multiple of 4) with vector stores.
-__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int64_t words) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  if (4 * i < words) reinterpret_cast<u32x4*>(p)[i] = u32x4{0u, 0u, 0u, 0u};
-}
-
 // ----------------------------------------------------------- contraction
 // One work-group = (channel c, 128 rows i, 128 columns j) of x_c = A_c B_c^T
 // (gemm_nt_128 over the np keys).  Work-groups of one channel are consecutive
 // in the logical order, and xcd_remap gives each XCD a contiguous range, so
 // the A and B row panels a range touches stay in that XCD's L2.
 // kSplit: gemm_nt_128_f16 (16-bit matrix cores, scaled fp16 planes), with
-// each row's exponent from the row maxima the projection recorded.
+// each row's exponent from the row maxima the projection recorded, on the
+// channel-blocked a and b of gated_split_kernel<kGatedTriMul> (channel c's
+// row r at ((c / 16) np / 32 np + r) 512 + (c % 16) 32, rows 512 floats
+// apart, 32-key runs np * 512 floats apart); the FP32 path reads a and b
+// channel-major ([128][np][np]).
 template <bool kSplit>
 __global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const float* __restrict__ pa,
                                                                  const float* __restrict__ pb,
@@ -199,8 +200,10 @@ __global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const float* __
     const uint32_t* rm = rowmax + ((int64_t)(t >> 7) * kChannels + c) * np + ((t >> 7) ? j0 : i0);
     (t >> 7 ? eb : ea)[t & 127] = plane_exp(__builtin_bit_cast(float, rm[t & 127]));
     __syncthreads();
-    gemm_nt_128_f16(pa + c * slice + (int64_t)i0 * np, np, pb + c * slice + (int64_t)j0 * np,
-                    np, np / kSplitK, As, Bs, ea, eb, acc);
+    const int64_t run = 512 * (int64_t)np;  // floats between a row's 32-key runs
+    const int64_t cbase = (int64_t)(c >> 4) * (np / 32) * run + (c & 15) * 32;
+    gemm_nt_128_f16(pa + cbase + 512 * (int64_t)i0, 512, pb + cbase + 512 * (int64_t)j0, 512,
+                    run, np / kSplitK, As, Bs, ea, eb, acc);
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
@@ -673,11 +676,6 @@ hipError_t launch_trimul(const TriMulArgs& a, hipStream_t stream) {
     g.np = a.np;
     g.rowmax = a.rowmax;
     if (a.rowmax == nullptr) return hipErrorInvalidValue;
-    const int64_t words = 2 * (int64_t)kChannels * a.np;
-    hipLaunchKernelGGL(zero_words_kernel, dim3((uint32_t)((words / 4 + 255) / 256)), dim3(256), 0,
-                       stream, a.rowmax, words);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
     e = launch_gated_split<kGatedTriMul>(g, stream);
   }
   if (e != hipSuccess) return e;
