@@ -9,10 +9,12 @@ registry.  The candidate runs the whole update as one C-ABI call,
 ``fpx_tri_mul`` (include/fireprot_amd.h):
 
 * LayerNorm_in, the four gated projections and the mask are fused and write
-  ``a``, ``b`` channel-major (the reference's sigmoid-pack step,
-  triangle_multiplication.py:301-316);
-* the per-channel contraction is a hand-written batched FP32-MFMA GEMM (the
-  reference's library BMM, ``packed_bmm``, :318);
+  ``a``, ``b`` channel-blocked, one contiguous 2 KB block per wave and
+  32-key tile, with each (channel, row)'s max |value| (the reference's
+  sigmoid-pack step, triangle_multiplication.py:301-316);
+* the per-channel contraction is a hand-written batched GEMM on the 16-bit
+  matrix cores with FP32 accuracy (power-of-two scaled fp16 hi/lo planes,
+  three terms; the reference's library BMM, ``packed_bmm``, :318);
 * LayerNorm_out, ``linear_z``, ``sigmoid(linear_g(LN_in z))`` and the
   residual are fused into one epilogue kernel (:321-339), which writes into
   ``z`` in place.
