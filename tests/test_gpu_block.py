@@ -2,10 +2,10 @@
 
 Bar (FP32): max-abs 1e-4 and rel 1e-4 elementwise against the native-order
 oracle on identical seeded inputs; NaN positions must agree.  Small and
-medium sizes compare every element; the N=1000 and N=1536 configurations
-compare a seeded subset of outer rows (rows are independent, so the oracle
-computes only those) and check size-independent properties on the full
-output.
+medium sizes compare every element; the N=1000, N=1536 and N=4096 (the
+largest the C ABI accepts) cases compare a seeded subset of outer rows (rows
+are independent, so the oracle computes only those) and check
+size-independent properties on the full output.
 """
 from __future__ import annotations
 
@@ -111,6 +111,49 @@ def test_long_configs_row_subset_and_transpose_identity(key):
     region_reports(f"{cfg.name} end", end_rows, exp_end, cfg.valid, rows)
     assert_f32_parity(f"{cfg.name} start rows", start_rows, exp_start)
     assert_f32_parity(f"{cfg.name} end rows", end_rows, exp_end)
+
+
+@pytest.mark.timeout(600)
+def test_maximum_n4096_row_subset_and_transpose_identity():
+    """The largest pair size the C ABI accepts (N = 4096: 128 key tiles, the
+    tile-flag words full, [N][N][128] tensors of 2^31 elements), with a
+    padding tail of 296 residues; both nodes on a few outer rows against the
+    oracle, and the ending node equal to T(start(T(z))) bit for bit.  z is
+    drawn on the GPU (a seeded device generator) and copied to the host for
+    the oracle."""
+    n, valid = 4096, 3800
+    print(f"case maximum n={n} valid={valid}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(419 + n)
+    zc = torch.randn(n, n, 128, generator=g, device="cuda")
+    mc = workloads.make_mask(n, valid).cuda()
+    w = workloads.make_weights()
+    weights = hip_weights(w)
+    gr = torch.Generator().manual_seed(n)
+    rows = torch.tensor(sorted({0, valid - 1, valid, n - 1,
+                                int(torch.randint(0, valid, (1,), generator=gr))}))
+    with torch.inference_mode():
+        start = hip_block.triangle_attention_block(zc, mc, weights, ending=False)
+        end = hip_block.triangle_attention_block(zc, mc, weights, ending=True)
+        start_rows = start[rows.cuda()].cpu()
+        end_rows = end.transpose(0, 1)[rows.cuda()].cpu()
+        assert torch.isfinite(start).all() and torch.isfinite(end).all()
+        del start
+        zt = zc.transpose(0, 1).contiguous()
+        end_ref = hip_block.triangle_attention_block(zt, mc.t().contiguous(), weights,
+                                                     ending=False).transpose(0, 1)
+        torch.cuda.synchronize()
+        assert torch.equal(end, end_ref), "ending node differs from T(start(T(z)))"
+    z = zc.cpu()
+    mask = mc.cpu()
+    del zc, zt, end, end_ref
+    torch.cuda.empty_cache()
+    params = oracle_params(w)
+    exp_start = oracle.block(z, mask, params, ending=False, outer_rows=rows)
+    exp_end = oracle.block(z, mask, params, ending=True, outer_rows=rows)
+    region_reports(f"n={n} start", start_rows, exp_start, valid, rows)
+    region_reports(f"n={n} end", end_rows, exp_end, valid, rows)
+    assert_f32_parity(f"n={n} start rows", start_rows, exp_start)
+    assert_f32_parity(f"n={n} end rows", end_rows, exp_end)
 
 
 @pytest.mark.parametrize("ending", [False, True])
