@@ -3,7 +3,8 @@
 Bar (FP32): max-abs 1e-4 and rel 1e-4 elementwise against
 ``oracle.triangle_multiplication`` (native op order) on identical seeded
 inputs; the float64 brute-force fixtures to 2e-5.  Small and medium sizes
-compare every element; N = 1000 and N = 1536 compare a seeded set of rows
+compare every element; N = 1000, 1536 and 4096 (the largest the C ABI
+accepts) compare a seeded set of rows
 against the oracle's row-subset path and check full-size properties: the
 incoming update equals the transposed outgoing update of z^T with the a and b
 branches swapped, repeat runs are bit-identical, in-place and separate
@@ -202,6 +203,45 @@ def test_long_rows_and_direction_identity(n):
                                                                  rows=rows))
     assert_f32_parity(f"n={n} incoming rows", got_in, tm.update(z, m, p, outgoing=False,
                                                                 rows=rows))
+
+
+@pytest.mark.timeout(600)
+def test_maximum_n4096_rows():
+    """N = 4096, the largest size the C ABI accepts (a and b of 2^31 values
+    each): both directions on five rows against the oracle's row-subset path,
+    and a repeat run bit-identical.  z is drawn on the GPU (a seeded device
+    generator) and copied to the host for the oracle."""
+    n = 4096
+    print(f"case trimul maximum n={n}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(419 + n)
+    zc = torch.randn(n, n, 128, generator=g, device="cuda")
+    m = _mask(n, "tail")
+    mc = m.cuda()
+    w = _weights()
+    wt = _hip_weights(w)
+    valid = int(m[0].sum())
+    gr = torch.Generator().manual_seed(n)
+    rows = torch.tensor(sorted({0, valid - 1, valid, n - 1,
+                                int(torch.randint(0, valid, (1,), generator=gr))}))
+    got = {}
+    with torch.inference_mode():
+        for outgoing in (True, False):
+            out = htm.triangle_multiplication(zc, mc, wt, outgoing=outgoing)
+            assert torch.isfinite(out).all()
+            got[outgoing] = out[rows.cuda()].cpu()
+            if not outgoing:
+                again = htm.triangle_multiplication(zc, mc, wt, outgoing=False)
+                torch.cuda.synchronize()
+                assert torch.equal(out, again), "not deterministic"
+                del again
+            del out
+    z = zc.cpu()
+    del zc
+    torch.cuda.empty_cache()
+    p = _params(w)
+    for outgoing in (True, False):
+        assert_f32_parity(f"n={n} outgoing={outgoing} rows", got[outgoing],
+                          tm.update(z, m, p, outgoing=outgoing, rows=rows))
 
 
 class _Module(torch.nn.Module):
