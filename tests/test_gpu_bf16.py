@@ -86,6 +86,43 @@ def test_c5_n2048_row_subset_transpose_and_determinism():
         assert rel <= BF16_REL
 
 
+@pytest.mark.timeout(600)
+def test_bf16_maximum_n4096_rows_with_tail():
+    """BF16 storage at N = 4096, the largest size the C ABI accepts, with a
+    padding tail of 296 residues: five outer rows per node against the
+    native bf16 ops, the ending node equal to T(start(T(z))) bit for bit.
+    z is drawn on the GPU (a seeded device generator)."""
+    n, valid = 4096, 3800
+    print(f"case bf16 maximum n={n} valid={valid}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(419 + n)
+    zc = torch.randn(n, n, 128, generator=g, device="cuda").to(torch.bfloat16)
+    mask = workloads.make_mask(n, valid)
+    mc = mask.cuda()
+    w = workloads.make_weights()
+    weights = _weights(w)
+    rows = torch.tensor([0, 1777, valid - 1, valid, n - 1])
+    with torch.inference_mode():
+        start = hip_block.triangle_attention_block(zc, mc, weights, ending=False)
+        end = hip_block.triangle_attention_block(zc, mc, weights, ending=True)
+        start_rows = start[rows.cuda()].cpu()
+        end_rows = end.transpose(0, 1)[rows.cuda()].cpu()
+        del start
+        zt = zc.transpose(0, 1).contiguous()
+        end_ref = hip_block.triangle_attention_block(zt, mc.t().contiguous(), weights,
+                                                     ending=False).transpose(0, 1)
+        torch.cuda.synchronize()
+        assert torch.equal(end, end_ref), "ending node differs from T(start(T(z)))"
+    z = zc.float().cpu()
+    del zc, zt, end, end_ref
+    torch.cuda.empty_cache()
+    params = oracle.BlockParams(**w)
+    for name, actual, ending in (("start", start_rows, False), ("end", end_rows, True)):
+        native = oracle.block_bf16(z, mask, params, ending=ending, outer_rows=rows)
+        rel = _rel(actual, native)
+        print(f"n={n} {name} rows: rel vs native-bf16 {rel:.2e}", flush=True)
+        assert rel <= BF16_REL
+
+
 def test_bf16_pair_step_residual_in_place():
     """The Pairformer's two residual updates in bf16, against the native bf16
     ops (z is rounded after each += dz, as the native in-place add does)."""
