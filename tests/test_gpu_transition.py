@@ -5,7 +5,7 @@ Bar (FP32): elementwise max-abs 1e-4 and rel 1e-4 against
 float64 brute-force fixtures to 1e-6 of their largest value.  Covers partial
 row tiles, strided 3-D and flat inputs, the in-place residual form, the
 N = 1536 pair stack (sampled rows against the oracle, repeat runs
-bit-identical), registry dispatch and the native fallback (the reference's
+bit-identical), the N = 4096 stack in place, registry dispatch and the native fallback (the reference's
 tests/backends/test_recycle.py and tests/operators/test_long1536_epilogues.py
 cover the same surface).
 """
@@ -96,6 +96,29 @@ def test_n1536_rows_and_determinism():
         got = first[rows.cuda()].cpu()
     del first, second
     assert_f32_parity("n1536 rows", got, tr.transition(z[rows], _params(w)))
+
+
+@pytest.mark.timeout(600)
+def test_maximum_n4096_rows_in_place():
+    """N = 4096, the largest pair size (16.8 M rows, a 34 GB hidden layer in
+    the workspace): the in-place residual update on five pair rows against
+    the oracle.  z is drawn on the GPU (a seeded device generator)."""
+    n = 4096
+    print(f"case transition maximum n={n}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(419 + n)
+    zc = torch.randn(n, n, 128, generator=g, device="cuda")
+    rows = torch.tensor([0, 1, 2047, 3000, n - 1])
+    z_rows = zc[rows.cuda()].cpu()
+    w = workloads.make_transition_weights()
+    with torch.inference_mode():
+        out = htr.transition(zc, _hip(w), out=zc, accumulate=True)
+        torch.cuda.synchronize()
+        assert out.data_ptr() == zc.data_ptr()
+        assert torch.isfinite(zc).all()
+        got = zc[rows.cuda()].cpu()
+    del zc, out
+    torch.cuda.empty_cache()
+    assert_f32_parity(f"n={n} rows in place", got, z_rows + tr.transition(z_rows, _params(w)))
 
 
 def _module(w):
