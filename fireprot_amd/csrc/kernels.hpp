@@ -333,9 +333,14 @@ struct TransitionArgs {
   const float* w_b;   // [512][128]
   const float* w_o;   // [128][512]
   float* h;
-  // fp16-plane path: [0] max |h| of the launch, [1 + c] max |W_o[c]|, as
-  // float bits (129 words)
+  // FP32-matrix-core path: [0] max |h| of the launch, [1 + c] max |W_o[c]|,
+  // as float bits (129 words)
   uint32_t* maxima;
+  // fp16-plane (fused) path: the 16 chunks' weight planes (fp16 bits, 768 KB),
+  // the folded biases [2][512] and the plane exponents (e_x, e_w, e_o, e_h)
+  __bf16* planes;
+  float* fbias;
+  int* exps;
   float* out;
   int64_t os_i;
   int64_t os_j;

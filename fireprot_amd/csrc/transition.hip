@@ -12,6 +12,10 @@
 // transition_down_kernel: one 128-row tile of h W_o^T per work-group on the
 //   shared gemm_nt_128 mainloop (K = 512), with the strided, optionally
 //   accumulated store.
+// Those two (FP32 matrix cores; h through HBM) serve FPX_ATTENTION_MFMA=f32.
+// The default path is one fused kernel on the 16-bit matrix cores, with h
+// never leaving the registers (transition_fused_kernel below).
+#include "attn_common.hpp"
 #include "common.hpp"
 #include "gated_split.hpp"
 #include "gemm.hpp"
@@ -191,6 +195,286 @@ __global__ __launch_bounds__(256, 2) void transition_down_kernel(TransitionArgs 
   }
 }
 
+
+// ------------------------------------------------------- fused, fp16 cores
+// out = x + silu(y Wa'^T + ba) * (y Wb'^T + bb) Wo^T with y = (x - mean)
+// rstd, the LayerNorm affine folded into the weights (W' = W diag(ln_w),
+// b = W ln_b), all three products on v_mfma_f32_32x32x16_f16 with
+// power-of-two scaled fp16 (hi, lo) planes and three terms (FP32 accuracy).
+// A wave owns 32 pair rows: its y^T planes (the B operand, 64 VGPRs) stay in
+// registers while the 512 hidden channels pass in 16 chunks of 32; per chunk
+//   value^T, gate^T [32 hidden][32 rows] = W' y^T      (48 MFMAs)
+//   h = silu(gate) * value, as planes scaled by 2^e_h  (the A operand: a
+//       lane holds its row's 16 hidden values, and W_o's columns are stored
+//       in that order)
+//   out [32 rows][128] += h W_o^T                       (24 MFMAs)
+// so h never leaves the registers.  The chunks' weight planes (48 KB each,
+// written once per call by transition_planes_kernel) go from L2 into a
+// double-buffered LDS ring by global_load_lds, shared by the 8 waves (256
+// rows) of a work-group.  Plane scales: y by 2^e_x (|y_c| <= sqrt(128)),
+// W' and W_o by one exponent each (their largest |value|), h by 2^e_h from
+// the bound |h_c| <= max(|g_c|, 0.2785) |v_c| with |g_c| <= sqrt(128)
+// |Wa'_c| + |ba_c| (likewise v), |silu(g)| <= max(|g|, 0.2785).
+constexpr int kFusedWaves = 8;
+constexpr int kFusedRows = 32 * kFusedWaves;               // rows per tile
+constexpr int kChunkHid = 32;
+constexpr int kChunks = kHid / kChunkHid;                  // 16
+constexpr int kUpBlocks = 2 * 8 * 2;                       // [a, b][k step][hi, lo]
+constexpr int kDownBlocks = 4 * 2 * 2;                     // [out block][k step][hi, lo]
+constexpr int kPlaneBlock = 32 * 16;                       // fp16 values of a 1 KB block
+constexpr int kChunkValues = (kUpBlocks + kDownBlocks) * kPlaneBlock;  // 24576 (48 KB)
+constexpr int kChunkBytes = kChunkValues * 2;
+
+// One work-group: the exponents and the folded biases.  exps: e_x, e_w, e_o,
+// e_h; fbias: [2][512] (ba, bb).
+__global__ __launch_bounds__(512) void transition_prep_kernel(TransitionArgs a) {
+  __shared__ float red[3][8];
+  const int c = threadIdx.x;  // hidden channel
+  const float* wa = a.w_a + (int64_t)c * kChannels;
+  const float* wb = a.w_b + (int64_t)c * kChannels;
+  float sa2 = 0.f, sa1 = 0.f, sb2 = 0.f, sb1 = 0.f, mw = 0.f;
+  for (int i = 0; i < kChannels; ++i) {
+    const float g = a.ln_w ? a.ln_w[i] : 1.f;
+    const float b = a.ln_b ? a.ln_b[i] : 0.f;
+    const float ga = g * wa[i], gb = g * wb[i];
+    sa2 = __builtin_fmaf(ga, ga, sa2);
+    sb2 = __builtin_fmaf(gb, gb, sb2);
+    sa1 = __builtin_fmaf(b, wa[i], sa1);
+    sb1 = __builtin_fmaf(b, wb[i], sb1);
+    mw = __builtin_elementwise_maximum(
+        mw, __builtin_elementwise_maximum(__builtin_fabsf(ga), __builtin_fabsf(gb)));
+  }
+  a.fbias[c] = sa1;
+  a.fbias[kHid + c] = sb1;
+  const float bg = __builtin_sqrtf(128.f * sa2) + __builtin_fabsf(sa1);
+  const float bv = __builtin_sqrtf(128.f * sb2) + __builtin_fabsf(sb1);
+  float bh = __builtin_elementwise_maximum(bg, 0.2785f) * bv;
+  float mo = 0.f;
+  if (c < kChannels) {
+    const float* wo = a.w_o + (int64_t)c * kHid;
+    for (int i = 0; i < kHid; ++i) mo = __builtin_elementwise_maximum(mo, __builtin_fabsf(wo[i]));
+  }
+  mw = wave_max(mw);
+  bh = wave_max(bh);
+  mo = wave_max(mo);
+  const int w = c >> 6;
+  if ((c & 63) == 0) {
+    red[0][w] = mw;
+    red[1][w] = bh;
+    red[2][w] = mo;
+  }
+  __syncthreads();
+  if (c == 0) {
+    for (int i = 1; i < 8; ++i) {
+      mw = __builtin_elementwise_maximum(mw, red[0][i]);
+      bh = __builtin_elementwise_maximum(bh, red[1][i]);
+      mo = __builtin_elementwise_maximum(mo, red[2][i]);
+    }
+    a.exps[0] = plane_exp(11.3137085f * (1.0f + 0x1p-10f));
+    a.exps[1] = plane_exp(mw);
+    a.exps[2] = plane_exp(mo);
+    // the margin covers the roundings of the bound and of g, v and h
+    a.exps[3] = plane_exp(bh * (1.0f + 0x1p-8f));
+  }
+}
+
+// The chunks' weight planes, one value (hi and lo) per thread.  Chunk c:
+//   up   [a, b][k step t][hi, lo][hidden m][16 k]: W'[32 c + m][16 t + k] 2^e_w
+//   down [out block ob][k step s][hi, lo][out o][16 k]: W_o[32 ob + o][32 c +
+//        16 s + 8 (k / 4 % 2) + 4 (k / 8) + k % 4] 2^e_o, the hidden order in
+//        which a lane of the value^T / gate^T results holds its row's values.
+__global__ __launch_bounds__(256) void transition_planes_kernel(TransitionArgs a) {
+  const int idx = (int)(blockIdx.x * 256 + threadIdx.x);
+  constexpr int kPer = kChunkValues / 2;  // values (hi, lo pairs) per chunk
+  if (idx >= kChunks * kPer) return;
+  const int c = idx / kPer;
+  int v = idx - c * kPer;
+  __bf16* chunk = a.planes + (int64_t)c * kChunkValues;
+  float x;
+  int e;
+  __bf16* dst;
+  if (v < (kUpBlocks / 2) * kPlaneBlock) {
+    const int ab = v / (8 * kPlaneBlock);
+    const int t = (v / kPlaneBlock) % 8;
+    const int m = (v / 16) % 32;
+    const int k = v % 16;
+    const int in = 16 * t + k;
+    x = (a.ln_w ? a.ln_w[in] : 1.f) *
+        (ab ? a.w_b : a.w_a)[(int64_t)(kChunkHid * c + m) * kChannels + in];
+    e = a.exps[1];
+    dst = chunk + ((ab * 8 + t) * 2) * kPlaneBlock + m * 16 + k;
+  } else {
+    v -= (kUpBlocks / 2) * kPlaneBlock;
+    const int ob = v / (2 * kPlaneBlock);
+    const int st = (v / kPlaneBlock) % 2;
+    const int o = (v / 16) % 32;
+    const int k = v % 16;
+    const int hid = kChunkHid * c + 16 * st + 8 * ((k >> 2) & 1) + 4 * (k >> 3) + (k & 3);
+    x = a.w_o[(int64_t)(32 * ob + o) * kHid + hid];
+    e = a.exps[2];
+    dst = chunk + kUpBlocks * kPlaneBlock + ((ob * 2 + st) * 2) * kPlaneBlock + o * 16 + k;
+  }
+  const float y = __builtin_ldexpf(x, e);
+  const _Float16 hi = (_Float16)y;
+  const _Float16 lo = (_Float16)(y - (float)hi);
+  dst[0] = __builtin_bit_cast(__bf16, hi);
+  dst[kPlaneBlock] = __builtin_bit_cast(__bf16, lo);
+}
+
+// Persistent: work-group g serves row tiles g, g + grid, ... (kFusedRows
+// rows each).  Chunk k of the work-group's sequence (chunk k % 16 of a tile)
+// sits in LDS buffer k % 2; it is copied in two chunks ahead, each wave
+// copying 6 KB of it.
+__global__ __launch_bounds__(kFusedWaves * 64, 1) void transition_fused_kernel(TransitionArgs a,
+                                                                              int64_t rows,
+                                                                              int64_t ntiles) {
+  __shared__ __attribute__((aligned(16))) uint8_t wbuf[2][kChunkBytes];
+  __shared__ __attribute__((aligned(16))) float fb[2][kHid];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+  const int ex = a.exps[0], ew = a.exps[1], eo = a.exps[2], eh = a.exps[3];
+  for (int i = tid; i < 2 * kHid; i += kFusedWaves * 64) fb[i / kHid][i % kHid] = a.fbias[i];
+
+  const int64_t my_tiles = ntiles > blockIdx.x ? (ntiles - 1 - blockIdx.x) / gridDim.x + 1 : 0;
+  const int64_t total = my_tiles * kChunks;  // chunks this work-group passes through
+  constexpr int kWaveBytes = kChunkBytes / kFusedWaves;  // 6 KB
+  const uint8_t* csrc = reinterpret_cast<const uint8_t*>(a.planes) + w * kWaveBytes + lane * 16;
+  auto dma = [&](int64_t k) {
+    const uint8_t* src = csrc + (k % kChunks) * kChunkBytes;
+    uint8_t* dst = wbuf[k & 1] + w * kWaveBytes;
+#pragma unroll
+    for (int i = 0; i < kWaveBytes / 1024; ++i) lds_dma16(src + 1024 * i, dst + 1024 * i);
+  };
+  if (total > 0) dma(0);
+  if (total > 1) dma(1);
+
+  // Operand reads: lane (l32, half) reads the 16 bytes of row l32 at half.
+  const uint32_t rd = (uint32_t)(l32 * 32 + half * 16);
+  auto blk = [&](int buf, int b) -> bf16x8 {
+    return *(const bf16x8*)(wbuf[buf] + b * 1024 + rd);
+  };
+
+  int64_t k = 0;
+  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    // This lane's row and its channels 16 t + 8 half + e (the B operand of
+    // the up products); rows past the end repeat the last row.
+    const int64_t row0 = tile * kFusedRows + 32 * w;
+    const int64_t rr = min(row0 + l32, rows - 1);
+    const int64_t ri = rr / a.rows_j;
+    const float* src = a.x + ri * a.xs_i + (rr - ri * a.rows_j) * a.xs_j + 8 * half;
+    f32x8 xv[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const f32x4 u = *(const f32x4*)(src + 16 * t);
+      const f32x4 v = *(const f32x4*)(src + 16 * t + 4);
+      xv[t] = f32x8{u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+    }
+    // LayerNorm over the row's 128 channels: this lane's 64 and lane l ^ 32's.
+    float s = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += xv[t][e];
+    }
+    const auto ts = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, s),
+                                                     __builtin_bit_cast(unsigned, s), false, false);
+    const float mean = (__builtin_bit_cast(float, (unsigned)ts[0]) +
+                        __builtin_bit_cast(float, (unsigned)ts[1])) * (1.0f / kChannels);
+    float q = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      xv[t] = xv[t] - mean;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) q += xv[t][e] * xv[t][e];
+    }
+    const auto tq = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, q),
+                                                     __builtin_bit_cast(unsigned, q), false, false);
+    const float var = (__builtin_bit_cast(float, (unsigned)tq[0]) +
+                       __builtin_bit_cast(float, (unsigned)tq[1])) * (1.0f / kChannels);
+    const float sc = __builtin_ldexpf(__builtin_amdgcn_rsqf(var + a.eps), ex);
+    bf16x8 yh[8], yl[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) split_f16(xv[t] * sc, yh[t], yl[t]);
+
+    f32x16 o[4] = {};
+    for (int c = 0; c < kChunks; ++c, ++k) {
+      // chunk k landed: only chunk k + 1's six copies may still be pending
+      if (k + 1 < total)
+        wait_vmcnt<6>();
+      else
+        wait_vmcnt<0>();
+      __syncthreads();
+      const int buf = (int)(k & 1);
+      f32x16 gacc = {}, vacc = {};
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const bf16x8 ah = blk(buf, (0 * 8 + t) * 2), al = blk(buf, (0 * 8 + t) * 2 + 1);
+        const bf16x8 bh = blk(buf, (1 * 8 + t) * 2), bl = blk(buf, (1 * 8 + t) * 2 + 1);
+        gacc = mfma_f16(ah, yh[t], gacc);
+        vacc = mfma_f16(bh, yh[t], vacc);
+        gacc = mfma_f16(ah, yl[t], gacc);
+        vacc = mfma_f16(bh, yl[t], vacc);
+        gacc = mfma_f16(al, yh[t], gacc);
+        vacc = mfma_f16(bl, yh[t], vacc);
+      }
+      // h of this lane's row for hidden channels 32 c + mfma_row(r, half)
+      f32x16 hv;
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int m = kChunkHid * c + 8 * qd + 4 * half;
+        const f32x4 ba = *(const f32x4*)&fb[0][m];
+        const f32x4 bb = *(const f32x4*)&fb[1][m];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * qd + e;
+          const float g = __builtin_ldexpf(gacc[r], -(ex + ew)) + ba[e];
+          const float v = __builtin_ldexpf(vacc[r], -(ex + ew)) + bb[e];
+          hv[r] = __builtin_ldexpf(g * sigmoidf_(g) * v, eh);  // silu(a) * b, scaled
+        }
+      }
+      bf16x8 hh[2], hl[2];
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+        split_f16(f32x8{hv[8 * st + 0], hv[8 * st + 1], hv[8 * st + 2], hv[8 * st + 3],
+                        hv[8 * st + 4], hv[8 * st + 5], hv[8 * st + 6], hv[8 * st + 7]},
+                  hh[st], hl[st]);
+#pragma unroll
+      for (int ob = 0; ob < 4; ++ob) {
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          const int b0 = kUpBlocks + (ob * 2 + st) * 2;
+          const bf16x8 wh = blk(buf, b0), wl = blk(buf, b0 + 1);
+          o[ob] = mfma_f16(hh[st], wh, o[ob]);
+          o[ob] = mfma_f16(hh[st], wl, o[ob]);
+          o[ob] = mfma_f16(hl[st], wh, o[ob]);
+        }
+      }
+      __syncthreads();  // every wave is done with buffer k % 2
+      if (k + 2 < total) dma(k + 2);
+    }
+
+    // out[row][32 ob + l32]: rows 32 w + mfma_row(r, half) of the tile
+    const bool residual = a.accumulate != 0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t row = row0 + mfma_row(r, half);
+      if (row >= rows) continue;
+      const int64_t i = row / a.rows_j;
+      float* d = a.out + i * a.os_i + (row - i * a.rows_j) * a.os_j + l32;
+#pragma unroll
+      for (int ob = 0; ob < 4; ++ob) {
+        const float val = __builtin_ldexpf(o[ob][r], -(eh + eo));
+        d[32 * ob] = residual ? d[32 * ob] + val : val;
+      }
+    }
+  }
+  wait_vmcnt<0>();  // no copy in flight when the work-group ends
+}
+
 int grid_cap(int per_cu) { return device_cu_count() * per_cu; }
 
 }  // namespace
@@ -207,6 +491,19 @@ hipError_t launch_transition(const TransitionArgs& a, hipStream_t stream) {
   if (slots > up_tiles) slots = up_tiles;
   if (slots < 1) slots = 1;
   hipError_t e;
+  if (!fp32_matrix_cores_selected()) {
+    if (a.planes == nullptr || a.fbias == nullptr || a.exps == nullptr) return hipErrorInvalidValue;
+    const int64_t tiles = (rows + kFusedRows - 1) / kFusedRows;
+    const int64_t grid = tiles < device_cu_count() ? tiles : device_cu_count();
+    hipLaunchKernelGGL(transition_prep_kernel, dim3(1), dim3(512), 0, stream, a);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(transition_planes_kernel, dim3((kChunks * kChunkValues / 2 + 255) / 256),
+                       dim3(256), 0, stream, a);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(transition_fused_kernel, dim3((uint32_t)grid), dim3(kFusedWaves * 64), 0,
+                       stream, a, rows, tiles);
+    return hipGetLastError();
+  }
   if (fp32_matrix_cores_selected()) {
     hipLaunchKernelGGL(transition_up_kernel, dim3((uint32_t)(slots * kQuarters)), dim3(256), 0,
                        stream, a, tiles_j, (int)up_tiles, (int)slots);
