@@ -210,8 +210,8 @@ __global__ __launch_bounds__(256, 2) void transition_down_kernel(TransitionArgs 
 //   out [32 rows][128] += h W_o^T                       (24 MFMAs)
 // so h never leaves the registers.  The chunks' weight planes (48 KB each,
 // written once per call by transition_planes_kernel) go from L2 into a
-// double-buffered LDS ring by global_load_lds, shared by the 8 waves (256
-// rows) of a work-group.  Plane scales: y by 2^e_x (|y_c| <= sqrt(128)),
+// three-stage LDS ring by global_load_lds, shared by the 8 waves (256 rows)
+// of a work-group, with one barrier per chunk.  Plane scales: y by 2^e_x (|y_c| <= sqrt(128)),
 // W' and W_o by one exponent each (their largest |value|), h by 2^e_h from
 // the bound |h_c| <= max(|g_c|, 0.2785) |v_c| with |g_c| <= sqrt(128)
 // |Wa'_c| + |ba_c| (likewise v), |silu(g)| <= max(|g|, 0.2785).
@@ -229,30 +229,48 @@ constexpr int kChunkBytes = kChunkValues * 2;
 // e_h; fbias: [2][512] (ba, bb).
 __global__ __launch_bounds__(512) void transition_prep_kernel(TransitionArgs a) {
   __shared__ float red[3][8];
+  __shared__ __attribute__((aligned(16))) float gb_lds[2][kChannels];
   const int c = threadIdx.x;  // hidden channel
+  if (c < kChannels) {
+    gb_lds[0][c] = a.ln_w ? a.ln_w[c] : 1.f;
+    gb_lds[1][c] = a.ln_b ? a.ln_b[c] : 0.f;
+  }
+  __syncthreads();
   const float* wa = a.w_a + (int64_t)c * kChannels;
   const float* wb = a.w_b + (int64_t)c * kChannels;
   float sa2 = 0.f, sa1 = 0.f, sb2 = 0.f, sb1 = 0.f, mw = 0.f;
-  for (int i = 0; i < kChannels; ++i) {
-    const float g = a.ln_w ? a.ln_w[i] : 1.f;
-    const float b = a.ln_b ? a.ln_b[i] : 0.f;
-    const float ga = g * wa[i], gb = g * wb[i];
-    sa2 = __builtin_fmaf(ga, ga, sa2);
-    sb2 = __builtin_fmaf(gb, gb, sb2);
-    sa1 = __builtin_fmaf(b, wa[i], sa1);
-    sb1 = __builtin_fmaf(b, wb[i], sb1);
-    mw = __builtin_elementwise_maximum(
-        mw, __builtin_elementwise_maximum(__builtin_fabsf(ga), __builtin_fabsf(gb)));
+#pragma unroll 8
+  for (int i = 0; i < kChannels; i += 4) {
+    const f32x4 va = *(const f32x4*)(wa + i), vb = *(const f32x4*)(wb + i);
+    const f32x4 g = *(const f32x4*)&gb_lds[0][i], b = *(const f32x4*)&gb_lds[1][i];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float ga = g[e] * va[e], gbv = g[e] * vb[e];
+      sa2 = __builtin_fmaf(ga, ga, sa2);
+      sb2 = __builtin_fmaf(gbv, gbv, sb2);
+      sa1 = __builtin_fmaf(b[e], va[e], sa1);
+      sb1 = __builtin_fmaf(b[e], vb[e], sb1);
+      mw = __builtin_elementwise_maximum(
+          mw, __builtin_elementwise_maximum(__builtin_fabsf(ga), __builtin_fabsf(gbv)));
+    }
   }
   a.fbias[c] = sa1;
   a.fbias[kHid + c] = sb1;
   const float bg = __builtin_sqrtf(128.f * sa2) + __builtin_fabsf(sa1);
   const float bv = __builtin_sqrtf(128.f * sb2) + __builtin_fabsf(sb1);
   float bh = __builtin_elementwise_maximum(bg, 0.2785f) * bv;
+  // max |W_o|: thread t covers a quarter of row t / 4
   float mo = 0.f;
-  if (c < kChannels) {
-    const float* wo = a.w_o + (int64_t)c * kHid;
-    for (int i = 0; i < kHid; ++i) mo = __builtin_elementwise_maximum(mo, __builtin_fabsf(wo[i]));
+  {
+    const float* wo = a.w_o + (int64_t)(c >> 2) * kHid + (c & 3) * (kHid / 4);
+#pragma unroll 8
+    for (int i = 0; i < kHid / 4; i += 4) {
+      const f32x4 v = *(const f32x4*)(wo + i);
+      mo = __builtin_elementwise_maximum(
+          mo, __builtin_elementwise_maximum(
+                  __builtin_elementwise_maximum(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
+                  __builtin_elementwise_maximum(__builtin_fabsf(v.z), __builtin_fabsf(v.w))));
+    }
   }
   mw = wave_max(mw);
   bh = wave_max(bh);
@@ -279,10 +297,12 @@ __global__ __launch_bounds__(512) void transition_prep_kernel(TransitionArgs a) 
 }
 
 // The chunks' weight planes, one value (hi and lo) per thread.  Chunk c:
-//   up   [a, b][k step t][hi, lo][hidden m][16 k]: W'[32 c + m][16 t + k] 2^e_w
-//   down [out block ob][k step s][hi, lo][out o][16 k]: W_o[32 ob + o][32 c +
+//   up   [a, b][k step t][hi, lo][k / 8][hidden m][k % 8]: W'[32 c + m][16 t + k] 2^e_w
+//   down [out block ob][k step s][hi, lo][k / 8][out o][k % 8]: W_o[32 ob + o][32 c +
 //        16 s + 8 (k / 4 % 2) + 4 (k / 8) + k % 4] 2^e_o, the hidden order in
 //        which a lane of the value^T / gate^T results holds its row's values.
+// A 1 KB block's two halves are the k / 8 halves, so the 32 lanes of a half
+// read 512 contiguous bytes (no LDS bank conflicts).
 __global__ __launch_bounds__(256) void transition_planes_kernel(TransitionArgs a) {
   const int idx = (int)(blockIdx.x * 256 + threadIdx.x);
   constexpr int kPer = kChunkValues / 2;  // values (hi, lo pairs) per chunk
@@ -302,7 +322,7 @@ __global__ __launch_bounds__(256) void transition_planes_kernel(TransitionArgs a
     x = (a.ln_w ? a.ln_w[in] : 1.f) *
         (ab ? a.w_b : a.w_a)[(int64_t)(kChunkHid * c + m) * kChannels + in];
     e = a.exps[1];
-    dst = chunk + ((ab * 8 + t) * 2) * kPlaneBlock + m * 16 + k;
+    dst = chunk + ((ab * 8 + t) * 2) * kPlaneBlock + (k >> 3) * 256 + m * 8 + (k & 7);
   } else {
     v -= (kUpBlocks / 2) * kPlaneBlock;
     const int ob = v / (2 * kPlaneBlock);
@@ -312,7 +332,8 @@ __global__ __launch_bounds__(256) void transition_planes_kernel(TransitionArgs a
     const int hid = kChunkHid * c + 16 * st + 8 * ((k >> 2) & 1) + 4 * (k >> 3) + (k & 3);
     x = a.w_o[(int64_t)(32 * ob + o) * kHid + hid];
     e = a.exps[2];
-    dst = chunk + kUpBlocks * kPlaneBlock + ((ob * 2 + st) * 2) * kPlaneBlock + o * 16 + k;
+    dst = chunk + kUpBlocks * kPlaneBlock + ((ob * 2 + st) * 2) * kPlaneBlock + (k >> 3) * 256 +
+          o * 8 + (k & 7);
   }
   const float y = __builtin_ldexpf(x, e);
   const _Float16 hi = (_Float16)y;
@@ -323,12 +344,13 @@ __global__ __launch_bounds__(256) void transition_planes_kernel(TransitionArgs a
 
 // Persistent: work-group g serves row tiles g, g + grid, ... (kFusedRows
 // rows each).  Chunk k of the work-group's sequence (chunk k % 16 of a tile)
-// sits in LDS buffer k % 2; it is copied in two chunks ahead, each wave
-// copying 6 KB of it.
+// sits in LDS stage k % 3; it is copied in two chunks ahead, each wave
+// copying 6 KB of it, right after the barrier that shows every wave done
+// with chunk k - 1, whose stage it takes.
 __global__ __launch_bounds__(kFusedWaves * 64, 1) void transition_fused_kernel(TransitionArgs a,
                                                                               int64_t rows,
                                                                               int64_t ntiles) {
-  __shared__ __attribute__((aligned(16))) uint8_t wbuf[2][kChunkBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t wbuf[3][kChunkBytes];
   __shared__ __attribute__((aligned(16))) float fb[2][kHid];
 
   const int tid = threadIdx.x;
@@ -345,15 +367,15 @@ __global__ __launch_bounds__(kFusedWaves * 64, 1) void transition_fused_kernel(T
   const uint8_t* csrc = reinterpret_cast<const uint8_t*>(a.planes) + w * kWaveBytes + lane * 16;
   auto dma = [&](int64_t k) {
     const uint8_t* src = csrc + (k % kChunks) * kChunkBytes;
-    uint8_t* dst = wbuf[k & 1] + w * kWaveBytes;
+    uint8_t* dst = wbuf[k % 3] + w * kWaveBytes;
 #pragma unroll
     for (int i = 0; i < kWaveBytes / 1024; ++i) lds_dma16(src + 1024 * i, dst + 1024 * i);
   };
   if (total > 0) dma(0);
   if (total > 1) dma(1);
 
-  // Operand reads: lane (l32, half) reads the 16 bytes of row l32 at half.
-  const uint32_t rd = (uint32_t)(l32 * 32 + half * 16);
+  // Operand reads: lane (l32, half) reads row l32's 8 values of k half `half`.
+  const uint32_t rd = (uint32_t)(half * 512 + l32 * 16);
   auto blk = [&](int buf, int b) -> bf16x8 {
     return *(const bf16x8*)(wbuf[buf] + b * 1024 + rd);
   };
@@ -407,8 +429,9 @@ __global__ __launch_bounds__(kFusedWaves * 64, 1) void transition_fused_kernel(T
         wait_vmcnt<6>();
       else
         wait_vmcnt<0>();
-      __syncthreads();
-      const int buf = (int)(k & 1);
+      __syncthreads();  // chunk k landed for every wave; chunk k - 1's stage is free
+      if (k + 2 < total) dma(k + 2);
+      const int buf = (int)(k % 3);
       f32x16 gacc = {}, vacc = {};
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
@@ -453,8 +476,6 @@ __global__ __launch_bounds__(kFusedWaves * 64, 1) void transition_fused_kernel(T
           o[ob] = mfma_f16(hl[st], wh, o[ob]);
         }
       }
-      __syncthreads();  // every wave is done with buffer k % 2
-      if (k + 2 < total) dma(k + 2);
     }
 
     // out[row][32 ob + l32]: rows 32 w + mfma_row(r, half) of the tile
