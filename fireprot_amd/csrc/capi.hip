@@ -234,10 +234,10 @@ TriMulWorkspace trimul_workspace(int n) {
   return w;
 }
 
-// Workspace of fpx_transition: a first segment holding either h
-// [round_up(rows, 128)][512] float (FP32-matrix-core kernels) or the fused
-// kernel's weight planes (16 chunks of 48 KB), folded biases [2][512] float
-// and four exponents, whichever is larger; then 129 maxima words.
+// Workspace of fpx_transition: either h [round_up(rows, 128)][512] float
+// (FP32-matrix-core kernels) or the fused kernel's weight planes (16 chunks
+// of 48 KB), folded biases [2][512] float and four exponents, whichever is
+// larger.
 constexpr size_t kTransitionPlanesBytes = 16 * 48 * 1024;
 constexpr size_t kTransitionFusedBytes = kTransitionPlanesBytes + 2 * 512 * sizeof(float) + 256;
 size_t transition_h_bytes(int64_t rows) {
@@ -245,9 +245,7 @@ size_t transition_h_bytes(int64_t rows) {
       round_up(rows, 128) * fpx::kTransitionHidden * (int64_t)sizeof(float), 256);
   return h > kTransitionFusedBytes ? h : kTransitionFusedBytes;
 }
-size_t transition_workspace(int64_t rows) {
-  return transition_h_bytes(rows) + (size_t)round_up(129 * (int64_t)sizeof(uint32_t), 256);
-}
+size_t transition_workspace(int64_t rows) { return transition_h_bytes(rows); }
 
 // A [batch][4][n][32] operand with channel stride 1 the strided attention
 // kernel can read: non-negative strides that keep 16-byte rows aligned, and
@@ -718,7 +716,6 @@ int fpx_transition(const float* x, int64_t rows_i, int64_t rows_j, int64_t x_str
   a.planes = static_cast<__bf16*>(workspace);
   a.fbias = as<float>(static_cast<char*>(workspace) + kTransitionPlanesBytes);
   a.exps = as<int>(static_cast<char*>(workspace) + kTransitionPlanesBytes + 2 * 512 * sizeof(float));
-  a.maxima = as<uint32_t>(static_cast<char*>(workspace) + transition_h_bytes((int64_t)rows_i * rows_j));
   a.out = out;
   a.os_i = out_stride_i;
   a.os_j = out_stride_j;

@@ -1,12 +1,11 @@
 // Gated pair-row projections on the CDNA4 16-bit matrix cores, FP32-accurate.
 //
-// Both the triangle multiplication's input projections and the pair
-// transition's hidden layer produce, per channel c of a pair row x,
+// The triangle multiplication's input projections produce, per channel c of
+// a pair row x,
 //
 //   value_c = LN(x) . Wv[c] + bv[c]    gate_c = LN(x) . Wg[c] + bg[c]
 //
-// and combine the two:  (mask * sigmoid(gate)) * value  (kGatedTriMul) or
-// silu(gate) * value  (kGatedTransition).  Rows and weights are held as
+// and combine the two:  (mask * sigmoid(gate)) * value.  Rows and weights are held as
 // power-of-two scaled fp16 (hi, lo) planes (split.hpp): the LN rows by one
 // 2^ex per launch from the LN affine (|y_c| <= sqrt(128) |ln_w_c| + |ln_b_c|,
 // applied by pre-scaling ln_w and ln_b), each weight column by its own 2^ew;
@@ -32,7 +31,7 @@
 
 namespace fpx {
 
-enum GatedMode { kGatedTriMul = 0, kGatedTransition = 1 };
+enum GatedMode { kGatedTriMul = 0 };
 
 struct GatedArgs {
   const float* x;        // pair row (r, k) at x + r * xs_r + k * xs_k
@@ -55,8 +54,6 @@ struct GatedArgs {
   int np;                // kGatedTriMul: packed extent of the output
   uint32_t* rowmax;      // kGatedTriMul: [slice][128][np] max |out| over k per (channel, row),
                          // float bits; null: none
-  uint32_t* out_max;     // kGatedTransition: max |out| of the launch, float bits by atomic
-                         // max (zeroed before the launch); null: none
 };
 
 template <int MODE>
@@ -64,10 +61,6 @@ struct GatedTraits;
 template <>
 struct GatedTraits<kGatedTriMul> {
   static constexpr int kSlices = 2;  // a, b
-};
-template <>
-struct GatedTraits<kGatedTransition> {
-  static constexpr int kSlices = 4;  // hidden quarters
 };
 
 constexpr int kGatedWaves = 8;
@@ -83,9 +76,6 @@ constexpr int kGatedPlaneRow = kChannels + 8;  // bf16 per LDS row: 272 bytes
 // operand layout.  Each work-group owns whole rows r (first, first +
 // streams, ...), so the row maxima are plain stores, and the work-groups
 // in flight write one run of adjacent blocks per channel group.
-// kGatedTransition writes out[slice][(r * rows_k + k) * 512 + c] for
-// k < rows_k (h rows, the slice's 128 columns of the 512); its work-groups
-// take tiles first, first + streams, ... of the row-major tile order.
 template <int MODE>
 __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedArgs a, int tiles_k,
                                                                           int ntiles,
@@ -154,21 +144,11 @@ __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedA
   lnb = ldexp8(lnb, ex);
 
   // This work-group's tiles, local index i < count (at least one).
-  int count;
-  if constexpr (MODE == kGatedTriMul)
-    count = tiles_k * ((a.rows_r - first + streams - 1) / streams);
-  else
-    count = (ntiles - first + streams - 1) / streams;
+  const int count = tiles_k * ((a.rows_r - first + streams - 1) / streams);
   auto origin = [&](int i, int& r, int& k0) {
-    if constexpr (MODE == kGatedTriMul) {
-      const int q = i / tiles_k;
-      r = first + streams * q;
-      k0 = (i - q * tiles_k) * kGatedRows;
-    } else {
-      const int tile = first + streams * i;
-      r = tile / tiles_k;
-      k0 = (tile - r * tiles_k) * kGatedRows;
-    }
+    const int q = i / tiles_k;
+    r = first + streams * q;
+    k0 = (i - q * tiles_k) * kGatedRows;
   };
 
   // Row loads with no branches on the data path (tile clamped to the last
@@ -250,7 +230,6 @@ __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedA
   // register r with r + 8 across the row pair leaves every lane the value
   // and gate of its channel for registers r + (odd ? 8 : 0), r < 8, i.e.
   // tile rows 8 rr + 4 half + e for rr = (odd ? 2 : 0) + r / 4, e = r % 4.
-  float out_max = 0.f;  // kGatedTransition: running max |value| stored
   float row_max = 0.f;  // kGatedTriMul: max |value| of this lane's channel over the row so far
   auto store = [&](const f32x16& res, int i) {
     f32x8 val;
@@ -265,13 +244,9 @@ __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedA
                                                       false, false);
       const float p = __builtin_bit_cast(float, (unsigned)s[0]) + bv;
       const float g = __builtin_bit_cast(float, (unsigned)s[1]);
-      if constexpr (MODE == kGatedTriMul) {
-        const int row = 8 * ((odd ? 2 : 0) + (r >> 2)) + 4 * half + (r & 3);
-        // native order: a = mask; a = a * sigmoid(g); a = a * p
-        val[r] = (ms[i & 3][row] * sigmoidf_(g + bg)) * p;
-      } else {
-        val[r] = g * sigmoidf_(g) * p;  // silu(a) * b
-      }
+      const int row = 8 * ((odd ? 2 : 0) + (r >> 2)) + 4 * half + (r & 3);
+      // native order: a = mask; a = a * sigmoid(g); a = a * p
+      val[r] = (ms[i & 3][row] * sigmoidf_(g + bg)) * p;
     }
     int r_out, k0;
     origin(i, r_out, k0);
@@ -306,16 +281,6 @@ __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedA
       for (int q = 0; q < 2; ++q)
         *(f32x4*)(dst + 8 * (rr0 + q)) =
             f32x4{val[4 * q + 0], val[4 * q + 1], val[4 * q + 2], val[4 * q + 3]};
-    } else {
-      float* dst = a.out[slice] + (int64_t)r_out * a.rows_k * 512 + ch;
-#pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const int kk = k0 + 8 * (rr0 + (r >> 2)) + 4 * half + (r & 3);
-        if (kk < a.rows_k) {
-          dst[(int64_t)kk * 512] = val[r];
-          out_max = __builtin_elementwise_maximum(out_max, __builtin_fabsf(val[r]));
-        }
-      }
     }
   };
 
@@ -367,11 +332,6 @@ __global__ __launch_bounds__(kGatedWaves * 64, 1) void gated_split_kernel(GatedA
     ++i;
   }
   if (!lead) store(res, i - 1);
-  if (MODE == kGatedTransition && a.out_max != nullptr) {
-    // one atomic per wave: the NaN-propagating max of the values it stored
-    const float m = wave_max(out_max);
-    if (lane == 0) atomicMax(a.out_max, __builtin_bit_cast(uint32_t, m));
-  }
 }
 
 // Launches gated_split_kernel<MODE> over rows_r x span_k / 32 row tiles.
@@ -383,13 +343,12 @@ hipError_t launch_gated_split(const GatedArgs& a, hipStream_t stream) {
   if (ntiles == 0) return hipSuccess;
   if (a.span_k % kGatedRows || a.span_k < a.rows_k || a.rows_k < 1 || ntiles > 0x7fffffffll)
     return hipErrorInvalidValue;
-  if (MODE == kGatedTriMul && a.rows_r > a.np) return hipErrorInvalidValue;
+  if (a.rows_r > a.np) return hipErrorInvalidValue;
   int64_t cap = (int64_t)device_cu_count() / kSlices;
   if (cap >= 8) cap -= cap % 8;
   if (cap < 1) cap = 1;
-  // kGatedTriMul: whole rows per work-group
-  const int64_t units = MODE == kGatedTriMul ? (int64_t)a.rows_r : ntiles;
-  const int streams = (int)(units < cap ? units : cap);
+  // whole rows per work-group
+  const int streams = (int)(a.rows_r < cap ? a.rows_r : cap);
   hipLaunchKernelGGL(gated_split_kernel<MODE>, dim3(streams * kSlices), dim3(kGatedWaves * 64), 0,
                      stream, a, tiles_k, (int)ntiles, streams);
   return hipGetLastError();

@@ -332,10 +332,7 @@ struct TransitionArgs {
   const float* w_a;   // [512][128]
   const float* w_b;   // [512][128]
   const float* w_o;   // [128][512]
-  float* h;
-  // FP32-matrix-core path: [0] max |h| of the launch, [1 + c] max |W_o[c]|,
-  // as float bits (129 words)
-  uint32_t* maxima;
+  float* h;           // FP32-matrix-core path: [round_up(rows, 128)][512]
   // fp16-plane (fused) path: the 16 chunks' weight planes (fp16 bits, 768 KB),
   // the folded biases [2][512] and the plane exponents (e_x, e_w, e_o, e_h)
   __bf16* planes;

@@ -17,7 +17,6 @@
 // never leaving the registers (transition_fused_kernel below).
 #include "attn_common.hpp"
 #include "common.hpp"
-#include "gated_split.hpp"
 #include "gemm.hpp"
 #include "kernels.hpp"
 
@@ -115,37 +114,10 @@ __global__ __launch_bounds__(256, 2) void transition_up_kernel(TransitionArgs a,
   }
 }
 
-// The fp16-plane path's maxima: max |W_o| of each output row, and the h max
-// cleared for the up-projection's atomics.  One work-group of 256 threads.
-__global__ __launch_bounds__(256) void transition_maxima_kernel(const float* __restrict__ w_o,
-                                                                uint32_t* __restrict__ maxima) {
-  const int t = threadIdx.x;
-  if (t < kChannels) {
-    const f32x4* row = reinterpret_cast<const f32x4*>(w_o + (int64_t)t * kHid);
-    float m = 0.f;
-    for (int i = 0; i < kHid / 4; ++i) {
-      const f32x4 v = row[i];
-      m = __builtin_elementwise_maximum(
-          m, __builtin_elementwise_maximum(
-                 __builtin_elementwise_maximum(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
-                 __builtin_elementwise_maximum(__builtin_fabsf(v.z), __builtin_fabsf(v.w))));
-    }
-    maxima[1 + t] = __builtin_bit_cast(uint32_t, m);
-  } else if (t == kChannels) {
-    maxima[0] = 0u;
-  }
-}
-
-// kSplit: gemm_nt_128_f16 (16-bit matrix cores, scaled fp16 planes): every h
-// row scaled by the launch's h exponent (the LN'd rows share one magnitude
-// range), each W_o row by its own.
-template <bool kSplit>
-__global__ __launch_bounds__(256, 2) void transition_down_kernel(TransitionArgs a,
-                                                                 int64_t rows) {
-  using Stage = std::conditional_t<kSplit, F16Stage, GemmStage>;
-  __shared__ __attribute__((aligned(16))) Stage As[2];
-  __shared__ __attribute__((aligned(16))) Stage Bs[2];
-  __shared__ int ea[kSplit ? kGemmTile : 1], eb[kSplit ? kGemmTile : 1];
+// h W_o^T for one 128-row tile of h on the FP32 matrix cores.
+__global__ __launch_bounds__(256, 2) void transition_down_kernel(TransitionArgs a, int64_t rows) {
+  __shared__ __attribute__((aligned(16))) GemmStage As[2];
+  __shared__ __attribute__((aligned(16))) GemmStage Bs[2];
   const int64_t r0 = (int64_t)blockIdx.x * kGemmTile;
   f32x16 acc[2][2] = {};
   const int lane = threadIdx.x & 63;
@@ -155,26 +127,7 @@ __global__ __launch_bounds__(256, 2) void transition_down_kernel(TransitionArgs 
   const int wi = (w >> 1) * 64;
   const int wj = (w & 1) * 64;
   // W_o is [128 out][512 in]: the B operand rows are output channels.
-  if constexpr (kSplit) {
-    const int t = threadIdx.x;
-    const int ex = plane_exp(__builtin_bit_cast(float, a.maxima[0]));
-    if (t < kGemmTile) ea[t] = ex;
-    else eb[t - kGemmTile] = plane_exp(__builtin_bit_cast(float, a.maxima[1 + t - kGemmTile]));
-    __syncthreads();
-    gemm_nt_128_f16(a.h + r0 * kHid, kHid, a.w_o, kHid, 32, kHid / kSplitK, As, Bs, ea, eb,
-                    acc);
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb) {
-        const int e = ex + eb[wj + 32 * cb + l32];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[rb][cb][r] = __builtin_ldexpf(acc[rb][cb][r], -e);
-      }
-    }
-  } else {
-    gemm_nt_128(a.h + r0 * kHid, kHid, a.w_o, kHid, kHid / kKStage, As, Bs, acc);
-  }
+  gemm_nt_128(a.h + r0 * kHid, kHid, a.w_o, kHid, kHid / kKStage, As, Bs, acc);
 
   const bool residual = a.accumulate != 0;
 #pragma unroll
@@ -194,7 +147,6 @@ __global__ __launch_bounds__(256, 2) void transition_down_kernel(TransitionArgs 
     }
   }
 }
-
 
 // ------------------------------------------------------- fused, fp16 cores
 // out = x + silu(y Wa'^T + ba) * (y Wb'^T + bb) Wo^T with y = (x - mean)
@@ -525,41 +477,11 @@ hipError_t launch_transition(const TransitionArgs& a, hipStream_t stream) {
                        stream, a, rows, tiles);
     return hipGetLastError();
   }
-  if (fp32_matrix_cores_selected()) {
-    hipLaunchKernelGGL(transition_up_kernel, dim3((uint32_t)(slots * kQuarters)), dim3(256), 0,
-                       stream, a, tiles_j, (int)up_tiles, (int)slots);
-    e = hipGetLastError();
-  } else {
-    GatedArgs g{};
-    g.x = a.x;
-    g.xs_r = a.xs_i;
-    g.xs_k = a.xs_j;
-    g.rows_r = a.rows_i;
-    g.rows_k = a.rows_j;
-    g.span_k = tiles_j * kRows;
-    g.ln_w = a.ln_w;
-    g.ln_b = a.ln_b;
-    g.eps = a.eps;
-    // h = silu(x W_a^T) * (x W_b^T): W_a rows are the gates, W_b rows the values.
-    for (int q = 0; q < kQuarters; ++q) {
-      g.w_value[q] = a.w_b + (int64_t)q * kChannels * kChannels;
-      g.w_gate[q] = a.w_a + (int64_t)q * kChannels * kChannels;
-      g.out[q] = a.h + q * kChannels;
-    }
-    if (a.maxima == nullptr) return hipErrorInvalidValue;
-    g.out_max = a.maxima;
-    hipLaunchKernelGGL(transition_maxima_kernel, dim3(1), dim3(256), 0, stream, a.w_o, a.maxima);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    e = launch_gated_split<kGatedTransition>(g, stream);
-  }
-  if (e != hipSuccess) return e;
-  if (fp32_matrix_cores_selected())
-    hipLaunchKernelGGL(transition_down_kernel<false>, dim3((uint32_t)down_tiles), dim3(256), 0,
-                       stream, a, rows);
-  else
-    hipLaunchKernelGGL(transition_down_kernel<true>, dim3((uint32_t)down_tiles), dim3(256), 0,
-                       stream, a, rows);
+  hipLaunchKernelGGL(transition_up_kernel, dim3((uint32_t)(slots * kQuarters)), dim3(256), 0,
+                     stream, a, tiles_j, (int)up_tiles, (int)slots);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(transition_down_kernel, dim3((uint32_t)down_tiles), dim3(256), 0, stream, a,
+                     rows);
   return hipGetLastError();
 }
 
