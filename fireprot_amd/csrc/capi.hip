@@ -236,10 +236,10 @@ TriMulWorkspace trimul_workspace(int n) {
 
 // Workspace of fpx_transition: either h [round_up(rows, 128)][512] float
 // (FP32-matrix-core kernels) or the fused kernel's weight planes (16 chunks
-// of 48 KB), folded biases [2][512] float and four exponents, whichever is
-// larger.
+// of 48 KB), folded biases [2][512] float and its plane exponents (5 KB),
+// whichever is larger.
 constexpr size_t kTransitionPlanesBytes = 16 * 48 * 1024;
-constexpr size_t kTransitionFusedBytes = kTransitionPlanesBytes + 2 * 512 * sizeof(float) + 256;
+constexpr size_t kTransitionFusedBytes = kTransitionPlanesBytes + 2 * 512 * sizeof(float) + 5120;
 size_t transition_h_bytes(int64_t rows) {
   const size_t h = (size_t)round_up(
       round_up(rows, 128) * fpx::kTransitionHidden * (int64_t)sizeof(float), 256);

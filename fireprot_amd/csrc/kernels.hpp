@@ -334,7 +334,8 @@ struct TransitionArgs {
   const float* w_o;   // [128][512]
   float* h;           // FP32-matrix-core path: [round_up(rows, 128)][512]
   // fp16-plane (fused) path: the 16 chunks' weight planes (fp16 bits, 768 KB),
-  // the folded biases [2][512] and the plane exponents (e_x, e_w, e_o, e_h)
+  // the folded biases [2][512] and the plane exponents (1156 ints, see
+  // transition.hip)
   __bf16* planes;
   float* fbias;
   int* exps;

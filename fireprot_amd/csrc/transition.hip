@@ -163,10 +163,10 @@ __global__ __launch_bounds__(256, 2) void transition_down_kernel(TransitionArgs 
 // so h never leaves the registers.  The chunks' weight planes (48 KB each,
 // written once per call by transition_planes_kernel) go from L2 into a
 // three-stage LDS ring by global_load_lds, shared by the 8 waves (256 rows)
-// of a work-group, with one barrier per chunk.  Plane scales: y by 2^e_x (|y_c| <= sqrt(128)),
-// W' and W_o by one exponent each (their largest |value|), h by 2^e_h from
-// the bound |h_c| <= max(|g_c|, 0.2785) |v_c| with |g_c| <= sqrt(128)
-// |Wa'_c| + |ba_c| (likewise v), |silu(g)| <= max(|g|, 0.2785).
+// of a work-group, with one barrier per chunk.  Plane scales: y by 2^e_x
+// (|y_c| <= sqrt(128)), each row of W' and of W_o by its own exponent, h by
+// 2^e_h from the bound |h_c| <= max(|g_c|, 0.2785) |v_c| with |g_c| <=
+// sqrt(128) |Wa'_c| + |ba_c| (likewise v), |silu(g)| <= max(|g|, 0.2785).
 constexpr int kFusedWaves = 8;
 constexpr int kFusedRows = 32 * kFusedWaves;               // rows per tile
 constexpr int kChunkHid = 32;
@@ -177,10 +177,16 @@ constexpr int kPlaneBlock = 32 * 16;                       // fp16 values of a 1
 constexpr int kChunkValues = (kUpBlocks + kDownBlocks) * kPlaneBlock;  // 24576 (48 KB)
 constexpr int kChunkBytes = kChunkValues * 2;
 
-// One work-group: the exponents and the folded biases.  exps: e_x, e_w, e_o,
-// e_h; fbias: [2][512] (ba, bb).
+// Plane exponents (TransitionArgs::exps): e_x of the y planes, e_h of h, one
+// per W' row (a, then b) and one per W_o row.
+constexpr int kExpX = 0;
+constexpr int kExpH = 1;
+constexpr int kExpW = 4;                 // [2][512]
+constexpr int kExpO = kExpW + 2 * kHid;  // [128]
+
+// One work-group: the exponents and the folded biases ([2][512]: ba, bb).
 __global__ __launch_bounds__(512) void transition_prep_kernel(TransitionArgs a) {
-  __shared__ float red[3][8];
+  __shared__ float red[8];
   __shared__ __attribute__((aligned(16))) float gb_lds[2][kChannels];
   const int c = threadIdx.x;  // hidden channel
   if (c < kChannels) {
@@ -190,7 +196,7 @@ __global__ __launch_bounds__(512) void transition_prep_kernel(TransitionArgs a) 
   __syncthreads();
   const float* wa = a.w_a + (int64_t)c * kChannels;
   const float* wb = a.w_b + (int64_t)c * kChannels;
-  float sa2 = 0.f, sa1 = 0.f, sb2 = 0.f, sb1 = 0.f, mw = 0.f;
+  float sa2 = 0.f, sa1 = 0.f, sb2 = 0.f, sb1 = 0.f, ma = 0.f, mb = 0.f;
 #pragma unroll 8
   for (int i = 0; i < kChannels; i += 4) {
     const f32x4 va = *(const f32x4*)(wa + i), vb = *(const f32x4*)(wb + i);
@@ -202,49 +208,39 @@ __global__ __launch_bounds__(512) void transition_prep_kernel(TransitionArgs a) 
       sb2 = __builtin_fmaf(gbv, gbv, sb2);
       sa1 = __builtin_fmaf(b[e], va[e], sa1);
       sb1 = __builtin_fmaf(b[e], vb[e], sb1);
-      mw = __builtin_elementwise_maximum(
-          mw, __builtin_elementwise_maximum(__builtin_fabsf(ga), __builtin_fabsf(gbv)));
+      ma = __builtin_elementwise_maximum(ma, __builtin_fabsf(ga));
+      mb = __builtin_elementwise_maximum(mb, __builtin_fabsf(gbv));
     }
   }
   a.fbias[c] = sa1;
   a.fbias[kHid + c] = sb1;
+  a.exps[kExpW + c] = plane_exp(ma);
+  a.exps[kExpW + kHid + c] = plane_exp(mb);
   const float bg = __builtin_sqrtf(128.f * sa2) + __builtin_fabsf(sa1);
   const float bv = __builtin_sqrtf(128.f * sb2) + __builtin_fabsf(sb1);
   float bh = __builtin_elementwise_maximum(bg, 0.2785f) * bv;
-  // max |W_o|: thread t covers a quarter of row t / 4
-  float mo = 0.f;
-  {
-    const float* wo = a.w_o + (int64_t)(c >> 2) * kHid + (c & 3) * (kHid / 4);
+  // max |W_o| of output row c (threads c < 128)
+  if (c < kChannels) {
+    const float* wo = a.w_o + (int64_t)c * kHid;
+    float mo = 0.f;
 #pragma unroll 8
-    for (int i = 0; i < kHid / 4; i += 4) {
+    for (int i = 0; i < kHid; i += 4) {
       const f32x4 v = *(const f32x4*)(wo + i);
       mo = __builtin_elementwise_maximum(
           mo, __builtin_elementwise_maximum(
                   __builtin_elementwise_maximum(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
                   __builtin_elementwise_maximum(__builtin_fabsf(v.z), __builtin_fabsf(v.w))));
     }
+    a.exps[kExpO + c] = plane_exp(mo);
   }
-  mw = wave_max(mw);
   bh = wave_max(bh);
-  mo = wave_max(mo);
-  const int w = c >> 6;
-  if ((c & 63) == 0) {
-    red[0][w] = mw;
-    red[1][w] = bh;
-    red[2][w] = mo;
-  }
+  if ((c & 63) == 0) red[c >> 6] = bh;
   __syncthreads();
   if (c == 0) {
-    for (int i = 1; i < 8; ++i) {
-      mw = __builtin_elementwise_maximum(mw, red[0][i]);
-      bh = __builtin_elementwise_maximum(bh, red[1][i]);
-      mo = __builtin_elementwise_maximum(mo, red[2][i]);
-    }
-    a.exps[0] = plane_exp(11.3137085f * (1.0f + 0x1p-10f));
-    a.exps[1] = plane_exp(mw);
-    a.exps[2] = plane_exp(mo);
+    for (int i = 1; i < 8; ++i) bh = __builtin_elementwise_maximum(bh, red[i]);
+    a.exps[kExpX] = plane_exp(11.3137085f * (1.0f + 0x1p-10f));
     // the margin covers the roundings of the bound and of g, v and h
-    a.exps[3] = plane_exp(bh * (1.0f + 0x1p-8f));
+    a.exps[kExpH] = plane_exp(bh * (1.0f + 0x1p-8f));
   }
 }
 
@@ -273,7 +269,7 @@ __global__ __launch_bounds__(256) void transition_planes_kernel(TransitionArgs a
     const int in = 16 * t + k;
     x = (a.ln_w ? a.ln_w[in] : 1.f) *
         (ab ? a.w_b : a.w_a)[(int64_t)(kChunkHid * c + m) * kChannels + in];
-    e = a.exps[1];
+    e = a.exps[kExpW + ab * kHid + kChunkHid * c + m];
     dst = chunk + ((ab * 8 + t) * 2) * kPlaneBlock + (k >> 3) * 256 + m * 8 + (k & 7);
   } else {
     v -= (kUpBlocks / 2) * kPlaneBlock;
@@ -283,7 +279,7 @@ __global__ __launch_bounds__(256) void transition_planes_kernel(TransitionArgs a
     const int k = v % 16;
     const int hid = kChunkHid * c + 16 * st + 8 * ((k >> 2) & 1) + 4 * (k >> 3) + (k & 3);
     x = a.w_o[(int64_t)(32 * ob + o) * kHid + hid];
-    e = a.exps[2];
+    e = a.exps[kExpO + 32 * ob + o];
     dst = chunk + kUpBlocks * kPlaneBlock + ((ob * 2 + st) * 2) * kPlaneBlock + (k >> 3) * 256 +
           o * 8 + (k & 7);
   }
@@ -304,14 +300,22 @@ __global__ __launch_bounds__(kFusedWaves * 64, 1) void transition_fused_kernel(T
                                                                               int64_t ntiles) {
   __shared__ __attribute__((aligned(16))) uint8_t wbuf[3][kChunkBytes];
   __shared__ __attribute__((aligned(16))) float fb[2][kHid];
+  __shared__ __attribute__((aligned(16))) int few[2][kHid];  // -(e_x + e_w) per W' row
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5;
   const int l32 = lane & 31;
-  const int ex = a.exps[0], ew = a.exps[1], eo = a.exps[2], eh = a.exps[3];
-  for (int i = tid; i < 2 * kHid; i += kFusedWaves * 64) fb[i / kHid][i % kHid] = a.fbias[i];
+  const int ex = a.exps[kExpX], eh = a.exps[kExpH];
+  for (int i = tid; i < 2 * kHid; i += kFusedWaves * 64) {
+    fb[i / kHid][i % kHid] = a.fbias[i];
+    few[i / kHid][i % kHid] = -(ex + a.exps[kExpW + i]);
+  }
+  // -(e_h + e_o) of this lane's output channels 32 ob + l32
+  int eout[4];
+#pragma unroll
+  for (int ob = 0; ob < 4; ++ob) eout[ob] = -(eh + a.exps[kExpO + 32 * ob + l32]);
 
   const int64_t my_tiles = ntiles > blockIdx.x ? (ntiles - 1 - blockIdx.x) / gridDim.x + 1 : 0;
   const int64_t total = my_tiles * kChunks;  // chunks this work-group passes through
@@ -403,11 +407,14 @@ __global__ __launch_bounds__(kFusedWaves * 64, 1) void transition_fused_kernel(T
         const int m = kChunkHid * c + 8 * qd + 4 * half;
         const f32x4 ba = *(const f32x4*)&fb[0][m];
         const f32x4 bb = *(const f32x4*)&fb[1][m];
+        typedef int i32x4 __attribute__((ext_vector_type(4)));
+        const i32x4 sa = *(const i32x4*)&few[0][m];
+        const i32x4 sb = *(const i32x4*)&few[1][m];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = 4 * qd + e;
-          const float g = __builtin_ldexpf(gacc[r], -(ex + ew)) + ba[e];
-          const float v = __builtin_ldexpf(vacc[r], -(ex + ew)) + bb[e];
+          const float g = __builtin_ldexpf(gacc[r], sa[e]) + ba[e];
+          const float v = __builtin_ldexpf(vacc[r], sb[e]) + bb[e];
           hv[r] = __builtin_ldexpf(g * sigmoidf_(g) * v, eh);  // silu(a) * b, scaled
         }
       }
@@ -440,7 +447,7 @@ __global__ __launch_bounds__(kFusedWaves * 64, 1) void transition_fused_kernel(T
       float* d = a.out + i * a.os_i + (row - i * a.rows_j) * a.os_j + l32;
 #pragma unroll
       for (int ob = 0; ob < 4; ++ob) {
-        const float val = __builtin_ldexpf(o[ob][r], -(eh + eo));
+        const float val = __builtin_ldexpf(o[ob][r], eout[ob]);
         d[32 * ob] = residual ? d[32 * ob] + val : val;
       }
     }
