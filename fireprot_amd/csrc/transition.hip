@@ -187,6 +187,7 @@ constexpr int kExpO = kExpW + 2 * kHid;  // [128]
 // One work-group: the exponents and the folded biases ([2][512]: ba, bb).
 __global__ __launch_bounds__(512) void transition_prep_kernel(TransitionArgs a) {
   __shared__ float red[8];
+  __shared__ float red_o[4 * kChannels];
   __shared__ __attribute__((aligned(16))) float gb_lds[2][kChannels];
   const int c = threadIdx.x;  // hidden channel
   if (c < kChannels) {
@@ -219,23 +220,28 @@ __global__ __launch_bounds__(512) void transition_prep_kernel(TransitionArgs a) 
   const float bg = __builtin_sqrtf(128.f * sa2) + __builtin_fabsf(sa1);
   const float bv = __builtin_sqrtf(128.f * sb2) + __builtin_fabsf(sb1);
   float bh = __builtin_elementwise_maximum(bg, 0.2785f) * bv;
-  // max |W_o| of output row c (threads c < 128)
-  if (c < kChannels) {
-    const float* wo = a.w_o + (int64_t)c * kHid;
+  // max |W_o| of output row c / 4, a quarter of it per thread, then per row
+  {
+    const float* wo = a.w_o + (int64_t)(c >> 2) * kHid + (c & 3) * (kHid / 4);
     float mo = 0.f;
 #pragma unroll 8
-    for (int i = 0; i < kHid; i += 4) {
+    for (int i = 0; i < kHid / 4; i += 4) {
       const f32x4 v = *(const f32x4*)(wo + i);
       mo = __builtin_elementwise_maximum(
           mo, __builtin_elementwise_maximum(
                   __builtin_elementwise_maximum(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
                   __builtin_elementwise_maximum(__builtin_fabsf(v.z), __builtin_fabsf(v.w))));
     }
-    a.exps[kExpO + c] = plane_exp(mo);
+    red_o[c] = mo;
   }
   bh = wave_max(bh);
   if ((c & 63) == 0) red[c >> 6] = bh;
   __syncthreads();
+  if (c < kChannels) {
+    const float m01 = __builtin_elementwise_maximum(red_o[4 * c], red_o[4 * c + 1]);
+    const float m23 = __builtin_elementwise_maximum(red_o[4 * c + 2], red_o[4 * c + 3]);
+    a.exps[kExpO + c] = plane_exp(__builtin_elementwise_maximum(m01, m23));
+  }
   if (c == 0) {
     for (int i = 1; i < 8; ++i) bh = __builtin_elementwise_maximum(bh, red[i]);
     a.exps[kExpX] = plane_exp(11.3137085f * (1.0f + 0x1p-10f));
