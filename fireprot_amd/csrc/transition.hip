@@ -298,9 +298,9 @@ __global__ __launch_bounds__(256) void transition_planes_kernel(TransitionArgs a
 
 // Persistent: work-group g serves row tiles g, g + grid, ... (kFusedRows
 // rows each).  Chunk k of the work-group's sequence (chunk k % 16 of a tile)
-// sits in LDS stage k % 3; it is copied in two chunks ahead, each wave
-// copying 6 KB of it, right after the barrier that shows every wave done
-// with chunk k - 1, whose stage it takes.
+// sits in LDS stage k % 3; it is copied in two chunks ahead (each wave
+// copying 6 KB of it): at chunk k - 2, right after the barrier that shows
+// every wave done with chunk k - 3, whose stage it takes.
 __global__ __launch_bounds__(kFusedWaves * 64, 1) void transition_fused_kernel(TransitionArgs a,
                                                                               int64_t rows,
                                                                               int64_t ntiles) {
