@@ -178,30 +178,38 @@ constexpr int kChunkValues = (kUpBlocks + kDownBlocks) * kPlaneBlock;  // 24576 
 constexpr int kChunkBytes = kChunkValues * 2;
 
 // Plane exponents (TransitionArgs::exps): e_x of the y planes, e_h of h, one
-// per W' row (a, then b) and one per W_o row.
+// per W' row (a, then b) and one per W_o row; then the prep work-groups'
+// largest h bounds (float bits), which transition_planes_kernel reduces to
+// e_h.
 constexpr int kExpX = 0;
 constexpr int kExpH = 1;
 constexpr int kExpW = 4;                 // [2][512]
 constexpr int kExpO = kExpW + 2 * kHid;  // [128]
+constexpr int kPrepGroups = 4;
+constexpr int kExpPart = kExpO + kChannels;  // [kPrepGroups]
 
-// One work-group: the exponents and the folded biases ([2][512]: ba, bb).
+// kPrepGroups work-groups of 512 threads: the folded biases ([2][512]: ba,
+// bb) and the exponents.  Work-group g: hidden channels 128 g .. + 127, four
+// threads per channel (32 inputs each), and W_o rows 32 g .. + 31, sixteen
+// threads per row.
 __global__ __launch_bounds__(512) void transition_prep_kernel(TransitionArgs a) {
   __shared__ float red[8];
-  __shared__ float red_o[4 * kChannels];
   __shared__ __attribute__((aligned(16))) float gb_lds[2][kChannels];
-  const int c = threadIdx.x;  // hidden channel
-  if (c < kChannels) {
-    gb_lds[0][c] = a.ln_w ? a.ln_w[c] : 1.f;
-    gb_lds[1][c] = a.ln_b ? a.ln_b[c] : 0.f;
+  const int tid = threadIdx.x;
+  if (tid < kChannels) {
+    gb_lds[0][tid] = a.ln_w ? a.ln_w[tid] : 1.f;
+    gb_lds[1][tid] = a.ln_b ? a.ln_b[tid] : 0.f;
   }
   __syncthreads();
-  const float* wa = a.w_a + (int64_t)c * kChannels;
-  const float* wb = a.w_b + (int64_t)c * kChannels;
+  const int c = (int)blockIdx.x * (kHid / kPrepGroups) + (tid >> 2);  // hidden channel
+  const int i0 = (tid & 3) * (kChannels / 4);
+  const float* wa = a.w_a + (int64_t)c * kChannels + i0;
+  const float* wb = a.w_b + (int64_t)c * kChannels + i0;
   float sa2 = 0.f, sa1 = 0.f, sb2 = 0.f, sb1 = 0.f, ma = 0.f, mb = 0.f;
-#pragma unroll 8
-  for (int i = 0; i < kChannels; i += 4) {
+#pragma unroll
+  for (int i = 0; i < kChannels / 4; i += 4) {
     const f32x4 va = *(const f32x4*)(wa + i), vb = *(const f32x4*)(wb + i);
-    const f32x4 g = *(const f32x4*)&gb_lds[0][i], b = *(const f32x4*)&gb_lds[1][i];
+    const f32x4 g = *(const f32x4*)&gb_lds[0][i0 + i], b = *(const f32x4*)&gb_lds[1][i0 + i];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float ga = g[e] * va[e], gbv = g[e] * vb[e];
@@ -213,40 +221,50 @@ __global__ __launch_bounds__(512) void transition_prep_kernel(TransitionArgs a) 
       mb = __builtin_elementwise_maximum(mb, __builtin_fabsf(gbv));
     }
   }
-  a.fbias[c] = sa1;
-  a.fbias[kHid + c] = sb1;
-  a.exps[kExpW + c] = plane_exp(ma);
-  a.exps[kExpW + kHid + c] = plane_exp(mb);
-  const float bg = __builtin_sqrtf(128.f * sa2) + __builtin_fabsf(sa1);
-  const float bv = __builtin_sqrtf(128.f * sb2) + __builtin_fabsf(sb1);
-  float bh = __builtin_elementwise_maximum(bg, 0.2785f) * bv;
-  // max |W_o| of output row c / 4, a quarter of it per thread, then per row
+  // the channel's four threads are lanes 4 q .. 4 q + 3
+#pragma unroll
+  for (int d = 1; d < 4; d <<= 1) {
+    sa2 += __shfl_xor(sa2, d);
+    sb2 += __shfl_xor(sb2, d);
+    sa1 += __shfl_xor(sa1, d);
+    sb1 += __shfl_xor(sb1, d);
+    ma = __builtin_elementwise_maximum(ma, __shfl_xor(ma, d));
+    mb = __builtin_elementwise_maximum(mb, __shfl_xor(mb, d));
+  }
+  float bh = 0.f;
+  if ((tid & 3) == 0) {
+    a.fbias[c] = sa1;
+    a.fbias[kHid + c] = sb1;
+    a.exps[kExpW + c] = plane_exp(ma);
+    a.exps[kExpW + kHid + c] = plane_exp(mb);
+    const float bg = __builtin_sqrtf(128.f * sa2) + __builtin_fabsf(sa1);
+    const float bv = __builtin_sqrtf(128.f * sb2) + __builtin_fabsf(sb1);
+    bh = __builtin_elementwise_maximum(bg, 0.2785f) * bv;
+  }
+  // max |W_o| of row 32 g + tid / 16, a sixteenth of it per thread
   {
-    const float* wo = a.w_o + (int64_t)(c >> 2) * kHid + (c & 3) * (kHid / 4);
+    const int o = (int)blockIdx.x * (kChannels / kPrepGroups) + (tid >> 4);
+    const float* wo = a.w_o + (int64_t)o * kHid + (tid & 15) * (kHid / 16);
     float mo = 0.f;
-#pragma unroll 8
-    for (int i = 0; i < kHid / 4; i += 4) {
+#pragma unroll
+    for (int i = 0; i < kHid / 16; i += 4) {
       const f32x4 v = *(const f32x4*)(wo + i);
       mo = __builtin_elementwise_maximum(
           mo, __builtin_elementwise_maximum(
                   __builtin_elementwise_maximum(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
                   __builtin_elementwise_maximum(__builtin_fabsf(v.z), __builtin_fabsf(v.w))));
     }
-    red_o[c] = mo;
+#pragma unroll
+    for (int d = 1; d < 16; d <<= 1) mo = __builtin_elementwise_maximum(mo, __shfl_xor(mo, d));
+    if ((tid & 15) == 0) a.exps[kExpO + o] = plane_exp(mo);
   }
   bh = wave_max(bh);
-  if ((c & 63) == 0) red[c >> 6] = bh;
+  if ((tid & 63) == 0) red[tid >> 6] = bh;
   __syncthreads();
-  if (c < kChannels) {
-    const float m01 = __builtin_elementwise_maximum(red_o[4 * c], red_o[4 * c + 1]);
-    const float m23 = __builtin_elementwise_maximum(red_o[4 * c + 2], red_o[4 * c + 3]);
-    a.exps[kExpO + c] = plane_exp(__builtin_elementwise_maximum(m01, m23));
-  }
-  if (c == 0) {
+  if (tid == 0) {
     for (int i = 1; i < 8; ++i) bh = __builtin_elementwise_maximum(bh, red[i]);
-    a.exps[kExpX] = plane_exp(11.3137085f * (1.0f + 0x1p-10f));
-    // the margin covers the roundings of the bound and of g, v and h
-    a.exps[kExpH] = plane_exp(bh * (1.0f + 0x1p-8f));
+    a.exps[kExpPart + blockIdx.x] = __builtin_bit_cast(int, bh);
+    if (blockIdx.x == 0) a.exps[kExpX] = plane_exp(11.3137085f * (1.0f + 0x1p-10f));
   }
 }
 
@@ -259,6 +277,13 @@ __global__ __launch_bounds__(512) void transition_prep_kernel(TransitionArgs a) 
 // read 512 contiguous bytes (no LDS bank conflicts).
 __global__ __launch_bounds__(256) void transition_planes_kernel(TransitionArgs a) {
   const int idx = (int)(blockIdx.x * 256 + threadIdx.x);
+  if (idx == 0) {
+    float bh = 0.f;
+    for (int g = 0; g < kPrepGroups; ++g)
+      bh = __builtin_elementwise_maximum(bh, __builtin_bit_cast(float, a.exps[kExpPart + g]));
+    // the margin covers the roundings of the bound and of g, v and h
+    a.exps[kExpH] = plane_exp(bh * (1.0f + 0x1p-8f));
+  }
   constexpr int kPer = kChunkValues / 2;  // values (hi, lo pairs) per chunk
   if (idx >= kChunks * kPer) return;
   const int c = idx / kPer;
@@ -481,7 +506,7 @@ hipError_t launch_transition(const TransitionArgs& a, hipStream_t stream) {
     if (a.planes == nullptr || a.fbias == nullptr || a.exps == nullptr) return hipErrorInvalidValue;
     const int64_t tiles = (rows + kFusedRows - 1) / kFusedRows;
     const int64_t grid = tiles < device_cu_count() ? tiles : device_cu_count();
-    hipLaunchKernelGGL(transition_prep_kernel, dim3(1), dim3(512), 0, stream, a);
+    hipLaunchKernelGGL(transition_prep_kernel, dim3(kPrepGroups), dim3(512), 0, stream, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(transition_planes_kernel, dim3((kChunks * kChunkValues / 2 + 255) / 256),
                        dim3(256), 0, stream, a);
