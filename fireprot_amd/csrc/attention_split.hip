@@ -82,10 +82,12 @@ __device__ __forceinline__ int v_position(int g) {
 
 // Rows whose mask bias is one finite nonzero value m on every key < n
 // (padding rows: inf (mask - 1) = -1e9), when the products are bounded below
-// half a unit in the last place of m: then fl(s + m) = m for every key
-// (|s| <= 32 max|q| max|k|, with a margin for the native rounding of s), so
-// the native logit fl(fl(s + m) + bias) is fl(m + bias), the same for every
-// such row.
+// half the float32 spacing next to m on either side: then fl(s + m) = m for
+// every key (|s| <= 32 max|q| max|k|, with a margin for the native rounding
+// of s), so the native logit fl(fl(s + m) + bias) is fl(m + bias), the same
+// for every such row.  With |m| = f 2^e, f in [0.5, 1), the spacing above
+// |m| is 2^(e - 24); toward zero it is the same unless |m| is a power of two
+// (f = 0.5), where it halves.
 __device__ __forceinline__ bool constant_mask_row(const AttnArgs& a, int b, float& m) {
   if (a.magnitudes == nullptr || a.magnitudes[4] != 1u) return false;
   const uint32_t* f3 =
@@ -97,7 +99,9 @@ __device__ __forceinline__ bool constant_mask_row(const AttnArgs& a, int b, floa
   const float mq = __builtin_bit_cast(float, a.magnitudes[0]);
   const float mk = __builtin_bit_cast(float, a.magnitudes[1]);
   const float s_bound = 32.0f * mq * mk * (1.0f + 0x1p-10f);
-  const float half_ulp = __builtin_ldexpf(1.0f, __builtin_amdgcn_frexp_expf(hi) - 25);
+  const bool power_of_two = (__builtin_bit_cast(uint32_t, hi) & 0x7fffffu) == 0u;
+  const float half_ulp =
+      __builtin_ldexpf(1.0f, __builtin_amdgcn_frexp_expf(hi) - (power_of_two ? 26 : 25));
   m = hi;
   return s_bound < half_ulp;
 }

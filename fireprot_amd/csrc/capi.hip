@@ -509,15 +509,15 @@ int fpx_attn_core_masked(const float* q, const float* k, const float* v, const f
 
 int fpx_attn_core(float* q, float* k, float* v, float* bias, float* out, int batch, int n,
                   void* stream) {
-  // the reference's physical bias row stride (fireprot_ck_attention.cpp:37)
-  return fpx_attn_core_masked(q, k, v, nullptr, 0, bias, n == 1536 ? n + 16 : n, out, batch, n,
-                              stream);
+  return fpx_attn_core_masked(q, k, v, nullptr, 0, bias, n, out, batch, n, stream);
 }
 
 int ck_attention(float* q, float* k, float* v, float* bias, float* out, int batch, int n,
                  void* stream) {
   if (!((batch == 1000 && n == 1000) || (batch == 512 && n == 1536))) return FPX_ERR_DIMS;
-  return fpx_attn_core(q, k, v, bias, out, batch, n, stream);
+  // the reference's physical bias row stride (fireprot_ck_attention.cpp:37)
+  return fpx_attn_core_masked(q, k, v, nullptr, 0, bias, n == 1536 ? n + 16 : n, out, batch, n,
+                              stream);
 }
 
 int ck_attention_exact1536(float* q, float* k, float* v, float* bias, float* out, int batch,
@@ -691,11 +691,12 @@ int fpx_transition(const float* x, int64_t rows_i, int64_t rows_j, int64_t x_str
   const size_t need = fpx_transition_workspace_bytes(rows_i, rows_j, c, expansion);
   if (need == 0) return FPX_ERR_DIMS;
   if (accumulate != 0 && accumulate != 1) return FPX_ERR_DIMS;
-  if (x_stride_i < 0 || x_stride_j < 0 || x_stride_i % 2 || x_stride_j % 2) return FPX_ERR_DIMS;
+  // x rows are read as 16-byte vectors: strides in multiples of 4 floats
+  if (x_stride_i < 0 || x_stride_j < 0 || x_stride_i % 4 || x_stride_j % 4) return FPX_ERR_DIMS;
   if (out_stride_i < 0 || out_stride_j < 0) return FPX_ERR_DIMS;
   if (!(eps >= 0.0f)) return FPX_ERR_DIMS;
   if (out == x && (out_stride_i != x_stride_i || out_stride_j != x_stride_j)) return FPX_ERR_DIMS;
-  if (!aligned(x, 8) || !aligned(w_a, 16) || !aligned(w_b, 16) || !aligned(w_o, 16) ||
+  if (!aligned(x, 16) || !aligned(w_a, 16) || !aligned(w_b, 16) || !aligned(w_o, 16) ||
       !aligned(out, 4) || !aligned_or_null(ln_w, 8) || !aligned_or_null(ln_b, 8))
     return FPX_ERR_POINTER;
   if (!aligned(workspace, 256)) return FPX_ERR_POINTER;

@@ -91,14 +91,15 @@ def transition(x: torch.Tensor, weights: TransitionWeights, *, out: torch.Tensor
                accumulate: bool = False, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """One ``fpx_transition`` call on x's device and current stream.
 
-    ``x`` is ``[..., 128]`` float32 (3-D with any even row strides, otherwise
-    contiguous); the result has x's shape.  ``out=x, accumulate=True`` is the
+    ``x`` is ``[..., 128]`` float32 (3-D with row strides in multiples of 4
+    floats and a 16-byte aligned start, otherwise copied contiguous first);
+    the result has x's shape.  ``out=x, accumulate=True`` is the
     in-place ``x += transition(x)``.
     """
     if not x.is_cuda or x.dtype != torch.float32:
         raise ValueError("x must be a float32 tensor on a HIP device")
     src = _rows(x)
-    if src is None or src[2] % 2 or src[3] % 2 or x.data_ptr() % 8:
+    if src is None or src[2] % 4 or src[3] % 4 or x.data_ptr() % 16:
         x = x.contiguous()
         src = _rows(x)
     if out is None:

@@ -165,8 +165,11 @@ MAX_N = 4096  # the largest pair size the block's C ABI accepts
 _packed: "weakref.WeakKeyDictionary[Any, tuple[tuple, BlockWeights]]" = weakref.WeakKeyDictionary()
 
 
-def _parameter_key(module: Any) -> tuple:
-    """Identity, storage and version of every tensor _weights_of reads."""
+def _parameter_key(module: Any) -> tuple | None:
+    """Identity, storage and version of every tensor _weights_of reads, or
+    None when one of them is an inference tensor (created under
+    ``torch.inference_mode``: such tensors keep no version counter, so an
+    in-place change could not be seen and the weights are packed afresh)."""
     owners = ((module.layer_norm, module.linear, module.mha.linear_q, module.mha.linear_k,
                module.mha.linear_v, module.mha.linear_g, module.mha.linear_o)
               if hasattr(module, "mha") else
@@ -176,6 +179,8 @@ def _parameter_key(module: Any) -> tuple:
     for owner in owners:
         for name in ("weight", "bias"):
             t = getattr(owner, name, None)
+            if t is not None and t.is_inference():
+                return None
             key.append(None if t is None else
                        (id(t), t.data_ptr(), t._version, t.dtype, str(t.device)))
     key.append((float(getattr(module, "inf", 1e9)),))
@@ -189,7 +194,7 @@ def _weights_of(module: Any) -> BlockWeights:
         raise TypeError(f"unrecognised triangle-attention module {type(module).__name__}")
     try:
         key = _parameter_key(module)
-        hit = _packed.get(module)
+        hit = None if key is None else _packed.get(module)
     except TypeError:  # not weak-referenceable: no cache
         key, hit = None, None
     if hit is not None and hit[0] == key:

@@ -150,10 +150,10 @@ int fpx_tri_attn_finish(int dtype, const void* w_o, const void* b_o, int n, int 
  * n % 4 == 0 (the reference entries accept two shapes only).
  * q, k, v, out: [batch][heads=4][n][32] viewed with strides (n*128, 32, 128, 1),
  * i.e. memory [batch][n][4][32]; q already scaled by 1/sqrt(32).
- * bias: [1][4][n][S] shared by every batch row, with the reference's physical
- * row stride S = n + 16 at n == 1536 (ck_attention.py:126-130,
- * fireprot_ck_attention.cpp:37) and S = n otherwise.  Head stride n * S.
- * Requires 16-byte aligned pointers (status 3 otherwise). */
+ * bias: [1][4][n][n] contiguous, shared by every batch row (the reference's
+ * padded N = 1536 rows of 1552 floats are ck_attention's and
+ * ck_attention_exact1536's convention; fpx_attn_core_masked takes any row
+ * stride).  Requires 16-byte aligned pointers (status 3 otherwise). */
 int fpx_attn_core(float* q, float* k, float* v, float* bias, float* out, int batch, int n,
                   void* stream);
 
@@ -271,7 +271,7 @@ size_t fpx_transition_workspace_bytes(int64_t rows_i, int64_t rows_j, int c, int
  * transition_projection = silu(a) * b of kernels/amd/fireprot_amd_ops.cu:
  * 1111-1165, then linear_no_bias), for any row count.
  *   x        rows x[i][j] at x + i*x_stride_i + j*x_stride_j, 128 channels
- *            with stride 1 (strides even, x 8-byte aligned); a flat
+ *            with stride 1 (strides multiples of 4, x 16-byte aligned); a flat
  *            [rows][128] tensor is rows_i = 1, x_stride_j = 128
  *   ln_w/b   nullable LayerNorm affine [128]; eps as in the module (1e-5)
  *   w_a, w_b [512][128]; w_o [128][512] (torch [out, in], no biases)

@@ -265,3 +265,20 @@ def test_packed_block_weights_are_cached_until_a_parameter_changes():
     third = ta._weights_of(m)
     assert third is not second and torch.equal(third.w_o, m.mha.linear_o.weight)
     assert ta._weights_of(m) is third
+
+
+def test_modules_built_under_inference_mode_are_packed_without_the_cache():
+    """Parameters created under torch.inference_mode are inference tensors,
+    which keep no version counter: the packed weights are rebuilt on every
+    call (an in-place change under inference mode stays visible) and the
+    eligibility check passes instead of raising."""
+    with torch.inference_mode():
+        m = _TriangleAttentionModule()
+        first = ta._weights_of(m)
+        assert torch.equal(first.w_qkvg[:128], m.mha.linear_q.weight)
+        m.mha.linear_q.weight.mul_(3.0)
+        second = ta._weights_of(m)
+    assert second is not first
+    assert torch.equal(second.w_qkvg[:128], m.mha.linear_q.weight)
+    ok, reason = ta.block_eligible(m, _FakeHipTensor(8), None)  # weights and "z" on the CPU
+    assert ok and reason == "", reason

@@ -94,13 +94,19 @@ def test_reference_attention_flow(entry_name, batch, n):
     _check_rows(f"{entry_name} b={batch} n={n}", out.transpose(-2, -3), q, k, v, bias, rows)
 
 
-def test_fpx_attn_core_reads_the_reference_padded_rows_at_1536():
-    """fpx_attn_core keeps ck_attention's physical bias row stride at N=1536,
-    for a batch the reference entries do not accept."""
+def test_fpx_attn_core_reads_a_contiguous_bias_at_1536():
+    """fpx_attn_core reads a contiguous [1, 4, N, N] bias at every N, N=1536
+    included, for a batch the reference entries do not accept (the padded
+    1552-float rows are the ck_attention* entries' convention only)."""
     batch, n = 3, 1536
     q, k, v, bias = _operands(batch, n, 77)
+    entry = _bound("fpx_attn_core")
     with torch.inference_mode():
-        out = _reference_call(_bound("fpx_attn_core"), q, k, v, [bias])
+        output = torch.empty_like(q)
+        status = entry(q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.contiguous().data_ptr(),
+                       output.data_ptr(), batch, n, torch.cuda.current_stream().cuda_stream)
+        assert status == 0, status
+        out = output.transpose(-2, -3)
         torch.cuda.synchronize()
     _check_rows("fpx_attn_core b=3 n=1536", out.transpose(-2, -3), q, k, v, bias,
                 torch.arange(batch))

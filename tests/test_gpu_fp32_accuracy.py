@@ -158,23 +158,28 @@ def test_positive_mask_bias_rows_take_the_exact_path():
             strict_close(f"positive mask ending={ending} {region}", actual[sel], ref64, ref32)
 
 
-@pytest.mark.parametrize("qk_scale", [1.0, 8.0])
-def test_padding_rows_with_and_without_the_constant_mask_shortcut(qk_scale):
+@pytest.mark.parametrize("qk_scale,inf", [(1.0, 1e9), (8.0, 1e9), (2.5, 2.0 ** 30)])
+def test_padding_rows_with_and_without_the_constant_mask_shortcut(qk_scale, inf):
     """Padding rows carry one mask bias (-1e9) on every key.  While
     32 max|q| max|k| stays below half its float32 spacing (32), fl(s + m) = m
     and the attention skips S^T for them (qk_scale 1); scaling W_q and W_k by
     8 lifts |s| past that bound, so the same rows take the full exact path
-    with logits spread over several float32 buckets of -1e9.  Both must meet
-    the FP32 bar against float64 with float32-rounded logits."""
+    with logits spread over several float32 buckets of -1e9.  With
+    inf = 2^30 the mask bias -2^30 is a power of two: its spacing is 128
+    above |m| but 64 toward zero, so the bound is 32, not 64, and at
+    qk_scale 2.5 (32 max|q| max|k| = 51.6 on this workload) the rows must
+    take the exact path too.  All must meet the FP32 bar against float64
+    with float32-rounded logits."""
     n, valid = 160, 130
     z = workloads.make_pair(n)
     mask = workloads.make_mask(n, valid)
     w = workloads.make_weights(bias_scale=4.0)
     w["w_q"] = w["w_q"] * qk_scale
     w["w_k"] = w["w_k"] * qk_scale
+    w["inf"] = inf
     rows = torch.arange(n)
     for ending in (False, True):
-        print(f"case padding rows qk x{qk_scale} ending={ending}", flush=True)
+        print(f"case padding rows qk x{qk_scale} inf={inf:g} ending={ending}", flush=True)
         actual = _run_rows(z, mask, w, ending, rows)
-        _check_regions(f"padding qk x{qk_scale} ending={ending}", actual, z, mask, w, ending, rows,
-                       valid)
+        _check_regions(f"padding qk x{qk_scale} inf={inf:g} ending={ending}", actual, z, mask, w,
+                       ending, rows, valid)

@@ -79,6 +79,42 @@ def test_strided_flat_and_in_place():
     assert_f32_parity("in place", target.cpu(), z + expected)
 
 
+def test_x_offset_by_two_floats():
+    """x rows are read as 16-byte vectors: an x that starts 8 bytes past a
+    16-byte boundary is refused by the C ABI (status 3, before any launch)
+    and copied to an aligned buffer by the host wrapper, with the same
+    result; an odd-multiple-of-2 row stride is refused with status 2."""
+    from fireprot_amd import _native
+
+    n = 24
+    w = workloads.make_transition_weights(affine=True)
+    z = workloads.make_pair(n)
+    expected = tr.transition(z, _params(w))
+    wt = _hip(w)
+    buf = torch.zeros(n * n * 128 + 8, device="cuda")
+    x = buf[2:2 + n * n * 128].view(n, n, 128)
+    x.copy_(z.cuda())
+    assert x.data_ptr() % 16 == 8
+    lib = _native.library()
+    size = lib.fpx_transition_workspace_bytes(n, n, 128, 4)
+    ws = torch.empty(size, dtype=torch.uint8, device="cuda")
+    out = torch.empty(n, n, 128, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def call(ptr, si, sj):
+        return lib.fpx_transition(ptr, n, n, si, sj, wt.ln_w.data_ptr(), wt.ln_b.data_ptr(),
+                                  wt.eps, wt.w_a.data_ptr(), wt.w_b.data_ptr(),
+                                  wt.w_o.data_ptr(), 128, 4, 0, out.data_ptr(), n * 128, 128,
+                                  ws.data_ptr(), ws.numel(), stream)
+
+    assert call(x.data_ptr(), n * 128, 128) == 3
+    assert call(buf.data_ptr(), n * 128 + 2, 128) == 2
+    with torch.inference_mode():
+        actual = htr.transition(x, wt)
+        torch.cuda.synchronize()
+    assert_f32_parity("x offset by 2 floats", actual.cpu(), expected)
+
+
 def test_n1536_rows_and_determinism():
     n = 1536
     print("case transition n1536", flush=True)
