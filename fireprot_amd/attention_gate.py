@@ -14,7 +14,7 @@ from collections import Counter
 from collections.abc import Callable
 from typing import Any
 
-from . import _native
+from . import _native, switches
 from .triangle_attention import ARCHITECTURE, HEAD_DIM, HEADS, _architecture
 
 _lock = threading.RLock()
@@ -43,6 +43,8 @@ def sigmoid_mul_out(gate: Any, value: Any) -> Any:
 def supported(module: Any, o: Any, x: Any) -> bool:
     import torch
 
+    if switches.disabled("FPX_DISABLE_ATTENTION_GATE"):
+        return False
     if module.training or torch.is_grad_enabled():
         return False
     if getattr(module, "linear_g", None) is None:

@@ -15,7 +15,7 @@ from collections import Counter
 from collections.abc import Callable
 from typing import Any
 
-from . import _native
+from . import _native, switches
 from .triangle_attention import ARCHITECTURE, _architecture
 
 CHANNELS = 128
@@ -57,6 +57,8 @@ def layer_norm_c128(x: Any, weight: Any, bias: Any, eps: float) -> Any:
 def eligible(module: Any, x: Any) -> tuple[bool, str]:
     import torch
 
+    if (off := switches.rejection("FPX_DISABLE_LAYER_NORM")) is not None:
+        return off
     if getattr(x, "device", None) is None or x.device.type != "cuda":
         return False, "device is not CUDA/HIP"
     if _architecture(x) != ARCHITECTURE:

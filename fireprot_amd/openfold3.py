@@ -49,7 +49,7 @@ from contextvars import ContextVar
 from pathlib import Path
 from typing import Any
 
-from . import _native
+from . import _native, switches
 from .registry import OperationRegistry, signature_from_tensor
 
 # The upstream openfold3/core/model/primitives/attention.py the hook is written
@@ -277,6 +277,8 @@ class AttentionDispatcher:
         return False, attributes.get("reason") or "tensor contract mismatch"
 
     def _eligible(self, query: Any, key: Any, value: Any, biases: Any) -> tuple[bool, str]:
+        if (off := switches.rejection("FPX_DISABLE_OPENFOLD3_ATTENTION")) is not None:
+            return off
         if self.kernel is None:
             return False, "no HIP kernel"
         ok, reason = tensor_contract(query, key, value, biases)

@@ -14,7 +14,7 @@ from collections import Counter
 from collections.abc import Callable
 from typing import Any
 
-from . import _native
+from . import _native, switches
 from .triangle_attention import ARCHITECTURE, HEAD_DIM, HEADS, _architecture
 
 CHANNELS = 128
@@ -46,6 +46,8 @@ def qkv_projection(x: Any, wq: Any, wk: Any, wv: Any) -> Any:
 def supported(module: Any, q_x: Any, kv_x: Any, apply_scale: bool) -> bool:
     import torch
 
+    if switches.disabled("FPX_DISABLE_QKV_PROJECTION"):
+        return False
     if module.training or torch.is_grad_enabled() or not apply_scale:
         return False
     if getattr(module, "no_heads", None) != HEADS or getattr(module, "c_hidden", None) != HEAD_DIM:

@@ -20,7 +20,8 @@ from typing import Any
 
 import torch
 
-from . import _native
+from . import _native, switches
+from . import workspace as ws_cache
 from .registry import OperationSignature, registry, signature_from_tensor
 
 OPERATION = "gated_transition"
@@ -173,6 +174,8 @@ def eligible(module: Any, x: Any) -> tuple[bool, str]:
 
 
 def _supports(signature: OperationSignature) -> bool | tuple[bool, str]:
+    if (off := switches.rejection("FPX_DISABLE_TRANSITION")) is not None:
+        return off
     attributes = dict(signature.attributes)
     if signature.device_type != "cuda":
         return False, "device is not CUDA/HIP"
@@ -193,7 +196,11 @@ def _supports(signature: OperationSignature) -> bool | tuple[bool, str]:
 
 def _hip(*, module: Any, x: Any, native: Callable[..., Any]) -> Any:
     del native
-    return transition(x, TransitionWeights.from_module(module).to(x.device))
+    src = _rows(x)
+    size = (_native.library().fpx_transition_workspace_bytes(src[0], src[1], CHANNELS, EXPANSION)
+            if src is not None else 0)
+    ws = ws_cache.get(x.device, size, purpose="transition") if size else None
+    return transition(x, TransitionWeights.from_module(module).to(x.device), workspace=ws)
 
 
 def dispatch_transition(*, module: Any, x: Any, native: Callable[..., Any]) -> Any:

@@ -9,9 +9,13 @@ reference's signature and builds the same ``OperationSignature``
 (python/fireprot/backends/amd/triangle_attention.py:199-256); the HIP
 candidate ``amd-gfx950-hip-attention-f32`` takes q/k/v ``[B, H, N, 32]`` in
 the head-last projection layout (strides ``(N*128, 32, 128, 1)``), the
-triangle bias ``[1, 4, N, N]`` and optionally the mask bias ``[B, 1, 1, N]``,
-and returns ``[B, N, H, 32]`` like the native lambda
-``_attention(q, k, v, biases).transpose(-2, -3)``.
+triangle bias ``[1, 4, N, N]`` (any strides) and optionally the mask bias
+``[B|1, 1, 1, N]``, and returns ``[B, N, H, 32]`` like the native lambda
+``_attention(q, k, v, biases).transpose(-2, -3)``.  It runs
+``fpx_attn_strided`` (q, k, v staged into power-of-two scaled fp16 planes,
+then the block's attention kernel on the 16-bit matrix cores, FP32-accurate)
+with a workspace cached per device and stream; the reference's workspace-less
+entries ``ck_attention*`` stay on the FP32 matrix cores.
 
 ``triangle_attention_block`` -- the whole module call ``(z, mask) -> dz``,
 as AtlasFold's per-instance hook dispatches it
@@ -25,12 +29,14 @@ path of this package.
 from __future__ import annotations
 
 import functools
+import math
 import weakref
 from collections.abc import Callable, Sequence
 from typing import Any
 
-from . import _native
-from .block import BlockWeights, triangle_attention_block
+from . import _native, switches
+from . import workspace as ws_cache
+from .block import BlockWeights, triangle_attention_block, workspace_bytes
 from .registry import OperationSignature, registry, signature_from_tensor
 
 OPERATION = "triangle_attention"
@@ -41,6 +47,7 @@ BLOCK_BF16_IMPLEMENTATION = "amd-gfx950-hip-block-bf16"
 ARCHITECTURE = "gfx950"
 HEADS = 4
 HEAD_DIM = 32
+MAX_N = 4096  # the largest pair size the block and strided C ABI entries accept
 
 
 @functools.lru_cache(maxsize=None)
@@ -72,6 +79,8 @@ def _mode(module: Any, tensors: Sequence[Any]) -> str:
 # ------------------------------------------------------------------ core
 
 def _supports_core(signature: OperationSignature) -> bool | tuple[bool, str]:
+    if (off := switches.rejection("FPX_DISABLE_ATTENTION")) is not None:
+        return off
     attributes = dict(signature.attributes)
     if signature.device_type != "cuda":
         return False, "device is not CUDA/HIP"
@@ -86,8 +95,8 @@ def _supports_core(signature: OperationSignature) -> bool | tuple[bool, str]:
     batch, heads, n, dim = signature.shape
     if heads != HEADS or dim != HEAD_DIM:
         return False, "requires 4 heads of dimension 32"
-    if n % 4:
-        return False, "sequence length must be a multiple of 4"
+    if not 1 <= n <= MAX_N:
+        return False, f"sequence length must lie in 1..{MAX_N}"
     strides = (n * HEADS * HEAD_DIM, HEAD_DIM, HEADS * HEAD_DIM, 1)
     if attributes.get("qkv_strides") != repr((strides,) * 3):
         return False, "q/k/v must use the head-last projection layout"
@@ -112,22 +121,28 @@ def attention(*, module: Any, q: Any, k: Any, v: Any, biases: Sequence[Any],
     del module, native
     lib = _native.library()
     batch, _, n, _ = q.shape
+    bias = biases[-1]
+    if bias.data_ptr() % 4:
+        bias = bias.contiguous()
+    mask_ptr, m_sb, m_sk = None, 0, 0
+    if len(biases) == 2:
+        mask = biases[0]
+        if mask.data_ptr() % 4:
+            mask = mask.contiguous()
+        mask_ptr = mask.data_ptr()
+        m_sb = mask.stride(0) if mask.shape[0] > 1 else 0
+        m_sk = mask.stride(3)
     with torch.cuda.device(q.device):
-        bias = biases[-1].contiguous()
-        if bias.data_ptr() % 16:
-            bias = bias.clone()
-        mask_ptr, mask_stride = None, 0
-        if len(biases) == 2:
-            mask = biases[0].reshape(biases[0].shape[0], n)
-            if mask.stride(-1) != 1:
-                mask = mask.contiguous()
-            mask_ptr = mask.data_ptr()
-            mask_stride = mask.stride(0) if mask.shape[0] > 1 else 0
         output = torch.empty((batch, n, HEADS, HEAD_DIM), device=q.device, dtype=q.dtype)
-        code = lib.fpx_attn_core_masked(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), mask_ptr, mask_stride, bias.data_ptr(),
-            n, output.data_ptr(), batch, n, torch.cuda.current_stream(q.device).cuda_stream)
-    _native.check(code, "fpx_attn_core_masked")
+        size = lib.fpx_attn_strided_workspace_bytes(batch, n)
+        ws = ws_cache.get(q.device, size, purpose="attention")
+        o = output.transpose(1, 2)  # [B, H, N, D] view of the head-last output
+        code = lib.fpx_attn_strided(
+            q.data_ptr(), *q.stride()[:3], k.data_ptr(), *k.stride()[:3],
+            v.data_ptr(), *v.stride()[:3], mask_ptr, m_sb, m_sk,
+            bias.data_ptr(), *bias.stride()[1:], o.data_ptr(), *o.stride()[:3], batch, n,
+            ws.data_ptr(), size, torch.cuda.current_stream(q.device).cuda_stream)
+    _native.check(code, "fpx_attn_strided")
     return output
 
 
@@ -158,7 +173,6 @@ def dispatch_triangle_attention(*, module: Any, q: Any, k: Any, v: Any, biases: 
 
 # ----------------------------------------------------------------- block
 
-MAX_N = 4096  # the largest pair size the block's C ABI accepts
 
 # Packed weights per module, rebuilt only when one of the module's parameter
 # tensors changes (identity, storage or in-place version) or the device does.
@@ -187,26 +201,63 @@ def _parameter_key(module: Any) -> tuple | None:
     return tuple(key)
 
 
-def _weights_of(module: Any) -> BlockWeights:
-    """The module's weights packed for the block (w_qkvg concatenated), cached
-    per module while its parameters are unchanged."""
+def _pack_dtype(z: Any) -> Any:
+    """z's dtype when a CUDA autocast region computes in it (the module's
+    linears would then run on weights cast to it), else None: keep the
+    weights' own dtype."""
+    import torch
+
+    try:
+        if torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == z.dtype:
+            return z.dtype
+    except (AttributeError, TypeError):
+        pass
+    return None
+
+
+def _weights_of(module: Any, dtype: Any = None) -> BlockWeights:
+    """The module's weights packed for the block (w_qkvg concatenated) in
+    ``dtype`` (default: the weights' own), cached per module while its
+    parameters are unchanged."""
     if not (hasattr(module, "mha") or hasattr(module, "linear_qkv")):
         raise TypeError(f"unrecognised triangle-attention module {type(module).__name__}")
     try:
         key = _parameter_key(module)
+        key = None if key is None else key + ((str(dtype),),)
         hit = None if key is None else _packed.get(module)
     except TypeError:  # not weak-referenceable: no cache
         key, hit = None, None
     if hit is not None and hit[0] == key:
         return hit[1]
-    weights = (BlockWeights.from_protenix(module) if hasattr(module, "mha")
-               else BlockWeights.from_atlasfold(module))
+    weights = (BlockWeights.from_protenix(module, dtype=dtype) if hasattr(module, "mha")
+               else BlockWeights.from_atlasfold(module, dtype=dtype))
     if key is not None:
         try:
             _packed[module] = (key, weights)
         except TypeError:
             pass
     return weights
+
+
+def _has_hooks(module: Any) -> bool:
+    """Forward hooks on the module or the layers the block reads, or a
+    ``precision`` override on them: the fused block would skip them
+    (atlasfold/runtime.py:224-233 rejects the same)."""
+    import torch
+
+    layers = ((module.layer_norm, module.linear, module.mha, module.mha.linear_q,
+               module.mha.linear_k, module.mha.linear_v, module.mha.linear_g, module.mha.linear_o)
+              if hasattr(module, "mha") else
+              (getattr(module, "layernorm", None), getattr(module, "linear_qkv", None),
+               getattr(module, "linear_bias", None), getattr(module, "linear_g", None),
+               getattr(module, "linear_out", None)))
+    for layer in (module, *layers):
+        if isinstance(layer, torch.nn.Module) and (layer._forward_hooks or
+                                                   layer._forward_pre_hooks):
+            return True
+        if layer is not module and getattr(layer, "precision", None) is not None:
+            return True
+    return False
 
 
 def block_eligible(module: Any, z: Any, mask: Any) -> tuple[bool, str]:
@@ -229,9 +280,14 @@ def block_eligible(module: Any, z: Any, mask: Any) -> tuple[bool, str]:
                   getattr(module, "channel_hidden", None))
     if heads != HEADS or dim != HEAD_DIM:
         return False, "module must have 4 heads of dimension 32"
+    scale = getattr(module, "scale", None)
+    if scale is not None and abs(float(scale) * math.sqrt(HEAD_DIM) - 1.0) > 1e-6:
+        return False, "module q scale is not 1/sqrt(32)"
     try:
-        weights = _weights_of(module)
-    except (AttributeError, TypeError, ValueError) as error:
+        if _has_hooks(module):
+            return False, "module or one of its layers carries forward hooks or a precision override"
+        weights = _weights_of(module, _pack_dtype(z))
+    except (AttributeError, TypeError, ValueError, RuntimeError) as error:
         return False, f"module layout: {error}"
     if any(t is not None and (t.device != z.device or t.dtype != z.dtype)
            for t in weights.tensors()):
@@ -241,6 +297,9 @@ def block_eligible(module: Any, z: Any, mask: Any) -> tuple[bool, str]:
 
 def _supports_block(signature: OperationSignature, *,
                     dtype: str = "float32") -> bool | tuple[bool, str]:
+    flag = "FPX_DISABLE_BLOCK" if dtype == "float32" else "FPX_DISABLE_BLOCK_BF16"
+    if (off := switches.rejection(flag)) is not None:
+        return off
     attributes = dict(signature.attributes)
     if signature.device_type != "cuda":
         return False, "device is not CUDA/HIP"
@@ -258,9 +317,11 @@ def _supports_block(signature: OperationSignature, *,
 
 
 def _block(*, module: Any, z: Any, mask: Any, ending: bool, native: Any) -> Any:
+    """One block call with the workspace cached for z's device and stream."""
     del native
-    return triangle_attention_block(z, mask, _weights_of(module).to(z.device), ending=ending)
-
+    ws = ws_cache.get(z.device, workspace_bytes(z.shape[0], z.dtype), purpose="block")
+    weights = _weights_of(module, _pack_dtype(z)).to(z.device)
+    return triangle_attention_block(z, mask, weights, ending=ending, workspace=ws)
 
 
 def dispatch_triangle_attention_block(*, module: Any, z: Any, mask: Any, ending: bool,

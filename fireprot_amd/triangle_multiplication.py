@@ -35,7 +35,8 @@ from typing import Any
 
 import torch
 
-from . import _native
+from . import _native, switches
+from . import workspace as ws_cache
 from .registry import OperationSignature, registry, signature_from_tensor
 
 OPERATION = "triangle_multiplication"
@@ -216,6 +217,8 @@ def eligible(module: Any, z: Any, mask: Any) -> tuple[bool, str]:
 
 
 def _supports(signature: OperationSignature) -> bool | tuple[bool, str]:
+    if (off := switches.rejection("FPX_DISABLE_TRIANGLE_MULTIPLICATION")) is not None:
+        return off
     attributes = dict(signature.attributes)
     if signature.device_type != "cuda":
         return False, "device is not CUDA/HIP"
@@ -239,10 +242,11 @@ def _hip(*, module: Any, z: Any, mask: Any, inplace_safe: bool, add_with_inplace
     del inplace_chunk_size, native
     weights = TriMulWeights.from_module(module).to(z.device)
     outgoing = bool(module._outgoing)
+    ws = ws_cache.get(z.device, workspace_bytes(z.shape[0]), purpose="triangle_multiplication")
     if inplace_safe:
         return triangle_multiplication(z, mask, weights, outgoing=outgoing, out=z,
-                                       accumulate=add_with_inplace)
-    return triangle_multiplication(z, mask, weights, outgoing=outgoing)
+                                       accumulate=add_with_inplace, workspace=ws)
+    return triangle_multiplication(z, mask, weights, outgoing=outgoing, workspace=ws)
 
 
 def dispatch_triangle_multiplication(*, module: Any, z: Any, mask: Any, inplace_safe: bool,

@@ -152,3 +152,38 @@ def make_inputs(cfg: Workload | str):
         cfg = CONFIGS[cfg]
     return (make_pair(cfg.n, cfg.z_scale), make_mask(cfg.n, cfg.valid),
             make_weights(cfg.bias_scale))
+
+
+def make_protenix_module(weights: dict[str, torch.Tensor | None], *, starting: bool = True,
+                         device: str | torch.device = "cpu") -> torch.nn.Module:
+    """A module with Protenix ``TriangleAttention``'s attributes
+    (patches/protenix/0005-*.patch:32-45: ``layer_norm``, ``linear``,
+    ``mha.linear_{q,k,v,g,o}``, ``mha.no_heads``, ``mha.c_hidden``, ``inf``,
+    ``starting``) holding ``weights`` (``make_weights`` layout), in eval mode.
+    It has no forward of its own: it is the ``module`` argument of the block
+    dispatch, which reads its weights."""
+    def linear(w, b=None):
+        layer = torch.nn.Linear(w.shape[1], w.shape[0], bias=b is not None)
+        with torch.no_grad():
+            layer.weight.copy_(w)
+            if b is not None:
+                layer.bias.copy_(b)
+        return layer
+
+    module = torch.nn.Module()
+    module.starting = starting
+    module.layer_norm = torch.nn.LayerNorm(weights["ln_w"].shape[0])
+    with torch.no_grad():
+        module.layer_norm.weight.copy_(weights["ln_w"])
+        module.layer_norm.bias.copy_(weights["ln_b"])
+    module.linear = linear(weights["w_bias"])
+    module.mha = torch.nn.Module()
+    module.mha.linear_q = linear(weights["w_q"])
+    module.mha.linear_k = linear(weights["w_k"])
+    module.mha.linear_v = linear(weights["w_v"])
+    module.mha.linear_g = linear(weights["w_g"], weights["b_g"])
+    module.mha.linear_o = linear(weights["w_o"], weights["b_o"])
+    module.mha.no_heads = weights["w_bias"].shape[0]
+    module.mha.c_hidden = weights["w_q"].shape[0] // module.mha.no_heads
+    module.inf = float(weights.get("inf", 1e9) or 1e9)
+    return module.to(device).eval()

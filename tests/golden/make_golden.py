@@ -11,6 +11,9 @@ expected outputs in float64:
   dz_{start,end}_f32l -- the same, with every logit rounded to float32 at the
                          native add points (mask, then bias), which is what the
                          FP32 native path does to fully masked rows
+  dz_{start,end}_bf16 -- the native path on bfloat16 tensors: every stored
+                         intermediate rounded to bfloat16 where the native
+                         BF16 path stores it (brute.block rounding="bf16")
 
 Cases (H=4, d=32, c=128):
   n5_plain      N=5, no mask, LN gamma=1/beta=0, no gate/out biases
@@ -65,6 +68,7 @@ def _case(name, n, mask, weights):
     for ending, tag in ((False, "start"), (True, "end")):
         for mode, suffix in (("f64", "f64"), ("f32", "f32l")):
             arrays[f"dz_{tag}_{suffix}"] = brute.block(z, mask, params, ending=ending, logits=mode)
+        arrays[f"dz_{tag}_bf16"] = brute.block(z, mask, params, ending=ending, rounding="bf16")
     np.savez_compressed(OUT / f"{name}.npz", **arrays)
     print(f"wrote {name}.npz", flush=True)
 

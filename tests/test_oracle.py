@@ -3,14 +3,18 @@
 * against the committed fixtures written by the independent float64 brute
   force (tests/golden/make_golden.py): the float64 oracle to 1e-10, the FP32
   oracle to the float32-logit expectation (which fixes the native treatment of
-  fully masked rows);
+  fully masked rows), the BF16 oracle to the expectation with every stored
+  intermediate rounded to bfloat16 at the native points (equal up to a rare
+  last-place flip);
 * against closed forms of the core (N=1, uniform logits, a +80 key, an all
   -inf row, v = 1) and of LayerNorm and the gate;
 * against invariants (key permutation, masked keys, outer-row chunking, the
   ending node as T o start o T);
 * and by planting plausible mistakes in a copy of the oracle (a transposed
   bias, a transposed mask, a dropped gate, an unbiased variance, bias added
-  before the mask) and checking that the fixtures reject each one.
+  before the mask; for BF16: only the output rounded, the logits or the
+  softmax output kept in float32) and checking that the fixtures reject each
+  one.
 """
 from __future__ import annotations
 
@@ -239,6 +243,83 @@ def test_planted_mistakes_are_rejected(kind, monkeypatch):
 
 
 # ---------------------------------------------------------------- BF16 oracle
+
+def _bf16_mismatch(dz: torch.Tensor, ref: torch.Tensor) -> tuple[float, float]:
+    """(largest |dz - ref| in units of ref's bfloat16 spacing, fraction of
+    elements that differ)."""
+    dz, ref = dz.double(), ref.double()
+    spacing = torch.ldexp(torch.ones_like(ref), torch.frexp(ref.abs().float())[1].double() - 8)
+    spacing = torch.where(ref == 0, torch.full_like(ref, 2.0 ** -133), spacing)
+    diff = (dz - ref).abs()
+    return float((diff / spacing).max()), float((diff > 0).double().mean())
+
+
+@pytest.mark.parametrize("name", CASES)
+@pytest.mark.parametrize("ending", [False, True])
+def test_bf16_oracle_matches_the_bf16_brute_force(name, ending):
+    """block_bf16 (the native ops on bfloat16 tensors) against the brute force
+    with every stored intermediate rounded to bfloat16 at the native points
+    (``brute.block(rounding="bf16")``: the rounding points of
+    fireprot_pair_softmax.cu:19-26 and fireprot_mask_bias.cu:9-22): equal
+    except where a float32 sum and its float64 counterpart round to
+    neighbouring bfloat16 values."""
+    z, mask, params, expected = load_case(name, torch.float32)
+    tag = "end" if ending else "start"
+    dz = oracle.block_bf16(z, mask, params, ending=ending)
+    assert dz.dtype == torch.bfloat16
+    ulps, frac = _bf16_mismatch(dz, expected[f"dz_{tag}_bf16"])
+    assert ulps <= 1.0 and frac <= 0.02, (ulps, frac)
+
+
+def _bf16_mistake(kind, z, mask, params, ending):
+    """block_bf16 with one plausible rounding mistake."""
+    if kind == "output_only":  # FP32 arithmetic, only dz rounded
+        wr = oracle.BlockParams(**{k: (v.to(torch.bfloat16).float()
+                                       if isinstance(v, torch.Tensor) else v)
+                                   for k, v in params.__dict__.items()})
+        return oracle.block(z.to(torch.bfloat16).float(), mask, wr,
+                            ending=ending).to(torch.bfloat16)
+    if kind == "fp32_probs":  # the softmax output kept in float32 for P V
+        orig = oracle.attention_core
+
+        def core(q, k, v, biases, **kw):
+            a = torch.matmul(q, k.transpose(-1, -2))
+            for b in biases:
+                a += b
+            return torch.matmul(torch.softmax(a.float(), -1), v.float()).to(q.dtype)
+        oracle.attention_core = core
+    elif kind == "fp32_logits":  # q k^T and both adds kept in float32, softmax input rounded
+        orig = oracle.attention_core
+
+        def core(q, k, v, biases, **kw):
+            a = torch.matmul(q.float(), k.float().transpose(-1, -2))
+            for b in biases:
+                a = a + b.float()
+            return torch.matmul(torch.softmax(a.to(q.dtype), -1), v)
+        oracle.attention_core = core
+    else:
+        raise ValueError(kind)
+    try:
+        return oracle.block_bf16(z, mask, params, ending=ending)
+    finally:
+        oracle.attention_core = orig
+
+
+@pytest.mark.parametrize("kind", ["output_only", "fp32_probs", "fp32_logits"])
+def test_bf16_fixtures_reject_planted_rounding_mistakes(kind):
+    """Each mistake leaves the BF16 result close to the correct one, so only
+    the rounding points tell it apart: the bf16 brute-force fixtures must
+    reject it.  (Adding the bias before the mask is no mistake in BF16: the
+    bfloat16 spacing at -1e9 is 2^22, so both orders give the same logits.)"""
+    rejected = []
+    for name in CASES:
+        z, mask, params, expected = load_case(name, torch.float32)
+        for ending, tag in ((False, "start"), (True, "end")):
+            dz = _bf16_mistake(kind, z, mask, params, ending)
+            ulps, frac = _bf16_mismatch(dz, expected[f"dz_{tag}_bf16"])
+            rejected.append(ulps > 1.0 or frac > 0.02)
+    assert any(rejected), f"the bf16 fixtures did not catch {kind}"
+
 
 @pytest.mark.parametrize("ending", [False, True])
 def test_bf16_oracle_tracks_fp32_oracle_within_bf16_error(ending):
