@@ -195,6 +195,94 @@ def parity_report(cfg, gpu: dict, oracle_out: dict) -> dict:
         report[key] = entry
     return report
 
+F32_ATOL = 1e-4
+F32_RTOL = 1e-4
+FP32_BAR_REL = 2e-6
+BF16_RTOL = 2e-2
+BF16_FLOOR = 1e-3
+
+
+def sample_rows(n: int, valid: int | None, count: int = 12, seed: int = 11):
+    """Outer rows for the float64 comparison: both ends, the middle, both
+    sides of the masked tail, and ``count`` seeded draws."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    rows = {0, 1, n - 1, n // 2}
+    if valid is not None and valid < n:
+        rows |= {valid - 1, valid, min(valid + 1, n - 1)}
+    rows |= set(torch.randint(0, n, (count,), generator=g).tolist())
+    return torch.tensor(sorted(rows))
+
+
+def parity_gate(cfg, gpu: dict, oracle_out: dict, z_cpu, mask_cpu, weights) -> dict:
+    """The parity bars the headline is gated on, on the timed step's outputs.
+
+    FP32 configurations:
+      - functional bar (the stated FP32 tolerance), every element of both
+        nodes: |GPU - FP32 oracle| <= 1e-4 + 1e-4 |FP32 oracle|, NaN where it is;
+      - FP32 bar on sampled outer rows of both nodes, valid and padded rows
+        apart: max |GPU - float64 oracle| <= max(2e-6 max|ref|, 2 x the FP32
+        oracle's own error); padded (fully masked) rows against float64 with
+        float32-rounded logits, which reproduces the native ties at -1e9.
+    BF16 (c5): the oracle's native-bf16 rows elementwise, |GPU - ref| <=
+    2e-2 |ref| + 1e-3 max|ref|.
+    """
+    import torch
+
+    from oracle import triangle_attention as oracle
+
+    valid = cfg.valid if cfg.valid is not None else cfg.n
+    gate = {"pass": True}
+    if cfg.dtype == "bf16":
+        for key in ("start", "end"):
+            rows, ref = oracle_out[f"{key}_rows"]
+            full = gpu[key].transpose(0, 1) if key == "end" else gpu[key]
+            got, ref = full[rows].double(), ref.double()
+            floor = BF16_FLOOR * float(ref.abs().max())
+            excess = ((got - ref).abs() - BF16_RTOL * ref.abs()).max()
+            worst = float(((got - ref).abs() / (ref.abs() + floor / BF16_RTOL)).max())
+            ok = bool(float(excess) <= floor) and bool(torch.isfinite(got).all())
+            gate[key] = {"rows": int(len(rows)), "bar": f"|d| <= {BF16_RTOL} |ref| + {floor:.3e}",
+                         "worst_rel_to_bar": round(worst / BF16_RTOL, 4), "pass": ok}
+            gate["pass"] &= ok
+        return gate
+    p32 = oracle.BlockParams(**weights)
+    p64 = p32.to(torch.float64)
+    z64 = z_cpu.double()
+    m64 = None if mask_cpu is None else mask_cpu.double()
+    rows = sample_rows(cfg.n, cfg.valid)
+    for key, ending in (("start", False), ("end", True)):
+        if key not in oracle_out:  # the CPU leg timed one node only
+            gate[key] = {"pass": True, "note": "no CPU oracle output for this node"}
+            continue
+        got = gpu[key].transpose(0, 1) if ending else gpu[key]
+        ref32 = oracle_out[key].transpose(0, 1) if ending else oracle_out[key]
+        nan_same = bool(torch.equal(torch.isnan(got), torch.isnan(ref32)))
+        close = bool(torch.isclose(got, ref32, rtol=F32_RTOL, atol=F32_ATOL, equal_nan=True).all())
+        entry = {"functional": {"elements": got.numel(), "bar": f"{F32_ATOL} + {F32_RTOL} |ref|",
+                                "pass": close and nan_same}}
+        ok = close and nan_same
+        for region, sel in (("valid", rows < valid), ("padded", rows >= valid)):
+            if not bool(sel.any()):
+                continue
+            sub = rows[sel]
+            ref64 = oracle.block(z64, m64, p64, ending=ending, outer_rows=sub,
+                                 logits_f32=(region == "padded"))
+            keep = ~torch.isnan(ref64)
+            err = float((got[sub].double() - ref64)[keep].abs().max())
+            err32 = float((ref32[sub].double() - ref64)[keep].abs().max())
+            ref = float(ref64[keep].abs().max())
+            bar = max(FP32_BAR_REL * ref, 2.0 * err32)
+            entry[f"fp32_{region}"] = {"rows": int(len(sub)), "max_abs": err,
+                                       "fp32_oracle_err": err32, "bar": bar,
+                                       "pass": err <= bar}
+            ok &= err <= bar
+        entry["pass"] = ok
+        gate[key] = entry
+        gate["pass"] &= ok
+    return gate
+
 
 OF3_METRIC = "OpenFold3 _attention ms + TFLOP/s (% MFMA peak) at B=N=1536 FP32, 1 GPU"
 
@@ -599,6 +687,192 @@ def bench_transition(args) -> dict:
     return result
 
 
+CORE_METRIC = ("triangle-attention core ms + TFLOP/s (% MFMA peak) at B=512 N=1536 FP32, "
+               "operator route, 1 GPU")
+
+
+def p95(values: list[float]) -> float:
+    """The reference benchmark's 95th percentile (benchmark_attention.py:190):
+    ordered[(95 len + 99) // 100 - 1]."""
+    ordered = sorted(values)
+    return ordered[(95 * len(ordered) + 99) // 100 - 1]
+
+
+def strict_rows(name: str, out, q, k, v, biases, rows) -> dict:
+    """The FP32 bar on outer (batch) rows ``rows`` of an attention-core
+    result ``out`` ``[B, 4, N, 32]``: max |out - float64| <= max(2e-6 max|ref|,
+    2 x the FP32 oracle's own error)."""
+    import torch
+
+    from oracle import triangle_attention as oracle
+
+    qs, ks, vs = (t[rows].cpu() for t in (q, k, v))
+    bs = [b[rows].cpu() if b.shape[0] > 1 else b.cpu() for b in biases]
+    ref64 = oracle.attention_core(qs.double(), ks.double(), vs.double(), [b.double() for b in bs])
+    ref32 = oracle.attention_core(qs, ks, vs, [b.clone() for b in bs])
+    got = out[rows].double().cpu()
+    nan_same = bool(torch.equal(torch.isnan(got), torch.isnan(ref64)))
+    keep = ~torch.isnan(ref64)
+    err = float((got - ref64)[keep].abs().max())
+    err32 = float((ref32.double() - ref64)[keep].abs().max())
+    ref = float(ref64[keep].abs().max())
+    bar = max(2e-6 * ref, 2.0 * err32)
+    rec = {"rows": [int(r) for r in rows], "max_abs": err, "fp32_oracle_err": err32,
+           "max_ref": ref, "bar": bar, "nan_positions_equal": nan_same,
+           "pass": bool(nan_same and err <= bar)}
+    log(f"parity {name}: {json.dumps(rec)}")
+    return rec
+
+
+def bench_core(args) -> dict:
+    """The operator-level route of Protenix's triangle attention: the attention
+    core ``_attention(q, k, v, [bias])`` per 512-row chunk at N=1536 and per
+    1000-row call at N=1000, with the reference benchmark's inputs and timing
+    (benchmarks/protenix/benchmark_attention.py:145-198): seed 419, q, k, v
+    ``[B, 4, N, 32]`` views of ``[B, N, 4, 32]`` with q / sqrt(32), the bias
+    ``[1, 4, N, N]`` a permuted view of ``[N, N, 4]``; each call bracketed by
+    its own HIP events with its bias packing and output allocation inside, 5
+    warmups (``--warmup``), 20 timed calls (``--steps``), median and p95.
+
+    Timed routes per shape:
+      - ``dispatch``: ``dispatch_triangle_attention`` -> the registered
+        candidate ``amd-gfx950-hip-attention-f32`` (``fpx_attn_strided``:
+        q, k, v staged into fp16 planes, the block's attention kernel on
+        them; workspace cached per device and stream);
+      - ``ck_attention_exact1536`` / ``ck_attention_vector_bias1000``: the
+        reference's C ABI entries called as its ``attention()`` calls them
+        (ck_attention.py:115-141: the bias packed into 1552-float rows at
+        N=1536), on the FP32 matrix cores.
+    ``value``: the dispatch route at B=512, N=1536.  Every record carries the
+    FP32 bar on four batch rows against the float64 oracle.
+    """
+    import ctypes
+    from types import SimpleNamespace
+
+    import torch
+
+    from fireprot_amd import _native
+    from fireprot_amd import triangle_attention as ta
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    lib = ctypes.CDLL(str(_native.LIB_PATH))
+    records = []
+    inputs = {}
+    warmup, reps = args.warmup, args.steps
+    for batch, n, entry_name in ((512, 1536, "ck_attention_exact1536"),
+                                 (1000, 1000, "ck_attention_vector_bias1000")):
+        torch.manual_seed(419)
+        with torch.inference_mode():
+            q, k, v = [torch.randn(batch, n, 4, 32, device=dev).transpose(1, 2) for _ in range(3)]
+            q.div_(32 ** 0.5)
+            bias = torch.randn(n, n, 4, device=dev).permute(2, 0, 1).unsqueeze(0)
+        inputs[n] = (q, k, v, bias)
+        entry = getattr(lib, entry_name)
+        entry.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int] * 2 + [ctypes.c_void_p]
+        entry.restype = ctypes.c_int
+
+        def ck_call(entry=entry, q=q, k=k, v=v, bias=bias, n=n):
+            if n == 1536:
+                packed = torch.empty((1, 4, 1536, 1552), device=dev, dtype=q.dtype)
+                packed[..., :1536].copy_(bias)
+            else:
+                packed = bias.contiguous()
+                if packed.data_ptr() % 16:
+                    packed = packed.clone()
+            output = torch.empty_like(q)
+            status = entry(q.data_ptr(), k.data_ptr(), v.data_ptr(), packed.data_ptr(),
+                           output.data_ptr(), q.shape[0], q.shape[2], stream.cuda_stream)
+            if status:
+                raise RuntimeError(f"{entry_name} returned {status}")
+            return output.transpose(-2, -3)
+
+        def dispatch(q=q, k=k, v=v, bias=bias):
+            return ta.dispatch_triangle_attention(
+                module=SimpleNamespace(training=False), q=q, k=k, v=v, biases=[bias],
+                native=lambda **_: (_ for _ in ()).throw(RuntimeError("native selected")))
+
+        flop = 4 * 4 * 32 * batch * n * n
+        for name, fn in (("dispatch", dispatch), (entry_name, ck_call)):
+            times = []
+            with torch.inference_mode():
+                for it in range(warmup + reps):
+                    e0 = torch.cuda.Event(enable_timing=True)
+                    e1 = torch.cuda.Event(enable_timing=True)
+                    e0.record(stream)
+                    result = fn()
+                    e1.record(stream)
+                    e1.synchronize()
+                    if it >= warmup:
+                        times.append(e0.elapsed_time(e1))
+            median = statistics_median(times)
+            rows = torch.tensor([0, 1, batch // 2, batch - 1])
+            # result is [B, N, 4, 32]; the oracle's layout is [B, 4, N, 32]
+            parity = strict_rows(f"{name} b={batch} n={n}", result.transpose(1, 2), q, k, v,
+                                 [bias], rows)
+            peak = BF16_MFMA_PEAK_TFLOPS if name == "dispatch" else FP32_MFMA_PEAK_TFLOPS
+            rec = {"route": name, "batch": batch, "n": n, "median_ms": round(median, 4),
+                   "p95_ms": round(p95(times), 4), "min_ms": round(min(times), 4),
+                   "tflops": round(flop / (median * 1e-3) / 1e12, 3),
+                   "matrix_peak": peak,
+                   "peak_frac": round(flop / (median * 1e-3) / 1e12 / peak, 4),
+                   "flop": flop, "parity": parity}
+            records.append(rec)
+            log(f"{name} b={batch} n={n}: median {median:.3f} ms, p95 {rec['p95_ms']:.3f} ms, "
+                f"{rec['tflops']} TFLOP/s")
+            del result
+            torch.cuda.empty_cache()
+        assert ta.registry.count(ta.OPERATION, ta.IMPLEMENTATION) >= warmup + reps
+    head = records[0]
+    ok = all(r["parity"]["pass"] for r in records)
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import triangle_attention as oracle
+
+        threads = host_cores()
+        torch.set_num_threads(threads)
+        q, k, v, bias = inputs[1536]
+        qs, ks, vs = (t.cpu() for t in (q, k, v))
+        bs = bias.cpu()
+        chunk = 64  # batch rows per oracle call: 2.4 GB of scores
+        with torch.inference_mode():
+            oracle.attention_core(qs[:1], ks[:1], vs[:1], [bs])
+            t0 = time.perf_counter()
+            for r in range(0, qs.shape[0], chunk):
+                oracle.attention_core(qs[r:r + chunk], ks[r:r + chunk], vs[r:r + chunk], [bs])
+            spent = time.perf_counter() - t0
+        cpu = {"value": round(head["flop"] / spent / 1e12, 5), "unit": "TFLOP/s",
+               "kind": "port",
+               "sample": (f"CPU oracle attention_core (native op order, FP32, {threads} "
+                          f"threads) on the whole B=512 N=1536 call, batch rows in chunks of "
+                          f"{chunk}: {spent:.2f} s"),
+               "call_s": round(spent, 3), **host_record(threads)}
+    return {
+        "metric": CORE_METRIC, "value": head["tflops"] if ok else None, "unit": "TFLOP/s",
+        "n_gpus": 1, "steps": reps, "warmup": warmup, "ms_per_step": head["median_ms"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (torch.manual_seed(419) q, k, v and bias as the reference benchmark)",
+        "config": {"workload": "core-b512-n1536-f32: Protenix _attention per 512-row chunk "
+                               "(operator route); also b1000-n1000",
+                   "records": records},
+        "roofline": {"kernel": "fpx_attn_strided (stage_planes_kernel + stage_bias_kernel + "
+                               "mask_rows_kernel + attention_split_kernel<kAttnStaged>), "
+                               "per call",
+                     "bound": "mfma", "achieved": head["tflops"], "peak": BF16_MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": head["peak_frac"],
+                     "traffic": recorded_traffic("core-b512-n1536"),
+                     "avg_launch_ms": head["median_ms"]},
+        "cpu_baseline": cpu,
+        "parity": {"pass": ok},
+    }
+
+
+def statistics_median(values: list[float]) -> float:
+    import statistics
+
+    return statistics.median(values)
+
+
 OPS_METRIC = "pair LayerNorm and sigmoid gate HBM GB/s (% of 8 TB/s) at N=1536 FP32, 1 GPU"
 
 
@@ -697,12 +971,16 @@ def bench_ops(args) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default 10; the core workload: 20 calls)")
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed warmup steps (default 3; the core workload: 5 calls)")
     ap.add_argument("--config", default="c4", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--workload", default="block",
-                    choices=["block", "openfold3", "trimul", "transition", "ops"],
-                    help="block: the triangle-attention block (default); openfold3: "
+                    choices=["block", "core", "openfold3", "trimul", "transition", "ops"],
+                    help="block: the triangle-attention block (default); core: the "
+                         "attention core on the operator route (B512 N1536, B1000 N1000); "
+                         "openfold3: "
                          "OpenFold3's _attention through fpx_attn_strided; trimul: "
                          "triangle multiplication (fpx_tri_mul); transition: the pair "
                          "transition (fpx_transition); ops: the standalone pair "
@@ -712,6 +990,9 @@ def main() -> int:
                     help="also run a plain 1 GiB device-to-device copy (the known-size "
                          "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE scaling)")
     args = ap.parse_args()
+    core = args.workload == "core"
+    args.steps = args.steps if args.steps is not None else (20 if core else 10)
+    args.warmup = args.warmup if args.warmup is not None else (5 if core else 3)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py runs on exactly one GPU: the triangle-attention block is measured on "
@@ -727,6 +1008,12 @@ def main() -> int:
         print("bench.py needs a HIP device", file=sys.stderr)
         return 2
     lib = _native.library()
+    if args.workload == "core":
+        result = bench_core(args)
+        if args.calibrate_copy:
+            calibrate_copy(torch.device("cuda:0"))
+        print(json.dumps(result), flush=True)
+        return 0 if result["parity"]["pass"] else 1
     if args.workload == "openfold3":
         result = bench_openfold3(args)
         if args.calibrate_copy:
@@ -833,6 +1120,43 @@ def main() -> int:
         log(f"single block call (start): median {block_call['median_ms']:.3f} ms, "
             f"p95 {block_call['p95_ms']:.3f} ms")
 
+        # The module-level route a caller uses: the registry's block dispatch
+        # on a Protenix-shaped module (weights packed once and cached, the
+        # workspace cached per device and stream, dz allocated per call).
+        from fireprot_amd import triangle_attention as ta
+
+        module = workloads.make_protenix_module(w, starting=True, device=dev).to(dtype)
+
+        def module_call():
+            return ta.dispatch_triangle_attention_block(
+                module=module, z=z, mask=mask, ending=False,
+                native=lambda **_: (_ for _ in ()).throw(RuntimeError("native selected")))
+
+        for _ in range(2):
+            module_call()
+        module_times = []
+        for _ in range(20):
+            c0 = torch.cuda.Event(enable_timing=True)
+            c1 = torch.cuda.Event(enable_timing=True)
+            c0.record(stream)
+            module_call()
+            c1.record(stream)
+            c1.synchronize()
+            module_times.append(c0.elapsed_time(c1))
+        module_times.sort()
+        module_call_stats = {
+            "calls": 20, "route": "dispatch_triangle_attention_block -> "
+            + (ta.BLOCK_BF16_IMPLEMENTATION if dtype == torch.bfloat16 else ta.BLOCK_IMPLEMENTATION),
+            "median_ms": round(module_times[10], 4),
+            "p95_ms": round(module_times[int(0.95 * 19 + 0.5)], 4),
+            "min_ms": round(module_times[0], 4)}
+        log(f"module route (start): median {module_call_stats['median_ms']:.3f} ms, "
+            f"p95 {module_call_stats['p95_ms']:.3f} ms")
+        from fireprot_amd import workspace as ws_cache
+
+        ws_cache.release()
+        del module
+
         stages = {}
         for name, fn in (("prepare", prepare), ("attend", attend), ("finish", finish)):
             fn()
@@ -915,6 +1239,7 @@ def main() -> int:
             "step_flop": step_flop,
             "stage_ms_start_node": {k: round(v, 4) for k, v in stages.items()},
             "block_call_start_node": block_call,
+            "module_call_start_node": module_call_stats,
         },
         "roofline": roofline,
         "cpu_baseline": None,
@@ -926,7 +1251,15 @@ def main() -> int:
         record, oracle_out = cpu_baseline(cfg, z_cpu, mask_cpu, w)
         result["cpu_baseline"] = record
         result["parity"] = parity_report(cfg, gpu_out, oracle_out)
+        gate = parity_gate(cfg, gpu_out, oracle_out, z_cpu, mask_cpu, w)
+        result["parity"]["gate"] = gate
         log(f"parity vs CPU oracle: {json.dumps(result['parity'])}")
+        if not gate["pass"]:
+            # a result that misses its parity bar is not a measurement
+            result["value"] = None
+            print(json.dumps(result), flush=True)
+            log("PARITY FAILED: value withheld")
+            return 1
     print(json.dumps(result), flush=True)
     return 0
 

@@ -102,6 +102,8 @@ def transition(x: torch.Tensor, weights: TransitionWeights, *, out: torch.Tensor
     src = _rows(x)
     if src is None or src[2] % 4 or src[3] % 4 or x.data_ptr() % 16:
         x = x.contiguous()
+        if x.data_ptr() % 16:  # contiguous already, at a misaligned offset
+            x = x.clone()
         src = _rows(x)
     if out is None:
         out = torch.empty(x.shape, dtype=torch.float32, device=x.device)

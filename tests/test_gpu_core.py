@@ -48,7 +48,7 @@ def _cuda(q, k, v, biases):
 
 @pytest.mark.parametrize("batch,n,masked", [(3, 4, False), (5, 20, True), (4, 124, False),
                                             (4, 124, True), (2, 1000, False), (2, 1000, True),
-                                            (2, 1536, False), (1, 132, True)])
+                                            (2, 1536, False), (1, 132, True), (2, 1536, True)])
 def test_core_matches_native(batch, n, masked):
     print(f"case core batch={batch} n={n} masked={masked}", flush=True)
     q, k, v, biases = _inputs(batch, n, 100 + n, masked=masked)
@@ -156,14 +156,35 @@ def test_core_padded_bias_row_stride():
 
 
 def test_dispatch_falls_back_for_unsupported_shapes():
-    q, k, v, biases = _inputs(2, 6, 3)   # n % 4 != 0
-    qc, kc, vc, bc = _cuda(q, k, v, biases)
+    """Three heads of dimension 32 (the projection layout of another model):
+    the candidate rejects the shape with a reason and native runs."""
+    g = torch.Generator().manual_seed(3)
+    q, k, v = [torch.randn(2, 6, 3, 32, generator=g).transpose(1, 2).cuda() for _ in range(3)]
+    bias = torch.randn(1, 3, 6, 6, generator=g).cuda()
     registry.clear_runtime_state()
     with torch.inference_mode():
-        result = ta.dispatch_triangle_attention(module=SimpleNamespace(training=False), q=qc,
-                                                k=kc, v=vc, biases=bc,
+        result = ta.dispatch_triangle_attention(module=SimpleNamespace(training=False), q=q,
+                                                k=k, v=v, biases=[bias],
                                                 native=lambda **_: "native")
     assert result == "native"
     decision = registry.manifest()["decisions"][0]
     assert decision["selected"] == "native"
-    assert "multiple of 4" in decision["rejected"][0]["reason"]
+    assert "4 heads of dimension 32" in decision["rejected"][0]["reason"]
+
+
+@pytest.mark.parametrize("batch,n,masked", [(2, 6, False), (3, 129, True), (1, 1, False)])
+def test_dispatch_serves_any_sequence_length(batch, n, masked):
+    """The plane-staged route takes any N up to 4096 (N % 4 != 0 included):
+    the candidate is selected and meets the FP32 functional bar."""
+    print(f"case core any n batch={batch} n={n} masked={masked}", flush=True)
+    q, k, v, biases = _inputs(batch, n, 200 + n, masked=masked)
+    expected = _expected(q, k, v, biases)
+    qc, kc, vc, bc = _cuda(q, k, v, biases)
+    registry.clear_runtime_state()
+    with torch.inference_mode():
+        actual = ta.dispatch_triangle_attention(
+            module=SimpleNamespace(training=False), q=qc, k=kc, v=vc, biases=bc,
+            native=lambda **_: pytest.fail("native selected"))
+        torch.cuda.synchronize()
+    assert_f32_parity(f"core any n b={batch} n={n}", actual.cpu(), expected)
+    assert registry.count(ta.OPERATION, ta.IMPLEMENTATION) == 1
