@@ -10,15 +10,16 @@
 // and unlike the FP32 one it runs beside VALU work, so the softmax of one
 // tile overlaps the matrix work of the next.
 //
-//   S^T = K Q^T: q and k arrive as planes scaled per 32 x 32 tile (prepare
-//     projection or stage_planes_kernel); the logit is fma(acc, log2(e)
-//     2^-(e_q + e_k), bias log2(e)) (exact scaling, one rounding).  6 MFMAs
-//     per 32-key tile.
-//   O^T += V^T P^T: v^T arrives as planes scaled per key tile t (2^e_t), its
-//     keys in the S^T accumulator's register order; the weights P of tile t
-//     are split per tile into fp16 planes as P 2^(kVShift - (e_t - e_min))
-//     (at most 2^15), so every product carries the same 2^(e_min + kVShift),
-//     removed in the epilogue.  6 MFMAs per tile.
+//   S^T = K Q^T: q and k arrive as scaled planes, one scale per head (the
+//     block's prepare projection) or per 32 x 32 tile (stage_planes_kernel);
+//     the logit is fma(acc, log2(e) 2^-(e_q + e_k), bias log2(e)) (exact
+//     scaling, one rounding).  6 MFMAs per 32-key tile.
+//   O^T += V^T P^T: v^T arrives as planes scaled per key tile t (2^e_t; the
+//     block's one scale per head), its keys in the S^T accumulator's
+//     register order; the weights P of tile t are split per tile into fp16
+//     planes as P 2^(kVShift - (e_t - e_min)) (at most 2^15), so every
+//     product carries the same 2^(e_min + kVShift), removed in the epilogue.
+//     6 MFMAs per tile.
 //
 // Each key tile's four 2 KB planes (K hi, K lo, V^T hi, V^T lo) go straight
 // from global memory into a ring of LDS stages (global_load_lds_dwordx4, no
@@ -33,7 +34,9 @@
 //     query, moved up to the tile's max when a lane's weights of a tile
 //     would pass 2^15;
 //     P' = exp2(x - (c + g_t)) with the tile's exponent shift g_t folded into
-//     the exact integer c + g_t;
+//     the exact integer c + g_t.  The block's bias copy is stored relative
+//     to each query's reference (bias_reference_kernel): the reference then
+//     starts at 0, and while it and g_t stay 0 the weights are exp2(x);
 //   exact (fully masked rows, and rows whose logits are not bounded):
 //     fl(fl(s + mask) + bias) in natural units, as the native path rounds
 //     them, with a lazy max and one rounded reference, so equal quantised
@@ -65,6 +68,9 @@ constexpr int kStageBytes = 4 * kPlaneBytes;
 // 2^15), d_t = e_t - e_min >= 0 the v^T tile's exponent above the row's
 // smallest; kPlaneMax bounds a lane's 16 scaled weights of one tile.
 constexpr int kVShift = 7;
+// Relative bias: the largest product bound (log2 units) for which the
+// reference may start at 0 (see attend_item).
+constexpr float kRelBound = 4.0f;
 constexpr float kPlaneMax = 32768.0f;
 // Four waves per SIMD: four work-groups per CU (ring and mask row within
 // 40 KB of LDS at N <= 1536).
@@ -267,6 +273,10 @@ __device__ __forceinline__ void attend_item(const AttnArgs& a, int nqt, int nkt_
   // Exact rows that the constant-row kernel serves are left out; other
   // constant-mask rows (another m than their chunk's) still skip S^T here.
   if (EXACT && const_chunk_member(a, b)) return;
+  // The block's fast launch reads the log2 bias relative to each query's
+  // reference (launch_bias_reference): x' = x - C_q + kRelOffset.
+  const bool rel = kBlock && !EXACT && a.magnitudes != nullptr &&
+                   a.magnitudes[kRelativeBiasWord] == 1u;
   float m_row = 0.f;
   const bool constant_mask = EXACT && constant_mask_row(a, b, m_row);
   const int last = nkt - 1;
@@ -400,6 +410,37 @@ __device__ __forceinline__ void attend_item(const AttnArgs& a, int nqt, int nkt_
     float c_ref = 0.f;
     float w_ref = 1.f;  // exact path: 2^-(m_ref log2(e) - c_ref)
     bool has_ref = false;
+    // Relative bias: the reference starts at 0 (C_q - kRelOffset in absolute
+    // log2 units) when the products are bounded tightly enough.  With
+    // |s_qk| <= |q|_2 |k|_2 <= |q|_2 sqrt(32) max|k| below kRelBound (log2
+    // units) on every lane, a row's largest logit over the keys of the tiles
+    // before T lies in [C_q - 1 - kRelBound, C_q + kRelBound]; its weight
+    // P' = 2^(x' - g) then lies in [2^(kRelOffset - 1 - kRelBound),
+    // 2^(kRelOffset + kRelBound)] (g = 0 with the block's one v^T exponent
+    // per head), and a larger logit elsewhere moves the reference as usual.
+    // ref_zero (uniform): c_ref = 0 on every lane.
+    int ref_zero = 0;
+    if constexpr (!kExact) {
+      if (rel) {
+        float s2 = 0.f;
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          const f16x8 hv = __builtin_bit_cast(f16x8, qh[m]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) s2 = __builtin_fmaf((float)hv[e], (float)hv[e], s2);
+        }
+        // |q| <= |hi| (1 + 2^-11) per channel; the margin also covers the
+        // square root and products
+        const float qn = __builtin_sqrtf(xor32_sum(s2)) * sq * (1.0f + 0x1p-8f);
+        const float mk = __builtin_bit_cast(float, a.magnitudes[1]);
+        const float bound = qn * 5.65685425f * mk * kLog2e;
+        if (__all(bound <= kRelBound)) {  // false for NaN
+          has_ref = true;
+          m_ref = 0.f;
+          ref_zero = 1;
+        }
+      }
+    }
 
     // Logits x of tile t -> the weights' fp16 hi and lo planes (P operand).
     // Tile t's v^T planes carry 2^e_t, so its weights P enter as
@@ -410,7 +451,8 @@ __device__ __forceinline__ void attend_item(const AttnArgs& a, int nqt, int nkt_
     // fp16 planes' absolute resolution (2^-25).  The row sum adds the
     // unscaled P.
     auto softmax = [&](const f32x16& x, int t, bf16x8 (&ph)[2], bf16x8 (&pl)[2]) {
-      const int g = __builtin_amdgcn_readfirstlane(Ev[t]) - e_min - kVShift;  // uniform
+      // uniform; the relative bias holds the shift kVShift in kRelOffset
+      const int g = __builtin_amdgcn_readfirstlane(Ev[t]) - e_min - (rel ? 0 : kVShift);
       // The weights are formed, summed and split eight at a time (8 keys per
       // operand half m), so only half of them are live at once.
       auto sum8 = [](const f32x8& v) {
@@ -457,8 +499,14 @@ __device__ __forceinline__ void attend_item(const AttnArgs& a, int nqt, int nkt_
       // one query's 32 keys and keeps one reference.
       const float gf = (float)g;
       f32x16 p;
+      if (__builtin_amdgcn_readfirstlane(ref_zero) && g == 0) {
+        // the reference and the tile's shift are 0: P' = exp2(x')
 #pragma unroll
-      for (int r = 0; r < 16; ++r) p[r] = exp2_fast(x[r] - (c_ref + gf));
+        for (int r = 0; r < 16; ++r) p[r] = exp2_fast(x[r]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[r] = exp2_fast(x[r] - (c_ref + gf));
+      }
       float ps = sum16(p);
       // ps <= 2^15 bounds every P' of the lane; NaN or inf counts as over.
       if (!has_ref || __any(!(ps <= kPlaneMax))) {
@@ -480,11 +528,13 @@ __device__ __forceinline__ void attend_item(const AttnArgs& a, int nqt, int nkt_
         l_run *= alpha;
         c_ref = c_new;
         has_ref = __all(m_ref != -INFINITY);
+        ref_zero = __all(c_ref == 0.f);
 #pragma unroll
         for (int r = 0; r < 16; ++r) p[r] = exp2_fast(x[r] - (c_ref + gf));
         ps = sum16(p);
       }
-      l_run = __builtin_fmaf(ps, __builtin_ldexpf(1.0f, g), l_run);  // P = P' 2^g
+      // P = P' 2^(g - kVShift) with the relative bias (P' 2^g otherwise)
+      l_run = __builtin_fmaf(ps, __builtin_ldexpf(1.0f, rel ? g - kVShift : g), l_run);
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
         const f32x8 v = {p[8 * m + 0], p[8 * m + 1], p[8 * m + 2], p[8 * m + 3],
@@ -915,6 +965,83 @@ void attention_const_kernel(AttnArgs a, int nqt, int nkt, int nchunks, uint32_t 
   }
 }
 
+// The relative log2 bias of the block (launch_bias_reference).  One
+// work-group per (head, 32-query tile); every work-group first finds T, the
+// first 32-key tile with a nonzero mask bias, minimised over the rows that
+// have an unmasked key (so keys of tiles t < T are unmasked on every row the
+// fast softmax serves); nkt when no row has a masked key.  Lane (half, l32)
+// of a fragment holds 16 keys of query l32 (bias_frag_index), so a query's
+// largest log2 bias over tiles t < T is a per-lane max, an xor-32 max and a
+// max over the four waves (each takes every fourth tile).  C_q = ceil of it;
+// every tile of the query is then rewritten as bias_l2 - (C_q - kRelOffset),
+// one rounding.  With T = 0 nothing is rewritten and the flag stays 0.
+__global__ __launch_bounds__(256) void bias_reference_kernel(const uint32_t* __restrict__ flags,
+                                                             int batch, int n, int np,
+                                                             float* __restrict__ bias_l2,
+                                                             uint32_t* __restrict__ magnitudes) {
+  __shared__ int wmin[4];
+  __shared__ float qmax[4][32];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int nkt = (n + kBk - 1) / kBk;
+  const int nt = np >> 5;
+  int t_first = nkt;
+  for (int b = tid; b < batch; b += 256) {
+    const uint32_t* f = flags + (int64_t)b * kTileFlagParts * kTileFlagWords;
+    uint32_t open = 0u;
+    int first = nkt;
+#pragma unroll
+    for (int i = 0; i < kTileFlagWords; ++i) {
+      const int lo = 32 * i;
+      const uint32_t valid =
+          nkt >= lo + 32 ? 0xffffffffu : nkt > lo ? (1u << (nkt - lo)) - 1u : 0u;
+      open |= ~f[kTileFlagWords + i] & valid;
+      const uint32_t m = f[i] & valid;
+      if (first == nkt && m != 0u) first = lo + __builtin_ctz(m);
+    }
+    if (open != 0u) t_first = min(t_first, first);
+  }
+  // wave minimum, then the work-group's
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) t_first = min(t_first, __shfl_xor(t_first, d));
+  if (lane == 0) wmin[w] = t_first;
+  __syncthreads();
+  const int T = min(min(wmin[0], wmin[1]), min(wmin[2], wmin[3]));
+  if (T == 0) return;  // uniform
+  const int h = (int)blockIdx.x / nt;
+  const int qt = (int)blockIdx.x % nt;
+  float* frag = bias_l2 + ((int64_t)h * nt + qt) * nt * 1024 + lane * 4;
+  float m = -INFINITY;
+  for (int t = w; t < T; t += 4) {
+    const float* src = frag + (int64_t)t * 1024;
+    const f32x16 x = cat4(*(const f32x4*)src, *(const f32x4*)(src + 256),
+                          *(const f32x4*)(src + 512), *(const f32x4*)(src + 768));
+    m = __builtin_elementwise_maximum(m, max16(x));
+  }
+  m = xor32_max(m);
+  if (lane < 32) qmax[w][lane] = m;
+  __syncthreads();
+  const int q = lane & 31;
+  const float mq = __builtin_elementwise_maximum(
+      __builtin_elementwise_maximum(qmax[0][q], qmax[1][q]),
+      __builtin_elementwise_maximum(qmax[2][q], qmax[3][q]));
+  // |C_q| < 2^22 whenever the fast softmax runs (its logit bound); other
+  // values are never read, and keep the copy as it is
+  const float c = __builtin_ceilf(mq);
+  const float shift = __builtin_fabsf(c) < 4194304.0f ? c - kRelOffset : 0.0f;
+  for (int t = w; t < nt; t += 4) {
+    float* dst = frag + (int64_t)t * 1024;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 v = *(const f32x4*)(dst + 256 * i);
+      v = v - shift;
+      *(f32x4*)(dst + 256 * i) = v;
+    }
+  }
+  if (blockIdx.x == 0 && tid == 0) magnitudes[kRelativeBiasWord] = 1u;
+}
+
 }  // namespace
 
 hipError_t launch_attention_split(int layout, const AttnArgs& a, hipStream_t stream) {
@@ -962,6 +1089,16 @@ hipError_t launch_attention_split(int layout, const AttnArgs& a, hipStream_t str
   } else {
     return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_bias_reference(const uint32_t* flags, int batch, int n, int np, float* bias_l2,
+                                 uint32_t* magnitudes, hipStream_t stream) {
+  if (batch <= 0 || n <= 0) return hipSuccess;
+  if (np % kBq || np < n || round_up(n, kBk) / kBk > kTileFlagWords * 32 || magnitudes == nullptr)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(bias_reference_kernel, dim3((uint32_t)(kHeads * (np >> 5))), dim3(256), 0,
+                     stream, flags, batch, n, np, bias_l2, magnitudes);
   return hipGetLastError();
 }
 

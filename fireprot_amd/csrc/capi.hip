@@ -384,7 +384,10 @@ int fpx_tri_attn_prepare(int dtype, const void* z, int64_t z_stride0, int64_t z_
   p.magnitudes = w.magnitudes;
   p.scales = w.scales;
   p.np = w.np;
-  return status(fpx::launch_projection(fpx::kProjBlock, p, s));
+  e = fpx::launch_projection(fpx::kProjBlock, p, s);
+  if (e != hipSuccess || fpx::fp32_matrix_cores_selected()) return status(e);
+  // the fast softmax reads the log2 bias relative to each query's reference
+  return status(fpx::launch_bias_reference(w.flags, n, n, w.np, p.tri_bias_l2, w.magnitudes, s));
 }
 
 int fpx_tri_attn_attend(int dtype, int n, void* workspace, size_t workspace_bytes, void* stream) {

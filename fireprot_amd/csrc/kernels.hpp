@@ -72,8 +72,16 @@ constexpr float kFastBound = 2097152.0f;  // 2^21
 // bits (atomicMax on non-negative floats; a NaN sorts above inf, so any
 // non-finite value disables the skip), then 1 once the projection wrote them.
 // A skipped key with a non-finite v would have made the native row NaN
-// (0 * inf), hence max|v| must be finite too.
-constexpr int kMagnitudeWords = 5;
+// (0 * inf), hence max|v| must be finite too.  Word kRelativeBiasWord is 1
+// when launch_bias_reference rewrote the log2-scaled bias copy relative to
+// each query's reference (zeroed with the rest of the record by the mask
+// stage).
+constexpr int kMagnitudeWords = 6;
+constexpr int kRelativeBiasWord = 5;
+// The relative log2 bias: bias log2(e) - C_q + kRelOffset, C_q = the ceiling
+// of query q's largest log2 bias over the key tiles that precede every row's
+// first masked tile (the keys unmasked on every row with an unmasked key).
+constexpr float kRelOffset = 8.0f;
 
 struct AttnArgs {
   const float* q;
@@ -111,6 +119,12 @@ bool fp32_matrix_cores_selected();
 // kAttnBlock or kAttnStaged.
 hipError_t launch_attention(int layout, const AttnArgs& args, hipStream_t stream);
 hipError_t launch_attention_split(int layout, const AttnArgs& args, hipStream_t stream);
+// The FP32 block after its prepare stage: rewrite bias_l2 ([4][np][np],
+// bias_frag_index order) as bias log2(e) - C_q + kRelOffset and set
+// magnitudes[kRelativeBiasWord] = 1, unless no key tile precedes every row's
+// first masked tile (then nothing changes).  flags: the rows' tile flags.
+hipError_t launch_bias_reference(const uint32_t* flags, int batch, int n, int np, float* bias_l2,
+                                 uint32_t* magnitudes, hipStream_t stream);
 // kAttnStrided q, k, v of args -> the plane layout of kAttnStaged: q_planes,
 // k_planes, v_planes each [batch][4] slices of np * 128 bytes, scales
 // [3][batch][4][np / 32] floats.
@@ -156,18 +170,18 @@ struct ProjArgs {
   // Plane layout of q, k, v^T (set by launch_projection for the split
   // kernel; the FP32-matrix-core kernels keep plain FP32).  The (i, h) slice
   // of np * 128 bytes holds a hi plane and then a lo plane of 16-bit values:
-  //   q, k: [np rows j][32 channels] fp16 of the value times 2^e, e chosen
-  //         per 32 x 32 (rows j, head channels) tile so that the tile's max
-  //         |value| 2^e lies in [2^14, 2^15); hi = fp16(x 2^e) and lo =
-  //         fp16(x 2^e - hi) carry 22 bits;
+  //   q, k: [np rows j][32 channels] fp16 of the value times 2^e; hi =
+  //         fp16(x 2^e) and lo = fp16(x 2^e - hi) carry 22 bits;
   //   v^T:  [np / 32 key tiles][32 channels][32 key positions] fp16 of the
-  //         value times 2^e, e per key tile (value_plane_exp of its max
-  //         |value|: [2^14, 2^15) as above, kPlaneExpMax for a zero tile),
-  //         hi and lo as for q, k; key 4g + e of a tile at position
-  //         16 (g / 4) + 4 (0, 2, 1, 3)[g % 4] + e (the S^T accumulator's
-  //         register order);
+  //         value times 2^e, hi and lo as for q, k; key 4g + e of a tile at
+  //         position 16 (g / 4) + 4 (0, 2, 1, 3)[g % 4] + e (the S^T
+  //         accumulator's register order);
+  //   e: one per head and operand, from the bound sum_c |W_c| (sqrt(128)
+  //         |ln_w_c| + |ln_b_c|) on the values of LayerNorm-normalised rows
+  //         (times 1/sqrt(32) for q), so that the bound times 2^e lies in
+  //         [2^14, 2^15) (v^T: value_plane_exp of the bound);
   //   scales[(t * rows_i + i) * 4 + h][j / 32] = 2^-e for t = 0 (q), 1 (k),
-  //         2 (v^T).
+  //         2 (v^T): the same for every row i and tile of a head.
   int planes;
   float* scales;
   int np;

@@ -48,10 +48,12 @@ struct ProjTraits<kProjOut> {
 // 8*(r/4) + r%4 of the tile, column col_w of output group `group` (0 q, 1 k,
 // 2 v, 3 g; kProjOut: always 0), head or column block hw.  Row offsets are
 // compile-time constants once the lane's base includes its 4*half rows.
+// e_head: the plane exponent of this wave's head (kProjBlock planes: every
+// q, k and v^T tile of the head is scaled by 2^e_head, head_plane_exp).
 template <int MODE>
 __device__ __forceinline__ void store_tile(const ProjArgs& a, int tile, int tiles_j, int group,
                                            int hw, int col_w, float col_bias, int half, int l32,
-                                           const f32x16& acc) {
+                                           const f32x16& acc, int e_head) {
   const int i = tile / tiles_j;
   const int j0 = (tile % tiles_j) * kRows + 4 * half;
   if (MODE == kProjBlock && a.planes) {
@@ -60,21 +62,10 @@ __device__ __forceinline__ void store_tile(const ProjArgs& a, int tile, int tile
     const int64_t bh = (int64_t)i * kHeads + hw;
     const int64_t slice_bytes = (int64_t)a.np * 128;
     if (group == 0 || group == 1) {
-      // q, k: scaled fp16 planes [np rows][32 channels] with the tile's
+      // q, k: scaled fp16 planes [np rows][32 channels] with the head's
       // inverse scale.
       const float scale = group == 0 ? a.q_scale : 1.0f;
-      // NaN-propagating max |value| of the 32 x 32 tile (scaling by a
-      // positive constant keeps the maximum)
-      float m = 0.f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) m = __builtin_elementwise_maximum(m, __builtin_fabsf(acc[r]));
-      m = wave_max(m) * scale;
-      // m 2^e in [2^14, 2^15); e = 0 for a zero or non-finite tile
-      int e = 0;
-      if (m > 0.f && m < INFINITY) {
-        e = 15 - __builtin_amdgcn_frexp_expf(m);
-        e = e < -kPlaneExpMax ? -kPlaneExpMax : e > kPlaneExpMax ? kPlaneExpMax : e;
-      }
+      const int e = e_head;
       // (acc * scale) 2^e == acc * (scale 2^e): one rounding either way
       const float f = __builtin_ldexpf(scale, e);
       // Lane pairs (l32, l32 ^ 1) swap halves so that each lane stores one
@@ -103,15 +94,12 @@ __device__ __forceinline__ void store_tile(const ProjArgs& a, int tile, int tile
             __builtin_ldexpf(1.0f, -e);
     } else if (group == 2) {
       // v^T: fp16 planes [np / 32 tiles][32 channels][32 key positions],
-      // the tile scaled by 2^e (its max |value| in [2^14, 2^15), as q and k;
-      // value_plane_exp), keys of a tile in the order of the S^T accumulator
-      // registers (key group g of four at position 16 (g / 4) + 4 (0, 2, 1,
-      // 3)[g % 4]).  This lane's keys 8 rr + e + 4 half sit at positions
-      // 8 half + 4 rr + e (rr < 2) and 16 + 8 half + 4 (rr - 2) + e.
-      float m = 0.f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) m = __builtin_elementwise_maximum(m, __builtin_fabsf(acc[r]));
-      const int e = value_plane_exp(wave_max(m));
+      // every tile of the head scaled by 2^e_head, keys of a tile in the
+      // order of the S^T accumulator registers (key group g of four at
+      // position 16 (g / 4) + 4 (0, 2, 1, 3)[g % 4]).  This lane's keys
+      // 8 rr + e + 4 half sit at positions 8 half + 4 rr + e (rr < 2) and
+      // 16 + 8 half + 4 (rr - 2) + e.
+      const int e = e_head;
       const float f = __builtin_ldexpf(1.0f, e);
       uint8_t* base = reinterpret_cast<uint8_t*>(a.vt) + bh * slice_bytes +
                       (int64_t)(tile % tiles_j) * 2048 + l32 * 64 + 16 * half;
@@ -330,7 +318,7 @@ __global__ __launch_bounds__(ProjTraits<MODE>::kWaves * 64) void projection_kern
   };
 
   auto epilogue = [&](int tile, const f32x16& acc) {
-    store_tile<MODE>(a, tile, tiles_j, w >> 2, w & 3, col_w, col_bias, half, l32, acc);
+    store_tile<MODE>(a, tile, tiles_j, w >> 2, w & 3, col_w, col_bias, half, l32, acc, 0);
   };
 
   // Persistent loop: the tile after this one is fetched two tiles ahead and
@@ -365,6 +353,8 @@ __global__ __launch_bounds__(ProjTraits<MODE>::kWaves * 64) void projection_kern
 // against 64 v_mfma_f32_32x32x2_f32 of 8x less work each, with an error per
 // product below an FP32 dot product's.  Scales are powers of two:
 //   - each weight column by 2^ew, its max |w| in [2^14, 2^15);
+//   - kProjBlock's q, k and v^T outputs by one 2^e per head (store_tile's
+//     e_head, from a bound on the values of normalised rows);
 //   - LN rows (kProjBlock) by one 2^ex per launch from the LN affine: the
 //     centred, normalised row has 2-norm sqrt(128), so |y_c| <= sqrt(128)
 //     |ln_w_c| + |ln_b_c|; ln_w and ln_b are pre-scaled, so the scaled row
@@ -434,6 +424,41 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
   const int cb = __builtin_amdgcn_readfirstlane(slice * NW + w);  // 32-column block
   const int group = cb >> 2;
   const int hw = cb & 3;
+
+  // kProjBlock planes: one plane exponent per head for q, k and v^T (this
+  // wave's 32 columns are one head of one group), from a bound on the
+  // values instead of each tile's maximum.  Every LayerNorm output obeys
+  // |y_c| <= sqrt(128) |ln_w_c| + |ln_b_c|, so a column's values obey
+  // |x W^T| <= sum_c |W_c| (sqrt(128) |ln_w_c| + |ln_b_c|) (times 1/sqrt(32)
+  // for q).  With every tile of a head at one scale, the attention's product
+  // scale and v^T exponent are the same for every key tile.  Accuracy does
+  // not depend on the scale: the fp16 planes keep 22 significant bits
+  // relative to each value down to 2^-14 of the scaled unit, and the values
+  // of normalised rows lie within a few binary orders of the bound.
+  const int e_head = [&] {
+    if (!(MODE == kProjBlock && a.planes) || group > 2) return 0;
+    const float* src = a.w[group] + (int64_t)(32 * hw + l32) * kChannels + 8 * half;
+    float s = 0.f;
+    // a loop, not unrolled: few registers live beside the weight planes
+#pragma unroll 1
+    for (int t = 0; t < 8; ++t) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int c = 16 * t + 8 * half + e;
+        const float yb = 11.3137085f * __builtin_fabsf(a.ln_w ? a.ln_w[c] : 1.f) +
+                         __builtin_fabsf(a.ln_b ? a.ln_b[c] : 0.f);
+        s = __builtin_fmaf(__builtin_fabsf(src[16 * t + e]), yb, s);
+      }
+    }
+    const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, s),
+                                                     __builtin_bit_cast(unsigned, s), false, false);
+    s = __builtin_bit_cast(float, (unsigned)sw[0]) + __builtin_bit_cast(float, (unsigned)sw[1]);
+    // the margin covers the rounding of the LN output, the sums and q's scale
+    const float bound = wave_max(s) * (group == 0 ? a.q_scale : 1.0f) * (1.0f + 0x1p-8f);
+    if (group == 2) return value_plane_exp(bound);
+    const int e = plane_exp(bound);
+    return e < -kPlaneExpMax ? -kPlaneExpMax : e > kPlaneExpMax ? kPlaneExpMax : e;
+  }();
 
   // Weight planes: B[k][col] for col = 32*hw + l32 of group `group`, lane
   // holding channels 16t + 8*half + e of k step t, scaled by 2^ew (the
@@ -700,7 +725,8 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
       if (more) store_bias(bias, ni, nj0);
       if (result_tile >= 0) {
         note(result);
-        store_tile<MODE>(a, result_tile, tiles_j, group, hw, col_w, col_bias, half, l32, result);
+        store_tile<MODE>(a, result_tile, tiles_j, group, hw, col_w, col_bias, half, l32, result,
+                         e_head);
       }
       __builtin_amdgcn_sched_barrier(0);
     };
@@ -720,7 +746,8 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
     }
     if (!lead && tile - streams >= first) {
       note(res);
-      store_tile<MODE>(a, tile - streams, tiles_j, group, hw, col_w, col_bias, half, l32, res);
+      store_tile<MODE>(a, tile - streams, tiles_j, group, hw, col_w, col_bias, half, l32, res,
+                       e_head);
     }
     if (a.magnitudes != nullptr) {
       // Wave maxima (NaN-propagating), one atomic per wave and record word.
@@ -746,7 +773,8 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
         stage_vecs(buf ^ 1);
         if (next + streams < ntiles) fetch(next + streams);
       }
-      store_tile<MODE>(a, tile, tiles_j, group, hw, col_w, col_bias, half, l32, unscale(c0 + c1, buf));
+      store_tile<MODE>(a, tile, tiles_j, group, hw, col_w, col_bias, half, l32, unscale(c0 + c1, buf),
+                       e_head);
       __syncthreads();
       tile = next;
       next += streams;

@@ -48,12 +48,12 @@ def test_abi_version_and_workspace_sizes(lib):
         for dtype, e in ((0, 4), (1, 2)):
             copies = 2 if dtype == 0 else 1  # FP32: unscaled and log2(e)-scaled bias
             # q, k, v^T; gate (rows padded to np); gated output; bias; mask bias;
-            # tile flags (4 parts of 4 words per row) plus the 5-word magnitude record;
+            # tile flags (4 parts of 4 words per row) plus the 6-word magnitude record;
             # the q, k and v^T tiles' inverse scales of the plane layout
             expected = (3 * seg(n * 4 * np_ * 32 * e) + seg(n * np_ * 128 * e)
                         + seg(n * n * 128 * e)
                         + seg(4 * np_ * np_ * e * copies) + seg(n * np_ * 4)
-                        + seg((n * 16 + 5) * 4) + seg(3 * n * 4 * (np_ // 32) * 4))
+                        + seg((n * 16 + 6) * 4) + seg(3 * n * 4 * (np_ // 32) * 4))
             assert lib.fpx_tri_attn_workspace_bytes(n, 128, 4, 32, dtype) == expected
     for bad in ((0, 128, 4, 32, 0), (4097, 128, 4, 32, 0), (64, 64, 4, 32, 0),
                 (64, 128, 8, 32, 0), (64, 128, 4, 16, 0), (64, 128, 4, 32, 7)):
@@ -66,10 +66,10 @@ def test_strided_workspace_sizes(lib):
         np_ = -(-n // 128) * 128
         # two fragment-order bias copies; mask-bias rows; tile flags (4 x 4 words);
         # q, k, v planes (np * 128 bytes per row and head); their scales; the
-        # magnitude record (5 words); the staging's per-group maxima
+        # magnitude record (6 words); the staging's per-group maxima
         expected = (2 * seg(4 * np_ * np_ * 4) + seg(batch * np_ * 4) + seg(batch * 16 * 4)
                     + 3 * seg(batch * 4 * np_ * 128) + seg(3 * batch * 4 * (np_ // 32) * 4)
-                    + seg(5 * 4) + seg(3 * ((3 * batch * 4 * (np_ // 32) + 3) // 4) * 4))
+                    + seg(6 * 4) + seg(3 * ((3 * batch * 4 * (np_ // 32) + 3) // 4) * 4))
         assert lib.fpx_attn_strided_workspace_bytes(batch, n) == expected
     for bad in ((0, 8), (2, 0), (2, 4097)):
         assert lib.fpx_attn_strided_workspace_bytes(*bad) == 0

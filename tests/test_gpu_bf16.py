@@ -86,6 +86,46 @@ def test_c5_n2048_row_subset_transpose_and_determinism():
         assert rel <= BF16_REL
 
 
+BF16_FLOOR = 1e-3  # of max|ref|: elements near zero after cancellation
+
+
+def _elementwise(name, actual, native):
+    """|actual - native| <= 2e-2 |native| + 1e-3 max|native|, every element."""
+    a, r = actual.double(), native.double()
+    floor = BF16_FLOOR * float(r.abs().max())
+    excess = float(((a - r).abs() - BF16_REL * r.abs() - floor).max())
+    worst = float(((a - r).abs() / (BF16_REL * r.abs() + floor)).max())
+    print(f"{name}: elementwise worst |d| / (2e-2 |ref| + {floor:.2e}) = {worst:.3f}", flush=True)
+    assert torch.isfinite(a).all() and excess <= 0.0, f"{name}: {worst:.3f} of the bar"
+
+
+def test_c5_n2048_32_rows_elementwise():
+    """C5 (N=2048, BF16 storage) on 32 seeded outer rows per node, both sides of
+    the middle and both ends included, held elementwise to the native bf16 ops:
+    |d| <= 2e-2 |ref| + 1e-3 max|ref|."""
+    cfg = workloads.CONFIGS["c5"]
+    z, mask, w = workloads.make_inputs(cfg)
+    g = torch.Generator().manual_seed(5)
+    rows = torch.unique(torch.cat([torch.tensor([0, 1, 1023, 1024, 2046, 2047]),
+                                   torch.randint(0, cfg.n, (40,), generator=g)]))[:32]
+    print(f"case {cfg.name} 32 rows {rows.tolist()}", flush=True)
+    zc = z.to(torch.bfloat16).cuda()
+    weights = _weights(w)
+    with torch.inference_mode():
+        start = hip_block.triangle_attention_block(zc, None, weights, ending=False)
+        start_rows = start[rows.cuda()].cpu()
+        del start
+        end = hip_block.triangle_attention_block(zc, None, weights, ending=True)
+        end_rows = end.transpose(0, 1)[rows.cuda()].cpu()
+        torch.cuda.synchronize()
+    del zc, end
+    torch.cuda.empty_cache()
+    params = oracle.BlockParams(**w)
+    for name, actual, ending in (("start", start_rows, False), ("end", end_rows, True)):
+        native = oracle.block_bf16(z, None, params, ending=ending, outer_rows=rows)
+        _elementwise(f"{cfg.name} {name} 32 rows", actual, native)
+
+
 @pytest.mark.timeout(600)
 def test_bf16_maximum_n4096_rows_with_tail():
     """BF16 storage at N = 4096, the largest size the C ABI accepts, with a

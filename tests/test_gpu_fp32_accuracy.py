@@ -88,6 +88,25 @@ def test_c2_full_at_fp32_accuracy(ending):
     _check_regions(f"{cfg.name} ending={ending}", actual, z, mask, w, ending, rows, cfg.valid)
 
 
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("ending", [False, True])
+def test_c3_full_at_fp32_accuracy(ending):
+    """C3 (N=1000, no mask) in full: every element within the functional bar
+    of the FP32 oracle (1e-4 abs + 1e-4 rel) and every row within the FP32
+    bar against float64."""
+    from tests.helpers import assert_f32_parity
+
+    cfg = workloads.CONFIGS["c3"]
+    print(f"case {cfg.name} ending={ending} (all rows)", flush=True)
+    z, mask, w = workloads.make_inputs(cfg)
+    rows = torch.arange(cfg.n)
+    actual = _run_rows(z, mask, w, ending, rows)
+    ref32 = oracle.block(z, mask, oracle_params(w), ending=ending)
+    assert_f32_parity(f"{cfg.name} ending={ending} vs FP32 oracle",
+                      actual, ref32.transpose(0, 1) if ending else ref32)
+    _check_regions(f"{cfg.name} ending={ending}", actual, z, mask, w, ending, rows, cfg.valid)
+
+
 @pytest.mark.parametrize("key", ["c3", "c4"])
 @pytest.mark.parametrize("ending", [False, True])
 def test_long_configs_sampled_rows_at_fp32_accuracy(key, ending):
@@ -102,7 +121,7 @@ def test_long_configs_sampled_rows_at_fp32_accuracy(key, ending):
 @pytest.mark.parametrize("bias_scale,z_scale", [(60.0, 1.0), (1e-3, 1.0), (1.0, 1e-3), (8.0, 1e3)])
 def test_extreme_scales_at_fp32_accuracy(bias_scale, z_scale):
     """Logits of a few hundred, a near-zero bias, and tiny or huge z (LN
-    removes the z scale up to eps): the softmax reference and the per-tile
+    removes the z scale up to eps): the softmax reference and the per-head
     plane scales must keep FP32 accuracy across all of them."""
     n = 200
     z = workloads.make_pair(n, z_scale)
@@ -117,8 +136,8 @@ def test_extreme_scales_at_fp32_accuracy(bias_scale, z_scale):
 
 @pytest.mark.parametrize("v_scale", [1e-6, 1e4])
 def test_value_weight_scales_at_fp32_accuracy(v_scale):
-    """W_v scaled far from 1: v^T planes are scaled per tile, so the products
-    keep their accuracy relative to the values."""
+    """W_v scaled far from 1: the v^T planes' scale follows the weights'
+    bound, so the products keep their accuracy relative to the values."""
     n = 160
     z = workloads.make_pair(n)
     mask = workloads.make_mask(n, 150)
@@ -183,3 +202,41 @@ def test_padding_rows_with_and_without_the_constant_mask_shortcut(qk_scale, inf)
         actual = _run_rows(z, mask, w, ending, rows)
         _check_regions(f"padding qk x{qk_scale} inf={inf:g} ending={ending}", actual, z, mask, w,
                        ending, rows, valid)
+
+
+def test_relative_reference_moves_for_keys_past_the_common_prefix():
+    """The fast softmax starts from the relative reference C_q (the query's
+    largest bias over the keys every row leaves unmasked).  Rows whose
+    unmasked keys reach past that prefix can hold a far larger logit: pair
+    (j, 100) of z is set along W_bias's first head, so bias[0, j, 100] is
+    about 90 against a prefix maximum near 25 (bias x8), and rows with key
+    100 unmasked must move their reference.  Ragged row extents (40, 60, 80
+    ... 120 keys) make the common prefix one tile; both nodes meet the FP32
+    bar on every row."""
+    n = 160
+    w = workloads.make_weights(bias_scale=8.0)
+    z = workloads.make_pair(n)
+    direction = w["w_bias"][0] / w["w_bias"][0].norm()
+    for j in range(0, n, 7):
+        z[j, 100] = 40.0 * direction
+        z[100, j] = 40.0 * direction
+    mask = torch.zeros(n, n)
+    for i in range(n):
+        mask[i, :40 + 20 * (i % 5)] = 1.0
+    rows = torch.arange(n)
+    p32 = oracle_params(w)
+    p64 = p32.to(torch.float64)
+    for ending in (False, True):
+        print(f"case relative reference moves ending={ending}", flush=True)
+        actual = _run_rows(z, mask, w, ending, rows)
+        m_x = mask.t() if ending else mask
+        dead = ~(m_x > 0).any(1)  # rows with every key masked follow the FP32 ties
+        for region, sel in (("open", ~dead), ("fully masked", dead)):
+            if not sel.any():
+                continue
+            sub = rows[sel]
+            ref32 = oracle.block(z, mask, p32, ending=ending, outer_rows=sub)
+            ref64 = oracle.block(z.double(), mask.double(), p64, ending=ending, outer_rows=sub,
+                                 logits_f32=bool(region == "fully masked"))
+            strict_close(f"relative reference ending={ending} {region}", actual[sel], ref64,
+                         ref32)
