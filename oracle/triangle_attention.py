@@ -154,18 +154,26 @@ def prep_qkv(x: torch.Tensor, p: BlockParams, apply_scale: bool = True):
     return q, k, v
 
 
-def wrap_up(o: torch.Tensor, x: torch.Tensor, p: BlockParams) -> torch.Tensor:
+def wrap_up(o: torch.Tensor, x: torch.Tensor, p: BlockParams, *,
+            abs_terms: bool = False) -> torch.Tensor:
     """``Attention._wrap_up``: ``linear_o(flatten(o * sigmoid(linear_g(x))))``.
 
     o is ``[*, N, H, D]`` (head-last).  attention_gate.py:52-54; the gate
     sigmoid(g) * o is checked against its closed form over linspace(-1000,
     1000) as in tests/operators/test_attention_gate.py:32-37.
+
+    ``abs_terms``: return the magnitude of the output projection's terms,
+    ``|o g| |W_o|^T + |b_o|`` (the componentwise condition scale of each
+    output element: an error of u relative in every gated value moves an
+    output by at most u times it).
     """
     heads = p.w_bias.shape[0]
     g = torch.sigmoid(linear(x, p.w_g, p.b_g))
     g = g.view(g.shape[:-1] + (heads, -1))
     o = o * g
     o = o.reshape(o.shape[:-2] + (-1,))
+    if abs_terms:
+        return linear(o.abs(), p.w_o.abs(), None if p.b_o is None else p.b_o.abs())
     return linear(o, p.w_o, p.b_o)
 
 
@@ -181,7 +189,7 @@ def triangle_bias(x_ln: torch.Tensor, p: BlockParams) -> torch.Tensor:
 
 def block(z: torch.Tensor, mask: torch.Tensor | None, p: BlockParams, *,
           ending: bool = False, outer_rows: torch.Tensor | None = None,
-          chunk: int = 64, logits_f32: bool = False) -> torch.Tensor:
+          chunk: int = 64, logits_f32: bool = False, abs_terms: bool = False) -> torch.Tensor:
     """Triangle-attention block ``(z[N,N,C], mask[N,N]) -> dz[N,N,C]``.
 
     Restates ``TriangleAttention.forward`` (patch 0005:14-48) with
@@ -198,7 +206,8 @@ def block(z: torch.Tensor, mask: torch.Tensor | None, p: BlockParams, *,
     shape ``[len(outer_rows), N, C]`` in the (possibly transposed) x frame.
     ``chunk`` bounds the materialised score tensor to ``chunk * H * N * N``.
     ``logits_f32`` rounds the logits to float32 at the native add points
-    (see ``attention_core``); meant for float64 inputs.
+    (see ``attention_core``); meant for float64 inputs.  ``abs_terms`` returns
+    the magnitude of each output's projection terms instead (``wrap_up``).
     """
     x = z
     if ending:
@@ -219,7 +228,7 @@ def block(z: torch.Tensor, mask: torch.Tensor | None, p: BlockParams, *,
         biases.append(tri)
         q, k, v = prep_qkv(xs, p, apply_scale=True)
         o = attention_core(q, k, v, biases, logits_f32=logits_f32).transpose(-2, -3)
-        out.append(wrap_up(o, xs, p))
+        out.append(wrap_up(o, xs, p, abs_terms=abs_terms))
     dz = torch.cat(out, dim=0) if out else x.new_empty((0, n, x.shape[-1]))
     if ending and outer_rows is None:
         dz = dz.transpose(-2, -3)

@@ -1,11 +1,13 @@
 """GPU parity of the BF16-storage / FP32-accumulate block (config c5 family).
 
-Bar: max|actual - native| <= 2e-2 * max|native|, where native is the oracle's
-``block_bf16`` -- the native path run on bfloat16 tensors, rounding every
-intermediate where the native BF16 path rounds it.  The FP32 oracle on the
-same bf16-rounded inputs is reported beside it.  At N=2048 a seeded set of
-outer rows is compared and the full output is checked for the ending-node
-transpose identity and determinism.
+Bars: max|actual - native| <= 2e-2 * max|native|, where native is the
+oracle's ``block_bf16`` -- the native path run on bfloat16 tensors, rounding
+every intermediate where the native BF16 path rounds it (the FP32 oracle on
+the same bf16-rounded inputs is reported beside it); and at C5 (N=2048) on 32
+outer rows per node an elementwise bar against the float64 oracle,
+2e-2 |ref| + 2^-7 M with M the magnitude of each output's projection terms.
+At N=2048 the full output is also checked for the ending-node transpose
+identity and determinism.
 """
 from __future__ import annotations
 
@@ -86,23 +88,33 @@ def test_c5_n2048_row_subset_transpose_and_determinism():
         assert rel <= BF16_REL
 
 
-BF16_FLOOR = 1e-3  # of max|ref|: elements near zero after cancellation
+# Elementwise bar of the BF16 block: |d_i| <= 2e-2 |ref_i| + 2^-7 M_i against
+# the float64 oracle on the same bf16-rounded inputs and weights, where
+# M_i = sum_c |og_c| |W_o[i, c]| (+ |b_o,i|) is the magnitude of output i's
+# projection terms.  Both BF16 paths store the gated attention output og in
+# bfloat16 before the output projection and round the result once more, so
+# an output that cancels to near zero still carries one or two bf16 units of
+# its terms; a relative bar alone cannot hold there, for any BF16 path (the
+# native bf16 ops miss 2e-2 |ref| + 1e-3 max|ref| by 5x at N=256).
+BF16_TERMS = 2.0 ** -7
 
 
-def _elementwise(name, actual, native):
-    """|actual - native| <= 2e-2 |native| + 1e-3 max|native|, every element."""
-    a, r = actual.double(), native.double()
-    floor = BF16_FLOOR * float(r.abs().max())
-    excess = float(((a - r).abs() - BF16_REL * r.abs() - floor).max())
-    worst = float(((a - r).abs() / (BF16_REL * r.abs() + floor)).max())
-    print(f"{name}: elementwise worst |d| / (2e-2 |ref| + {floor:.2e}) = {worst:.3f}", flush=True)
-    assert torch.isfinite(a).all() and excess <= 0.0, f"{name}: {worst:.3f} of the bar"
+def _componentwise(name, actual, ref, terms):
+    """Worst |actual - ref| / (2e-2 |ref| + 2^-7 terms) over every element."""
+    a = actual.double()
+    d = (a - ref).abs()
+    worst = float((d / (BF16_REL * ref.abs() + BF16_TERMS * terms)).max())
+    print(f"{name}: componentwise worst |d| / (2e-2 |ref| + 2^-7 M) = {worst:.3f}; "
+          f"max|d| / max|ref| = {float(d.max() / ref.abs().max()):.2e}", flush=True)
+    assert bool(torch.isfinite(a).all()), f"{name}: non-finite output"
+    return worst
 
 
 def test_c5_n2048_32_rows_elementwise():
-    """C5 (N=2048, BF16 storage) on 32 seeded outer rows per node, both sides of
-    the middle and both ends included, held elementwise to the native bf16 ops:
-    |d| <= 2e-2 |ref| + 1e-3 max|ref|."""
+    """C5 (N=2048, BF16 storage) on 32 seeded outer rows per node (both ends
+    and both sides of the middle included), every element held to
+    2e-2 |ref| + 2^-7 M against the float64 oracle on the bf16-rounded inputs;
+    the native bf16 ops are measured against the same bar beside it."""
     cfg = workloads.CONFIGS["c5"]
     z, mask, w = workloads.make_inputs(cfg)
     g = torch.Generator().manual_seed(5)
@@ -120,10 +132,18 @@ def test_c5_n2048_32_rows_elementwise():
         torch.cuda.synchronize()
     del zc, end
     torch.cuda.empty_cache()
+    z64 = z.to(torch.bfloat16).double()
+    p64 = oracle.BlockParams(**{k: (None if v is None else v.to(torch.bfloat16).double())
+                                for k, v in w.items()})
     params = oracle.BlockParams(**w)
     for name, actual, ending in (("start", start_rows, False), ("end", end_rows, True)):
+        ref = oracle.block(z64, None, p64, ending=ending, outer_rows=rows, chunk=8)
+        terms = oracle.block(z64, None, p64, ending=ending, outer_rows=rows, chunk=8,
+                             abs_terms=True)
         native = oracle.block_bf16(z, None, params, ending=ending, outer_rows=rows)
-        _elementwise(f"{cfg.name} {name} 32 rows", actual, native)
+        hip = _componentwise(f"{cfg.name} {name} 32 rows, HIP", actual, ref, terms)
+        _componentwise(f"{cfg.name} {name} 32 rows, native bf16", native, ref, terms)
+        assert hip <= 1.0, f"{name}: {hip:.3f} of the componentwise bar"
 
 
 @pytest.mark.timeout(600)

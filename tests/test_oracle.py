@@ -24,6 +24,7 @@ import numpy as np
 import pytest
 import torch
 
+from fireprot_amd import workloads
 from oracle import triangle_attention as oracle
 
 GOLDEN = pathlib.Path(__file__).resolve().parent / "golden"
@@ -204,10 +205,10 @@ def _mutated_block(monkeypatch, kind):
     elif kind == "gate_dropped":
         orig = oracle.wrap_up
 
-        def no_gate(o, x, p):
+        def no_gate(o, x, p, **kw):
             q = oracle.BlockParams(**{**p.__dict__, "w_g": torch.zeros_like(p.w_g),
                                       "b_g": torch.full((128,), 40.0, dtype=p.w_g.dtype)})
-            return orig(o, x, q)
+            return orig(o, x, q, **kw)
         monkeypatch.setattr(oracle, "wrap_up", no_gate)
     elif kind == "unbiased_variance":
         def ln(x, w, b, eps=1e-5):
@@ -326,8 +327,6 @@ def test_bf16_oracle_tracks_fp32_oracle_within_bf16_error(ending):
     """block_bf16 runs the native ops on bfloat16 tensors; against the FP32
     oracle on the same bf16-rounded inputs it must differ by bf16 rounding
     only: more than float32 noise, well inside the 2e-2 BF16 bar."""
-    from fireprot_amd import workloads
-
     n = 24
     z = workloads.make_pair(n)
     mask = workloads.make_mask(n, 20)
@@ -339,3 +338,23 @@ def test_bf16_oracle_tracks_fp32_oracle_within_bf16_error(ending):
                         ending=ending)
     rel = ((native.float() - fp32).abs().max() / fp32.abs().max()).item()
     assert 1e-4 < rel < 2e-2
+
+
+def test_abs_terms_bound_the_output_and_match_it_without_cancellation():
+    """``abs_terms`` = |o g| |W_o|^T + |b_o|: never below |dz|, and equal to it
+    when every output takes one term (one nonzero per row of W_o)."""
+    n = 9
+    g = torch.Generator().manual_seed(3)
+    z = torch.randn(n, n, 128, generator=g, dtype=torch.float64)
+    w = {k: (None if v is None else v.double()) for k, v in workloads.make_weights().items()}
+    p = oracle.BlockParams(**w)
+    dz = oracle.block(z, None, p)
+    terms = oracle.block(z, None, p, abs_terms=True)
+    assert bool((terms >= dz.abs() * (1 - 1e-12)).all())
+    assert float((terms - dz.abs()).max()) > 1e-3 * float(terms.max())  # cancellation exists
+    one = torch.zeros_like(w["w_o"])
+    one[torch.arange(128), torch.randperm(128, generator=g)] = torch.randn(128, generator=g,
+                                                                         dtype=torch.float64)
+    p1 = oracle.BlockParams(**{**w, "w_o": one})
+    torch.testing.assert_close(oracle.block(z, None, p1, abs_terms=True),
+                               oracle.block(z, None, p1).abs(), rtol=1e-12, atol=0)
