@@ -242,15 +242,19 @@ __device__ __forceinline__ void attend_item(const AttnArgs& a, int nqt, int nkt_
   // contiguous.  Wave w fills plane w of a stage (K hi, K lo, V^T hi,
   // V^T lo): lane l writes chunk l % 4 of rows l / 4 and 16 + l / 4, read
   // from that row's chunk (l % 4) ^ swz(row).
+  // The copy source is a wave-uniform base (scalar registers) plus a lane
+  // offset; ring stages are compile-time indices (the tile loop is unrolled
+  // over the four stages), so stage addresses fold into immediates.
   const int64_t slice_bytes = (int64_t)a.np * 128;
-  const uint8_t* dma_src = reinterpret_cast<const uint8_t*>(w < 2 ? a.k : a.v) + bh * slice_bytes +
-                           (w & 1) * (slice_bytes >> 1) + (lane >> 2) * 64 +
-                           16 * ((lane & 3) ^ swz(lane >> 2));
+  const uint8_t* dma_base = reinterpret_cast<const uint8_t*>(w < 2 ? a.k : a.v) + bh * slice_bytes +
+                            (w & 1) * (slice_bytes >> 1);
+  const uint32_t dma_voff = (uint32_t)((lane >> 2) * 64 + 16 * ((lane & 3) ^ swz(lane >> 2)));
+  const uint32_t dma_voff2 = dma_voff + 1024;
+  const uint32_t dma_lds = lds_address(lds) + (uint32_t)w * kPlaneBytes;
   auto dma = [&](int t, int stage) {
-    const uint8_t* src = dma_src + (int64_t)t * kPlaneBytes;
-    const uint8_t* dst = lds + stage * kStageBytes + w * kPlaneBytes;
-    lds_dma16(src, dst);
-    lds_dma16(src + 1024, dst + 1024);
+    const uint8_t* src = dma_base + (int64_t)t * kPlaneBytes;
+    lds_dma16_s(dma_voff, src, dma_lds + stage * kStageBytes);
+    lds_dma16_s(dma_voff2, src, dma_lds + stage * kStageBytes + 1024);
   };
   // Operand reads: lane (l32, half) reads chunk 2m + half of row l32.
   const uint32_t rd0 = l32 * 64 + 16 * (half ^ swz(l32));
@@ -317,6 +321,11 @@ __device__ __forceinline__ void attend_item(const AttnArgs& a, int nqt, int nkt_
   f32x16 o = {};
   float l_run = 0.f;
   int e_min = 0;  // smallest v^T plane exponent over the visited tiles
+  // The block's prepare projection writes one plane exponent per head and
+  // operand, so the product scale and the v^T tile shift are the same for
+  // every key tile (set after the prologue's first barrier).
+  float st_head = 1.0f;
+  int g_head = 0;
 
   auto run = [&](auto exact_tag, auto constant_tag) {
     constexpr bool kExact = decltype(exact_tag)::value;
@@ -326,8 +335,8 @@ __device__ __forceinline__ void attend_item(const AttnArgs& a, int nqt, int nkt_
     const f32x16 zero16 = {};
     // Tile copies into the ring; the constant-mask shortcut needs no K tiles
     // (waves 0 and 1 copy K hi and K lo).
-    auto copy = [&](int t, int st) {
-      if (!kConst || w >= 2) dma(t, st);
+    auto copy = [&](int t, int stage) {
+      if (!kConst || w >= 2) dma(t, stage);
     };
 
     // Q planes, the B operand of S^T: lane holds Q[jq][16m + 8half + e], the
@@ -345,13 +354,13 @@ __device__ __forceinline__ void attend_item(const AttnArgs& a, int nqt, int nkt_
 
     // S^T of the tile in ring stage buf (scaled by 2^(e_q + e_k)); the
     // smallest terms first.
-    auto scores = [&](int buf) -> f32x16 {
+    auto scores = [&](int stage) -> f32x16 {
       f32x16 x = zero16;
       if (kConst) return x;
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
-        const bf16x8 kh = plane_rd(buf, 0, m);
-        const bf16x8 kl = plane_rd(buf, 1, m);
+        const bf16x8 kh = plane_rd(stage, 0, m);
+        const bf16x8 kl = plane_rd(stage, 1, m);
         x = mfma_f16(kl, qh[m], x);
         x = mfma_f16(kh, ql[m], x);
         x = mfma_f16(kh, qh[m], x);
@@ -375,7 +384,7 @@ __device__ __forceinline__ void attend_item(const AttnArgs& a, int nqt, int nkt_
         }
         return;
       }
-      const float st = sq * Sk[t];
+      const float st = kBlock ? st_head : sq * Sk[t];
       if (kExact) {
         if (masked(t)) {
           const f32x16 mb = mask_vals(t);
@@ -452,7 +461,8 @@ __device__ __forceinline__ void attend_item(const AttnArgs& a, int nqt, int nkt_
     // unscaled P.
     auto softmax = [&](const f32x16& x, int t, bf16x8 (&ph)[2], bf16x8 (&pl)[2]) {
       // uniform; the relative bias holds the shift kVShift in kRelOffset
-      const int g = __builtin_amdgcn_readfirstlane(Ev[t]) - e_min - (rel ? 0 : kVShift);
+      const int g = kBlock ? g_head
+                           : __builtin_amdgcn_readfirstlane(Ev[t]) - e_min - (rel ? 0 : kVShift);
       // The weights are formed, summed and split eight at a time (8 keys per
       // operand half m), so only half of them are live at once.
       auto sum8 = [](const f32x8& v) {
@@ -544,11 +554,11 @@ __device__ __forceinline__ void attend_item(const AttnArgs& a, int nqt, int nkt_
     };
 
     // O^T += V^T P^T for the tile in LDS buffer/stage buf.
-    auto pv = [&](int buf, const bf16x8 (&ph)[2], const bf16x8 (&pl)[2]) {
+    auto pv = [&](int stage, const bf16x8 (&ph)[2], const bf16x8 (&pl)[2]) {
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
-        const bf16x8 vh = plane_rd(buf, 2, m);
-        const bf16x8 vl = plane_rd(buf, 3, m);
+        const bf16x8 vh = plane_rd(stage, 2, m);
+        const bf16x8 vl = plane_rd(stage, 3, m);
         o = mfma_f16(vl, ph[m], o);
         o = mfma_f16(vh, pl[m], o);
         o = mfma_f16(vh, ph[m], o);
@@ -563,8 +573,9 @@ __device__ __forceinline__ void attend_item(const AttnArgs& a, int nqt, int nkt_
     // behind at the previous barrier.  The copy is issued after the
     // logits, whose bias-fragment loads the compiler waits for with a
     // count that also covers any later load.  Tiles past the last are
-    // clamped (in range, never used).
-    auto stage = [](int t) { return t & (kStages - 1); };
+    // clamped (in range, never used).  Tile t sits in stage t % 4; the main
+    // loop runs four tiles per iteration, so its stage indices are constants
+    // and every ring address folds into an instruction offset.
     f32x16 x_a = init(0);
     f32x16 x_b = init(clamp(1));
     copy(0, 0);
@@ -575,15 +586,20 @@ __device__ __forceinline__ void attend_item(const AttnArgs& a, int nqt, int nkt_
     e_min = __builtin_amdgcn_readfirstlane(
         inv_scale_exp(__builtin_elementwise_maximum(__builtin_elementwise_maximum(Wv[0], Wv[1]),
                                                     __builtin_elementwise_maximum(Wv[2], Wv[3]))));
+    if constexpr (kBlock) {
+      st_head = sq * Sk[0];
+      g_head = __builtin_amdgcn_readfirstlane(Ev[0]) - e_min - (rel ? 0 : kVShift);
+    }
     finish(x_a, scores(0), 0);
-    auto body = [&](int t, f32x16& cur, f32x16& nxt) {
-      const f32x16 acc = scores(stage(t + 1));
+    // Tile t in ring stage s with its successor's S^T; t + 1 <= last.
+    auto body = [&](int t, int s, f32x16& cur, f32x16& nxt) {
+      const f32x16 acc = scores((s + 1) & 3);
       bf16x8 ph[2], pl[2];
       softmax(cur, t, ph, pl);
       cur = init(clamp(t + 2));
-      pv(stage(t), ph, pl);
+      pv(s, ph, pl);
       finish(nxt, acc, t + 1);
-      copy(clamp(t + 3), stage(t + 3));
+      copy(clamp(t + 3), (s + 3) & 3);
       // Tile t+2 has landed once at most this iteration's two tile loads
       // and four bias-fragment loads are outstanding: vector memory loads
       // retire in issue order.
@@ -593,14 +609,20 @@ __device__ __forceinline__ void attend_item(const AttnArgs& a, int nqt, int nkt_
     auto tail = [&](const f32x16& cur, int t) {
       bf16x8 ph[2], pl[2];
       softmax(cur, t, ph, pl);
-      pv(stage(t), ph, pl);
+      pv(t & 3, ph, pl);
     };
+    for (; kt + 4 < nkt; kt += 4) {
+      body(kt, 0, x_a, x_b);
+      body(kt + 1, 1, x_b, x_a);
+      body(kt + 2, 2, x_a, x_b);
+      body(kt + 3, 3, x_b, x_a);
+    }
     for (; kt + 2 < nkt; kt += 2) {
-      body(kt, x_a, x_b);
-      body(kt + 1, x_b, x_a);
+      body(kt, kt & 3, x_a, x_b);
+      body(kt + 1, (kt + 1) & 3, x_b, x_a);
     }
     if (kt + 1 < nkt) {
-      body(kt, x_a, x_b);
+      body(kt, kt & 3, x_a, x_b);
       tail(x_b, kt + 1);
     } else {
       tail(x_a, kt);

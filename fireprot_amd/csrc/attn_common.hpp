@@ -99,6 +99,22 @@ __device__ __forceinline__ void lds_dma16(const void* src, const uint8_t* dst) {
                : "memory", "m0");
 }
 
+// The same copy addressed as a wave-uniform 64-bit base in SGPRs plus a
+// per-lane 32-bit offset (global_load_lds_dwordx4's saddr form), so that
+// advancing a copy by a tile costs scalar instructions only.  lds_addr: the
+// LDS byte address of lane 0's 16 bytes (wave-uniform).  The instruction
+// offset stays 0: it would move the LDS address as well as the global one.
+__device__ __forceinline__ void lds_dma16_s(uint32_t voff, const void* sbase, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(sbase), "s"(lds_addr)
+               : "memory", "m0");
+}
+// LDS byte address of a pointer into shared memory.
+__device__ __forceinline__ uint32_t lds_address(const uint8_t* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
+}
+
 // s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {

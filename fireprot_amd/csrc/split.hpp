@@ -86,11 +86,12 @@ __device__ __forceinline__ float opaque_minus_one() {
   return m;
 }
 // N values (N even) -> fp16 hi and lo planes, packed two per word.  hi is one
-// v_cvt_pk_f16_f32 per pair; each lo is one v_fma_mixlo_f16 / v_fma_mixhi_f16:
-// fma(float(hi half), -1, x) rounded to fp16 into the low / high half of the
-// word.  x - hi is exact in FP32, so lo = fp16(x - hi) with one rounding, the
-// same bits as a conversion of the FP32 residual (the compiler would spend a
-// v_fma_mix_f32 per value and a v_cvt_pk_f16_f32 per pair on it).
+// v_cvt_pk_f16_f32 per pair; the residuals x - hi are one v_fma_mix_f32 each,
+// fma(float(hi half), -1, x), exact in FP32, and lo is one more
+// v_cvt_pk_f16_f32 per pair: lo = fp16(x - hi) with one rounding.  On gfx950
+// v_fma_mix_f32 and v_cvt_pk_f16_f32 issue at the full VALU rate while
+// v_fma_mixlo_f16 / v_fma_mixhi_f16 (the residual rounded straight into a
+// half of the word) take two issue slots each, so this form is cheaper.
 template <int N>
 __device__ __forceinline__ void split_f16_words(const float* x, uint32_t* hi, uint32_t* lo) {
   const float m1 = opaque_minus_one();
@@ -99,14 +100,14 @@ __device__ __forceinline__ void split_f16_words(const float* x, uint32_t* hi, ui
     hi[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x[2 * i], x[2 * i + 1]}, f16x2));
 #pragma unroll
   for (int i = 0; i < N / 2; ++i) {
-    uint32_t l;
-    asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[1,0,0]"
-        : "=&v"(l)
+    float r0, r1;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]"
+        : "=v"(r0)
         : "v"(hi[i]), "s"(m1), "v"(x[2 * i]));
-    asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-        : "+v"(l)
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+        : "=v"(r1)
         : "v"(hi[i]), "s"(m1), "v"(x[2 * i + 1]));
-    lo[i] = l;
+    lo[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{r0, r1}, f16x2));
   }
 }
 // Already scaled values -> fp16 hi and lo planes (bit patterns in bf16x8/x4).
