@@ -884,11 +884,26 @@ __device__ __forceinline__ void const_item(const AttnArgs& a, int nqt, int nkt, 
     }
     l_run = __builtin_fmaf(ps, w_ref, l_run);
   };
-  // O_r += 2^-(e_t + kVShift) V'^T P'^T for every live row.
+  // O_r += 2^-(e_t + kVShift) V'^T P'^T for every live row.  The block's
+  // prepare projection gives every v^T tile of a head one plane exponent, the
+  // same for every row, so there the products accumulate into O_r directly
+  // and the factor is applied once in the epilogue.
   auto pv = [&](int stage, int t, const bf16x8 (&ph)[2], const bf16x8 (&pl)[2]) {
     for_const_rows([&](auto rc) {
       constexpr int r = decltype(rc)::value;
       if (!((live >> r) & 1u)) return;
+      if constexpr (kBlock) {
+        f32x16& orow = const_row<r>(o);
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          const bf16x8 vh = plane_rd(stage, r, 0, m);
+          const bf16x8 vl = plane_rd(stage, r, 1, m);
+          orow = mfma_f16(vl, ph[m], orow);
+          orow = mfma_f16(vh, pl[m], orow);
+          orow = mfma_f16(vh, ph[m], orow);
+        }
+        return;
+      }
       f32x16 acc = zero16;
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
@@ -956,11 +971,13 @@ __device__ __forceinline__ void const_item(const AttnArgs& a, int nqt, int nkt, 
       if (!((live >> r) & 1u)) return;
       const int b = chunk * kConstRows + r;
       const f32x16& orow = const_row<r>(o);
+      // the block's products carry the head's v^T factor (exact powers of two)
+      const float sc = kBlock ? Sv[r][0] : 1.0f;
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int c = 8 * rr + 4 * half;  // channels c..c+3 of head h
-        f32x4 ov4 = {orow[4 * rr + 0] / l_tot, orow[4 * rr + 1] / l_tot, orow[4 * rr + 2] / l_tot,
-                     orow[4 * rr + 3] / l_tot};
+        f32x4 ov4 = {orow[4 * rr + 0] * sc / l_tot, orow[4 * rr + 1] * sc / l_tot,
+                     orow[4 * rr + 2] * sc / l_tot, orow[4 * rr + 3] * sc / l_tot};
         if constexpr (kBlock) {
           const int64_t col = h * kHeadDim + c;
           if (a.gate) ov4 = ov4 * *(const f32x4*)(a.gate + ((int64_t)b * a.np + jq) * kHidden + col);
