@@ -17,8 +17,7 @@ matrix unit the kernel issues: the FP32 block computes its products on the
 so the peak is the 2.5 PFLOP/s dense fp16/bf16 figure; ``achieved`` counts
 the algorithmic FP32 flop of the key tiles the kernel visits (trailing
 masked tiles whose weights are exactly 0 are left out), and
-``executed_frac`` the 16-bit matrix work it actually issues.  Under
-``FPX_ATTENTION_MFMA=f32`` the peak is the 157.3 TFLOP/s FP32 matrix peak.
+``executed_frac`` the 16-bit matrix work it actually issues.
 ``roofline.traffic`` is the attention kernel's HBM bytes per launch from the
 committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary.  ``cpu_baseline`` times
 the CPU oracle (native PyTorch op order, FP32) on the lease's host cores on
@@ -422,10 +421,9 @@ def bench_openfold3(args) -> dict:
 
     flop = block_flops(n)["core"]
     tflops = flop / (ms * 1e-3) / 1e12
-    fp32_mfma = os.environ.get("FPX_ATTENTION_MFMA") == "f32"
-    of3_visited = visited_key_tiles(n, n - 184, skip=not fp32_mfma)
+    of3_visited = visited_key_tiles(n, n - 184, skip=True)
     of3_flop = flop * of3_visited // (n * -(-n // 32))
-    of3_peak = FP32_MFMA_PEAK_TFLOPS if fp32_mfma else BF16_MFMA_PEAK_TFLOPS
+    of3_peak = BF16_MFMA_PEAK_TFLOPS
     of3_achieved = of3_flop / (ms * 1e-3) / 1e12
     result = {
         "metric": OF3_METRIC,
@@ -448,16 +446,15 @@ def bench_openfold3(args) -> dict:
             "max_abs_vs_native": diff,
         },
         "roofline": {
-            "kernel": ("attention_kernel<kAttnStrided> + staging (fpx_attn_strided)" if fp32_mfma
-                       else "attention_split_kernel<kAttnStaged> + plane, mask and bias staging"
-                            " (fpx_attn_strided)"),
+            "kernel": ("attention_split_kernel<kAttnStaged> + plane, mask and bias staging"
+                       " (fpx_attn_strided)"),
             "bound": "mfma", "achieved": round(of3_achieved, 3), "peak": of3_peak,
             "unit": "TFLOP/s", "frac": round(of3_achieved / of3_peak, 4),
-            "traffic": recorded_traffic("openfold3/fp32-mfma" if fp32_mfma else "openfold3"),
+            "traffic": recorded_traffic("openfold3"),
             "flop_per_launch": of3_flop, "flop_all_tiles": flop,
             "fp32_algorithmic_tflops_all_tiles": round(tflops, 3),
             "avg_launch_ms": round(ms, 4),
-            **({} if fp32_mfma else split_executed(n, n, ms, of3_visited, fp16_planes=True)),
+            **split_executed(n, n, ms, of3_visited, fp16_planes=True),
         },
         "cpu_baseline": None,
     }
@@ -653,9 +650,8 @@ def bench_transition(args) -> dict:
 
     flop = flops(n * n)
     value = flop / (ms * 1e-3) / 1e12
-    # fp16 planes on the 16-bit matrix cores unless the FP32 ones are selected
-    tr_peak = (FP32_MFMA_PEAK_TFLOPS if os.environ.get("FPX_ATTENTION_MFMA") == "f32"
-               else BF16_MFMA_PEAK_TFLOPS)
+    # fp16 planes on the 16-bit matrix cores
+    tr_peak = BF16_MFMA_PEAK_TFLOPS
     result = {
         "metric": TRANSITION_METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
@@ -1178,19 +1174,15 @@ def main() -> int:
     flops = block.block_flops(n)
     step_flop = 2 * flops["block"]
     value = step_flop / (ms_per_step * 1e-3) / 1e12
-    fp32_mfma = os.environ.get("FPX_ATTENTION_MFMA") == "f32"
-    traffic = recorded_traffic(f"{cfg.name}/fp32-mfma" if fp32_mfma else cfg.name)
-    split = cfg.dtype != "bf16" and not fp32_mfma
+    traffic = recorded_traffic(cfg.name)
+    split = cfg.dtype != "bf16"
     if cfg.dtype == "bf16":
         kernel_name = "attention_bf16_kernel (fpx_tri_attn_attend, BF16)"
-    elif split:
+    else:
         kernel_name = ("attention_split_kernel<kAttnBlock, fast | exact> + "
                        "attention_const_kernel<kAttnBlock> (fpx_tri_attn_attend, fp16 planes)")
-    else:
-        kernel_name = "attention_kernel<kAttnBlock> (fpx_tri_attn_attend, FP32 matrix cores)"
-    # The peak of the matrix unit the kernel issues: fp16/bf16 unless the FP32
-    # matrix cores are selected.
-    peak = FP32_MFMA_PEAK_TFLOPS if fp32_mfma and cfg.dtype != "bf16" else BF16_MFMA_PEAK_TFLOPS
+    # The peak of the matrix unit the kernel issues: the dense fp16/bf16 one.
+    peak = BF16_MFMA_PEAK_TFLOPS
     nkt = -(-n // 32)
     visited = visited_key_tiles(n, cfg.valid, skip=cfg.dtype != "bf16")
     visited_flop = flops["core"] * visited // (n * nkt)

@@ -1,4 +1,8 @@
-// Flash-style triangle attention on the CDNA4 FP32 matrix cores.
+// Flash-style triangle attention on the CDNA4 FP32 matrix cores, on the
+// reference C-ABI layout (q, k, v, out [B][n][4][32], a shared [4][n][S]
+// bias): the kernel behind ck_attention, ck_attention_exact1536,
+// ck_attention_vector_bias1000, fpx_attn_core and fpx_attn_core_masked.
+// The block and the strided (OpenFold3) entries run attention_split_kernel.
 //
 // One work-group = (outer row b, head h, 128 queries); four wavefronts, each
 // owning 32 queries.  Keys are streamed in tiles of 32.  K and V^T tiles are
@@ -52,8 +56,6 @@
 #include "kernels.hpp"
 
 #include <cmath>
-#include <cstdlib>
-#include <cstring>
 #include <type_traits>
 
 namespace fpx {
@@ -69,53 +71,9 @@ constexpr int kThreads = 256;
 typedef float KTile[kBk][kHeadDim + kPad];  // [key][channel]
 typedef float VTile[kHeadDim][kBk + kPad];  // [channel][key]
 
-constexpr int kMaxKeys = kTileFlagWords * 32 * kBk;  // 4096: the block's np bound
-
 // Tile sources of one work-group.  Every tile index passed in is in range.
 template <int LAYOUT>
 struct Tiles;
-
-// The block's workspace: q, k [B][H][np][32]; v^T [B][H][32][np]; the bias in
-// fragment order (bias_frag_index), unscaled and scaled by log2(e).  Buffer
-// descriptors per work-group, so a tile's address is one scalar offset and
-// the loop spends no VALU on it.
-template <>
-struct Tiles<kAttnBlock> {
-  __amdgpu_buffer_rsrc_t rk, rv, rb, rb2;
-  uint32_t ok, ov, ob;
-  __device__ __forceinline__ Tiles(const AttnArgs& a, int b, int h, int qt32, int tid, int lane,
-                                   int /*half*/, int /*jq*/) {
-    const int64_t bh = (int64_t)b * kHeads + h;
-    const int64_t nt = a.np >> 5;
-    const int64_t slice = (int64_t)a.np * kHeadDim;
-    const int64_t frag = ((int64_t)h * nt + qt32) * nt * 1024;
-    rk = buffer(a.k + bh * slice, slice * 4);
-    rv = buffer(a.v + bh * slice, slice * 4);
-    rb = buffer(a.bias + frag, nt * 4096);
-    rb2 = buffer(a.bias_l2 + frag, nt * 4096);
-    const int row8 = tid >> 3;
-    const int col4 = (tid & 7) * 4;
-    ok = (uint32_t)(row8 * kHeadDim + col4) * 4;
-    ov = (uint32_t)(row8 * a.np + col4) * 4;
-    ob = (uint32_t)lane * 16;
-  }
-  // thread (row8 = key, col4 = channel group)
-  __device__ __forceinline__ f32x4 k(int t) const { return buffer_f4(rk, ok, (uint32_t)t * 4096); }
-  // thread (row8 = channel, col4 = key group)
-  __device__ __forceinline__ f32x4 v(int t) const { return buffer_f4(rv, ov, (uint32_t)t * 128); }
-  static __device__ __forceinline__ void store_v(VTile& vs, f32x4 v, int row8, int col4) {
-    *(f32x4*)&vs[row8][col4] = v;
-  }
-  // The wave's [32 queries x 32 keys] bias fragment of key tile t: one
-  // contiguous 4 KB block, four coalesced 1 KB loads.
-  __device__ __forceinline__ f32x16 frag(__amdgpu_buffer_rsrc_t r, int t) const {
-    const uint32_t s = (uint32_t)t * 4096;
-    return cat4(buffer_f4(r, ob, s), buffer_f4(r, ob + 1024, s), buffer_f4(r, ob + 2048, s),
-                buffer_f4(r, ob + 3072, s));
-  }
-  __device__ __forceinline__ f32x16 bias(int t) const { return frag(rb, t); }
-  __device__ __forceinline__ f32x16 bias_l2(int t) const { return frag(rb2, t); }
-};
 
 // The reference C-ABI layout (kernels/amd/fireprot_ck_attention.cpp:34-43):
 // q, k, v, out [B][n][H][32]; bias [H][n][bias_stride]; mask bias nullable.
@@ -175,50 +133,6 @@ struct Tiles<kAttnHeadLast> {
   }
 };
 
-// A caller's strided q/k/v/out (kAttnStrided) with the staged bias of the
-// block layout.  K and V rows are read through buffer descriptors over the
-// (b, h) slice; keys past n are clamped to key n - 1 (finite values whose
-// weights are exactly 0, since their staged mask bias is -inf).  V rows are
-// transposed on their way into LDS.
-template <>
-struct Tiles<kAttnStrided> {
-  __amdgpu_buffer_rsrc_t rk, rv, rb, rb2;
-  uint32_t ob, ck, cv, sk, sv;
-  int key, last_key;
-  __device__ __forceinline__ Tiles(const AttnArgs& a, int b, int h, int qt32, int tid, int lane,
-                                   int /*half*/, int /*jq*/) {
-    const int64_t nt = a.np >> 5;
-    const int64_t frag = ((int64_t)h * nt + qt32) * nt * 1024;
-    rk = buffer(a.k + b * a.ks[0] + h * a.ks[1], ((int64_t)(a.n - 1) * a.ks[2] + kHeadDim) * 4);
-    rv = buffer(a.v + b * a.vs[0] + h * a.vs[1], ((int64_t)(a.n - 1) * a.vs[2] + kHeadDim) * 4);
-    rb = buffer(a.bias + frag, nt * 4096);
-    rb2 = buffer(a.bias_l2 + frag, nt * 4096);
-    ob = (uint32_t)lane * 16;
-    key = tid >> 3;
-    last_key = a.n - 1;
-    ck = (uint32_t)((tid & 7) * 4) * 4;
-    sk = (uint32_t)a.ks[2] * 4;
-    sv = (uint32_t)a.vs[2] * 4;
-  }
-  __device__ __forceinline__ uint32_t row(int t) const {
-    const int j = t * kBk + key;
-    return (uint32_t)(j < last_key ? j : last_key);
-  }
-  // thread (row8 = key, col4 = channel group) for both K and V
-  __device__ __forceinline__ f32x4 k(int t) const { return buffer_f4(rk, row(t) * sk + ck, 0); }
-  __device__ __forceinline__ f32x4 v(int t) const { return buffer_f4(rv, row(t) * sv + ck, 0); }
-  static __device__ __forceinline__ void store_v(VTile& vs, f32x4 v, int row8, int col4) {
-    Tiles<kAttnHeadLast>::store_v(vs, v, row8, col4);
-  }
-  __device__ __forceinline__ f32x16 frag(__amdgpu_buffer_rsrc_t r, int t) const {
-    const uint32_t s = (uint32_t)t * 4096;
-    return cat4(buffer_f4(r, ob, s), buffer_f4(r, ob + 1024, s), buffer_f4(r, ob + 2048, s),
-                buffer_f4(r, ob + 3072, s));
-  }
-  __device__ __forceinline__ f32x16 bias(int t) const { return frag(rb, t); }
-  __device__ __forceinline__ f32x16 bias_l2(int t) const { return frag(rb2, t); }
-};
-
 // S^T[key][q] = c + sum_ch K[key][ch] Q[q][ch] for the 32 keys of ks; lane
 // half hb supplies channel 16*hb + s at step s.
 __device__ __forceinline__ f32x16 qk_chain(const KTile& ks, const float* qf, int l32, int half,
@@ -238,11 +152,9 @@ __device__ __forceinline__ f32x16 qk_chain(const KTile& ks, const float* qf, int
 template <int LAYOUT>
 __global__ __launch_bounds__(kThreads, FPX_ATTN_WAVES_PER_SIMD) void attention_kernel(
     AttnArgs a, int nqt, int nkt, uint32_t total) {
-  // Staged layouts carry the mask as a padded row plus tile flags.
-  constexpr bool kStaged = LAYOUT != kAttnHeadLast;
+  static_assert(LAYOUT == kAttnHeadLast, "the reference C-ABI layout only");
   __shared__ __attribute__((aligned(16))) KTile Ks[2];
   __shared__ __attribute__((aligned(16))) VTile Vs[2];
-  __shared__ __attribute__((aligned(16))) float Ms[kStaged ? kMaxKeys : 4];
 
   // Logical order, slowest to fastest: head, block of kRowGroup outer rows,
   // query tile, outer row in the block.  The work-groups that run together
@@ -273,69 +185,23 @@ __global__ __launch_bounds__(kThreads, FPX_ATTN_WAVES_PER_SIMD) void attention_k
 
   // Row classification.  masked(t): some key of tile t has a nonzero mask
   // bias.  has_unmasked: some key k < n of the row has a zero mask bias.
-  uint32_t mw[kTileFlagWords] = {0u, 0u, 0u, 0u};
-  bool any_masked, has_unmasked;
-  if (kStaged) {
-    const uint32_t* f = a.tile_flags + (int64_t)b * kTileFlagParts * kTileFlagWords;
-    uint32_t any = 0u, open = 0u;
-#pragma unroll
-    for (int i = 0; i < kTileFlagWords; ++i) {
-      const int lo = 32 * i;
-      const uint32_t valid = nkt >= lo + 32 ? 0xffffffffu : nkt > lo ? (1u << (nkt - lo)) - 1u : 0u;
-      mw[i] = f[i];
-      any |= mw[i] & valid;
-      open |= ~f[kTileFlagWords + i] & valid;
-    }
-    any_masked = any != 0u;
-    has_unmasked = open != 0u;
-  } else {
-    any_masked = a.mbias != nullptr || a.n % kBk != 0;
-    int found = a.mbias == nullptr;
-    if (!found) {
-      for (int k = tid; k < a.n; k += kThreads)
-        found |= a.mbias[(int64_t)b * a.mb_stride + k] == 0.0f;
-    }
-    has_unmasked = __syncthreads_or(found) != 0;
+  const bool any_masked = a.mbias != nullptr || a.n % kBk != 0;
+  int found = a.mbias == nullptr;
+  if (!found) {
+    for (int k = tid; k < a.n; k += kThreads) found |= a.mbias[(int64_t)b * a.mb_stride + k] == 0.0f;
   }
+  const bool has_unmasked = __syncthreads_or(found) != 0;
   auto masked = [&](int t) -> bool {
-    if (kStaged) {
-      const uint32_t word = t < 32 ? mw[0] : t < 64 ? mw[1] : t < 96 ? mw[2] : mw[3];
-      return (word >> (t & 31)) & 1u;
-    }
     return any_masked && (a.mbias != nullptr || (t + 1) * kBk > a.n);
   };
-  // The block's mask-bias row goes to LDS once (made visible by the prologue
-  // barrier); masked tiles then read their values with four b128 loads.
-  if (kStaged && any_masked) {
-    const float* src = a.mbias + (int64_t)b * a.mb_stride;
-    for (int k = 4 * tid; k < nkt * kBk; k += 4 * kThreads)
-      *(f32x4*)&Ms[k] = *(const f32x4*)(src + k);
-  }
-  auto mask_vals = [&](int t) -> f32x16 {
-    if constexpr (kStaged) {
-      const float* m = &Ms[t * kBk + 4 * half];
-      return cat4(*(const f32x4*)(m), *(const f32x4*)(m + 8), *(const f32x4*)(m + 16),
-                  *(const f32x4*)(m + 24));
-    } else {
-      return io.mask(t);
-    }
-  };
+  auto mask_vals = [&](int t) -> f32x16 { return io.mask(t); };
 
   // Q fragment (B operand of S^T = K Q^T): lane holds Q[jq][16*half + s].
   float qf[16];
   {
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-    const float* src;
-    bool ok = true;
-    if (LAYOUT == kAttnBlock) {
-      src = a.q + (((int64_t)b * kHeads + h) * a.np + jq) * kHeadDim + 16 * half;
-    } else if (LAYOUT == kAttnStrided) {
-      ok = jq < a.n;
-      src = a.q + b * a.qs[0] + h * a.qs[1] + (int64_t)(ok ? jq : 0) * a.qs[2] + 16 * half;
-    } else {
-      ok = jq < a.n;
-      src = a.q + (((int64_t)b * a.n + (ok ? jq : 0)) * kHeads + h) * kHeadDim + 16 * half;
-    }
+    const bool ok = jq < a.n;
+    const float* src = a.q + (((int64_t)b * a.n + (ok ? jq : 0)) * kHeads + h) * kHeadDim + 16 * half;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const f32x4 v = ok ? *(const f32x4*)(src + 4 * t) : zero;
@@ -516,53 +382,23 @@ __global__ __launch_bounds__(kThreads, FPX_ATTN_WAVES_PER_SIMD) void attention_k
       const int c = 8 * rr + 4 * half;  // channels c..c+3 of head h
       f32x4 ov = {o[4 * rr + 0] / l_tot, o[4 * rr + 1] / l_tot, o[4 * rr + 2] / l_tot,
                   o[4 * rr + 3] / l_tot};
-      if (LAYOUT == kAttnBlock) {
-        const int64_t col = h * kHeadDim + c;
-        if (a.gate) ov = ov * *(const f32x4*)(a.gate + ((int64_t)b * a.np + jq) * kHidden + col);
-        *(f32x4*)(a.out + ((int64_t)b * a.n + jq) * kHidden + col) = ov;
-      } else if (LAYOUT == kAttnStrided) {
-        *(f32x4*)(a.out + b * a.os[0] + h * a.os[1] + (int64_t)jq * a.os[2] + c) = ov;
-      } else {
-        *(f32x4*)(a.out + (((int64_t)b * a.n + jq) * kHeads + h) * kHeadDim + c) = ov;
-      }
+      *(f32x4*)(a.out + (((int64_t)b * a.n + jq) * kHeads + h) * kHeadDim + c) = ov;
     }
   }
 }
 
 }  // namespace
 
-bool fp32_matrix_cores_selected() {
-  static const bool fp32 = [] {
-    const char* v = std::getenv("FPX_ATTENTION_MFMA");
-    return v != nullptr && std::strcmp(v, "f32") == 0;
-  }();
-  return fp32;
-}
-
 hipError_t launch_attention(int layout, const AttnArgs& a, hipStream_t stream) {
-  if (layout == kAttnBlock && !fp32_matrix_cores_selected()) return launch_attention_split(layout, a, stream);
-  // Query tiles cover the padded extent; key tiles stop at the last real key
-  // (tiles wholly past n hold only -inf mask bias and contribute nothing).
-  const int nqt = (int)((layout != kAttnHeadLast ? a.np : round_up(a.n, kBq)) / kBq);
+  if (layout != kAttnHeadLast) return hipErrorInvalidValue;
+  const int nqt = (int)(round_up(a.n, kBq) / kBq);
   const int nkt = (int)(round_up(a.n, kBk) / kBk);
   const uint64_t groups = ((uint64_t)a.batch + kRowGroup - 1) / kRowGroup;
   const uint64_t total = groups * kRowGroup * kHeads * nqt;
   if (total == 0) return hipSuccess;
   if (total > 0x7fffffffull) return hipErrorInvalidValue;
-  if (layout != kAttnHeadLast) {
-    if (a.tile_flags == nullptr || a.bias_l2 == nullptr || nkt > kTileFlagWords * 32)
-      return hipErrorInvalidValue;
-    if (layout == kAttnBlock) {
-      hipLaunchKernelGGL(attention_kernel<kAttnBlock>, dim3((uint32_t)total), dim3(kThreads), 0,
-                         stream, a, nqt, nkt, (uint32_t)total);
-    } else {
-      hipLaunchKernelGGL(attention_kernel<kAttnStrided>, dim3((uint32_t)total), dim3(kThreads),
-                         0, stream, a, nqt, nkt, (uint32_t)total);
-    }
-  } else {
-    hipLaunchKernelGGL(attention_kernel<kAttnHeadLast>, dim3((uint32_t)total), dim3(kThreads), 0,
-                       stream, a, nqt, nkt, (uint32_t)total);
-  }
+  hipLaunchKernelGGL(attention_kernel<kAttnHeadLast>, dim3((uint32_t)total), dim3(kThreads), 0,
+                     stream, a, nqt, nkt, (uint32_t)total);
   return hipGetLastError();
 }
 

@@ -37,8 +37,8 @@ size_t elem_bytes(int dtype) { return dtype == FPX_BF16 ? 2 : 4; }
 //   tile flags [n][kTileFlagParts * kTileFlagWords] uint32, then the
 //   kMagnitudeWords words of the magnitude record; scales [3][n][4][np / 32]
 //   float (the plane layout's per-tile inverse scales of q, k and v^T).
-// FP32 blocks on the BF16 matrix cores hold q, k and v^T in the plane layout
-// (ProjArgs::planes), in the same bytes as FP32 values.
+// FP32 blocks hold q, k and v^T in the fp16 plane layout (ProjArgs), in the
+// same bytes as FP32 values.
 struct BlockWorkspace {
   size_t qh, kh, vt, gs, og, bias, mbias, flags, scales, total;
 };
@@ -215,8 +215,7 @@ StridedWorkspace strided_workspace(int batch, int n) {
 }
 
 // Workspace of fpx_tri_mul, 256-byte aligned segments: a and b, 128 np^2
-// floats each (channel-blocked [8][np / 32][np][16][32] on the fp16-plane
-// path, channel-major [128][np][np] on the FP32 one); x blocked
+// floats each (channel-blocked [8][np / 32][np][16][32]); x blocked
 // [n][np / 32][128][32] float; the row maxima of a and b [2][128][np] uint32.
 struct TriMulWorkspace {
   size_t pa, pb, x, rowmax, total;
@@ -234,18 +233,12 @@ TriMulWorkspace trimul_workspace(int n) {
   return w;
 }
 
-// Workspace of fpx_transition: either h [round_up(rows, 128)][512] float
-// (FP32-matrix-core kernels) or the fused kernel's weight planes (16 chunks
+// Workspace of fpx_transition: the fused kernel's weight planes (16 chunks
 // of 48 KB), folded biases [2][512] float and its plane exponents (5 KB),
-// whichever is larger.
+// whatever the number of rows.
 constexpr size_t kTransitionPlanesBytes = 16 * 48 * 1024;
 constexpr size_t kTransitionFusedBytes = kTransitionPlanesBytes + 2 * 512 * sizeof(float) + 5120;
-size_t transition_h_bytes(int64_t rows) {
-  const size_t h = (size_t)round_up(
-      round_up(rows, 128) * fpx::kTransitionHidden * (int64_t)sizeof(float), 256);
-  return h > kTransitionFusedBytes ? h : kTransitionFusedBytes;
-}
-size_t transition_workspace(int64_t rows) { return transition_h_bytes(rows); }
+size_t transition_workspace(int64_t /*rows*/) { return kTransitionFusedBytes; }
 
 // A [batch][4][n][32] operand with channel stride 1 the strided attention
 // kernel can read: non-negative strides that keep 16-byte rows aligned, and
@@ -385,7 +378,7 @@ int fpx_tri_attn_prepare(int dtype, const void* z, int64_t z_stride0, int64_t z_
   p.scales = w.scales;
   p.np = w.np;
   e = fpx::launch_projection(fpx::kProjBlock, p, s);
-  if (e != hipSuccess || fpx::fp32_matrix_cores_selected()) return status(e);
+  if (e != hipSuccess) return status(e);
   // the fast softmax reads the log2 bias relative to each query's reference
   return status(fpx::launch_bias_reference(w.flags, n, n, w.np, p.tri_bias_l2, w.magnitudes, s));
 }
@@ -428,7 +421,7 @@ int fpx_tri_attn_attend(int dtype, int n, void* workspace, size_t workspace_byte
   a.batch = n;
   a.n = n;
   a.np = w.np;
-  return status(fpx::launch_attention(fpx::kAttnBlock, a, s));
+  return status(fpx::launch_attention_split(fpx::kAttnBlock, a, s));
 }
 
 int fpx_tri_attn_finish(int dtype, const void* w_o, const void* b_o, int n, int ending, void* dz,
@@ -568,8 +561,7 @@ int fpx_attn_strided(const float* q, int64_t q_sb, int64_t q_sh, int64_t q_sn, c
   float* mbias = as<float>(base + ws.mbias);
   uint32_t* flags = as<uint32_t>(base + ws.flags);
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  const bool planes = !fpx::fp32_matrix_cores_selected();
-  uint32_t* mag = planes ? as<uint32_t>(base + ws.magnitudes) : nullptr;
+  uint32_t* mag = as<uint32_t>(base + ws.magnitudes);
   hipError_t e =
       fpx::launch_mask_rows(mask_bias, m_sb, m_sk, batch, n, np, mbias, flags, mag, st);
   if (e != hipSuccess) return status(e);
@@ -593,7 +585,6 @@ int fpx_attn_strided(const float* q, int64_t q_sb, int64_t q_sh, int64_t q_sn, c
   a.batch = batch;
   a.n = n;
   a.np = np;
-  if (!planes) return status(fpx::launch_attention(fpx::kAttnStrided, a, st));
   // q, k, v into the plane layout, then the block attention's kernel on it;
   // the magnitude record enables its trailing masked-tile skip
   void* qp = base + ws.qp;
@@ -716,7 +707,6 @@ int fpx_transition(const float* x, int64_t rows_i, int64_t rows_j, int64_t x_str
   a.w_a = w_a;
   a.w_b = w_b;
   a.w_o = w_o;
-  a.h = static_cast<float*>(workspace);
   a.planes = static_cast<__bf16*>(workspace);
   a.fbias = as<float>(static_cast<char*>(workspace) + kTransitionPlanesBytes);
   a.exps = as<int>(static_cast<char*>(workspace) + kTransitionPlanesBytes + 2 * 512 * sizeof(float));

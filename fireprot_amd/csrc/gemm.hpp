@@ -1,17 +1,10 @@
-// GEMM mainloops shared by the triangle-multiplication contraction and the
-// pair transition's output projection: FP32 matrix cores (gemm_nt_128) and
-// FP32-accurate fp16 planes (gemm_nt_128_f16).
+// The GEMM mainloop of the triangle-multiplication contraction:
+// FP32-accurate products on the 16-bit matrix cores (fp16 hi/lo planes).
 //
 // One work-group (256 threads, four waves) accumulates a 128 x 128 tile
 //   C[i][j] = sum_k A[i][k] B[j][k]
-// with both operands K-contiguous (row-major, row strides lda / ldb floats).
-// Wave w owns the 64 x 64 quadrant (64 (w / 2), 64 (w % 2)) as 2 x 2 blocks
-// of v_mfma_f32_32x32x2_f32.  Keys are consumed in 32-wide stages staged in
-// LDS (rows padded to 36 floats: the b128 fragment reads of 16 lanes hit 64
-// distinct banks), double-buffered so the next stage's global loads are in
-// flight during this stage's 64 MFMAs per wave; one barrier per stage.  Per
-// stage, lane half h feeds keys 16h .. 16h + 15 of the stage (the sum over
-// keys is order-free), so both fragments are contiguous row segments.
+// with both operands K-contiguous.  Wave w owns the 64 x 64 quadrant
+// (64 (w / 2), 64 (w % 2)) as 2 x 2 blocks of 32 x 32 MFMA tiles.
 #pragma once
 
 #include "common.hpp"
@@ -20,10 +13,6 @@
 namespace fpx {
 
 constexpr int kGemmTile = 128;
-constexpr int kKStage = 32;
-constexpr int kKPad = kKStage + 4;
-
-typedef float GemmStage[kGemmTile][kKPad];
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const float* base, int64_t bytes) {
   // dword 3 = 0x00020000: raw 32-bit buffer access on gfx9-family parts.
@@ -36,88 +25,12 @@ __device__ __forceinline__ f32x4 buffer_load_f4(__amdgpu_buffer_rsrc_t r, uint32
   return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
-// acc[rb][cb] (lane l, register r) += C[64 (w / 2) + 32 rb + mfma_row(r, l / 32)]
-//                                       [64 (w % 2) + 32 cb + l % 32]
-// over keys 0 .. 32 nk - 1.  a and b point at row 0 of the two 128-row
-// tiles; all 128 rows of both and all 32 nk keys must be readable (callers
-// pad their buffers), and (127 ld + 32 nk) * 4 bytes must stay below 2 GiB.
-// As and Bs are the caller's LDS stages; the routine ends with a barrier, so
-// they may be reused at once.
-__device__ __forceinline__ void gemm_nt_128(const float* a, int64_t lda, const float* b,
-                                            int64_t ldb, int nk, GemmStage* As, GemmStage* Bs,
-                                            f32x16 (&acc)[2][2]) {
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int half = lane >> 5;
-  const int l32 = lane & 31;
-  const int wi = (w >> 1) * 64;
-  const int wj = (w & 1) * 64;
-
-  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a, (127 * lda + kKStage * nk) * 4);
-  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(b, (127 * ldb + kKStage * nk) * 4);
-  // Thread (row = tid / 8 + 32 u, keys 4 (tid % 8) .. +3) of each stage.
-  const int lrow = tid >> 3;
-  const int lc4 = (tid & 7) * 4;
-  const uint32_t va = (uint32_t)((lrow * lda + lc4) * 4);
-  const uint32_t vb = (uint32_t)((lrow * ldb + lc4) * 4);
-  const uint32_t pa = (uint32_t)(32 * lda * 4);  // 32 rows further down
-  const uint32_t pb = (uint32_t)(32 * ldb * 4);
-
-  f32x4 ga[4], gb[4];
-  auto load = [&](int kt) {
-    const uint32_t s = (uint32_t)kt * (kKStage * 4);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      ga[u] = buffer_load_f4(ra, va + u * pa, s);
-      gb[u] = buffer_load_f4(rb, vb + u * pb, s);
-    }
-  };
-  auto store = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      *(f32x4*)&As[buf][lrow + 32 * u][lc4] = ga[u];
-      *(f32x4*)&Bs[buf][lrow + 32 * u][lc4] = gb[u];
-    }
-  };
-
-  load(0);
-  store(0);
-  if (nk > 1) load(1);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int kc = 16 * half + 4 * t;
-      const f32x4 a0 = *(const f32x4*)&As[buf][wi + l32][kc];
-      const f32x4 a1 = *(const f32x4*)&As[buf][wi + 32 + l32][kc];
-      const f32x4 b0 = *(const f32x4*)&Bs[buf][wj + l32][kc];
-      const f32x4 b1 = *(const f32x4*)&Bs[buf][wj + 32 + l32][kc];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        acc[0][0] = mfma32(a0[e], b0[e], acc[0][0]);
-        acc[0][1] = mfma32(a0[e], b1[e], acc[0][1]);
-        acc[1][0] = mfma32(a1[e], b0[e], acc[1][0]);
-        acc[1][1] = mfma32(a1[e], b1[e], acc[1][1]);
-      }
-    }
-    if (kt + 1 < nk) {
-      store(buf ^ 1);
-      if (kt + 2 < nk) load(kt + 2);
-    }
-    __syncthreads();
-  }
-}
-
-// ------------------------------------------------ FP32-accurate, fp16 cores
-//
 // Stages of 16 keys (one k step), double-buffered; rows padded to 24 16-bit
 // values (48 B), conflict-free b128 reads.
 constexpr int kSplitK = 16;
 constexpr int kSplitRow = kSplitK + 8;
 
-// The same product on v_mfma_f32_32x32x16_f16 with power-of-two scaled fp16
+// The product on v_mfma_f32_32x32x16_f16 with power-of-two scaled fp16
 // (hi, lo) planes (split.hpp): row r of A is scaled by 2^ea[r] and row r of
 // B by 2^eb[r] (ea, eb: 128 per-row exponents, plane_exp of each row's max
 // |value| over all keys, in LDS), so acc[rb][cb] comes out scaled by

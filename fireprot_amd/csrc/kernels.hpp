@@ -13,8 +13,8 @@ namespace fpx {
 //
 // kAttnBlock:  the block's own workspace layout (all extents padded to np,
 //              a multiple of 128; padded keys carry -inf in mbias):
-//                q, k : [B][H][np][32]   (q pre-scaled by 1/sqrt(32))
-//                v    : [B][H][32][np]   (transposed per head)
+//                q, k, v: the plane layout of ProjArgs (q pre-scaled by
+//                        1/sqrt(32); v transposed per head), scales beside
 //                mbias: [B][np]          (required)
 //                tile_flags: [B][kTileFlagParts][kTileFlagWords] bit t of
 //                        part 0 = some key of 32-key tile t has a nonzero
@@ -33,7 +33,8 @@ namespace fpx {
 //                q, k, v, out : [B][n][H][32] (strides n*128, 32, 128, 1)
 //                bias : [H][n][bias_stride]  (batch stride 0)
 //                mbias: nullable, [B] rows of n values, row stride mb_stride
-// kAttnStrided: any caller layout with channel stride 1:
+// kAttnStrided: any caller layout with channel stride 1 (the input of
+//                launch_stage_planes):
 //                q, k, v, out : element (b, h, j, c) at b*s[0] + h*s[1] + j*s[2] + c
 //                               (qs, ks, vs, os), rows 16-byte aligned
 //                mbias, tile_flags, bias, bias_l2 : staged as for kAttnBlock
@@ -97,7 +98,7 @@ struct AttnArgs {
   float* out;
   const uint32_t* tile_flags;
   const uint32_t* magnitudes;  // kAttnBlock: nullable; enables the trailing-tile skip
-  const float* scales;  // kAttnBlock: q, k, v in the plane layout (ProjArgs::planes), or null
+  const float* scales;  // kAttnBlock, kAttnStaged: the planes' inverse scales
   int64_t qs[3];  // kAttnStrided: (batch, head, row) element strides
   int64_t ks[3];
   int64_t vs[3];
@@ -107,16 +108,10 @@ struct AttnArgs {
   int np;
 };
 
-// True when the environment sets FPX_ATTENTION_MFMA=f32 (read once per
-// process): the FP32 attention and projections then run on the FP32 matrix
-// cores (v_mfma_f32_32x32x2_f32) instead of their exact bf16 splits.
-bool fp32_matrix_cores_selected();
-
-// launch_attention: kAttnBlock runs attention_split_kernel (FP32-accurate
-// products on the 16-bit matrix cores) unless fp32_matrix_cores_selected(),
-// which selects attention_kernel; kAttnStrided and kAttnHeadLast run
-// attention_kernel.  launch_attention_split runs attention_split_kernel for
-// kAttnBlock or kAttnStaged.
+// launch_attention: kAttnHeadLast (the reference C-ABI layout) on the FP32
+// matrix cores (attention_kernel).  launch_attention_split runs
+// attention_split_kernel (FP32-accurate products on the 16-bit matrix cores)
+// for kAttnBlock or kAttnStaged.
 hipError_t launch_attention(int layout, const AttnArgs& args, hipStream_t stream);
 hipError_t launch_attention_split(int layout, const AttnArgs& args, hipStream_t stream);
 // The FP32 block after its prepare stage: rewrite bias_l2 ([4][np][np],
@@ -167,9 +162,8 @@ struct ProjArgs {
   float* tri_bias;     // fragment order (bias_frag_index)
   float* tri_bias_l2;  // the same scaled by log2(e)
   uint32_t* magnitudes;  // nullable: max|q|, max|k|, max|v|, max|bias| (kMagnitudeWords)
-  // Plane layout of q, k, v^T (set by launch_projection for the split
-  // kernel; the FP32-matrix-core kernels keep plain FP32).  The (i, h) slice
-  // of np * 128 bytes holds a hi plane and then a lo plane of 16-bit values:
+  // Plane layout of q, k, v^T (kProjBlock): the (i, h) slice of np * 128
+  // bytes holds a hi plane and then a lo plane of 16-bit values:
   //   q, k: [np rows j][32 channels] fp16 of the value times 2^e; hi =
   //         fp16(x 2^e) and lo = fp16(x 2^e - hi) carry 22 bits;
   //   v^T:  [np / 32 key tiles][32 channels][32 key positions] fp16 of the
@@ -182,7 +176,6 @@ struct ProjArgs {
   //         [2^14, 2^15) (v^T: value_plane_exp of the bound);
   //   scales[(t * rows_i + i) * 4 + h][j / 32] = 2^-e for t = 0 (q), 1 (k),
   //         2 (v^T): the same for every row i and tile of a head.
-  int planes;
   float* scales;
   int np;
   // kProjQkv / kProjOut outputs
@@ -192,8 +185,7 @@ struct ProjArgs {
   int accumulate;  // kProjOut: out = out + (x W_o^T + b_o), the residual update
 };
 
-// projection_split_kernel (exact three-plane bf16 splits on the BF16 matrix
-// cores) unless fp32_matrix_cores_selected(), which selects projection_kernel.
+// projection_split_kernel: fp16 hi/lo planes on the 16-bit matrix cores.
 hipError_t launch_projection(int mode, const ProjArgs& args, hipStream_t stream);
 
 // -------------------------------------------------------------- elementwise
@@ -289,8 +281,7 @@ hipError_t launch_attention_bf16(const Bf16AttnArgs& args, hipStream_t stream);
 // Outgoing / incoming triangle multiplicative update, c_z = c_hidden = 128
 // (trimul.hip).  Workspace roles: a and b, 128 np^2 floats each (rows of the
 // contraction frame; rows >= n unused, keys >= n zero): channel-blocked
-// [8][np / 32][np][16][32] on the fp16-plane path, channel-major
-// [128][np][np] on the FP32 one; x blocked [n][np / 32][128][32].  np is a
+// [8][np / 32][np][16][32]; x blocked [n][np / 32][128][32].  np is a
 // multiple of 128.
 struct TriMulArgs {
   const float* z;
@@ -346,10 +337,8 @@ struct TransitionArgs {
   const float* w_a;   // [512][128]
   const float* w_b;   // [512][128]
   const float* w_o;   // [128][512]
-  float* h;           // FP32-matrix-core path: [round_up(rows, 128)][512]
-  // fp16-plane (fused) path: the 16 chunks' weight planes (fp16 bits, 768 KB),
-  // the folded biases [2][512] and the plane exponents (1156 ints, see
-  // transition.hip)
+  // the 16 chunks' weight planes (fp16 bits, 768 KB), the folded biases
+  // [2][512] and the plane exponents (1156 ints, see transition.hip)
   __bf16* planes;
   float* fbias;
   int* exps;

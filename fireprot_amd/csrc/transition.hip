@@ -1,152 +1,23 @@
-// Pair transition (Protenix Transition, n = 4, c = 128) on the CDNA4 FP32
-// matrix cores:
+// Pair transition (Protenix Transition, n = 4, c = 128) on the CDNA4 16-bit
+// matrix cores, FP32-accurate:
 //
 //   h   = silu(LN(x) W_a^T) * (LN(x) W_b^T)       [rows][512]
 //   out = h W_o^T  (or out + h W_o^T, the residual)  [rows][128]
 //
-// transition_up_kernel: persistent; a work-group serves one quarter (128) of
-//   the 512 hidden channels for its whole life, each of its 4 waves holding
-//   the W_a and W_b fragments of 32 hidden channels in 128 VGPRs.  Per tile of
-//   32 pair rows: LayerNorm of the raw rows (fetched a tile ahead) into a
-//   second LDS buffer, 128 MFMAs per wave, and h stored row-major.
-// transition_down_kernel: one 128-row tile of h W_o^T per work-group on the
-//   shared gemm_nt_128 mainloop (K = 512), with the strided, optionally
-//   accumulated store.
-// Those two (FP32 matrix cores; h through HBM) serve FPX_ATTENTION_MFMA=f32.
-// The default path is one fused kernel on the 16-bit matrix cores, with h
-// never leaving the registers (transition_fused_kernel below).
+// One fused kernel with h never leaving the registers
+// (transition_fused_kernel below), after two small kernels that fold the
+// LayerNorm affine into the weights and split them into scaled fp16 planes.
 #include "attn_common.hpp"
 #include "common.hpp"
-#include "gemm.hpp"
 #include "kernels.hpp"
+#include "split.hpp"
 
 #include <type_traits>
 
 namespace fpx {
 namespace {
 
-constexpr int kRows = 32;
-constexpr int kLds = kChannels + 4;
 constexpr int kHid = kTransitionHidden;
-constexpr int kQuarters = kHid / kChannels;  // 4
-
-__global__ __launch_bounds__(256, 2) void transition_up_kernel(TransitionArgs a, int tiles_j,
-                                                               int ntiles, int slots) {
-  __shared__ __attribute__((aligned(16))) float xs[2][kRows][kLds];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int half = lane >> 5;
-  const int l32 = lane & 31;
-  const int quarter = (int)(blockIdx.x % kQuarters);
-  const int col = quarter * kChannels + 32 * w + l32;  // hidden channel of this lane
-
-  float wa[64], wb[64];
-  load_fragment(a.w_a, col, half, wa);
-  load_fragment(a.w_b, col, half, wb);
-  f32x2 lnw = {1.f, 1.f}, lnb = {0.f, 0.f};
-  if (a.ln_w) lnw = *(const f32x2*)(a.ln_w + 2 * lane);
-  if (a.ln_b) lnb = *(const f32x2*)(a.ln_b + 2 * lane);
-
-  f32x2 st[kRows / 4];
-  auto fetch = [&](int tile) {
-    const int i = tile / tiles_j;
-    const int j0 = (tile % tiles_j) * kRows;
-#pragma unroll
-    for (int rr = 0; rr < kRows / 4; ++rr) {
-      const int j = j0 + 8 * w + rr;
-      st[rr] = j < a.rows_j
-                   ? *(const f32x2*)(a.x + (int64_t)i * a.xs_i + (int64_t)j * a.xs_j + 2 * lane)
-                   : f32x2{0.f, 0.f};
-    }
-  };
-  auto stage = [&](int buf) {
-#pragma unroll
-    for (int rr = 0; rr < kRows / 4; ++rr) {
-      float d0, d1, rstd;
-      ln_stats_c128(st[rr].x, st[rr].y, a.eps, d0, d1, rstd);
-      *(f32x2*)&xs[buf][8 * w + rr][2 * lane] =
-          f32x2{d0 * rstd * lnw.x + lnb.x, d1 * rstd * lnw.y + lnb.y};
-    }
-  };
-
-  __builtin_amdgcn_s_waitcnt(0);
-  int tile = (int)(blockIdx.x / kQuarters);  // this work-group's slot; grid <= 4 * ntiles
-  fetch(tile);
-  stage(0);
-  int next = tile + slots;
-  if (next < ntiles) fetch(next);
-  __syncthreads();
-  for (int buf = 0; tile < ntiles; buf ^= 1) {
-    f32x16 acc_a = {}, acc_b = {};
-#pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      const f32x4 av = *(const f32x4*)&xs[buf][l32][64 * half + 4 * t];
-      acc_a = mfma32(av.x, wa[4 * t + 0], acc_a);
-      acc_b = mfma32(av.x, wb[4 * t + 0], acc_b);
-      acc_a = mfma32(av.y, wa[4 * t + 1], acc_a);
-      acc_b = mfma32(av.y, wb[4 * t + 1], acc_b);
-      acc_a = mfma32(av.z, wa[4 * t + 2], acc_a);
-      acc_b = mfma32(av.z, wb[4 * t + 2], acc_b);
-      acc_a = mfma32(av.w, wa[4 * t + 3], acc_a);
-      acc_b = mfma32(av.w, wb[4 * t + 3], acc_b);
-    }
-    if (next < ntiles) {
-      stage(buf ^ 1);
-      if (next + slots < ntiles) fetch(next + slots);
-    }
-    // h row of pair (i, j) is i * rows_j + j; rows past rows_j are not stored.
-    const int i = tile / tiles_j;
-    const int j0 = (tile % tiles_j) * kRows;
-    float* dst = a.h + ((int64_t)i * a.rows_j) * kHid + col;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int j = j0 + mfma_row(r, half);
-      if (j < a.rows_j) {
-        const float av = acc_a[r];
-        dst[(int64_t)j * kHid] = av * sigmoidf_(av) * acc_b[r];  // silu(a) * b
-      }
-    }
-    __syncthreads();
-    tile = next;
-    next += slots;
-  }
-}
-
-// h W_o^T for one 128-row tile of h on the FP32 matrix cores.
-__global__ __launch_bounds__(256, 2) void transition_down_kernel(TransitionArgs a, int64_t rows) {
-  __shared__ __attribute__((aligned(16))) GemmStage As[2];
-  __shared__ __attribute__((aligned(16))) GemmStage Bs[2];
-  const int64_t r0 = (int64_t)blockIdx.x * kGemmTile;
-  f32x16 acc[2][2] = {};
-  const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-  const int half = lane >> 5;
-  const int l32 = lane & 31;
-  const int wi = (w >> 1) * 64;
-  const int wj = (w & 1) * 64;
-  // W_o is [128 out][512 in]: the B operand rows are output channels.
-  gemm_nt_128(a.h + r0 * kHid, kHid, a.w_o, kHid, kHid / kKStage, As, Bs, acc);
-
-  const bool residual = a.accumulate != 0;
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int64_t row = r0 + wi + 32 * rb + mfma_row(r, half);
-      if (row >= rows) continue;
-      const int64_t i = row / a.rows_j;
-      const int64_t j = row - i * a.rows_j;
-      float* d = a.out + i * a.os_i + j * a.os_j + wj + l32;
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb) {
-        const float v = acc[rb][cb][r];
-        d[32 * cb] = residual ? d[32 * cb] + v : v;
-      }
-    }
-  }
-}
 
 // ------------------------------------------------------- fused, fp16 cores
 // out = x + silu(y Wa'^T + ba) * (y Wb'^T + bb) Wo^T with y = (x - mean)
@@ -486,40 +357,23 @@ __global__ __launch_bounds__(kFusedWaves * 64, 1) void transition_fused_kernel(T
   wait_vmcnt<0>();  // no copy in flight when the work-group ends
 }
 
-int grid_cap(int per_cu) { return device_cu_count() * per_cu; }
-
 }  // namespace
 
 hipError_t launch_transition(const TransitionArgs& a, hipStream_t stream) {
   const int64_t rows = (int64_t)a.rows_i * a.rows_j;
   if (rows == 0) return hipSuccess;
-  const int tiles_j = (a.rows_j + kRows - 1) / kRows;
-  const int64_t up_tiles = (int64_t)a.rows_i * tiles_j;
-  const int64_t down_tiles = (rows + kGemmTile - 1) / kGemmTile;
-  if (up_tiles > 0x7fffffff || down_tiles > 0x7fffffff) return hipErrorInvalidValue;
-  // Persistent up-projection: slots per quarter, 2 work-groups per CU in all.
-  int64_t slots = grid_cap(2) / kQuarters;
-  if (slots > up_tiles) slots = up_tiles;
-  if (slots < 1) slots = 1;
+  if (a.planes == nullptr || a.fbias == nullptr || a.exps == nullptr) return hipErrorInvalidValue;
+  const int64_t tiles = (rows + kFusedRows - 1) / kFusedRows;
+  if (tiles > 0x7fffffff) return hipErrorInvalidValue;
+  const int64_t grid = tiles < device_cu_count() ? tiles : device_cu_count();
   hipError_t e;
-  if (!fp32_matrix_cores_selected()) {
-    if (a.planes == nullptr || a.fbias == nullptr || a.exps == nullptr) return hipErrorInvalidValue;
-    const int64_t tiles = (rows + kFusedRows - 1) / kFusedRows;
-    const int64_t grid = tiles < device_cu_count() ? tiles : device_cu_count();
-    hipLaunchKernelGGL(transition_prep_kernel, dim3(kPrepGroups), dim3(512), 0, stream, a);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(transition_planes_kernel, dim3((kChunks * kChunkValues / 2 + 255) / 256),
-                       dim3(256), 0, stream, a);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(transition_fused_kernel, dim3((uint32_t)grid), dim3(kFusedWaves * 64), 0,
-                       stream, a, rows, tiles);
-    return hipGetLastError();
-  }
-  hipLaunchKernelGGL(transition_up_kernel, dim3((uint32_t)(slots * kQuarters)), dim3(256), 0,
-                     stream, a, tiles_j, (int)up_tiles, (int)slots);
+  hipLaunchKernelGGL(transition_prep_kernel, dim3(kPrepGroups), dim3(512), 0, stream, a);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL(transition_down_kernel, dim3((uint32_t)down_tiles), dim3(256), 0, stream, a,
-                     rows);
+  hipLaunchKernelGGL(transition_planes_kernel, dim3((kChunks * kChunkValues / 2 + 255) / 256),
+                     dim3(256), 0, stream, a);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(transition_fused_kernel, dim3((uint32_t)grid), dim3(kFusedWaves * 64), 0,
+                     stream, a, rows, tiles);
   return hipGetLastError();
 }
 

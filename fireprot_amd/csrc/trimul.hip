@@ -1,5 +1,6 @@
-// Triangle multiplicative update (outgoing and incoming) on the CDNA4 FP32
-// matrix cores, c_z = c_hidden = 128.
+// Triangle multiplicative update (outgoing and incoming) on the CDNA4 16-bit
+// matrix cores, FP32-accurate (scaled fp16 hi/lo planes, three terms per
+// product), c_z = c_hidden = 128.
 //
 //   a[r, k, c] = mask[r, k] * sigmoid(LN_in(z) W_a_g^T + b)[c] * (LN_in(z) W_a_p^T + b)[c]
 //   b[r, k, c] = the same with the b weights
@@ -11,176 +12,48 @@
 // z[k, r] for the incoming one, so both directions are one kernel chain; the
 // incoming read of z^T goes through strides, with no transposed copy.
 //
-// Three launches (the default fp16-plane kernels; the FP32-matrix-core
-// ones in brackets):
-//   gated_split_kernel<kGatedTriMul> [trimul_project_kernel]
+// Three launches:
+//   gated_split_kernel<kGatedTriMul>
 //                          LN_in, the four 128x128 projections, sigmoid gates
 //                          and the mask; writes a and b channel-blocked (each
 //                          channel's rows as 32-key runs, gated_split.hpp)
-//                          with each (channel, row)'s max |value| [channel-
-//                          major [128][np rows][np keys], keys contiguous]
+//                          with each (channel, row)'s max |value|
 //   trimul_contract_kernel x_c = A_c B_c^T for the 128 channels: a batched
 //                          GEMM on 128 x 128 output tiles, key stages
 //                          double-buffered in LDS, XCD-aware tile order
-//   trimul_finish_split_kernel [trimul_finish_kernel]
+//   trimul_finish_split_kernel
 //                          LN_out(x) W_z^T and LN_in(z) W_g^T for 32 pairs
 //                          per tile, the sigmoid gate and the in-place write
 #include "common.hpp"
 #include "gated_split.hpp"
 
-#include <type_traits>
 #include "gemm.hpp"
 #include "kernels.hpp"
 
 namespace fpx {
 namespace {
 
-constexpr int kRows = 32;                 // pair rows per projection tile
-constexpr int kLds = kChannels + 4;       // padded LDS row (floats)
-
-// ------------------------------------------------------------ projection
-// Persistent; 8 waves: waves 0-3 produce a, waves 4-7 produce b, each for 32
-// channels, with both the projection and the gate fragments resident (two
-// accumulators, 128 MFMAs per wave per 32-row tile).  The next tile's raw
-// rows are fetched two tiles ahead and normalised into the second LDS buffer
-// while this tile's MFMAs run.
-constexpr int kProjWaves = 8;
-
-__global__ __launch_bounds__(kProjWaves * 64) void trimul_project_kernel(TriMulArgs a, int tiles_k,
-                                                                         int ntiles) {
-  constexpr int kRowsPerWave = kRows / kProjWaves;
-  __shared__ __attribute__((aligned(16))) float xs[2][kRows][kLds];
-  __shared__ float ms[2][kRows];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int half = lane >> 5;
-  const int l32 = lane & 31;
-  const int side = w >> 2;             // 0: a, 1: b
-  const int col = 32 * (w & 3) + l32;  // hidden channel of this lane
-
-  float wp[64], wg[64];
-  load_fragment(a.w_ab[2 * side], col, half, wp);
-  load_fragment(a.w_ab[2 * side + 1], col, half, wg);
-  const float bp = a.b_ab[2 * side] ? a.b_ab[2 * side][col] : 0.f;
-  const float bq = a.b_ab[2 * side + 1] ? a.b_ab[2 * side + 1][col] : 0.f;
-  f32x2 lnw = {1.f, 1.f}, lnb = {0.f, 0.f};
-  if (a.ln_in_w) lnw = *(const f32x2*)(a.ln_in_w + 2 * lane);
-  if (a.ln_in_b) lnb = *(const f32x2*)(a.ln_in_b + 2 * lane);
-
-  // Contraction frame: pair (r, k) is z[r, k] (outgoing) or z[k, r] (incoming).
-  const int64_t zr = a.outgoing ? a.zs_i : a.zs_j;
-  const int64_t zk = a.outgoing ? a.zs_j : a.zs_i;
-  const int64_t mr = a.outgoing ? a.ms_i : a.ms_j;
-  const int64_t mk = a.outgoing ? a.ms_j : a.ms_i;
-  const int n = a.n;
-  const int np = a.np;
-
-  f32x2 st[kRowsPerWave];
-  float st_mask = 0.f;
-
-  auto fetch = [&](int tile) {
-    const int r = tile / tiles_k;
-    const int k0 = (tile % tiles_k) * kRows;
-#pragma unroll
-    for (int rr = 0; rr < kRowsPerWave; ++rr) {
-      const int k = k0 + w * kRowsPerWave + rr;
-      st[rr] = k < n ? *(const f32x2*)(a.z + (int64_t)r * zr + (int64_t)k * zk + 2 * lane)
-                     : f32x2{0.f, 0.f};
-    }
-    if (tid < kRows) {
-      const int k = k0 + tid;
-      st_mask = k < n ? (a.mask ? a.mask[(int64_t)r * mr + (int64_t)k * mk] : 1.f) : 0.f;
-    }
-  };
-
-  auto stage = [&](int buf) {
-#pragma unroll
-    for (int rr = 0; rr < kRowsPerWave; ++rr) {
-      const int row = w * kRowsPerWave + rr;
-      float d0, d1, rstd;
-      ln_stats_c128(st[rr].x, st[rr].y, a.eps_in, d0, d1, rstd);
-      *(f32x2*)&xs[buf][row][2 * lane] =
-          f32x2{d0 * rstd * lnw.x + lnb.x, d1 * rstd * lnw.y + lnb.y};
-    }
-    if (tid < kRows) ms[buf][tid] = st_mask;
-  };
-
-  auto epilogue = [&](int tile, int buf, const f32x16& acc_p, const f32x16& acc_g) {
-    const int r = tile / tiles_k;
-    const int k0 = (tile % tiles_k) * kRows;
-    float* dst = (side ? a.pb : a.pa) + ((int64_t)col * np + r) * np + k0 + 4 * half;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      float v[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int kk = 8 * rr + 4 * half + e;
-        const float m = ms[buf][kk];
-        // native order: a = mask; a = a * sigmoid(g); a = a * p
-        const float val = (m * sigmoidf_(acc_g[4 * rr + e] + bq)) * (acc_p[4 * rr + e] + bp);
-        v[e] = k0 + kk < n ? val : 0.f;
-      }
-      *(f32x4*)(dst + 8 * rr) = f32x4{v[0], v[1], v[2], v[3]};
-    }
-  };
-
-  __builtin_amdgcn_s_waitcnt(0);
-  int tile = blockIdx.x;  // grid <= ntiles
-  fetch(tile);
-  stage(0);
-  int next = tile + (int)gridDim.x;
-  if (next < ntiles) fetch(next);
-  __syncthreads();
-  for (int buf = 0; tile < ntiles; buf ^= 1) {
-    f32x16 acc_p = {}, acc_g = {};
-#pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      const f32x4 av = *(const f32x4*)&xs[buf][l32][64 * half + 4 * t];
-      acc_p = mfma32(av.x, wp[4 * t + 0], acc_p);
-      acc_g = mfma32(av.x, wg[4 * t + 0], acc_g);
-      acc_p = mfma32(av.y, wp[4 * t + 1], acc_p);
-      acc_g = mfma32(av.y, wg[4 * t + 1], acc_g);
-      acc_p = mfma32(av.z, wp[4 * t + 2], acc_p);
-      acc_g = mfma32(av.z, wg[4 * t + 2], acc_g);
-      acc_p = mfma32(av.w, wp[4 * t + 3], acc_p);
-      acc_g = mfma32(av.w, wg[4 * t + 3], acc_g);
-    }
-    if (next < ntiles) {
-      stage(buf ^ 1);
-      if (next + (int)gridDim.x < ntiles) fetch(next + gridDim.x);
-    }
-    epilogue(tile, buf, acc_p, acc_g);
-    __syncthreads();
-    tile = next;
-    next += gridDim.x;
-  }
-}
+constexpr int kRows = 32;                 // pair rows per finish tile
 
 // ----------------------------------------------------------- contraction
 // One work-group = (channel c, 128 rows i, 128 columns j) of x_c = A_c B_c^T
-// (gemm_nt_128 over the np keys).  Work-groups of one channel are consecutive
+// (gemm_nt_128_f16 over the np keys).  Work-groups of one channel are consecutive
 // in the logical order, and xcd_remap gives each XCD a contiguous range, so
 // the A and B row panels a range touches stay in that XCD's L2.
-// kSplit: gemm_nt_128_f16 (16-bit matrix cores, scaled fp16 planes), with
-// each row's exponent from the row maxima the projection recorded, on the
+// gemm_nt_128_f16 (16-bit matrix cores, scaled fp16 planes), with each row's
+// exponent from the row maxima the projection recorded, on the
 // channel-blocked a and b of gated_split_kernel<kGatedTriMul> (channel c's
 // row r at ((c / 16) np / 32 np + r) 512 + (c % 16) 32, rows 512 floats
-// apart, 32-key runs np * 512 floats apart); the FP32 path reads a and b
-// channel-major ([128][np][np]).
-template <bool kSplit>
+// apart, 32-key runs np * 512 floats apart).
 __global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const float* __restrict__ pa,
                                                                  const float* __restrict__ pb,
                                                                  const uint32_t* __restrict__ rowmax,
                                                                  float* __restrict__ x, int n,
                                                                  int np, int tiles,
                                                                  uint32_t total) {
-  // fp16 planes take two thirds of the FP32 stages' LDS: three work-groups per CU.
-  using Stage = std::conditional_t<kSplit, F16Stage, GemmStage>;
-  __shared__ __attribute__((aligned(16))) Stage As[2];
-  __shared__ __attribute__((aligned(16))) Stage Bs[2];
-  __shared__ int ea[kSplit ? kGemmTile : 1], eb[kSplit ? kGemmTile : 1];
+  __shared__ __attribute__((aligned(16))) F16Stage As[2];
+  __shared__ __attribute__((aligned(16))) F16Stage Bs[2];
+  __shared__ int ea[kGemmTile], eb[kGemmTile];
 
   const uint32_t logical = xcd_remap(blockIdx.x, total);
   const int per_channel = tiles * tiles;
@@ -193,9 +66,8 @@ __global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const float* __
   const int half = lane >> 5;
   const int l32 = lane & 31;
 
-  const int64_t slice = (int64_t)np * np;
   f32x16 acc[2][2] = {};
-  if constexpr (kSplit) {
+  {
     const int t = threadIdx.x;
     const uint32_t* rm = rowmax + ((int64_t)(t >> 7) * kChannels + c) * np + ((t >> 7) ? j0 : i0);
     (t >> 7 ? eb : ea)[t & 127] = plane_exp(__builtin_bit_cast(float, rm[t & 127]));
@@ -214,9 +86,7 @@ __global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const float* __
           acc[rb][cb][r] = __builtin_ldexpf(acc[rb][cb][r], -(ea[(w >> 1) * 64 + 32 * rb + mfma_row(r, half)] + ej));
       }
     }
-  } else
-    gemm_nt_128(pa + c * slice + (int64_t)i0 * np, np, pb + c * slice + (int64_t)j0 * np, np,
-                np / kKStage, As, Bs, acc);
+  }
 
   // x is blocked [n][np / 32][128 channels][32 columns]: the finish kernel
   // reads one contiguous 16 KB block per 32-pair tile.
@@ -240,124 +110,9 @@ __global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const float* __
 }
 
 // ---------------------------------------------------------------- finish
-// Persistent; 4 waves, each owning 32 output channels with the W_z and W_g
-// fragments resident.  Per tile of 32 pairs (i, j0 .. j0 + 31): the x block
-// is read (16 KB, contiguous) and transposed into LDS, z's rows are read in
-// the natural frame, both are normalised in place, then two 64-MFMA chains
-// per wave and the gated, optionally accumulated, store.
-__global__ __launch_bounds__(256, 2) void trimul_finish_kernel(TriMulArgs a, int tiles_j,
-                                                               int ntiles) {
-  __shared__ __attribute__((aligned(16))) float xs[kRows][kLds];
-  __shared__ __attribute__((aligned(16))) float zs[kRows][kLds];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int half = lane >> 5;
-  const int l32 = lane & 31;
-  const int col = 32 * w + l32;
-
-  float wz[64], wg[64];
-  load_fragment(a.w_z, col, half, wz);
-  load_fragment(a.w_g, col, half, wg);
-  const float bz = a.b_z ? a.b_z[col] : 0.f;
-  const float bg = a.b_g ? a.b_g[col] : 0.f;
-  f32x2 lnw_in = {1.f, 1.f}, lnb_in = {0.f, 0.f}, lnw_out = {1.f, 1.f}, lnb_out = {0.f, 0.f};
-  if (a.ln_in_w) lnw_in = *(const f32x2*)(a.ln_in_w + 2 * lane);
-  if (a.ln_in_b) lnb_in = *(const f32x2*)(a.ln_in_b + 2 * lane);
-  if (a.ln_out_w) lnw_out = *(const f32x2*)(a.ln_out_w + 2 * lane);
-  if (a.ln_out_b) lnb_out = *(const f32x2*)(a.ln_out_b + 2 * lane);
-  const int n = a.n;
-  const int64_t nb = a.np / 32;
-  const bool residual = a.accumulate != 0;
-
-  // Raw tile in registers: x (thread: channel tid/8 + 32u, columns
-  // 4*(tid%8)..+3) and z (thread: row tid/32 + 8u, channels 4*(tid%32)..+3).
-  f32x4 rx[4], rz[4];
-  auto fetch = [&](int tile) {
-    const int i = tile / tiles_j;
-    const int jb = tile % tiles_j;
-    const int j0 = jb * kRows;
-    const float* xb = a.x + ((int64_t)i * nb + jb) * kChannels * 32;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int idx = tid + 256 * u;
-      rx[u] = *(const f32x4*)(xb + (idx >> 3) * 32 + (idx & 7) * 4);
-      const int j = j0 + (idx >> 5);
-      rz[u] = j < n ? *(const f32x4*)(a.z + (int64_t)i * a.zs_i + (int64_t)j * a.zs_j +
-                                      (idx & 31) * 4)
-                    : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-  };
-
-  __builtin_amdgcn_s_waitcnt(0);
-  int tile = blockIdx.x;
-  fetch(tile);
-  for (; tile < ntiles; tile += gridDim.x) {
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int idx = tid + 256 * u;
-      const int c = idx >> 3;
-      const int j4 = (idx & 7) * 4;
-      xs[j4 + 0][c] = rx[u].x;
-      xs[j4 + 1][c] = rx[u].y;
-      xs[j4 + 2][c] = rx[u].z;
-      xs[j4 + 3][c] = rx[u].w;
-      *(f32x4*)&zs[idx >> 5][(idx & 31) * 4] = rz[u];
-    }
-    __syncthreads();
-    // Rows past n hold values K2 never wrote: they are normalised and
-    // multiplied like the others (rows are independent) and never stored.
-#pragma unroll
-    for (int rr = 0; rr < kRows / 4; ++rr) {
-      const int row = 8 * w + rr;
-      float d0, d1, rstd;
-      const f32x2 xv = *(const f32x2*)&xs[row][2 * lane];
-      ln_stats_c128(xv.x, xv.y, a.eps_out, d0, d1, rstd);
-      *(f32x2*)&xs[row][2 * lane] =
-          f32x2{d0 * rstd * lnw_out.x + lnb_out.x, d1 * rstd * lnw_out.y + lnb_out.y};
-      const f32x2 zv = *(const f32x2*)&zs[row][2 * lane];
-      ln_stats_c128(zv.x, zv.y, a.eps_in, d0, d1, rstd);
-      *(f32x2*)&zs[row][2 * lane] =
-          f32x2{d0 * rstd * lnw_in.x + lnb_in.x, d1 * rstd * lnw_in.y + lnb_in.y};
-    }
-    __syncthreads();
-    const int next = tile + (int)gridDim.x;
-    if (next < ntiles) fetch(next);
-    f32x16 acc_z = {}, acc_g = {};
-#pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      const f32x4 ax = *(const f32x4*)&xs[l32][64 * half + 4 * t];
-      const f32x4 az = *(const f32x4*)&zs[l32][64 * half + 4 * t];
-      acc_z = mfma32(ax.x, wz[4 * t + 0], acc_z);
-      acc_g = mfma32(az.x, wg[4 * t + 0], acc_g);
-      acc_z = mfma32(ax.y, wz[4 * t + 1], acc_z);
-      acc_g = mfma32(az.y, wg[4 * t + 1], acc_g);
-      acc_z = mfma32(ax.z, wz[4 * t + 2], acc_z);
-      acc_g = mfma32(az.z, wg[4 * t + 2], acc_g);
-      acc_z = mfma32(ax.w, wz[4 * t + 3], acc_z);
-      acc_g = mfma32(az.w, wg[4 * t + 3], acc_g);
-    }
-    const int i = tile / tiles_j;
-    const int j0 = (tile % tiles_j) * kRows;
-    float* dst = a.out + (int64_t)i * a.os_i + col;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int j = j0 + mfma_row(r, half);
-      if (j < n) {
-        float* d = dst + (int64_t)j * a.os_j;
-        // native: value = sigmoid(g) * x; z + value when adding
-        const float v = sigmoidf_(acc_g[r] + bg) * (acc_z[r] + bz);
-        *d = residual ? *d + v : v;
-      }
-    }
-    __syncthreads();
-  }
-}
-
-// ------------------------------------------------- finish, BF16 cores
-// The finish on v_mfma_f32_16x16x32_bf16 with exact three-plane splits of
-// both normalised inputs and both weights (six terms, FP32 rounding level).
+// The finish on v_mfma_f32_16x16x32_f16 with power-of-two scaled fp16 (hi,
+// lo) planes of both normalised inputs and both weights (three terms, FP32
+// rounding level).
 // The 16 x 16 shape lets a wave hold W_z and W_g planes for 16 output
 // channels in 96 VGPRs while the value (LN_out(x) W_z^T) and gate
 // (LN_in(z) W_g^T) results of one channel land in the same lane, so a
@@ -638,8 +393,7 @@ int grid_for(int64_t ntiles, int per_cu) {
 hipError_t launch_trimul(const TriMulArgs& a, hipStream_t stream) {
   if (a.n <= 0) return hipSuccess;
   if (a.np % kGemmTile || a.np < a.n) return hipErrorInvalidValue;
-  const int tiles_k = a.np / kRows;
-  const int64_t proj_tiles = (int64_t)a.n * tiles_k;
+  const int64_t proj_tiles = (int64_t)a.n * (a.np / kRows);
   const int tiles = a.np / kGemmTile;
   const uint64_t gemm_total = (uint64_t)kChannels * tiles * tiles;
   const int tiles_j = (a.n + kRows - 1) / kRows;
@@ -647,11 +401,7 @@ hipError_t launch_trimul(const TriMulArgs& a, hipStream_t stream) {
   if (proj_tiles > 0x7fffffff || gemm_total > 0x7fffffffu || fin_tiles > 0x7fffffff)
     return hipErrorInvalidValue;
   hipError_t e;
-  if (fp32_matrix_cores_selected()) {
-    hipLaunchKernelGGL(trimul_project_kernel, dim3(grid_for(proj_tiles, 1)),
-                       dim3(kProjWaves * 64), 0, stream, a, tiles_k, (int)proj_tiles);
-    e = hipGetLastError();
-  } else {
+  {
     GatedArgs g{};
     g.x = a.z;
     g.xs_r = a.outgoing ? a.zs_i : a.zs_j;
@@ -679,20 +429,12 @@ hipError_t launch_trimul(const TriMulArgs& a, hipStream_t stream) {
     e = launch_gated_split<kGatedTriMul>(g, stream);
   }
   if (e != hipSuccess) return e;
-  if (fp32_matrix_cores_selected())
-    hipLaunchKernelGGL(trimul_contract_kernel<false>, dim3((uint32_t)gemm_total), dim3(256), 0,
-                       stream, a.pa, a.pb, a.rowmax, a.x, a.n, a.np, tiles, (uint32_t)gemm_total);
-  else
-    hipLaunchKernelGGL(trimul_contract_kernel<true>, dim3((uint32_t)gemm_total), dim3(256), 0,
-                       stream, a.pa, a.pb, a.rowmax, a.x, a.n, a.np, tiles, (uint32_t)gemm_total);
+  hipLaunchKernelGGL(trimul_contract_kernel, dim3((uint32_t)gemm_total), dim3(256), 0, stream,
+                     a.pa, a.pb, a.rowmax, a.x, a.n, a.np, tiles, (uint32_t)gemm_total);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (fp32_matrix_cores_selected())
-    hipLaunchKernelGGL(trimul_finish_kernel, dim3(grid_for(fin_tiles, 2)), dim3(256), 0, stream,
-                       a, tiles_j, (int)fin_tiles);
-  else
-    hipLaunchKernelGGL(trimul_finish_split_kernel, dim3(grid_for(fin_tiles, 1)), dim3(512), 0,
-                       stream, a, tiles_j, (int)fin_tiles);
+  hipLaunchKernelGGL(trimul_finish_split_kernel, dim3(grid_for(fin_tiles, 1)), dim3(512), 0,
+                     stream, a, tiles_j, (int)fin_tiles);
   return hipGetLastError();
 }
 

@@ -171,8 +171,8 @@ int fpx_attn_core(float* q, float* k, float* v, float* bias, float* out, int bat
  *                                (fireprot_ck_attention.cpp:102-107)
  * A null or misaligned (16-byte) pointer returns 3 before any launch, as the
  * reference's vector_bias1000 entry does (fireprot_ck_attention.cpp:106-107);
- * the computation is FP32 on the FP32 matrix cores, asynchronous on the
- * caller's stream, with no allocation. */
+ * the computation is FP32 on the FP32 matrix cores (v_mfma_f32_32x32x2_f32),
+ * asynchronous on the caller's stream, with no allocation. */
 int ck_attention(float* q, float* k, float* v, float* bias, float* out, int batch, int n,
                  void* stream);
 int ck_attention_exact1536(float* q, float* k, float* v, float* bias, float* out, int batch,
@@ -259,8 +259,9 @@ int fpx_tri_mul(const float* z, int64_t z_stride0, int64_t z_stride1, const floa
                 int accumulate, float* out, int64_t out_stride0, int64_t out_stride1,
                 void* workspace, size_t workspace_bytes, void* stream);
 
-/* Bytes of workspace fpx_transition needs for rows_i x rows_j pair rows; 0
- * for unsupported sizes. */
+/* Bytes of workspace fpx_transition needs for rows_i x rows_j pair rows (the
+ * fused kernel's weight planes, about 0.8 MB, whatever the row count); 0 for
+ * unsupported sizes. */
 size_t fpx_transition_workspace_bytes(int64_t rows_i, int64_t rows_j, int c, int expansion);
 
 /* Pair transition: out = W_o (silu(W_a LN(x)) * (W_b LN(x))) per 128-channel
