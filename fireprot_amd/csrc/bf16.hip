@@ -390,10 +390,15 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
   const int crow = 16 * (w & 1) + (lane >> 2);
   const int cchunk = (lane & 3) ^ swz(lane >> 2);
   // K rows and V^T tiles are both 2 KB blocks per 32-key tile, rows of 64 bytes.
-  const __bf16* csrc = (w < 2 ? a.k : a.v) + bh * slice + crow * kHeadDim + 8 * cchunk;
+  // The copy source is a wave-uniform base (scalar registers) plus a lane
+  // offset; the tile loop's stage indices are constants (four tiles per
+  // iteration), so ring addresses fold into instruction offsets.
+  const __bf16* cbase = (w < 2 ? a.k : a.v) + bh * slice + 16 * (w & 1) * kHeadDim;
+  const uint32_t cvoff = (uint32_t)(((crow - 16 * (w & 1)) * kHeadDim + 8 * cchunk) * 2);
+  const uint32_t clds = lds_address(ring) + (uint32_t)((w >> 1) * kTileBytesB + (w & 1) * 1024);
   const int64_t ctile = kBk * kHeadDim;  // elements from tile t to t + 1
   auto dma = [&](int t, int stage) {
-    lds_dma16(csrc + t * ctile, ring + stage * kStageBytesB + (w >> 1) * kTileBytesB + (w & 1) * 1024);
+    lds_dma16_s(cvoff, cbase + t * ctile, clds + stage * kStageBytesB);
   };
   // Operand reads: lane (l32, half) reads chunks half and 2 + half of row l32.
   const uint32_t rd0 = l32 * 64 + 16 * (half ^ swz(l32));
@@ -595,19 +600,23 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
     // barrier; cur = logits of tile kt; bw = bias words of tile kt+1,
     // refilled with tile kt+3.  Tiles past the last are clamped (in range,
     // never used).
-    auto body = [&](int kt, f32x16& cur, f32x16& nxt, BiasWords& bw) {
-      nxt = scores(stage(kt + 1), kExact ? zero16 : widen(bw));
+    // Tile kt in ring stage s (s == kt % 4).
+    auto body4 = [&](int kt, int s, f32x16& cur, f32x16& nxt, BiasWords& bw) {
+      nxt = scores((s + 1) & 3, kExact ? zero16 : widen(bw));
       if (!kExact) bw = load_frag(clamp(kt + 3));
       bf16x8 p0, p1;
       softmax(cur, p0, p1);
-      pv(stage(kt), p0, p1);
+      pv(s, p0, p1);
       finish(nxt, kt + 1);
-      dma(clamp(kt + 3), stage(kt + 3));
+      dma(clamp(kt + 3), (s + 3) & 3);
       // Tile kt+2 has landed once at most this iteration's copy and (fast
       // path) its two bias-word loads are outstanding: vector memory loads
       // retire in issue order.
       wait_vmcnt<kExact ? 1 : 3>();
       __syncthreads();
+    };
+    auto body = [&](int kt, f32x16& cur, f32x16& nxt, BiasWords& bw) {
+      body4(kt, stage(kt), cur, nxt, bw);
     };
     auto tail = [&](const f32x16& cur, int kt) {
       bf16x8 p0, p1;
@@ -615,6 +624,13 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
       pv(stage(kt), p0, p1);
     };
     int kt = 0;
+    // four tiles per iteration: kt % 4 == 0, so every stage is a constant
+    for (; kt + 4 < nkt; kt += 4) {
+      body4(kt, 0, x_a, x_b, bw_o);
+      body4(kt + 1, 1, x_b, x_a, bw_e);
+      body4(kt + 2, 2, x_a, x_b, bw_o);
+      body4(kt + 3, 3, x_b, x_a, bw_e);
+    }
     for (; kt + 2 < nkt; kt += 2) {
       body(kt, x_a, x_b, bw_o);
       body(kt + 1, x_b, x_a, bw_e);
