@@ -299,29 +299,28 @@ def visited_key_tiles(n: int, valid: int | None, skip: bool) -> int:
 
 
 def split_executed(batch: int, n: int, ms: float, tiles: int | None = None,
-                   fp16_planes: bool = False, const_tiles: int = 0) -> dict:
+                   const_tiles: int = 0, per_head_scale: bool = True) -> dict:
     """16-bit matrix-core work the split attention kernel executes for its
     FP32-accurate products, per 32 x 32 (query x key) wave tile, counted in
     32x32x16 MFMAs of 32768 flop each (two K-halves per product term)
-    against 2 * 65536 algorithmic flop:
-      - caller-supplied q/k/v (strided layout): 6 bf16 terms of S^T and 3 of
-        O^T = 18 MFMAs;
-      - fp16 planes (the block's, and the staged strided operands): 3 fp16
-        terms of S^T and 3 of O^T = 12.
-    fp16 and bf16 MFMAs share one dense peak.  Query rows are padded to 128,
-    keys to 32.  ``tiles``: key tiles visited summed over the outer rows
-    (default: every tile of every row).  ``const_tiles``: the part of
-    ``tiles`` on constant-mask rows (padding rows, fl(s + m) = m for every
-    key), whose S^T the kernel leaves out: 6 MFMAs per wave tile (O^T only)."""
+    against 2 * 65536 algorithmic flop: 3 fp16 terms of S^T and 3 of O^T =
+    12 MFMAs.  fp16 and bf16 MFMAs share one dense peak.  Query rows are
+    padded to 128, keys to 32.  ``tiles``: key tiles visited summed over the
+    outer rows (default: every tile of every row).  ``const_tiles``: the part
+    of ``tiles`` on constant-mask rows (padding rows, fl(s + m) = m for every
+    key), whose S^T the kernel leaves out: 6 MFMAs per wave tile (O^T only).
+    ``per_head_scale``: the block's planes carry one power of two per head
+    and operand; the staged (strided) route's one per 32 x 32 tile of q and
+    k and per key tile of v^T."""
     np_ = -(-n // 128) * 128
     nkt = -(-n // 32)
     visited = batch * nkt if tiles is None else tiles
-    per_tile = 12 if fp16_planes else 18
-    executed = ((visited - const_tiles) * per_tile + const_tiles * 6) * 4 * (np_ // 32) * 32768
+    executed = ((visited - const_tiles) * 12 + const_tiles * 6) * 4 * (np_ // 32) * 32768
     executed_tflops = executed / (ms * 1e-3) / 1e12
-    unit = ("fp16 hi/lo planes scaled by powers of two (q, k per 32x32 tile; v^T per key "
-            "tile; p per tile), three terms per product" if fp16_planes
-            else "bf16 (exact 3-plane split of K and Q, 2-plane V and P)")
+    unit = ("fp16 hi/lo planes scaled by powers of two ("
+            + ("one per head for q, k and v^T" if per_head_scale
+               else "q, k per 32x32 tile; v^T per key tile")
+            + "; p per tile), three terms per product")
     return {
         "matrix_unit": unit,
         "visited_key_tile_frac": round(visited / (batch * nkt), 4),
@@ -454,7 +453,7 @@ def bench_openfold3(args) -> dict:
             "flop_per_launch": of3_flop, "flop_all_tiles": flop,
             "fp32_algorithmic_tflops_all_tiles": round(tflops, 3),
             "avg_launch_ms": round(ms, 4),
-            **split_executed(n, n, ms, of3_visited, fp16_planes=True),
+            **split_executed(n, n, ms, of3_visited, per_head_scale=False),
         },
         "cpu_baseline": None,
     }
@@ -1205,7 +1204,7 @@ def main() -> int:
     if split:
         # padding rows of a tail mask take the constant-mask kernel (no S^T)
         const_tiles = 0 if cfg.valid is None or cfg.valid >= n else (n - cfg.valid) * nkt
-        roofline.update(split_executed(n, n, stages["attend"], visited, fp16_planes=True,
+        roofline.update(split_executed(n, n, stages["attend"], visited,
                                        const_tiles=const_tiles))
     result = {
         "metric": METRIC,

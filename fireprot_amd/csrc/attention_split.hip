@@ -2,8 +2,9 @@
 //
 // Every FP32 operand of the two products is held as power-of-two scaled fp16
 // (hi, lo) planes: x 2^e = hi + lo with hi = fp16(x 2^e), lo = fp16(x 2^e -
-// hi), 22 significant bits, e chosen per tile so the tile's max |value| 2^e
-// lies in [2^14, 2^15).  A product then takes three terms (hi hi, hi lo,
+// hi), 22 significant bits, e chosen per block of values (a head, from a
+// bound on its values, or a 32 x 32 tile) so the block's max |value| 2^e stays
+// below 2^15.  A product then takes three terms (hi hi, hi lo,
 // lo hi) on v_mfma_f32_32x32x16_f16 with FP32 accumulation, an error per
 // product of about 2^-22, at the level of an FP32 dot product.  That
 // instruction does 8x the work of v_mfma_f32_32x32x2_f32 in half its cycles,

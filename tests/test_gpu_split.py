@@ -3,8 +3,9 @@
 Every product of the FP32 block, the triangle multiplication and the
 transition runs on the 16-bit matrix cores over operands scaled by a power of
 two per block and split as hi = fp16(x), lo = fp16(x - hi) (round to nearest
-even; x - hi is exact in FP32).  The device forms hi with v_cvt_pk_f16_f32 and
-lo with one v_fma_mix{lo,hi}_f16 per value.  ``fpx_split_planes`` runs that
+even; x - hi is exact in FP32).  The device forms hi with v_cvt_pk_f16_f32,
+the residual with one v_fma_mix_f32 per value and lo with one more
+v_cvt_pk_f16_f32 per pair.  ``fpx_split_planes`` runs that
 device split; the expected planes here come from numpy's float16 conversion
 of the value and of its exact float32 residual.
 """
