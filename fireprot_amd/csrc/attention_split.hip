@@ -116,7 +116,6 @@ __device__ __forceinline__ bool constant_mask_row(const AttnArgs& a, int b, floa
 // The constant-row kernel serves chunks of kConstRows consecutive outer
 // rows: the rows of a chunk that satisfy constant_mask_row with the m of
 // the chunk's first such row.  The exact launch leaves exactly those out.
-constexpr int kConstRows = 4;
 __device__ __forceinline__ bool const_chunk_member(const AttnArgs& a, int b) {
   float m;
   if (!constant_mask_row(a, b, m)) return false;
@@ -745,26 +744,11 @@ typedef float ConstScales[kTileFlagWords * 32];  // 2^-(e_t + kVShift) per tile 
 
 // One work item of the constant-row kernel; uniform per work-group, returns
 // at once (before any LDS access) when the item has no constant-mask rows.
-template <int LAYOUT>
-__device__ __forceinline__ void const_item(const AttnArgs& a, int nqt, int nkt, int nchunks,
-                                           uint32_t item, uint8_t* ring, ConstScales* Sv) {
-  constexpr bool kBlock = LAYOUT == kAttnBlock;
-  static_assert(LAYOUT == kAttnBlock || LAYOUT == kAttnStaged, "plane layouts only");
-  const int nhq = kHeads * nqt;
-  const int xcd = (int)(item % kXcds);
-  const int slot = (int)(item / kXcds);
-  const int hq0 = xcd * nhq / kXcds;
-  const int nh = (xcd + 1) * nhq / kXcds - hq0;
-  if (nh == 0 || slot >= nh * nchunks) return;
-  const int chunk = slot / nh;
-  const int hq = hq0 + slot % nh;
-  const int h = hq / nqt;
-  const int qt = hq % nqt;
-
-  // The chunk's rows served here, bit r for row chunk kConstRows + r
-  // (uniform across the work-group).
+// The rows of chunk `chunk` served by one item (bit r for row
+// kConstRows chunk + r) and their m; uniform across the work-group.
+__device__ __forceinline__ uint32_t const_chunk_rows(const AttnArgs& a, int chunk, float& m_row) {
   uint32_t live = 0u;
-  float m_row = 0.f;
+  m_row = 0.f;
   for (int r = 0; r < kConstRows; ++r) {
     const int b = chunk * kConstRows + r;
     float m = 0.f;
@@ -773,8 +757,30 @@ __device__ __forceinline__ void const_item(const AttnArgs& a, int nqt, int nkt, 
       live |= 1u << r;
     }
   }
-  live = __builtin_amdgcn_readfirstlane(live);
+  return live;
+}
+
+// One work item: the chunk's constant-mask rows for (head, query tile) hq.
+template <int LAYOUT, bool LOADED>
+__device__ __forceinline__ void const_item(const AttnArgs& a, int nqt, int nkt, int chunk, int hq,
+                                           uint8_t* ring, ConstScales* Sv) {
+  constexpr bool kBlock = LAYOUT == kAttnBlock;
+  static_assert(LAYOUT == kAttnBlock || LAYOUT == kAttnStaged, "plane layouts only");
+  const int h = hq / nqt;
+  const int qt = hq % nqt;
+
+  float m_row = 0.f;
+  const uint32_t live = __builtin_amdgcn_readfirstlane(const_chunk_rows(a, chunk, m_row));
   if (live == 0u) return;
+  // Chunks whose m has the block's precomputed weights (const_weights_kernel,
+  // formed once per (head, 32-query tile)) belong to the LOADED launch: its
+  // tile loop loads those weights in place of the bias fragments and runs
+  // no softmax.  The other launch serves every other chunk.
+  const bool has_weights = kBlock && a.const_m != nullptr &&
+                           __builtin_amdgcn_readfirstlane(a.const_m[0]) ==
+                               __builtin_bit_cast(uint32_t, m_row);
+  if (has_weights != LOADED) return;
+  constexpr bool loaded = LOADED;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -786,7 +792,14 @@ __device__ __forceinline__ void const_item(const AttnArgs& a, int nqt, int nkt, 
   const int qt32 = (j0 >> 5) + w;
   const int64_t nt = a.np >> 5;
   const int64_t frag = ((int64_t)h * nt + qt32) * nt * 1024;
-  const __amdgpu_buffer_rsrc_t rb = buffer(a.bias + frag, nt * 4096);
+  // Per key tile 4 KB at the same lane offsets: the bias fragment (x), or
+  // the loaded weights' planes (ph[0], ph[1], pl[0], pl[1] in x's four
+  // 16-byte parts).
+  const __amdgpu_buffer_rsrc_t rb =
+      loaded ? buffer(reinterpret_cast<const float*>(
+                          a.const_p + (((int64_t)h * nt + qt32) * nkt) * 4096),
+                      (int64_t)nkt * 4096)
+             : buffer(a.bias + frag, nt * 4096);
   const uint32_t ob = (uint32_t)lane * 16;
   const int64_t slice_bytes = (int64_t)a.np * 128;
 
@@ -833,6 +846,7 @@ __device__ __forceinline__ void const_item(const AttnArgs& a, int nqt, int nkt, 
   // Logits of tile t from its bias fragment: fl(m + bias), -inf past key n.
   const int full_tiles = a.n / kBk;
   auto finish = [&](f32x16& x, int t) {
+    if constexpr (loaded) return;
     if (t < full_tiles) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) x[r] = m_row + x[r];
@@ -856,6 +870,13 @@ __device__ __forceinline__ void const_item(const AttnArgs& a, int nqt, int nkt, 
   // P = exp2(x log2(e) - c_ref) w_ref (at most 2^8 by the lazy max), into
   // fp16 planes as P 2^kVShift.
   auto softmax = [&](const f32x16& x, bf16x8 (&ph)[2], bf16x8 (&pl)[2]) {
+    if constexpr (loaded) {
+      ph[0] = __builtin_bit_cast(bf16x8, f32x4{x[0], x[1], x[2], x[3]});
+      ph[1] = __builtin_bit_cast(bf16x8, f32x4{x[4], x[5], x[6], x[7]});
+      pl[0] = __builtin_bit_cast(bf16x8, f32x4{x[8], x[9], x[10], x[11]});
+      pl[1] = __builtin_bit_cast(bf16x8, f32x4{x[12], x[13], x[14], x[15]});
+      return;
+    }
     const float mt = xor32_max(max16(x));
     if (__any(mt > m_ref + kRescaleNat)) {
       const float m_new = __builtin_elementwise_maximum(m_ref, mt);
@@ -965,7 +986,7 @@ __device__ __forceinline__ void const_item(const AttnArgs& a, int nqt, int nkt, 
   }
   wait_vmcnt<0>();  // the clamped tail loads land before the LDS is released
 
-  const float l_tot = xor32_sum(l_run);
+  const float l_tot = loaded ? a.const_l[h * a.np + jq] : xor32_sum(l_run);
   if (jq < a.n) {
     for_const_rows([&](auto rc) {
       constexpr int r = decltype(rc)::value;
@@ -991,17 +1012,160 @@ __device__ __forceinline__ void const_item(const AttnArgs& a, int nqt, int nkt, 
   }
 }
 
+// The weights of the block's constant-mask rows, once for every such row
+// (const_item's loaded path).  Every row whose keys all carry the mask bias
+// m of the first constant-mask row has the logits x = fl(m + bias) for each
+// (head, query, key), whatever its outer row.  One work-group per (head,
+// 32-query tile), wave w on key tiles w, w + 4, ...: pass 1 each query's max
+// m_q over all keys; pass 2 the exact softmax's weights with the reference
+// at that max, P = exp2(x log2(e) - c) w, c = fl(m_q log2(e)),
+// w = 2^-(m_q log2(e) - c) (equal quantised logits get equal weights), their
+// sum l_q, and P 2^kVShift split into fp16 planes in the P.V operand order,
+// stored as the four 16-byte parts of a bias fragment.  With no
+// constant-mask row, const_m[0] becomes a NaN (no row's m matches it).
+// Work-group 0 also writes the two chunk lists of the constant-mask launches
+// (AttnArgs::const_m): the chunks whose rows have that m, and the others.
+__global__ __launch_bounds__(kThreads) void const_weights_kernel(AttnArgs a, int nkt) {
+  __shared__ int first;
+  __shared__ int counts[2];
+  __shared__ float red[kThreads / 64][32];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+  const int nt = a.np >> 5;
+  const int h = (int)blockIdx.x / nt;
+  const int qt32 = (int)blockIdx.x % nt;
+  if (tid == 0) first = a.batch;
+  __syncthreads();
+  for (int b = tid; b < a.batch; b += kThreads) {
+    float m;
+    if (constant_mask_row(a, b, m)) {
+      atomicMin(&first, b);
+      break;
+    }
+  }
+  __syncthreads();
+  const int b0 = first;
+  float m_c = 0.f;
+  const bool any = b0 < a.batch && constant_mask_row(a, b0, m_c);
+  const uint32_t m_bits = any ? __builtin_bit_cast(uint32_t, m_c) : 0x7fc00000u;
+  if (blockIdx.x == 0) {
+    if (tid < 2) counts[tid] = 0;
+    __syncthreads();
+    const int nchunks = (a.batch + kConstRows - 1) / kConstRows;
+    for (int c = tid; c < nchunks; c += kThreads) {
+      float m_row;
+      if (const_chunk_rows(a, c, m_row) == 0u) continue;
+      const int list = __builtin_bit_cast(uint32_t, m_row) == m_bits ? 0 : 1;
+      const int at = atomicAdd(&counts[list], 1);
+      a.const_m[kConstListWord + list * nchunks + at] = (uint32_t)c;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      a.const_m[0] = m_bits;
+      a.const_m[1] = (uint32_t)counts[0];
+      a.const_m[2] = (uint32_t)counts[1];
+    }
+  }
+  if (!any) return;
+
+  const __amdgpu_buffer_rsrc_t rb =
+      buffer(a.bias + ((int64_t)h * nt + qt32) * nt * 1024, (int64_t)nt * 4096);
+  const uint32_t ob = (uint32_t)lane * 16;
+  const int full_tiles = a.n / kBk;
+  auto logits = [&](int t) -> f32x16 {
+    const uint32_t so = (uint32_t)t * 4096;
+    f32x16 x = cat4(buffer_f4(rb, ob, so), buffer_f4(rb, ob + 1024, so),
+                    buffer_f4(rb, ob + 2048, so), buffer_f4(rb, ob + 3072, so));
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = t * kBk + 8 * (r >> 2) + 4 * half + (r & 3);
+      x[r] = (t < full_tiles || key < a.n) ? m_c + x[r] : -INFINITY;
+    }
+    return x;
+  };
+  float mx = -INFINITY;
+  for (int t = w; t < nkt; t += kThreads / 64) mx = __builtin_elementwise_maximum(mx, max16(logits(t)));
+  mx = xor32_max(mx);
+  if (half == 0) red[w][l32] = mx;
+  __syncthreads();
+  const float m_q = __builtin_elementwise_maximum(
+      __builtin_elementwise_maximum(red[0][l32], red[1][l32]),
+      __builtin_elementwise_maximum(red[2][l32], red[3][l32]));
+  __syncthreads();
+  const float c = m_q * kLog2e;
+  const float wr = exp2_fast(-__builtin_fmaf(m_q, kLog2e, -c));
+  const float f = wr * (float)(1 << kVShift);
+  uint8_t* const dst = a.const_p + (((int64_t)h * nt + qt32) * nkt) * 4096 + ob;
+  float ps = 0.f;
+  for (int t = w; t < nkt; t += kThreads / 64) {
+    const f32x16 x = logits(t);
+    bf16x8 ph[2], pl[2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      f32x8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = exp2_fast(__builtin_fmaf(x[8 * m + e], kLog2e, -c));
+      ps += ((v[0] + v[4]) + (v[1] + v[5])) + ((v[2] + v[6]) + (v[3] + v[7]));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] *= f;
+      split_f16(v, ph[m], pl[m]);
+    }
+    uint8_t* d = dst + (int64_t)t * 4096;
+    *(bf16x8*)(d) = ph[0];
+    *(bf16x8*)(d + 1024) = ph[1];
+    *(bf16x8*)(d + 2048) = pl[0];
+    *(bf16x8*)(d + 3072) = pl[1];
+  }
+  ps = xor32_sum(ps);
+  if (half == 0) red[w][l32] = ps;
+  __syncthreads();
+  if (tid < 32)
+    a.const_l[h * a.np + qt32 * 32 + tid] =
+        ((red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid])) * wr;
+}
+
 // A work-group per item: the few items with work spread over the whole
 // chip as the empty ones leave (a grid that walks the items would give some
 // work-groups one item more than others).  The loop serves any grid.
-template <int LAYOUT>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// LOADED: the chunks with precomputed weights (no softmax registers, three
+// work-groups per CU, as many as the LDS holds); the other launch keeps two.
+template <int LAYOUT, bool LOADED>
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(2, 2)))
 void attention_const_kernel(AttnArgs a, int nqt, int nkt, int nchunks, uint32_t items) {
   __shared__ __attribute__((aligned(16))) uint8_t ring[kConstStages * kStageBytesC];
   __shared__ ConstScales Sv[kConstRows];
+  // XCD x serves the (head, query tile) pairs [x H nqt / 8, (x + 1) H nqt / 8)
+  // of every chunk, chunk-major.
+  const int nhq = kHeads * nqt;
+  const int xcd = (int)(blockIdx.x % kXcds);
+  const int hq0 = xcd * nhq / kXcds;
+  const int nh = (xcd + 1) * nhq / kXcds - hq0;
+  if (nh == 0) return;
+  if (LAYOUT == kAttnBlock && a.const_m != nullptr) {
+    // The block's chunk lists (const_weights_kernel): a persistent grid, a
+    // multiple of kXcds work-groups, walks this launch's list.
+    const int count = (int)__builtin_amdgcn_readfirstlane(a.const_m[LOADED ? 1 : 2]);
+    const uint32_t* list = a.const_m + kConstListWord + (LOADED ? 0 : nchunks);
+    const int stride = (int)(gridDim.x / kXcds);
+    for (int slot = (int)(blockIdx.x / kXcds); slot < nh * count; slot += stride) {
+      const int chunk = (int)__builtin_amdgcn_readfirstlane(list[slot / nh]);
+      const_item<LAYOUT, LOADED>(a, nqt, nkt, chunk, hq0 + slot % nh, ring, Sv);
+      __syncthreads();
+    }
+    return;
+  }
+  // Every (chunk, pair) item, one work-group each (the items without
+  // constant-mask rows leave at once).
   for (uint32_t item = blockIdx.x; item < items; item += gridDim.x) {
-    const_item<LAYOUT>(a, nqt, nkt, nchunks, item, ring, Sv);
-    __syncthreads();
+    const int slot = (int)(item / kXcds);
+    if (slot < nh * nchunks) {
+      const_item<LAYOUT, LOADED>(a, nqt, nkt, slot / nh, hq0 + slot % nh, ring, Sv);
+      __syncthreads();
+    }
   }
 }
 
@@ -1115,8 +1279,25 @@ hipError_t launch_attention_split(int layout, const AttnArgs& a, hipStream_t str
     hipLaunchKernelGGL((attention_split_kernel<kAttnBlock, true>), dim3(exact_grid),
                        dim3(kThreads), mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total, ppg);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-    hipLaunchKernelGGL((attention_const_kernel<kAttnBlock>), dim3(const_grid), dim3(kThreads), 0,
-                       stream, a, nqt, nkt, nchunks, (uint32_t)const_items);
+    if (a.const_m != nullptr) {
+      // the shared weights and the chunk lists, then both constant-mask
+      // launches on persistent grids (two work-groups per CU) over them
+      if (a.const_l == nullptr || a.const_p == nullptr) return hipErrorInvalidValue;
+      hipLaunchKernelGGL(const_weights_kernel, dim3((uint32_t)(kHeads * (a.np >> 5))),
+                         dim3(kThreads), 0, stream, a, nkt);
+      if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+      int cap = device_cu_count() * 2;
+      cap -= cap % kXcds;
+      const uint32_t grid = (uint32_t)std::max(cap, kXcds);
+      hipLaunchKernelGGL((attention_const_kernel<kAttnBlock, true>), dim3(grid), dim3(kThreads), 0,
+                         stream, a, nqt, nkt, nchunks, (uint32_t)const_items);
+      if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+      hipLaunchKernelGGL((attention_const_kernel<kAttnBlock, false>), dim3(grid), dim3(kThreads), 0,
+                         stream, a, nqt, nkt, nchunks, (uint32_t)const_items);
+    } else {
+      hipLaunchKernelGGL((attention_const_kernel<kAttnBlock, false>), dim3(const_grid),
+                         dim3(kThreads), 0, stream, a, nqt, nkt, nchunks, (uint32_t)const_items);
+    }
   } else if (layout == kAttnStaged) {
     hipLaunchKernelGGL((attention_split_kernel<kAttnStaged, false>), dim3((uint32_t)total),
                        dim3(kThreads), mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total, ppg);
@@ -1124,7 +1305,7 @@ hipError_t launch_attention_split(int layout, const AttnArgs& a, hipStream_t str
     hipLaunchKernelGGL((attention_split_kernel<kAttnStaged, true>), dim3(exact_grid),
                        dim3(kThreads), mask_row_bytes, stream, a, nqt, nkt, (uint32_t)total, ppg);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-    hipLaunchKernelGGL((attention_const_kernel<kAttnStaged>), dim3(const_grid), dim3(kThreads), 0,
+    hipLaunchKernelGGL((attention_const_kernel<kAttnStaged, false>), dim3(const_grid), dim3(kThreads), 0,
                        stream, a, nqt, nkt, nchunks, (uint32_t)const_items);
   } else {
     return hipErrorInvalidValue;

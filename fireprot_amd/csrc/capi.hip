@@ -36,11 +36,15 @@ size_t elem_bytes(int dtype) { return dtype == FPX_BF16 ? 2 : 4; }
 //   log2(e); BF16: bias_frag_index_bf16, once); mbias [n][np] float;
 //   tile flags [n][kTileFlagParts * kTileFlagWords] uint32, then the
 //   kMagnitudeWords words of the magnitude record; scales [3][n][4][np / 32]
-//   float (the plane layout's per-tile inverse scales of q, k and v^T).
+//   float (the plane layout's per-tile inverse scales of q, k and v^T); FP32
+//   only: the constant-mask rows' weights and chunk lists (AttnArgs::const_m,
+//   const_l, const_p: kConstListWord words and two lists of
+//   ceil(n / kConstRows) chunk indices, l [4][np] float, the planes
+//   [4][np / 32][ceil(n / 32)] x 4 KB).
 // FP32 blocks hold q, k and v^T in the fp16 plane layout (ProjArgs), in the
 // same bytes as FP32 values.
 struct BlockWorkspace {
-  size_t qh, kh, vt, gs, og, bias, mbias, flags, scales, total;
+  size_t qh, kh, vt, gs, og, bias, mbias, flags, scales, cw_m, cw_l, cw_p, total;
 };
 
 BlockWorkspace block_workspace(int n, int dtype) {
@@ -64,7 +68,17 @@ BlockWorkspace block_workspace(int n, int dtype) {
   w.mbias = w.bias + bias;
   w.flags = w.mbias + mb;
   w.scales = w.flags + fl;
-  w.total = w.scales + seg((size_t)3 * n * fpx::kHeads * (np / 32) * sizeof(float));
+  const size_t cw_m = w.scales + seg((size_t)3 * n * fpx::kHeads * (np / 32) * sizeof(float));
+  w.cw_m = cw_m;
+  if (dtype == FPX_F32) {
+    const size_t nkt = (size_t)(n + 31) / 32;
+    const size_t chunks = (size_t)(n + fpx::kConstRows - 1) / fpx::kConstRows;
+    w.cw_l = cw_m + seg((fpx::kConstListWord + 2 * chunks) * sizeof(uint32_t));
+    w.cw_p = w.cw_l + seg((size_t)fpx::kHeads * np * sizeof(float));
+    w.total = w.cw_p + (size_t)fpx::kHeads * (np / 32) * nkt * 4096;
+  } else {
+    w.cw_l = w.cw_p = w.total = cw_m;
+  }
   return w;
 }
 
@@ -81,6 +95,9 @@ struct BlockPointers {
   uint32_t* flags;
   uint32_t* magnitudes;
   float* scales;
+  uint32_t* const_m;  // FP32 only (else null), as const_l and const_p
+  float* const_l;
+  uint8_t* const_p;
   int np;
 };
 
@@ -98,6 +115,11 @@ BlockPointers block_pointers(void* workspace, int n, int dtype) {
   p.flags = reinterpret_cast<uint32_t*>(base + ws.flags);
   p.magnitudes = p.flags + (size_t)n * fpx::kTileFlagParts * fpx::kTileFlagWords;
   p.scales = reinterpret_cast<float*>(base + ws.scales);
+  if (dtype == FPX_F32) {
+    p.const_m = reinterpret_cast<uint32_t*>(base + ws.cw_m);
+    p.const_l = reinterpret_cast<float*>(base + ws.cw_l);
+    p.const_p = reinterpret_cast<uint8_t*>(base + ws.cw_p);
+  }
   p.np = (int)round_up(n, kQueryTile);
   return p;
 }
@@ -418,6 +440,9 @@ int fpx_tri_attn_attend(int dtype, int n, void* workspace, size_t workspace_byte
   a.tile_flags = w.flags;
   a.magnitudes = w.magnitudes;
   a.scales = w.scales;
+  a.const_m = w.const_m;
+  a.const_l = w.const_l;
+  a.const_p = w.const_p;
   a.batch = n;
   a.n = n;
   a.np = w.np;

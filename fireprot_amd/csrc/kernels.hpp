@@ -84,6 +84,11 @@ constexpr int kRelativeBiasWord = 5;
 // first masked tile (the keys unmasked on every row with an unmasked key).
 constexpr float kRelOffset = 8.0f;
 
+// The constant-mask attention serves chunks of kConstRows consecutive outer
+// rows; kConstListWord: the first chunk-list word of AttnArgs::const_m.
+constexpr int kConstRows = 4;
+constexpr int kConstListWord = 64;
+
 struct AttnArgs {
   const float* q;
   const float* k;
@@ -99,6 +104,18 @@ struct AttnArgs {
   const uint32_t* tile_flags;
   const uint32_t* magnitudes;  // kAttnBlock: nullable; enables the trailing-tile skip
   const float* scales;  // kAttnBlock, kAttnStaged: the planes' inverse scales
+  // kAttnBlock, nullable: the constant-mask rows' shared weights and work
+  // lists, written by the split launch itself (const_weights_kernel):
+  // const_m[0] the mask bias m the weights serve (float bits; a NaN when no
+  // row has a constant mask), const_m[1] and const_m[2] the numbers of
+  // kConstRows-row chunks with constant-mask rows of that m and of another
+  // m, their chunk indices from word kConstListWord (the first list) and
+  // kConstListWord + ceil(batch / kConstRows) (the second);
+  // const_l[4][np] each query's weight sum, const_p the weights' fp16 planes,
+  // 4 KB per (head, 32-query tile, key tile).  Each may be null only with all.
+  uint32_t* const_m;
+  float* const_l;
+  uint8_t* const_p;
   int64_t qs[3];  // kAttnStrided: (batch, head, row) element strides
   int64_t ks[3];
   int64_t vs[3];

@@ -49,11 +49,17 @@ def test_abi_version_and_workspace_sizes(lib):
             copies = 2 if dtype == 0 else 1  # FP32: unscaled and log2(e)-scaled bias
             # q, k, v^T; gate (rows padded to np); gated output; bias; mask bias;
             # tile flags (4 parts of 4 words per row) plus the 6-word magnitude record;
-            # the q, k and v^T tiles' inverse scales of the plane layout
+            # the q, k and v^T tiles' inverse scales of the plane layout; FP32:
+            # the constant-mask rows' weights (64 words and two lists of
+            # ceil(n / 4) chunk indices, the weight sums [4][np], 4 KB of
+            # planes per (head, 32-query tile, 32-key tile))
             expected = (3 * seg(n * 4 * np_ * 32 * e) + seg(n * np_ * 128 * e)
                         + seg(n * n * 128 * e)
                         + seg(4 * np_ * np_ * e * copies) + seg(n * np_ * 4)
                         + seg((n * 16 + 6) * 4) + seg(3 * n * 4 * (np_ // 32) * 4))
+            if dtype == 0:
+                expected += (seg((64 + 2 * -(-n // 4)) * 4) + seg(4 * np_ * 4)
+                             + 4 * (np_ // 32) * (-(-n // 32)) * 4096)
             assert lib.fpx_tri_attn_workspace_bytes(n, 128, 4, 32, dtype) == expected
     for bad in ((0, 128, 4, 32, 0), (4097, 128, 4, 32, 0), (64, 64, 4, 32, 0),
                 (64, 128, 8, 32, 0), (64, 128, 4, 16, 0), (64, 128, 4, 32, 7)):
