@@ -5,7 +5,7 @@ The C ABI entries never allocate: the caller passes a workspace of at least
 the entry's ``*_workspace_bytes(...)``.  The registered candidates are called
 per module call, so they keep one uint8 buffer per (device, stream) and grow
 it when a call needs more, instead of asking the caching allocator for a
-multi-GB block on every call (6.1 GB for a block at N=1536).
+multi-GB block on every call (6.2 GB for a block at N=1536).
 
 Keying by stream keeps two streams of one device from sharing a buffer
 (their calls may overlap); calls on one stream are ordered, so they can
