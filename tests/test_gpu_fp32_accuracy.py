@@ -204,6 +204,52 @@ def test_padding_rows_with_and_without_the_constant_mask_shortcut(qk_scale, inf)
                        ending, rows, valid)
 
 
+def test_padding_rows_with_two_mask_values():
+    """Two kinds of padding rows in one block: rows 110-134 carry the mask
+    bias -1e9 on every key (mask 0), rows 135-159 carry -5e8 (mask 0.5).
+    The first kind has the shared weights formed once (the first constant
+    row's m); chunks of four rows whose first constant row carries -5e8 take
+    the per-chunk softmax; row 135, the one -5e8 row in a chunk that starts
+    with -1e9 rows, takes the exact path.  W_q is scaled by 1/4 so that
+    32 max|q| max|k| stays below half the float32 spacing of both mask
+    biases (32 and 16).  The ending node gets the transposed mask, so its
+    rows in z's transposed frame have the same kinds.  Every row meets the
+    FP32 bar against float64 (float32-rounded logits on the padding rows)."""
+    n, valid = 160, 110
+    z = workloads.make_pair(n)
+    w = workloads.make_weights(bias_scale=4.0)
+    w["w_q"] = w["w_q"] * 0.25
+    mask = torch.zeros(n, n)
+    mask[:valid, :valid] = 1.0
+    mask[135:, :] = 0.5
+    rows = torch.arange(n)
+    # The workspace ends with the constant-mask segment: 64 words and two
+    # chunk lists (padded to 256 bytes), the weight sums [4][np], and 4 KB of
+    # weight planes per (head, 32-query tile, 32-key tile).  Words 1 and 2
+    # count the four-row chunks of each list: chunks 27-33 start with a -1e9
+    # row, chunks 34-39 with a -5e8 row.
+    np_, nkt, chunks = 256, 5, 40
+    seg = lambda b: -(-b // 256) * 256  # noqa: E731
+    words_at = (hip_block.workspace_bytes(n) - 4 * (np_ // 32) * nkt * 4096 - seg(4 * np_ * 4)
+                - seg((64 + 2 * chunks) * 4))
+    for ending in (False, True):
+        m = mask.t().contiguous() if ending else mask
+        print(f"case two padding mask values ending={ending}", flush=True)
+        ws = torch.empty(hip_block.workspace_bytes(n), dtype=torch.uint8, device="cuda")
+        with torch.inference_mode():
+            out = hip_block.triangle_attention_block(z.cuda(), m.cuda(), hip_weights(w),
+                                                     ending=ending, workspace=ws)
+            torch.cuda.synchronize()
+        x_frame = out.transpose(0, 1) if ending else out
+        actual = x_frame.cpu()
+        words = ws[words_at:words_at + 12].cpu().view(torch.int32)
+        assert words[1].item() == 7 and words[2].item() == 6, words[:3].tolist()
+        assert words[0].item() == torch.tensor([-1e9]).view(torch.int32).item()
+        del out, x_frame, ws
+        torch.cuda.empty_cache()
+        _check_regions(f"two mask values ending={ending}", actual, z, m, w, ending, rows, valid)
+
+
 def test_relative_reference_moves_for_keys_past_the_common_prefix():
     """The fast softmax starts from the relative reference C_q (the query's
     largest bias over the keys every row leaves unmasked).  Rows whose
