@@ -170,3 +170,35 @@ def test_cached_workspace_is_reused_across_calls(protenix_cls):
     assert ws_cache.get(z.device, 1, purpose="block").data_ptr() == buf.data_ptr()
     assert torch.equal(first, second)
     ws_cache.release()
+
+
+def test_protenix_layout_bf16_module_both_nodes(protenix_cls):
+    """A bfloat16 model (module weights, z and mask in bfloat16) through the
+    installed hook takes the BF16 block candidate; both nodes at N = 160 with
+    a 20-residue padding tail stay within 2e-2 (of the largest value) of the
+    native path run on bfloat16 tensors, the BF16 bar of
+    tests/test_gpu_bf16.py."""
+    from oracle import triangle_attention as oracle
+
+    n, valid = 160, 140
+    z = workloads.make_pair(n)
+    mask = workloads.make_mask(n, valid)
+    w = workloads.make_weights()
+    zc = z.to(torch.bfloat16).cuda()
+    mc = mask.to(torch.bfloat16).cuda()
+    registry.clear_runtime_state()
+    ws_cache.release()
+    for ending in (False, True):
+        print(f"case protenix bf16 n={n} ending={ending}", flush=True)
+        module = protenix_cls(w, starting=not ending).cuda().eval().to(torch.bfloat16)
+        with torch.inference_mode():
+            dz = module(zc, mc)
+            torch.cuda.synchronize()
+        assert dz.dtype == torch.bfloat16
+        native = oracle.block_bf16(z, mask, oracle.BlockParams(**w), ending=ending)
+        rel = ((dz.float().cpu() - native.float()).abs().max() / native.float().abs().max()).item()
+        print(f"protenix bf16 ending={ending}: rel vs native-bf16 {rel:.2e}", flush=True)
+        assert rel <= 2e-2
+    assert registry.count(ta.BLOCK_OPERATION, ta.BLOCK_BF16_IMPLEMENTATION) == 2
+    assert registry.count(ta.BLOCK_OPERATION, ta.BLOCK_IMPLEMENTATION) == 0
+    ws_cache.release()
