@@ -45,6 +45,13 @@
 //     spacing of 64).
 // K is staged one tile ahead of V, and the S^T MFMAs of tile t + 1 are issued
 // before the softmax of tile t.
+//
+// Rows whose keys all carry one mask bias m, small enough products given
+// (constant_mask_row), have the same weights fl-softmax(m + bias) on every
+// such row: attention_const_kernel runs only O^T for them, four rows per
+// work item.  For the block, const_weights_kernel first forms those weights
+// once for the m of the first such row, and lists the four-row chunks of
+// that m and of any other m; the constant-mask launches walk those lists.
 #include "attn_common.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
