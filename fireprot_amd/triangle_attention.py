@@ -179,25 +179,47 @@ def dispatch_triangle_attention(*, module: Any, q: Any, k: Any, v: Any, biases: 
 _packed: "weakref.WeakKeyDictionary[Any, tuple[tuple, BlockWeights]]" = weakref.WeakKeyDictionary()
 
 
-def _parameter_key(module: Any) -> tuple | None:
+def _layers(module: Any) -> tuple[tuple, tuple]:
+    """The layers whose weights the block packs, in packing order, and the
+    other sub-layers whose hooks would run in the module's own forward
+    (Protenix: patches/protenix/0005-*.patch:32-45; AtlasFold:
+    python/fireprot/adapters/atlasfold/runtime.py:224-233)."""
+    if hasattr(module, "mha"):
+        mha = module.mha
+        return ((module.layer_norm, module.linear, mha.linear_q, mha.linear_k, mha.linear_v,
+                 mha.linear_g, mha.linear_o), (mha,))
+    if hasattr(module, "linear_qkv"):
+        return ((module.layernorm, module.linear_qkv, module.linear_bias, module.linear_g,
+                 module.linear_out), ())
+    raise TypeError(f"unrecognised triangle-attention module {type(module).__name__}")
+
+
+def _tensor(owner: Any, name: str) -> Any:
+    """``owner.<name>`` or None; a registered parameter is read from the
+    module's parameter table (``nn.Module`` attribute lookup would go through
+    its Python ``__getattr__``)."""
+    params = getattr(owner, "__dict__", {}).get("_parameters")
+    if params is not None and name in params:
+        return params[name]
+    return getattr(owner, name, None)
+
+
+def _parameter_key(module: Any, layers: tuple | None = None) -> tuple | None:
     """Identity, storage and version of every tensor _weights_of reads, or
     None when one of them is an inference tensor (created under
     ``torch.inference_mode``: such tensors keep no version counter, so an
     in-place change could not be seen and the weights are packed afresh)."""
-    owners = ((module.layer_norm, module.linear, module.mha.linear_q, module.mha.linear_k,
-               module.mha.linear_v, module.mha.linear_g, module.mha.linear_o)
-              if hasattr(module, "mha") else
-              (module.layernorm, module.linear_qkv, module.linear_bias, module.linear_g,
-               module.linear_out))
     key = []
-    for owner in owners:
+    for owner in (_layers(module)[0] if layers is None else layers):
         for name in ("weight", "bias"):
-            t = getattr(owner, name, None)
-            if t is not None and t.is_inference():
+            t = _tensor(owner, name)
+            if t is None:
+                key.append(None)
+                continue
+            if t.is_inference():
                 return None
-            key.append(None if t is None else
-                       (id(t), t.data_ptr(), t._version, t.dtype, str(t.device)))
-    key.append((float(getattr(module, "inf", 1e9)),))
+            key.append((id(t), t.data_ptr(), t._version, t.dtype, t.device))
+    key.append(float(getattr(module, "inf", 1e9)))
     return tuple(key)
 
 
@@ -215,15 +237,15 @@ def _pack_dtype(z: Any) -> Any:
     return None
 
 
-def _weights_of(module: Any, dtype: Any = None) -> BlockWeights:
+def _weights_of(module: Any, dtype: Any = None, layers: tuple | None = None) -> BlockWeights:
     """The module's weights packed for the block (w_qkvg concatenated) in
     ``dtype`` (default: the weights' own), cached per module while its
     parameters are unchanged."""
-    if not (hasattr(module, "mha") or hasattr(module, "linear_qkv")):
-        raise TypeError(f"unrecognised triangle-attention module {type(module).__name__}")
+    if layers is None:
+        layers = _layers(module)[0]
     try:
-        key = _parameter_key(module)
-        key = None if key is None else key + ((str(dtype),),)
+        key = _parameter_key(module, layers)
+        key = None if key is None else key + (str(dtype),)
         hit = None if key is None else _packed.get(module)
     except TypeError:  # not weak-referenceable: no cache
         key, hit = None, None
@@ -239,60 +261,75 @@ def _weights_of(module: Any, dtype: Any = None) -> BlockWeights:
     return weights
 
 
-def _has_hooks(module: Any) -> bool:
+def _precision(layer: Any) -> Any:
+    """The layer's ``precision`` override, or None (read from the instance
+    dictionary first: a missing attribute costs ``nn.Module.__getattr__`` an
+    exception)."""
+    own = getattr(layer, "__dict__", {})
+    return own["precision"] if "precision" in own else getattr(type(layer), "precision", None)
+
+
+def _has_hooks(module: Any, layers: tuple[tuple, tuple] | None = None) -> bool:
     """Forward hooks on the module or the layers the block reads, or a
     ``precision`` override on them: the fused block would skip them
     (atlasfold/runtime.py:224-233 rejects the same)."""
     import torch
 
-    layers = ((module.layer_norm, module.linear, module.mha, module.mha.linear_q,
-               module.mha.linear_k, module.mha.linear_v, module.mha.linear_g, module.mha.linear_o)
-              if hasattr(module, "mha") else
-              (getattr(module, "layernorm", None), getattr(module, "linear_qkv", None),
-               getattr(module, "linear_bias", None), getattr(module, "linear_g", None),
-               getattr(module, "linear_out", None)))
-    for layer in (module, *layers):
+    packed, others = _layers(module) if layers is None else layers
+    for layer in (module, *others, *packed):
         if isinstance(layer, torch.nn.Module) and (layer._forward_hooks or
                                                    layer._forward_pre_hooks):
             return True
-        if layer is not module and getattr(layer, "precision", None) is not None:
+        if layer is not module and _precision(layer) is not None:
             return True
     return False
 
 
-def block_eligible(module: Any, z: Any, mask: Any) -> tuple[bool, str]:
-    """Check the tensor/module contract that the signature cannot carry."""
+def _block_check(module: Any, z: Any, mask: Any) -> tuple[bool, str, BlockWeights | None]:
+    """block_eligible's verdict and, when it passes, the packed weights."""
     import torch
 
     if not getattr(z, "is_cuda", False) or z.dtype not in (torch.float32, torch.bfloat16):
-        return False, "z is not a float32 or bfloat16 HIP tensor"
+        return False, "z is not a float32 or bfloat16 HIP tensor", None
     if z.dim() != 3 or z.shape[0] != z.shape[1] or z.shape[2] != 128 or z.stride(2) != 1:
-        return False, "z must be [N, N, 128] with unit channel stride"
+        return False, "z must be [N, N, 128] with unit channel stride", None
     if not 1 <= z.shape[0] <= MAX_N:
-        return False, f"N must lie in 1..{MAX_N}"
+        return False, f"N must lie in 1..{MAX_N}", None
     align = 16 // z.element_size()
     if z.stride(0) % align or z.stride(1) % align or z.data_ptr() % 16:
-        return False, "z rows are not 16-byte aligned"
+        return False, "z rows are not 16-byte aligned", None
     if mask is not None and (tuple(mask.shape) != tuple(z.shape[:2]) or mask.device != z.device):
-        return False, "mask must be [N, N] on z's device"
-    heads = getattr(getattr(module, "mha", module), "no_heads", getattr(module, "num_heads", None))
-    dim = getattr(getattr(module, "mha", module), "c_hidden",
-                  getattr(module, "channel_hidden", None))
+        return False, "mask must be [N, N] on z's device", None
+    owner = getattr(module, "mha", module)
+    heads = getattr(owner, "no_heads", None)
+    if heads is None:
+        heads = getattr(module, "num_heads", None)
+    dim = getattr(owner, "c_hidden", None)
+    if dim is None:
+        dim = getattr(module, "channel_hidden", None)
     if heads != HEADS or dim != HEAD_DIM:
-        return False, "module must have 4 heads of dimension 32"
+        return False, "module must have 4 heads of dimension 32", None
     scale = getattr(module, "scale", None)
     if scale is not None and abs(float(scale) * math.sqrt(HEAD_DIM) - 1.0) > 1e-6:
-        return False, "module q scale is not 1/sqrt(32)"
+        return False, "module q scale is not 1/sqrt(32)", None
     try:
-        if _has_hooks(module):
-            return False, "module or one of its layers carries forward hooks or a precision override"
-        weights = _weights_of(module, _pack_dtype(z))
+        layers = _layers(module)
+        if _has_hooks(module, layers):
+            return (False, "module or one of its layers carries forward hooks or a precision "
+                    "override", None)
+        weights = _weights_of(module, _pack_dtype(z), layers[0])
     except (AttributeError, TypeError, ValueError, RuntimeError) as error:
-        return False, f"module layout: {error}"
+        return False, f"module layout: {error}", None
     if any(t is not None and (t.device != z.device or t.dtype != z.dtype)
            for t in weights.tensors()):
-        return False, "weights do not have z's dtype and device"
-    return True, ""
+        return False, "weights do not have z's dtype and device", None
+    return True, "", weights
+
+
+def block_eligible(module: Any, z: Any, mask: Any) -> tuple[bool, str]:
+    """Check the tensor/module contract that the signature cannot carry."""
+    eligible, reason, _ = _block_check(module, z, mask)
+    return eligible, reason
 
 
 def _supports_block(signature: OperationSignature, *,
@@ -316,24 +353,36 @@ def _supports_block(signature: OperationSignature, *,
     return True
 
 
-def _block(*, module: Any, z: Any, mask: Any, ending: bool, native: Any) -> Any:
+def _run_block(z: Any, mask: Any, weights: BlockWeights, ending: bool) -> Any:
     """One block call with the workspace cached for z's device and stream."""
-    del native
     ws = ws_cache.get(z.device, workspace_bytes(z.shape[0], z.dtype), purpose="block")
-    weights = _weights_of(module, _pack_dtype(z)).to(z.device)
     return triangle_attention_block(z, mask, weights, ending=ending, workspace=ws)
+
+
+def _block(*, module: Any, z: Any, mask: Any, ending: bool, native: Any) -> Any:
+    """The registered implementation: the module's packed weights, then one
+    block call (the weights' device and dtype are checked again there)."""
+    del native
+    return _run_block(z, mask, _weights_of(module, _pack_dtype(z)), ending)
 
 
 def dispatch_triangle_attention_block(*, module: Any, z: Any, mask: Any, ending: bool,
                                       native: Callable[..., Any]) -> Any:
-    """Module-level drop-in ``(z, mask) -> dz`` with native fallback."""
-    eligible, reason = block_eligible(module, z, mask)
+    """Module-level drop-in ``(z, mask) -> dz`` with native fallback.
+
+    The registry selects as ``registry.dispatch`` does; when it selects one of
+    this module's block candidates, the weights the eligibility check packed
+    are used directly (one walk over the module per call)."""
+    eligible, reason, weights = _block_check(module, z, mask)
     signature = signature_from_tensor(
         BLOCK_OPERATION, z, architecture=_architecture(z),
         mode=_mode(module, (z,)), mask="none" if mask is None else "pair-mask", inplace=False,
         attributes={"eligible": eligible, "reason": reason, "ending": bool(ending)})
-    return registry.dispatch(signature, native, module=module, z=z, mask=mask, ending=ending,
-                             native=native)
+    chosen = registry.resolve(signature).implementation
+    if chosen is not None and chosen.function is _block and weights is not None:
+        return _run_block(z, mask, weights, ending)
+    function = chosen.function if chosen is not None else native
+    return function(module=module, z=z, mask=mask, ending=ending, native=native)
 
 
 registry.register(operation=OPERATION, name=IMPLEMENTATION, function=attention,

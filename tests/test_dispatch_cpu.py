@@ -111,6 +111,35 @@ def test_block_dispatch_falls_back_on_cpu_and_reports_reason():
     assert ta.block_eligible(m, z, None) == (False, "z is not a float32 or bfloat16 HIP tensor")
 
 
+def test_block_dispatch_calls_a_preferred_candidate_with_the_hook_arguments():
+    """A candidate registered above the HIP block gets the call with the
+    reference hook's keyword arguments (the packed-weights shortcut applies
+    only when the registry selects this package's block)."""
+    m = _protenix_like()
+    z = torch.randn(8, 8, 128)
+    seen = {}
+
+    def override(**kwargs):
+        seen.update(kwargs)
+        return "override"
+
+    registry.register(operation=ta.BLOCK_OPERATION, name="user-override", function=override,
+                      supports=lambda signature: True, priority=99, version="1")
+    try:
+        registry.clear_runtime_state()
+        with torch.inference_mode():
+            native = lambda **_: "native"  # noqa: E731
+            assert ta.dispatch_triangle_attention_block(module=m, z=z, mask=None, ending=True,
+                                                        native=native) == "override"
+        assert set(seen) == {"module", "z", "mask", "ending", "native"}
+        assert seen["module"] is m and seen["z"] is z and seen["ending"] is True
+        assert seen["native"] is native
+        assert registry.count(ta.BLOCK_OPERATION, "user-override") == 1
+    finally:
+        registry.unregister(ta.BLOCK_OPERATION, "user-override")
+        registry.clear_runtime_state()
+
+
 def test_block_entry_raises_without_a_device():
     z = torch.randn(4, 4, 128)
     w = block.BlockWeights.from_protenix(_protenix_like())
