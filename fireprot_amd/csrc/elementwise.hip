@@ -73,19 +73,22 @@ __global__ __launch_bounds__(256) void mask_rows_kernel(const float* __restrict_
 }
 
 // Zero rows [n, np) of every head of the triangle bias (padded queries), in
-// the FP32 or the BF16 fragment order.
+// the FP32 or the BF16 fragment order, in each of `copies` consecutive
+// [4][np][np] copies (the FP32 block keeps the bias and its log2(e) copy).
 template <typename BiasT>
-__global__ void bias_pad_kernel(int n, int np, BiasT* __restrict__ tri_bias) {
+__global__ void bias_pad_kernel(int n, int np, BiasT* __restrict__ tri_bias, int copies) {
   const int64_t per_head = (int64_t)(np - n) * np;
   const int64_t total = kHeads * per_head;
+  const int64_t copy_elems = (int64_t)kHeads * np * np;
   for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
        idx += (int64_t)gridDim.x * blockDim.x) {
     const int h = (int)(idx / per_head);
     const int64_t r = idx % per_head;
     const int q = n + (int)(r / np);
     const int k = (int)(r % np);
-    tri_bias[sizeof(BiasT) == 4 ? bias_frag_index(h, q, k, np)
-                                : bias_frag_index_bf16(h, q, k, np)] = (BiasT)0.0f;
+    const int64_t at = sizeof(BiasT) == 4 ? bias_frag_index(h, q, k, np)
+                                          : bias_frag_index_bf16(h, q, k, np);
+    for (int c = 0; c < copies; ++c) tri_bias[c * copy_elems + at] = (BiasT)0.0f;
   }
 }
 
@@ -235,17 +238,12 @@ hipError_t launch_mask_bias(const float* mask, int64_t ms_i, int64_t ms_j, int n
   if (blocks > cap) blocks = cap;
   if (bias_bf16) {
     hipLaunchKernelGGL(bias_pad_kernel<__bf16>, dim3((uint32_t)blocks), dim3(256), 0, stream, n,
-                       np, static_cast<__bf16*>(tri_bias));
-    return hipGetLastError();
-  }
-  float* copy = static_cast<float*>(tri_bias);
-  for (int c = 0; c < 2; ++c) {
+                       np, static_cast<__bf16*>(tri_bias), 1);
+  } else {
     hipLaunchKernelGGL(bias_pad_kernel<float>, dim3((uint32_t)blocks), dim3(256), 0, stream, n,
-                       np, copy + (int64_t)c * kHeads * np * np);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
+                       np, static_cast<float*>(tri_bias), 2);
   }
-  return hipSuccess;
+  return hipGetLastError();
 }
 
 hipError_t launch_mask_rows(const float* values, int64_t vs_i, int64_t vs_k, int rows, int n,
