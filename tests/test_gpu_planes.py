@@ -248,3 +248,42 @@ def test_relative_log2_bias(case):
     c = np.ceil(log2[:, :, :32 * t_first].max(axis=2))      # [4, np]
     want = (log2 - (c - np.float32(8.0))[:, :, None].astype(np.float32)).astype(np.float32)
     np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("n,ending", [(64, False), (100, True), (300, False)])
+def test_prepare_magnitude_record(n, ending):
+    """The prepare stage's magnitude record holds max |q| (times 1/sqrt(32)),
+    max |k|, max |v| and max |triangle bias| over the pair, and its valid
+    word.  The attention bounds its logits and picks its softmax path from
+    these maxima, so each must be the projections' own maximum: each work-group
+    combines its waves' maxima before one atomic per word, and at N=64
+    every work-group holds a single tile and all finish together."""
+    z = workloads.make_pair(n)
+    w = workloads.make_weights(bias_scale=8.0)
+    weights = hip_block.BlockWeights.from_tensors(**w).to("cuda")
+    lib = _native.library()
+    ws_bytes = hip_block.workspace_bytes(n, torch.float32)
+    ws = torch.full((ws_bytes,), 0xFF, dtype=torch.uint8, device="cuda")
+    zc = z.cuda()
+    code = lib.fpx_tri_attn_prepare(
+        0, zc.data_ptr(), zc.stride(0), zc.stride(1), None, 0, 0,
+        weights.ln_w.data_ptr(), weights.ln_b.data_ptr(), weights.eps,
+        weights.w_qkvg.data_ptr(), None, weights.w_bias.data_ptr(), weights.inf, n, int(ending),
+        ws.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream)
+    _native.check(code, "fpx_tri_attn_prepare")
+    torch.cuda.synchronize()
+    o = _offsets(n)
+    raw = ws.cpu().numpy()
+    words = raw[o["flags"] + n * 16 * 4:o["flags"] + n * 16 * 4 + 5 * 4]
+    record = words.view(np.float32)
+    assert words.view(np.uint32)[4] == 1
+
+    params = oracle_params(w).to(torch.float64)
+    x = z.transpose(0, 1) if ending else z
+    xl = oracle.layer_norm(x.double(), params.ln_w, params.ln_b, params.eps)
+    eq, ek, ev = oracle.prep_qkv(xl, params, apply_scale=True)
+    bias = oracle.triangle_bias(xl, params)
+    want = [float(t.abs().max()) for t in (eq, ek, ev, bias)]
+    for name, got, ref in zip(("q", "k", "v", "bias"), record[:4], want):
+        print(f"n={n} ending={ending} max|{name}|: record {got:.9g}, float64 {ref:.9g}", flush=True)
+        assert abs(float(got) - ref) <= 1e-5 * ref, name
