@@ -1,0 +1,87 @@
+"""Seeded sweep of pair sizes, masks and weights, held to the float64 oracle.
+
+The fixtures and the C2-C5 cases cover chosen shapes; this sweep draws the
+rest at random (fixed seeds): pair sizes from 1 to 260, so every remainder
+of the 32-key tiles and 128-query work-groups occurs, per-row valid lengths,
+scattered masked keys, fully masked rows, a fractional mask value, random
+LayerNorm affines and weight scales, and both nodes.  Every output row meets
+the FP32 bar of tests/test_gpu_fp32_accuracy.py against the float64 oracle:
+rows with an unmasked key against plain float64, fully masked rows against
+float64 with the logits rounded to float32 where the native path adds them
+(their -1e9 ties).
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from fireprot_amd import block as hip_block
+from oracle import triangle_attention as oracle
+from tests.helpers import hip_weights, oracle_params
+from tests.test_gpu_fp32_accuracy import strict_close
+
+pytestmark = pytest.mark.gpu
+
+SIZES = (1, 2, 5, 31, 32, 33, 64, 97, 127, 128, 129, 160, 191, 224, 257, 260)
+
+
+def _case(seed: int):
+    g = torch.Generator().manual_seed(9000 + seed)
+    n = SIZES[seed % len(SIZES)]
+    z = torch.randn(n, n, 128, generator=g) * float(torch.empty(1).uniform_(0.3, 3.0, generator=g))
+    kind = (seed + seed // len(SIZES)) % 4
+    mask = torch.ones(n, n)
+    if kind == 0:  # a valid prefix per row and per column (padded residues)
+        valid = int(torch.randint(1, n + 1, (1,), generator=g))
+        keep = torch.arange(n) < valid
+        mask = (keep[:, None] & keep[None, :]).float()
+    elif kind == 1:  # ragged per-row lengths, some rows fully masked
+        lengths = torch.randint(0, n + 1, (n,), generator=g)
+        mask = (torch.arange(n)[None, :] < lengths[:, None]).float()
+    elif kind == 2:  # scattered masked keys
+        mask = (torch.rand(n, n, generator=g) > 0.15).float()
+        if n > 3:
+            mask[n // 3] = 0.0
+    else:  # a fractional mask value on a band of keys
+        mask[:, : max(1, n // 4)] = 0.5
+        if n > 2:
+            mask[-1] = 0.0
+    h = 4 * 32
+    weights = {
+        "ln_w": 1.0 + 0.3 * torch.randn(128, generator=g),
+        "ln_b": 0.2 * torch.randn(128, generator=g),
+        "w_q": 0.05 * torch.randn(h, 128, generator=g),
+        "w_k": 0.05 * torch.randn(h, 128, generator=g),
+        "w_v": 0.05 * torch.randn(h, 128, generator=g),
+        "w_g": 0.05 * torch.randn(h, 128, generator=g),
+        "b_g": 0.1 * torch.randn(h, generator=g),
+        "w_bias": float(torch.empty(1).uniform_(0.1, 8.0, generator=g)) * torch.randn(4, 128, generator=g) / 11.3,
+        "w_o": 0.05 * torch.randn(128, h, generator=g),
+        "b_o": 0.1 * torch.randn(128, generator=g),
+        "eps": 1e-5,
+        "inf": 1e9,
+    }
+    ending = bool((seed // 4) % 2)
+    return n, z, mask, weights, ending
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_random_case_meets_the_fp32_bar(seed):
+    n, z, mask, w, ending = _case(seed)
+    print(f"seed={seed} n={n} ending={ending} masked={(mask == 0).float().mean():.3f}", flush=True)
+    with torch.inference_mode():
+        out = hip_block.triangle_attention_block(z.cuda(), mask.cuda(), hip_weights(w),
+                                                 ending=ending)
+        x_frame = (out.transpose(0, 1) if ending else out).cpu()
+    mask_x = mask.transpose(0, 1) if ending else mask
+    dead = (mask_x == 0).all(dim=1)  # rows whose keys are all masked
+    p32 = oracle_params(w)
+    p64 = p32.to(torch.float64)
+    for region, sel in (("open", ~dead), ("masked", dead)):
+        rows = torch.nonzero(sel).flatten()
+        if rows.numel() == 0:
+            continue
+        ref32 = oracle.block(z, mask, p32, ending=ending, outer_rows=rows)
+        ref64 = oracle.block(z.double(), mask.double(), p64, ending=ending, outer_rows=rows,
+                             logits_f32=(region == "masked"))
+        strict_close(f"seed {seed} n={n} {region}", x_frame[rows], ref64, ref32)
