@@ -179,7 +179,7 @@ struct SplitTraits<kProjOut> {
 constexpr int kPlaneRow = kChannels + 8;  // bf16 per LDS row: 272 bytes, conflict-free b128 reads
 typedef __bf16 XPlane[kRows][kPlaneRow];
 
-template <int MODE>
+template <int MODE, bool kFew>
 __global__ __launch_bounds__(SplitTraits<MODE>::kWaves * 64, SplitTraits<MODE>::kMinBlocks) void
 projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
   using T = SplitTraits<MODE>;
@@ -212,37 +212,63 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
   const int group = cb >> 2;
   const int hw = cb & 3;
 
-  // kProjBlock: the LayerNorm output bound of each channel,
-  // |y_c| <= sqrt(128) |ln_w_c| + |ln_b_c|, for the per-head exponents.
-  __shared__ __attribute__((aligned(16))) float ybound[kLn ? kChannels : 1];
-  if constexpr (kLn) {
-    if (tid < kChannels)
-      ybound[tid] = __builtin_fmaf(11.3137085f, __builtin_fabsf(a.ln_w ? a.ln_w[tid] : 1.f),
-                                   __builtin_fabsf(a.ln_b ? a.ln_b[tid] : 0.f));
-    __syncthreads();
-  }
-
-  // Weight planes: B[k][col] for col = 32*hw + l32 of group `group`, lane
-  // holding channels 16t + 8*half + e of k step t, scaled by 2^ew (the
-  // column's max |w| over both halves of the wave).
-  //
   // kProjBlock planes: one plane exponent per head for q, k and v^T (this
   // wave's 32 columns are one head of one group), from a bound on the
   // values instead of each tile's maximum.  Every LayerNorm output obeys
-  // the bound above, so a column's values obey
+  // |y_c| <= sqrt(128) |ln_w_c| + |ln_b_c|, so a column's values obey
   // |x W^T| <= sum_c |W_c| (sqrt(128) |ln_w_c| + |ln_b_c|) (times 1/sqrt(32)
   // for q).  With every tile of a head at one scale, the attention's product
   // scale and v^T exponent are the same for every key tile.  Accuracy does
   // not depend on the scale: the fp16 planes keep 22 significant bits
   // relative to each value down to 2^-14 of the scaled unit, and the values
-  // of normalised rows lie within a few binary orders of the bound.  The
-  // sum reads the weights loaded for the planes.
+  // of normalised rows lie within a few binary orders of the bound.
+  // Large launches sum the bound here, in a loop of its own loads; launches
+  // of a few tiles per work-group (kFew), where this prologue is a visible
+  // part of the run, sum the weights loaded for the planes below against a
+  // table of the channel bounds in LDS, the same terms in the same order.
+  const int e_loop = [&] {
+    if (MODE != kProjBlock || group > 2 || kFew) return 0;
+    const float* src = a.w[group] + (int64_t)(32 * hw + l32) * kChannels + 8 * half;
+    float s = 0.f;
+    // a loop, not unrolled: few registers live beside the weight planes
+#pragma unroll 1
+    for (int t = 0; t < 8; ++t) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int c = 16 * t + 8 * half + e;
+        const float yb = 11.3137085f * __builtin_fabsf(a.ln_w ? a.ln_w[c] : 1.f) +
+                         __builtin_fabsf(a.ln_b ? a.ln_b[c] : 0.f);
+        s = __builtin_fmaf(__builtin_fabsf(src[16 * t + e]), yb, s);
+      }
+    }
+    const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, s),
+                                                     __builtin_bit_cast(unsigned, s), false, false);
+    s = __builtin_bit_cast(float, (unsigned)sw[0]) + __builtin_bit_cast(float, (unsigned)sw[1]);
+    // the margin covers the rounding of the LN output, the sums and q's scale
+    const float bound = wave_max(s) * (group == 0 ? a.q_scale : 1.0f) * (1.0f + 0x1p-8f);
+    if (group == 2) return value_plane_exp(bound);
+    const int e = plane_exp(bound);
+    return e < -kPlaneExpMax ? -kPlaneExpMax : e > kPlaneExpMax ? kPlaneExpMax : e;
+  }();
+  constexpr bool kTable = MODE == kProjBlock && kFew;
+  __shared__ __attribute__((aligned(16))) float ybound[kTable ? kChannels : 1];
+  if constexpr (kTable) {
+    if (tid < kChannels)
+      ybound[tid] = 11.3137085f * __builtin_fabsf(a.ln_w ? a.ln_w[tid] : 1.f) +
+                    __builtin_fabsf(a.ln_b ? a.ln_b[tid] : 0.f);
+    __syncthreads();
+  }
+  int e_table = 0;
+
+  // Weight planes: B[k][col] for col = 32*hw + l32 of group `group`, lane
+  // holding channels 16t + 8*half + e of k step t, scaled by 2^ew (the
+  // column's max |w| over both halves of the wave).
   bf16x8 wh[8], wl[8];
-  int ew, e_head = 0;
+  int ew;
   {
     const float* src = a.w[group] + (int64_t)(32 * hw + l32) * kChannels + 8 * half;
     f32x8 wv[8];
-    float m = 0.f, s = 0.f;
+    float m = 0.f;
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       const f32x4 u = *(const f32x4*)(src + 16 * t);
@@ -256,28 +282,31 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
     m = __builtin_elementwise_maximum(__builtin_bit_cast(float, (unsigned)sw[0]),
                                       __builtin_bit_cast(float, (unsigned)sw[1]));
     ew = plane_exp(m);
-    if (MODE == kProjBlock && group <= 2) {
+    if constexpr (kTable) {
+      if (group <= 2) {
+        float s = 0.f;
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const f32x8 yb = *(const f32x8*)&ybound[16 * t + 8 * half];
+        for (int t = 0; t < 8; ++t) {
+          const f32x8 yb = *(const f32x8*)&ybound[16 * t + 8 * half];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s = __builtin_fmaf(__builtin_fabsf(wv[t][e]), yb[e], s);
-      }
-      const auto ss = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, s),
-                                                       __builtin_bit_cast(unsigned, s), false, false);
-      s = __builtin_bit_cast(float, (unsigned)ss[0]) + __builtin_bit_cast(float, (unsigned)ss[1]);
-      // the margin covers the rounding of the LN output, the sums and q's scale
-      const float bound = wave_max(s) * (group == 0 ? a.q_scale : 1.0f) * (1.0f + 0x1p-8f);
-      if (group == 2) {
-        e_head = value_plane_exp(bound);
-      } else {
-        const int e = plane_exp(bound);
-        e_head = e < -kPlaneExpMax ? -kPlaneExpMax : e > kPlaneExpMax ? kPlaneExpMax : e;
+          for (int e = 0; e < 8; ++e) s = __builtin_fmaf(__builtin_fabsf(wv[t][e]), yb[e], s);
+        }
+        const auto ss = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, s),
+                                                         __builtin_bit_cast(unsigned, s), false, false);
+        s = __builtin_bit_cast(float, (unsigned)ss[0]) + __builtin_bit_cast(float, (unsigned)ss[1]);
+        const float bound = wave_max(s) * (group == 0 ? a.q_scale : 1.0f) * (1.0f + 0x1p-8f);
+        if (group == 2) {
+          e_table = value_plane_exp(bound);
+        } else {
+          const int e = plane_exp(bound);
+          e_table = e < -kPlaneExpMax ? -kPlaneExpMax : e > kPlaneExpMax ? kPlaneExpMax : e;
+        }
       }
     }
 #pragma unroll
     for (int t = 0; t < 8; ++t) split_f16(ldexp8(wv[t], ew), wh[t], wl[t]);
   }
+  const int e_head = kFew ? e_table : e_loop;
   const int col_w = MODE == kProjOut ? 32 * w + l32 : 32 * hw + l32;
   const float col_bias = (MODE != kProjQkv && a.b_g != nullptr) ? a.b_g[col_w] : 0.f;
 
@@ -543,25 +572,36 @@ projection_split_kernel(ProjArgs a, int tiles_j, int ntiles, int streams) {
                        e_head);
     }
     if (a.magnitudes != nullptr) {
-      // Maxima (NaN-propagating) over the work-group, then one atomic per
-      // record word: waves 0-3 hold one group, waves 4-7 the next.  The
-      // work-groups of a small launch finish together, and atomics from
-      // every wave on the same words would wait on each other.
-      __shared__ uint32_t wg_max[NW][2];
       const float om = wave_max(out_max), bm = wave_max(bias_max);
-      if (lane == 0) {
-        wg_max[w][0] = __builtin_bit_cast(uint32_t, group == 0 ? om * a.q_scale : om);
-        wg_max[w][1] = __builtin_bit_cast(uint32_t, bm);
-      }
-      __syncthreads();
-      if (tid < 3) {
-        // Non-negative floats (and NaN above them) order as their bits.
-        const int from = tid == 1 ? NW / 2 : 0, to = tid == 0 ? NW / 2 : NW;
-        uint32_t r = 0;
-        for (int v = from; v < to; ++v) r = max(r, wg_max[v][tid == 2]);
-        const int word = tid == 2 ? 3 : (slice * NW + from) >> 2;
-        if (word < 3 || tid == 2) atomicMax(&a.magnitudes[word], r);
-        if (blockIdx.x == 0 && tid == 0) a.magnitudes[4] = 1u;
+      if constexpr (!kFew) {
+        // Wave maxima (NaN-propagating), one atomic per wave and record word.
+        if (lane == 0) {
+          if (group < 3)
+            atomicMax(&a.magnitudes[group],
+                      __builtin_bit_cast(uint32_t, group == 0 ? om * a.q_scale : om));
+          atomicMax(&a.magnitudes[3], __builtin_bit_cast(uint32_t, bm));
+          if (blockIdx.x == 0 && w == 0) a.magnitudes[4] = 1u;
+        }
+      } else {
+        // The work-group's maxima first, then one atomic per record word:
+        // waves 0-3 hold one group, waves 4-7 the next.  The work-groups of
+        // a launch of few tiles finish together, and atomics from every
+        // wave on the same words would wait on each other.
+        __shared__ uint32_t wg_max[NW][2];
+        if (lane == 0) {
+          wg_max[w][0] = __builtin_bit_cast(uint32_t, group == 0 ? om * a.q_scale : om);
+          wg_max[w][1] = __builtin_bit_cast(uint32_t, bm);
+        }
+        __syncthreads();
+        if (tid < 3) {
+          // Non-negative floats (and NaN above them) order as their bits.
+          const int from = tid == 1 ? NW / 2 : 0, to = tid == 0 ? NW / 2 : NW;
+          uint32_t r = 0;
+          for (int v = from; v < to; ++v) r = max(r, wg_max[v][tid == 2]);
+          const int word = tid == 2 ? 3 : (slice * NW + from) >> 2;
+          if (word < 3 || tid == 2) atomicMax(&a.magnitudes[word], r);
+          if (blockIdx.x == 0 && tid == 0) a.magnitudes[4] = 1u;
+        }
       }
     }
   } else {
@@ -599,8 +639,18 @@ hipError_t launch_split(const ProjArgs& a, hipStream_t stream) {
   int64_t cap = (int64_t)device_cu_count() * T::kMinBlocks / T::kSlices;
   if (cap >= 8) cap -= cap % 8;
   const int streams = (int)(ntiles < cap ? ntiles : cap);
-  hipLaunchKernelGGL(projection_split_kernel<MODE>, dim3(streams * T::kSlices), dim3(T::kWaves * 64),
-                     0, stream, a, tiles_j, (int)ntiles, streams);
+  // The block projection at up to 64 row tiles per work-group (N up to
+  // about 512) takes the variant with the shorter prologue and epilogue
+  // (kFew); larger launches keep the other, whose tile loop was tuned.
+  if constexpr (MODE == kProjBlock) {
+    if (ntiles <= (int64_t)64 * streams) {
+      hipLaunchKernelGGL((projection_split_kernel<MODE, true>), dim3(streams * T::kSlices),
+                         dim3(T::kWaves * 64), 0, stream, a, tiles_j, (int)ntiles, streams);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((projection_split_kernel<MODE, false>), dim3(streams * T::kSlices),
+                     dim3(T::kWaves * 64), 0, stream, a, tiles_j, (int)ntiles, streams);
   return hipGetLastError();
 }
 
