@@ -262,11 +262,13 @@ def _weights_of(module: Any, dtype: Any = None, layers: tuple | None = None) -> 
 
 
 def _precision(layer: Any) -> Any:
-    """The layer's ``precision`` override, or None (read from the instance
-    dictionary first: a missing attribute costs ``nn.Module.__getattr__`` an
-    exception)."""
-    own = getattr(layer, "__dict__", {})
-    return own["precision"] if "precision" in own else getattr(type(layer), "precision", None)
+    """The layer's ``precision`` override, or None.  When its class defines
+    no ``precision`` (a value or a property), the instance dictionary holds
+    it or nothing does; reading it there spares ``nn.Module.__getattr__`` the
+    exception of a missing attribute."""
+    if hasattr(type(layer), "precision"):
+        return getattr(layer, "precision", None)
+    return getattr(layer, "__dict__", {}).get("precision")
 
 
 def _has_hooks(module: Any, layers: tuple[tuple, tuple] | None = None) -> bool:

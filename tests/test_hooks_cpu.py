@@ -219,3 +219,39 @@ def test_block_eligibility_rejects_hooked_layers_and_other_q_scales():
     m.linear_qkv.precision = None
     m.scale = 0.25
     assert ta.block_eligible(m, _Hip(), None) == (False, "module q scale is not 1/sqrt(32)")
+
+
+def test_precision_override_read_as_attribute_lookup_does():
+    """A ``precision`` defined by a layer's class (a value or a property)
+    counts as the attribute lookup resolves it; an instance value counts; a
+    class value of None or none at all lets the block run."""
+    class _Hip:
+        is_cuda, dtype, shape, device = True, torch.float32, (8, 8, 128), torch.device("cpu")
+
+        def dim(self):
+            return 3
+
+        def stride(self, d=None):
+            s = (1024, 128, 1)
+            return s if d is None else s[d]
+
+        def element_size(self):
+            return 4
+
+        def data_ptr(self):
+            return 0
+
+    m = StartingNode().eval()
+    linear = m.linear_qkv
+    base = type(linear)
+    for attrs, expected in (({"precision": None}, True),
+                            ({"precision": torch.float64}, False),
+                            ({"precision": property(lambda self: None)}, True),
+                            ({"precision": property(lambda self: torch.float64)}, False)):
+        linear.__class__ = type("Linear", (base,), attrs)
+        assert ta.block_eligible(m, _Hip(), None)[0] is expected, attrs
+    linear.__class__ = base
+    linear.precision = torch.bfloat16
+    assert not ta.block_eligible(m, _Hip(), None)[0]
+    del linear.precision
+    assert ta.block_eligible(m, _Hip(), None) == (True, "")
