@@ -6,9 +6,13 @@ of the 32-key tiles and 128-query work-groups occurs, per-row valid lengths,
 scattered masked keys, fully masked rows, a fractional mask value, random
 LayerNorm affines and weight scales, and both nodes.  Every output row meets
 the FP32 bar of tests/test_gpu_fp32_accuracy.py against the float64 oracle:
-rows with an unmasked key against plain float64, fully masked rows against
-float64 with the logits rounded to float32 where the native path adds them
-(their -1e9 ties).
+rows with an unmasked key against plain float64, fully masked rows (their
+-1e9 ties) and the draws with a fractional mask value (a -5e8 mask bias,
+whose FP32 spacing of 32 swallows the products) against float64 with the
+logits rounded to float32 where the native path adds them.  The BF16
+storage path is held to the FP32 oracle on the same bf16-rounded inputs:
+within the BF16 bar of tests/test_gpu_bf16.py, or within twice the error of
+the native BF16 path (``oracle.block_bf16``) where that is larger.
 """
 from __future__ import annotations
 
@@ -62,12 +66,12 @@ def _case(seed: int):
         "inf": 1e9,
     }
     ending = bool((seed // 4) % 2)
-    return n, z, mask, weights, ending
+    return n, z, mask, weights, ending, kind
 
 
 @pytest.mark.parametrize("seed", range(32))
 def test_random_case_meets_the_fp32_bar(seed):
-    n, z, mask, w, ending = _case(seed)
+    n, z, mask, w, ending, kind = _case(seed)
     print(f"seed={seed} n={n} ending={ending} masked={(mask == 0).float().mean():.3f}", flush=True)
     with torch.inference_mode():
         out = hip_block.triangle_attention_block(z.cuda(), mask.cuda(), hip_weights(w),
@@ -83,5 +87,38 @@ def test_random_case_meets_the_fp32_bar(seed):
             continue
         ref32 = oracle.block(z, mask, p32, ending=ending, outer_rows=rows)
         ref64 = oracle.block(z.double(), mask.double(), p64, ending=ending, outer_rows=rows,
-                             logits_f32=(region == "masked"))
+                             logits_f32=(region == "masked" or kind == 3))
         strict_close(f"seed {seed} n={n} {region}", x_frame[rows], ref64, ref32)
+
+
+@pytest.mark.parametrize("seed", range(0, 32, 2))
+def test_random_case_bf16_meets_the_bf16_bar(seed):
+    """The same draws with BF16 storage.  Reference: the FP32 oracle on the
+    same bf16-rounded inputs and weights.  Bar: max|HIP - ref| within the
+    BF16 bar (2e-2 max|ref|) or twice the native BF16 path's own distance
+    from ref (``oracle.block_bf16``: every intermediate rounded where the
+    native path rounds it), whichever is larger -- these draws' weights give
+    logits large enough that rounding them to bf16 alone moves some weights
+    by percents."""
+    from tests.test_gpu_bf16 import BF16_REL
+
+    n, z, mask, w, ending, _ = _case(seed)
+    print(f"bf16 seed={seed} n={n} ending={ending} masked={(mask == 0).float().mean():.3f}",
+          flush=True)
+    weights = hip_block.BlockWeights.from_tensors(**w, dtype=torch.bfloat16).to("cuda")
+    with torch.inference_mode():
+        out = hip_block.triangle_attention_block(z.to(torch.bfloat16).cuda(), mask.cuda(),
+                                                 weights, ending=ending).cpu()
+    assert out.dtype == torch.bfloat16 and torch.isfinite(out.float()).all()
+    rounded = {k: (v.to(torch.bfloat16).float() if isinstance(v, torch.Tensor) else v)
+               for k, v in w.items()}
+    ref = oracle.block(z.to(torch.bfloat16).float(), mask, oracle.BlockParams(**rounded),
+                       ending=ending)
+    native = oracle.block_bf16(z, mask, oracle_params(w), ending=ending)
+    scale = ref.abs().max().item()
+    err = (out.float() - ref).abs().max().item()
+    err_native = (native.float() - ref).abs().max().item()
+    bar = max(BF16_REL * scale, 2.0 * err_native)
+    print(f"bf16 seed {seed} n={n}: max|err| {err:.3e}, native bf16 {err_native:.3e}, "
+          f"bar {bar:.3e} (max|ref| {scale:.3e})", flush=True)
+    assert err <= bar
