@@ -327,8 +327,11 @@ __global__ __launch_bounds__(512, 1) void trimul_finish_split_kernel(TriMulArgs 
     for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
+        // native: value = sigmoid(g) * x, rounded; z + value when adding.
+        // No fused multiply-add: the update is rounded before the sum, so
+        // the in-place form equals z plus the separate update.
+#pragma clang fp contract(off)
         const int j = jb * kRows + 16 * rb + 4 * g4 + r;
-        // native: value = sigmoid(g) * x; z + value when adding
         const float v = sigmoidf_(acc[rb][1][r] + bg) * (acc[rb][0][r] + bz);
         if (j < n) o[(int64_t)j * a.os_j] = residual ? resid[rb][r] + v : v;
       }
