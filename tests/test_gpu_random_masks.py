@@ -122,3 +122,21 @@ def test_random_case_bf16_meets_the_bf16_bar(seed):
     print(f"bf16 seed {seed} n={n}: max|err| {err:.3e}, native bf16 {err_native:.3e}, "
           f"bar {bar:.3e} (max|ref| {scale:.3e})", flush=True)
     assert err <= bar
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("seed", [3, 10, 21, 28])
+def test_random_case_residual_equals_z_plus_update(seed, dtype):
+    """The residual entry (z += dz in place, the Pairformer's update) equals z
+    plus the separate block output, rounded once in z's dtype, as the native
+    z = z + tri_att(z) rounds it."""
+    n, z, mask, w, ending, _ = _case(seed)
+    print(f"residual seed={seed} n={n} ending={ending} dtype={dtype}", flush=True)
+    weights = hip_block.BlockWeights.from_tensors(**w, dtype=dtype).to("cuda")
+    with torch.inference_mode():
+        zc = z.to(dtype).cuda()
+        mc = mask.cuda()
+        dz = hip_block.triangle_attention_block(zc, mc, weights, ending=ending)
+        want = zc + dz
+        hip_block.triangle_attention_block(zc, mc, weights, ending=ending, residual=True)
+        assert torch.equal(zc, want), "in-place update differs from z + dz"
