@@ -918,6 +918,41 @@ __device__ __forceinline__ void const_item(const AttnArgs& a, int nqt, int nkt, 
   // same for every row, so there the products accumulate into O_r directly
   // and the factor is applied once in the epilogue.
   auto pv = [&](int stage, int t, const bf16x8 (&ph)[2], const bf16x8 (&pl)[2]) {
+    if constexpr (kBlock && loaded) {
+      // Every row's operands are read first and the 24 products issued row
+      // by row within each term, so consecutive MFMAs are independent and no
+      // LDS read waits on the MFMA before it.  Rows that are not live run on
+      // whatever their stage holds (their copies are skipped) and are never
+      // stored.
+      bf16x8 vh[kConstRows][2], vl[kConstRows][2];
+      for_const_rows([&](auto rc) {
+        constexpr int r = decltype(rc)::value;
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          vh[r][m] = plane_rd(stage, r, 0, m);
+          vl[r][m] = plane_rd(stage, r, 1, m);
+        }
+      });
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        for_const_rows([&](auto rc) {
+          constexpr int r = decltype(rc)::value;
+          f32x16& orow = const_row<r>(o);
+          orow = mfma_f16(vl[r][m], ph[m], orow);
+        });
+        for_const_rows([&](auto rc) {
+          constexpr int r = decltype(rc)::value;
+          f32x16& orow = const_row<r>(o);
+          orow = mfma_f16(vh[r][m], pl[m], orow);
+        });
+        for_const_rows([&](auto rc) {
+          constexpr int r = decltype(rc)::value;
+          f32x16& orow = const_row<r>(o);
+          orow = mfma_f16(vh[r][m], ph[m], orow);
+        });
+      }
+      return;
+    }
     for_const_rows([&](auto rc) {
       constexpr int r = decltype(rc)::value;
       if (!((live >> r) & 1u)) return;
@@ -972,7 +1007,12 @@ __device__ __forceinline__ void const_item(const AttnArgs& a, int nqt, int nkt, 
     copy(clamp(t + 2), stage(t + 2));
     // Tile t + 1 has landed once at most this iteration's four bias-fragment
     // loads and four tile copies are outstanding (loads retire in order).
-    wait_vmcnt<8>();
+    // When tile t + 2 is past the last, nothing reads the loaded fragment
+    // and the compiler may drop its loads: then only the four copies count.
+    if (t + 2 <= last)
+      wait_vmcnt<8>();
+    else
+      wait_vmcnt<4>();
     __syncthreads();
   };
   auto tail = [&](const f32x16& cur, int t) {

@@ -611,8 +611,13 @@ __global__ __launch_bounds__(kThreads, 3) void attention_bf16_kernel(Bf16AttnArg
       dma(clamp(kt + 3), (s + 3) & 3);
       // Tile kt+2 has landed once at most this iteration's copy and (fast
       // path) its two bias-word loads are outstanding: vector memory loads
-      // retire in issue order.
-      wait_vmcnt<kExact ? 1 : 3>();
+      // retire in issue order.  When no later iteration reads the bias words
+      // of tile kt+3, the compiler may drop their loads: then only the copy
+      // counts.
+      if (kExact || kt + 3 > last)
+        wait_vmcnt<1>();
+      else
+        wait_vmcnt<3>();
       __syncthreads();
     };
     auto body = [&](int kt, f32x16& cur, f32x16& nxt, BiasWords& bw) {
