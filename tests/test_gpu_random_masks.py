@@ -20,6 +20,7 @@ import pytest
 import torch
 
 from fireprot_amd import block as hip_block
+from fireprot_amd import workloads
 from oracle import triangle_attention as oracle
 from tests.helpers import hip_weights, oracle_params
 from tests.test_gpu_fp32_accuracy import strict_close
@@ -140,3 +141,25 @@ def test_random_case_residual_equals_z_plus_update(seed, dtype):
         want = zc + dz
         hip_block.triangle_attention_block(zc, mc, weights, ending=ending, residual=True)
         assert torch.equal(zc, want), "in-place update differs from z + dz"
+
+
+@pytest.mark.parametrize("n,valid,dtype", [(300, 250, torch.float32), (1536, 1352, torch.float32),
+                                           (160, 140, torch.bfloat16), (1024, 900, torch.bfloat16)])
+def test_repeat_calls_are_bit_identical(n, valid, dtype):
+    """Padding rows with the standard weights take the constant-mask launch
+    (FP32) and the BF16 block's last ring stages; both depend on counted
+    waits for their LDS copies.  Eight calls on fresh workspaces, both nodes,
+    must agree bit for bit."""
+    print(f"repeat n={n} valid={valid} dtype={dtype}", flush=True)
+    z = workloads.make_pair(n).to(dtype).cuda()
+    mask = workloads.make_mask(n, valid).cuda()
+    weights = hip_block.BlockWeights.from_tensors(**workloads.make_weights(bias_scale=8.0),
+                                                  dtype=dtype).to("cuda")
+    with torch.inference_mode():
+        for ending in (False, True):
+            first = hip_block.triangle_attention_block(z, mask, weights, ending=ending)
+            for rep in range(7):
+                again = hip_block.triangle_attention_block(z, mask, weights, ending=ending)
+                assert torch.equal(first, again), f"call {rep + 1} differs (ending={ending})"
+            del first, again
+            torch.cuda.empty_cache()
