@@ -63,8 +63,10 @@ __device__ __forceinline__ void gemm_nt_128_f16(const float* a, int64_t lda, con
   const int xa[2] = {ea[lrow], ea[lrow + 64]};
   const int xb[2] = {eb[lrow], eb[lrow + 64]};
 
-  f32x4 ga[2], gb[2];
-  auto load = [&](int kt) {
+  // Two register slots of staged rows: stage s sits in slot s % 2 from its
+  // loads (issued two stages ahead) until its split into LDS.
+  f32x4 ga[2][2], gb[2][2];
+  auto load = [&](int kt, int slot) {
     // one buffer resource per 32-key run: the 32-bit offsets span 128 rows
     const int64_t run = (int64_t)(kt >> 1) * kblock;
     const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a + run, (127 * lda + 2 * kSplitK) * 4);
@@ -72,29 +74,28 @@ __device__ __forceinline__ void gemm_nt_128_f16(const float* a, int64_t lda, con
     const uint32_t s = (uint32_t)((kt & 1) * kSplitK * 4);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      ga[u] = buffer_load_f4(ra, va + u * pa, s);
-      gb[u] = buffer_load_f4(rb, vb + u * pb, s);
+      ga[slot][u] = buffer_load_f4(ra, va + u * pa, s);
+      gb[slot][u] = buffer_load_f4(rb, vb + u * pb, s);
     }
   };
-  auto store = [&](int buf) {
+  auto store = [&](int buf, int slot) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       bf16x4 h, l;
-      split_f16(ldexp4(ga[u], xa[u]), h, l);
+      split_f16(ldexp4(ga[slot][u], xa[u]), h, l);
       *(bf16x4*)&As[buf][0][lrow + 64 * u][lc4] = h;
       *(bf16x4*)&As[buf][1][lrow + 64 * u][lc4] = l;
-      split_f16(ldexp4(gb[u], xb[u]), h, l);
+      split_f16(ldexp4(gb[slot][u], xb[u]), h, l);
       *(bf16x4*)&Bs[buf][0][lrow + 64 * u][lc4] = h;
       *(bf16x4*)&Bs[buf][1][lrow + 64 * u][lc4] = l;
     }
   };
 
-  load(0);
-  store(0);
-  if (nk > 1) load(1);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
+  // Stage kt: its products from LDS buffer kt % 2; then stage kt + 1 goes
+  // from its slot into the other buffer and stage kt + 3 is loaded into
+  // that slot.  The slots and buffers are compile-time indices (two stages
+  // per loop iteration).
+  auto step = [&](int kt, int buf, int slot) {
     bf16x8 ap[2][2], bp[2][2];
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
@@ -115,10 +116,20 @@ __device__ __forceinline__ void gemm_nt_128_f16(const float* a, int64_t lda, con
       }
     }
     if (kt + 1 < nk) {
-      store(buf ^ 1);
-      if (kt + 2 < nk) load(kt + 2);
+      store(buf ^ 1, slot);
+      if (kt + 3 < nk) load(kt + 3, slot);
     }
     __syncthreads();
+  };
+
+  load(0, 0);
+  if (nk > 1) load(1, 1);
+  store(0, 0);
+  if (nk > 2) load(2, 0);  // after stage 0's split has read slot 0
+  __syncthreads();
+  for (int kt = 0; kt < nk; kt += 2) {
+    step(kt, 0, 1);
+    if (kt + 1 < nk) step(kt + 1, 1, 0);
   }
 }
 
